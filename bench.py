@@ -1,0 +1,317 @@
+"""Benchmark of the TCFP-12 hot path on one MI355X.
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--skip-extras]
+
+Headline (BASELINE.json ``metric``, configs[1]): the fused dual-FP8 GEMM
+``out = X W_hi^T s_x s_hi + X W_lo^T s_x s_lo`` at M = N = K = 4096,
+per-tensor scales, FP32 accumulation, bf16 output, inputs resident in HBM.
+One step = one dual-GEMM launch; ``value`` is TFLOP/s counting the dual as
+two GEMMs (2 * 2 * 4096^3 FLOP per step).
+
+The same JSON line carries the roofline of that kernel (HIP events on the
+stream the kernel runs on), the CPU baseline (the numpy oracle on host
+cores, a bounded row sample of the same problem), and secondary figures:
+library comparators at the same shape, the dual-quant kernels' HBM rate,
+and the 1024 -> 4096 -> 1024 MLP training step against BF16.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+FP8_PEAK_TFLOPS = 5000.0   # MI355X dense FP8 MFMA (AMD published)
+BF16_PEAK_TFLOPS = 2500.0  # MI355X dense BF16 MFMA
+HBM_PEAK_GBS = 8000.0      # MI355X HBM3E
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def event_time_ms(fn, iters, stream):
+    import torch
+
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(iters):
+        fn()
+    end.record(stream)
+    end.synchronize()
+    return start.elapsed_time(end) / iters
+
+
+def bench_dual_gemm(steps, warmup):
+    import torch
+
+    from tcfp_amd import kernels as K
+
+    dev = torch.device("cuda:0")
+    n = 4096
+    xb = torch.randn(n, n, generator=torch.Generator().manual_seed(0)).bfloat16().to(dev)
+    w = torch.randn(n, n, generator=torch.Generator().manual_seed(1)).to(dev)
+    a, sa = K.quantize_per_tensor(xb)
+    h, l, ih, il = K.dual_quantize_per_tensor(w)
+    out = torch.empty(n, n, dtype=torch.bfloat16, device=dev)
+
+    def step():
+        return K.fused_dual_gemm_forward(a, h, l, sa, ih, il, out_dtype=torch.bfloat16)
+
+    for _ in range(warmup):
+        out = step()
+    stream = torch.cuda.current_stream(dev)
+    torch.cuda.synchronize()
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    ev0.record(stream)
+    for _ in range(steps):
+        out = step()
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    wall_ms = (t1 - t0) * 1e3 / steps
+    kern_ms = ev0.elapsed_time(ev1) / steps
+    flop = 2 * 2 * n**3
+    # parity of the timed output against a torch fp32 dequant matmul
+    ref = (a.float() * sa) @ (h.float() * ih + l.float() * il).t()
+    rel = ((out.float() - ref).norm() / ref.norm()).item()
+    return {
+        "n": n, "flop": flop, "wall_ms": wall_ms, "kern_ms": kern_ms,
+        "tflops_wall": flop / (wall_ms * 1e-3) / 1e12,
+        "tflops_kern": flop / (kern_ms * 1e-3) / 1e12,
+        "rel_fro": rel, "tensors": (a, h, l, sa, ih, il, xb, w),
+    }
+
+
+def bench_comparators(t, iters=20):
+    import torch
+
+    a, h, l, sa, ih, il, xb, w = t
+    stream = torch.cuda.current_stream()
+    n = a.shape[0]
+    res = {}
+    try:
+        def naive():
+            o1 = torch._scaled_mm(a, h.t(), scale_a=sa, scale_b=ih, out_dtype=torch.bfloat16)
+            o2 = torch._scaled_mm(a, l.t(), scale_a=sa, scale_b=il, out_dtype=torch.bfloat16)
+            return o1 + o2
+        naive()
+        ms = event_time_ms(naive, iters, stream)
+        res["naive_2x_scaled_mm_add_ms"] = ms
+        res["naive_2x_scaled_mm_add_tflops"] = 4 * n**3 / (ms * 1e-3) / 1e12
+
+        def single():
+            return torch._scaled_mm(a, h.t(), scale_a=sa, scale_b=ih, out_dtype=torch.bfloat16)
+        single()
+        ms = event_time_ms(single, iters, stream)
+        res["scaled_mm_single_ms"] = ms
+        res["scaled_mm_single_tflops"] = 2 * n**3 / (ms * 1e-3) / 1e12
+    except Exception as e:  # library path unavailable on this build
+        res["scaled_mm_error"] = str(e)[:200]
+    wb = w.bfloat16()
+
+    def bf16():
+        return xb @ wb.t()
+    bf16()
+    ms = event_time_ms(bf16, iters, stream)
+    res["bf16_matmul_ms"] = ms
+    res["bf16_matmul_tflops"] = 2 * n**3 / (ms * 1e-3) / 1e12
+    return res
+
+
+def bench_dual_quant(iters=20):
+    import torch
+
+    from tcfp_amd import kernels as K
+
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream(dev)
+    out = {}
+    n, k = 4096, 4096
+    w = torch.randn(n, k, device=dev) * 0.02
+    ef = torch.zeros(n, k, device=dev)
+    # per-tensor with EF (update in place): 14 algorithmic B/elem
+    ms = event_time_ms(lambda: K.dual_quantize_per_tensor(w, ef), iters, stream)
+    out["per_tensor_ef_4096x4096_ms"] = ms
+    out["per_tensor_ef_4096x4096_GBs"] = 14 * n * k / (ms * 1e-3) / 1e9
+    # block-64 with EF: 14 + 2/64 B/elem
+    ms = event_time_ms(lambda: K.fused_dual_quantize_fp8(w, 64, error_buf=ef), iters, stream)
+    out["block64_ef_4096x4096_ms"] = ms
+    out["block64_ef_4096x4096_GBs"] = (14 + 2 / 64) * n * k / (ms * 1e-3) / 1e9
+    # SRR block-64 on the C5 scale-up weight [16384, 4096]: 6 + 2/64 B/elem
+    w2 = torch.randn(16384, 4096, device=dev) * 0.02
+    ms = event_time_ms(lambda: K.fused_dual_quantize_fp8(w2, 64, stochastic_lo=True, seed=1),
+                       iters, stream)
+    out["block64_srr_16384x4096_ms"] = ms
+    out["block64_srr_16384x4096_GBs"] = (6 + 2 / 64) * 16384 * 4096 / (ms * 1e-3) / 1e9
+    # act quant bf16 [8192, 1024] -> e4m3 (+ transposed copy): 2 + 1 (+1) B/elem
+    x = torch.randn(8192, 1024, device=dev).bfloat16()
+    ms = event_time_ms(lambda: K.quantize_per_tensor(x), iters, stream)
+    out["act_quant_bf16_8192x1024_ms"] = ms
+    out["act_quant_bf16_8192x1024_GBs"] = 3 * x.numel() / (ms * 1e-3) / 1e9
+    return out
+
+
+def bench_mlp(steps=100, time_iters=20):
+    """1024 -> 4096 -> 1024 GELU MLP, 8192 tokens, MSE, AdamW 1e-3."""
+    import torch
+    import torch.nn as nn
+
+    from tcfp_amd.nn import convert_to_tcfp
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(8192, 1024, generator=g).bfloat16().to(dev)
+    y = torch.randn(8192, 1024, generator=g).to(dev)
+
+    def make(tcfp):
+        torch.manual_seed(1)
+        m = nn.Sequential(nn.Linear(1024, 4096), nn.GELU(), nn.Linear(4096, 1024)).to(dev)
+        if tcfp:
+            convert_to_tcfp(m, use_tensor_cores=True)
+        return m
+
+    def run(tcfp):
+        m = make(tcfp)
+        opt = torch.optim.AdamW(m.parameters(), lr=1e-3)
+
+        def step():
+            if tcfp:
+                out = m(x)
+            else:
+                with torch.autocast("cuda", dtype=torch.bfloat16):
+                    out = m(x)
+            loss = (out.float() - y).square().mean()
+            opt.zero_grad(set_to_none=True)
+            loss.backward()
+            opt.step()
+            return loss
+
+        losses = []
+        for i in range(steps):
+            losses.append(step())
+        torch.cuda.synchronize()
+        ms = event_time_ms(step, time_iters, torch.cuda.current_stream(dev))
+        return [float(v) for v in torch.stack(losses).cpu()], ms
+
+    l_t, ms_t = run(True)
+    l_b, ms_b = run(False)
+    return {
+        "tcfp_step_ms": ms_t, "bf16_autocast_step_ms": ms_b, "speedup_vs_bf16": ms_b / ms_t,
+        "loss_step1_tcfp": l_t[0], "loss_step100_tcfp": l_t[-1],
+        "loss_step100_bf16": l_b[-1], "loss_rel_diff_step100": abs(l_t[-1] - l_b[-1]) / l_b[-1],
+        "steps": steps,
+    }
+
+
+def cpu_baseline(t):
+    """The numpy oracle (float64 dequant matmul) on a row sample of C2."""
+    import numpy as np
+    from threadpoolctl import threadpool_info, threadpool_limits
+
+    from oracle import fp8 as ofp8
+    from oracle import gemm as og
+
+    a, h, l, sa, ih, il = (x.cpu() for x in t[:6])
+    rows = 1024
+    import torch
+
+    av = a[:rows].view(torch.uint8).numpy()
+    hv, lv = h.view(torch.uint8).numpy(), l.view(torch.uint8).numpy()
+    cores = os.cpu_count() or 1
+    with threadpool_limits(limits=cores):
+        threads = max((p.get("num_threads", 1) for p in threadpool_info()), default=1)
+        times = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            og.dual_gemm_nt(av, ofp8.E4M3, hv, lv, sa.item(), ih.item(), il.item())
+            times.append(time.perf_counter() - t0)
+    s = statistics.median(times)
+    flop = 2 * 2 * rows * 4096 * 4096
+    return {
+        "value": flop / s / 1e12, "unit": "TFLOP/s", "cores": int(threads), "kind": "port",
+        "sample": f"oracle.gemm.dual_gemm_nt (numpy float64 dequant matmul) on rows "
+                  f"0..{rows - 1} of the 4096^3 C2 problem, median of 3 ({s:.2f} s each)",
+    }
+
+
+def traffic_from_profiles():
+    p = ROOT / "profiles" / "dual_gemm_4096_traffic.json"
+    if p.exists():
+        try:
+            return json.loads(p.read_text()).get("hbm_bytes_per_launch")
+        except Exception:
+            return None
+    return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--skip-extras", action="store_true",
+                    help="only the headline dual GEMM (no comparators, MLP, CPU baseline)")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py: this build measures one GPU only (the TCFP-12 path has no "
+              "multi-GPU component); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    log(f"[bench] dual GEMM 4096^3: warmup {args.warmup}, steps {args.steps}")
+    r = bench_dual_gemm(args.steps, args.warmup)
+    log(f"[bench] dual GEMM: {r['tflops_wall']:.1f} TFLOP/s wall, {r['tflops_kern']:.1f} "
+        f"TFLOP/s events, rel_fro {r['rel_fro']:.2e}")
+    extras = {}
+    cpu = None
+    if not args.skip_extras:
+        log("[bench] comparators")
+        extras["comparators_4096"] = bench_comparators(r["tensors"])
+        log("[bench] dual quant")
+        extras["quant_kernels"] = bench_dual_quant()
+        log("[bench] MLP train step (configs[3])")
+        extras["mlp_train_step"] = bench_mlp()
+        log("[bench] CPU baseline")
+        cpu = cpu_baseline(r["tensors"])
+    achieved = r["tflops_kern"]
+    line = {
+        "metric": "dual-FP8 GEMM TFLOP/s @4096^3 (% FP8 MFMA peak); MLP train-step ms",
+        "value": round(r["tflops_wall"], 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(r["wall_ms"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp8_e4m3 (fp32 accumulate, bf16 out)",
+        "data": "synthetic (seeded randn, bf16 X quantised per-tensor, fp32 W dual-quantised)",
+        "config": {"workload": "configs[1]: fused dual FP8 GEMM, per-tensor scales, "
+                               "M=N=K=4096, bf16 out", "M": 4096, "N": 4096, "K": 4096,
+                   "parallelism": "single GPU"},
+        "pct_fp8_peak": round(100 * r["tflops_wall"] / FP8_PEAK_TFLOPS, 2),
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": FP8_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved / FP8_PEAK_TFLOPS, 4),
+                     "traffic": traffic_from_profiles()},
+        "cpu_baseline": cpu,
+        "parity_rel_fro": r["rel_fro"],
+        **extras,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,163 @@
+/* tcfp_hip.h -- C ABI of the MI355X-native TCFP-12 kernel library
+ * (libtcfp_hip.so, hand-written HIP for gfx950).
+ *
+ * Every entry point takes raw device pointers, int64 sizes/leading
+ * dimensions and a hipStream_t (passed as void*), enqueues its kernels on
+ * that stream and returns a status code.  No torch types cross this
+ * boundary; the library does not allocate device memory.  Scalars that the
+ * reference keeps as (1,) fp32 device tensors (per-tensor inverse scales)
+ * are device pointers here too, so no call synchronises with the host.
+ *
+ * Layout conventions (all row-major, innermost index contiguous):
+ *   activations  [M, K]        (K = in_features)
+ *   weights      [N, K]        (nn.Linear layout, N = out_features)
+ *   block exps   [K/bs, rows]  int8, scale = 2^e (reference layout,
+ *                              tcfp/kernels.py:1700)
+ *
+ * Each declaration cites the reference interface (path:line under the
+ * reference tree) whose behaviour it replaces.
+ */
+#ifndef TCFP_HIP_H_
+#define TCFP_HIP_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- enums ------------------------------------------------------------- */
+#define TCFP_FP8_E4M3 0 /* OCP float8_e4m3fn */
+#define TCFP_FP8_E5M2 1 /* OCP float8_e5m2   */
+
+#define TCFP_DTYPE_F32 0
+#define TCFP_DTYPE_BF16 1
+
+/* ---- status codes ------------------------------------------------------ */
+#define TCFP_OK 0
+#define TCFP_ERR_SHAPE 1     /* bad size / leading dimension / divisibility */
+#define TCFP_ERR_DTYPE 2     /* unsupported dtype / format code            */
+#define TCFP_ERR_ALIGN 3     /* pointer or leading dimension misaligned    */
+#define TCFP_ERR_HIP 4       /* a HIP runtime call failed                  */
+#define TCFP_ERR_WORKSPACE 5 /* workspace missing or too small             */
+#define TCFP_ERR_EXCLUSIVE 6 /* mutually exclusive options requested       */
+
+/* Human-readable text for a status code (static storage). */
+const char* tcfp_status_string(int status);
+
+/* Bytes of zero-initialised device workspace the per-tensor reductions
+ * need.  The library leaves the workspace zeroed again when each call's
+ * kernels finish, so one buffer serves every call on a stream.  Calls
+ * that overlap in time must use different workspaces. */
+size_t tcfp_workspace_bytes(void);
+
+/* ---- per-tensor quantisation ------------------------------------------- */
+
+/* Per-tensor FP8 quantisation of x [rows, cols] (f32 or bf16).
+ * Replaces tcfp.core.to_fp8_e4m3 (tcfp/core.py:85-106) and to_fp8_e5m2
+ * (tcfp/core.py:137-158), used for activations at tcfp/nn/__init__.py:390
+ * and gradients at :494.
+ *   scale_in  optional device fp32 scalar: use it instead of the amax rule.
+ *   q         [rows, cols] fp8 codes.
+ *   q_t       optional [cols, rows] transposed codes (wgrad operand).
+ *   scale_out optional device fp32 scalar receiving the scale used.
+ *   inv_out   device fp32 scalar receiving 1/scale.
+ * Without scale_in: amax = max|x| (NaN-propagating), clamped at 1e-12,
+ * scale = reciprocal(amax) * FP8_MAX with both ops rounded to x's dtype,
+ * q = RNE(clamp(x * scale, +-FP8_MAX)), inv = 1/scale (IEEE fp32). */
+int tcfp_quantize_per_tensor(const void* x, int x_dtype, int64_t rows, int64_t cols,
+                             int fp8_fmt, const float* scale_in, uint8_t* q, uint8_t* q_t,
+                             float* scale_out, float* inv_out, void* workspace,
+                             void* stream);
+
+/* Per-tensor dual quantisation with optional error feedback.
+ * Replaces the body of _TCFP12TensorCoreFunction.forward that builds
+ * W_hi/W_lo (tcfp/nn/__init__.py:343-383, with ErrorFeedbackState
+ * get_error/update_error, tcfp/core.py:320-326).
+ *   w       [n, k] f32 or bf16 master weight.
+ *   ef      optional [n, k] fp32 error buffer; read as e_prev, and if
+ *           update_ef != 0 overwritten in place with
+ *           e_new = W - (hi*inv_hi + lo*inv_lo).
+ *   stochastic_lo  round W_lo stochastically (SRR, tcfp/core.py:109-134,
+ *           418-464) with Philox4x32-10 keyed by (seed, offset).
+ *   w_hi_t, w_lo_t optional [k, n] transposed codes (dgrad operands). */
+int tcfp_dual_quantize_per_tensor(const void* w, int w_dtype, int64_t n, int64_t k,
+                                  float* ef, int update_ef, int stochastic_lo,
+                                  uint64_t seed, uint64_t offset, uint8_t* w_hi,
+                                  uint8_t* w_lo, float* inv_hi, float* inv_lo,
+                                  uint8_t* w_hi_t, uint8_t* w_lo_t, void* workspace,
+                                  void* stream);
+
+/* ---- per-block quantisation -------------------------------------------- */
+
+/* Per-(row, K-block) FP8 quantisation.  Replaces block_quantize_fp8
+ * (tcfp/kernels.py:1675-1722, kernel :205-275).
+ *   x [m, k] f32/bf16; block in {32, 64, 128}; k % block == 0.
+ *   q [m, k] codes; exps [k/block, m] int8 with
+ *   e = max(ceil(log2(max(amax,1e-12)/FP8_MAX)), -126), q = RNE(clamp(x/2^e)). */
+int tcfp_block_quantize(const void* x, int x_dtype, int64_t m, int64_t k, int block,
+                        int fp8_fmt, uint8_t* q, int8_t* exps, void* stream);
+
+/* Fused block dual quantisation.  Replaces fused_dual_quantize_fp8
+ * (tcfp/kernels.py:1749-1875, kernel :288-459) including the error update
+ * the reference performs afterwards (:1867-1873), in one pass.
+ *   ef      optional [n, k] fp32 buffer, read then overwritten in place
+ *           with W - deq(hi) - deq(lo) unless update_ef == 0.
+ *   e_lo    holds -128 for blocks whose residual amax < 1e-12.
+ *   stochastic_lo and ef are mutually exclusive (TCFP_ERR_EXCLUSIVE). */
+int tcfp_block_dual_quantize(const void* w, int w_dtype, int64_t n, int64_t k, int block,
+                             float* ef, int update_ef, int stochastic_lo, uint64_t seed,
+                             uint64_t offset, uint8_t* w_hi, uint8_t* w_lo, int8_t* e_hi,
+                             int8_t* e_lo, void* stream);
+
+/* Block dequantisation fp8 * 2^e -> fp32 (tcfp/kernels.py:1725-1746).
+ * A -128 exponent is decoded as 2^-128 like the reference's exp2. */
+int tcfp_block_dequantize(const uint8_t* q, int fp8_fmt, const int8_t* exps, int64_t m,
+                          int64_t k, int block, float* out, void* stream);
+
+/* ---- GEMMs ------------------------------------------------------------- */
+
+/* Fused dual FP8 GEMM, both operands K-contiguous ("NT"):
+ *   out[i,j] = s_a*s_hi * sum_k A[i,k] B_hi[j,k] + s_a*s_lo * sum_k A[i,k] B_lo[j,k]
+ *              (+ bias[j]).
+ * Replaces fused_dual_gemm_forward (tcfp/kernels.py:1545-1601),
+ * cuda_ext_dual_gemm_forward (tcfp/cuda_ext.py:241-259, C++
+ * tcfp/csrc/fused_dual_gemm.cu:119-274) and, with B = W^T, the dgrad
+ * fused_dual_gemm_backward_dx (tcfp/kernels.py:1604-1666).
+ * With b_lo == NULL it is the single scaled GEMM s_a*s_hi*(A B_hi^T): the
+ * FP8 wgrad of tcfp/nn/__init__.py:546-555 (A = G^T, B = X^T).
+ *   a [m, k] (lda), b_hi/b_lo [n, k] (ldb); k % 16 == 0; lda, ldb % 16 == 0;
+ *   pointers 16-byte aligned.  s_* are device fp32 scalars (inverse scales).
+ *   out [m, n] (ldo) fp32 or bf16; accumulation is fp32. */
+int tcfp_dual_gemm(const uint8_t* a, int a_fmt, int64_t lda, const uint8_t* b_hi,
+                   const uint8_t* b_lo, int b_fmt, int64_t ldb, int64_t m, int64_t n,
+                   int64_t k, const float* s_a, const float* s_hi, const float* s_lo,
+                   const float* bias, void* out, int out_dtype, int64_t ldo, void* stream);
+
+/* ---- layout helpers ---------------------------------------------------- */
+
+/* dst[c, r] = src[r, c] for a [rows, cols] byte matrix (ld = cols / rows).
+ * Used where the reference calls ensure_column_major / .t().contiguous()
+ * (tcfp/core.py:196-213, tcfp/nn/__init__.py:546-555). */
+int tcfp_transpose_u8(const uint8_t* src, int64_t rows, int64_t cols, uint8_t* dst,
+                      void* stream);
+
+/* ---- self-test hooks (no reference counterpart) ------------------------ */
+
+/* Converts every float32 whose bit pattern lies in [lo_bits, hi_bits] (and
+ * its negation) with both the hardware and the software FP8 encoder and
+ * counts mismatches into *mismatches (device uint64, accumulated). */
+int tcfp_selftest_fp8_cvt(uint32_t lo_bits, uint32_t hi_bits, int fp8_fmt,
+                          unsigned long long* mismatches, void* stream);
+
+/* Fills out[4*i .. 4*i+3] with Philox4x32-10 of counter (i + ctr0, ctr1,
+ * ctr2, ctr3) under key (k0, k1), for i < n. */
+int tcfp_selftest_philox(uint32_t ctr0, uint32_t ctr1, uint32_t ctr2, uint32_t ctr3,
+                         uint32_t k0, uint32_t k1, int64_t n, uint32_t* out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TCFP_HIP_H_ */

@@ -1,0 +1,221 @@
+"""Quantisation restatement in numpy (test oracle; see package docstring).
+
+All arrays are float32 holding the exact values of the reference tensor's
+dtype ("f32" or "bf16"); the dtype tag only changes where the reference's
+scale arithmetic rounds.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+from .fp8 import E4M3, FP8_MAX, bf16_round, decode, encode
+
+F32 = np.float32
+
+# Largest mantissa offset j (q = 2^k (1 + j 2^-23)) for which a correctly
+# rounded fp32 log2(q) still rounds to the integer k, indexed by p, the
+# binade exponent of the fp32 numbers adjacent to k on the side of k + L.
+_J_TABLE = np.array([0, 0, 1, 2, 5, 11, 22], dtype=np.int64)
+
+
+def ceil_log2_f32(q: np.ndarray) -> np.ndarray:
+    """``torch.ceil(torch.log2(q))`` for positive normal fp32 ``q`` (int64 out).
+
+    Restates the exponent rule of ``tcfp/kernels.py:257-260`` /
+    ``tcfp/core.py:250`` *as evaluated by a correctly rounded fp32 log2*
+    (which is what torch's CPU ``log2`` gives at every boundary input):
+    for ``q = 2^k (1 + f)`` with small ``f > 0`` the fp32 log2 can round to
+    exactly ``k``, so ``ceil`` returns ``k`` instead of ``k + 1``.
+    Subnormal inputs return -127 (callers clamp to -126).
+    """
+    q = np.ascontiguousarray(q, dtype=F32)
+    bits = q.view(np.uint32).astype(np.int64)
+    ef = (bits >> 23) & 0xFF
+    j = bits & 0x7FFFFF
+    k = ef - 127
+    a = np.abs(k)
+    safe_a = np.maximum(a, 1)
+    p = np.floor(np.log2(safe_a)).astype(np.int64)
+    pow2 = (safe_a & (safe_a - 1)) == 0
+    p = np.where((k < 0) & pow2, p - 1, p)
+    p = np.where(k == 0, 0, p)
+    jmax = np.where(p < 0, 0, _J_TABLE[np.clip(p, 0, 6)])
+    e = np.where(j == 0, k, np.where(j <= jmax, k, k + 1))
+    return np.where(ef == 0, -127, e)
+
+
+def _round_dtype(x: np.ndarray, dtype: str) -> np.ndarray:
+    return bf16_round(x) if dtype == "bf16" else np.asarray(x, dtype=F32)
+
+
+def per_tensor_scale(t: np.ndarray, dtype: str, fmt: str = E4M3) -> np.float32:
+    """``scale = (FP8_MAX / amax.clamp(min=1e-12)).to(float32)`` (core.py:100-101).
+
+    ``python_float / tensor`` is ``tensor.reciprocal() * python_float``
+    (torch ``Tensor.__rtruediv__``), each op rounded to the tensor's dtype.
+    """
+    amax = np.max(np.abs(t)) if t.size else F32(0)
+    amax = np.maximum(F32(amax), _round_dtype(np.array([1e-12], F32), dtype)[0])
+    rcp = _round_dtype(np.array([F32(1.0) / F32(amax)], F32), dtype)[0]
+    scale = _round_dtype(np.array([F32(rcp) * F32(FP8_MAX[fmt])], F32), dtype)[0]
+    return F32(scale)
+
+
+def to_fp8_per_tensor(t: np.ndarray, dtype: str = "f32", fmt: str = E4M3,
+                      scale: np.float32 | None = None):
+    """``to_fp8_e4m3`` / ``to_fp8_e5m2`` (core.py:85-106, :137-158).
+
+    Returns ``(codes uint8, inv_scale float32, scale float32)``.
+    """
+    t = np.asarray(t, dtype=F32)
+    if scale is None:
+        scale = per_tensor_scale(t, dtype, fmt)
+    mx = F32(FP8_MAX[fmt])
+    scaled = np.clip(t * F32(scale), -mx, mx)
+    codes = encode(scaled, fmt)
+    inv = F32(F32(1.0) / F32(scale))
+    return codes, inv, F32(scale)
+
+
+def dual_quant_per_tensor(W: np.ndarray, ef: np.ndarray | None = None):
+    """Per-tensor dual-quant + error feedback (nn/__init__.py:343-383).
+
+    ``W`` holds the weight's values as float32.  Returns
+    ``(hi, lo, inv_hi, inv_lo, ef_new, residual)``; ``ef_new`` is relative
+    to the original W, not to ``W + ef`` (nn/__init__.py:378-383).
+    """
+    W = np.asarray(W, dtype=F32)
+    w = W + ef if ef is not None else W
+    hi, inv_hi, _ = to_fp8_per_tensor(w, "f32")
+    deq_hi = decode(hi, E4M3) * inv_hi
+    residual = w - deq_hi
+    lo, inv_lo, _ = to_fp8_per_tensor(residual, "f32")
+    deq_lo = decode(lo, E4M3) * inv_lo
+    ef_new = W - (deq_hi + deq_lo)
+    return hi, lo, F32(inv_hi), F32(inv_lo), ef_new, residual
+
+
+def sr_candidates_per_tensor(x: np.ndarray):
+    """Deterministic part of ``stochastic_round_to_fp8_e4m3`` (core.py:418-464).
+
+    ``x`` is the already scaled and clamped tensor.  Returns
+    ``(lo_codes, hi_codes, frac, exact)``: the result is ``lo`` where
+    ``exact``, else ``hi`` with probability ``frac``.  Note ``hi`` can be
+    NaN-coded (0x7F) near the top of the range; ``rand < NaN`` is false, so
+    such elements always keep ``lo``.
+    """
+    x = np.asarray(x, dtype=F32)
+    lo = encode(x, E4M3)
+    lo_f = decode(lo, E4M3)
+    d = np.sign(x - lo_f).astype(F32)
+    exact = x == lo_f
+    nudge = d * F32(2.0 ** -6) * F32(0.5)
+    hi = encode(lo_f + nudge, E4M3)
+    same = (decode(hi, E4M3) == lo_f) & ~exact
+    abs_lo = np.maximum(np.abs(lo_f), F32(2.0 ** -6))
+    larger = d * abs_lo * F32(0.25)
+    hi_retry = encode(lo_f + larger, E4M3)
+    hi = np.where(same, hi_retry, hi)
+    with np.errstate(invalid="ignore"):
+        gap = np.maximum(np.abs(decode(hi, E4M3) - lo_f), F32(1e-45))
+        gap = np.where(np.isnan(decode(hi, E4M3)), np.nan, gap).astype(F32)
+        frac = np.clip(np.abs(x - lo_f) / gap, F32(0), F32(1))
+    return lo, hi.astype(np.uint8), frac.astype(F32), exact
+
+
+def _blocks(x: np.ndarray, bs: int) -> np.ndarray:
+    m, k = x.shape
+    assert k % bs == 0
+    return x.reshape(m, k // bs, bs)
+
+
+def block_exponent(amax: np.ndarray, fmt: str = E4M3) -> np.ndarray:
+    """``max(ceil(log2(max(amax, 1e-12) / FP8_MAX)), -126)`` (kernels.py:253-260)."""
+    a = np.maximum(np.asarray(amax, dtype=F32), F32(1e-12))
+    q = (a / F32(FP8_MAX[fmt])).astype(F32)
+    return np.maximum(ceil_log2_f32(q), -126)
+
+
+def _pow2(e: np.ndarray) -> np.ndarray:
+    return np.ldexp(np.ones_like(e, dtype=F32), e.astype(np.int32)).astype(F32)
+
+
+def block_quantize(x: np.ndarray, bs: int, fmt: str = E4M3):
+    """``block_quantize_fp8`` (kernels.py:1675-1722, kernel :205-275).
+
+    ``x`` [M, K] float32 values.  Returns ``(codes [M,K] uint8, exps int8
+    [K/bs, M])`` with ``scale = 2^exp`` (divide before the cast).
+    """
+    x = np.asarray(x, dtype=F32)
+    xb = _blocks(x, bs)
+    e = block_exponent(np.max(np.abs(xb), axis=-1), fmt)
+    mx = F32(FP8_MAX[fmt])
+    scaled = np.clip(xb * _pow2(-e)[..., None], -mx, mx)
+    codes = encode(scaled, fmt).reshape(x.shape)
+    return codes, np.ascontiguousarray(e.T.astype(np.int8))
+
+
+def block_dequantize(codes: np.ndarray, exps: np.ndarray, bs: int,
+                     fmt: str = E4M3) -> np.ndarray:
+    """``block_dequantize_fp8`` (kernels.py:1725-1746): ``fp8 * exp2(e)``."""
+    m, k = codes.shape
+    vals = decode(codes, fmt).reshape(m, k // bs, bs)
+    scl = np.exp2(exps.astype(F32)).astype(F32).T[..., None]
+    return (vals * scl).reshape(m, k).astype(F32)
+
+
+def block_dual_quantize(w: np.ndarray, bs: int, ef: np.ndarray | None = None):
+    """``fused_dual_quantize_fp8`` without SR (kernels.py:1749-1875, :288-459).
+
+    Returns ``(hi, lo, e_hi int8 [K/bs,N], e_lo int8 [K/bs,N], ef_new|None)``.
+    ``e_lo`` is -128 for blocks whose residual amax is below 1e-12; the new
+    error is ``w - deq(hi) - deq(lo)`` evaluated left to right
+    (kernels.py:1870-1873).
+    """
+    w = np.asarray(w, dtype=F32)
+    wc = w + ef if ef is not None else w
+    wb = _blocks(wc, bs)
+    e_hi = block_exponent(np.max(np.abs(wb), axis=-1))
+    mx = F32(448.0)
+    hi = encode(np.clip(wb * _pow2(-e_hi)[..., None], -mx, mx), E4M3)
+    deq_hi = decode(hi, E4M3) * _pow2(e_hi)[..., None]
+    r = (wb - deq_hi).astype(F32)
+    amax_lo = np.max(np.abs(r), axis=-1)
+    zero = amax_lo < F32(1e-12)
+    e_lo = block_exponent(amax_lo)
+    div = np.where(zero, F32(1.0), _pow2(e_lo))
+    lo = encode(np.clip(r / div[..., None], -mx, mx), E4M3)
+    e_lo_store = np.where(zero, -128, e_lo)
+    shape = w.shape
+    hi = hi.reshape(shape)
+    lo = lo.reshape(shape)
+    e_hi8 = np.ascontiguousarray(e_hi.T.astype(np.int8))
+    e_lo8 = np.ascontiguousarray(e_lo_store.T.astype(np.int8))
+    ef_new = None
+    if ef is not None:
+        ef_new = (w - block_dequantize(hi, e_hi8, bs)) - block_dequantize(lo, e_lo8, bs)
+    return hi, lo, e_hi8, e_lo8, ef_new
+
+
+def sr_candidates_block(x: np.ndarray):
+    """Deterministic part of the in-kernel SR of kernels.py:398-423.
+
+    ``x`` is the scaled and clamped residual.  Returns ``(rtn, other, frac,
+    exact)``.  The Triton cast saturates (``satfinite``) so ``other`` never
+    leaves +-448.
+    """
+    x = np.asarray(x, dtype=F32)
+    mx = F32(448.0)
+    rtn = encode(x, E4M3)
+    rtn_f = decode(rtn, E4M3)
+    diff = x - rtn_f
+    d = np.where(diff >= 0, F32(1), F32(-1))
+    abs_rtn = np.maximum(np.abs(rtn_f), F32(1e-12))
+    nudge = d * abs_rtn * F32(0.25)
+    other = encode(np.clip(rtn_f + nudge, -mx, mx), E4M3)
+    other_f = decode(other, E4M3)
+    gap = np.maximum(np.abs(other_f - rtn_f), F32(1e-45))
+    frac = np.minimum(np.abs(diff) / gap, F32(1))
+    boundary = np.abs(other_f - rtn_f) < F32(1e-45)
+    exact = (np.abs(diff) < F32(1e-45)) | boundary
+    return rtn, other, frac.astype(F32), exact

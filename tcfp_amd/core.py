@@ -1,0 +1,123 @@
+"""FP8 primitives of the TCFP-12 path (drop-in for ``tcfp.core``).
+
+``to_fp8_e4m3`` / ``to_fp8_e5m2`` keep the reference's exact semantics
+(``tcfp/core.py:85-158``) -- codes and scales bit-identical -- but run as
+HIP kernels (one amax pass, one quantise pass, no host synchronisation).
+``ErrorFeedbackState`` is the reference's per-parameter buffer store
+(``tcfp/core.py:298-326``), keyed by parameter name.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+from enum import Enum, auto
+
+import torch
+
+from . import kernels as _k
+
+FP8_E4M3_MAX: float = 448.0
+FP8_E4M3_MIN: float = -448.0
+FP8_E4M3_SMALLEST_NORMAL: float = 2**-6
+FP8_E5M2_MAX: float = 57344.0
+FP8_E5M2_MIN: float = -57344.0
+
+DEFAULT_BLOCK_SIZE: int = 32
+VALID_BLOCK_SIZES: tuple[int, ...] = (16, 32, 64, 128)
+
+
+class TCFPMode(Enum):
+    """Available TCFP precision modes (reference ``tcfp/core.py:46-49``)."""
+
+    TCFP12 = auto()
+
+
+@dataclass
+class FP8Config:
+    """Configuration record (reference ``tcfp/core.py:52-77``)."""
+
+    mode: TCFPMode = TCFPMode.TCFP12
+    block_size: int = DEFAULT_BLOCK_SIZE
+    e4m3_for_weights: bool = True
+    e5m2_for_grads: bool = True
+    error_feedback: bool = True
+    stochastic_rounding: bool = False
+
+    def __post_init__(self) -> None:
+        if self.block_size not in VALID_BLOCK_SIZES:
+            raise ValueError(
+                f"block_size must be one of {VALID_BLOCK_SIZES}, got {self.block_size}"
+            )
+
+
+def to_fp8_e4m3(
+    tensor: torch.Tensor,
+    scale: torch.Tensor | None = None,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Per-tensor FP8 E4M3 cast; returns ``(fp8, inv_scale)`` with inv_scale (1,) fp32.
+
+    Without ``scale``: ``amax = |t|.max().clamp(min=1e-12)``,
+    ``scale = 448 / amax`` evaluated as torch does (reciprocal then product,
+    both in t's dtype), ``fp8 = RNE(clamp(t.float() * scale))``,
+    ``inv = 1 / scale``.
+    """
+    q, inv = _k.quantize_per_tensor(tensor, torch.float8_e4m3fn, scale)
+    return q, inv
+
+
+def to_fp8_e5m2(
+    tensor: torch.Tensor,
+    scale: torch.Tensor | None = None,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Per-tensor FP8 E5M2 cast (``tcfp/core.py:137-158``), FP8_MAX = 57344."""
+    q, inv = _k.quantize_per_tensor(tensor, torch.float8_e5m2, scale)
+    return q, inv
+
+
+def ensure_column_major(t: torch.Tensor) -> torch.Tensor:
+    """Column-major view (or copy) of a 2-D tensor (``tcfp/core.py:196-213``)."""
+    assert t.ndim == 2, f"ensure_column_major requires 2-D tensor, got {t.ndim}-D"
+    if t.stride(0) == 1 and t.stride(1) == t.shape[0]:
+        return t
+    return t.t().contiguous().t()
+
+
+class ErrorFeedbackState:
+    """Per-parameter FP32 error-feedback buffers (``tcfp/core.py:298-326``).
+
+    ``get_error`` lazily creates a zero buffer shaped like ``like`` (fp32);
+    ``update_error`` rebinds the stored tensor.  The HIP dual-quant kernels
+    update the stored buffer in place, which is observationally the same
+    for the state machine (``tcfp/nn/__init__.py:375-383``).  The
+    delayed-scaling dictionaries exist for checkpoint-format compatibility
+    (``tcfp/training/checkpointing.py:200-224``) and stay empty here.
+    """
+
+    def __init__(
+        self,
+        ema_decay: float = 0.999,
+        residual_validation_interval: int = 100,
+    ) -> None:
+        self._buffers: dict[str, torch.Tensor] = {}
+        self._amax_ema: dict[str, torch.Tensor] = {}
+        self._ema_decay: float = ema_decay
+        self._delayed_amax: dict[str, torch.Tensor] = {}
+        self._residual_ratio: dict[str, torch.Tensor] = {}
+        self._step_count: dict[str, int] = {}
+        self._residual_validation_interval: int = residual_validation_interval
+
+    def get_error(self, name: str, like: torch.Tensor) -> torch.Tensor:
+        buf = self._buffers.get(name)
+        if buf is None or buf.shape != like.shape:
+            buf = torch.zeros(like.shape, dtype=torch.float32, device=like.device)
+            self._buffers[name] = buf
+        return buf
+
+    def update_error(self, name: str, error: torch.Tensor) -> None:
+        self._buffers[name] = error.detach()
+
+    def reset(self) -> None:
+        self._buffers.clear()
+        self._amax_ema.clear()
+        self._delayed_amax.clear()
+        self._residual_ratio.clear()
+        self._step_count.clear()

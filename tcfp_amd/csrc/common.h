@@ -1,0 +1,218 @@
+// Shared device helpers for the TCFP-12 HIP kernels (gfx950 / CDNA4).
+//
+// Numerics follow the reference's torch semantics bit-for-bit:
+//   * FP8 casts are round-to-nearest-even (torch `.to(float8_*)`),
+//   * per-tensor scales are `reciprocal(amax) * FP8_MAX` in the input dtype
+//     (torch `Tensor.__rtruediv__`, reference tcfp/core.py:100-101),
+//   * block exponents are `ceil(log2(amax / FP8_MAX))` as a correctly
+//     rounded fp32 log2 evaluates it (reference tcfp/kernels.py:253-260).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/tcfp_hip.h"
+
+#define TCFP_DEV __device__ __forceinline__
+
+namespace tcfp {
+
+constexpr float kE4M3Max = 448.0f;
+constexpr float kE5M2Max = 57344.0f;
+
+TCFP_DEV float fp8_max(int fmt) { return fmt == TCFP_FP8_E5M2 ? kE5M2Max : kE4M3Max; }
+
+// ---------------------------------------------------------------------------
+// bfloat16
+// ---------------------------------------------------------------------------
+TCFP_DEV float bf16_to_f32(uint16_t h) { return __uint_as_float(uint32_t(h) << 16); }
+
+TCFP_DEV uint16_t f32_to_bf16_rne(float x) {
+  uint32_t b = __float_as_uint(x);
+  if ((b & 0x7FFFFFFFu) > 0x7F800000u) return uint16_t((b >> 16) | 0x40u);
+  b += 0x7FFFu + ((b >> 16) & 1u);
+  return uint16_t(b >> 16);
+}
+
+TCFP_DEV float round_bf16(float x) { return bf16_to_f32(f32_to_bf16_rne(x)); }
+
+// ---------------------------------------------------------------------------
+// FP8 encode / decode (software, exact).  `sat` selects saturation to the
+// largest finite code instead of torch's overflow codes (E4M3FN: NaN 0x7F,
+// E5M2: inf 0x7C); the reference clamps before casting, so both agree on
+// its inputs.
+// ---------------------------------------------------------------------------
+TCFP_DEV uint32_t f32_to_e4m3(float x, bool sat = false) {
+  uint32_t b = __float_as_uint(x);
+  uint32_t s = (b >> 24) & 0x80u;
+  uint32_t m = b & 0x7FFFFFFFu;
+  if (m > 0x7F800000u) return s | 0x7Fu;
+  uint32_t q;
+  if (m < 0x3C800000u) {  // below 2^-6: multiples of 2^-9
+    q = uint32_t(__float2int_rn(__uint_as_float(m) * 512.0f));
+  } else {
+    uint32_t r = m + 0x7FFFFu + ((m >> 20) & 1u);
+    q = (r >> 20) - (120u << 3);
+    uint32_t top = sat ? 0x7Eu : 0x7Fu;
+    q = q > top ? top : q;
+  }
+  return s | q;
+}
+
+TCFP_DEV uint32_t f32_to_e5m2(float x, bool sat = false) {
+  uint32_t b = __float_as_uint(x);
+  uint32_t s = (b >> 24) & 0x80u;
+  uint32_t m = b & 0x7FFFFFFFu;
+  if (m > 0x7F800000u) return s | 0x7Fu;
+  uint32_t q;
+  if (m < 0x38800000u) {  // below 2^-14: multiples of 2^-16
+    q = uint32_t(__float2int_rn(__uint_as_float(m) * 65536.0f));
+  } else {
+    uint32_t r = m + 0xFFFFFu + ((m >> 21) & 1u);
+    q = (r >> 21) - (112u << 2);
+    uint32_t top = sat ? 0x7Bu : 0x7Cu;
+    q = q > top ? top : q;
+  }
+  return s | q;
+}
+
+template <int FMT>
+TCFP_DEV uint32_t f32_to_fp8(float x, bool sat = false) {
+  if constexpr (FMT == TCFP_FP8_E5M2) return f32_to_e5m2(x, sat);
+  else return f32_to_e4m3(x, sat);
+}
+
+TCFP_DEV float e4m3_to_f32(uint32_t c) {
+  uint32_t s = (c & 0x80u) << 24;
+  uint32_t e = (c >> 3) & 0xFu, m = c & 7u;
+  uint32_t mag;
+  if (e == 0) mag = __float_as_uint(float(m) * 0.001953125f);  // m * 2^-9
+  else if (e == 15 && m == 7) mag = 0x7FC00000u;
+  else mag = ((e + 120u) << 23) | (m << 20);
+  return __uint_as_float(s | mag);
+}
+
+TCFP_DEV float e5m2_to_f32(uint32_t c) {
+  uint32_t s = (c & 0x80u) << 24;
+  uint32_t e = (c >> 2) & 0x1Fu, m = c & 3u;
+  uint32_t mag;
+  if (e == 0) mag = __float_as_uint(float(m) * 1.52587890625e-05f);  // m * 2^-16
+  else if (e == 31) mag = m ? 0x7FC00000u : 0x7F800000u;
+  else mag = ((e + 112u) << 23) | (m << 21);
+  return __uint_as_float(s | mag);
+}
+
+template <int FMT>
+TCFP_DEV float fp8_to_f32(uint32_t c) {
+  if constexpr (FMT == TCFP_FP8_E5M2) return e5m2_to_f32(c);
+  else return e4m3_to_f32(c);
+}
+
+// Hardware conversion of four clamped, finite floats (gfx950 OCP FP8,
+// round-to-nearest-even).  Bit-identity with the software path above on
+// every finite in-range float32 is checked on the GPU by the test suite.
+template <int FMT>
+TCFP_DEV uint32_t cvt4_fp8(float a, float b, float c, float d) {
+  int r;
+  if constexpr (FMT == TCFP_FP8_E5M2) {
+    r = __builtin_amdgcn_cvt_pk_bf8_f32(a, b, 0, false);
+    r = __builtin_amdgcn_cvt_pk_bf8_f32(c, d, r, true);
+  } else {
+    r = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+    r = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, r, true);
+  }
+  return uint32_t(r);
+}
+
+template <int FMT>
+TCFP_DEV uint32_t sw4_fp8(float a, float b, float c, float d) {
+  return f32_to_fp8<FMT>(a) | (f32_to_fp8<FMT>(b) << 8) | (f32_to_fp8<FMT>(c) << 16) |
+         (f32_to_fp8<FMT>(d) << 24);
+}
+
+// ---------------------------------------------------------------------------
+// ceil(log2(q)) as torch evaluates it for positive normal fp32 q:
+// exact integer logic reproducing a correctly rounded fp32 log2 followed by
+// ceil.  For q = 2^k (1 + j 2^-23) the rounded log2 equals k exactly when
+// j <= J(p), where p is the binade exponent of the fp32 numbers just past k
+// toward k + log2(1+f); J = floor(ln2 * 2^(p-1)) = {0,0,1,2,5,11,22}.
+// Subnormal q returns -127 (callers clamp at -126).
+// ---------------------------------------------------------------------------
+TCFP_DEV int ceil_log2_f32(float q) {
+  uint32_t b = __float_as_uint(q);
+  int ef = int((b >> 23) & 0xFFu);
+  if (ef == 0) return -127;
+  int k = ef - 127;
+  uint32_t j = b & 0x7FFFFFu;
+  if (j == 0) return k;
+  int a = k < 0 ? -k : k;
+  int p = 0;
+  if (a != 0) {
+    p = 31 - __clz(a);
+    if (k < 0 && (a & (a - 1)) == 0) p -= 1;
+  }
+  const uint64_t table = 0x16'0B'05'02'01'00'00ull;  // J(p) bytes, p = 0..6
+  uint32_t jmax = p <= 0 ? 0u : uint32_t((table >> (8 * p)) & 0xFFu);
+  return j <= jmax ? k : k + 1;
+}
+
+// Block exponent rule: max(ceil(log2(max(amax,1e-12) / FP8_MAX)), -126).
+TCFP_DEV int block_exponent(float amax, float fmax) {
+  float a = fmaxf(amax, 1e-12f);
+  int e = ceil_log2_f32(__fdiv_rn(a, fmax));
+  return e < -126 ? -126 : e;
+}
+
+// 2^e as float for e in [-149, 127].
+TCFP_DEV float exp2i(int e) {
+  if (e >= -126) return __uint_as_float(uint32_t(e + 127) << 23);
+  return __uint_as_float(1u << (e + 149));
+}
+
+// ---------------------------------------------------------------------------
+// Philox4x32-10 (Salmon, Moraes, Dror, Shaw: "Parallel random numbers: as
+// easy as 1, 2, 3", SC'11).  Counter-based: each element draws from its own
+// (index, offset) counter, so results do not depend on launch shape.
+// ---------------------------------------------------------------------------
+struct u32x4 { uint32_t x, y, z, w; };
+
+TCFP_DEV u32x4 philox4x32_10(u32x4 c, uint32_t k0, uint32_t k1) {
+#pragma unroll
+  for (int r = 0; r < 10; ++r) {
+    uint64_t p0 = uint64_t(0xD2511F53u) * c.x;
+    uint64_t p1 = uint64_t(0xCD9E8D57u) * c.z;
+    u32x4 n;
+    n.x = uint32_t(p1 >> 32) ^ c.y ^ k0;
+    n.y = uint32_t(p1);
+    n.z = uint32_t(p0 >> 32) ^ c.w ^ k1;
+    n.w = uint32_t(p0);
+    c = n;
+    k0 += 0x9E3779B9u;
+    k1 += 0xBB67AE85u;
+  }
+  return c;
+}
+
+TCFP_DEV float u32_to_unit(uint32_t v) { return float(v >> 8) * 5.9604644775390625e-08f; }
+
+// ---------------------------------------------------------------------------
+// Reductions (wave64)
+// ---------------------------------------------------------------------------
+TCFP_DEV float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+// |x| max that propagates NaN like torch.max.
+TCFP_DEV float nanmax(float a, float b) {
+  return (a != a || b != b) ? __uint_as_float(0x7FC00000u) : fmaxf(a, b);
+}
+
+TCFP_DEV float wave_nanmax(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = nanmax(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+}  // namespace tcfp

@@ -1,0 +1,981 @@
+// Quantisation kernels for the TCFP-12 path on gfx950.
+//
+// Built with -ffp-contract=off: the reference evaluates every product and
+// sum as a separately rounded torch op (tcfp/nn/__init__.py:364, 378-383,
+// tcfp/kernels.py:1870-1873), and the codes / error buffers here must match
+// it bit for bit, so no multiply-add may be fused.
+//
+// HBM layout: inputs are read once per pass with 16-byte vector loads; each
+// thread owns whole 8-element vectors, so the in-place error-feedback update
+// of a vector is done by the thread that read it.
+#include "common.h"
+
+using namespace tcfp;
+
+namespace {
+
+// Per-stream reduction state.  Zero at rest: the last workgroup of each
+// reducing kernel consumes and re-zeroes the accumulator and the ticket.
+struct ReduceWs {
+  unsigned int amax_bits;  // max |x| as float bits (monotone for x >= 0)
+  unsigned int ticket;     // workgroups finished
+  unsigned int pad[2];
+  float scale[4];          // {scale_hi, inv_hi, scale_lo, inv_lo}
+};
+
+constexpr int kThreads = 256;
+
+int g_num_cu = 0;
+
+int num_cu() {
+  if (g_num_cu == 0) {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+        n > 0)
+      g_num_cu = n;
+    else
+      g_num_cu = 256;
+  }
+  return g_num_cu;
+}
+
+inline int grid_for(int64_t work_items, int per_cu) {
+  int64_t g = (work_items + kThreads - 1) / kThreads;
+  int64_t cap = int64_t(num_cu()) * per_cu;
+  if (g > cap) g = cap;
+  if (g < 1) g = 1;
+  return int(g);
+}
+
+inline int launch_status() { return hipGetLastError() == hipSuccess ? TCFP_OK : TCFP_ERR_HIP; }
+
+// ---- vector loads: 8 consecutive elements as float -----------------------
+TCFP_DEV void load8(const float* p, float v[8]) {
+  float4 a = *reinterpret_cast<const float4*>(p);
+  float4 b = *reinterpret_cast<const float4*>(p + 4);
+  v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+  v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+}
+TCFP_DEV void load8(const uint16_t* p, float v[8]) {
+  uint4 a = *reinterpret_cast<const uint4*>(p);
+  uint32_t w[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    v[2 * i] = __uint_as_float(w[i] << 16);
+    v[2 * i + 1] = __uint_as_float(w[i] & 0xFFFF0000u);
+  }
+}
+TCFP_DEV float load1(const float* p) { return *p; }
+TCFP_DEV float load1(const uint16_t* p) { return bf16_to_f32(*p); }
+
+TCFP_DEV void store8(float* p, const float v[8]) {
+  *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+  *reinterpret_cast<float4*>(p + 4) = make_float4(v[4], v[5], v[6], v[7]);
+}
+
+// torch.clamp semantics: NaN passes through.
+TCFP_DEV float clampf(float v, float mx) { return v > mx ? mx : (v < -mx ? -mx : v); }
+
+template <int FMT>
+TCFP_DEV uint2 encode8(const float v[8]) {
+#ifdef TCFP_SW_CVT
+  return make_uint2(sw4_fp8<FMT>(v[0], v[1], v[2], v[3]), sw4_fp8<FMT>(v[4], v[5], v[6], v[7]));
+#else
+  return make_uint2(cvt4_fp8<FMT>(v[0], v[1], v[2], v[3]), cvt4_fp8<FMT>(v[4], v[5], v[6], v[7]));
+#endif
+}
+
+template <int FMT>
+TCFP_DEV uint32_t encode1(float v) {
+#ifdef TCFP_SW_CVT
+  return f32_to_fp8<FMT>(v);
+#else
+  return cvt4_fp8<FMT>(v, 0.f, 0.f, 0.f) & 0xFFu;
+#endif
+}
+
+TCFP_DEV uint32_t byte_of(uint2 c, int j) { return ((j < 4 ? c.x : c.y) >> (8 * (j & 3))) & 0xFFu; }
+
+// ---- per-tensor scale rule (tcfp/core.py:100-101, 105) ---------------------
+// amax is NaN-propagating; clamp(min=1e-12) keeps NaN; the reciprocal and the
+// product with FP8_MAX are each rounded to the input dtype.
+TCFP_DEV void scale_from_amax(float amax, bool bf16_rule, float fmax, float* scale, float* inv) {
+  float a = amax;
+  if (bf16_rule) {
+    const float lo = round_bf16(1e-12f);
+    a = (a != a) ? a : fmaxf(a, lo);
+    float rcp = round_bf16(__fdiv_rn(1.0f, a));
+    *scale = round_bf16(__fmul_rn(rcp, fmax));
+  } else {
+    a = (a != a) ? a : fmaxf(a, 1e-12f);
+    float rcp = __fdiv_rn(1.0f, a);
+    *scale = __fmul_rn(rcp, fmax);
+  }
+  *inv = __fdiv_rn(1.0f, *scale);
+}
+
+// Block-level uint max (256 threads), result valid in thread 0.
+TCFP_DEV uint32_t block_umax(uint32_t m) {
+  __shared__ uint32_t red[kThreads / 64];
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    uint32_t other = __shfl_xor(m, o, 64);
+    m = m > other ? m : other;
+  }
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+#pragma unroll
+    for (int i = 1; i < kThreads / 64; ++i) m = m > red[i] ? m : red[i];
+  }
+  return m;
+}
+
+// Folds this workgroup's max into ws; the last workgroup to arrive turns the
+// global max into (scale, inv) in ws->scale[slot*2 .. +1] (and the optional
+// outputs) and re-zeroes the accumulator and ticket.
+TCFP_DEV void reduce_and_finalize(uint32_t m, ReduceWs* ws, int slot, bool bf16_rule, float fmax,
+                                  float* scale_out, float* inv_out) {
+  m = block_umax(m);
+  if (threadIdx.x == 0) {
+    atomicMax(&ws->amax_bits, m);
+    __threadfence();
+    unsigned int t = atomicAdd(&ws->ticket, 1u);
+    if (t == gridDim.x - 1) {
+      __threadfence();
+      uint32_t bits = atomicMax(&ws->amax_bits, 0u);
+      float scale, inv;
+      scale_from_amax(__uint_as_float(bits), bf16_rule, fmax, &scale, &inv);
+      ws->scale[slot * 2] = scale;
+      ws->scale[slot * 2 + 1] = inv;
+      if (scale_out) *scale_out = scale;
+      if (inv_out) *inv_out = inv;
+      atomicExch(&ws->amax_bits, 0u);
+      atomicExch(&ws->ticket, 0u);
+    }
+  }
+}
+
+TCFP_DEV uint32_t absbits(float v) { return __float_as_uint(v) & 0x7FFFFFFFu; }
+TCFP_DEV uint32_t umax(uint32_t a, uint32_t b) { return a > b ? a : b; }
+
+// ===========================================================================
+// Per-tensor quantisation
+// ===========================================================================
+
+// max |x (+ ef)| -> scale / inv in ws slot.
+template <typename InT, bool HAS_EF>
+__global__ __launch_bounds__(kThreads) void amax_kernel(const InT* __restrict__ x,
+                                                        const float* __restrict__ ef, int64_t n,
+                                                        ReduceWs* ws, int slot, int bf16_rule,
+                                                        float fmax, float* scale_out,
+                                                        float* inv_out) {
+  uint32_t m = 0;
+  const int64_t nvec = n >> 3;
+  const int64_t stride = int64_t(gridDim.x) * kThreads;
+  for (int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x; i < nvec; i += stride) {
+    float v[8];
+    load8(x + i * 8, v);
+    if constexpr (HAS_EF) {
+      float e[8];
+      load8(ef + i * 8, e);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = v[j] + e[j];
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) m = umax(m, absbits(v[j]));
+  }
+  for (int64_t i = nvec * 8 + int64_t(blockIdx.x) * kThreads + threadIdx.x; i < n; i += stride) {
+    float v = load1(x + i);
+    if constexpr (HAS_EF) v = v + ef[i];
+    m = umax(m, absbits(v));
+  }
+  reduce_and_finalize(m, ws, slot, bf16_rule != 0, fmax, scale_out, inv_out);
+}
+
+// q = RNE(clamp(x * scale)), flat.
+template <typename InT, int FMT>
+__global__ __launch_bounds__(kThreads) void quant_flat_kernel(const InT* __restrict__ x, int64_t n,
+                                                              const float* __restrict__ scale_p,
+                                                              uint8_t* __restrict__ q) {
+  const float s = *scale_p;
+  const float mx = FMT == TCFP_FP8_E5M2 ? kE5M2Max : kE4M3Max;
+  const int64_t nvec = n >> 3;
+  const int64_t stride = int64_t(gridDim.x) * kThreads;
+  for (int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x; i < nvec; i += stride) {
+    float v[8];
+    load8(x + i * 8, v);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = clampf(v[j] * s, mx);
+    *reinterpret_cast<uint2*>(q + i * 8) = encode8<FMT>(v);
+  }
+  for (int64_t i = nvec * 8 + int64_t(blockIdx.x) * kThreads + threadIdx.x; i < n; i += stride)
+    q[i] = uint8_t(encode1<FMT>(clampf(load1(x + i) * s, mx)));
+}
+
+// Same quantisation on 64x64 tiles, also writing the transposed codes
+// qt[c, r] through an LDS tile.
+template <typename InT, int FMT>
+__global__ __launch_bounds__(kThreads) void quant_tiled_kernel(const InT* __restrict__ x,
+                                                               int64_t rows, int64_t cols,
+                                                               const float* __restrict__ scale_p,
+                                                               uint8_t* __restrict__ q,
+                                                               uint8_t* __restrict__ qt) {
+  __shared__ uint8_t tile[64][64 + 4];
+  const float s = *scale_p;
+  const float mx = FMT == TCFP_FP8_E5M2 ? kE5M2Max : kE4M3Max;
+  const int64_t r0 = int64_t(blockIdx.y) * 64, c0 = int64_t(blockIdx.x) * 64;
+  const int t = threadIdx.x, cg = t & 15, rg = t >> 4;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int lr = rg * 4 + i;
+    const int64_t r = r0 + lr;
+    float v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t c = c0 + cg * 4 + j;
+      v[j] = (r < rows && c < cols) ? clampf(load1(x + r * cols + c) * s, mx) : 0.0f;
+    }
+#ifdef TCFP_SW_CVT
+    uint32_t code = sw4_fp8<FMT>(v[0], v[1], v[2], v[3]);
+#else
+    uint32_t code = cvt4_fp8<FMT>(v[0], v[1], v[2], v[3]);
+#endif
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t c = c0 + cg * 4 + j;
+      const uint8_t b = uint8_t(code >> (8 * j));
+      tile[lr][cg * 4 + j] = b;
+      if (r < rows && c < cols) q[r * cols + c] = b;
+    }
+  }
+  __syncthreads();
+  const int tr = t >> 2, seg = t & 3;
+  const int64_t c = c0 + tr;
+  if (c < cols) {
+#pragma unroll
+    for (int b = 0; b < 16; ++b) {
+      const int lr = seg * 16 + b;
+      const int64_t r = r0 + lr;
+      if (r < rows) qt[c * rows + r] = tile[lr][tr];
+    }
+  }
+}
+
+// ===========================================================================
+// Per-tensor dual quantisation (tcfp/nn/__init__.py:343-383)
+// ===========================================================================
+
+// Pass 2: W_hi codes and max |residual| -> scale_lo.
+template <typename InT, bool HAS_EF>
+__global__ __launch_bounds__(kThreads) void dualq_hi_kernel(const InT* __restrict__ w,
+                                                            const float* __restrict__ ef,
+                                                            int64_t n, ReduceWs* ws,
+                                                            uint8_t* __restrict__ hi,
+                                                            float* inv_lo_out) {
+  const float s_hi = ws->scale[0], inv_hi = ws->scale[1];
+  uint32_t m = 0;
+  const int64_t nvec = n >> 3;
+  const int64_t stride = int64_t(gridDim.x) * kThreads;
+  for (int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x; i < nvec; i += stride) {
+    float v[8], c[8];
+    load8(w + i * 8, v);
+    if constexpr (HAS_EF) {
+      float e[8];
+      load8(ef + i * 8, e);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = v[j] + e[j];
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) c[j] = clampf(v[j] * s_hi, kE4M3Max);
+    const uint2 code = encode8<TCFP_FP8_E4M3>(c);
+    *reinterpret_cast<uint2*>(hi + i * 8) = code;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float r = v[j] - e4m3_to_f32(byte_of(code, j)) * inv_hi;
+      m = umax(m, absbits(r));
+    }
+  }
+  for (int64_t i = nvec * 8 + int64_t(blockIdx.x) * kThreads + threadIdx.x; i < n; i += stride) {
+    float v = load1(w + i);
+    if constexpr (HAS_EF) v = v + ef[i];
+    const uint32_t code = encode1<TCFP_FP8_E4M3>(clampf(v * s_hi, kE4M3Max));
+    hi[i] = uint8_t(code);
+    m = umax(m, absbits(v - e4m3_to_f32(code) * inv_hi));
+  }
+  reduce_and_finalize(m, ws, 1, false, kE4M3Max, nullptr, inv_lo_out);
+}
+
+// Stochastic rounding of an already scaled and clamped value, following
+// stochastic_round_to_fp8_e4m3 (tcfp/core.py:418-464) with torch's cast
+// semantics (a candidate past 448 is the NaN code and is never selected).
+TCFP_DEV uint32_t sr_per_tensor(float x, float u) {
+  const uint32_t lo = f32_to_e4m3(x);
+  const float lo_f = e4m3_to_f32(lo);
+  if (x == lo_f) return lo;
+  const float d = x > lo_f ? 1.0f : (x < lo_f ? -1.0f : 0.0f);
+  uint32_t hi = f32_to_e4m3(lo_f + (d * 0.015625f) * 0.5f);
+  if (e4m3_to_f32(hi) == lo_f) {
+    const float abs_lo = fmaxf(fabsf(lo_f), 0.015625f);
+    hi = f32_to_e4m3(lo_f + (d * abs_lo) * 0.25f);
+  }
+  const float hi_f = e4m3_to_f32(hi);
+  float gap = fabsf(hi_f - lo_f);
+  gap = (gap != gap) ? gap : fmaxf(gap, 1.4e-45f);
+  float frac = fabsf(x - lo_f) / gap;
+  frac = (frac != frac) ? frac : fminf(fmaxf(frac, 0.0f), 1.0f);
+  return (u < frac) ? hi : lo;
+}
+
+// Pass 3: W_lo codes (RNE or SR) and, optionally, the new error in place.
+template <typename InT, bool HAS_EF, bool UPDATE, bool SR>
+__global__ __launch_bounds__(kThreads) void dualq_lo_kernel(const InT* __restrict__ w,
+                                                            float* __restrict__ ef, int64_t n,
+                                                            const ReduceWs* ws,
+                                                            uint8_t* __restrict__ lo,
+                                                            uint32_t k0, uint32_t k1,
+                                                            uint32_t off0, uint32_t off1) {
+  const float s_hi = ws->scale[0], inv_hi = ws->scale[1];
+  const float s_lo = ws->scale[2], inv_lo = ws->scale[3];
+  const int64_t nvec = n >> 3;
+  const int64_t stride = int64_t(gridDim.x) * kThreads;
+  for (int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x; i < nvec; i += stride) {
+    float W[8], v[8], c[8], x[8];
+    load8(w + i * 8, W);
+    if constexpr (HAS_EF) {
+      float e[8];
+      load8(ef + i * 8, e);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = W[j] + e[j];
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = W[j];
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) c[j] = clampf(v[j] * s_hi, kE4M3Max);
+    const uint2 hcode = encode8<TCFP_FP8_E4M3>(c);
+    float dh[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      dh[j] = e4m3_to_f32(byte_of(hcode, j)) * inv_hi;
+      x[j] = clampf((v[j] - dh[j]) * s_lo, kE4M3Max);
+    }
+    uint2 lcode;
+    if constexpr (SR) {
+      const uint64_t base = uint64_t(i) * 2;
+      u32x4 r0 = philox4x32_10({uint32_t(base), uint32_t(base >> 32), off0, off1}, k0, k1);
+      u32x4 r1 = philox4x32_10({uint32_t(base + 1), uint32_t((base + 1) >> 32), off0, off1}, k0, k1);
+      const uint32_t rr[8] = {r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, r1.z, r1.w};
+      uint32_t b[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) b[j] = sr_per_tensor(x[j], u32_to_unit(rr[j]));
+      lcode = make_uint2(b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24),
+                         b[4] | (b[5] << 8) | (b[6] << 16) | (b[7] << 24));
+    } else {
+      lcode = encode8<TCFP_FP8_E4M3>(x);
+    }
+    *reinterpret_cast<uint2*>(lo + i * 8) = lcode;
+    if constexpr (HAS_EF && UPDATE) {
+      float e[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float dl = e4m3_to_f32(byte_of(lcode, j)) * inv_lo;
+        e[j] = W[j] - (dh[j] + dl);
+      }
+      store8(ef + i * 8, e);
+    }
+  }
+  for (int64_t i = nvec * 8 + int64_t(blockIdx.x) * kThreads + threadIdx.x; i < n; i += stride) {
+    const float W = load1(w + i);
+    float v = W;
+    if constexpr (HAS_EF) v = W + ef[i];
+    const uint32_t hcode = encode1<TCFP_FP8_E4M3>(clampf(v * s_hi, kE4M3Max));
+    const float dh = e4m3_to_f32(hcode) * inv_hi;
+    const float x = clampf((v - dh) * s_lo, kE4M3Max);
+    uint32_t lcode;
+    if constexpr (SR) {
+      const uint64_t ctr = (uint64_t(1) << 62) + uint64_t(i);
+      u32x4 r = philox4x32_10({uint32_t(ctr), uint32_t(ctr >> 32), off0, off1}, k0, k1);
+      lcode = sr_per_tensor(x, u32_to_unit(r.x));
+    } else {
+      lcode = encode1<TCFP_FP8_E4M3>(x);
+    }
+    lo[i] = uint8_t(lcode);
+    if constexpr (HAS_EF && UPDATE) ef[i] = W - (dh + e4m3_to_f32(lcode) * inv_lo);
+  }
+}
+
+// ===========================================================================
+// Block quantisation (tcfp/kernels.py:205-275)
+// ===========================================================================
+
+// Segment geometry: one (row, K-block) segment of BS elements is read by
+// L = BS / VEC lanes with one 16-byte load each; a 256-thread workgroup
+// covers 256 / L consecutive rows of one K-block, so the int8 exponents of
+// a workgroup ([K/bs, M] layout) are contiguous.
+template <typename InT, int BS>
+struct Seg {
+  static constexpr int VEC = 16 / int(sizeof(InT));
+  static constexpr int L = BS / VEC;
+  static constexpr int ROWS = kThreads / L;
+};
+
+template <int L>
+TCFP_DEV uint32_t seg_umax(uint32_t m) {
+#pragma unroll
+  for (int o = L / 2; o > 0; o >>= 1) m = umax(m, __shfl_xor(m, o, 64));
+  return m;
+}
+
+template <typename InT>
+TCFP_DEV void loadv(const InT* p, float* v);
+template <>
+TCFP_DEV void loadv<float>(const float* p, float* v) {
+  float4 a = *reinterpret_cast<const float4*>(p);
+  v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+}
+template <>
+TCFP_DEV void loadv<uint16_t>(const uint16_t* p, float* v) { load8(p, v); }
+
+template <int N>
+TCFP_DEV void loadf(const float* p, float* v) {
+#pragma unroll
+  for (int i = 0; i < N; i += 4) {
+    float4 a = *reinterpret_cast<const float4*>(p + i);
+    v[i] = a.x; v[i + 1] = a.y; v[i + 2] = a.z; v[i + 3] = a.w;
+  }
+}
+template <int N>
+TCFP_DEV void storef(float* p, const float* v) {
+#pragma unroll
+  for (int i = 0; i < N; i += 4)
+    *reinterpret_cast<float4*>(p + i) = make_float4(v[i], v[i + 1], v[i + 2], v[i + 3]);
+}
+
+template <int N, int FMT>
+TCFP_DEV void encodeN(const float* v, uint8_t* dst) {
+  if constexpr (N == 4) {
+#ifdef TCFP_SW_CVT
+    *reinterpret_cast<uint32_t*>(dst) = sw4_fp8<FMT>(v[0], v[1], v[2], v[3]);
+#else
+    *reinterpret_cast<uint32_t*>(dst) = cvt4_fp8<FMT>(v[0], v[1], v[2], v[3]);
+#endif
+  } else {
+    *reinterpret_cast<uint2*>(dst) = encode8<FMT>(v);
+  }
+}
+
+template <int N, int FMT>
+TCFP_DEV void encode_words(const float* v, uint32_t* words) {
+#pragma unroll
+  for (int i = 0; i < N; i += 4) {
+#ifdef TCFP_SW_CVT
+    words[i / 4] = sw4_fp8<FMT>(v[i], v[i + 1], v[i + 2], v[i + 3]);
+#else
+    words[i / 4] = cvt4_fp8<FMT>(v[i], v[i + 1], v[i + 2], v[i + 3]);
+#endif
+  }
+}
+
+template <int N>
+TCFP_DEV void store_words(uint8_t* dst, const uint32_t* words) {
+  if constexpr (N == 4) *reinterpret_cast<uint32_t*>(dst) = words[0];
+  else *reinterpret_cast<uint2*>(dst) = make_uint2(words[0], words[1]);
+}
+
+TCFP_DEV uint32_t wbyte(const uint32_t* words, int j) { return (words[j >> 2] >> (8 * (j & 3))) & 0xFFu; }
+
+template <typename InT, int FMT, int BS>
+__global__ __launch_bounds__(kThreads) void block_quant_kernel(const InT* __restrict__ x,
+                                                               int64_t m, int64_t k,
+                                                               uint8_t* __restrict__ q,
+                                                               int8_t* __restrict__ exps) {
+  using G = Seg<InT, BS>;
+  constexpr int VEC = G::VEC;
+  const int64_t kb = blockIdx.y;
+  const int64_t row = int64_t(blockIdx.x) * G::ROWS + threadIdx.x / G::L;
+  const int li = threadIdx.x % G::L;
+  const bool valid = row < m;
+  const int64_t off = row * k + kb * BS + li * VEC;
+  float v[VEC];
+  if (valid) {
+    loadv<InT>(x + off, v);
+  } else {
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) v[j] = 0.0f;
+  }
+  uint32_t a = 0;
+#pragma unroll
+  for (int j = 0; j < VEC; ++j) a = umax(a, absbits(v[j]));
+  a = seg_umax<G::L>(a);
+  const float mx = FMT == TCFP_FP8_E5M2 ? kE5M2Max : kE4M3Max;
+  const int e = block_exponent(__uint_as_float(a), mx);
+  const float mul = exp2i(-e);
+#pragma unroll
+  for (int j = 0; j < VEC; ++j) v[j] = clampf(v[j] * mul, mx);
+  if (valid) {
+    encodeN<VEC, FMT>(v, q + off);
+    if (li == 0) exps[kb * m + row] = int8_t(e);
+  }
+}
+
+// Block stochastic rounding (tcfp/kernels.py:398-423): the neighbour is
+// found by a quarter-magnitude nudge under a saturating cast.
+TCFP_DEV uint32_t sr_block(float x, float u) {
+  const uint32_t rtn = f32_to_e4m3(x, true);
+  const float rtn_f = e4m3_to_f32(rtn);
+  const float diff = x - rtn_f;
+  const float d = diff >= 0.0f ? 1.0f : -1.0f;
+  const float abs_rtn = fmaxf(fabsf(rtn_f), 1e-12f);
+  const float nud = rtn_f + (d * abs_rtn) * 0.25f;
+  const uint32_t other = f32_to_e4m3(clampf(nud, kE4M3Max), true);
+  const float other_f = e4m3_to_f32(other);
+  const float g = fabsf(other_f - rtn_f);
+  const float gap = fmaxf(g, 1.4e-45f);
+  const float frac = fminf(fabsf(diff) / gap, 1.0f);
+  const bool exact = (fabsf(diff) < 1.4e-45f) || (g < 1.4e-45f);
+  return exact ? rtn : (u < frac ? other : rtn);
+}
+
+// Fused block dual quantisation + error update (tcfp/kernels.py:288-459 and
+// :1867-1873).  The error buffer is read and rewritten by the same lane.
+template <typename InT, int BS, bool HAS_EF, bool UPDATE, bool SR>
+__global__ __launch_bounds__(kThreads) void block_dualq_kernel(
+    const InT* __restrict__ w, float* __restrict__ ef, int64_t n, int64_t k,
+    uint8_t* __restrict__ hi, uint8_t* __restrict__ lo, int8_t* __restrict__ ehi,
+    int8_t* __restrict__ elo, uint32_t k0, uint32_t k1, uint32_t off0, uint32_t off1) {
+  using G = Seg<InT, BS>;
+  constexpr int VEC = G::VEC;
+  const int64_t kb = blockIdx.y;
+  const int64_t row = int64_t(blockIdx.x) * G::ROWS + threadIdx.x / G::L;
+  const int li = threadIdx.x % G::L;
+  const bool valid = row < n;
+  const int64_t off = row * k + kb * BS + li * VEC;
+  float W[VEC], v[VEC];
+  if (valid) {
+    loadv<InT>(w + off, W);
+  } else {
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) W[j] = 0.0f;
+  }
+  if constexpr (HAS_EF) {
+    float e[VEC];
+    if (valid) {
+      loadf<VEC>(ef + off, e);
+    } else {
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) e[j] = 0.0f;
+    }
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) v[j] = W[j] + e[j];
+  } else {
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) v[j] = W[j];
+  }
+  // W_hi
+  uint32_t a = 0;
+#pragma unroll
+  for (int j = 0; j < VEC; ++j) a = umax(a, absbits(v[j]));
+  a = seg_umax<G::L>(a);
+  const int e_hi = block_exponent(__uint_as_float(a), kE4M3Max);
+  const float mul_hi = exp2i(-e_hi), s_hi = exp2i(e_hi);
+  float c[VEC];
+#pragma unroll
+  for (int j = 0; j < VEC; ++j) c[j] = clampf(v[j] * mul_hi, kE4M3Max);
+  uint32_t hc[VEC / 4];
+  encode_words<VEC, TCFP_FP8_E4M3>(c, hc);
+  float dh[VEC], r[VEC];
+  uint32_t b = 0;
+#pragma unroll
+  for (int j = 0; j < VEC; ++j) {
+    dh[j] = e4m3_to_f32(wbyte(hc, j)) * s_hi;
+    r[j] = v[j] - dh[j];
+    b = umax(b, absbits(r[j]));
+  }
+  // W_lo
+  b = seg_umax<G::L>(b);
+  const float amax_lo = __uint_as_float(b);
+  const bool zero = amax_lo < 1e-12f;
+  const int e_lo = block_exponent(amax_lo, kE4M3Max);
+  const float mul_lo = zero ? 1.0f : exp2i(-e_lo);
+#pragma unroll
+  for (int j = 0; j < VEC; ++j) c[j] = clampf(r[j] * mul_lo, kE4M3Max);
+  uint32_t lc[VEC / 4];
+  if constexpr (SR) {
+    const int64_t gidx = off;  // element index of c[0] in the [n, k] matrix
+#pragma unroll
+    for (int j = 0; j < VEC; j += 4) {
+      const uint64_t ctr = uint64_t(gidx + j) >> 2;
+      u32x4 rr = philox4x32_10({uint32_t(ctr), uint32_t(ctr >> 32), off0, off1}, k0, k1);
+      lc[j / 4] = sr_block(c[j], u32_to_unit(rr.x)) | (sr_block(c[j + 1], u32_to_unit(rr.y)) << 8) |
+                  (sr_block(c[j + 2], u32_to_unit(rr.z)) << 16) |
+                  (sr_block(c[j + 3], u32_to_unit(rr.w)) << 24);
+    }
+  } else {
+    encode_words<VEC, TCFP_FP8_E4M3>(c, lc);
+  }
+  const int e_lo_store = zero ? -128 : e_lo;
+  if (valid) {
+    store_words<VEC>(hi + off, hc);
+    store_words<VEC>(lo + off, lc);
+    if (li == 0) {
+      ehi[kb * n + row] = int8_t(e_hi);
+      elo[kb * n + row] = int8_t(e_lo_store);
+    }
+    if constexpr (HAS_EF && UPDATE) {
+      const float s_lo = exp2i(e_lo_store);
+      float e[VEC];
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) e[j] = (W[j] - dh[j]) - e4m3_to_f32(wbyte(lc, j)) * s_lo;
+      storef<VEC>(ef + off, e);
+    }
+  }
+}
+
+template <int FMT>
+__global__ __launch_bounds__(kThreads) void block_dequant_kernel(const uint8_t* __restrict__ q,
+                                                                 const int8_t* __restrict__ exps,
+                                                                 int64_t m, int64_t k, int bs,
+                                                                 float* __restrict__ out) {
+  const int64_t n = m * k;
+  const int64_t stride = int64_t(gridDim.x) * kThreads;
+  for (int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x; i < n; i += stride) {
+    const int64_t r = i / k, c = i - r * k;
+    out[i] = fp8_to_f32<FMT>(q[i]) * exp2i(exps[(c / bs) * m + r]);
+  }
+}
+
+// ===========================================================================
+// Byte transpose through LDS (64x64 tiles)
+// ===========================================================================
+__global__ __launch_bounds__(kThreads) void transpose_u8_kernel(const uint8_t* __restrict__ src,
+                                                                int64_t rows, int64_t cols,
+                                                                uint8_t* __restrict__ dst) {
+  __shared__ uint8_t tile[64][64 + 4];
+  const int64_t r0 = int64_t(blockIdx.y) * 64, c0 = int64_t(blockIdx.x) * 64;
+  const int t = threadIdx.x;
+  const int lr = t >> 2, seg = t & 3;
+  const int64_t r = r0 + lr;
+#pragma unroll
+  for (int b = 0; b < 16; ++b) {
+    const int64_t c = c0 + seg * 16 + b;
+    tile[lr][seg * 16 + b] = (r < rows && c < cols) ? src[r * cols + c] : 0;
+  }
+  __syncthreads();
+  const int64_t c = c0 + lr;
+  if (c < cols) {
+#pragma unroll
+    for (int b = 0; b < 16; ++b) {
+      const int64_t rr = r0 + seg * 16 + b;
+      if (rr < rows) dst[c * rows + rr] = tile[seg * 16 + b][lr];
+    }
+  }
+}
+
+// ===========================================================================
+// Self tests
+// ===========================================================================
+template <int FMT>
+__global__ __launch_bounds__(kThreads) void selftest_cvt_kernel(uint32_t lo, uint32_t hi,
+                                                                unsigned long long* bad) {
+  const uint64_t span = uint64_t(hi) - lo + 1;
+  const uint64_t stride = uint64_t(gridDim.x) * kThreads;
+  uint32_t cnt = 0;
+  for (uint64_t i = uint64_t(blockIdx.x) * kThreads + threadIdx.x; i < span; i += stride) {
+    const float x = __uint_as_float(lo + uint32_t(i));
+    const uint32_t h = cvt4_fp8<FMT>(x, -x, 0.f, 0.f) & 0xFFFFu;
+    const uint32_t s = f32_to_fp8<FMT>(x) | (f32_to_fp8<FMT>(-x) << 8);
+    cnt += (h != s);
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) cnt += __shfl_xor(cnt, o, 64);
+  if ((threadIdx.x & 63) == 0 && cnt) atomicAdd(bad, (unsigned long long)cnt);
+}
+
+__global__ __launch_bounds__(kThreads) void selftest_philox_kernel(uint32_t c0, uint32_t c1,
+                                                                   uint32_t c2, uint32_t c3,
+                                                                   uint32_t k0, uint32_t k1,
+                                                                   int64_t n, uint32_t* out) {
+  const int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+  if (i >= n) return;
+  u32x4 r = philox4x32_10({c0 + uint32_t(i), c1, c2, c3}, k0, k1);
+  out[4 * i] = r.x; out[4 * i + 1] = r.y; out[4 * i + 2] = r.z; out[4 * i + 3] = r.w;
+}
+
+// inv = 1 / scale (IEEE) for an explicitly supplied scale (tcfp/core.py:105).
+__global__ void inverse_kernel(const float* s, float* inv, float* echo) {
+  if (threadIdx.x != 0) return;
+  const float v = *s;
+  *inv = __fdiv_rn(1.0f, v);
+  if (echo) *echo = v;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace
+
+// ===========================================================================
+// C ABI
+// ===========================================================================
+extern "C" {
+
+const char* tcfp_status_string(int status) {
+  switch (status) {
+    case TCFP_OK: return "ok";
+    case TCFP_ERR_SHAPE: return "invalid shape, leading dimension or divisibility";
+    case TCFP_ERR_DTYPE: return "unsupported dtype or fp8 format";
+    case TCFP_ERR_ALIGN: return "pointer or leading dimension not 16-byte aligned";
+    case TCFP_ERR_HIP: return "HIP runtime error";
+    case TCFP_ERR_WORKSPACE: return "workspace missing";
+    case TCFP_ERR_EXCLUSIVE: return "stochastic_lo and error feedback are mutually exclusive";
+    default: return "unknown status";
+  }
+}
+
+size_t tcfp_workspace_bytes(void) { return 256; }
+
+int tcfp_quantize_per_tensor(const void* x, int x_dtype, int64_t rows, int64_t cols,
+                             int fp8_fmt, const float* scale_in, uint8_t* q, uint8_t* q_t,
+                             float* scale_out, float* inv_out, void* workspace,
+                             void* stream) {
+  if (rows < 0 || cols < 0) return TCFP_ERR_SHAPE;
+  if (x_dtype != TCFP_DTYPE_F32 && x_dtype != TCFP_DTYPE_BF16) return TCFP_ERR_DTYPE;
+  if (fp8_fmt != TCFP_FP8_E4M3 && fp8_fmt != TCFP_FP8_E5M2) return TCFP_ERR_DTYPE;
+  if (!aligned16(x) || !inv_out) return TCFP_ERR_ALIGN;
+  if (!scale_in && !workspace) return TCFP_ERR_WORKSPACE;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t n = rows * cols;
+  const float fmax = fp8_fmt == TCFP_FP8_E5M2 ? kE5M2Max : kE4M3Max;
+  ReduceWs* ws = static_cast<ReduceWs*>(workspace);
+  const bool bf = x_dtype == TCFP_DTYPE_BF16;
+  const float* scale_p;
+  if (scale_in) {
+    scale_p = scale_in;
+    // inv = 1/scale and scale echo: reuse the finalize path on a 1-thread grid
+    // is overkill; compute with a tiny kernel below.
+  } else {
+    const int g = grid_for((n + 7) / 8, 4);
+    if (bf)
+      amax_kernel<uint16_t, false><<<g, kThreads, 0, st>>>(static_cast<const uint16_t*>(x),
+                                                           nullptr, n, ws, 0, 1, fmax,
+                                                           scale_out, inv_out);
+    else
+      amax_kernel<float, false><<<g, kThreads, 0, st>>>(static_cast<const float*>(x), nullptr,
+                                                        n, ws, 0, 0, fmax, scale_out, inv_out);
+  }
+  if (scale_in) inverse_kernel<<<1, 64, 0, st>>>(scale_in, inv_out, scale_out);
+  else scale_p = &ws->scale[0];
+  if (n == 0) return launch_status();
+  if (q_t) {
+    dim3 grid(unsigned((cols + 63) / 64), unsigned((rows + 63) / 64));
+#define TCFP_QT(T, F)                                                                         \
+  quant_tiled_kernel<T, F><<<grid, kThreads, 0, st>>>(static_cast<const T*>(x), rows, cols, \
+                                                       scale_p, q, q_t)
+    if (bf) {
+      if (fp8_fmt == TCFP_FP8_E5M2) TCFP_QT(uint16_t, TCFP_FP8_E5M2); else TCFP_QT(uint16_t, TCFP_FP8_E4M3);
+    } else {
+      if (fp8_fmt == TCFP_FP8_E5M2) TCFP_QT(float, TCFP_FP8_E5M2); else TCFP_QT(float, TCFP_FP8_E4M3);
+    }
+#undef TCFP_QT
+  } else {
+    if (!aligned16(q) && n >= 8) {
+      // the flat kernel stores 8 codes at a time
+      if ((reinterpret_cast<uintptr_t>(q) & 7u) != 0) return TCFP_ERR_ALIGN;
+    }
+    const int g = grid_for((n + 7) / 8, 16);
+#define TCFP_QF(T, F) \
+  quant_flat_kernel<T, F><<<g, kThreads, 0, st>>>(static_cast<const T*>(x), n, scale_p, q)
+    if (bf) {
+      if (fp8_fmt == TCFP_FP8_E5M2) TCFP_QF(uint16_t, TCFP_FP8_E5M2); else TCFP_QF(uint16_t, TCFP_FP8_E4M3);
+    } else {
+      if (fp8_fmt == TCFP_FP8_E5M2) TCFP_QF(float, TCFP_FP8_E5M2); else TCFP_QF(float, TCFP_FP8_E4M3);
+    }
+#undef TCFP_QF
+  }
+  return launch_status();
+}
+
+int tcfp_dual_quantize_per_tensor(const void* w, int w_dtype, int64_t n, int64_t k,
+                                  float* ef, int update_ef, int stochastic_lo,
+                                  uint64_t seed, uint64_t offset, uint8_t* w_hi,
+                                  uint8_t* w_lo, float* inv_hi, float* inv_lo,
+                                  uint8_t* w_hi_t, uint8_t* w_lo_t, void* workspace,
+                                  void* stream) {
+  if (n < 0 || k < 0) return TCFP_ERR_SHAPE;
+  if (w_dtype != TCFP_DTYPE_F32 && w_dtype != TCFP_DTYPE_BF16) return TCFP_ERR_DTYPE;
+  if (!workspace) return TCFP_ERR_WORKSPACE;
+  if (!aligned16(w) || !aligned16(w_hi) || !aligned16(w_lo) || (ef && !aligned16(ef)))
+    return TCFP_ERR_ALIGN;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  ReduceWs* ws = static_cast<ReduceWs*>(workspace);
+  const int64_t total = n * k;
+  const int gr = grid_for((total + 7) / 8, 4);
+  const int gq = grid_for((total + 7) / 8, 8);
+  const bool bf = w_dtype == TCFP_DTYPE_BF16;
+  const bool has_ef = ef != nullptr;
+  const bool upd = has_ef && update_ef;
+  const uint32_t k0 = uint32_t(seed), k1 = uint32_t(seed >> 32);
+  const uint32_t o0 = uint32_t(offset), o1 = uint32_t(offset >> 32);
+
+#define TCFP_DQ(T, EF)                                                                        \
+  do {                                                                                        \
+    const T* wp = static_cast<const T*>(w);                                                   \
+    amax_kernel<T, EF><<<gr, kThreads, 0, st>>>(wp, ef, total, ws, 0, 0, kE4M3Max, nullptr,  \
+                                                 inv_hi);                                     \
+    dualq_hi_kernel<T, EF><<<gr, kThreads, 0, st>>>(wp, ef, total, ws, w_hi, inv_lo);         \
+    if (stochastic_lo) {                                                                      \
+      if (upd)                                                                                \
+        dualq_lo_kernel<T, EF, EF, true><<<gq, kThreads, 0, st>>>(wp, ef, total, ws, w_lo, k0, \
+                                                                  k1, o0, o1);                \
+      else                                                                                    \
+        dualq_lo_kernel<T, EF, false, true><<<gq, kThreads, 0, st>>>(wp, ef, total, ws, w_lo,  \
+                                                                     k0, k1, o0, o1);         \
+    } else {                                                                                  \
+      if (upd)                                                                                \
+        dualq_lo_kernel<T, EF, EF, false><<<gq, kThreads, 0, st>>>(wp, ef, total, ws, w_lo,    \
+                                                                   k0, k1, o0, o1);           \
+      else                                                                                    \
+        dualq_lo_kernel<T, EF, false, false><<<gq, kThreads, 0, st>>>(wp, ef, total, ws, w_lo, \
+                                                                      k0, k1, o0, o1);        \
+    }                                                                                         \
+  } while (0)
+
+  if (bf) {
+    if (has_ef) TCFP_DQ(uint16_t, true); else TCFP_DQ(uint16_t, false);
+  } else {
+    if (has_ef) TCFP_DQ(float, true); else TCFP_DQ(float, false);
+  }
+#undef TCFP_DQ
+  if (w_hi_t || w_lo_t) {
+    dim3 grid(unsigned((k + 63) / 64), unsigned((n + 63) / 64));
+    if (w_hi_t) transpose_u8_kernel<<<grid, kThreads, 0, st>>>(w_hi, n, k, w_hi_t);
+    if (w_lo_t) transpose_u8_kernel<<<grid, kThreads, 0, st>>>(w_lo, n, k, w_lo_t);
+  }
+  return launch_status();
+}
+
+int tcfp_block_quantize(const void* x, int x_dtype, int64_t m, int64_t k, int block,
+                        int fp8_fmt, uint8_t* q, int8_t* exps, void* stream) {
+  if (m < 0 || k < 0) return TCFP_ERR_SHAPE;
+  if (block != 32 && block != 64 && block != 128) return TCFP_ERR_SHAPE;
+  if (k % block != 0) return TCFP_ERR_SHAPE;
+  if (x_dtype != TCFP_DTYPE_F32 && x_dtype != TCFP_DTYPE_BF16) return TCFP_ERR_DTYPE;
+  if (fp8_fmt != TCFP_FP8_E4M3 && fp8_fmt != TCFP_FP8_E5M2) return TCFP_ERR_DTYPE;
+  if (!aligned16(x) || !aligned16(q)) return TCFP_ERR_ALIGN;
+  if (m == 0 || k == 0) return TCFP_OK;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const unsigned kbs = unsigned(k / block);
+#define TCFP_BQ(T, F, B)                                                                    \
+  do {                                                                                      \
+    dim3 grid(unsigned((m + Seg<T, B>::ROWS - 1) / Seg<T, B>::ROWS), kbs);                  \
+    block_quant_kernel<T, F, B><<<grid, kThreads, 0, st>>>(static_cast<const T*>(x), m, k,  \
+                                                           q, exps);                        \
+  } while (0)
+#define TCFP_BQ_B(T, F)                                 \
+  do {                                                  \
+    if (block == 32) TCFP_BQ(T, F, 32);                 \
+    else if (block == 64) TCFP_BQ(T, F, 64);            \
+    else TCFP_BQ(T, F, 128);                            \
+  } while (0)
+  if (x_dtype == TCFP_DTYPE_BF16) {
+    if (fp8_fmt == TCFP_FP8_E5M2) TCFP_BQ_B(uint16_t, TCFP_FP8_E5M2); else TCFP_BQ_B(uint16_t, TCFP_FP8_E4M3);
+  } else {
+    if (fp8_fmt == TCFP_FP8_E5M2) TCFP_BQ_B(float, TCFP_FP8_E5M2); else TCFP_BQ_B(float, TCFP_FP8_E4M3);
+  }
+#undef TCFP_BQ_B
+#undef TCFP_BQ
+  return launch_status();
+}
+
+int tcfp_block_dual_quantize(const void* w, int w_dtype, int64_t n, int64_t k, int block,
+                             float* ef, int update_ef, int stochastic_lo, uint64_t seed,
+                             uint64_t offset, uint8_t* w_hi, uint8_t* w_lo, int8_t* e_hi,
+                             int8_t* e_lo, void* stream) {
+  if (n < 0 || k < 0) return TCFP_ERR_SHAPE;
+  if (block != 32 && block != 64 && block != 128) return TCFP_ERR_SHAPE;
+  if (k % block != 0) return TCFP_ERR_SHAPE;
+  if (w_dtype != TCFP_DTYPE_F32 && w_dtype != TCFP_DTYPE_BF16) return TCFP_ERR_DTYPE;
+  if (stochastic_lo && ef) return TCFP_ERR_EXCLUSIVE;
+  if (!aligned16(w) || !aligned16(w_hi) || !aligned16(w_lo) || (ef && !aligned16(ef)))
+    return TCFP_ERR_ALIGN;
+  if (n == 0 || k == 0) return TCFP_OK;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const unsigned kbs = unsigned(k / block);
+  const uint32_t k0 = uint32_t(seed), k1 = uint32_t(seed >> 32);
+  const uint32_t o0 = uint32_t(offset), o1 = uint32_t(offset >> 32);
+  const bool upd = ef && update_ef;
+#define TCFP_BDQ(T, B, EF, UP, SR)                                                             \
+  do {                                                                                         \
+    dim3 grid(unsigned((n + Seg<T, B>::ROWS - 1) / Seg<T, B>::ROWS), kbs);                     \
+    block_dualq_kernel<T, B, EF, UP, SR><<<grid, kThreads, 0, st>>>(                           \
+        static_cast<const T*>(w), ef, n, k, w_hi, w_lo, e_hi, e_lo, k0, k1, o0, o1);           \
+  } while (0)
+#define TCFP_BDQ_MODE(T, B)                                     \
+  do {                                                          \
+    if (stochastic_lo) TCFP_BDQ(T, B, false, false, true);      \
+    else if (ef && upd) TCFP_BDQ(T, B, true, true, false);      \
+    else if (ef) TCFP_BDQ(T, B, true, false, false);            \
+    else TCFP_BDQ(T, B, false, false, false);                   \
+  } while (0)
+#define TCFP_BDQ_B(T)                                 \
+  do {                                                \
+    if (block == 32) TCFP_BDQ_MODE(T, 32);            \
+    else if (block == 64) TCFP_BDQ_MODE(T, 64);       \
+    else TCFP_BDQ_MODE(T, 128);                       \
+  } while (0)
+  if (w_dtype == TCFP_DTYPE_BF16) TCFP_BDQ_B(uint16_t); else TCFP_BDQ_B(float);
+#undef TCFP_BDQ_B
+#undef TCFP_BDQ_MODE
+#undef TCFP_BDQ
+  return launch_status();
+}
+
+int tcfp_block_dequantize(const uint8_t* q, int fp8_fmt, const int8_t* exps, int64_t m,
+                          int64_t k, int block, float* out, void* stream) {
+  if (m < 0 || k < 0 || block <= 0 || k % block != 0) return TCFP_ERR_SHAPE;
+  if (fp8_fmt != TCFP_FP8_E4M3 && fp8_fmt != TCFP_FP8_E5M2) return TCFP_ERR_DTYPE;
+  if (m == 0 || k == 0) return TCFP_OK;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int g = grid_for(m * k, 16);
+  if (fp8_fmt == TCFP_FP8_E5M2)
+    block_dequant_kernel<TCFP_FP8_E5M2><<<g, kThreads, 0, st>>>(q, exps, m, k, block, out);
+  else
+    block_dequant_kernel<TCFP_FP8_E4M3><<<g, kThreads, 0, st>>>(q, exps, m, k, block, out);
+  return launch_status();
+}
+
+int tcfp_transpose_u8(const uint8_t* src, int64_t rows, int64_t cols, uint8_t* dst,
+                      void* stream) {
+  if (rows < 0 || cols < 0) return TCFP_ERR_SHAPE;
+  if (rows == 0 || cols == 0) return TCFP_OK;
+  dim3 grid(unsigned((cols + 63) / 64), unsigned((rows + 63) / 64));
+  transpose_u8_kernel<<<grid, kThreads, 0, static_cast<hipStream_t>(stream)>>>(src, rows, cols,
+                                                                               dst);
+  return launch_status();
+}
+
+int tcfp_selftest_fp8_cvt(uint32_t lo_bits, uint32_t hi_bits, int fp8_fmt,
+                          unsigned long long* mismatches, void* stream) {
+  if (hi_bits < lo_bits) return TCFP_ERR_SHAPE;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int g = num_cu() * 8;
+  if (fp8_fmt == TCFP_FP8_E5M2)
+    selftest_cvt_kernel<TCFP_FP8_E5M2><<<g, kThreads, 0, st>>>(lo_bits, hi_bits, mismatches);
+  else if (fp8_fmt == TCFP_FP8_E4M3)
+    selftest_cvt_kernel<TCFP_FP8_E4M3><<<g, kThreads, 0, st>>>(lo_bits, hi_bits, mismatches);
+  else
+    return TCFP_ERR_DTYPE;
+  return launch_status();
+}
+
+int tcfp_selftest_philox(uint32_t ctr0, uint32_t ctr1, uint32_t ctr2, uint32_t ctr3,
+                         uint32_t k0, uint32_t k1, int64_t n, uint32_t* out, void* stream) {
+  if (n <= 0) return n == 0 ? TCFP_OK : TCFP_ERR_SHAPE;
+  const int g = int((n + kThreads - 1) / kThreads);
+  selftest_philox_kernel<<<g, kThreads, 0, static_cast<hipStream_t>(stream)>>>(
+      ctr0, ctr1, ctr2, ctr3, k0, k1, n, out);
+  return launch_status();
+}
+
+}  // extern "C"

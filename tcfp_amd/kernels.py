@@ -1,0 +1,395 @@
+"""Operator API of the TCFP-12 hot path, backed by hand-written HIP (gfx950).
+
+Names, argument meaning, output layouts and error behaviour follow the
+reference's Python wrappers (``tcfp/kernels.py:1545-2469``) so that
+``tcfp_amd.nn`` -- and users of the reference's operator layer -- can switch
+over unchanged.  Every op runs the HIP kernels in ``libtcfp_hip.so`` on the
+tensors' GPU and current stream; there is no CPU or Triton path.
+
+Additions over the reference interface, all keyword-only:
+
+* ``out_dtype`` on the GEMMs (bf16 output for the raw-GEMM benchmark),
+* ``bias`` fused into the GEMM epilogue,
+* transposed operand copies (``w_hi_t``/``w_lo_t``) so dgrad and wgrad use
+  the same K-contiguous MFMA kernel as the forward.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _hip
+from ._hip import DTYPE_BF16, DTYPE_F32, FP8_E4M3, FP8_E5M2, check, ptr
+
+_FP8_E4M3_MAX = 448.0
+_FP8_E5M2_MAX = 57344.0
+
+_FMT = {torch.float8_e4m3fn: FP8_E4M3, torch.float8_e5m2: FP8_E5M2}
+
+
+def is_hip_available() -> bool:
+    """HIP library built and a GPU visible."""
+    return _hip.is_available()
+
+
+def _fmt(dtype: torch.dtype) -> int:
+    try:
+        return _FMT[dtype]
+    except KeyError:
+        raise TypeError(f"unsupported fp8 dtype {dtype}") from None
+
+
+def _in_dtype(t: torch.Tensor) -> int:
+    if t.dtype == torch.float32:
+        return DTYPE_F32
+    if t.dtype == torch.bfloat16:
+        return DTYPE_BF16
+    raise TypeError(f"unsupported input dtype {t.dtype}: expected float32 or bfloat16")
+
+
+def _out_dtype(dtype: torch.dtype) -> int:
+    if dtype == torch.float32:
+        return DTYPE_F32
+    if dtype == torch.bfloat16:
+        return DTYPE_BF16
+    raise TypeError(f"unsupported output dtype {dtype}")
+
+
+def _scalar(t: torch.Tensor, name: str) -> torch.Tensor:
+    if t.numel() != 1 or t.dtype != torch.float32:
+        raise ValueError(f"{name} must be a single-element float32 tensor")
+    return t if t.is_contiguous() else t.contiguous()
+
+
+# ---------------------------------------------------------------------------
+# Per-tensor quantisation
+# ---------------------------------------------------------------------------
+
+
+def quantize_per_tensor(
+    x: torch.Tensor,
+    fp8_dtype: torch.dtype = torch.float8_e4m3fn,
+    scale: torch.Tensor | None = None,
+    transpose: bool = False,
+    return_scale: bool = False,
+):
+    """Per-tensor FP8 cast with amax scaling (``to_fp8_e4m3`` / ``to_fp8_e5m2``
+    semantics, reference ``tcfp/core.py:85-158``).
+
+    Returns ``(q, inv)``, plus ``q_t`` ([cols, rows], the transposed codes of
+    the 2-D view) when ``transpose``, plus the fp32 ``scale`` when
+    ``return_scale``.  ``x`` is viewed as ``[numel / x.shape[-1], x.shape[-1]]``.
+    """
+    dev = _hip.require_gpu(x, scale)
+    xc = x if x.is_contiguous() else x.contiguous()
+    cols = xc.shape[-1] if xc.dim() > 0 else 1
+    rows = xc.numel() // cols if cols else 0
+    q = torch.empty(x.shape, dtype=fp8_dtype, device=dev)
+    q_t = torch.empty((cols, rows), dtype=fp8_dtype, device=dev) if transpose else None
+    inv = torch.empty(1, dtype=torch.float32, device=dev)
+    scale_out = torch.empty(1, dtype=torch.float32, device=dev) if return_scale else None
+    s_in = _scalar(scale.to(torch.float32), "scale") if scale is not None else None
+    ws = _hip.workspace(dev) if scale is None else None
+    check(
+        _hip.lib().tcfp_quantize_per_tensor(
+            ptr(xc), _in_dtype(xc), rows, cols, _fmt(fp8_dtype), ptr(s_in), ptr(q), ptr(q_t),
+            ptr(scale_out), ptr(inv), ptr(ws), _hip.stream_of(dev),
+        ),
+        "quantize_per_tensor",
+    )
+    out = (q, inv)
+    if transpose:
+        out = out + (q_t,)
+    if return_scale:
+        out = out + (scale_out,)
+    return out
+
+
+def dual_quantize_per_tensor(
+    weight: torch.Tensor,
+    error_buf: torch.Tensor | None = None,
+    update_ef: bool = True,
+    stochastic_lo: bool = False,
+    transposed: bool = False,
+    seed: int | None = None,
+):
+    """W (+ error feedback) -> (W_hi, W_lo, inv_hi, inv_lo[, W_hi^T, W_lo^T]).
+
+    The per-tensor decomposition of ``_TCFP12TensorCoreFunction.forward``
+    (reference ``tcfp/nn/__init__.py:343-383``).  ``error_buf`` ([N, K]
+    fp32) is read as the previous error and, when ``update_ef``, overwritten
+    in place with ``W - (deq(hi) + deq(lo))``.  ``stochastic_lo`` rounds
+    W_lo stochastically (SRR); the Philox key is drawn from torch's CPU
+    generator unless ``seed`` is given.
+    """
+    dev = _hip.require_gpu(weight, error_buf)
+    assert weight.dim() == 2, "weight must be 2-D (N, K)"
+    w = weight if weight.is_contiguous() else weight.contiguous()
+    n, k = w.shape
+    if error_buf is not None:
+        assert error_buf.dtype == torch.float32, "error_buf must be float32"
+        assert error_buf.shape == (n, k), (
+            f"error_buf shape {tuple(error_buf.shape)} != weight shape {(n, k)}"
+        )
+        assert error_buf.is_contiguous(), "error_buf must be contiguous"
+    w_hi = torch.empty((n, k), dtype=torch.float8_e4m3fn, device=dev)
+    w_lo = torch.empty((n, k), dtype=torch.float8_e4m3fn, device=dev)
+    inv_hi = torch.empty(1, dtype=torch.float32, device=dev)
+    inv_lo = torch.empty(1, dtype=torch.float32, device=dev)
+    w_hi_t = torch.empty((k, n), dtype=torch.float8_e4m3fn, device=dev) if transposed else None
+    w_lo_t = torch.empty((k, n), dtype=torch.float8_e4m3fn, device=dev) if transposed else None
+    if stochastic_lo and seed is None:
+        seed = int(torch.randint(0, 2**62, (1,)).item())
+    check(
+        _hip.lib().tcfp_dual_quantize_per_tensor(
+            ptr(w), _in_dtype(w), n, k, ptr(error_buf), int(bool(update_ef)),
+            int(bool(stochastic_lo)), int(seed or 0), 0, ptr(w_hi), ptr(w_lo), ptr(inv_hi),
+            ptr(inv_lo), ptr(w_hi_t), ptr(w_lo_t), ptr(_hip.workspace(dev)),
+            _hip.stream_of(dev),
+        ),
+        "dual_quantize_per_tensor",
+    )
+    if transposed:
+        return w_hi, w_lo, inv_hi, inv_lo, w_hi_t, w_lo_t
+    return w_hi, w_lo, inv_hi, inv_lo
+
+
+def transpose_fp8(t: torch.Tensor) -> torch.Tensor:
+    """Contiguous transpose of a 2-D 8-bit tensor (HIP, LDS-tiled)."""
+    dev = _hip.require_gpu(t)
+    assert t.dim() == 2 and t.element_size() == 1, "expects a 2-D 8-bit tensor"
+    src = t if t.is_contiguous() else t.contiguous()
+    rows, cols = src.shape
+    out = torch.empty((cols, rows), dtype=t.dtype, device=dev)
+    check(
+        _hip.lib().tcfp_transpose_u8(ptr(src), rows, cols, ptr(out), _hip.stream_of(dev)),
+        "transpose_fp8",
+    )
+    return out
+
+
+# ---------------------------------------------------------------------------
+# GEMMs
+# ---------------------------------------------------------------------------
+
+
+def _gemm_operand(t: torch.Tensor, name: str) -> torch.Tensor:
+    if t.dtype not in _FMT:
+        raise TypeError(f"{name} must be float8_e4m3fn or float8_e5m2, got {t.dtype}")
+    if t.dim() != 2:
+        raise ValueError(f"{name} must be 2-D")
+    if t.stride(1) != 1 or t.stride(0) % 16 != 0 or t.data_ptr() % 16 != 0:
+        t = t.contiguous()
+    return t
+
+
+def _dual_gemm(a, b_hi, b_lo, s_a, s_hi, s_lo, bias, out_dtype):
+    dev = _hip.require_gpu(a, b_hi, b_lo, s_a, s_hi, s_lo, bias)
+    a = _gemm_operand(a, "A")
+    b_hi = _gemm_operand(b_hi, "B_hi")
+    b_lo = _gemm_operand(b_lo, "B_lo") if b_lo is not None else None
+    m, k = a.shape
+    n = b_hi.shape[0]
+    if k % 16 != 0:
+        raise ValueError(f"K ({k}) must be divisible by 16")
+    if b_hi.stride(0) != (b_lo.stride(0) if b_lo is not None else b_hi.stride(0)):
+        b_lo = b_lo.contiguous()
+        b_hi = b_hi.contiguous()
+    out = torch.empty((m, n), dtype=out_dtype, device=dev)
+    if bias is not None:
+        bias = bias.to(torch.float32).contiguous()
+        assert bias.shape == (n,), f"bias shape {tuple(bias.shape)} != ({n},)"
+    check(
+        _hip.lib().tcfp_dual_gemm(
+            ptr(a), _fmt(a.dtype), a.stride(0), ptr(b_hi), ptr(b_lo), _fmt(b_hi.dtype),
+            b_hi.stride(0), m, n, k, ptr(_scalar(s_a, "scale_a")), ptr(_scalar(s_hi, "scale_hi")),
+            ptr(_scalar(s_lo, "scale_lo")) if s_lo is not None else None, ptr(bias), ptr(out),
+            _out_dtype(out_dtype), n, _hip.stream_of(dev),
+        ),
+        "dual_gemm",
+    )
+    return out
+
+
+def fused_dual_gemm_forward(
+    act_fp8: torch.Tensor,
+    w_hi_fp8: torch.Tensor,
+    w_lo_fp8: torch.Tensor,
+    act_inv: torch.Tensor,
+    w_hi_inv: torch.Tensor,
+    w_lo_inv: torch.Tensor,
+    *,
+    bias: torch.Tensor | None = None,
+    out_dtype: torch.dtype = torch.float32,
+) -> torch.Tensor:
+    """``(act @ W_hi.T) * s_a s_hi + (act @ W_lo.T) * s_a s_lo`` (+ bias).
+
+    Reference: ``fused_dual_gemm_forward`` (``tcfp/kernels.py:1545-1601``)
+    and ``cuda_ext_dual_gemm_forward`` (``tcfp/cuda_ext.py:241-259``).
+    act [M, K], W [N, K] FP8; returns [M, N] (fp32 by default).
+    """
+    M, K = act_fp8.shape
+    N, K2 = w_hi_fp8.shape
+    assert K == K2 and tuple(w_lo_fp8.shape) == (N, K), (
+        f"Shape mismatch: act({M},{K}), w_hi({N},{K2}), w_lo{tuple(w_lo_fp8.shape)}"
+    )
+    return _dual_gemm(act_fp8, w_hi_fp8, w_lo_fp8, act_inv, w_hi_inv, w_lo_inv, bias, out_dtype)
+
+
+def fused_dual_gemm_backward_dx(
+    grad_fp8: torch.Tensor,
+    w_hi_fp8: torch.Tensor,
+    w_lo_fp8: torch.Tensor,
+    grad_inv: torch.Tensor,
+    w_hi_inv: torch.Tensor,
+    w_lo_inv: torch.Tensor,
+    *,
+    w_hi_t: torch.Tensor | None = None,
+    w_lo_t: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """``dX = (grad @ W_hi) s_g s_hi + (grad @ W_lo) s_g s_lo`` (fp32 [M, D_in]).
+
+    Reference: ``fused_dual_gemm_backward_dx`` (``tcfp/kernels.py:1604-1666``).
+    grad [M, D_out] (E5M2), W [D_out, D_in].  ``w_hi_t``/``w_lo_t`` are the
+    [D_in, D_out] copies emitted by the dual-quant kernel; without them the
+    transposes are made here.
+    """
+    M, D_out = grad_fp8.shape
+    D_out2, D_in = w_hi_fp8.shape
+    assert D_out == D_out2 and tuple(w_lo_fp8.shape) == (D_out, D_in), (
+        f"Shape mismatch: grad({M},{D_out}), "
+        f"w_hi({D_out2},{D_in}), w_lo{tuple(w_lo_fp8.shape)}"
+    )
+    if w_hi_t is None:
+        w_hi_t = transpose_fp8(w_hi_fp8)
+    if w_lo_t is None:
+        w_lo_t = transpose_fp8(w_lo_fp8)
+    return _dual_gemm(grad_fp8, w_hi_t, w_lo_t, grad_inv, w_hi_inv, w_lo_inv, None, torch.float32)
+
+
+def fp8_gemm_nt(
+    a_fp8: torch.Tensor,
+    b_fp8: torch.Tensor,
+    scale_a: torch.Tensor,
+    scale_b: torch.Tensor,
+    *,
+    out_dtype: torch.dtype = torch.float32,
+    bias: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Single scaled FP8 GEMM ``(A @ B.T) * s_a s_b`` with A [M, K], B [N, K].
+
+    The FP8 wgrad of ``tcfp/nn/__init__.py:546-555`` is
+    ``fp8_gemm_nt(grad^T, act^T, grad_inv, act_inv)``; it also stands in for
+    ``torch._scaled_mm`` in the reference's ABD dgrad (``:499-508``).
+    """
+    assert a_fp8.shape[1] == b_fp8.shape[1], (
+        f"K mismatch: A {tuple(a_fp8.shape)} vs B {tuple(b_fp8.shape)}"
+    )
+    return _dual_gemm(a_fp8, b_fp8, None, scale_a, scale_b, None, bias, out_dtype)
+
+
+# ---------------------------------------------------------------------------
+# Block quantisation
+# ---------------------------------------------------------------------------
+
+
+def block_quantize_fp8(
+    tensor: torch.Tensor,
+    block_size: int = 128,
+    fp8_dtype: torch.dtype = torch.float8_e4m3fn,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Per-(row, K-block) FP8 quantisation; returns ``(fp8 [M,K], int8 exps
+    [K // block_size, M])`` with scale = 2^exp.
+
+    Reference: ``block_quantize_fp8`` (``tcfp/kernels.py:1675-1722``).
+    """
+    dev = _hip.require_gpu(tensor)
+    M, K = tensor.shape
+    assert K % block_size == 0, f"K ({K}) must be divisible by block_size ({block_size})"
+    if block_size not in (32, 64, 128):
+        raise ValueError(f"block_size must be 32, 64, or 128, got {block_size}")
+    x = tensor if tensor.is_contiguous() else tensor.contiguous()
+    q = torch.empty((M, K), dtype=fp8_dtype, device=dev)
+    exps = torch.empty((K // block_size, M), dtype=torch.int8, device=dev)
+    check(
+        _hip.lib().tcfp_block_quantize(
+            ptr(x), _in_dtype(x), M, K, block_size, _fmt(fp8_dtype), ptr(q), ptr(exps),
+            _hip.stream_of(dev),
+        ),
+        "block_quantize_fp8",
+    )
+    return q, exps
+
+
+def block_dequantize_fp8(
+    fp8_tensor: torch.Tensor,
+    block_scales: torch.Tensor,
+    block_size: int,
+) -> torch.Tensor:
+    """``fp8 * 2^exp`` -> fp32 [M, K] (reference ``tcfp/kernels.py:1725-1746``)."""
+    dev = _hip.require_gpu(fp8_tensor, block_scales)
+    M, K = fp8_tensor.shape
+    q = fp8_tensor.contiguous()
+    e = block_scales.contiguous()
+    assert e.dtype == torch.int8 and tuple(e.shape) == (K // block_size, M), (
+        f"block_scales must be int8 ({K // block_size}, {M})"
+    )
+    out = torch.empty((M, K), dtype=torch.float32, device=dev)
+    check(
+        _hip.lib().tcfp_block_dequantize(
+            ptr(q), _fmt(q.dtype), ptr(e), M, K, block_size, ptr(out), _hip.stream_of(dev)
+        ),
+        "block_dequantize_fp8",
+    )
+    return out
+
+
+def fused_dual_quantize_fp8(
+    weight: torch.Tensor,
+    block_size: int = 128,
+    error_buf: torch.Tensor | None = None,
+    stochastic_lo: bool = False,
+    update_ef: bool = True,
+    seed: int | None = None,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+    """W (+ EF) -> ``(w_hi, w_lo, scales_hi, scales_lo)``, one HBM pass.
+
+    Reference: ``fused_dual_quantize_fp8`` (``tcfp/kernels.py:1749-1875``).
+    The error update the reference runs afterwards in Python
+    (``:1867-1873``) happens inside the same kernel here; ``error_buf`` is
+    modified in place (unless ``update_ef=False``).  Scales are int8
+    exponents [K // block_size, N]; W_lo blocks with zero residual carry
+    the -128 sentinel.
+    """
+    assert weight.is_contiguous(), "Weight must be contiguous (N, K) row-major"
+    N, K = weight.shape
+    assert K % block_size == 0, f"K ({K}) must be divisible by block_size ({block_size})"
+    if stochastic_lo and error_buf is not None:
+        raise ValueError(
+            "stochastic_lo and error_buf are mutually exclusive: "
+            "SRR eliminates the need for error feedback buffers."
+        )
+    if error_buf is not None:
+        assert error_buf.dtype == torch.float32, "error_buf must be float32"
+        assert tuple(error_buf.shape) == (N, K), (
+            f"error_buf shape {tuple(error_buf.shape)} != weight shape {(N, K)}"
+        )
+        assert error_buf.is_contiguous(), "error_buf must be contiguous"
+    if block_size not in (32, 64, 128):
+        raise ValueError(f"block_size must be 32, 64, or 128, got {block_size}")
+    dev = _hip.require_gpu(weight, error_buf)
+    num_kb = K // block_size
+    w_hi = torch.empty((N, K), dtype=torch.float8_e4m3fn, device=dev)
+    w_lo = torch.empty((N, K), dtype=torch.float8_e4m3fn, device=dev)
+    sh = torch.empty((num_kb, N), dtype=torch.int8, device=dev)
+    sl = torch.empty((num_kb, N), dtype=torch.int8, device=dev)
+    if stochastic_lo and seed is None:
+        seed = int(torch.randint(0, 2**62, (1,)).item())
+    check(
+        _hip.lib().tcfp_block_dual_quantize(
+            ptr(weight), _in_dtype(weight), N, K, block_size, ptr(error_buf),
+            int(bool(update_ef)), int(bool(stochastic_lo)), int(seed or 0), 0, ptr(w_hi),
+            ptr(w_lo), ptr(sh), ptr(sl), _hip.stream_of(dev),
+        ),
+        "fused_dual_quantize_fp8",
+    )
+    return w_hi, w_lo, sh, sl

@@ -1,0 +1,498 @@
+"""TCFP-12 modules and autograd Functions (drop-in for ``tcfp.nn``'s tensor-core path).
+
+``TCFPLinear`` / ``convert_to_tcfp`` keep the reference's constructor and
+conversion API (``tcfp/nn/__init__.py:769-1077, 1190-1351``).  The two
+autograd Functions keep the reference's positional signatures and
+saved-state semantics:
+
+* ``_TCFP12TensorCoreFunction.apply`` -- 15 args (``tcfp/nn/__init__.py:312-566``)
+* ``_TCFP12BlockScaledFunction.apply`` -- 10 args (``tcfp/nn/__init__.py:574-761``)
+
+but their bodies call the HIP operator layer (``tcfp_amd.kernels``):
+
+* per-tensor forward: one dual-quant launch chain (W + EF -> W_hi, W_lo,
+  scales, new EF, and the transposed copies dgrad needs), one act-quant
+  chain (codes + the transposed copy wgrad needs), one fused dual FP8 GEMM
+  with the bias in its epilogue;
+* per-tensor backward: E5M2 grad quant (+ transposed copy), dual FP8 dgrad,
+  single FP8 wgrad, all on the same K-contiguous MFMA kernel.  dX is
+  skipped when autograd does not need it (the reference always computes it;
+  the results of the gradients that are returned are unchanged).
+
+The reference's fake-quantise path (``use_tensor_cores=False``, int4/NF4
+residual via ``tcfp.tcfp12``), delayed scaling and NF-aware scaling are not
+part of this build and raise ``NotImplementedError``.
+"""
+from __future__ import annotations
+
+import warnings
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from .. import kernels as K
+from ..core import DEFAULT_BLOCK_SIZE, ErrorFeedbackState, TCFPMode
+
+__all__ = [
+    "TCFPLinear",
+    "convert_to_tcfp",
+    "_TCFP12TensorCoreFunction",
+    "_TCFP12BlockScaledFunction",
+]
+
+
+def _flatten(t: torch.Tensor) -> torch.Tensor:
+    return t.reshape(-1, t.shape[-1]) if t.ndim != 2 else t
+
+
+def _ef_buffer(state: ErrorFeedbackState | None, name: str, weight: torch.Tensor):
+    if state is None:
+        return None
+    return state.get_error(name, weight)
+
+
+class _TCFP12TensorCoreFunction(torch.autograd.Function):
+    """TCFP-12 per-tensor dual-FP8 linear (reference ``tcfp/nn/__init__.py:312-566``).
+
+    Forward: ``out = X W_hi^T s_x s_hi + X W_lo^T s_x s_lo (+ bias)`` in fp32.
+    Backward: ``dX`` = dual FP8 dgrad with E5M2 gradients (W_hi only under
+    ABD); ``dW`` = FP8 wgrad, or ``grad^T @ input`` when ``hp_grad_weight``,
+    or ``grad^T @ dequant(act)`` when the token count is not a multiple of
+    16 (reference ``:540-555``).
+    """
+
+    @staticmethod
+    def forward(  # noqa: PLR0913
+        ctx,
+        input: torch.Tensor,
+        weight: torch.Tensor,
+        bias: torch.Tensor | None,
+        nf_aware_scaling: bool,
+        sigma_factor: float,
+        stochastic_rounding: bool,
+        hp_grad_weight: bool,
+        error_state: ErrorFeedbackState | None,
+        param_name: str,
+        delayed_scaling: bool = False,
+        use_fused_kernel: bool = True,
+        use_cuda_ext: bool = True,
+        abd: bool = False,
+        srr: bool = False,
+        update_ef: bool = True,
+    ) -> torch.Tensor:
+        if nf_aware_scaling:
+            raise NotImplementedError("nf_aware_scaling is not part of this build")
+        if delayed_scaling:
+            raise NotImplementedError("delayed_scaling is not part of this build")
+        need_dx = ctx.needs_input_grad[0]
+        need_dw = ctx.needs_input_grad[1]
+
+        # 1-4. dual quantisation of W (+ EF read and in-place update)
+        error_buf = _ef_buffer(error_state, param_name, weight)
+        w_hi, w_lo, inv_hi, inv_lo, w_hi_t, w_lo_t = K.dual_quantize_per_tensor(
+            weight, error_buf, update_ef=update_ef, stochastic_lo=srr, transposed=True
+        ) if need_dx else (*K.dual_quantize_per_tensor(
+            weight, error_buf, update_ef=update_ef, stochastic_lo=srr
+        ), None, None)
+
+        # 5. activation quantisation (and the transposed copy FP8 wgrad reads)
+        input_shape = input.shape
+        input_2d = _flatten(input)
+        M = input_2d.shape[0]
+        fp8_wgrad = need_dw and not hp_grad_weight and M % 16 == 0
+        if fp8_wgrad:
+            act_fp8, act_inv, act_t = K.quantize_per_tensor(input_2d, transpose=True)
+        else:
+            act_fp8, act_inv = K.quantize_per_tensor(input_2d)
+            act_t = None
+
+        # 6-7. fused dual GEMM, bias in the epilogue
+        out_2d = K.fused_dual_gemm_forward(
+            act_fp8, w_hi, w_lo, act_inv, inv_hi, inv_lo, bias=bias
+        )
+        output = out_2d.reshape(*input_shape[:-1], out_2d.shape[-1])
+
+        # 8. save for backward
+        ctx.hp_grad_weight = hp_grad_weight
+        ctx.input_shape = input_shape
+        ctx.has_bias = bias is not None
+        ctx.abd = abd
+        ctx.fp8_wgrad = fp8_wgrad
+        if not need_dw:
+            saved_act = None
+        elif hp_grad_weight:
+            saved_act = input_2d
+        elif fp8_wgrad:
+            saved_act = act_t
+        else:
+            saved_act = act_fp8
+        ctx.save_for_backward(
+            saved_act, act_inv, w_hi_t, None if abd else w_lo_t, inv_hi, inv_lo
+        )
+        return output
+
+    @staticmethod
+    def backward(ctx, grad_output: torch.Tensor):
+        saved_act, act_inv, w_hi_t, w_lo_t, inv_hi, inv_lo = ctx.saved_tensors
+        need_dx, need_dw, need_db = ctx.needs_input_grad[:3]
+        grad_2d = _flatten(grad_output)
+        if not grad_2d.is_contiguous():
+            grad_2d = grad_2d.contiguous()
+
+        grad_input = grad_weight = grad_bias = None
+        if need_dx or (need_dw and ctx.fp8_wgrad):
+            if need_dw and ctx.fp8_wgrad:
+                grad_fp8, grad_inv, grad_t = K.quantize_per_tensor(
+                    grad_2d, torch.float8_e5m2, transpose=True
+                )
+            else:
+                grad_fp8, grad_inv = K.quantize_per_tensor(grad_2d, torch.float8_e5m2)
+                grad_t = None
+            if need_dx:
+                if ctx.abd:
+                    gi = K.fp8_gemm_nt(grad_fp8, w_hi_t, grad_inv, inv_hi)
+                else:
+                    gi = K._dual_gemm(grad_fp8, w_hi_t, w_lo_t, grad_inv, inv_hi, inv_lo,
+                                      None, torch.float32)
+                grad_input = gi.reshape(ctx.input_shape)
+        if need_dw:
+            if ctx.hp_grad_weight:
+                grad_weight = grad_2d.t() @ saved_act.to(grad_2d.dtype)
+            elif ctx.fp8_wgrad:
+                grad_weight = K.fp8_gemm_nt(grad_t, saved_act, grad_inv, act_inv)
+            else:
+                grad_weight = grad_2d.t() @ (saved_act.float() * act_inv).to(grad_2d.dtype)
+        if need_db and ctx.has_bias:
+            grad_bias = grad_2d.sum(dim=0)
+        return (grad_input, grad_weight, grad_bias) + (None,) * 12
+
+
+class _TCFP12BlockScaledFunction(torch.autograd.Function):
+    """TCFP-12 with per-block (32/64/128 along K) power-of-two scales
+    (reference ``tcfp/nn/__init__.py:574-761``)."""
+
+    @staticmethod
+    def forward(
+        ctx,
+        input: torch.Tensor,
+        weight: torch.Tensor,
+        bias: torch.Tensor | None,
+        scale_block_size: int,
+        hp_grad_weight: bool,
+        error_state: ErrorFeedbackState | None,
+        param_name: str,
+        abd: bool = False,
+        srr: bool = False,
+        update_ef: bool = True,
+    ) -> torch.Tensor:
+        bs = scale_block_size
+        error_buf = _ef_buffer(error_state, param_name, weight)
+        w = weight if weight.is_contiguous() else weight.contiguous()
+        # EF is read, and rewritten in place only when update_ef (the
+        # reference clones the buffer instead, :597-608).
+        w_hi, w_lo, sh, sl = K.fused_dual_quantize_fp8(
+            w, block_size=bs, error_buf=error_buf, stochastic_lo=srr, update_ef=update_ef
+        )
+        input_shape = input.shape
+        input_2d = _flatten(input)
+        act_fp8, act_scales = K.block_quantize_fp8(input_2d, block_size=bs)
+        out_2d = K.fused_block_scaled_dual_gemm_forward(
+            act_fp8, w_hi, w_lo, act_scales, sh, sl, block_size=bs, bias=bias
+        )
+        output = out_2d.reshape(*input_shape[:-1], out_2d.shape[-1])
+
+        ctx.hp_grad_weight = hp_grad_weight
+        ctx.input_shape = input_shape
+        ctx.has_bias = bias is not None
+        ctx.bs = bs
+        ctx.abd = abd
+        saved_act = input_2d if hp_grad_weight else act_fp8
+        saved_act_scales = None if hp_grad_weight else act_scales
+        ctx.save_for_backward(saved_act, saved_act_scales, w_hi, None if abd else w_lo, sh,
+                              None if abd else sl)
+        return output
+
+    @staticmethod
+    def backward(ctx, grad_output: torch.Tensor):
+        saved_act, act_scales, w_hi, w_lo, sh, sl = ctx.saved_tensors
+        need_dx, need_dw, need_db = ctx.needs_input_grad[:3]
+        bs = ctx.bs
+        grad_2d = _flatten(grad_output)
+        if not grad_2d.is_contiguous():
+            grad_2d = grad_2d.contiguous()
+        grad_input = grad_weight = grad_bias = None
+        if need_dx:
+            grad_fp8, grad_scales = K.block_quantize_fp8(
+                grad_2d, block_size=bs, fp8_dtype=torch.float8_e5m2
+            )
+            grad_input = K.fused_block_scaled_dual_gemm_backward_dx(
+                grad_fp8, w_hi, w_lo, grad_scales, sh, sl, block_size=bs
+            ).reshape(ctx.input_shape)
+        if need_dw:
+            if ctx.hp_grad_weight:
+                act_f = saved_act.to(grad_2d.dtype)
+            else:
+                act_f = K.block_dequantize_fp8(saved_act, act_scales, bs).to(grad_2d.dtype)
+            grad_weight = grad_2d.t() @ act_f
+        if need_db and ctx.has_bias:
+            grad_bias = grad_2d.sum(dim=0)
+        return (grad_input, grad_weight, grad_bias) + (None,) * 7
+
+
+class TCFPLinear(nn.Module):
+    """Drop-in ``nn.Linear`` on the TCFP-12 dual-FP8 tensor-core path.
+
+    Same constructor as the reference (``tcfp/nn/__init__.py:810-832``).
+    ``use_tensor_cores`` must be True (the fake-quantise path is not part of
+    this build); ``use_fused_kernel`` / ``use_cuda_ext`` are accepted and
+    ignored -- every call runs the HIP kernels.
+    """
+
+    def __init__(
+        self,
+        in_features: int,
+        out_features: int,
+        bias: bool = True,
+        mode: TCFPMode = TCFPMode.TCFP12,
+        block_size: int = DEFAULT_BLOCK_SIZE,
+        *,
+        nf4_residual: bool = False,
+        nf_aware_scaling: bool = False,
+        sigma_factor: float = 3.0,
+        stochastic_rounding: bool = False,
+        warmup_steps: int = 0,
+        use_tensor_cores: bool = False,
+        hp_grad_weight: bool = False,
+        error_feedback: bool = True,
+        delayed_scaling: bool = False,
+        use_fused_kernel: bool = True,
+        use_cuda_ext: bool = True,
+        scale_block_size: int | None = None,
+        abd: bool = False,
+        srr: bool = False,
+        device=None,
+        dtype=None,
+    ) -> None:
+        super().__init__()
+        if not use_tensor_cores:
+            raise NotImplementedError(
+                "TCFPLinear(use_tensor_cores=False) is the fake-quantise path, which is "
+                "not part of this build; pass use_tensor_cores=True"
+            )
+        if nf_aware_scaling:
+            raise NotImplementedError("nf_aware_scaling is not part of this build")
+        if nf4_residual:
+            warnings.warn(
+                "nf4_residual is ignored in tensor core mode — NF4 cannot "
+                "run on tensor cores. The residual uses FP8 E4M3 instead.",
+                stacklevel=2,
+            )
+        if scale_block_size is not None:
+            if scale_block_size not in (32, 64, 128):
+                raise ValueError(
+                    f"scale_block_size must be 32, 64, or 128, got {scale_block_size}"
+                )
+            if in_features % scale_block_size != 0:
+                raise ValueError(
+                    f"in_features ({in_features}) must be divisible by "
+                    f"scale_block_size ({scale_block_size})"
+                )
+            if out_features % scale_block_size != 0:
+                raise ValueError(
+                    f"out_features ({out_features}) must be divisible by "
+                    f"scale_block_size ({scale_block_size}). Backward pass "
+                    f"block-quantizes gradients along the output dimension."
+                )
+            if delayed_scaling:
+                warnings.warn(
+                    "Per-block scaling (scale_block_size) and delayed_scaling "
+                    "are mutually exclusive. Ignoring delayed_scaling.",
+                    stacklevel=2,
+                )
+                delayed_scaling = False
+        if srr and delayed_scaling:
+            warnings.warn(
+                "srr=True is mutually exclusive with delayed_scaling=True. "
+                "Disabling delayed_scaling.",
+                stacklevel=2,
+            )
+            delayed_scaling = False
+        if delayed_scaling:
+            raise NotImplementedError("delayed_scaling is not part of this build")
+
+        self.in_features = in_features
+        self.out_features = out_features
+        self.mode = mode
+        self.block_size = block_size
+        self.nf4_residual = nf4_residual
+        self.nf_aware_scaling = nf_aware_scaling
+        self.sigma_factor = sigma_factor
+        self.stochastic_rounding = stochastic_rounding
+        self._warmup_steps = warmup_steps
+        self._warmup_remaining = warmup_steps
+        self.use_tensor_cores = use_tensor_cores
+        self.hp_grad_weight = hp_grad_weight
+        self.use_fused_kernel = use_fused_kernel
+        self.use_cuda_ext = use_cuda_ext
+        self.scale_block_size = scale_block_size
+        self.delayed_scaling = delayed_scaling
+        self.abd = abd
+        self.srr = srr
+        self._error_state: ErrorFeedbackState | None = (
+            ErrorFeedbackState() if (error_feedback and not srr) else None
+        )
+        self._param_name: str = ""
+        self._last_weight_version: int = -1
+        self._bf16_fallback: bool = False
+
+        factory = {"device": device, "dtype": dtype}
+        self.weight = nn.Parameter(torch.empty(out_features, in_features, **factory))
+        if bias:
+            self.bias = nn.Parameter(torch.empty(out_features, **factory))
+        else:
+            self.register_parameter("bias", None)
+        self.reset_parameters()
+
+    def reset_parameters(self) -> None:
+        nn.init.kaiming_uniform_(self.weight, a=5**0.5)
+        if self.bias is not None:
+            fan_in = self.weight.shape[1]
+            bound = 1 / fan_in**0.5
+            nn.init.uniform_(self.bias, -bound, bound)
+
+    def fallback_to_bf16(self) -> None:
+        """Switch this layer to the unquantised pass-through."""
+        self._bf16_fallback = True
+
+    def restore_tcfp(self) -> None:
+        self._bf16_fallback = False
+
+    @torch.compiler.disable
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if self._bf16_fallback:
+            return F.linear(x, self.weight, self.bias)
+        if self._warmup_remaining > 0:
+            self._warmup_remaining -= 1
+            return F.linear(x, self.weight, self.bias)
+        # EF guard (reference :983-994): update only when the weight changed
+        # since the last update and autograd is recording.
+        ver = self.weight._version
+        update_ef = ver != self._last_weight_version and torch.is_grad_enabled()
+        if update_ef:
+            self._last_weight_version = ver
+        if self.scale_block_size is not None:
+            return _TCFP12BlockScaledFunction.apply(
+                x, self.weight, self.bias, self.scale_block_size, self.hp_grad_weight,
+                self._error_state, self._param_name, self.abd, self.srr, update_ef,
+            )
+        return _TCFP12TensorCoreFunction.apply(
+            x, self.weight, self.bias, self.nf_aware_scaling, self.sigma_factor,
+            self.stochastic_rounding, self.hp_grad_weight, self._error_state,
+            self._param_name, self.delayed_scaling, self.use_fused_kernel, self.use_cuda_ext,
+            self.abd, self.srr, update_ef,
+        )
+
+    def extra_repr(self) -> str:
+        parts = [
+            f"in_features={self.in_features}",
+            f"out_features={self.out_features}",
+            f"bias={self.bias is not None}",
+            f"mode={self.mode.name}",
+            f"block_size={self.block_size}",
+            "use_tensor_cores=True",
+        ]
+        if self.hp_grad_weight:
+            parts.append("hp_grad_weight=True")
+        if self.use_fused_kernel:
+            parts.append("use_fused_kernel=True")
+        if self.scale_block_size is not None:
+            parts.append(f"scale_block_size={self.scale_block_size}")
+        if self.abd:
+            parts.append("abd=True")
+        if self.srr:
+            parts.append("srr=True")
+        if self._warmup_steps > 0:
+            parts.append(f"warmup_steps={self._warmup_steps}")
+        if self._bf16_fallback:
+            parts.append("bf16_fallback=True")
+        return ", ".join(parts)
+
+
+def convert_to_tcfp(
+    model: nn.Module,
+    mode: TCFPMode = TCFPMode.TCFP12,
+    block_size: int = DEFAULT_BLOCK_SIZE,
+    skip_patterns: tuple[str, ...] = ("head",),
+    *,
+    nf4_residual: bool = False,
+    nf_aware_scaling: bool = False,
+    stochastic_rounding: bool = False,
+    warmup_steps: int = 0,
+    use_tensor_cores: bool = False,
+    hp_grad_weight: bool = False,
+    error_feedback: bool = True,
+    delayed_scaling: bool = False,
+    use_fused_kernel: bool = True,
+    use_cuda_ext: bool = True,
+    scale_block_size: int | None = None,
+    abd: bool = False,
+    srr: bool = False,
+    _parent_path: str = "",
+) -> nn.Module:
+    """Replace ``nn.Linear`` layers with ``TCFPLinear`` in place
+    (reference ``tcfp/nn/__init__.py:1190-1351``).
+
+    Same eligibility rules: children are converted depth-first, names
+    matching ``skip_patterns`` are skipped, a layer is converted only when
+    ``in_features % block_size == 0`` and both dims are multiples of 16,
+    and ``scale_block_size`` is dropped per layer when it does not divide
+    both dims.  The new module shares the original Parameters and gets
+    ``_param_name`` = its module path.  Layers the reference would put on
+    the fake-quantise path (``use_tensor_cores=False`` or dims not multiples
+    of 16) stay ``nn.Linear``; ``nn.LayerNorm`` / ``nn.Embedding`` are left
+    unchanged for the same reason.
+    """
+    for name, module in model.named_children():
+        full_path = f"{_parent_path}.{name}" if _parent_path else name
+        convert_to_tcfp(
+            module, mode, block_size, skip_patterns,
+            nf4_residual=nf4_residual, nf_aware_scaling=nf_aware_scaling,
+            stochastic_rounding=stochastic_rounding, warmup_steps=warmup_steps,
+            use_tensor_cores=use_tensor_cores, hp_grad_weight=hp_grad_weight,
+            error_feedback=error_feedback, delayed_scaling=delayed_scaling,
+            use_fused_kernel=use_fused_kernel, use_cuda_ext=use_cuda_ext,
+            scale_block_size=scale_block_size, abd=abd, srr=srr, _parent_path=full_path,
+        )
+        if any(pat in name for pat in skip_patterns):
+            continue
+        if not isinstance(module, nn.Linear) or isinstance(module, TCFPLinear):
+            continue
+        if module.in_features % block_size != 0:
+            continue
+        layer_tc = use_tensor_cores and (
+            module.in_features % 16 == 0 and module.out_features % 16 == 0
+        )
+        if not layer_tc:
+            continue
+        layer_sbs = scale_block_size
+        if layer_sbs is not None and (
+            module.in_features % layer_sbs != 0 or module.out_features % layer_sbs != 0
+        ):
+            layer_sbs = None
+        new_module = TCFPLinear(
+            module.in_features, module.out_features, bias=module.bias is not None,
+            mode=mode, block_size=block_size, nf4_residual=nf4_residual,
+            nf_aware_scaling=nf_aware_scaling, stochastic_rounding=stochastic_rounding,
+            warmup_steps=warmup_steps, use_tensor_cores=True, hp_grad_weight=hp_grad_weight,
+            error_feedback=error_feedback, delayed_scaling=delayed_scaling,
+            use_fused_kernel=use_fused_kernel, use_cuda_ext=use_cuda_ext,
+            scale_block_size=layer_sbs, abd=abd, srr=srr,
+            device="meta",
+        )
+        new_module._param_name = full_path
+        new_module.weight = module.weight
+        if module.bias is not None:
+            new_module.bias = module.bias
+        setattr(model, name, new_module)
+    return model

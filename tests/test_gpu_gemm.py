@@ -1,0 +1,129 @@
+"""GPU parity of the FP8 MFMA GEMMs against the float64 dequant oracle.
+
+Tolerance: relative Frobenius error <= 1e-2 against the dequantised
+matmul of the same FP8 operands (the reference's own
+tests use atol=rtol=1e-2 against 2x _scaled_mm, tests/test_fused_kernels.py
+upstream).  In practice the fp32-accumulated MFMA result is ~1e-6.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import fp8 as ofp8
+from oracle import gemm as og
+from oracle import quant as oq
+from tcfp_amd import kernels as K
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-2
+
+
+def u8(t):
+    return t.view(torch.uint8).cpu().numpy()
+
+
+def make_pair(shape, seed, dev):
+    g = torch.Generator().manual_seed(seed)
+    w = torch.randn(shape, generator=g)
+    h, l, ih, il = K.dual_quantize_per_tensor(w.to(dev))
+    return h, l, ih, il
+
+
+def make_act(shape, seed, dev, fp8=torch.float8_e4m3fn):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(shape, generator=g)
+    q, inv = K.quantize_per_tensor(x.to(dev), fp8)
+    return q, inv
+
+
+SHAPES = [(64, 128, 64), (256, 512, 256), (128, 256, 512), (48, 80, 112), (16, 16, 16),
+          (300, 200, 1024), (1024, 1024, 1024)]
+
+
+@pytest.mark.parametrize("M,K_,N", SHAPES)
+def test_dual_gemm_forward_matches_oracle(dev, M, K_, N):
+    a, sa = make_act((M, K_), M + K_, dev)
+    h, l, ih, il = make_pair((N, K_), N + 1, dev)
+    out = K.fused_dual_gemm_forward(a, h, l, sa, ih, il)
+    assert out.dtype == torch.float32 and out.shape == (M, N)
+    ref = og.dual_gemm_nt(u8(a), ofp8.E4M3, u8(h), u8(l), sa.item(), ih.item(), il.item())
+    err = og.rel_fro(out.cpu().numpy(), ref)
+    print(f"dual fwd M={M} K={K_} N={N} rel_fro={err:.2e}")
+    assert err < 1e-5  # fp32 accumulation of exact fp8 products
+
+
+@pytest.mark.parametrize("M,K_,N", [(64, 128, 64), (48, 80, 112), (512, 1024, 256)])
+def test_dual_gemm_bf16_out_and_bias(dev, M, K_, N):
+    a, sa = make_act((M, K_), 5, dev)
+    h, l, ih, il = make_pair((N, K_), 6, dev)
+    bias = torch.randn(N, device=dev)
+    out = K.fused_dual_gemm_forward(a, h, l, sa, ih, il, bias=bias, out_dtype=torch.bfloat16)
+    assert out.dtype == torch.bfloat16
+    ref = og.dual_gemm_nt(u8(a), ofp8.E4M3, u8(h), u8(l), sa.item(), ih.item(), il.item())
+    ref = ref + bias.cpu().double().numpy()
+    assert og.rel_fro(out.float().cpu().numpy(), ref) < TOL
+
+
+def test_zero_lo_matches_single_gemm(dev):
+    a, sa = make_act((128, 256), 1, dev)
+    h, _, ih, _ = make_pair((192, 256), 2, dev)
+    zero = torch.zeros_like(h)
+    dual = K.fused_dual_gemm_forward(a, h, zero, sa, ih, ih)
+    single = K.fp8_gemm_nt(a, h, sa, ih)
+    torch.testing.assert_close(dual, single, atol=1e-4, rtol=1e-4)
+
+
+def test_scales_applied_linearly(dev):
+    a, sa = make_act((64, 128), 3, dev)
+    h, l, ih, il = make_pair((64, 128), 4, dev)
+    base = K.fused_dual_gemm_forward(a, h, l, sa, ih, il)
+    two = K.fused_dual_gemm_forward(a, h, l, sa * 2, ih, il)
+    torch.testing.assert_close(two, 2 * base, atol=1e-5, rtol=1e-5)
+    only_hi = K.fused_dual_gemm_forward(a, h, l, sa, ih, torch.zeros_like(il))
+    torch.testing.assert_close(only_hi, K.fp8_gemm_nt(a, h, sa, ih), atol=1e-4, rtol=1e-4)
+
+
+@pytest.mark.parametrize("M,D_out,D_in", [(64, 128, 64), (256, 512, 256), (48, 112, 80),
+                                          (512, 1024, 4096)])
+def test_dual_gemm_backward_dx_e5m2(dev, M, D_out, D_in):
+    g, sg = make_act((M, D_out), 7, dev, torch.float8_e5m2)
+    h, l, ih, il = make_pair((D_out, D_in), 8, dev)
+    dx = K.fused_dual_gemm_backward_dx(g, h, l, sg, ih, il)
+    assert dx.shape == (M, D_in)
+    G = ofp8.decode(u8(g), ofp8.E5M2).astype(np.float64)
+    W = (ofp8.decode(u8(h), ofp8.E4M3).astype(np.float64) * ih.item()
+         + ofp8.decode(u8(l), ofp8.E4M3).astype(np.float64) * il.item())
+    ref = (G @ W) * sg.item()
+    assert og.rel_fro(dx.cpu().numpy(), ref) < 1e-5
+
+
+@pytest.mark.parametrize("N,M,K_", [(128, 64, 256), (1024, 8192, 4096), (80, 48, 112)])
+def test_single_gemm_wgrad_layout(dev, N, M, K_):
+    # dW = G^T X with K = tokens: A = G^T [N, M], B = X^T [K, M]
+    g, sg, gt = K.quantize_per_tensor(torch.randn(M, N, device=dev), torch.float8_e5m2,
+                                      transpose=True)
+    x, sx, xt = K.quantize_per_tensor(torch.randn(M, K_, device=dev), transpose=True)
+    dw = K.fp8_gemm_nt(gt, xt, sg, sx)
+    assert dw.shape == (N, K_)
+    ref = og.gemm_nt(u8(gt), ofp8.E5M2, u8(xt), ofp8.E4M3, sg.item(), sx.item())
+    assert og.rel_fro(dw.cpu().numpy(), ref) < 1e-5
+
+
+def test_c2_4096_cubed_against_torch_fp32(dev):
+    # full benchmark shape; torch fp32 matmul of the dequantised operands
+    g = torch.Generator().manual_seed(0)
+    xb = torch.randn(4096, 4096, generator=g).bfloat16().to(dev)
+    w = torch.randn(4096, 4096, generator=torch.Generator().manual_seed(1)).to(dev)
+    a, sa = K.quantize_per_tensor(xb)
+    h, l, ih, il = K.dual_quantize_per_tensor(w)
+    out = K.fused_dual_gemm_forward(a, h, l, sa, ih, il, out_dtype=torch.bfloat16)
+    A = a.float() * sa
+    Wd = h.float() * ih + l.float() * il
+    ref = A @ Wd.t()
+    err = ((out.float() - ref).norm() / ref.norm()).item()
+    print(f"C2 4096^3 bf16-out rel_fro={err:.3e}")
+    assert err < TOL
+    # and W_hi + W_lo reconstructs W much better than W_hi alone
+    e_dual = ((Wd - w).norm() / w.norm()).item()
+    e_hi = ((h.float() * ih - w).norm() / w.norm()).item()
+    assert e_dual < e_hi / 8

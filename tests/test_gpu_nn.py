@@ -1,0 +1,145 @@
+"""GPU tests of the drop-in modules: TCFPLinear forward/backward against the
+oracle, the error-feedback state machine, and short training runs."""
+import numpy as np
+import pytest
+import torch
+import torch.nn as nn
+
+from oracle import fp8 as ofp8
+from oracle import gemm as og
+from oracle import quant as oq
+from tcfp_amd.nn import TCFPLinear, _TCFP12TensorCoreFunction, convert_to_tcfp
+
+pytestmark = pytest.mark.gpu
+
+
+def _layer(dev, k, n, **kw):
+    torch.manual_seed(0)
+    return TCFPLinear(k, n, use_tensor_cores=True, **kw).to(dev)
+
+
+@pytest.mark.parametrize("xdtype", [torch.float32, torch.bfloat16])
+def test_forward_backward_matches_oracle(dev, xdtype):
+    M, Kd, N = 256, 512, 384
+    lin = _layer(dev, Kd, N)
+    g = torch.Generator().manual_seed(1)
+    x = torch.randn(M, Kd, generator=g).to(xdtype)
+    xd = x.to(dev).requires_grad_(True)
+    out = lin(xd)
+    assert out.dtype == torch.float32 and out.shape == (M, N)
+    gout = torch.randn(M, N, generator=g)
+    out.backward(gout.to(dev))
+    # oracle forward
+    W = lin.weight.detach().cpu().numpy()
+    hi, lo, ih, il, ef_new, _ = oq.dual_quant_per_tensor(W, np.zeros_like(W))
+    aq, ai, _ = oq.to_fp8_per_tensor(x.float().numpy(), "bf16" if xdtype == torch.bfloat16 else "f32")
+    ref = og.dual_gemm_nt(aq, ofp8.E4M3, hi, lo, ai, ih, il) + lin.bias.detach().cpu().double().numpy()
+    assert og.rel_fro(out.detach().cpu().numpy(), ref) < 1e-5
+    assert np.array_equal(lin._error_state._buffers[""].cpu().numpy(), ef_new)
+    # oracle backward: E5M2 grad, dual dgrad, FP8 wgrad, fp32 bias grad
+    gq, gi, _ = oq.to_fp8_per_tensor(gout.numpy(), "f32", ofp8.E5M2)
+    G = ofp8.decode(gq, ofp8.E5M2).astype(np.float64) * gi
+    Wd = ofp8.decode(hi, ofp8.E4M3).astype(np.float64) * ih + ofp8.decode(lo, ofp8.E4M3) * il
+    # dX is returned in the input's dtype (bf16 rounding ~2^-9)
+    tol_dx = 1e-5 if xdtype == torch.float32 else 8e-3
+    assert og.rel_fro(xd.grad.float().cpu().numpy(), G @ Wd) < tol_dx
+    A = ofp8.decode(aq, ofp8.E4M3).astype(np.float64) * ai
+    assert og.rel_fro(lin.weight.grad.cpu().numpy(), G.T @ A) < 1e-5
+    np.testing.assert_allclose(lin.bias.grad.cpu().numpy(), gout.sum(0).numpy(), rtol=1e-4, atol=1e-3)
+
+
+def test_3d_input_and_hp_grad_weight(dev):
+    lin = _layer(dev, 128, 64, hp_grad_weight=True)
+    x = torch.randn(4, 32, 128, device=dev, requires_grad=True)
+    y = lin(x)
+    assert y.shape == (4, 32, 64)
+    y.sum().backward()
+    assert x.grad.shape == x.shape and torch.isfinite(lin.weight.grad).all()
+    ref_gw = torch.ones(128, 64, device=dev).t() @ x.detach().reshape(-1, 128)
+    torch.testing.assert_close(lin.weight.grad, ref_gw, rtol=1e-4, atol=1e-3)
+
+
+def test_ragged_token_count_uses_dequant_wgrad(dev):
+    lin = _layer(dev, 64, 32)
+    x = torch.randn(37, 64, device=dev)
+    lin(x).sum().backward()
+    assert torch.isfinite(lin.weight.grad).all()
+
+
+def test_abd_backward_uses_hi_only(dev):
+    lin = _layer(dev, 128, 64, abd=True)
+    x = torch.randn(32, 128, device=dev, requires_grad=True)
+    lin(x).sum().backward()
+    assert torch.isfinite(x.grad).all()
+
+
+def test_no_input_grad_skips_dgrad(dev):
+    lin = _layer(dev, 64, 64)
+    x = torch.randn(16, 64, device=dev)  # no requires_grad
+    lin(x).sum().backward()
+    assert lin.weight.grad is not None
+
+
+def test_ef_guard_grad_accumulation_and_no_grad(dev):
+    lin = _layer(dev, 64, 64)
+    x = torch.randn(32, 64, device=dev)
+    lin(x).sum().backward()
+    ef1 = lin._error_state._buffers[""].clone()
+    # second micro-batch, weight unchanged -> EF must not change
+    lin(x).sum().backward()
+    assert torch.equal(lin._error_state._buffers[""], ef1)
+    # no_grad (checkpoint recompute) -> EF must not change
+    with torch.no_grad():
+        lin(x)
+    assert torch.equal(lin._error_state._buffers[""], ef1)
+    # after an optimizer step the EF updates
+    with torch.no_grad():
+        lin.weight.add_(1e-3)
+    lin(x).sum().backward()
+    assert not torch.equal(lin._error_state._buffers[""], ef1)
+
+
+def test_activation_checkpoint_recompute_keeps_ef(dev):
+    from torch.utils.checkpoint import checkpoint
+
+    lin = _layer(dev, 64, 64)
+    x = torch.randn(16, 64, device=dev, requires_grad=True)
+    y = checkpoint(lin, x, use_reentrant=False)
+    ef1 = lin._error_state._buffers[""].clone()
+    y.sum().backward()
+    assert torch.equal(lin._error_state._buffers[""], ef1)
+
+
+def test_srr_forward_backward(dev):
+    lin = _layer(dev, 128, 128, srr=True)
+    assert lin._error_state is None
+    x = torch.randn(64, 128, device=dev, requires_grad=True)
+    lin(x).square().mean().backward()
+    assert torch.isfinite(x.grad).all()
+
+
+def test_function_apply_positional_signature(dev):
+    w = torch.randn(32, 64, device=dev, requires_grad=True)
+    x = torch.randn(16, 64, device=dev)
+    y = _TCFP12TensorCoreFunction.apply(x, w, None, False, 3.0, False, False, None, "",
+                                        False, True, True, False, False, True)
+    assert y.shape == (16, 32)
+    y.sum().backward()
+    assert w.grad.shape == w.shape
+
+
+def test_tiny_mlp_converges(dev):
+    torch.manual_seed(0)
+    model = nn.Sequential(nn.Linear(64, 128), nn.GELU(), nn.Linear(128, 64)).to(dev)
+    convert_to_tcfp(model, use_tensor_cores=True)
+    x = torch.randn(256, 64, device=dev)
+    y = torch.randn(256, 64, device=dev) * 0.5
+    opt = torch.optim.Adam(model.parameters(), lr=3e-3)
+    first = None
+    for _ in range(60):
+        loss = (model(x) - y).square().mean()
+        opt.zero_grad()
+        loss.backward()
+        opt.step()
+        first = first if first is not None else loss.item()
+    assert loss.item() < 0.5 * first

@@ -1,0 +1,268 @@
+"""GPU parity of the quantisation kernels against the numpy oracle.
+
+Codes, exponents, scales and error buffers must be bit-identical
+(integer/byte work); stochastic rounding is checked statistically, as the
+reference does (tests/test_fused_dual_quant.py:467-526 upstream).
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import fp8 as ofp8
+from oracle import quant as oq
+from tcfp_amd import _hip
+from tcfp_amd import kernels as K
+from tcfp_amd.core import to_fp8_e4m3, to_fp8_e5m2
+
+pytestmark = pytest.mark.gpu
+
+
+def u8(t):
+    return t.view(torch.uint8).cpu().numpy()
+
+
+def i8(t):
+    return t.cpu().numpy()
+
+
+# ------------------------------------------------------------ self tests
+@pytest.mark.parametrize("fmt,top", [(0, 0x43E00000), (1, 0x47600000)])
+def test_hw_fp8_convert_matches_software_exhaustively(dev, fmt, top):
+    # every float32 in [0, FP8_MAX] and its negation
+    bad = torch.zeros(1, dtype=torch.int64, device=dev)
+    _hip.check(_hip.lib().tcfp_selftest_fp8_cvt(0, top, fmt, bad.data_ptr(),
+                                                 _hip.stream_of(dev)), "selftest")
+    torch.cuda.synchronize()
+    assert bad.item() == 0
+
+
+def test_philox_known_answers(dev):
+    # Random123 known-answer vectors for philox4x32-10
+    cases = [
+        ((0, 0, 0, 0), (0, 0), (0x6627E8D5, 0xE169C58D, 0xBC57AC4C, 0x9B00DBD8)),
+        ((0xFFFFFFFF,) * 4, (0xFFFFFFFF,) * 2, (0x408F276D, 0x41C83B0E, 0xA20BC7C6, 0x6D5451FD)),
+        ((0x243F6A88, 0x85A308D3, 0x13198A2E, 0x03707344), (0xA4093822, 0x299F31D0),
+         (0xD16CFE09, 0x94FDCCEB, 0x5001E420, 0x24126EA1)),
+    ]
+    for ctr, key, want in cases:
+        out = torch.zeros(4, dtype=torch.int32, device=dev)
+        _hip.check(_hip.lib().tcfp_selftest_philox(*ctr, *key, 1, out.data_ptr(),
+                                                    _hip.stream_of(dev)), "philox")
+        got = tuple(int(v) & 0xFFFFFFFF for v in out.cpu().tolist())
+        assert got == want
+
+
+# ------------------------------------------------------- per-tensor (a1/a8)
+SHAPES = [(1, 1), (3, 5), (64, 128), (257, 1000), (8192, 1024)]
+
+
+@pytest.mark.parametrize("shape", SHAPES)
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("fp8", [torch.float8_e4m3fn, torch.float8_e5m2])
+def test_per_tensor_quant_bitexact(dev, shape, dtype, fp8):
+    g = torch.Generator().manual_seed(shape[0] * 131 + shape[1] + (dtype == torch.bfloat16) * 7
+                                      + (fp8 == torch.float8_e5m2) * 13)
+    x = (torch.randn(shape, generator=g) * 3.0).to(dtype)
+    fmt = ofp8.E4M3 if fp8 == torch.float8_e4m3fn else ofp8.E5M2
+    codes, inv, scale = oq.to_fp8_per_tensor(x.float().numpy(),
+                                             "bf16" if dtype == torch.bfloat16 else "f32", fmt)
+    q, inv_d, qt, s_d = K.quantize_per_tensor(x.to(dev), fp8, transpose=True, return_scale=True)
+    assert q.dtype == fp8 and tuple(q.shape) == shape
+    assert np.array_equal(u8(q), codes)
+    assert np.array_equal(u8(qt), codes.T)
+    assert inv_d.item() == float(inv) and s_d.item() == float(scale)
+    # core API: same result without the transposed copy
+    q2, inv2 = (to_fp8_e4m3 if fmt == ofp8.E4M3 else to_fp8_e5m2)(x.to(dev))
+    assert np.array_equal(u8(q2), codes) and inv2.shape == (1,)
+
+
+def test_per_tensor_quant_special_inputs(dev):
+    x = torch.zeros(16, 32)
+    x[3, 7] = 1e-30  # tiny amax -> scale 448/1e-30
+    q, inv = to_fp8_e4m3(x.to(dev))
+    codes, inv_o, _ = oq.to_fp8_per_tensor(x.numpy())
+    assert np.array_equal(u8(q), codes) and inv.item() == float(inv_o)
+    z = torch.zeros(5, 8, device=dev)
+    q, inv = to_fp8_e4m3(z)
+    assert (u8(q) == 0).all() and inv.item() == float(np.float32(1) / oq.per_tensor_scale(np.zeros(1, np.float32), "f32"))
+    big = torch.tensor([[3.0e38, -1.0, 2.0 ** -140]], device=dev)
+    q, inv = to_fp8_e4m3(big)
+    codes, inv_o, _ = oq.to_fp8_per_tensor(big.cpu().numpy())
+    assert np.array_equal(u8(q), codes) and inv.item() == float(inv_o)
+
+
+def test_per_tensor_explicit_scale(dev):
+    x = torch.randn(33, 65)
+    s = torch.tensor([7.5])
+    q, inv = to_fp8_e4m3(x.to(dev), scale=s.to(dev))
+    codes, inv_o, _ = oq.to_fp8_per_tensor(x.numpy(), scale=np.float32(7.5))
+    assert np.array_equal(u8(q), codes) and inv.item() == float(inv_o)
+
+
+def test_per_tensor_empty(dev):
+    q, inv = to_fp8_e4m3(torch.empty(0, 16, device=dev))
+    assert q.shape == (0, 16)
+
+
+def test_workspace_is_left_clean(dev):
+    ws = _hip.workspace(dev)
+    for _ in range(3):
+        to_fp8_e4m3(torch.randn(100, 100, device=dev))
+        K.dual_quantize_per_tensor(torch.randn(64, 64, device=dev), torch.zeros(64, 64, device=dev))
+    torch.cuda.synchronize()
+    assert (ws[:8] == 0).all()
+
+
+# ---------------------------------------------------- dual quant (a2)
+@pytest.mark.parametrize("shape", [(64, 128), (100, 200), (4096, 1024), (1024, 4096)])
+@pytest.mark.parametrize("wdtype", [torch.float32, torch.bfloat16])
+def test_dual_quant_per_tensor_ef_steps_bitexact(dev, shape, wdtype):
+    g = torch.Generator().manual_seed(11)
+    W = (torch.randn(shape, generator=g) * 0.02).to(wdtype)
+    ef_o = np.zeros(shape, np.float32)
+    ef_d = torch.zeros(shape, device=dev)
+    Wd = W.to(dev)
+    for step in range(3):
+        hi, lo, ih, il, ef_new, _ = oq.dual_quant_per_tensor(W.float().numpy(), ef_o)
+        h, l, ihd, ild, ht, lt = K.dual_quantize_per_tensor(Wd, ef_d, transposed=True)
+        assert np.array_equal(u8(h), hi), f"step {step} hi"
+        assert np.array_equal(u8(l), lo), f"step {step} lo"
+        assert np.array_equal(u8(ht), hi.T) and np.array_equal(u8(lt), lo.T)
+        assert ihd.item() == float(ih) and ild.item() == float(il)
+        assert np.array_equal(ef_d.cpu().numpy(), ef_new), f"step {step} ef"
+        ef_o = ef_new
+        # the "optimizer" moves W a little between steps
+        W = (W.float() + 1e-4 * torch.randn(shape, generator=g)).to(wdtype)
+        Wd = W.to(dev)
+
+
+def test_dual_quant_no_update_leaves_ef(dev):
+    W = torch.randn(64, 64, device=dev) * 0.02
+    ef = torch.randn(64, 64, device=dev) * 1e-4
+    before = ef.clone()
+    a = K.dual_quantize_per_tensor(W, ef, update_ef=False)
+    assert torch.equal(ef, before)
+    b = K.dual_quantize_per_tensor(W, before.clone(), update_ef=True)
+    assert all(torch.equal(x.view(torch.uint8) if x.dtype.itemsize == 1 else x,
+                           y.view(torch.uint8) if y.dtype.itemsize == 1 else y)
+               for x, y in zip(a, b))
+
+
+def test_dual_quant_no_ef_matches_zero_ef(dev):
+    W = torch.randn(96, 160, device=dev)
+    a = K.dual_quantize_per_tensor(W, None)
+    b = K.dual_quantize_per_tensor(W, torch.zeros_like(W))
+    for x, y in zip(a, b):
+        assert torch.equal(x.view(torch.uint8) if x.dtype.itemsize == 1 else x,
+                           y.view(torch.uint8) if y.dtype.itemsize == 1 else y)
+
+
+def test_dual_quant_sr_candidates_and_unbiased(dev):
+    g = torch.Generator().manual_seed(3)
+    W = torch.randn(128, 256, generator=g)
+    hi_o, lo_rtn, ih_o, il_o, _, res = oq.dual_quant_per_tensor(W.numpy(), None)
+    scale_lo = oq.per_tensor_scale(res, "f32")
+    x = np.clip(res * scale_lo, -448, 448).astype(np.float32)
+    lo_c, hi_c, frac, exact = oq.sr_candidates_per_tensor(x)
+    acc = np.zeros(x.shape, np.float64)
+    n = 200
+    for i in range(n):
+        h, l, ih, il = K.dual_quantize_per_tensor(W.to(dev), None, stochastic_lo=True, seed=1000 + i)
+        assert np.array_equal(u8(h), hi_o) and il.item() == float(il_o)
+        c = u8(l)
+        assert np.all((c == lo_c) | (c == hi_c)), "SR picked a code outside the candidate pair"
+        assert np.all(c[exact] == lo_c[exact])
+        acc += (c == hi_c) & (hi_c != lo_c)
+    p = acc / n
+    m = ~exact & (hi_c != lo_c) & np.isfinite(frac)
+    # empirical up-rounding rate tracks frac (binomial noise, n = 200)
+    assert abs(float((p[m] - frac[m]).mean())) < 0.01
+    assert float(np.abs(p[m] - frac[m]).max()) < 0.2
+
+
+# ------------------------------------------------------ block quant (a4)
+@pytest.mark.parametrize("bs", [32, 64, 128])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("fp8", [torch.float8_e4m3fn, torch.float8_e5m2])
+@pytest.mark.parametrize("m", [1, 37, 512])
+def test_block_quantize_bitexact(dev, bs, dtype, fp8, m):
+    g = torch.Generator().manual_seed(bs * 7 + m)
+    k = 4 * bs
+    x = (torch.randn(m, k, generator=g) * 2.0 ** torch.randint(-20, 20, (m, 1), generator=g)).to(dtype)
+    fmt = ofp8.E4M3 if fp8 == torch.float8_e4m3fn else ofp8.E5M2
+    codes, exps = oq.block_quantize(x.float().numpy(), bs, fmt)
+    q, e = K.block_quantize_fp8(x.to(dev), bs, fp8)
+    assert tuple(e.shape) == (k // bs, m) and e.dtype == torch.int8
+    assert np.array_equal(i8(e), exps)
+    assert np.array_equal(u8(q), codes)
+
+
+def test_block_quantize_zero_and_boundary(dev):
+    x = torch.zeros(4, 64)
+    x[1, :32] = 448.0 * 2.0 ** -10 * (1 + 2.0 ** -23)  # amax/448 just above 2^-10
+    x[2, 32:] = 448.0 * 2.0 ** -10
+    codes, exps = oq.block_quantize(x.numpy(), 32)
+    q, e = K.block_quantize_fp8(x.to(dev), 32)
+    assert np.array_equal(i8(e), exps) and np.array_equal(u8(q), codes)
+
+
+@pytest.mark.parametrize("bs", [32, 64, 128])
+def test_block_dequantize(dev, bs):
+    x = torch.randn(40, 2 * bs)
+    q, e = K.block_quantize_fp8(x.to(dev), bs)
+    d = K.block_dequantize_fp8(q, e, bs).cpu().numpy()
+    assert np.array_equal(d, oq.block_dequantize(u8(q), i8(e), bs))
+
+
+# ------------------------------------------------- block dual quant (a3)
+@pytest.mark.parametrize("bs", [32, 64, 128])
+@pytest.mark.parametrize("wdtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("shape", [(64, 256), (200, 512), (4096, 1024)])
+def test_block_dual_quantize_ef_bitexact(dev, bs, wdtype, shape):
+    g = torch.Generator().manual_seed(bs + shape[0])
+    W = torch.randn(shape, generator=g).to(wdtype)
+    ef_o = (np.random.default_rng(bs).standard_normal(shape) * 1e-3).astype(np.float32)
+    ef_d = torch.from_numpy(ef_o.copy()).to(dev)
+    for step in range(2):
+        hi, lo, eh, el, ef_new = oq.block_dual_quantize(W.float().numpy(), bs, ef_o)
+        h, l, sh, sl = K.fused_dual_quantize_fp8(W.to(dev), bs, error_buf=ef_d)
+        assert np.array_equal(u8(h), hi) and np.array_equal(u8(l), lo)
+        assert np.array_equal(i8(sh), eh) and np.array_equal(i8(sl), el)
+        assert np.array_equal(ef_d.cpu().numpy(), ef_new), f"step {step}"
+        ef_o = ef_new
+
+
+def test_block_dual_quantize_sentinel_and_no_ef(dev):
+    W = torch.zeros(8, 64)
+    W[2] = 1.0
+    W[5, :32] = torch.randn(32)
+    hi, lo, eh, el, _ = oq.block_dual_quantize(W.numpy(), 32)
+    h, l, sh, sl = K.fused_dual_quantize_fp8(W.to(dev), 32)
+    assert np.array_equal(i8(sl), el) and (i8(sl)[:, 2] == -128).all()
+    assert np.array_equal(u8(h), hi) and np.array_equal(u8(l), lo)
+
+
+def test_block_dual_quantize_sr(dev):
+    g = torch.Generator().manual_seed(9)
+    W = torch.randn(64, 256, generator=g)
+    hi, lo_rtn, eh, el, _ = oq.block_dual_quantize(W.numpy(), 64)
+    wb = W.numpy().reshape(64, 4, 64)
+    deq_hi = oq.block_dequantize(hi, eh, 64).reshape(64, 4, 64)
+    r = (wb - deq_hi).astype(np.float32)
+    x = np.clip(r * (2.0 ** -el.T.astype(np.float64))[..., None], -448, 448).astype(np.float32).reshape(64, 256)
+    rtn, other, frac, exact = oq.sr_candidates_block(x)
+    assert np.array_equal(rtn, lo_rtn)
+    acc = np.zeros(x.shape)
+    n = 200
+    for i in range(n):
+        h, l, sh, sl = K.fused_dual_quantize_fp8(W.to(dev), 64, stochastic_lo=True, seed=77 + i)
+        assert np.array_equal(u8(h), hi) and np.array_equal(i8(sl), el)
+        c = u8(l)
+        assert np.all((c == rtn) | (c == other))
+        assert np.all(c[exact] == rtn[exact])
+        acc += (c == other) & (other != rtn)
+    m = ~exact & (other != rtn)
+    p = acc / n
+    assert abs(float((p[m] - frac[m]).mean())) < 0.01
+    # unbiased: E[deq(lo)] ~= residual
+    assert float(np.abs(p[m] - frac[m]).max()) < 0.2

@@ -1,0 +1,137 @@
+"""CPU tests of the host side: the C-ABI library loads and exports every
+symbol include/tcfp_hip.h declares, the Python boundary validates like the
+reference, and the module/state-machine logic behaves like tcfp.nn.
+No kernel is launched here."""
+import re
+from pathlib import Path
+
+import pytest
+import torch
+import torch.nn as nn
+
+from tcfp_amd import _hip
+from tcfp_amd import kernels as K
+from tcfp_amd.core import ErrorFeedbackState, FP8Config, to_fp8_e4m3
+from tcfp_amd.nn import TCFPLinear, convert_to_tcfp
+
+HEADER = Path(__file__).resolve().parent.parent / "include" / "tcfp_hip.h"
+
+
+def _declared():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(tcfp_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _hip.load_library()
+    declared = _declared()
+    assert declared, "no declarations parsed"
+    missing = [s for s in declared if not hasattr(lib, s)]
+    assert not missing, missing
+    # and the ctypes table binds exactly the declared set
+    assert sorted(_hip.exported_symbols()) == declared
+
+
+def test_status_strings_and_workspace_size():
+    lib = _hip.load_library()
+    assert lib.tcfp_status_string(0) == b"ok"
+    assert b"mutually exclusive" in lib.tcfp_status_string(6)
+    assert lib.tcfp_workspace_bytes() >= 32
+
+
+def test_argument_validation_without_launch():
+    lib = _hip.load_library()
+    # bad shapes/dtypes are rejected before any HIP call
+    assert lib.tcfp_block_quantize(None, 0, 4, 48, 32, 0, None, None, None) == 1
+    assert lib.tcfp_block_quantize(None, 7, 4, 64, 32, 0, None, None, None) == 2
+    assert lib.tcfp_dual_gemm(None, 0, 32, None, None, 0, 32, 4, 4, 24, None, None, None, None,
+                              None, 0, 4, None) == 1  # K % 16
+    assert lib.tcfp_block_dual_quantize(None, 0, 4, 64, 32, 1, 1, 1, 0, 0, None, None, None,
+                                        None, None) == 6  # SR + EF
+
+
+def test_cpu_tensors_fail_loudly():
+    with pytest.raises(RuntimeError, match="only on the GPU"):
+        to_fp8_e4m3(torch.randn(4, 4))
+    with pytest.raises(RuntimeError, match="only on the GPU"):
+        K.block_quantize_fp8(torch.randn(4, 64), 32)
+
+
+def test_fused_dual_quantize_validation_messages():
+    w = torch.randn(8, 64)
+    with pytest.raises(AssertionError, match="contiguous"):
+        K.fused_dual_quantize_fp8(w.t(), block_size=32)
+    with pytest.raises(AssertionError, match="divisible"):
+        K.fused_dual_quantize_fp8(torch.randn(8, 48), block_size=32)
+    with pytest.raises(ValueError, match="mutually exclusive"):
+        K.fused_dual_quantize_fp8(w, 32, error_buf=torch.zeros(8, 64), stochastic_lo=True)
+    with pytest.raises(AssertionError, match="float32"):
+        K.fused_dual_quantize_fp8(w, 32, error_buf=torch.zeros(8, 64, dtype=torch.float64))
+    with pytest.raises(AssertionError, match="shape"):
+        K.fused_dual_quantize_fp8(w, 32, error_buf=torch.zeros(8, 32))
+
+
+def test_error_feedback_state():
+    st = ErrorFeedbackState()
+    w = torch.randn(4, 8)
+    b = st.get_error("a", w)
+    assert b.dtype == torch.float32 and b.shape == w.shape and (b == 0).all()
+    assert st.get_error("a", w) is b
+    st.update_error("a", torch.ones(4, 8, requires_grad=True))
+    assert not st._buffers["a"].requires_grad
+    assert st.get_error("a", torch.randn(2, 2)).shape == (2, 2)  # shape change re-inits
+    st.reset()
+    assert st._buffers == {}
+
+
+def test_fp8_config_validation():
+    with pytest.raises(ValueError):
+        FP8Config(block_size=24)
+
+
+def test_tcfplinear_validation_messages():
+    with pytest.raises(ValueError, match="32, 64, or 128"):
+        TCFPLinear(64, 64, use_tensor_cores=True, scale_block_size=16)
+    with pytest.raises(ValueError, match="in_features.*divisible"):
+        TCFPLinear(48, 64, use_tensor_cores=True, scale_block_size=32)
+    with pytest.raises(ValueError, match="out_features.*divisible"):
+        TCFPLinear(64, 48, use_tensor_cores=True, scale_block_size=32)
+    with pytest.raises(NotImplementedError):
+        TCFPLinear(64, 64)  # fake-quantise path is out of scope
+
+
+def test_tcfplinear_state_and_srr_disables_ef():
+    lin = TCFPLinear(32, 16, use_tensor_cores=True)
+    assert lin._error_state is not None and lin.weight.shape == (16, 32)
+    assert TCFPLinear(32, 16, use_tensor_cores=True, srr=True)._error_state is None
+    assert TCFPLinear(32, 16, use_tensor_cores=True, error_feedback=False)._error_state is None
+    assert "use_tensor_cores=True" in repr(lin)
+
+
+def test_convert_to_tcfp_structure():
+    model = nn.Sequential(
+        nn.Linear(64, 128), nn.GELU(), nn.Linear(128, 64),
+        nn.Sequential(nn.Linear(64, 40)),  # 40 % 16 != 0 -> stays nn.Linear
+    )
+    model.head = nn.Linear(64, 64)
+    w0 = model[0].weight
+    convert_to_tcfp(model, use_tensor_cores=True, scale_block_size=64)
+    assert isinstance(model[0], TCFPLinear) and model[0].weight is w0
+    assert model[0]._param_name == "0" and model[2]._param_name == "2"
+    assert model[0].scale_block_size == 64
+    assert type(model[3][0]) is nn.Linear
+    assert type(model.head) is nn.Linear  # skip pattern
+    # scale block dropped per layer when it does not divide
+    m2 = convert_to_tcfp(nn.Sequential(nn.Linear(96, 64)), use_tensor_cores=True,
+                         scale_block_size=64)
+    assert m2[0].scale_block_size is None
+
+
+def test_ef_guard_version_logic_cpu():
+    # the guard reads weight._version; in-place optimizer steps bump it
+    lin = TCFPLinear(32, 16, use_tensor_cores=True)
+    v0 = lin.weight._version
+    with torch.no_grad():
+        lin.weight.add_(1.0)
+    assert lin.weight._version != v0

@@ -1,0 +1,247 @@
+"""CPU tests pinning the numpy oracle (no GPU).
+
+The oracle is checked against (a) the committed torch-CPU fixtures in
+tests/golden/ (torch is the library the reference's FP8 path is written in),
+(b) brute force over the FP8 code tables and exact integer maths, and
+(c) the invariants the reference's own tests assert.  Each check is chosen
+so that a plausible slip in the oracle (wrong rounding direction, a dropped
+clamp, dtype of the scale arithmetic, op order of the error update) fails.
+"""
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from oracle import fp8 as ofp8
+from oracle import gemm as og
+from oracle import quant as oq
+
+GOLD = np.load(Path(__file__).parent / "golden" / "torch_primitives.npz")
+
+
+# ---------------------------------------------------------------- fp8 casts
+def test_decode_tables_match_torch():
+    for fmt, key in ((ofp8.E4M3, "dec_e4m3"), (ofp8.E5M2, "dec_e5m2")):
+        mine = ofp8.DECODE[fmt]
+        ref = GOLD[key]
+        same = (mine == ref) | (np.isnan(mine) & np.isnan(ref))
+        assert same.all(), fmt
+
+
+@pytest.mark.parametrize("fmt", [ofp8.E4M3, ofp8.E5M2])
+def test_encode_matches_torch_fixture(fmt):
+    x, c = (GOLD["x_e4m3"], GOLD["c_e4m3"]) if fmt == ofp8.E4M3 else (GOLD["x_e5m2"], GOLD["c_e5m2"])
+    assert np.array_equal(ofp8.encode(x, fmt), c)
+
+
+def _brute_nearest_even(x, fmt):
+    """Nearest finite code by exhaustive search; ties -> even mantissa."""
+    table = ofp8.DECODE[fmt].astype(np.float64)
+    codes = np.arange(256)
+    ok = np.isfinite(table)
+    table, codes = table[ok], codes[ok]
+    out = np.empty(x.shape, dtype=np.uint8)
+    for i, v in enumerate(x.astype(np.float64)):
+        d = np.abs(table - v)
+        best = d.min()
+        cand = codes[d == best]
+        # prefer same sign (signed zero) then even mantissa bit
+        sgn = 0x80 if np.signbit(v) else 0
+        cand = sorted(cand, key=lambda c: (((c & 0x80) != sgn), c & 1))
+        out[i] = cand[0]
+    return out
+
+
+@pytest.mark.parametrize("fmt", [ofp8.E4M3, ofp8.E5M2])
+def test_encode_is_nearest_even_by_brute_force(fmt):
+    rng = np.random.default_rng(1)
+    mx = ofp8.FP8_MAX[fmt]
+    fin = np.unique(ofp8.DECODE[fmt][np.isfinite(ofp8.DECODE[fmt])]).astype(np.float64)
+    mids = ((fin[:-1] + fin[1:]) / 2).astype(np.float32)
+    x = np.concatenate([
+        rng.uniform(-mx, mx, 1500).astype(np.float32),
+        (rng.standard_normal(1500) * 2.0 ** rng.integers(-20, 4, 1500)).astype(np.float32),
+        mids, np.nextafter(mids, np.float32(np.inf)), np.nextafter(mids, np.float32(-np.inf)),
+        np.float32([0.0, -0.0, 1e-30, -1e-30, mx, -mx]),
+    ]).astype(np.float32)
+    assert np.array_equal(ofp8.encode(x, fmt), _brute_nearest_even(x, fmt))
+
+
+def test_bf16_round_matches_torch():
+    import torch
+
+    rng = np.random.default_rng(2)
+    x = (rng.standard_normal(200000) * 10.0 ** rng.uniform(-10, 10, 200000)).astype(np.float32)
+    assert np.array_equal(ofp8.bf16_round(x), torch.from_numpy(x).bfloat16().float().numpy())
+
+
+# ------------------------------------------------------------ ceil(log2(q))
+def test_ceil_log2_matches_torch_fixture():
+    assert np.array_equal(oq.ceil_log2_f32(GOLD["q"]), GOLD["clog2"].astype(np.int64))
+
+
+def test_ceil_log2_is_exact_away_from_boundaries():
+    # for q far from a power of two, ceil(log2(q)) is the exact integer
+    rng = np.random.default_rng(3)
+    k = rng.integers(-126, 120, 50000)
+    m = rng.uniform(1.01, 1.99, 50000)
+    q = (m * 2.0 ** k).astype(np.float32)
+    assert np.array_equal(oq.ceil_log2_f32(q), k + 1)
+    # exact powers of two
+    p = (2.0 ** np.arange(-126, 127)).astype(np.float32)
+    assert np.array_equal(oq.ceil_log2_f32(p), np.arange(-126, 127))
+
+
+def test_ceil_log2_boundary_rounds_like_correctly_rounded_log2():
+    # q = 2^k (1 + j 2^-23): a correctly rounded fp32 log2 returns exactly k
+    # for small j; high-precision log2 + fp32 rounding decides which j.
+    ks = np.arange(-126, 121)
+    js = np.arange(1, 30)
+    bits = ((ks[:, None] + 127) << 23) | js[None, :]
+    q = bits.astype(np.uint32).view(np.float32)
+    exact = np.log2(1.0 + js.astype(np.longdouble) * np.longdouble(2.0) ** -23)
+    rl = (ks[:, None].astype(np.longdouble) + exact[None, :]).astype(np.float32)
+    expect = np.where(rl == ks[:, None].astype(np.float32), ks[:, None], ks[:, None] + 1)
+    assert np.array_equal(oq.ceil_log2_f32(q.ravel()), expect.ravel())
+
+
+# ------------------------------------------------------ per-tensor scaling
+def test_per_tensor_scale_matches_torch_rdiv_fp32():
+    for a, s, inv in zip(GOLD["amax"], GOLD["scale_f32"], GOLD["inv_f32"]):
+        t = np.array([a, -a / 2], dtype=np.float32)
+        sc = oq.per_tensor_scale(t, "f32")
+        assert sc == s and np.float32(1.0) / sc == inv
+
+
+def test_per_tensor_scale_matches_torch_rdiv_e5m2():
+    for a, s in zip(GOLD["amax"][:500], GOLD["scale_f32_e5m2"][:500]):
+        assert oq.per_tensor_scale(np.array([a], np.float32), "f32", ofp8.E5M2) == s
+
+
+def test_per_tensor_scale_bf16_rounds_in_bf16():
+    for a, s, inv in zip(GOLD["amax_bf16"], GOLD["scale_bf16"], GOLD["inv_bf16"]):
+        sc = oq.per_tensor_scale(np.array([a], np.float32), "bf16")
+        assert sc == s and np.float32(1.0) / sc == inv
+    # the C1 example: X ~ N(0,1) bf16 with amax 5.25 -> 85.5 (not 85.33)
+    assert oq.per_tensor_scale(np.array([5.25], np.float32), "bf16") == np.float32(85.5)
+
+
+def test_to_fp8_per_tensor_special_cases():
+    z = np.zeros((4, 8), np.float32)
+    codes, inv, scale = oq.to_fp8_per_tensor(z)
+    assert (codes == 0).all() and scale == np.float32(448.0) / np.float32(1e-12) * 0 + oq.per_tensor_scale(z, "f32")
+    # the amax element maps exactly to +-448
+    x = np.array([[0.5, -3.0, 1.0]], np.float32)
+    codes, inv, scale = oq.to_fp8_per_tensor(x)
+    assert ofp8.decode(codes, ofp8.E4M3)[0, 1] == -448.0
+    # values below half the smallest subnormal flush to (signed) zero
+    x = np.array([448.0, 2.0 ** -10, -(2.0 ** -10), 2.0 ** -9], np.float32)
+    codes, _, _ = oq.to_fp8_per_tensor(x)
+    assert list(codes) == [0x7E, 0x00, 0x80, 0x01]
+
+
+# ------------------------------------------------------- dual quant (a2)
+def test_dual_quant_per_tensor_invariants():
+    rng = np.random.default_rng(4)
+    W = (rng.standard_normal((64, 96)) * 0.02).astype(np.float32)
+    ef = (rng.standard_normal((64, 96)) * 1e-5).astype(np.float32)
+    hi, lo, ih, il, ef_new, res = oq.dual_quant_per_tensor(W, ef)
+    w = W + ef
+    # hi is the plain per-tensor cast of W + EF, lo the cast of the residual
+    hi2, ih2, _ = oq.to_fp8_per_tensor(w)
+    assert np.array_equal(hi, hi2) and ih == ih2
+    lo2, il2, _ = oq.to_fp8_per_tensor(w - ofp8.decode(hi, ofp8.E4M3) * ih)
+    assert np.array_equal(lo, lo2) and il == il2
+    # error is relative to W (not W + EF) and closes the decomposition
+    rec = ofp8.decode(hi, ofp8.E4M3) * ih + ofp8.decode(lo, ofp8.E4M3) * il
+    assert np.allclose(rec + ef_new, W, atol=1e-9, rtol=0)
+    assert not np.allclose(rec + ef_new, w, atol=1e-9, rtol=0)
+    # dual FP8 beats a single FP8 cast by a wide margin
+    single = ofp8.decode(hi2, ofp8.E4M3) * ih2
+    assert np.abs(W - rec).mean() < np.abs(w - single).mean() / 4
+    # zero EF == no EF
+    a = oq.dual_quant_per_tensor(W, np.zeros_like(W))
+    b = oq.dual_quant_per_tensor(W, None)
+    assert all(np.array_equal(x, y) for x, y in zip(a, b))
+
+
+def test_sr_candidates_per_tensor():
+    rng = np.random.default_rng(5)
+    x = np.clip(rng.standard_normal(20000).astype(np.float32) * 100, -448, 448)
+    lo, hi, frac, exact = oq.sr_candidates_per_tensor(x)
+    lo_f, hi_f = ofp8.decode(lo, ofp8.E4M3), ofp8.decode(hi, ofp8.E4M3)
+    ok = ~exact & np.isfinite(hi_f)
+    # x lies between the two candidates and frac is its relative position
+    assert (np.minimum(lo_f, hi_f)[ok] <= x[ok]).all() and (x[ok] <= np.maximum(lo_f, hi_f)[ok]).all()
+    e = lo_f + np.sign(hi_f - lo_f) * frac * np.abs(hi_f - lo_f)
+    assert np.allclose(e[ok], x[ok], rtol=1e-5, atol=1e-6)
+
+
+# ------------------------------------------------------- block quant (a4)
+@pytest.mark.parametrize("bs", [32, 64, 128])
+def test_block_quantize_exponent_and_codes(bs):
+    import torch
+
+    rng = np.random.default_rng(6 + bs)
+    x = (rng.standard_normal((16, 4 * bs)) * 2.0 ** rng.integers(-20, 20, (16, 1))).astype(np.float32)
+    codes, exps = oq.block_quantize(x, bs)
+    assert exps.shape == (4, 16) and exps.dtype == np.int8
+    # exponent: torch's ceil(log2(amax / 448)) on the block amax
+    amax = torch.from_numpy(np.abs(x).reshape(16, 4, bs).max(-1)).clamp(min=1e-12)
+    e_t = torch.clamp(torch.ceil(torch.log2(amax / 448.0)), min=-126).to(torch.int8).numpy()
+    assert np.array_equal(exps.T, e_t)
+    # codes: brute-force nearest-even of x / 2^e
+    scaled = x.reshape(16, 4, bs) / (2.0 ** exps.T.astype(np.float64))[..., None]
+    assert np.array_equal(codes.ravel(), _brute_nearest_even(np.clip(scaled, -448, 448).astype(np.float32).ravel(), ofp8.E4M3))
+
+
+def test_block_quantize_zero_and_e5m2():
+    codes, exps = oq.block_quantize(np.zeros((3, 64), np.float32), 32)
+    assert (codes == 0).all() and (exps == -48).all()  # ceil(log2(1e-12/448)) = -48
+    x = np.full((2, 32), 2.0 ** 20, np.float32)  # amax/57344 = 18.3 -> e = 5
+    c, e = oq.block_quantize(x, 32, ofp8.E5M2)
+    assert (e == 5).all()
+    assert np.all(ofp8.decode(c, ofp8.E5M2) * 2.0 ** e.T.repeat(32, 1).astype(np.float64) == 2.0 ** 20)
+
+
+# ----------------------------------------------- block dual quant (a3)
+@pytest.mark.parametrize("bs", [32, 64, 128])
+def test_block_dual_equals_separate_block_quantize(bs):
+    # the reference's bitwise fused-vs-separate test (test_fused_dual_quant.py:79-155)
+    rng = np.random.default_rng(7)
+    w = rng.standard_normal((32, 2 * bs)).astype(np.float32)
+    ef = (rng.standard_normal(w.shape) * 1e-3).astype(np.float32)
+    hi, lo, eh, el, ef_new = oq.block_dual_quantize(w, bs, ef)
+    wc = w + ef
+    hi2, eh2 = oq.block_quantize(wc, bs)
+    assert np.array_equal(hi, hi2) and np.array_equal(eh, eh2)
+    res = wc - oq.block_dequantize(hi2, eh2, bs)
+    lo2, el2 = oq.block_quantize(res, bs)
+    assert np.array_equal(lo, lo2) and np.array_equal(el, el2)
+    expect = w - (oq.block_dequantize(hi, eh, bs) + oq.block_dequantize(lo, el, bs))
+    assert np.allclose(ef_new, expect, atol=1e-5, rtol=1e-5)
+
+
+def test_block_dual_zero_residual_sentinel():
+    w = np.zeros((4, 64), np.float32)
+    w[1] = 1.0  # exactly representable: residual is zero
+    hi, lo, eh, el, _ = oq.block_dual_quantize(w, 32)
+    assert (el == -128).all() and (lo == 0).all()
+    assert ((el >= -126) | (el == -128)).all()
+
+
+# ------------------------------------------------------- GEMM oracle
+def test_dual_gemm_oracle_closed_forms():
+    rng = np.random.default_rng(8)
+    a = rng.integers(0, 256, (8, 32)).astype(np.uint8)
+    a[(a & 0x7F) == 0x7F] = 0  # no NaN codes
+    hi = rng.integers(0, 256, (5, 32)).astype(np.uint8)
+    hi[(hi & 0x7F) == 0x7F] = 1
+    lo = np.zeros_like(hi)
+    out = og.dual_gemm_nt(a, ofp8.E4M3, hi, lo, 0.5, 2.0, 3.0)
+    A = ofp8.decode(a, ofp8.E4M3).astype(np.float64)
+    B = ofp8.decode(hi, ofp8.E4M3).astype(np.float64)
+    brute = np.array([[sum(A[i, k] * B[j, k] for k in range(32)) for j in range(5)] for i in range(8)])
+    assert np.allclose(out, brute, rtol=1e-12, atol=0)
+    # linear in each scale
+    assert np.allclose(og.dual_gemm_nt(a, ofp8.E4M3, lo, hi, 0.5, 2.0, 3.0), 1.5 * brute)
