@@ -215,7 +215,8 @@ def sr_candidates_block(x: np.ndarray):
     other = encode(np.clip(rtn_f + nudge, -mx, mx), E4M3)
     other_f = decode(other, E4M3)
     gap = np.maximum(np.abs(other_f - rtn_f), F32(1e-45))
-    frac = np.minimum(np.abs(diff) / gap, F32(1))
+    with np.errstate(over="ignore"):
+        frac = np.minimum(np.abs(diff) / gap, F32(1))
     boundary = np.abs(other_f - rtn_f) < F32(1e-45)
     exact = (np.abs(diff) < F32(1e-45)) | boundary
     return rtn, other, frac.astype(F32), exact
