@@ -41,8 +41,12 @@ def make_act(shape, seed, dev, fp8=torch.float8_e4m3fn):
     return q, inv
 
 
+# (M, K, N): K = 16 and 192 give an odd number of 64-wide K steps, K = 80 and
+# 208 a partial last step; N = 130 and 1000 exercise the column tail (N % 4,
+# N % 128) and M = 260, 33 the row tail.
 SHAPES = [(64, 128, 64), (256, 512, 256), (128, 256, 512), (48, 80, 112), (16, 16, 16),
-          (300, 208, 1000), (1024, 1024, 1024)]
+          (300, 208, 1000), (1024, 1024, 1024), (260, 192, 130), (33, 320, 72),
+          (512, 64, 384)]
 
 
 @pytest.mark.parametrize("M,K_,N", SHAPES)
