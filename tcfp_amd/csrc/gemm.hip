@@ -386,15 +386,19 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_nt_dma_kernel(
   const int nt = (K + kSK - 1) / kSK;
   const int krem = K - (nt - 1) * kSK;  // valid K columns of the last stage
 
-  // DMA of stage t (K columns t*128 ..) into buffer t & 1.
+  // DMA of stage t (K columns t*128 ..) into buffer t & 1.  Stages past the
+  // end are issued as all-out-of-range loads (zeros into a buffer nobody
+  // reads again): the issue stays branch-free, so the loop body is a single
+  // basic block and the compiler cannot sink MFMAs across the barrier.
   auto issue = [&](int t) {
     const uint32_t dst = lds_base + uint32_t(t & 1) * kStageBytes;
-    const uint32_t soff = uint32_t(t) * kSK;
+    const bool live = t < nt;
+    const uint32_t soff = uint32_t(live ? t : 0) * kSK;
     const bool last = t == nt - 1;
 #pragma unroll
     for (int i = 0; i < DI; ++i) {
       const int c = (i & 1) ? chunk1 : chunk0;
-      dma16(rsrc, (last && c * 16 >= krem) ? kOob : voff[i], soff, dst + i * 1024);
+      dma16(rsrc, (!live || (last && c * 16 >= krem)) ? kOob : voff[i], soff, dst + i * 1024);
     }
   };
 
@@ -442,10 +446,15 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_nt_dma_kernel(
   auto interleave = [&]() { interleave_mfma_lds<4 * MB, 2 * (4 + MB), 0>(); };
   // All DMA issued so far has landed and every wave's LDS reads are done
   // (gfx9 s_waitcnt: vmcnt bits [3:0] and [15:14], expcnt [6:4], lgkmcnt [11:8]).
+  // sched_barrier(0) keeps the scheduler from moving MFMAs across it: MFMAs
+  // touch no memory, so without it they drift past the barrier and the LDS
+  // reads before it are left with nothing to hide behind.
   auto sync_all = [&]() {
+    __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0), expcnt untouched
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
   };
 
   v8i f0[4 + MB], f1[4 + MB];
@@ -466,7 +475,8 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_nt_dma_kernel(
     interleave();
     // stage t + 1 landed, every wave has its stage-t fragments: refill t's buffer
     sync_all();
-    if (t + 2 < nt) issue(t + 2);
+    issue(t + 2);
+    __builtin_amdgcn_sched_barrier(0);
     // sub-step 1 of stage t; fragments of stage t + 1 sub-step 0 stream in
     // (after the last stage they read a stale buffer and are never used)
     read_frags(f0, t + 1, 0);
@@ -474,41 +484,71 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_nt_dma_kernel(
     interleave();
   }
 
-  // ---- epilogue: lane holds rows m, columns n..n+3 of each 32x32 block
+  // ---- epilogue -----------------------------------------------------------
+  // A lane holds rows m, columns n..n+3 of each 32x32 block: storing that
+  // directly writes 16 bytes into each of 32 rows per instruction.  Instead
+  // each wave stages its 64-column tile (per slot) through its own LDS
+  // region and stores whole rows: 8 (bf16) or 4 (fp32) rows of 128/256
+  // bytes per instruction, i.e. full cache lines.
+  constexpr int EB = int(sizeof(OutT));      // output element bytes
+  constexpr int RB = 64 * EB;                // bytes of one staged tile row
+  constexpr int CPR = RB / 16;               // 16-byte chunks per row (8 / 16)
+  constexpr int RPI = 64 / CPR;              // rows per store instruction
+  uint8_t* eps = lds + wave * (TMW * RB);    // this wave's staging region
   const float sa = *s_a;
   const float c0s = sa * *s_0;
   const float c1s = SPLIT ? c0s : sa * *s_1;
-  const bool vec = (ldo & 3) == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0;
+  const bool vec = (ldo % (16 / EB)) == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0;
+  // every wave is done with the operand buffers before they are reused
+  __builtin_amdgcn_s_waitcnt(0x0070);
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
 #pragma unroll
-  for (int i = 0; i < MB; ++i) {
-    const int m = m0 + wm * TMW + i * 32 + lr;
-    if (m >= M) continue;
-    OutT* orow = out + int64_t(m) * ldo;
+  for (int s = 0; s < (SPLIT ? 2 : 1); ++s) {
+    const int nb = (s ? n1 : n0) + wn * 64;  // first output column of this tile
 #pragma unroll
-    for (int s = 0; s < (SPLIT ? 2 : 1); ++s)
+    for (int i = 0; i < MB; ++i)
 #pragma unroll
       for (int j = 0; j < 2; ++j)
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-          const int n = (s ? n1 : n0) + wn * 64 + j * 32 + g * 8 + lg * 4;
+          const int row = i * 32 + lr, col = j * 32 + g * 8 + lg * 4;
           float v[4];
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
             const int r = g * 4 + q;
             v[q] = SPLIT ? acc[s][j][i][r] * c0s : acc[0][j][i][r] * c0s + acc[1][j][i][r] * c1s;
           }
-          if (vec && n + 3 < N) {
-            if (bias) {
-              const float4 b = *reinterpret_cast<const float4*>(bias + n);
-              v[0] += b.x; v[1] += b.y; v[2] += b.z; v[3] += b.w;
-            }
-            store4<OutT>(orow + n, v[0], v[1], v[2], v[3]);
-          } else {
+          if (bias) {
 #pragma unroll
-            for (int q = 0; q < 4; ++q)
-              if (n + q < N) store_out<OutT>(orow + n + q, v[q] + (bias ? bias[n + q] : 0.0f));
+            for (int q = 0; q < 4; ++q) v[q] += nb + col + q < N ? bias[nb + col + q] : 0.0f;
           }
+          // 16-byte chunk index within the row, XOR-permuted by row
+          const int byte = col * EB;
+          const int chunk = (byte >> 4) ^ (row & (CPR - 1));
+          store4<OutT>(reinterpret_cast<OutT*>(eps + row * RB + chunk * 16 + (byte & 15)), v[0],
+                       v[1], v[2], v[3]);
         }
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int it = 0; it < TMW / RPI; ++it) {
+      const int row = it * RPI + lane / CPR, cl = lane % CPR;
+      const uint4 d = *reinterpret_cast<const uint4*>(eps + row * RB + ((cl ^ (row & (CPR - 1))) * 16));
+      const int m = m0 + wm * TMW + row;
+      const int n = nb + cl * (16 / EB);
+      if (m < M) {
+        OutT* o = out + int64_t(m) * ldo + n;
+        if (vec && n + 16 / EB <= N) {
+          *reinterpret_cast<uint4*>(o) = d;
+        } else {
+          const OutT* e = reinterpret_cast<const OutT*>(&d);
+#pragma unroll
+          for (int q = 0; q < 16 / EB; ++q)
+            if (n + q < N) o[q] = e[q];
+        }
+      }
+    }
+    asm volatile("" ::: "memory");
   }
 }
 
