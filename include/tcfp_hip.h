@@ -46,10 +46,12 @@ extern "C" {
 /* Human-readable text for a status code (static storage). */
 const char* tcfp_status_string(int status);
 
-/* Bytes of zero-initialised device workspace the per-tensor reductions
- * need.  The library leaves the workspace zeroed again when each call's
- * kernels finish, so one buffer serves every call on a stream.  Calls
- * that overlap in time must use different workspaces. */
+/* Bytes of device workspace the per-tensor reductions need.  Reducing
+ * kernels store one partial maximum per workgroup there and the kernel that
+ * consumes the scale reduces them again, so the workspace needs no
+ * initialisation and is never left in a state a later call depends on.
+ * Calls that may run concurrently (different streams) need different
+ * workspaces; calls ordered on one stream can share one. */
 size_t tcfp_workspace_bytes(void);
 
 /* ---- per-tensor quantisation ------------------------------------------- */
@@ -135,6 +137,24 @@ int tcfp_dual_gemm(const uint8_t* a, int a_fmt, int64_t lda, const uint8_t* b_hi
                    int64_t k, const float* s_a, const float* s_hi, const float* s_lo,
                    const float* bias, void* out, int out_dtype, int64_t ldo, void* stream);
 
+/* Block-scaled dual FP8 GEMM, both operands K-contiguous ("NT"):
+ *   out[i,j] = sum_kb 2^ea[kb,i] * ( 2^ehi[kb,j] * sum_{k in kb} A[i,k] B_hi[j,k]
+ *                                  + 2^elo[kb,j] * sum_{k in kb} A[i,k] B_lo[j,k] ) (+ bias[j])
+ * with int8 exponent arrays e_a [k/block, m], e_hi / e_lo [k/block, n]
+ * (the layout block_quantize / block_dual_quantize produce).  An exponent
+ * of -128 in e_lo (a zero-residual block) contributes nothing.
+ * Replaces fused_block_scaled_dual_gemm_forward (tcfp/kernels.py:1939-2028,
+ * kernel :628-796); with b_lo == NULL it is the single block-scaled GEMM
+ * block_scaled_gemm (tcfp/kernels.py:1878-1936, kernel :491-600).
+ *   block in {32, 64, 128}; k % block == 0; other constraints as
+ *   tcfp_dual_gemm.  The exponents are applied by the MFMA's E8M0 scale
+ *   operands (exact powers of two); accumulation is fp32. */
+int tcfp_block_dual_gemm(const uint8_t* a, int a_fmt, int64_t lda, const int8_t* e_a,
+                         const uint8_t* b_hi, const uint8_t* b_lo, int b_fmt, int64_t ldb,
+                         const int8_t* e_hi, const int8_t* e_lo, int64_t m, int64_t n,
+                         int64_t k, int block, const float* bias, void* out, int out_dtype,
+                         int64_t ldo, void* stream);
+
 /* ---- layout helpers ---------------------------------------------------- */
 
 /* dst[c, r] = src[r, c] for a [rows, cols] byte matrix (ld = cols / rows).
@@ -142,6 +162,13 @@ int tcfp_dual_gemm(const uint8_t* a, int a_fmt, int64_t lda, const uint8_t* b_hi
  * (tcfp/core.py:196-213, tcfp/nn/__init__.py:546-555). */
 int tcfp_transpose_u8(const uint8_t* src, int64_t rows, int64_t cols, uint8_t* dst,
                       void* stream);
+
+/* ---- tuning hooks (no reference counterpart) --------------------------- */
+
+/* GEMM tile selection for all later calls in the process: 0 automatic (the
+ * 256 x 128 tile unless it would leave CUs idle), 1 always 256 x 128,
+ * 2 always 128 x 64.  Results do not depend on the policy. */
+int tcfp_gemm_set_tile_policy(int policy);
 
 /* ---- self-test hooks (no reference counterpart) ------------------------ */
 

@@ -42,6 +42,10 @@ _SIGNATURES = {
     "tcfp_dual_gemm": [_c_void_p, _i32, _i64, _c_void_p, _c_void_p, _i32, _i64, _i64, _i64, _i64,
                        _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i32, _i64,
                        _c_void_p],
+    "tcfp_block_dual_gemm": [_c_void_p, _i32, _i64, _c_void_p, _c_void_p, _c_void_p, _i32, _i64,
+                             _c_void_p, _c_void_p, _i64, _i64, _i64, _i32, _c_void_p, _c_void_p,
+                             _i32, _i64, _c_void_p],
+    "tcfp_gemm_set_tile_policy": [_i32],
     "tcfp_transpose_u8": [_c_void_p, _i64, _i64, _c_void_p, _c_void_p],
     "tcfp_selftest_fp8_cvt": [_u32, _u32, _i32, _c_void_p, _c_void_p],
     "tcfp_selftest_philox": [_u32, _u32, _u32, _u32, _u32, _u32, _i64, _c_void_p, _c_void_p],
@@ -113,17 +117,18 @@ _ws: dict[tuple[int, int], torch.Tensor] = {}
 
 
 def workspace(device: torch.device) -> torch.Tensor:
-    """Zeroed reduction workspace for the current stream of ``device``.
+    """Reduction scratch for the current stream of ``device``.
 
-    The kernels leave it zeroed again after every call, so one buffer per
-    (device, stream) is reused for all calls enqueued on that stream.
+    Per-tensor reductions pass per-workgroup partial maxima from one launch
+    to the next through it; it needs no initialisation, and stream order
+    makes one buffer per (device, stream) safe for every call on that stream.
     """
     idx = device.index if device.index is not None else torch.cuda.current_device()
     key = (idx, stream_of(device))
     ws = _ws.get(key)
     if ws is None:
         nbytes = int(lib().tcfp_workspace_bytes())
-        ws = torch.zeros(nbytes, dtype=torch.uint8, device=device)
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=device)
         _ws[key] = ws
     return ws
 

@@ -229,14 +229,23 @@ constexpr int kBK = 64;
 // Main kernel: LDS double buffer filled by direct global->LDS DMA
 // ===========================================================================
 //
-// Same 256 x (2 x 128) workgroup tile and 2 x 2 wave grid as above, with
-// the choices that measured fastest on gfx950:
+// A workgroup owns a BM (activation rows) x BN (weight rows) output tile
+// and stages, per 128-column K step, BM activation rows and BN rows of each
+// of two weight "slots" (W_hi and W_lo for the dual GEMM; adjacent column
+// halves of one 2*BN-wide tile for a single GEMM).  Waves form a
+// (NW/2) x 2 grid.  Two shapes are built:
+//   BM = 256, BN = 128, 8 waves  -- one workgroup per CU, 128 KiB of LDS;
+//   BM = 128, BN =  64, 4 waves  -- two workgroups per CU, so one
+//       workgroup's epilogue overlaps the other's main loop; used when the
+//       large tile would leave CUs idle (e.g. the wgrad GEMMs, whose
+//       outputs are small and whose K is the token count).
+// Choices that measured fastest on gfx950:
 //  * Operand tiles go from HBM/L2 straight into LDS with
 //    `buffer_load_dwordx4 ... lds` (no VGPR staging, no LDS store
 //    instructions).  A stage covers 128 K columns, so every row
 //    contributes one full 128-byte cache line per stage: fetching half
 //    lines (64 K columns) halves the L2->LDS rate (27 vs 57 B/clk/CU
-//    measured).  Two 64 KiB stages fill 128 KiB of the 160 KiB LDS.
+//    measured).
 //  * Each stage is two MFMA sub-steps of 64 K.  Fragments live in two
 //    register sets: while the MFMAs of one sub-step run, the fragments of
 //    the next are read from LDS, one 16-byte LDS read per MFMA.  The DMA
@@ -250,23 +259,36 @@ constexpr int kBK = 64;
 //    so an accumulator lane holds four consecutive output columns of one
 //    row: the epilogue writes 8/16-byte vectors instead of 2-byte scalars.
 //
+// Scaling (SCALE):
+//  0  per-tensor fp32 scalars, applied in the epilogue (neutral E8M0
+//     scales in the MFMA);
+//  1  per-(row, K-block) power-of-two exponents (int8, [K/bs, rows], the
+//     reference's block format).  An MFMA lane holds 32 consecutive K
+//     values of one row, which lie in a single block for bs >= 32, so the
+//     exponent goes straight into the MFMA's E8M0 scale operand (bias 127)
+//     and the hardware applies it: no per-block partial sums or rescaling.
+//     The MFMA reads its scale from byte 0 of the operand VGPR whatever the
+//     opsel field says, so each sub-step has its own scale register.
+//     The exponent -128 (the
+//     reference's "zero W_lo block" sentinel, whose codes are all zero)
+//     becomes the E8M0 code 0 (2^-127).
+//
 // The DMA is issued from inline assembly: the compiler's wait-count pass
 // does not know these writes do not alias the LDS reads of the other
 // buffer and would otherwise drain all loads before every LDS read.  Wait
 // counts for the DMA are therefore explicit (s_waitcnt before the barrier).
 //
-// Stage layout (512 rows of 128 bytes): rows 0-255 activation rows m0..,
-// rows 256-383 slot-0 weight rows, rows 384-511 slot-1 weight rows.  The
-// eight 16-byte chunks of a row are permuted by swz(row) = (row >> 1) & 7,
-// which makes the MFMA operand reads (32 consecutive rows, same chunk)
-// bank-conflict free on the 64-bank (256 B/clk) LDS.
+// Stage layout (BM + 2*BN rows of 128 bytes): activation rows, then slot-0
+// weight rows, then slot-1 weight rows.  The eight 16-byte chunks of a row
+// are permuted by swz(row) = (row >> 1) & 7, which makes the MFMA operand
+// reads (32 consecutive rows, same chunk) bank-conflict free on the
+// 64-bank (256 B/clk) LDS.
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 #define TCFP_LDS __attribute__((address_space(3)))
 
 constexpr int kSK = 128;                 // K columns per stage
 constexpr int kRowB = kSK;               // bytes per stage row
-constexpr int kStageBytes = 512 * kRowB; // 64 KiB
 constexpr uint32_t kOob = 0x80000000u;   // beyond every descriptor's range
 
 TCFP_DEV int swz(int row) { return (row >> 1) & 7; }
@@ -317,36 +339,61 @@ TCFP_DEV void interleave_mfma_lds() {
   }
 }
 
-// NW = 4: one wave per SIMD, 2 x 2 wave grid, 128 x 64 (x2 slots) per wave.
-// NW = 8: two waves per SIMD, 4 x 2 wave grid, 64 x 64 (x2 slots) per wave;
-//         half the accumulators per wave, so two waves fit one SIMD and the
-//         MFMA pipe keeps issuing while the other wave waits.
-template <int AF, int BF, bool SPLIT, typename OutT, int NW>
-__global__ __launch_bounds__(NW * 64, 1) void gemm_nt_dma_kernel(
-    const uint8_t* __restrict__ A, const uint8_t* __restrict__ B0, const uint8_t* __restrict__ B1,
-    int M, int N, int K, int64_t lda, int64_t ldb, const float* __restrict__ s_a,
-    const float* __restrict__ s_0, const float* __restrict__ s_1, const float* __restrict__ bias,
-    OutT* __restrict__ out, int64_t ldo, int tiles_m, int tiles_n) {
-  constexpr int WM = NW / 2;        // wave rows
-  constexpr int TMW = kBM / WM;     // activation rows per wave (128 or 64)
-  constexpr int MB = TMW / 32;      // 32-row m-blocks per wave (4 or 2)
-  constexpr int RPW = 512 / NW;     // stage rows DMA'd by each wave (128 or 64)
-  constexpr int DI = RPW / 8;       // 1 KiB DMA instructions per wave and stage
-  __shared__ __align__(16) uint8_t lds[2 * kStageBytes];
+// E8M0 code of a block exponent (bias 127; -128 and anything below -127
+// map to code 0 = 2^-127).
+TCFP_DEV uint32_t e8m0_of(int e) { return e < -127 ? 0u : uint32_t(e + 127); }
 
-  // ---- tile mapping (XCD-aware, grouped; as in gemm_nt_kernel) ----
-  const int T = tiles_m * tiles_n;
+struct GemmArgs {
+  const uint8_t* A;
+  const uint8_t* B0;
+  const uint8_t* B1;
+  int M, N, K;
+  int64_t lda, ldb;
+  const float* s_a;  // per-tensor scalars (SCALE 0)
+  const float* s_0;
+  const float* s_1;
+  const int8_t* e_a;  // block exponents (SCALE 1): [K/bs, M], [K/bs, N], [K/bs, N]
+  const int8_t* e_0;
+  const int8_t* e_1;
+  int bs_shift;  // log2(block size)
+  const float* bias;
+  void* out;
+  int64_t ldo;
+  int tiles_m, tiles_n;
+};
+
+template <int AF, int BF, bool SPLIT, typename OutT, int NW, int BM, int BN, int SCALE>
+__global__ __launch_bounds__(NW * 64, (NW == 4 ? 2 : 1)) void gemm_nt_dma_kernel(GemmArgs g) {
+  constexpr int WM = NW / 2;        // wave rows
+  constexpr int TMW = BM / WM;      // activation rows per wave
+  constexpr int MB = TMW / 32;      // 32-row m-blocks per wave
+  constexpr int TNW = BN / 2;       // weight rows per wave and slot
+  constexpr int NB = TNW / 32;      // 32-row n-blocks per wave and slot
+  constexpr int NF = 2 * NB;        // weight fragments per sub-step
+  constexpr int SROWS = BM + 2 * BN;
+  constexpr int STAGE = SROWS * kRowB;
+  constexpr int RPW = SROWS / NW;   // stage rows DMA'd by each wave
+  constexpr int DI = RPW / 8;       // 1 KiB DMA instructions per wave and stage
+  static_assert(RPW % 16 == 0 && BM % RPW == 0 && BN % RPW == 0, "DMA rows must tile regions");
+  static_assert(MB >= 1 && NB >= 1, "tile too small for the wave grid");
+  __shared__ __align__(16) uint8_t lds[2 * STAGE];
+
+  const int M = g.M, N = g.N, K = g.K;
+  OutT* __restrict__ out = static_cast<OutT*>(g.out);
+
+  // ---- tile mapping (XCD-aware, grouped) ----
+  const int T = g.tiles_m * g.tiles_n;
   int l = blockIdx.x;
   if ((T & 7) == 0) l = (l & 7) * (T >> 3) + (l >> 3);
   constexpr int G = 8;
-  const int per_group = G * tiles_n;
+  const int per_group = G * g.tiles_n;
   const int first_m = (l / per_group) * G;
-  const int gm = min(tiles_m - first_m, G);
+  const int gm = min(g.tiles_m - first_m, G);
   const int tm = first_m + (l % per_group) % gm;
   const int tn = (l % per_group) / gm;
-  const int m0 = tm * kBM;
-  const int n0 = SPLIT ? tn * (2 * kBN) : tn * kBN;
-  const int n1 = SPLIT ? n0 + kBN : n0;
+  const int m0 = tm * BM;
+  const int n0 = SPLIT ? tn * (2 * BN) : tn * BN;
+  const int n1 = SPLIT ? n0 + BN : n0;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -354,23 +401,25 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_nt_dma_kernel(
   const int wm = wave >> 1, wn = wave & 1;
   const int lr = lane & 31, lg = lane >> 5;
 
-  // ---- this wave's DMA source: stage rows [wave*RPW, +RPW) lie in one of
-  // the activation (0-255), slot-0 (256-383) or slot-1 (384-511) regions
+  // ---- this wave's DMA source: its RPW stage rows lie in the activation,
+  // slot-0 or slot-1 region
   const int srow0 = wave * RPW;
   const uint8_t* src;
   int64_t ld;
   int rows_left, row_base;
-  if (srow0 < 256) {
-    src = A + int64_t(m0) * lda; ld = lda; rows_left = min(M - m0, kBM); row_base = srow0;
-  } else if (srow0 < 384) {
-    src = B0 + int64_t(n0) * ldb; ld = ldb; rows_left = min(N - n0, kBN); row_base = srow0 - 256;
+  if (srow0 < BM) {
+    src = g.A + int64_t(m0) * g.lda; ld = g.lda; rows_left = min(M - m0, BM); row_base = srow0;
+  } else if (srow0 < BM + BN) {
+    src = g.B0 + int64_t(n0) * g.ldb; ld = g.ldb; rows_left = min(N - n0, BN);
+    row_base = srow0 - BM;
   } else {
-    src = B1 + int64_t(n1) * ldb; ld = ldb; rows_left = min(N - n1, kBN); row_base = srow0 - 384;
+    src = g.B1 + int64_t(n1) * g.ldb; ld = g.ldb; rows_left = min(N - n1, BN);
+    row_base = srow0 - BM - BN;
   }
   const uint32_t nrec = rows_left > 0 ? uint32_t(int64_t(rows_left - 1) * ld + K) : 0u;
   const v4i rsrc = make_rsrc(src, nrec);
   // Instruction i fills stage rows srow0 + i*8 .. +8 (1 KiB); lane writes row
-  // +lane/8 at physical chunk lane%8.  srow0 is a multiple of 64, so the
+  // +lane/8 at physical chunk lane%8.  srow0 is a multiple of 16, so the
   // logical chunk depends on i only through i's low bit.
   const int chunk0 = (lane & 7) ^ swz(lane >> 3);        // even i
   const int chunk1 = (lane & 7) ^ swz(8 + (lane >> 3));  // odd i
@@ -388,10 +437,9 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_nt_dma_kernel(
 
   // DMA of stage t (K columns t*128 ..) into buffer t & 1.  Stages past the
   // end are issued as all-out-of-range loads (zeros into a buffer nobody
-  // reads again): the issue stays branch-free, so the loop body is a single
-  // basic block and the compiler cannot sink MFMAs across the barrier.
+  // reads again), so the issue stays branch-free.
   auto issue = [&](int t) {
-    const uint32_t dst = lds_base + uint32_t(t & 1) * kStageBytes;
+    const uint32_t dst = lds_base + uint32_t(t & 1) * STAGE;
     const bool live = t < nt;
     const uint32_t soff = uint32_t(live ? t : 0) * kSK;
     const bool last = t == nt - 1;
@@ -402,48 +450,103 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_nt_dma_kernel(
     }
   };
 
-  // ---- per-lane LDS read offsets: sub-step h, 16-byte half q of a fragment
+  // ---- per-lane LDS read offsets: sub-step h, 16-byte half q of a fragment.
+  // The MFMA takes byte j of lane l as K index 16*(l/32) + 32*(j/16) + j%16
+  // of its 64-wide step, and the E8M0 scale of lane l covers the 32-wide K
+  // block l/32 -- i.e. bytes 16*(l/32) .. +15 of BOTH lane halves.  So lane
+  // half g loads 16-byte chunks g and 2 + g of the sub-step: its scale then
+  // covers exactly the 32 K columns 32*g .. 32*g + 31 that one block of the
+  // exponent arrays describes.  (For unscaled products any K order works.)
   int ro[2][2];
 #pragma unroll
   for (int h = 0; h < 2; ++h)
 #pragma unroll
-    for (int q = 0; q < 2; ++q) ro[h][q] = lr * kRowB + (((4 * h + 2 * lg + q) ^ swz(lr)) << 4);
+    for (int q = 0; q < 2; ++q) ro[h][q] = lr * kRowB + (((4 * h + lg + 2 * q) ^ swz(lr)) << 4);
 
-  v16f acc[2][2][MB];  // [slot][n-block][m-block]
+  // ---- block exponents (SCALE 1).  Fragment q's weight row is
+  // rw + dq(q) and fragment i's activation row is ra + 32*i; offsets into
+  // the [K/bs, rows] exponent arrays are 32-bit from uniform bases.
+  const uint32_t rw = uint32_t(n0 + wn * TNW + lr);
+  const uint32_t ra = uint32_t(m0 + wm * TMW + lr);
+  auto dq = [&](int q) { return uint32_t(((q / NB) ? n1 - n0 : 0) + (q % NB) * 32); };
+  // Raw exponents of stage t, one register per (fragment, sub-step); rows
+  // or K past the matrix read as 0 (2^0, multiplying zero operands).
+  auto load_raw = [&](int* raw, int t) {
+    if constexpr (SCALE == 1) {
 #pragma unroll
-  for (int s = 0; s < 2; ++s)
+      for (int h = 0; h < 2; ++h) {
+        const int k = t * kSK + h * 64 + lg * 32;
+        const bool kin = k < K;
+        const uint32_t kb = uint32_t(k >> g.bs_shift);
+        const uint32_t ow = kb * uint32_t(N) + rw, oa = kb * uint32_t(M) + ra;
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+        for (int q = 0; q < NF; ++q) {
+          const int8_t* e = (!SPLIT && (q / NB)) ? g.e_1 : g.e_0;
+          raw[2 * q + h] = (kin && rw + dq(q) < uint32_t(N)) ? int(e[ow + dq(q)]) : 0;
+        }
+#pragma unroll
+        for (int i = 0; i < MB; ++i)
+          raw[2 * (NF + i) + h] =
+              (kin && ra + 32 * i < uint32_t(M)) ? int(g.e_a[oa + 32 * i]) : 0;
+      }
+    }
+  };
+  // E8M0 operand per (fragment, sub-step).  The scale always comes from
+  // byte 0 of the VGPR (the MFMA's opsel does not select other bytes), so
+  // each sub-step gets its own register.
+  auto pack = [&](uint32_t* sc, const int* raw) {
+    if constexpr (SCALE == 1) {
+#pragma unroll
+      for (int f = 0; f < 2 * (NF + MB); ++f) sc[f] = e8m0_of(raw[f]);
+    }
+  };
+
+  // [slot][n-block][m-block].  Block-scaled dual GEMMs keep one set: the
+  // MFMA applies each slot's scales, so W_hi and W_lo products add directly.
+  constexpr int NACC = (SCALE == 1 && !SPLIT) ? 1 : 2;
+  v16f acc[NACC][NB][MB];
+#pragma unroll
+  for (int s = 0; s < NACC; ++s)
+#pragma unroll
+    for (int j = 0; j < NB; ++j)
 #pragma unroll
       for (int i = 0; i < MB; ++i)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[s][j][i][r] = 0.0f;
 
-  // Fragments of sub-step h of stage t: [0..3] weights (slot, n-block),
-  // [4..4+MB) activations (m-block).
+  // Fragments of sub-step h of stage t: [0, NF) weights (slot, n-block),
+  // [NF, NF + MB) activations (m-block).
   auto read_frags = [&](v8i* f, int t, int h) {
-    const uint8_t* st = lds + (t & 1) * kStageBytes;
+    const uint8_t* st = lds + (t & 1) * STAGE;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int rb = (256 + (q >> 1) * 128 + wn * 64 + (q & 1) * 32) * kRowB;
+    for (int q = 0; q < NF; ++q) {
+      const int rb = (BM + (q / NB) * BN + wn * TNW + (q % NB) * 32) * kRowB;
       f[q] = make_frag(lds_read16(st, rb + ro[h][0]), lds_read16(st, rb + ro[h][1]));
     }
 #pragma unroll
     for (int i = 0; i < MB; ++i) {
       const int rb = (wm * TMW + i * 32) * kRowB;
-      f[4 + i] = make_frag(lds_read16(st, rb + ro[h][0]), lds_read16(st, rb + ro[h][1]));
+      f[NF + i] = make_frag(lds_read16(st, rb + ro[h][0]), lds_read16(st, rb + ro[h][1]));
     }
   };
-  auto mfmas = [&](const v8i* f) {
+  // One sub-step (h) of MFMAs; `sc` holds the stage's E8M0 scales.
+  auto mfmas = [&](const v8i* f, const uint32_t* sc, int h) {
 #pragma unroll
     for (int i = 0; i < MB; ++i)
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
-        acc[q >> 1][q & 1][i] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-            f[q], f[4 + i], acc[q >> 1][q & 1][i], BF, AF, 0, 127, 0, 127);
+      for (int q = 0; q < NF; ++q) {
+        v16f& c = acc[(q / NB) % NACC][q % NB][i];
+        if constexpr (SCALE == 1) {
+          c = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+              f[q], f[NF + i], c, BF, AF, 0, int(sc[2 * q + h]), 0, int(sc[2 * (NF + i) + h]));
+        } else {
+          c = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f[q], f[NF + i], c, BF, AF, 0, 127,
+                                                               0, 127);
+        }
+      }
   };
-  // 4*MB MFMAs and 2*(4+MB) LDS reads per sub-step: spread the reads evenly
-  auto interleave = [&]() { interleave_mfma_lds<4 * MB, 2 * (4 + MB), 0>(); };
+  // NF*MB MFMAs and 2*(NF+MB) LDS reads per sub-step: spread the reads evenly
+  auto interleave = [&]() { interleave_mfma_lds<NF * MB, 2 * (NF + MB), 0>(); };
   // All DMA issued so far has landed and every wave's LDS reads are done
   // (gfx9 s_waitcnt: vmcnt bits [3:0] and [15:14], expcnt [6:4], lgkmcnt [11:8]).
   // sched_barrier(0) keeps the scheduler from moving MFMAs across it: MFMAs
@@ -457,21 +560,29 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_nt_dma_kernel(
     __builtin_amdgcn_sched_barrier(0);
   };
 
-  v8i f0[4 + MB], f1[4 + MB];
+  v8i f0[NF + MB], f1[NF + MB];
+  uint32_t sc[2 * (NF + MB)];  // E8M0 scales of the current stage
+  int raw[2 * (NF + MB)];   // exponents of the next stage, in flight
   if (nt > 0) {
+    load_raw(raw, 0);
     issue(0);
     if (nt > 1) issue(1);
-    // wait for stage 0 only: stage 1's DI loads may stay in flight
+    // wait for stage 0 only: stage 1's DI loads may stay in flight (the
+    // exponent loads were issued before both and are complete too)
     if (nt > 1) __builtin_amdgcn_s_waitcnt((DI & 15) | (7 << 4) | ((DI >> 4) << 14));
     else __builtin_amdgcn_s_waitcnt(0x0070);
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
+    pack(sc, raw);
     read_frags(f0, 0, 0);
   }
   for (int t = 0; t < nt; ++t) {
+    // exponents of stage t + 1: the vmcnt(0) of this stage's barrier covers them
+    load_raw(raw, t + 1);
+    __builtin_amdgcn_sched_barrier(0);
     // sub-step 0 of stage t; fragments of sub-step 1 stream in
     read_frags(f1, t, 1);
-    mfmas(f0);
+    mfmas(f0, sc, 0);
     interleave();
     // stage t + 1 landed, every wave has its stage-t fragments: refill t's buffer
     sync_all();
@@ -480,48 +591,54 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_nt_dma_kernel(
     // sub-step 1 of stage t; fragments of stage t + 1 sub-step 0 stream in
     // (after the last stage they read a stale buffer and are never used)
     read_frags(f0, t + 1, 0);
-    mfmas(f1);
+    mfmas(f1, sc, 1);
     interleave();
+    pack(sc, raw);
   }
 
   // ---- epilogue -----------------------------------------------------------
   // A lane holds rows m, columns n..n+3 of each 32x32 block: storing that
   // directly writes 16 bytes into each of 32 rows per instruction.  Instead
-  // each wave stages its 64-column tile (per slot) through its own LDS
-  // region and stores whole rows: 8 (bf16) or 4 (fp32) rows of 128/256
-  // bytes per instruction, i.e. full cache lines.
+  // each wave stages its TNW-column tile (per slot) through its own LDS
+  // region and stores whole row segments of 16-byte chunks.
   constexpr int EB = int(sizeof(OutT));      // output element bytes
-  constexpr int RB = 64 * EB;                // bytes of one staged tile row
-  constexpr int CPR = RB / 16;               // 16-byte chunks per row (8 / 16)
+  constexpr int RB = TNW * EB;               // bytes of one staged tile row
+  constexpr int CPR = RB / 16;               // 16-byte chunks per row
   constexpr int RPI = 64 / CPR;              // rows per store instruction
+  static_assert(NW * TMW * RB <= 2 * STAGE, "epilogue staging must fit the operand buffers");
   uint8_t* eps = lds + wave * (TMW * RB);    // this wave's staging region
-  const float sa = *s_a;
-  const float c0s = sa * *s_0;
-  const float c1s = SPLIT ? c0s : sa * *s_1;
-  const bool vec = (ldo % (16 / EB)) == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0;
+  float c0s = 1.0f, c1s = 1.0f;
+  if constexpr (SCALE == 0) {
+    const float sa = *g.s_a;
+    c0s = sa * *g.s_0;
+    c1s = SPLIT ? c0s : sa * *g.s_1;
+  }
+  const bool vec = (g.ldo % (16 / EB)) == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0;
   // every wave is done with the operand buffers before they are reused
   __builtin_amdgcn_s_waitcnt(0x0070);
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
 #pragma unroll
   for (int s = 0; s < (SPLIT ? 2 : 1); ++s) {
-    const int nb = (s ? n1 : n0) + wn * 64;  // first output column of this tile
+    const int nb = (s ? n1 : n0) + wn * TNW;  // first output column of this tile
 #pragma unroll
     for (int i = 0; i < MB; ++i)
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
+      for (int j = 0; j < NB; ++j)
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int row = i * 32 + lr, col = j * 32 + g * 8 + lg * 4;
+        for (int gq = 0; gq < 4; ++gq) {
+          const int row = i * 32 + lr, col = j * 32 + gq * 8 + lg * 4;
           float v[4];
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
-            const int r = g * 4 + q;
-            v[q] = SPLIT ? acc[s][j][i][r] * c0s : acc[0][j][i][r] * c0s + acc[1][j][i][r] * c1s;
+            const int r = gq * 4 + q;
+            if constexpr (SPLIT) v[q] = acc[s][j][i][r] * c0s;
+            else if constexpr (NACC == 1) v[q] = acc[0][j][i][r];
+            else v[q] = acc[0][j][i][r] * c0s + acc[NACC - 1][j][i][r] * c1s;
           }
-          if (bias) {
+          if (g.bias) {
 #pragma unroll
-            for (int q = 0; q < 4; ++q) v[q] += nb + col + q < N ? bias[nb + col + q] : 0.0f;
+            for (int q = 0; q < 4; ++q) v[q] += nb + col + q < N ? g.bias[nb + col + q] : 0.0f;
           }
           // 16-byte chunk index within the row, XOR-permuted by row
           const int byte = col * EB;
@@ -537,7 +654,7 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_nt_dma_kernel(
       const int m = m0 + wm * TMW + row;
       const int n = nb + cl * (16 / EB);
       if (m < M) {
-        OutT* o = out + int64_t(m) * ldo + n;
+        OutT* o = out + int64_t(m) * g.ldo + n;
         if (vec && n + 16 / EB <= N) {
           *reinterpret_cast<uint4*>(o) = d;
         } else {
@@ -554,57 +671,103 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_nt_dma_kernel(
 
 // Largest byte span any DMA descriptor may cover (offsets are 32-bit and
 // the out-of-range sentinel must stay beyond every span).
-#ifndef TCFP_DMA_WAVES
-#define TCFP_DMA_WAVES 8
-#endif
-constexpr int kDmaWaves = TCFP_DMA_WAVES;
-
 constexpr int64_t kMaxSpan = (int64_t(1) << 31) - (int64_t(1) << 20);
 
-template <int AF, int BF, bool SPLIT, typename OutT>
-int launch_gemm(const uint8_t* a, int64_t lda, const uint8_t* b0, const uint8_t* b1, int64_t ldb,
-                int m, int n, int k, const float* s_a, const float* s_0, const float* s_1,
-                const float* bias, OutT* out, int64_t ldo, hipStream_t st) {
-  const int tiles_m = (m + kBM - 1) / kBM;
-  const int tn_w = SPLIT ? 2 * kBN : kBN;
-  const int tiles_n = (n + tn_w - 1) / tn_w;
-  const bool dma_ok = int64_t(kBM) * lda + k < kMaxSpan && int64_t(kBN) * ldb + k < kMaxSpan &&
-                      (bias == nullptr || (reinterpret_cast<uintptr_t>(bias) & 15) == 0);
-  if (dma_ok) {
-    gemm_nt_dma_kernel<AF, BF, SPLIT, OutT, kDmaWaves><<<tiles_m * tiles_n, kDmaWaves * 64, 0, st>>>(
-        a, b0, b1, m, n, k, lda, ldb, s_a, s_0, s_1, bias, out, ldo, tiles_m, tiles_n);
-    return hipGetLastError() == hipSuccess ? TCFP_OK : TCFP_ERR_HIP;
+// Tile policy: 0 = automatic, 1 = always 256 x 128, 2 = always 128 x 64.
+int g_tile_policy = 0;
+
+int num_cus() {
+  static int n = 0;
+  if (n == 0) {
+    int dev = 0, v = 0;
+    if (hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+        v > 0)
+      n = v;
+    else
+      n = 256;
   }
-  const int smem = 2 * Lds<kBK>::STAGE;
-  auto kern = gemm_nt_kernel<AF, BF, SPLIT, kBK, OutT>;
-  static bool attr_set = false;
-  if (!attr_set) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, smem) != hipSuccess)
-      return TCFP_ERR_HIP;
-    attr_set = true;
-  }
-  kern<<<tiles_m * tiles_n, kNT, smem, st>>>(a, b0, b1, m, n, k, lda, ldb, s_a, s_0, s_1, bias,
-                                             out, ldo, tiles_m, tiles_n);
-  return hipGetLastError() == hipSuccess ? TCFP_OK : TCFP_ERR_HIP;
+  return n;
 }
 
-template <bool SPLIT, typename OutT>
-int dispatch_fmt(int a_fmt, int b_fmt, const uint8_t* a, int64_t lda, const uint8_t* b0,
-                 const uint8_t* b1, int64_t ldb, int m, int n, int k, const float* s_a,
-                 const float* s_0, const float* s_1, const float* bias, OutT* out, int64_t ldo,
-                 hipStream_t st) {
-#define TCFP_G(AF, BF) \
-  launch_gemm<AF, BF, SPLIT, OutT>(a, lda, b0, b1, ldb, m, n, k, s_a, s_0, s_1, bias, out, ldo, st)
-  if (a_fmt == TCFP_FP8_E4M3 && b_fmt == TCFP_FP8_E4M3) return TCFP_G(0, 0);
-  if (a_fmt == TCFP_FP8_E5M2 && b_fmt == TCFP_FP8_E4M3) return TCFP_G(1, 0);
-  if (a_fmt == TCFP_FP8_E4M3 && b_fmt == TCFP_FP8_E5M2) return TCFP_G(0, 1);
-  if (a_fmt == TCFP_FP8_E5M2 && b_fmt == TCFP_FP8_E5M2) return TCFP_G(1, 1);
-#undef TCFP_G
+template <int AF, int BF, bool SPLIT, typename OutT, int SCALE>
+int launch_gemm(GemmArgs ga, hipStream_t st) {
+  const int m = ga.M, n = ga.N, k = ga.K;
+  // large tile unless it would leave CUs idle
+  const int big_tiles = ((m + 255) / 256) * ((n + (SPLIT ? 255 : 127)) / (SPLIT ? 256 : 128));
+  // (block-scaled single GEMMs keep two accumulator sets, which only the
+  // small tile fits in registers)
+  const bool small = (SCALE == 1 && SPLIT) || g_tile_policy == 2 ||
+                     (g_tile_policy == 0 && big_tiles < num_cus());
+  const int BMv = small ? 128 : 256, BNv = small ? 64 : 128;
+  ga.tiles_m = (m + BMv - 1) / BMv;
+  ga.tiles_n = (n + (SPLIT ? 2 * BNv : BNv) - 1) / (SPLIT ? 2 * BNv : BNv);
+  const bool dma_ok = int64_t(BMv) * ga.lda + k < kMaxSpan && int64_t(BNv) * ga.ldb + k < kMaxSpan &&
+                      (ga.bias == nullptr || (reinterpret_cast<uintptr_t>(ga.bias) & 15) == 0);
+  if (dma_ok) {
+    const unsigned grid = unsigned(ga.tiles_m) * unsigned(ga.tiles_n);
+    if (small)
+      gemm_nt_dma_kernel<AF, BF, SPLIT, OutT, 4, 128, 64, SCALE><<<grid, 256, 0, st>>>(ga);
+    else if constexpr (!(SCALE == 1 && SPLIT))
+      gemm_nt_dma_kernel<AF, BF, SPLIT, OutT, 8, 256, 128, SCALE><<<grid, 512, 0, st>>>(ga);
+    return hipGetLastError() == hipSuccess ? TCFP_OK : TCFP_ERR_HIP;
+  }
+  if constexpr (SCALE != 0) {
+    return TCFP_ERR_SHAPE;  // block-scaled GEMMs need spans the DMA path covers
+  } else {
+    const int tiles_m = (m + kBM - 1) / kBM;
+    const int tn_w = SPLIT ? 2 * kBN : kBN;
+    const int tiles_n = (n + tn_w - 1) / tn_w;
+    const int smem = 2 * Lds<kBK>::STAGE;
+    auto kern = gemm_nt_kernel<AF, BF, SPLIT, kBK, OutT>;
+    static bool attr_set = false;
+    if (!attr_set) {
+      if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, smem) != hipSuccess)
+        return TCFP_ERR_HIP;
+      attr_set = true;
+    }
+    kern<<<tiles_m * tiles_n, kNT, smem, st>>>(ga.A, ga.B0, ga.B1, m, n, k, ga.lda, ga.ldb,
+                                               ga.s_a, ga.s_0, ga.s_1, ga.bias,
+                                               static_cast<OutT*>(ga.out), ga.ldo, tiles_m,
+                                               tiles_n);
+    return hipGetLastError() == hipSuccess ? TCFP_OK : TCFP_ERR_HIP;
+  }
+}
+
+template <bool SPLIT, typename OutT, int SCALE>
+int dispatch_fmt(int a_fmt, int b_fmt, const GemmArgs& ga, hipStream_t st) {
+  if (a_fmt == TCFP_FP8_E4M3 && b_fmt == TCFP_FP8_E4M3) return launch_gemm<0, 0, SPLIT, OutT, SCALE>(ga, st);
+  if (a_fmt == TCFP_FP8_E5M2 && b_fmt == TCFP_FP8_E4M3) return launch_gemm<1, 0, SPLIT, OutT, SCALE>(ga, st);
+  if (a_fmt == TCFP_FP8_E4M3 && b_fmt == TCFP_FP8_E5M2) return launch_gemm<0, 1, SPLIT, OutT, SCALE>(ga, st);
+  if (a_fmt == TCFP_FP8_E5M2 && b_fmt == TCFP_FP8_E5M2) return launch_gemm<1, 1, SPLIT, OutT, SCALE>(ga, st);
   return TCFP_ERR_DTYPE;
 }
 
+template <int SCALE>
+int dispatch_all(int a_fmt, int b_fmt, bool dual, int out_dtype, const GemmArgs& ga,
+                 hipStream_t st) {
+  if (dual) {
+    if (out_dtype == TCFP_DTYPE_F32) return dispatch_fmt<false, float, SCALE>(a_fmt, b_fmt, ga, st);
+    return dispatch_fmt<false, uint16_t, SCALE>(a_fmt, b_fmt, ga, st);
+  }
+  if (out_dtype == TCFP_DTYPE_F32) return dispatch_fmt<true, float, SCALE>(a_fmt, b_fmt, ga, st);
+  return dispatch_fmt<true, uint16_t, SCALE>(a_fmt, b_fmt, ga, st);
+}
+
 bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int check_common(int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldb, int64_t ldo,
+                 const void* a, const void* b_hi, const void* b_lo, int out_dtype) {
+  if (m < 0 || n < 0 || k < 0 || m > INT32_MAX || n > INT32_MAX || k > INT32_MAX)
+    return TCFP_ERR_SHAPE;
+  if (k % 16 != 0) return TCFP_ERR_SHAPE;
+  if (lda < k || ldb < k || ldo < n) return TCFP_ERR_SHAPE;
+  if (lda % 16 != 0 || ldb % 16 != 0) return TCFP_ERR_ALIGN;
+  if (!al16(a) || !al16(b_hi) || (b_lo && !al16(b_lo))) return TCFP_ERR_ALIGN;
+  if (out_dtype != TCFP_DTYPE_F32 && out_dtype != TCFP_DTYPE_BF16) return TCFP_ERR_DTYPE;
+  return TCFP_OK;
+}
 
 }  // namespace
 
@@ -613,27 +776,43 @@ extern "C" int tcfp_dual_gemm(const uint8_t* a, int a_fmt, int64_t lda, const ui
                               int64_t k, const float* s_a, const float* s_hi, const float* s_lo,
                               const float* bias, void* out, int out_dtype, int64_t ldo,
                               void* stream) {
-  if (m < 0 || n < 0 || k < 0 || m > INT32_MAX || n > INT32_MAX || k > INT32_MAX)
-    return TCFP_ERR_SHAPE;
-  if (k % 16 != 0) return TCFP_ERR_SHAPE;
-  if (lda < k || ldb < k || ldo < n) return TCFP_ERR_SHAPE;
-  if (lda % 16 != 0 || ldb % 16 != 0) return TCFP_ERR_ALIGN;
-  if (!al16(a) || !al16(b_hi) || (b_lo && !al16(b_lo))) return TCFP_ERR_ALIGN;
+  const int rc = check_common(m, n, k, lda, ldb, ldo, a, b_hi, b_lo, out_dtype);
+  if (rc != TCFP_OK) return rc;
   if (!s_a || !s_hi || (b_lo && !s_lo)) return TCFP_ERR_SHAPE;
-  if (out_dtype != TCFP_DTYPE_F32 && out_dtype != TCFP_DTYPE_BF16) return TCFP_ERR_DTYPE;
   if (m == 0 || n == 0) return TCFP_OK;
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  const int M = int(m), N = int(n), K = int(k);
-  if (b_lo) {
-    if (out_dtype == TCFP_DTYPE_F32)
-      return dispatch_fmt<false, float>(a_fmt, b_fmt, a, lda, b_hi, b_lo, ldb, M, N, K, s_a, s_hi,
-                                        s_lo, bias, static_cast<float*>(out), ldo, st);
-    return dispatch_fmt<false, uint16_t>(a_fmt, b_fmt, a, lda, b_hi, b_lo, ldb, M, N, K, s_a, s_hi,
-                                         s_lo, bias, static_cast<uint16_t*>(out), ldo, st);
-  }
-  if (out_dtype == TCFP_DTYPE_F32)
-    return dispatch_fmt<true, float>(a_fmt, b_fmt, a, lda, b_hi, b_hi, ldb, M, N, K, s_a, s_hi,
-                                     s_hi, bias, static_cast<float*>(out), ldo, st);
-  return dispatch_fmt<true, uint16_t>(a_fmt, b_fmt, a, lda, b_hi, b_hi, ldb, M, N, K, s_a, s_hi,
-                                      s_hi, bias, static_cast<uint16_t*>(out), ldo, st);
+  GemmArgs ga{};
+  ga.A = a; ga.B0 = b_hi; ga.B1 = b_lo ? b_lo : b_hi;
+  ga.M = int(m); ga.N = int(n); ga.K = int(k); ga.lda = lda; ga.ldb = ldb;
+  ga.s_a = s_a; ga.s_0 = s_hi; ga.s_1 = b_lo ? s_lo : s_hi;
+  ga.bias = bias; ga.out = out; ga.ldo = ldo;
+  return dispatch_all<0>(a_fmt, b_fmt, b_lo != nullptr, out_dtype, ga,
+                         static_cast<hipStream_t>(stream));
+}
+
+extern "C" int tcfp_block_dual_gemm(const uint8_t* a, int a_fmt, int64_t lda, const int8_t* e_a,
+                                    const uint8_t* b_hi, const uint8_t* b_lo, int b_fmt,
+                                    int64_t ldb, const int8_t* e_hi, const int8_t* e_lo,
+                                    int64_t m, int64_t n, int64_t k, int block,
+                                    const float* bias, void* out, int out_dtype, int64_t ldo,
+                                    void* stream) {
+  const int rc = check_common(m, n, k, lda, ldb, ldo, a, b_hi, b_lo, out_dtype);
+  if (rc != TCFP_OK) return rc;
+  if (block != 32 && block != 64 && block != 128) return TCFP_ERR_SHAPE;
+  if (k % block != 0) return TCFP_ERR_SHAPE;
+  if (!e_a || !e_hi || (b_lo && !e_lo)) return TCFP_ERR_SHAPE;
+  if (m == 0 || n == 0) return TCFP_OK;
+  GemmArgs ga{};
+  ga.A = a; ga.B0 = b_hi; ga.B1 = b_lo ? b_lo : b_hi;
+  ga.M = int(m); ga.N = int(n); ga.K = int(k); ga.lda = lda; ga.ldb = ldb;
+  ga.e_a = e_a; ga.e_0 = e_hi; ga.e_1 = b_lo ? e_lo : e_hi;
+  ga.bs_shift = block == 32 ? 5 : (block == 64 ? 6 : 7);
+  ga.bias = bias; ga.out = out; ga.ldo = ldo;
+  return dispatch_all<1>(a_fmt, b_fmt, b_lo != nullptr, out_dtype, ga,
+                         static_cast<hipStream_t>(stream));
+}
+
+extern "C" int tcfp_gemm_set_tile_policy(int policy) {
+  if (policy < 0 || policy > 2) return TCFP_ERR_SHAPE;
+  g_tile_policy = policy;
+  return TCFP_OK;
 }

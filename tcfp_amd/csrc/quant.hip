@@ -8,19 +8,25 @@
 // HBM layout: inputs are read once per pass with 16-byte vector loads; each
 // thread owns whole 8-element vectors, so the in-place error-feedback update
 // of a vector is done by the thread that read it.
+#include <algorithm>
+
 #include "common.h"
 
 using namespace tcfp;
 
 namespace {
 
-// Per-stream reduction state.  Zero at rest: the last workgroup of each
-// reducing kernel consumes and re-zeroes the accumulator and the ticket.
-struct ReduceWs {
-  unsigned int amax_bits;  // max |x| as float bits (monotone for x >= 0)
-  unsigned int ticket;     // workgroups finished
-  unsigned int pad[2];
-  float scale[4];          // {scale_hi, inv_hi, scale_lo, inv_lo}
+// Per-tensor reductions.  Each workgroup of a reducing kernel stores its
+// partial max |x| (as float bits: monotone for non-negative floats, and any
+// NaN sorts above +inf, so torch.max's NaN propagation is kept) into its own
+// slot of a workspace array with a plain store.  The kernel that consumes the
+// scale re-reduces every slot in every workgroup (at most 4 KiB, served from
+// L2), so the two launches need nothing but stream order: no atomics, no
+// fences, no zero-at-rest requirement, and the result is deterministic.
+constexpr int kMaxParts = 1024;
+struct PartWs {
+  uint32_t a[kMaxParts];  // partial amax of the first reduction
+  uint32_t b[kMaxParts];  // partial amax of the residual (dual quantisation)
 };
 
 constexpr int kThreads = 256;
@@ -43,6 +49,16 @@ int num_cu() {
 inline int grid_for(int64_t work_items, int per_cu) {
   int64_t g = (work_items + kThreads - 1) / kThreads;
   int64_t cap = int64_t(num_cu()) * per_cu;
+  if (g > cap) g = cap;
+  if (g < 1) g = 1;
+  return int(g);
+}
+
+// Workgroups of a kernel that writes partials: about four 8-element vectors
+// per thread, never more than the workspace holds.
+inline int parts_for(int64_t nvec) {
+  int64_t g = (nvec + 4 * kThreads - 1) / (4 * kThreads);
+  const int64_t cap = std::min<int64_t>(kMaxParts, int64_t(num_cu()) * 4);
   if (g > cap) g = cap;
   if (g < 1) g = 1;
   return int(g);
@@ -87,6 +103,15 @@ TCFP_DEV uint2 encode8(const float v[8]) {
 }
 
 template <int FMT>
+TCFP_DEV uint32_t encode4(float a, float b, float c, float d) {
+#ifdef TCFP_SW_CVT
+  return sw4_fp8<FMT>(a, b, c, d);
+#else
+  return cvt4_fp8<FMT>(a, b, c, d);
+#endif
+}
+
+template <int FMT>
 TCFP_DEV uint32_t encode1(float v) {
 #ifdef TCFP_SW_CVT
   return f32_to_fp8<FMT>(v);
@@ -115,196 +140,308 @@ TCFP_DEV void scale_from_amax(float amax, bool bf16_rule, float fmax, float* sca
   *inv = __fdiv_rn(1.0f, *scale);
 }
 
-// Block-level uint max (256 threads), result valid in thread 0.
-TCFP_DEV uint32_t block_umax(uint32_t m) {
-  __shared__ uint32_t red[kThreads / 64];
+TCFP_DEV uint32_t absbits(float v) { return __float_as_uint(v) & 0x7FFFFFFFu; }
+TCFP_DEV uint32_t umax(uint32_t a, uint32_t b) { return a > b ? a : b; }
+
+// Workgroup-wide uint max (256 threads), returned to every thread.  `red`
+// is the caller's LDS scratch: one call per array between barriers.
+TCFP_DEV uint32_t block_umax_all(uint32_t m, uint32_t* red) {
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    uint32_t other = __shfl_xor(m, o, 64);
-    m = m > other ? m : other;
-  }
+  for (int o = 32; o > 0; o >>= 1) m = umax(m, uint32_t(__shfl_xor(int(m), o, 64)));
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
   __syncthreads();
-  if (threadIdx.x == 0) {
+  m = red[0];
 #pragma unroll
-    for (int i = 1; i < kThreads / 64; ++i) m = m > red[i] ? m : red[i];
-  }
+  for (int i = 1; i < kThreads / 64; ++i) m = umax(m, red[i]);
   return m;
 }
 
-// Folds this workgroup's max into ws; the last workgroup to arrive turns the
-// global max into (scale, inv) in ws->scale[slot*2 .. +1] (and the optional
-// outputs) and re-zeroes the accumulator and ticket.
-TCFP_DEV void reduce_and_finalize(uint32_t m, ReduceWs* ws, int slot, bool bf16_rule, float fmax,
-                                  float* scale_out, float* inv_out) {
-  m = block_umax(m);
-  if (threadIdx.x == 0) {
-    atomicMax(&ws->amax_bits, m);
-    __threadfence();
-    unsigned int t = atomicAdd(&ws->ticket, 1u);
-    if (t == gridDim.x - 1) {
-      __threadfence();
-      uint32_t bits = atomicMax(&ws->amax_bits, 0u);
-      float scale, inv;
-      scale_from_amax(__uint_as_float(bits), bf16_rule, fmax, &scale, &inv);
-      ws->scale[slot * 2] = scale;
-      ws->scale[slot * 2 + 1] = inv;
-      if (scale_out) *scale_out = scale;
-      if (inv_out) *inv_out = inv;
-      atomicExch(&ws->amax_bits, 0u);
-      atomicExch(&ws->ticket, 0u);
-    }
-  }
+// max over the partials p[0 .. g) written by the previous launch.
+TCFP_DEV float reduce_parts(const uint32_t* __restrict__ p, int g, uint32_t* red) {
+  uint32_t m = 0;
+  for (int i = threadIdx.x; i < g; i += kThreads) m = umax(m, p[i]);
+  return __uint_as_float(block_umax_all(m, red));
 }
 
-TCFP_DEV uint32_t absbits(float v) { return __float_as_uint(v) & 0x7FFFFFFFu; }
-TCFP_DEV uint32_t umax(uint32_t a, uint32_t b) { return a > b ? a : b; }
+// The scale a per-tensor consumer kernel works with: the explicit one, or
+// the amax rule over the partials.  Workgroup 0 publishes (scale, inv).
+TCFP_DEV float consumer_scale(const float* scale_in, const uint32_t* part, int g, bool bf16_rule,
+                              float fmax, float* scale_out, float* inv_out, uint32_t* red) {
+  float s, inv;
+  if (scale_in) {
+    s = *scale_in;
+    inv = __fdiv_rn(1.0f, s);
+  } else {
+    scale_from_amax(reduce_parts(part, g, red), bf16_rule, fmax, &s, &inv);
+  }
+  if (blockIdx.x == 0 && threadIdx.x == 0) {
+    if (scale_out) *scale_out = s;
+    if (inv_out) *inv_out = inv;
+  }
+  return s;
+}
+
+// Eight elements of x (+ ef) starting at element 8*i.
+template <typename InT, bool HAS_EF>
+TCFP_DEV void load_w8(const InT* __restrict__ x, const float* __restrict__ ef, int64_t i,
+                      float W[8], float v[8]) {
+  load8(x + i * 8, W);
+  if constexpr (HAS_EF) {
+    float e[8];
+    load8(ef + i * 8, e);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = W[j] + e[j];
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = W[j];
+  }
+}
 
 // ===========================================================================
 // Per-tensor quantisation
 // ===========================================================================
 
-// max |x (+ ef)| -> scale / inv in ws slot.
+// Partial max |x (+ ef)| of this workgroup's share -> part[blockIdx.x].
+// Four vectors are loaded before any is reduced, so each thread keeps 64 or
+// 128 bytes in flight.
 template <typename InT, bool HAS_EF>
-__global__ __launch_bounds__(kThreads) void amax_kernel(const InT* __restrict__ x,
-                                                        const float* __restrict__ ef, int64_t n,
-                                                        ReduceWs* ws, int slot, int bf16_rule,
-                                                        float fmax, float* scale_out,
-                                                        float* inv_out) {
+__global__ __launch_bounds__(kThreads) void amax_part_kernel(const InT* __restrict__ x,
+                                                             const float* __restrict__ ef,
+                                                             int64_t n, uint32_t* __restrict__ part) {
+  __shared__ uint32_t red[kThreads / 64];
   uint32_t m = 0;
   const int64_t nvec = n >> 3;
   const int64_t stride = int64_t(gridDim.x) * kThreads;
-  for (int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x; i < nvec; i += stride) {
-    float v[8];
-    load8(x + i * 8, v);
-    if constexpr (HAS_EF) {
-      float e[8];
-      load8(ef + i * 8, e);
+  int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+  for (; i + 3 * stride < nvec; i += 4 * stride) {
+    float W[4][8], v[4][8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) v[j] = v[j] + e[j];
-    }
+    for (int u = 0; u < 4; ++u) load_w8<InT, HAS_EF>(x, ef, i + u * stride, W[u], v[u]);
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) m = umax(m, absbits(v[u][j]));
+  }
+  for (; i < nvec; i += stride) {
+    float W[8], v[8];
+    load_w8<InT, HAS_EF>(x, ef, i, W, v);
 #pragma unroll
     for (int j = 0; j < 8; ++j) m = umax(m, absbits(v[j]));
   }
-  for (int64_t i = nvec * 8 + int64_t(blockIdx.x) * kThreads + threadIdx.x; i < n; i += stride) {
-    float v = load1(x + i);
-    if constexpr (HAS_EF) v = v + ef[i];
+  for (int64_t t = nvec * 8 + int64_t(blockIdx.x) * kThreads + threadIdx.x; t < n; t += stride) {
+    float v = load1(x + t);
+    if constexpr (HAS_EF) v = v + ef[t];
     m = umax(m, absbits(v));
   }
-  reduce_and_finalize(m, ws, slot, bf16_rule != 0, fmax, scale_out, inv_out);
+  m = block_umax_all(m, red);
+  if (threadIdx.x == 0) part[blockIdx.x] = m;
 }
 
-// q = RNE(clamp(x * scale)), flat.
+// q = RNE(clamp(x * scale)), flat, two vectors in flight per thread.
 template <typename InT, int FMT>
-__global__ __launch_bounds__(kThreads) void quant_flat_kernel(const InT* __restrict__ x, int64_t n,
-                                                              const float* __restrict__ scale_p,
-                                                              uint8_t* __restrict__ q) {
-  const float s = *scale_p;
+__global__ __launch_bounds__(kThreads) void quant_flat_kernel(
+    const InT* __restrict__ x, int64_t n, const uint32_t* __restrict__ part, int g, int bf16_rule,
+    const float* __restrict__ scale_in, uint8_t* __restrict__ q, float* scale_out, float* inv_out) {
+  __shared__ uint32_t red[kThreads / 64];
   const float mx = FMT == TCFP_FP8_E5M2 ? kE5M2Max : kE4M3Max;
+  const float s = consumer_scale(scale_in, part, g, bf16_rule != 0, mx, scale_out, inv_out, red);
   const int64_t nvec = n >> 3;
   const int64_t stride = int64_t(gridDim.x) * kThreads;
-  for (int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x; i < nvec; i += stride) {
+  int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+  for (; i + stride < nvec; i += 2 * stride) {
+    float v[2][8];
+    load8(x + i * 8, v[0]);
+    load8(x + (i + stride) * 8, v[1]);
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[u][j] = clampf(v[u][j] * s, mx);
+      *reinterpret_cast<uint2*>(q + (i + u * stride) * 8) = encode8<FMT>(v[u]);
+    }
+  }
+  for (; i < nvec; i += stride) {
     float v[8];
     load8(x + i * 8, v);
 #pragma unroll
     for (int j = 0; j < 8; ++j) v[j] = clampf(v[j] * s, mx);
     *reinterpret_cast<uint2*>(q + i * 8) = encode8<FMT>(v);
   }
-  for (int64_t i = nvec * 8 + int64_t(blockIdx.x) * kThreads + threadIdx.x; i < n; i += stride)
-    q[i] = uint8_t(encode1<FMT>(clampf(load1(x + i) * s, mx)));
+  for (int64_t t = nvec * 8 + int64_t(blockIdx.x) * kThreads + threadIdx.x; t < n; t += stride)
+    q[t] = uint8_t(encode1<FMT>(clampf(load1(x + t) * s, mx)));
 }
 
-// Same quantisation on 64x64 tiles, also writing the transposed codes
-// qt[c, r] through an LDS tile.
+// ---- 128 x 128 tiles with a transposed copy ------------------------------
+// A workgroup quantises a 128 x 128 tile with 16-byte loads (a tile row is
+// read by 32 (fp32) or 16 (bf16) consecutive lanes), stores the codes row by
+// row, keeps them in LDS as 32 words per row, and writes the transposed
+// tile: each lane gathers 16 rows of one word column, transposes the 4 x 4
+// byte blocks in registers and stores 16-byte runs; 8 consecutive lanes
+// cover one 128-byte output row segment.  Requires cols % 8 == 0, so every
+// vector lies inside one row.
+constexpr int kTile = 128;
+constexpr int kTilePitch = kTile / 4 + 1;  // words per LDS row (+1 against bank conflicts)
+
+struct TileGeom {
+  int64_t r0, c0;
+  int tiles_c;
+  TCFP_DEV TileGeom(int64_t cols) {
+    tiles_c = int((cols + kTile - 1) / kTile);
+    r0 = int64_t(blockIdx.x / tiles_c) * kTile;
+    c0 = int64_t(blockIdx.x % tiles_c) * kTile;
+  }
+};
+
+// 16 tile rows of word column c4 -> 4 output columns of 16 bytes each.
+TCFP_DEV void gather_transpose(const uint32_t* tile, int rc, int c4, uint4 out[4]) {
+  uint32_t w[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) w[j] = tile[(rc * 16 + j) * kTilePitch + c4];
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    uint32_t o[4];
+#pragma unroll
+    for (int qd = 0; qd < 4; ++qd) {
+      const int sh = 8 * b;
+      o[qd] = ((w[4 * qd] >> sh) & 0xFFu) | (((w[4 * qd + 1] >> sh) & 0xFFu) << 8) |
+              (((w[4 * qd + 2] >> sh) & 0xFFu) << 16) | (((w[4 * qd + 3] >> sh) & 0xFFu) << 24);
+    }
+    out[b] = make_uint4(o[0], o[1], o[2], o[3]);
+  }
+}
+
+// Writes the transposed tile held in `tile` to dst [cols, rows].
+TCFP_DEV void store_transposed(const uint32_t* tile, const TileGeom& tg, int64_t rows,
+                               int64_t cols, uint8_t* __restrict__ dst) {
+  const int c4 = threadIdx.x >> 3, rc = threadIdx.x & 7;
+  uint4 out[4];
+  gather_transpose(tile, rc, c4, out);
+  const int64_t r = tg.r0 + rc * 16;
+  const bool fast = (rows % 16 == 0) && (r + 16 <= rows);
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    const int64_t c = tg.c0 + c4 * 4 + b;
+    if (c >= cols) continue;
+    uint8_t* o = dst + c * rows + r;
+    if (fast) {
+      *reinterpret_cast<uint4*>(o) = out[b];
+    } else {
+      const uint32_t wd[4] = {out[b].x, out[b].y, out[b].z, out[b].w};
+#pragma unroll
+      for (int j = 0; j < 16; ++j)
+        if (r + j < rows) o[j] = uint8_t(wd[j >> 2] >> (8 * (j & 3)));
+    }
+  }
+}
+
+template <typename InT>
+struct TileLoad {
+  static constexpr int VEC = 16 / int(sizeof(InT));  // elements per 16-byte load
+  static constexpr int TPR = kTile / VEC;             // lanes per tile row
+  static constexpr int RPI = kThreads / TPR;          // tile rows per pass
+};
+
+template <typename InT>
+TCFP_DEV void loadvec(const InT* p, float* v);
+template <>
+TCFP_DEV void loadvec<float>(const float* p, float* v) {
+  const float4 a = *reinterpret_cast<const float4*>(p);
+  v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+}
+template <>
+TCFP_DEV void loadvec<uint16_t>(const uint16_t* p, float* v) { load8(p, v); }
+
 template <typename InT, int FMT>
-__global__ __launch_bounds__(kThreads) void quant_tiled_kernel(const InT* __restrict__ x,
-                                                               int64_t rows, int64_t cols,
-                                                               const float* __restrict__ scale_p,
-                                                               uint8_t* __restrict__ q,
-                                                               uint8_t* __restrict__ qt) {
-  __shared__ uint8_t tile[64][64 + 4];
-  const float s = *scale_p;
+__global__ __launch_bounds__(kThreads) void quant_t_kernel(
+    const InT* __restrict__ x, int64_t rows, int64_t cols, const uint32_t* __restrict__ part,
+    int g, int bf16_rule, const float* __restrict__ scale_in, uint8_t* __restrict__ q,
+    uint8_t* __restrict__ qt, float* scale_out, float* inv_out) {
+  using TL = TileLoad<InT>;
+  constexpr int VEC = TL::VEC;
+  __shared__ uint32_t red[kThreads / 64];
+  __shared__ uint32_t tile[kTile * kTilePitch];
   const float mx = FMT == TCFP_FP8_E5M2 ? kE5M2Max : kE4M3Max;
-  const int64_t r0 = int64_t(blockIdx.y) * 64, c0 = int64_t(blockIdx.x) * 64;
-  const int t = threadIdx.x, cg = t & 15, rg = t >> 4;
+  const float s = consumer_scale(scale_in, part, g, bf16_rule != 0, mx, scale_out, inv_out, red);
+  const TileGeom tg(cols);
+  const int tc = (threadIdx.x % TL::TPR) * VEC;
+  const int64_t c = tg.c0 + tc;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int lr = rg * 4 + i;
-    const int64_t r = r0 + lr;
-    float v[4];
+  for (int it = 0; it < kTile / TL::RPI; ++it) {
+    const int tr = it * TL::RPI + threadIdx.x / TL::TPR;
+    const int64_t r = tg.r0 + tr;
+    const bool valid = r < rows && c < cols;
+    float v[VEC];
+    if (valid) {
+      loadvec<InT>(x + r * cols + c, v);
+    } else {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int64_t c = c0 + cg * 4 + j;
-      v[j] = (r < rows && c < cols) ? clampf(load1(x + r * cols + c) * s, mx) : 0.0f;
+      for (int j = 0; j < VEC; ++j) v[j] = 0.0f;
     }
-#ifdef TCFP_SW_CVT
-    uint32_t code = sw4_fp8<FMT>(v[0], v[1], v[2], v[3]);
-#else
-    uint32_t code = cvt4_fp8<FMT>(v[0], v[1], v[2], v[3]);
-#endif
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int64_t c = c0 + cg * 4 + j;
-      const uint8_t b = uint8_t(code >> (8 * j));
-      tile[lr][cg * 4 + j] = b;
-      if (r < rows && c < cols) q[r * cols + c] = b;
+    for (int j = 0; j < VEC; ++j) v[j] = clampf(v[j] * s, mx);
+    uint32_t wd[VEC / 4];
+#pragma unroll
+    for (int j = 0; j < VEC; j += 4) wd[j / 4] = encode4<FMT>(v[j], v[j + 1], v[j + 2], v[j + 3]);
+    if (valid) {
+      if constexpr (VEC == 4) *reinterpret_cast<uint32_t*>(q + r * cols + c) = wd[0];
+      else *reinterpret_cast<uint2*>(q + r * cols + c) = make_uint2(wd[0], wd[1]);
     }
+#pragma unroll
+    for (int j = 0; j < VEC / 4; ++j) tile[tr * kTilePitch + tc / 4 + j] = wd[j];
   }
   __syncthreads();
-  const int tr = t >> 2, seg = t & 3;
-  const int64_t c = c0 + tr;
-  if (c < cols) {
-#pragma unroll
-    for (int b = 0; b < 16; ++b) {
-      const int lr = seg * 16 + b;
-      const int64_t r = r0 + lr;
-      if (r < rows) qt[c * rows + r] = tile[lr][tr];
-    }
-  }
+  store_transposed(tile, tg, rows, cols, qt);
 }
 
 // ===========================================================================
 // Per-tensor dual quantisation (tcfp/nn/__init__.py:343-383)
 // ===========================================================================
+// Pass 1 is amax_part_kernel<InT, HAS_EF> (partials a).
 
-// Pass 2: W_hi codes and max |residual| -> scale_lo.
+// Pass 2: W_hi codes and the partial max |residual| (partials b).
 template <typename InT, bool HAS_EF>
-__global__ __launch_bounds__(kThreads) void dualq_hi_kernel(const InT* __restrict__ w,
-                                                            const float* __restrict__ ef,
-                                                            int64_t n, ReduceWs* ws,
-                                                            uint8_t* __restrict__ hi,
-                                                            float* inv_lo_out) {
-  const float s_hi = ws->scale[0], inv_hi = ws->scale[1];
+__global__ __launch_bounds__(kThreads) void dualq_hi_kernel(
+    const InT* __restrict__ w, const float* __restrict__ ef, int64_t n,
+    const uint32_t* __restrict__ pa, int ga, uint8_t* __restrict__ hi, uint32_t* __restrict__ pb,
+    float* inv_hi_out) {
+  __shared__ uint32_t red[kThreads / 64];
+  __shared__ uint32_t red2[kThreads / 64];
+  const float s_hi =
+      consumer_scale(nullptr, pa, ga, false, kE4M3Max, nullptr, inv_hi_out, red);
+  const float inv_hi = __fdiv_rn(1.0f, s_hi);
   uint32_t m = 0;
   const int64_t nvec = n >> 3;
   const int64_t stride = int64_t(gridDim.x) * kThreads;
-  for (int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x; i < nvec; i += stride) {
-    float v[8], c[8];
-    load8(w + i * 8, v);
-    if constexpr (HAS_EF) {
-      float e[8];
-      load8(ef + i * 8, e);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) v[j] = v[j] + e[j];
-    }
+  auto body = [&](const float v[8], int64_t i) {
+    float c[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) c[j] = clampf(v[j] * s_hi, kE4M3Max);
     const uint2 code = encode8<TCFP_FP8_E4M3>(c);
     *reinterpret_cast<uint2*>(hi + i * 8) = code;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const float r = v[j] - e4m3_to_f32(byte_of(code, j)) * inv_hi;
-      m = umax(m, absbits(r));
-    }
+    for (int j = 0; j < 8; ++j) m = umax(m, absbits(v[j] - e4m3_to_f32(byte_of(code, j)) * inv_hi));
+  };
+  int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+  for (; i + stride < nvec; i += 2 * stride) {
+    float W[2][8], v[2][8];
+    load_w8<InT, HAS_EF>(w, ef, i, W[0], v[0]);
+    load_w8<InT, HAS_EF>(w, ef, i + stride, W[1], v[1]);
+    body(v[0], i);
+    body(v[1], i + stride);
   }
-  for (int64_t i = nvec * 8 + int64_t(blockIdx.x) * kThreads + threadIdx.x; i < n; i += stride) {
-    float v = load1(w + i);
-    if constexpr (HAS_EF) v = v + ef[i];
+  for (; i < nvec; i += stride) {
+    float W[8], v[8];
+    load_w8<InT, HAS_EF>(w, ef, i, W, v);
+    body(v, i);
+  }
+  for (int64_t t = nvec * 8 + int64_t(blockIdx.x) * kThreads + threadIdx.x; t < n; t += stride) {
+    float v = load1(w + t);
+    if constexpr (HAS_EF) v = v + ef[t];
     const uint32_t code = encode1<TCFP_FP8_E4M3>(clampf(v * s_hi, kE4M3Max));
-    hi[i] = uint8_t(code);
+    hi[t] = uint8_t(code);
     m = umax(m, absbits(v - e4m3_to_f32(code) * inv_hi));
   }
-  reduce_and_finalize(m, ws, 1, false, kE4M3Max, nullptr, inv_lo_out);
+  m = block_umax_all(m, red2);
+  if (threadIdx.x == 0) pb[blockIdx.x] = m;
 }
 
 // Stochastic rounding of an already scaled and clamped value, following
@@ -328,84 +465,189 @@ TCFP_DEV uint32_t sr_per_tensor(float x, float u) {
   return (u < frac) ? hi : lo;
 }
 
-// Pass 3: W_lo codes (RNE or SR) and, optionally, the new error in place.
+// W_lo codes of 4 consecutive elements starting at flat element `e0`
+// (a multiple of 4).  SR draws Philox counter (e0 / 4) so that the random
+// bits of an element depend only on its index.
+template <bool SR>
+TCFP_DEV uint32_t lo_codes4(const float x[4], int64_t e0, uint32_t k0, uint32_t k1, uint32_t o0,
+                            uint32_t o1) {
+  if constexpr (SR) {
+    const uint64_t ctr = uint64_t(e0) >> 2;
+    const u32x4 r = philox4x32_10({uint32_t(ctr), uint32_t(ctr >> 32), o0, o1}, k0, k1);
+    return sr_per_tensor(x[0], u32_to_unit(r.x)) | (sr_per_tensor(x[1], u32_to_unit(r.y)) << 8) |
+           (sr_per_tensor(x[2], u32_to_unit(r.z)) << 16) |
+           (sr_per_tensor(x[3], u32_to_unit(r.w)) << 24);
+  } else {
+    return encode4<TCFP_FP8_E4M3>(x[0], x[1], x[2], x[3]);
+  }
+}
+
+struct DualScales {
+  float s_hi, inv_hi, s_lo, inv_lo;
+};
+
+// Pass-3 arithmetic for 4 elements: W_hi codes (recomputed exactly as in
+// pass 2), W_lo codes, and the new error W - (deq(hi) + deq(lo)).
+template <bool SR>
+TCFP_DEV void dual_codes4(const float W[4], const float v[4], const DualScales& sc, int64_t e0,
+                          uint32_t k0, uint32_t k1, uint32_t o0, uint32_t o1, uint32_t* hcode,
+                          uint32_t* lcode, float err[4]) {
+  float c[4], dh[4], x[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) c[j] = clampf(v[j] * sc.s_hi, kE4M3Max);
+  const uint32_t h = encode4<TCFP_FP8_E4M3>(c[0], c[1], c[2], c[3]);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    dh[j] = e4m3_to_f32((h >> (8 * j)) & 0xFFu) * sc.inv_hi;
+    x[j] = clampf((v[j] - dh[j]) * sc.s_lo, kE4M3Max);
+  }
+  const uint32_t l = lo_codes4<SR>(x, e0, k0, k1, o0, o1);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const float dl = e4m3_to_f32((l >> (8 * j)) & 0xFFu) * sc.inv_lo;
+    err[j] = W[j] - (dh[j] + dl);
+  }
+  *hcode = h;
+  *lcode = l;
+}
+
+TCFP_DEV DualScales dual_scales(const uint32_t* pa, int ga, const uint32_t* pb, int gb,
+                                float* inv_lo_out, uint32_t* red, uint32_t* red2) {
+  DualScales sc;
+  sc.s_hi = consumer_scale(nullptr, pa, ga, false, kE4M3Max, nullptr, nullptr, red);
+  sc.inv_hi = __fdiv_rn(1.0f, sc.s_hi);
+  sc.s_lo = consumer_scale(nullptr, pb, gb, false, kE4M3Max, nullptr, inv_lo_out, red2);
+  sc.inv_lo = __fdiv_rn(1.0f, sc.s_lo);
+  return sc;
+}
+
+// Pass 3 (flat): W_lo codes (RNE or SR) and, optionally, the new error in place.
 template <typename InT, bool HAS_EF, bool UPDATE, bool SR>
-__global__ __launch_bounds__(kThreads) void dualq_lo_kernel(const InT* __restrict__ w,
-                                                            float* __restrict__ ef, int64_t n,
-                                                            const ReduceWs* ws,
-                                                            uint8_t* __restrict__ lo,
-                                                            uint32_t k0, uint32_t k1,
-                                                            uint32_t off0, uint32_t off1) {
-  const float s_hi = ws->scale[0], inv_hi = ws->scale[1];
-  const float s_lo = ws->scale[2], inv_lo = ws->scale[3];
+__global__ __launch_bounds__(kThreads) void dualq_lo_kernel(
+    const InT* __restrict__ w, float* __restrict__ ef, int64_t n, const uint32_t* __restrict__ pa,
+    int ga, const uint32_t* __restrict__ pb, int gb, uint8_t* __restrict__ lo, float* inv_lo_out,
+    uint32_t k0, uint32_t k1, uint32_t off0, uint32_t off1) {
+  __shared__ uint32_t red[kThreads / 64];
+  __shared__ uint32_t red2[kThreads / 64];
+  const DualScales sc = dual_scales(pa, ga, pb, gb, inv_lo_out, red, red2);
   const int64_t nvec = n >> 3;
   const int64_t stride = int64_t(gridDim.x) * kThreads;
-  for (int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x; i < nvec; i += stride) {
-    float W[8], v[8], c[8], x[8];
-    load8(w + i * 8, W);
-    if constexpr (HAS_EF) {
-      float e[8];
-      load8(ef + i * 8, e);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) v[j] = W[j] + e[j];
-    } else {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) v[j] = W[j];
-    }
-#pragma unroll
-    for (int j = 0; j < 8; ++j) c[j] = clampf(v[j] * s_hi, kE4M3Max);
-    const uint2 hcode = encode8<TCFP_FP8_E4M3>(c);
-    float dh[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      dh[j] = e4m3_to_f32(byte_of(hcode, j)) * inv_hi;
-      x[j] = clampf((v[j] - dh[j]) * s_lo, kE4M3Max);
-    }
-    uint2 lcode;
-    if constexpr (SR) {
-      const uint64_t base = uint64_t(i) * 2;
-      u32x4 r0 = philox4x32_10({uint32_t(base), uint32_t(base >> 32), off0, off1}, k0, k1);
-      u32x4 r1 = philox4x32_10({uint32_t(base + 1), uint32_t((base + 1) >> 32), off0, off1}, k0, k1);
-      const uint32_t rr[8] = {r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, r1.z, r1.w};
-      uint32_t b[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) b[j] = sr_per_tensor(x[j], u32_to_unit(rr[j]));
-      lcode = make_uint2(b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24),
-                         b[4] | (b[5] << 8) | (b[6] << 16) | (b[7] << 24));
-    } else {
-      lcode = encode8<TCFP_FP8_E4M3>(x);
-    }
-    *reinterpret_cast<uint2*>(lo + i * 8) = lcode;
-    if constexpr (HAS_EF && UPDATE) {
-      float e[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const float dl = e4m3_to_f32(byte_of(lcode, j)) * inv_lo;
-        e[j] = W[j] - (dh[j] + dl);
-      }
-      store8(ef + i * 8, e);
-    }
+  auto body = [&](const float W[8], const float v[8], int64_t i) {
+    uint32_t hc[2], lc[2];
+    float e[8];
+    dual_codes4<SR>(W, v, sc, i * 8, k0, k1, off0, off1, &hc[0], &lc[0], e);
+    dual_codes4<SR>(W + 4, v + 4, sc, i * 8 + 4, k0, k1, off0, off1, &hc[1], &lc[1], e + 4);
+    *reinterpret_cast<uint2*>(lo + i * 8) = make_uint2(lc[0], lc[1]);
+    if constexpr (HAS_EF && UPDATE) store8(ef + i * 8, e);
+  };
+  int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+  for (; i + stride < nvec; i += 2 * stride) {
+    float W[2][8], v[2][8];
+    load_w8<InT, HAS_EF>(w, ef, i, W[0], v[0]);
+    load_w8<InT, HAS_EF>(w, ef, i + stride, W[1], v[1]);
+    body(W[0], v[0], i);
+    body(W[1], v[1], i + stride);
   }
-  for (int64_t i = nvec * 8 + int64_t(blockIdx.x) * kThreads + threadIdx.x; i < n; i += stride) {
-    const float W = load1(w + i);
+  for (; i < nvec; i += stride) {
+    float W[8], v[8];
+    load_w8<InT, HAS_EF>(w, ef, i, W, v);
+    body(W, v, i);
+  }
+  for (int64_t t = nvec * 8 + int64_t(blockIdx.x) * kThreads + threadIdx.x; t < n; t += stride) {
+    const float W = load1(w + t);
     float v = W;
-    if constexpr (HAS_EF) v = W + ef[i];
-    const uint32_t hcode = encode1<TCFP_FP8_E4M3>(clampf(v * s_hi, kE4M3Max));
-    const float dh = e4m3_to_f32(hcode) * inv_hi;
-    const float x = clampf((v - dh) * s_lo, kE4M3Max);
+    if constexpr (HAS_EF) v = W + ef[t];
+    const uint32_t hcode = encode1<TCFP_FP8_E4M3>(clampf(v * sc.s_hi, kE4M3Max));
+    const float dh = e4m3_to_f32(hcode) * sc.inv_hi;
+    const float x = clampf((v - dh) * sc.s_lo, kE4M3Max);
     uint32_t lcode;
     if constexpr (SR) {
-      const uint64_t ctr = (uint64_t(1) << 62) + uint64_t(i);
+      const uint64_t ctr = (uint64_t(1) << 62) + uint64_t(t);
       u32x4 r = philox4x32_10({uint32_t(ctr), uint32_t(ctr >> 32), off0, off1}, k0, k1);
       lcode = sr_per_tensor(x, u32_to_unit(r.x));
     } else {
       lcode = encode1<TCFP_FP8_E4M3>(x);
     }
-    lo[i] = uint8_t(lcode);
-    if constexpr (HAS_EF && UPDATE) ef[i] = W - (dh + e4m3_to_f32(lcode) * inv_lo);
+    lo[t] = uint8_t(lcode);
+    if constexpr (HAS_EF && UPDATE) ef[t] = W - (dh + e4m3_to_f32(lcode) * sc.inv_lo);
   }
 }
 
+// Pass 3 (tiled, cols % 8 == 0): as dualq_lo_kernel on 128 x 128 tiles, and
+// also writes the transposed W_hi and W_lo codes (the dgrad operands).
+template <typename InT, bool HAS_EF, bool UPDATE, bool SR>
+__global__ __launch_bounds__(kThreads) void dualq_lo_t_kernel(
+    const InT* __restrict__ w, float* __restrict__ ef, int64_t rows, int64_t cols,
+    const uint32_t* __restrict__ pa, int ga, const uint32_t* __restrict__ pb, int gb,
+    uint8_t* __restrict__ lo, float* inv_lo_out, uint8_t* __restrict__ hi_t,
+    uint8_t* __restrict__ lo_t, uint32_t k0, uint32_t k1, uint32_t off0, uint32_t off1) {
+  using TL = TileLoad<InT>;
+  constexpr int VEC = TL::VEC;
+  __shared__ uint32_t red[kThreads / 64];
+  __shared__ uint32_t red2[kThreads / 64];
+  __shared__ uint32_t tile_h[kTile * kTilePitch];
+  __shared__ uint32_t tile_l[kTile * kTilePitch];
+  const DualScales sc = dual_scales(pa, ga, pb, gb, inv_lo_out, red, red2);
+  const TileGeom tg(cols);
+  const int tc = (threadIdx.x % TL::TPR) * VEC;
+  const int64_t c = tg.c0 + tc;
+#pragma unroll 2
+  for (int it = 0; it < kTile / TL::RPI; ++it) {
+    const int tr = it * TL::RPI + threadIdx.x / TL::TPR;
+    const int64_t r = tg.r0 + tr;
+    const bool valid = r < rows && c < cols;
+    const int64_t off = r * cols + c;
+    float W[VEC], v[VEC];
+    if (valid) {
+      loadvec<InT>(w + off, W);
+    } else {
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) W[j] = 0.0f;
+    }
+    if constexpr (HAS_EF) {
+      float e[VEC];
+      if (valid) {
+#pragma unroll
+        for (int j = 0; j < VEC; j += 4) {
+          const float4 a = *reinterpret_cast<const float4*>(ef + off + j);
+          e[j] = a.x; e[j + 1] = a.y; e[j + 2] = a.z; e[j + 3] = a.w;
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) e[j] = 0.0f;
+      }
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) v[j] = W[j] + e[j];
+    } else {
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) v[j] = W[j];
+    }
+    uint32_t hc[VEC / 4], lc[VEC / 4];
+    float err[VEC];
+#pragma unroll
+    for (int j = 0; j < VEC; j += 4)
+      dual_codes4<SR>(W + j, v + j, sc, off + j, k0, k1, off0, off1, &hc[j / 4], &lc[j / 4],
+                      err + j);
+    if (valid) {
+      if constexpr (VEC == 4) *reinterpret_cast<uint32_t*>(lo + off) = lc[0];
+      else *reinterpret_cast<uint2*>(lo + off) = make_uint2(lc[0], lc[1]);
+      if constexpr (HAS_EF && UPDATE) {
+#pragma unroll
+        for (int j = 0; j < VEC; j += 4)
+          *reinterpret_cast<float4*>(ef + off + j) =
+              make_float4(err[j], err[j + 1], err[j + 2], err[j + 3]);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < VEC / 4; ++j) {
+      tile_h[tr * kTilePitch + tc / 4 + j] = hc[j];
+      tile_l[tr * kTilePitch + tc / 4 + j] = lc[j];
+    }
+  }
+  __syncthreads();
+  if (hi_t) store_transposed(tile_h, tg, rows, cols, hi_t);
+  if (lo_t) store_transposed(tile_l, tg, rows, cols, lo_t);
+}
 // ===========================================================================
 // Block quantisation (tcfp/kernels.py:205-275)
 // ===========================================================================
@@ -703,14 +945,6 @@ __global__ __launch_bounds__(kThreads) void selftest_philox_kernel(uint32_t c0, 
   out[4 * i] = r.x; out[4 * i + 1] = r.y; out[4 * i + 2] = r.z; out[4 * i + 3] = r.w;
 }
 
-// inv = 1 / scale (IEEE) for an explicitly supplied scale (tcfp/core.py:105).
-__global__ void inverse_kernel(const float* s, float* inv, float* echo) {
-  if (threadIdx.x != 0) return;
-  const float v = *s;
-  *inv = __fdiv_rn(1.0f, v);
-  if (echo) *echo = v;
-}
-
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 }  // namespace
@@ -733,7 +967,7 @@ const char* tcfp_status_string(int status) {
   }
 }
 
-size_t tcfp_workspace_bytes(void) { return 256; }
+size_t tcfp_workspace_bytes(void) { return sizeof(PartWs); }
 
 int tcfp_quantize_per_tensor(const void* x, int x_dtype, int64_t rows, int64_t cols,
                              int fp8_fmt, const float* scale_in, uint8_t* q, uint8_t* q_t,
@@ -744,54 +978,53 @@ int tcfp_quantize_per_tensor(const void* x, int x_dtype, int64_t rows, int64_t c
   if (fp8_fmt != TCFP_FP8_E4M3 && fp8_fmt != TCFP_FP8_E5M2) return TCFP_ERR_DTYPE;
   if (!aligned16(x) || !inv_out) return TCFP_ERR_ALIGN;
   if (!scale_in && !workspace) return TCFP_ERR_WORKSPACE;
-  hipStream_t st = static_cast<hipStream_t>(stream);
   const int64_t n = rows * cols;
-  const float fmax = fp8_fmt == TCFP_FP8_E5M2 ? kE5M2Max : kE4M3Max;
-  ReduceWs* ws = static_cast<ReduceWs*>(workspace);
+  if (n >= 8 && (reinterpret_cast<uintptr_t>(q) & 7u) != 0) return TCFP_ERR_ALIGN;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  PartWs* ws = static_cast<PartWs*>(workspace);
   const bool bf = x_dtype == TCFP_DTYPE_BF16;
-  const float* scale_p;
-  if (scale_in) {
-    scale_p = scale_in;
-    // inv = 1/scale and scale echo: reuse the finalize path on a 1-thread grid
-    // is overkill; compute with a tiny kernel below.
-  } else {
-    const int g = grid_for((n + 7) / 8, 4);
+  uint32_t* part = ws ? ws->a : nullptr;
+  int g = 0;
+  if (!scale_in) {
+    g = parts_for((n + 7) / 8);
     if (bf)
-      amax_kernel<uint16_t, false><<<g, kThreads, 0, st>>>(static_cast<const uint16_t*>(x),
-                                                           nullptr, n, ws, 0, 1, fmax,
-                                                           scale_out, inv_out);
+      amax_part_kernel<uint16_t, false><<<g, kThreads, 0, st>>>(static_cast<const uint16_t*>(x),
+                                                                nullptr, n, part);
     else
-      amax_kernel<float, false><<<g, kThreads, 0, st>>>(static_cast<const float*>(x), nullptr,
-                                                        n, ws, 0, 0, fmax, scale_out, inv_out);
+      amax_part_kernel<float, false><<<g, kThreads, 0, st>>>(static_cast<const float*>(x),
+                                                             nullptr, n, part);
   }
-  if (scale_in) inverse_kernel<<<1, 64, 0, st>>>(scale_in, inv_out, scale_out);
-  else scale_p = &ws->scale[0];
-  if (n == 0) return launch_status();
-  if (q_t) {
-    dim3 grid(unsigned((cols + 63) / 64), unsigned((rows + 63) / 64));
-#define TCFP_QT(T, F)                                                                         \
-  quant_tiled_kernel<T, F><<<grid, kThreads, 0, st>>>(static_cast<const T*>(x), rows, cols, \
-                                                       scale_p, q, q_t)
+  const int bfr = bf ? 1 : 0;
+  const bool tiled = q_t && n > 0 && cols % 8 == 0;
+  if (tiled) {
+    const int64_t tiles = ((rows + kTile - 1) / kTile) * ((cols + kTile - 1) / kTile);
+    if (tiles > INT32_MAX) return TCFP_ERR_SHAPE;
+#define TCFP_QT(T, F)                                                                          \
+  quant_t_kernel<T, F><<<unsigned(tiles), kThreads, 0, st>>>(static_cast<const T*>(x), rows,  \
+                                                             cols, part, g, bfr, scale_in, q, \
+                                                             q_t, scale_out, inv_out)
     if (bf) {
       if (fp8_fmt == TCFP_FP8_E5M2) TCFP_QT(uint16_t, TCFP_FP8_E5M2); else TCFP_QT(uint16_t, TCFP_FP8_E4M3);
     } else {
       if (fp8_fmt == TCFP_FP8_E5M2) TCFP_QT(float, TCFP_FP8_E5M2); else TCFP_QT(float, TCFP_FP8_E4M3);
     }
 #undef TCFP_QT
+    return launch_status();
+  }
+  // flat (also for empty tensors: one workgroup still publishes scale / inv)
+  const int gq = grid_for((n + 15) / 16, 8);
+#define TCFP_QF(T, F)                                                                        \
+  quant_flat_kernel<T, F><<<gq, kThreads, 0, st>>>(static_cast<const T*>(x), n, part, g, bfr, \
+                                                    scale_in, q, scale_out, inv_out)
+  if (bf) {
+    if (fp8_fmt == TCFP_FP8_E5M2) TCFP_QF(uint16_t, TCFP_FP8_E5M2); else TCFP_QF(uint16_t, TCFP_FP8_E4M3);
   } else {
-    if (!aligned16(q) && n >= 8) {
-      // the flat kernel stores 8 codes at a time
-      if ((reinterpret_cast<uintptr_t>(q) & 7u) != 0) return TCFP_ERR_ALIGN;
-    }
-    const int g = grid_for((n + 7) / 8, 16);
-#define TCFP_QF(T, F) \
-  quant_flat_kernel<T, F><<<g, kThreads, 0, st>>>(static_cast<const T*>(x), n, scale_p, q)
-    if (bf) {
-      if (fp8_fmt == TCFP_FP8_E5M2) TCFP_QF(uint16_t, TCFP_FP8_E5M2); else TCFP_QF(uint16_t, TCFP_FP8_E4M3);
-    } else {
-      if (fp8_fmt == TCFP_FP8_E5M2) TCFP_QF(float, TCFP_FP8_E5M2); else TCFP_QF(float, TCFP_FP8_E4M3);
-    }
+    if (fp8_fmt == TCFP_FP8_E5M2) TCFP_QF(float, TCFP_FP8_E5M2); else TCFP_QF(float, TCFP_FP8_E4M3);
+  }
 #undef TCFP_QF
+  if (q_t && n > 0) {
+    const dim3 grid(unsigned((cols + 63) / 64), unsigned((rows + 63) / 64));
+    transpose_u8_kernel<<<grid, kThreads, 0, st>>>(q, rows, cols, q_t);
   }
   return launch_status();
 }
@@ -808,37 +1041,41 @@ int tcfp_dual_quantize_per_tensor(const void* w, int w_dtype, int64_t n, int64_t
   if (!aligned16(w) || !aligned16(w_hi) || !aligned16(w_lo) || (ef && !aligned16(ef)))
     return TCFP_ERR_ALIGN;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  ReduceWs* ws = static_cast<ReduceWs*>(workspace);
+  PartWs* ws = static_cast<PartWs*>(workspace);
   const int64_t total = n * k;
-  const int gr = grid_for((total + 7) / 8, 4);
-  const int gq = grid_for((total + 7) / 8, 8);
+  const int64_t nvec = (total + 7) / 8;
+  const int ga = parts_for(nvec);
+  const int gb = parts_for(nvec);
+  const int gq = grid_for((nvec + 1) / 2, 8);
   const bool bf = w_dtype == TCFP_DTYPE_BF16;
   const bool has_ef = ef != nullptr;
   const bool upd = has_ef && update_ef;
+  const bool tiled = (w_hi_t || w_lo_t) && total > 0 && k % 8 == 0;
+  const int64_t tiles = ((n + kTile - 1) / kTile) * ((k + kTile - 1) / kTile);
+  if (tiled && tiles > INT32_MAX) return TCFP_ERR_SHAPE;
   const uint32_t k0 = uint32_t(seed), k1 = uint32_t(seed >> 32);
   const uint32_t o0 = uint32_t(offset), o1 = uint32_t(offset >> 32);
 
-#define TCFP_DQ(T, EF)                                                                        \
-  do {                                                                                        \
-    const T* wp = static_cast<const T*>(w);                                                   \
-    amax_kernel<T, EF><<<gr, kThreads, 0, st>>>(wp, ef, total, ws, 0, 0, kE4M3Max, nullptr,  \
-                                                 inv_hi);                                     \
-    dualq_hi_kernel<T, EF><<<gr, kThreads, 0, st>>>(wp, ef, total, ws, w_hi, inv_lo);         \
-    if (stochastic_lo) {                                                                      \
-      if (upd)                                                                                \
-        dualq_lo_kernel<T, EF, EF, true><<<gq, kThreads, 0, st>>>(wp, ef, total, ws, w_lo, k0, \
-                                                                  k1, o0, o1);                \
-      else                                                                                    \
-        dualq_lo_kernel<T, EF, false, true><<<gq, kThreads, 0, st>>>(wp, ef, total, ws, w_lo,  \
-                                                                     k0, k1, o0, o1);         \
-    } else {                                                                                  \
-      if (upd)                                                                                \
-        dualq_lo_kernel<T, EF, EF, false><<<gq, kThreads, 0, st>>>(wp, ef, total, ws, w_lo,    \
-                                                                   k0, k1, o0, o1);           \
-      else                                                                                    \
-        dualq_lo_kernel<T, EF, false, false><<<gq, kThreads, 0, st>>>(wp, ef, total, ws, w_lo, \
-                                                                      k0, k1, o0, o1);        \
-    }                                                                                         \
+#define TCFP_LO(T, EF, UP, SR)                                                                  \
+  do {                                                                                          \
+    if (tiled)                                                                                  \
+      dualq_lo_t_kernel<T, EF, UP, SR><<<unsigned(tiles), kThreads, 0, st>>>(                   \
+          wp, ef, n, k, ws->a, ga, ws->b, gb, w_lo, inv_lo, w_hi_t, w_lo_t, k0, k1, o0, o1);    \
+    else                                                                                        \
+      dualq_lo_kernel<T, EF, UP, SR><<<gq, kThreads, 0, st>>>(wp, ef, total, ws->a, ga, ws->b, \
+                                                              gb, w_lo, inv_lo, k0, k1, o0, o1); \
+  } while (0)
+#define TCFP_DQ(T, EF)                                                                          \
+  do {                                                                                          \
+    const T* wp = static_cast<const T*>(w);                                                     \
+    amax_part_kernel<T, EF><<<ga, kThreads, 0, st>>>(wp, ef, total, ws->a);                    \
+    dualq_hi_kernel<T, EF><<<gb, kThreads, 0, st>>>(wp, ef, total, ws->a, ga, w_hi, ws->b,     \
+                                                    inv_hi);                                    \
+    if (stochastic_lo) {                                                                        \
+      if (upd) TCFP_LO(T, EF, EF, true); else TCFP_LO(T, EF, false, true);                      \
+    } else {                                                                                    \
+      if (upd) TCFP_LO(T, EF, EF, false); else TCFP_LO(T, EF, false, false);                    \
+    }                                                                                           \
   } while (0)
 
   if (bf) {
@@ -847,8 +1084,9 @@ int tcfp_dual_quantize_per_tensor(const void* w, int w_dtype, int64_t n, int64_t
     if (has_ef) TCFP_DQ(float, true); else TCFP_DQ(float, false);
   }
 #undef TCFP_DQ
-  if (w_hi_t || w_lo_t) {
-    dim3 grid(unsigned((k + 63) / 64), unsigned((n + 63) / 64));
+#undef TCFP_LO
+  if (!tiled && total > 0 && (w_hi_t || w_lo_t)) {
+    const dim3 grid(unsigned((k + 63) / 64), unsigned((n + 63) / 64));
     if (w_hi_t) transpose_u8_kernel<<<grid, kThreads, 0, st>>>(w_hi, n, k, w_hi_t);
     if (w_lo_t) transpose_u8_kernel<<<grid, kThreads, 0, st>>>(w_lo, n, k, w_lo_t);
   }

@@ -393,3 +393,109 @@ def fused_dual_quantize_fp8(
         "fused_dual_quantize_fp8",
     )
     return w_hi, w_lo, sh, sl
+
+
+# ---------------------------------------------------------------------------
+# Block-scaled GEMMs
+# ---------------------------------------------------------------------------
+
+
+def _block_exps(e: torch.Tensor, rows: int, num_kb: int, name: str) -> torch.Tensor:
+    if e.dtype != torch.int8:
+        raise TypeError(f"{name} must be int8 power-of-two exponents, got {e.dtype}")
+    if tuple(e.shape) != (num_kb, rows):
+        raise ValueError(f"{name} must have shape ({num_kb}, {rows}), got {tuple(e.shape)}")
+    return e if e.is_contiguous() else e.contiguous()
+
+
+def _block_gemm(a, e_a, b_hi, b_lo, e_hi, e_lo, block_size, bias, out_dtype):
+    dev = _hip.require_gpu(a, e_a, b_hi, b_lo, e_hi, e_lo, bias)
+    a = _gemm_operand(a, "A")
+    b_hi = _gemm_operand(b_hi, "B_hi")
+    b_lo = _gemm_operand(b_lo, "B_lo") if b_lo is not None else None
+    m, k = a.shape
+    n = b_hi.shape[0]
+    assert k % block_size == 0, f"K ({k}) not divisible by block_size ({block_size})"
+    if block_size not in (32, 64, 128):
+        raise ValueError(f"block_size must be 32, 64, or 128, got {block_size}")
+    num_kb = k // block_size
+    e_a = _block_exps(e_a, m, num_kb, "scales_a")
+    e_hi = _block_exps(e_hi, n, num_kb, "scales_b")
+    e_lo = _block_exps(e_lo, n, num_kb, "scales_lo") if b_lo is not None else None
+    if b_lo is not None and b_hi.stride(0) != b_lo.stride(0):
+        b_hi, b_lo = b_hi.contiguous(), b_lo.contiguous()
+    out = torch.empty((m, n), dtype=out_dtype, device=dev)
+    if bias is not None:
+        bias = bias.to(torch.float32).contiguous()
+        assert bias.shape == (n,), f"bias shape {tuple(bias.shape)} != ({n},)"
+    check(
+        _hip.lib().tcfp_block_dual_gemm(
+            ptr(a), _fmt(a.dtype), a.stride(0), ptr(e_a), ptr(b_hi), ptr(b_lo),
+            _fmt(b_hi.dtype), b_hi.stride(0), ptr(e_hi), ptr(e_lo), m, n, k, block_size,
+            ptr(bias), ptr(out), _out_dtype(out_dtype), n, _hip.stream_of(dev),
+        ),
+        "block_dual_gemm",
+    )
+    return out
+
+
+def block_scaled_gemm(
+    a_fp8: torch.Tensor,
+    b_fp8: torch.Tensor,
+    scales_a: torch.Tensor,
+    scales_b: torch.Tensor,
+    block_size: int = 128,
+    *,
+    out_dtype: torch.dtype = torch.float32,
+) -> torch.Tensor:
+    """``C = sum_kb 2^sa[kb,m] 2^sb[kb,n] (A_kb @ B_kb^T)``, fp32 [M, N].
+
+    Reference: ``block_scaled_gemm`` (``tcfp/kernels.py:1878-1936``).
+    A [M, K], B [N, K] FP8; scales are the int8 exponents
+    ``[K // block_size, rows]`` produced by ``block_quantize_fp8``.  The
+    exponents enter the MFMA as hardware E8M0 block scales.
+    """
+    M, K = a_fp8.shape
+    N, K2 = b_fp8.shape
+    assert K == K2, f"K mismatch: A ({K}) vs B ({K2})"
+    return _block_gemm(a_fp8, scales_a, b_fp8, None, scales_b, None, block_size, None, out_dtype)
+
+
+def fused_block_scaled_dual_gemm_forward(
+    act_fp8: torch.Tensor,
+    w_hi_fp8: torch.Tensor,
+    w_lo_fp8: torch.Tensor,
+    act_scales: torch.Tensor,
+    w_hi_scales: torch.Tensor,
+    w_lo_scales: torch.Tensor,
+    block_size: int,
+    sparse_threshold: float = 0.0,
+    persistent: bool = True,
+    launch_mult: int = 1,
+    *,
+    bias: torch.Tensor | None = None,
+    out_dtype: torch.dtype = torch.float32,
+) -> torch.Tensor:
+    """``sum_kb sa (shi A Whi^T + slo A Wlo^T)`` over K-blocks, fp32 [M, N].
+
+    Reference: ``fused_block_scaled_dual_gemm_forward``
+    (``tcfp/kernels.py:1939-2028``).  W_lo exponents of -128 (zero residual
+    blocks) contribute nothing.  ``sparse_threshold``, ``persistent`` and
+    ``launch_mult`` are scheduling hints of the reference's Triton kernel;
+    they do not change the result and are accepted for API compatibility
+    (the W_lo skip is output-neutral: skipped blocks hold zero codes).
+    """
+    M, K = act_fp8.shape
+    N, K2 = w_hi_fp8.shape
+    assert K == K2 and tuple(w_lo_fp8.shape) == (N, K), (
+        f"Shape mismatch: act({M},{K}), w_hi({N},{K2}), w_lo{tuple(w_lo_fp8.shape)}"
+    )
+    return _block_gemm(act_fp8, act_scales, w_hi_fp8, w_lo_fp8, w_hi_scales, w_lo_scales,
+                       block_size, bias, out_dtype)
+
+
+def set_gemm_tile_policy(policy: str) -> None:
+    """Tuning hook: ``"auto"`` (default), ``"large"`` (256 x 128 tiles) or
+    ``"small"`` (128 x 64 tiles, two workgroups per CU)."""
+    code = {"auto": 0, "large": 1, "small": 2}[policy]
+    check(_hip.lib().tcfp_gemm_set_tile_policy(code), "set_gemm_tile_policy")

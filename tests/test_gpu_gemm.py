@@ -136,3 +136,111 @@ def test_c2_4096_cubed_against_torch_fp32(dev):
     e_dual = ((Wd - w).norm() / w.norm()).item()
     e_hi = ((h.float() * ih - w).norm() / w.norm()).item()
     assert e_dual < e_hi / 8
+
+
+# ------------------------------------------------- tile shapes agree
+@pytest.mark.parametrize("M,K_,N", [(300, 208, 1000), (1024, 1024, 1024), (33, 320, 72)])
+def test_tile_policies_agree_bitwise(dev, M, K_, N):
+    """The 256x128 and 128x64 tiles accumulate each output in the same K
+    order, so their results are identical."""
+    a, sa = make_act((M, K_), 7, dev)
+    h, l, ih, il = make_pair((N, K_), 8, dev)
+    outs = []
+    try:
+        for pol in ("large", "small"):
+            K.set_gemm_tile_policy(pol)
+            outs.append(K.fused_dual_gemm_forward(a, h, l, sa, ih, il))
+            outs.append(K.fp8_gemm_nt(a, h, sa, ih))
+    finally:
+        K.set_gemm_tile_policy("auto")
+    assert torch.equal(outs[0], outs[2]) and torch.equal(outs[1], outs[3])
+
+
+# ------------------------------------------------- block-scaled (a10, a13)
+def make_block_operands(M, N, K_, bs, dev, seed, act_fp8=torch.float8_e4m3fn):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(M, K_, generator=g)
+    # a few rows with very different magnitudes so the exponents vary widely
+    x[: max(1, M // 7)] *= 300.0
+    w = torch.randn(N, K_, generator=g) * 0.02
+    w[:, : bs] *= 1e-3
+    a, ea = K.block_quantize_fp8(x.to(dev), bs, act_fp8)
+    h, l, eh, el = K.fused_dual_quantize_fp8(w.to(dev), bs)
+    return a, ea, h, l, eh, el
+
+
+def npy(t):
+    return t.cpu().numpy()
+
+
+BLOCK_SHAPES = [(64, 128, 64), (256, 512, 256), (300, 256, 1000), (48, 128, 112),
+                (1024, 1024, 1024), (33, 384, 72), (520, 640, 136)]
+
+
+@pytest.mark.parametrize("bs", [32, 64, 128])
+@pytest.mark.parametrize("M,K_,N", BLOCK_SHAPES)
+def test_block_dual_gemm_matches_oracle(dev, bs, M, K_, N):
+    a, ea, h, l, eh, el = make_block_operands(M, N, K_, bs, dev, M + N + bs)
+    out = K.fused_block_scaled_dual_gemm_forward(a, h, l, ea, eh, el, bs)
+    assert out.dtype == torch.float32 and out.shape == (M, N)
+    ref = og.block_dual_gemm_nt(u8(a), npy(ea), u8(h), u8(l), npy(eh), npy(el), bs)
+    err = og.rel_fro(npy(out), ref)
+    print(f"block dual bs={bs} M={M} K={K_} N={N} rel_fro={err:.2e}")
+    assert err < EXACT
+    # the reference's own contract: atol 1e-3 against the dequant matmul
+    # (tests/test_block_scaling_kernels.py:210-240), relative to the scale
+    assert np.abs(npy(out) - ref).max() <= 1e-3 * max(1.0, np.abs(ref).max())
+
+
+@pytest.mark.parametrize("bs", [32, 64, 128])
+def test_block_dual_gemm_zero_residual_sentinel(dev, bs):
+    """W exactly representable in E4M3 per block: every W_lo block carries
+    the -128 sentinel and the dual GEMM equals the single GEMM on W_hi."""
+    M, N, K_ = 128, 192, 4 * bs
+    g = torch.Generator().manual_seed(bs)
+    codes = torch.randint(0, 120, (N, K_), generator=g, dtype=torch.uint8)
+    w = codes.view(torch.float8_e4m3fn).float() * (2.0 ** -3)
+    w[w.abs() > 0] *= torch.where(torch.rand(w[w.abs() > 0].shape, generator=g) > 0.5, 1.0, -1.0)
+    a, ea = K.block_quantize_fp8(torch.randn(M, K_, generator=g).to(dev), bs)
+    h, l, eh, el = K.fused_dual_quantize_fp8(w.to(dev), bs)
+    assert (el == -128).any()
+    out = K.fused_block_scaled_dual_gemm_forward(a, h, l, ea, eh, el, bs)
+    single = K.block_scaled_gemm(a, h, ea, eh, bs)
+    ref = og.block_dual_gemm_nt(u8(a), npy(ea), u8(h), u8(l), npy(eh), npy(el), bs)
+    assert og.rel_fro(npy(out), ref) < EXACT
+    assert og.rel_fro(npy(out), npy(single)) < EXACT
+
+
+@pytest.mark.parametrize("bs", [32, 64, 128])
+@pytest.mark.parametrize("fp8", [torch.float8_e4m3fn, torch.float8_e5m2])
+@pytest.mark.parametrize("M,K_,N", [(256, 256, 256), (300, 384, 1000), (64, 128, 48)])
+def test_block_scaled_single_gemm(dev, bs, fp8, M, K_, N):
+    g = torch.Generator().manual_seed(M + bs)
+    a, ea = K.block_quantize_fp8(torch.randn(M, K_, generator=g).to(dev), bs, fp8)
+    b, eb = K.block_quantize_fp8(torch.randn(N, K_, generator=g).to(dev), bs)
+    out = K.block_scaled_gemm(a, b, ea, eb, bs)
+    afmt = ofp8.E5M2 if fp8 == torch.float8_e5m2 else ofp8.E4M3
+    ref = og.block_deq64(u8(a), npy(ea), bs, afmt) @ og.block_deq64(u8(b), npy(eb), bs).T
+    err = og.rel_fro(npy(out), ref)
+    print(f"block single bs={bs} {fp8} M={M} K={K_} N={N} rel_fro={err:.2e}")
+    assert err < EXACT
+
+
+def test_block_dual_gemm_bf16_out_bias_and_policies(dev):
+    M, N, K_, bs = 384, 512, 512, 64
+    a, ea, h, l, eh, el = make_block_operands(M, N, K_, bs, dev, 99)
+    bias = torch.randn(N, generator=torch.Generator().manual_seed(1)).to(dev)
+    ref = og.block_dual_gemm_nt(u8(a), npy(ea), u8(h), u8(l), npy(eh), npy(el), bs)
+    ref = ref + npy(bias).astype(np.float64)
+    outs = []
+    try:
+        for pol in ("large", "small"):
+            K.set_gemm_tile_policy(pol)
+            outs.append(K.fused_block_scaled_dual_gemm_forward(a, h, l, ea, eh, el, bs, bias=bias))
+    finally:
+        K.set_gemm_tile_policy("auto")
+    assert torch.equal(outs[0], outs[1])
+    assert og.rel_fro(npy(outs[0]), ref) < EXACT
+    ob = K.fused_block_scaled_dual_gemm_forward(a, h, l, ea, eh, el, bs, bias=bias,
+                                                out_dtype=torch.bfloat16)
+    assert og.rel_fro(ob.float().cpu().numpy(), ref) < 1e-2
