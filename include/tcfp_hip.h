@@ -155,6 +155,25 @@ int tcfp_block_dual_gemm(const uint8_t* a, int a_fmt, int64_t lda, const int8_t*
                          int64_t k, int block, const float* bias, void* out, int out_dtype,
                          int64_t ldo, void* stream);
 
+/* Block-scaled dual dgrad:
+ *   dx[i,k] = sum_n 2^eg[n/block,i] G[i,n] * ( 2^ehi[k/block,n] W_hi[n,k]
+ *                                          + 2^elo[k/block,n] W_lo[n,k] )
+ * with g [m, d_out] (E5M2 or E4M3, g_fmt), e_g [d_out/block, m],
+ * w_hi / w_lo [d_out, d_in] E4M3, e_hi / e_lo [d_in/block, d_out];
+ * dx [m, d_in] fp32.  e_lo == -128 marks a zero W_lo block.  w_lo == NULL
+ * uses W_hi alone (ABD).  Replaces fused_block_scaled_dual_gemm_backward_dx
+ * (tcfp/kernels.py:2428-2469, kernel :1051-1205).  The operands are
+ * dequantised exactly into bf16 in `workspace` (G as is, W transposed) and
+ * multiplied on the bf16 MFMA with fp32 accumulation.
+ *   d_out % block == 0, d_in % block == 0; workspace 16-byte aligned and at
+ *   least tcfp_block_dual_gemm_dx_workspace_bytes(m, d_out, d_in) bytes. */
+size_t tcfp_block_dual_gemm_dx_workspace_bytes(int64_t m, int64_t d_out, int64_t d_in);
+int tcfp_block_dual_gemm_dx(const uint8_t* g, int g_fmt, const int8_t* e_g,
+                            const uint8_t* w_hi, const uint8_t* w_lo, const int8_t* e_hi,
+                            const int8_t* e_lo, int64_t m, int64_t d_out, int64_t d_in,
+                            int block, float* dx, void* workspace, size_t workspace_bytes,
+                            void* stream);
+
 /* ---- layout helpers ---------------------------------------------------- */
 
 /* dst[c, r] = src[r, c] for a [rows, cols] byte matrix (ld = cols / rows).

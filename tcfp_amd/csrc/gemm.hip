@@ -343,12 +343,25 @@ TCFP_DEV void interleave_mfma_lds() {
 // map to code 0 = 2^-127).
 TCFP_DEV uint32_t e8m0_of(int e) { return e < -127 ? 0u : uint32_t(e + 127); }
 
+// Operand-format code for bf16 elements (the fp8 codes 0 = E4M3 and
+// 1 = E5M2 double as the MFMA's cbsz / blgp format selectors).
+constexpr int kBF16 = 16;
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef int v4i_ __attribute__((ext_vector_type(4)));
+
+// 16-byte half q of a 32-byte fragment as eight bf16.
+TCFP_DEV bf16x8 bf16_half(const v8i& f, int q) {
+  const v4i_ h = q == 0 ? v4i_{f[0], f[1], f[2], f[3]} : v4i_{f[4], f[5], f[6], f[7]};
+  return __builtin_bit_cast(bf16x8, h);
+}
+
 struct GemmArgs {
   const uint8_t* A;
   const uint8_t* B0;
   const uint8_t* B1;
-  int M, N, K;
-  int64_t lda, ldb;
+  int M, N, K;       // K and the leading dimensions count bytes of an
+  int64_t lda, ldb;  // operand row: elements for fp8, 2 x elements for bf16
   const float* s_a;  // per-tensor scalars (SCALE 0)
   const float* s_0;
   const float* s_1;
@@ -536,7 +549,13 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 ? 2 : 1)) void gemm_nt_dma_kernel
 #pragma unroll
       for (int q = 0; q < NF; ++q) {
         v16f& c = acc[(q / NB) % NACC][q % NB][i];
-        if constexpr (SCALE == 1) {
+        if constexpr (AF == kBF16) {
+          // a fragment holds 16 bf16 K values: two K=16 MFMAs
+          c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bf16_half(f[q], 0), bf16_half(f[NF + i], 0),
+                                                      c, 0, 0, 0);
+          c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bf16_half(f[q], 1), bf16_half(f[NF + i], 1),
+                                                      c, 0, 0, 0);
+        } else if constexpr (SCALE == 1) {
           c = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
               f[q], f[NF + i], c, BF, AF, 0, int(sc[2 * q + h]), 0, int(sc[2 * (NF + i) + h]));
         } else {
@@ -546,7 +565,9 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 ? 2 : 1)) void gemm_nt_dma_kernel
       }
   };
   // NF*MB MFMAs and 2*(NF+MB) LDS reads per sub-step: spread the reads evenly
-  auto interleave = [&]() { interleave_mfma_lds<NF * MB, 2 * (NF + MB), 0>(); };
+  auto interleave = [&]() {
+    interleave_mfma_lds<NF * MB * (AF == kBF16 ? 2 : 1), 2 * (NF + MB), 0>();
+  };
   // All DMA issued so far has landed and every wave's LDS reads are done
   // (gfx9 s_waitcnt: vmcnt bits [3:0] and [15:14], expcnt [6:4], lgkmcnt [11:8]).
   // sched_barrier(0) keeps the scheduler from moving MFMAs across it: MFMAs
@@ -608,7 +629,7 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 ? 2 : 1)) void gemm_nt_dma_kernel
   static_assert(NW * TMW * RB <= 2 * STAGE, "epilogue staging must fit the operand buffers");
   uint8_t* eps = lds + wave * (TMW * RB);    // this wave's staging region
   float c0s = 1.0f, c1s = 1.0f;
-  if constexpr (SCALE == 0) {
+  if (SCALE == 0 && g.s_a) {
     const float sa = *g.s_a;
     c0s = sa * *g.s_0;
     c1s = SPLIT ? c0s : sa * *g.s_1;
@@ -712,8 +733,8 @@ int launch_gemm(GemmArgs ga, hipStream_t st) {
       gemm_nt_dma_kernel<AF, BF, SPLIT, OutT, 8, 256, 128, SCALE><<<grid, 512, 0, st>>>(ga);
     return hipGetLastError() == hipSuccess ? TCFP_OK : TCFP_ERR_HIP;
   }
-  if constexpr (SCALE != 0) {
-    return TCFP_ERR_SHAPE;  // block-scaled GEMMs need spans the DMA path covers
+  if constexpr (SCALE != 0 || AF == kBF16) {
+    return TCFP_ERR_SHAPE;  // block-scaled and bf16 GEMMs need spans the DMA path covers
   } else {
     const int tiles_m = (m + kBM - 1) / kBM;
     const int tn_w = SPLIT ? 2 * kBN : kBN;
@@ -815,4 +836,150 @@ extern "C" int tcfp_gemm_set_tile_policy(int policy) {
   if (policy < 0 || policy > 2) return TCFP_ERR_SHAPE;
   g_tile_policy = policy;
   return TCFP_OK;
+}
+
+// ===========================================================================
+// Block-scaled dgrad (reference fused_block_scaled_dual_gemm_backward_dx)
+// ===========================================================================
+//
+// dX[m, k] = sum_n deq(G)[m, n] * (deq(W_hi)[n, k] + deq(W_lo)[n, k]) where the
+// W exponents vary per (k-block, n): along the contraction index n they
+// change every element, which no per-32-K MFMA scale can express.  Every
+// dequantised operand value fp8 * 2^e is exactly representable in bf16, so
+// the operands are dequantised once into bf16 (G as is, W transposed to
+// [D_in, D_out] so the contraction is contiguous) and multiplied on the
+// bf16 MFMA with fp32 accumulation: every product is exact, which is at
+// least as accurate as the reference's dequantise-then-tf32 dot.
+namespace {
+
+// out[r, c] = bf16(q[r, c] * 2^e[c / bs, r]); 8 elements per thread
+// (one block, since bs >= 32 and c % 8 == 0).
+template <int FMT>
+__global__ __launch_bounds__(256) void dequant_rows_bf16_kernel(
+    const uint8_t* __restrict__ q, const int8_t* __restrict__ e, int64_t rows, int64_t cols,
+    int bs_shift, int zero_sentinel, uint16_t* __restrict__ out) {
+  const int64_t nvec = rows * cols / 8;
+  const int64_t stride = int64_t(gridDim.x) * 256;
+  for (int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x; i < nvec; i += stride) {
+    const int64_t r = (i * 8) / cols, c = (i * 8) - r * cols;
+    const int ex = e[(c >> bs_shift) * rows + r];
+    const float sc = (zero_sentinel && ex == -128) ? 0.0f : exp2i(ex);
+    const uint2 w = *reinterpret_cast<const uint2*>(q + i * 8);
+    uint32_t o[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t word = j < 2 ? w.x : w.y;
+      const float a = fp8_to_f32<FMT>((word >> (16 * (j & 1))) & 0xFFu) * sc;
+      const float b = fp8_to_f32<FMT>((word >> (16 * (j & 1) + 8)) & 0xFFu) * sc;
+      o[j] = uint32_t(f32_to_bf16_rne(a)) | (uint32_t(f32_to_bf16_rne(b)) << 16);
+    }
+    *reinterpret_cast<uint4*>(out + i * 8) = make_uint4(o[0], o[1], o[2], o[3]);
+  }
+}
+
+// out[c, r] = bf16(q[r, c] * 2^e[c / bs, r]) through a 64 x 64 LDS tile.
+template <int FMT>
+__global__ __launch_bounds__(256) void dequant_t_bf16_kernel(
+    const uint8_t* __restrict__ q, const int8_t* __restrict__ e, int64_t rows, int64_t cols,
+    int bs_shift, int zero_sentinel, uint16_t* __restrict__ out) {
+  __shared__ uint16_t tile[64][64 + 2];
+  const int tiles_c = int((cols + 63) / 64);
+  const int64_t r0 = int64_t(blockIdx.x / tiles_c) * 64, c0 = int64_t(blockIdx.x % tiles_c) * 64;
+  const int t = threadIdx.x;
+  {
+    const int lr = t >> 2, lc = (t & 3) * 16;
+    const int64_t r = r0 + lr;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int64_t c = c0 + lc + j;
+      uint16_t v = 0;
+      if (r < rows && c < cols) {
+        const int ex = e[(c >> bs_shift) * rows + r];
+        const float sc = (zero_sentinel && ex == -128) ? 0.0f : exp2i(ex);
+        v = f32_to_bf16_rne(fp8_to_f32<FMT>(q[r * cols + c]) * sc);
+      }
+      tile[lc + j][lr] = v;
+    }
+  }
+  __syncthreads();
+  {
+    const int lc = t >> 2, lr = (t & 3) * 16;
+    const int64_t c = c0 + lc;
+    if (c < cols) {
+      uint16_t* o = out + c * rows + r0 + lr;
+      if ((rows % 8) == 0 && r0 + lr + 16 <= rows) {
+        uint32_t w[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          w[j] = uint32_t(tile[lc][lr + 2 * j]) | (uint32_t(tile[lc][lr + 2 * j + 1]) << 16);
+        reinterpret_cast<uint4*>(o)[0] = make_uint4(w[0], w[1], w[2], w[3]);
+        reinterpret_cast<uint4*>(o)[1] = make_uint4(w[4], w[5], w[6], w[7]);
+      } else {
+        for (int j = 0; j < 16; ++j)
+          if (r0 + lr + j < rows) o[j] = tile[lc][lr + j];
+      }
+    }
+  }
+}
+
+size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
+
+}  // namespace
+
+extern "C" size_t tcfp_block_dual_gemm_dx_workspace_bytes(int64_t m, int64_t d_out, int64_t d_in) {
+  if (m < 0 || d_out < 0 || d_in < 0) return 0;
+  return align256(size_t(m) * size_t(d_out) * 2) + 2 * align256(size_t(d_in) * size_t(d_out) * 2);
+}
+
+extern "C" int tcfp_block_dual_gemm_dx(const uint8_t* g, int g_fmt, const int8_t* e_g,
+                                       const uint8_t* w_hi, const uint8_t* w_lo,
+                                       const int8_t* e_hi, const int8_t* e_lo, int64_t m,
+                                       int64_t d_out, int64_t d_in, int block, float* dx,
+                                       void* workspace, size_t workspace_bytes, void* stream) {
+  if (m < 0 || d_out < 0 || d_in < 0 || m > INT32_MAX || d_in > INT32_MAX ||
+      2 * d_out > INT32_MAX)
+    return TCFP_ERR_SHAPE;
+  if (block != 32 && block != 64 && block != 128) return TCFP_ERR_SHAPE;
+  if (d_out % block != 0 || d_in % block != 0) return TCFP_ERR_SHAPE;
+  if (g_fmt != TCFP_FP8_E4M3 && g_fmt != TCFP_FP8_E5M2) return TCFP_ERR_DTYPE;
+  if (!g || !e_g || !w_hi || !e_hi || (w_lo && !e_lo) || !dx) return TCFP_ERR_SHAPE;
+  if (m == 0 || d_in == 0) return TCFP_OK;
+  if (!workspace || workspace_bytes < tcfp_block_dual_gemm_dx_workspace_bytes(m, d_out, d_in))
+    return TCFP_ERR_WORKSPACE;
+  if (!al16(workspace) || !al16(dx)) return TCFP_ERR_ALIGN;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int shift = block == 32 ? 5 : (block == 64 ? 6 : 7);
+  uint8_t* ws = static_cast<uint8_t*>(workspace);
+  uint16_t* gd = reinterpret_cast<uint16_t*>(ws);
+  uint16_t* wth = reinterpret_cast<uint16_t*>(ws + align256(size_t(m) * size_t(d_out) * 2));
+  uint16_t* wtl = reinterpret_cast<uint16_t*>(reinterpret_cast<uint8_t*>(wth) +
+                                              align256(size_t(d_in) * size_t(d_out) * 2));
+  // dequantised operands
+  {
+    const int64_t nvec = m * d_out / 8;
+    int64_t gr = (nvec + 255) / 256;
+    gr = gr > int64_t(num_cus()) * 8 ? int64_t(num_cus()) * 8 : (gr < 1 ? 1 : gr);
+    if (g_fmt == TCFP_FP8_E5M2)
+      dequant_rows_bf16_kernel<TCFP_FP8_E5M2><<<unsigned(gr), 256, 0, st>>>(g, e_g, m, d_out, shift, 0, gd);
+    else
+      dequant_rows_bf16_kernel<TCFP_FP8_E4M3><<<unsigned(gr), 256, 0, st>>>(g, e_g, m, d_out, shift, 0, gd);
+    const int64_t tiles = ((d_out + 63) / 64) * ((d_in + 63) / 64);
+    if (tiles > INT32_MAX) return TCFP_ERR_SHAPE;
+    dequant_t_bf16_kernel<TCFP_FP8_E4M3><<<unsigned(tiles), 256, 0, st>>>(w_hi, e_hi, d_out, d_in,
+                                                                           shift, 0, wth);
+    if (w_lo)
+      dequant_t_bf16_kernel<TCFP_FP8_E4M3><<<unsigned(tiles), 256, 0, st>>>(w_lo, e_lo, d_out,
+                                                                             d_in, shift, 1, wtl);
+    if (hipGetLastError() != hipSuccess) return TCFP_ERR_HIP;
+  }
+  // bf16 dual GEMM: A = G [m, d_out], B = W^T [d_in, d_out]; K counts bytes
+  GemmArgs ga{};
+  ga.A = reinterpret_cast<const uint8_t*>(gd);
+  ga.B0 = reinterpret_cast<const uint8_t*>(wth);
+  ga.B1 = reinterpret_cast<const uint8_t*>(w_lo ? wtl : wth);
+  ga.M = int(m); ga.N = int(d_in); ga.K = int(2 * d_out);
+  ga.lda = 2 * d_out; ga.ldb = 2 * d_out;
+  ga.out = dx; ga.ldo = d_in;
+  if (w_lo) return launch_gemm<kBF16, kBF16, false, float, 0>(ga, st);
+  return launch_gemm<kBF16, kBF16, true, float, 0>(ga, st);
 }

@@ -494,6 +494,57 @@ def fused_block_scaled_dual_gemm_forward(
                        block_size, bias, out_dtype)
 
 
+def fused_block_scaled_dual_gemm_backward_dx(
+    grad_fp8: torch.Tensor,
+    w_hi_fp8: torch.Tensor,
+    w_lo_fp8: torch.Tensor | None,
+    grad_scales: torch.Tensor,
+    w_hi_scales: torch.Tensor,
+    w_lo_scales: torch.Tensor | None,
+    block_size: int,
+) -> torch.Tensor:
+    """``dX = deq(grad) @ (deq(W_hi) + deq(W_lo))``, fp32 [M, D_in].
+
+    Reference: ``fused_block_scaled_dual_gemm_backward_dx``
+    (``tcfp/kernels.py:2428-2469``, kernel ``:1051-1205``).  grad [M, D_out]
+    (E5M2 or E4M3) with exponents [D_out // bs, M]; W [D_out, D_in] E4M3
+    with exponents [D_in // bs, D_out].  The W exponents change along the
+    contraction index, so the operands are dequantised exactly into bf16
+    and multiplied on the bf16 MFMA (fp32 accumulation); ``w_lo_fp8=None``
+    (ABD) uses W_hi alone.
+    """
+    M, D_out = grad_fp8.shape
+    D_out2, D_in = w_hi_fp8.shape
+    assert D_out == D_out2, f"Shape mismatch: grad({M},{D_out}), w_hi({D_out2},{D_in})"
+    if w_lo_fp8 is not None:
+        assert tuple(w_lo_fp8.shape) == (D_out, D_in), "w_lo shape mismatch"
+    assert D_out % block_size == 0, f"D_out ({D_out}) not divisible by block_size ({block_size})"
+    assert D_in % block_size == 0, f"D_in ({D_in}) not divisible by block_size ({block_size})"
+    if block_size not in (32, 64, 128):
+        raise ValueError(f"block_size must be 32, 64, or 128, got {block_size}")
+    dev = _hip.require_gpu(grad_fp8, w_hi_fp8, w_lo_fp8, grad_scales, w_hi_scales, w_lo_scales)
+    g = grad_fp8.contiguous()
+    wh = w_hi_fp8.contiguous()
+    wl = w_lo_fp8.contiguous() if w_lo_fp8 is not None else None
+    eg = _block_exps(grad_scales, M, D_out // block_size, "grad_scales")
+    eh = _block_exps(w_hi_scales, D_out, D_in // block_size, "w_hi_scales")
+    el = (_block_exps(w_lo_scales, D_out, D_in // block_size, "w_lo_scales")
+          if wl is not None else None)
+    if wh.dtype != torch.float8_e4m3fn or (wl is not None and wl.dtype != torch.float8_e4m3fn):
+        raise TypeError("W_hi / W_lo must be float8_e4m3fn")
+    out = torch.empty((M, D_in), dtype=torch.float32, device=dev)
+    nbytes = int(_hip.lib().tcfp_block_dual_gemm_dx_workspace_bytes(M, D_out, D_in))
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
+    check(
+        _hip.lib().tcfp_block_dual_gemm_dx(
+            ptr(g), _fmt(g.dtype), ptr(eg), ptr(wh), ptr(wl), ptr(eh), ptr(el), M, D_out, D_in,
+            block_size, ptr(out), ptr(ws), nbytes, _hip.stream_of(dev),
+        ),
+        "block_dual_gemm_dx",
+    )
+    return out
+
+
 def set_gemm_tile_policy(policy: str) -> None:
     """Tuning hook: ``"auto"`` (default), ``"large"`` (256 x 128 tiles) or
     ``"small"`` (128 x 64 tiles, two workgroups per CU)."""

@@ -244,3 +244,28 @@ def test_block_dual_gemm_bf16_out_bias_and_policies(dev):
     ob = K.fused_block_scaled_dual_gemm_forward(a, h, l, ea, eh, el, bs, bias=bias,
                                                 out_dtype=torch.bfloat16)
     assert og.rel_fro(ob.float().cpu().numpy(), ref) < 1e-2
+
+
+# ------------------------------------------------- block dgrad (a12)
+@pytest.mark.parametrize("bs", [32, 64, 128])
+@pytest.mark.parametrize("M,D_out,D_in", [(64, 128, 256), (300, 256, 384), (1024, 512, 1024),
+                                          (33, 384, 128)])
+def test_block_dgrad_matches_oracle(dev, bs, M, D_out, D_in):
+    g = torch.Generator().manual_seed(M + D_out + bs)
+    grad = torch.randn(M, D_out, generator=g) * 1e-3
+    grad[: max(1, M // 9)] *= 1e4
+    w = torch.randn(D_out, D_in, generator=g) * 0.02
+    gq, eg = K.block_quantize_fp8(grad.to(dev), bs, torch.float8_e5m2)
+    h, l, eh, el = K.fused_dual_quantize_fp8(w.to(dev), bs)
+    dx = K.fused_block_scaled_dual_gemm_backward_dx(gq, h, l, eg, eh, el, bs)
+    assert dx.dtype == torch.float32 and dx.shape == (M, D_in)
+    ref = og.block_dgrad(u8(gq), npy(eg), u8(h), u8(l), npy(eh), npy(el), bs, "e5m2")
+    err = og.rel_fro(npy(dx), ref)
+    print(f"block dgrad bs={bs} M={M} D_out={D_out} D_in={D_in} rel_fro={err:.2e}")
+    # exact bf16 operands, fp32 accumulation
+    assert err < EXACT
+    # ABD: W_hi only
+    dxa = K.fused_block_scaled_dual_gemm_backward_dx(gq, h, None, eg, eh, None, bs)
+    Gd = og.block_deq64(u8(gq), npy(eg), bs, "e5m2")
+    refa = Gd @ og.block_deq64(u8(h), npy(eh), bs)
+    assert og.rel_fro(npy(dxa), refa) < EXACT

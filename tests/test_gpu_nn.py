@@ -143,3 +143,40 @@ def test_tiny_mlp_converges(dev):
         opt.step()
         first = first if first is not None else loss.item()
     assert loss.item() < 0.5 * first
+
+
+# ------------------------------------------------ block-scaled path (a3, a4, a10, a12, a14)
+@pytest.mark.parametrize("bs", [32, 64, 128])
+@pytest.mark.parametrize("hp", [False, True])
+def test_block_scaled_layer_matches_oracle(dev, bs, hp):
+    M, Kd, N = 256, 512, 384
+    lin = _layer(dev, Kd, N, scale_block_size=bs, hp_grad_weight=hp)
+    g = torch.Generator().manual_seed(bs)
+    x = torch.randn(M, Kd, generator=g)
+    xd = x.to(dev).requires_grad_(True)
+    out = lin(xd)
+    assert out.dtype == torch.float32 and out.shape == (M, N)
+    gout = torch.randn(M, N, generator=g) * 1e-2
+    out.backward(gout.to(dev))
+    W = lin.weight.detach().cpu().numpy()
+    hi, lo, eh, el, ef_new = oq.block_dual_quantize(W, bs, np.zeros_like(W))
+    aq, ea = oq.block_quantize(x.numpy(), bs)
+    ref = og.block_dual_gemm_nt(aq, ea, hi, lo, eh, el, bs) + lin.bias.detach().cpu().double().numpy()
+    assert og.rel_fro(out.detach().cpu().numpy(), ref) < 1e-4
+    assert np.array_equal(lin._error_state._buffers[""].cpu().numpy(), ef_new)
+    gq, eg = oq.block_quantize(gout.numpy(), bs, ofp8.E5M2)
+    dx_ref = og.block_dgrad(gq, eg, hi, lo, eh, el, bs, "e5m2")
+    assert og.rel_fro(xd.grad.cpu().numpy(), dx_ref) < 1e-4
+    A = x.numpy().astype(np.float64) if hp else og.block_deq64(aq, ea, bs)
+    dw_ref = gout.numpy().astype(np.float64).T @ A
+    assert og.rel_fro(lin.weight.grad.cpu().numpy(), dw_ref) < 1e-4
+    np.testing.assert_allclose(lin.bias.grad.cpu().numpy(), gout.sum(0).numpy(), rtol=1e-4, atol=1e-4)
+
+
+def test_block_scaled_srr_and_abd(dev):
+    lin = _layer(dev, 256, 256, scale_block_size=64, srr=True, abd=True)
+    assert lin._error_state is None
+    x = torch.randn(128, 256, device=dev, requires_grad=True)
+    y = lin(x)
+    y.square().mean().backward()
+    assert torch.isfinite(x.grad).all() and torch.isfinite(lin.weight.grad).all()
