@@ -1,6 +1,6 @@
 """Benchmark of the TCFP-12 hot path on one MI355X.
 
-    python bench.py [--steps K] [--warmup W] [--gpus 1] [--skip-extras]
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--part all|gemm|quant|block|mlp|copy]
 
 Headline (BASELINE.json ``metric``, configs[1]): the fused dual-FP8 GEMM
 ``out = X W_hi^T s_x s_hi + X W_lo^T s_x s_lo`` at M = N = K = 4096,
@@ -36,9 +36,15 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def event_time_ms(fn, iters, stream):
+def event_time_ms(fn, iters, stream, warmup=3):
+    """Average time per call of ``fn`` over ``iters`` calls, from HIP events
+    on ``stream`` (the stream the kernels are launched on), after
+    ``warmup`` untimed calls (the first launch of a kernel also loads its
+    code object)."""
     import torch
 
+    for _ in range(warmup):
+        fn()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     start.record(stream)
@@ -128,6 +134,48 @@ def bench_comparators(t, iters=20):
     return res
 
 
+def bench_block_gemms(iters=20):
+    """block-scaled dual GEMM at 4096^3, bs 32/64/128 (int8
+    power-of-two exponents, the reference's block format), plus the single
+    block-scaled GEMM at bs 64.  fp32 out, as the reference's kernels."""
+    import torch
+
+    from tcfp_amd import kernels as K
+
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream(dev)
+    n = 4096
+    x = torch.randn(n, n, generator=torch.Generator().manual_seed(0)).bfloat16().to(dev)
+    w = torch.randn(n, n, generator=torch.Generator().manual_seed(1)).to(dev)
+    res = {}
+    for bs in (32, 64, 128):
+        a, ea = K.block_quantize_fp8(x, bs)
+        h, l, eh, el = K.fused_dual_quantize_fp8(w, bs)
+        ms = event_time_ms(
+            lambda: K.fused_block_scaled_dual_gemm_forward(a, h, l, ea, eh, el, bs), iters, stream)
+        res[f"block{bs}_dual_ms"] = ms
+        res[f"block{bs}_dual_tflops"] = 4 * n**3 / (ms * 1e-3) / 1e12
+        if bs == 64:
+            ms = event_time_ms(lambda: K.block_scaled_gemm(a, h, ea, eh, bs), iters, stream)
+            res["block64_single_ms"] = ms
+            res["block64_single_tflops"] = 2 * n**3 / (ms * 1e-3) / 1e12
+    return res
+
+
+def bench_copy(steps):
+    """Calibration workload for the PMC traffic counters: a plain device
+    copy of 256 MiB (256 MiB read + 256 MiB written per launch)."""
+    import torch
+
+    dev = torch.device("cuda:0")
+    src = torch.empty(256 << 20, dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(steps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    return {"copy_bytes_each_way": 256 << 20, "launches": steps}
+
+
 def bench_dual_quant(iters=20):
     import torch
 
@@ -161,7 +209,7 @@ def bench_dual_quant(iters=20):
     return out
 
 
-def bench_mlp(steps=100, time_iters=20):
+def bench_mlp(steps=100, time_iters=20, arms=("tcfp", "bf16")):
     """1024 -> 4096 -> 1024 GELU MLP, 8192 tokens, MSE, AdamW 1e-3."""
     import torch
     import torch.nn as nn
@@ -201,16 +249,20 @@ def bench_mlp(steps=100, time_iters=20):
             losses.append(step())
         torch.cuda.synchronize()
         ms = event_time_ms(step, time_iters, torch.cuda.current_stream(dev))
-        return [float(v) for v in torch.stack(losses).cpu()], ms
+        return [float(v) for v in torch.stack(losses).detach().cpu()], ms
 
-    l_t, ms_t = run(True)
-    l_b, ms_b = run(False)
-    return {
-        "tcfp_step_ms": ms_t, "bf16_autocast_step_ms": ms_b, "speedup_vs_bf16": ms_b / ms_t,
-        "loss_step1_tcfp": l_t[0], "loss_step100_tcfp": l_t[-1],
-        "loss_step100_bf16": l_b[-1], "loss_rel_diff_step100": abs(l_t[-1] - l_b[-1]) / l_b[-1],
-        "steps": steps,
-    }
+    res = {"steps": steps}
+    if "tcfp" in arms:
+        l_t, ms_t = run(True)
+        res.update({"tcfp_step_ms": ms_t, "loss_step1_tcfp": l_t[0],
+                    f"loss_step{steps}_tcfp": l_t[-1]})
+    if "bf16" in arms:
+        l_b, ms_b = run(False)
+        res.update({"bf16_autocast_step_ms": ms_b, f"loss_step{steps}_bf16": l_b[-1]})
+    if "tcfp" in arms and "bf16" in arms:
+        res["speedup_vs_bf16"] = ms_b / ms_t
+        res[f"loss_rel_diff_step{steps}"] = abs(l_t[-1] - l_b[-1]) / l_b[-1]
+    return res
 
 
 def cpu_baseline(t):
@@ -259,9 +311,16 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--skip-extras", action="store_true",
-                    help="only the headline dual GEMM (no comparators, MLP, CPU baseline)")
+    ap.add_argument("--part", choices=("all", "gemm", "quant", "block", "mlp", "copy"),
+                    default="all",
+                    help="all (default) = headline + every secondary figure; the others run "
+                         "one workload (for profiling)")
+    ap.add_argument("--arm", choices=("both", "tcfp", "bf16"), default="both",
+                    help="--part mlp: which model(s) to run")
+    ap.add_argument("--skip-extras", action="store_true", help="same as --part gemm")
     args = ap.parse_args()
+    if args.skip_extras:
+        args.part = "gemm"
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU only (the TCFP-12 path has no "
               "multi-GPU component); run with --gpus 1", file=sys.stderr)
@@ -270,15 +329,24 @@ def main():
     import torch
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
+    if args.part != "all" and args.part != "gemm":
+        fn = {"quant": lambda: bench_dual_quant(), "block": lambda: bench_block_gemms(),
+              "mlp": lambda: bench_mlp(
+                  steps=args.steps, arms=("tcfp", "bf16") if args.arm == "both" else (args.arm,)), "copy": lambda: bench_copy(args.steps)}
+        log(f"[bench] part {args.part}")
+        print(json.dumps({"part": args.part, **fn[args.part]()}), flush=True)
+        return
     log(f"[bench] dual GEMM 4096^3: warmup {args.warmup}, steps {args.steps}")
     r = bench_dual_gemm(args.steps, args.warmup)
     log(f"[bench] dual GEMM: {r['tflops_wall']:.1f} TFLOP/s wall, {r['tflops_kern']:.1f} "
         f"TFLOP/s events, rel_fro {r['rel_fro']:.2e}")
     extras = {}
     cpu = None
-    if not args.skip_extras:
+    if args.part == "all":
         log("[bench] comparators")
         extras["comparators_4096"] = bench_comparators(r["tensors"])
+        log("[bench] block-scaled GEMMs (configs[2])")
+        extras["block_scaled_4096"] = bench_block_gemms()
         log("[bench] dual quant")
         extras["quant_kernels"] = bench_dual_quant()
         log("[bench] MLP train step (configs[3])")
