@@ -1,6 +1,6 @@
 """Benchmark of the TCFP-12 hot path on one MI355X.
 
-    python bench.py [--steps K] [--warmup W] [--gpus 1] [--part all|gemm|quant|block|mlp|copy]
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--part all|gemm|quant|block|mlp|c5|copy]
 
 Headline (BASELINE.json ``metric``, configs[1]): the fused dual-FP8 GEMM
 ``out = X W_hi^T s_x s_hi + X W_lo^T s_x s_lo`` at M = N = K = 4096,
@@ -265,6 +265,141 @@ def bench_mlp(steps=100, time_iters=20, arms=("tcfp", "bf16")):
     return res
 
 
+def _tiny_gpt(vocab=256, d=256, layers=4, heads=4, ffn=1024, seq=128):
+    """configs[4] model: decoder-only transformer (pre-LN, GELU FFN, tied
+    head), the architecture of the reference's TinyGPT
+    (examples/train_convergence.py:192-260) at BASELINE's vocab of 256.
+    Attention runs in float32 with contiguous operands in both arms."""
+    import torch
+    import torch.nn as nn
+    import torch.nn.functional as F
+
+    class Attn(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.h, self.dh = heads, d // heads
+            self.qkv = nn.Linear(d, 3 * d)
+            self.proj = nn.Linear(d, d)
+
+        def forward(self, x):
+            B, T, C = x.shape
+            qkv = self.qkv(x).float().reshape(B, T, 3, self.h, self.dh)
+            q, k, v = (t.transpose(1, 2).contiguous() for t in qkv.unbind(2))
+            with torch.autocast("cuda", enabled=False):
+                att = torch.matmul(q, k.transpose(-2, -1).contiguous()) / self.dh**0.5
+                mask = torch.triu(torch.ones(T, T, device=x.device, dtype=torch.bool), 1)
+                att = F.softmax(att.masked_fill(mask, float("-inf")), dim=-1)
+                y = torch.matmul(att, v).transpose(1, 2).reshape(B, T, C).contiguous()
+            return self.proj(y)
+
+    class Block(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.ln1, self.ln2 = nn.LayerNorm(d), nn.LayerNorm(d)
+            self.attn = Attn()
+            self.ffn = nn.Sequential(nn.Linear(d, ffn), nn.GELU(), nn.Linear(ffn, d))
+
+        def forward(self, x):
+            x = x + self.attn(self.ln1(x))
+            return x + self.ffn(self.ln2(x))
+
+    class TinyGPT(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.tok = nn.Embedding(vocab, d)
+            self.pos = nn.Embedding(seq, d)
+            self.blocks = nn.ModuleList([Block() for _ in range(layers)])
+            self.ln_f = nn.LayerNorm(d)
+            self.head = nn.Linear(d, vocab, bias=False)
+            self.head.weight = self.tok.weight
+            for m in self.modules():
+                if isinstance(m, nn.Linear):
+                    nn.init.normal_(m.weight, std=0.02)
+                    if m.bias is not None:
+                        nn.init.zeros_(m.bias)
+                elif isinstance(m, nn.Embedding):
+                    nn.init.normal_(m.weight, std=0.02)
+
+        def forward(self, idx):
+            T = idx.shape[1]
+            x = self.tok(idx) + self.pos(torch.arange(T, device=idx.device))
+            for b in self.blocks:
+                x = b(x)
+            return self.head(self.ln_f(x).float())
+
+    return TinyGPT()
+
+
+def bench_c5(steps=50, time_iters=10):
+    """TinyGPT (d 256, 4 layers, 4 heads, FFN 1024, vocab 256,
+    seq 128, batch 32) with every QKV/O/FFN linear TCFP-12 block-64 + SRR,
+    against BF16 autocast; and the 4096 -> 16384 -> 4096 scale-up layer at
+    8192 tokens (peak memory and fwd+bwd time: block-64 SRR, block-64 EF,
+    BF16)."""
+    import torch
+    import torch.nn as nn
+    import torch.nn.functional as F
+
+    from tcfp_amd.nn import convert_to_tcfp
+
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream(dev)
+    g = torch.Generator().manual_seed(0)
+    data = torch.randint(0, 256, (steps + time_iters + 3, 32, 129), generator=g).to(dev)
+    res = {}
+    for arm in ("tcfp_block64_srr", "bf16"):
+        torch.manual_seed(1)
+        model = _tiny_gpt().to(dev)
+        if arm != "bf16":
+            convert_to_tcfp(model, use_tensor_cores=True, scale_block_size=64, srr=True,
+                            skip_patterns=("head",))
+        opt = torch.optim.AdamW(model.parameters(), lr=3e-4, weight_decay=0.01)
+        it = iter(range(data.shape[0]))
+
+        def step():
+            b = data[next(it)]
+            with torch.autocast("cuda", dtype=torch.bfloat16, enabled=(arm == "bf16")):
+                logits = model(b[:, :-1])
+            loss = F.cross_entropy(logits.float().reshape(-1, 256), b[:, 1:].reshape(-1))
+            opt.zero_grad(set_to_none=True)
+            loss.backward()
+            opt.step()
+            return loss
+
+        losses = [step() for _ in range(steps)]
+        ms = event_time_ms(step, time_iters, stream, warmup=0)
+        lv = [float(v) for v in torch.stack(losses).detach().cpu()]
+        res[arm] = {"step_ms": ms, "loss_first": lv[0], "loss_last": lv[-1], "steps": steps}
+    res["loss_rel_diff_last"] = (abs(res["tcfp_block64_srr"]["loss_last"] - res["bf16"]["loss_last"])
+                                 / res["bf16"]["loss_last"])
+    # scale-up layer
+    x = torch.randn(8192, 4096, generator=g).bfloat16().to(dev)
+    for arm, kw in (("block64_srr", dict(scale_block_size=64, srr=True)),
+                    ("block64_ef", dict(scale_block_size=64)), ("bf16", None)):
+        torch.manual_seed(2)
+        m = nn.Sequential(nn.Linear(4096, 16384), nn.GELU(), nn.Linear(16384, 4096)).to(dev)
+        if kw is not None:
+            convert_to_tcfp(m, use_tensor_cores=True, **kw)
+        xx = x.clone().requires_grad_(False)
+
+        def fb():
+            with torch.autocast("cuda", dtype=torch.bfloat16, enabled=kw is None):
+                y = m(xx)
+            y.float().square().mean().backward()
+
+        fb()
+        torch.cuda.synchronize()
+        torch.cuda.reset_peak_memory_stats(dev)
+        base = torch.cuda.memory_allocated(dev)
+        ms = event_time_ms(fb, 5, stream, warmup=1)
+        peak = torch.cuda.max_memory_allocated(dev)
+        res[f"scaleup_{arm}"] = {"fwd_bwd_ms": ms, "peak_mem_MB": peak / 1e6,
+                                 "resident_MB": base / 1e6}
+        del m
+        torch.cuda.empty_cache()
+    return res
+
+
 def cpu_baseline(t):
     """The numpy oracle (float64 dequant matmul) on a row sample of C2."""
     import numpy as np
@@ -311,7 +446,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--part", choices=("all", "gemm", "quant", "block", "mlp", "copy"),
+    ap.add_argument("--part", choices=("all", "gemm", "quant", "block", "mlp", "c5", "copy"),
                     default="all",
                     help="all (default) = headline + every secondary figure; the others run "
                          "one workload (for profiling)")
@@ -331,6 +466,7 @@ def main():
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     if args.part != "all" and args.part != "gemm":
         fn = {"quant": lambda: bench_dual_quant(), "block": lambda: bench_block_gemms(),
+              "c5": lambda: bench_c5(),
               "mlp": lambda: bench_mlp(
                   steps=args.steps, arms=("tcfp", "bf16") if args.arm == "both" else (args.arm,)), "copy": lambda: bench_copy(args.steps)}
         log(f"[bench] part {args.part}")
@@ -351,6 +487,8 @@ def main():
         extras["quant_kernels"] = bench_dual_quant()
         log("[bench] MLP train step (configs[3])")
         extras["mlp_train_step"] = bench_mlp()
+        log("[bench] TinyGPT + scale-up layer (configs[4])")
+        extras["c5"] = bench_c5()
         log("[bench] CPU baseline")
         cpu = cpu_baseline(r["tensors"])
     achieved = r["tflops_kern"]

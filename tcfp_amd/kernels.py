@@ -494,6 +494,47 @@ def fused_block_scaled_dual_gemm_forward(
                        block_size, bias, out_dtype)
 
 
+def fused_act_quant_dual_gemm_forward(
+    act: torch.Tensor,
+    w_hi_fp8: torch.Tensor,
+    w_lo_fp8: torch.Tensor,
+    w_hi_scales: torch.Tensor,
+    w_lo_scales: torch.Tensor,
+    block_size: int,
+    sparse_threshold: float = 0.0,
+    persistent: bool = True,
+    launch_mult: int = 1,
+    save_side_outputs: bool = True,
+    *,
+    bias: torch.Tensor | None = None,
+) -> tuple[torch.Tensor, torch.Tensor | None, torch.Tensor | None]:
+    """Activation block-quantisation + block-scaled dual GEMM.
+
+    Reference: ``fused_act_quant_dual_gemm_forward`` (``tcfp/kernels.py:
+    2031-2149``, kernel ``:826-1041``).  ``act`` [M, K] bf16/fp32 is
+    quantised per (row, K-block) to E4M3 with the ``block_quantize_fp8``
+    exponent rule, then multiplied with W_hi/W_lo as
+    ``fused_block_scaled_dual_gemm_forward``.  Returns ``(out fp32 [M, N],
+    act_fp8, act_scales)`` -- the side outputs are bitwise what
+    ``block_quantize_fp8`` returns -- or ``(out, None, None)`` when
+    ``save_side_outputs`` is False.  Runs as two HIP launches (block
+    quantisation, then the GEMM with the exponents in the MFMA's scale
+    operands).
+    """
+    M, K = act.shape
+    N, K2 = w_hi_fp8.shape
+    assert K == K2 and tuple(w_lo_fp8.shape) == (N, K), (
+        f"Shape mismatch: act({M},{K}), w_hi({N},{K2}), w_lo{tuple(w_lo_fp8.shape)}"
+    )
+    assert K % block_size == 0, f"K ({K}) must be divisible by block_size ({block_size})"
+    act_fp8, act_scales = block_quantize_fp8(act, block_size)
+    out = _block_gemm(act_fp8, act_scales, w_hi_fp8, w_lo_fp8, w_hi_scales, w_lo_scales,
+                      block_size, bias, torch.float32)
+    if save_side_outputs:
+        return out, act_fp8, act_scales
+    return out, None, None
+
+
 def fused_block_scaled_dual_gemm_backward_dx(
     grad_fp8: torch.Tensor,
     w_hi_fp8: torch.Tensor,

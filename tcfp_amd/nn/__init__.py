@@ -196,10 +196,17 @@ class _TCFP12BlockScaledFunction(torch.autograd.Function):
         )
         input_shape = input.shape
         input_2d = _flatten(input)
-        act_fp8, act_scales = K.block_quantize_fp8(input_2d, block_size=bs)
-        out_2d = K.fused_block_scaled_dual_gemm_forward(
-            act_fp8, w_hi, w_lo, act_scales, sh, sl, block_size=bs, bias=bias
-        )
+        # the reference's dispatch (tcfp/nn/__init__.py:617-650): the fused
+        # act-quant entry point for narrow layers, separate quant otherwise
+        if (w.shape[0] + 127) // 128 <= 4:
+            out_2d, act_fp8, act_scales = K.fused_act_quant_dual_gemm_forward(
+                input_2d, w_hi, w_lo, sh, sl, block_size=bs, bias=bias
+            )
+        else:
+            act_fp8, act_scales = K.block_quantize_fp8(input_2d, block_size=bs)
+            out_2d = K.fused_block_scaled_dual_gemm_forward(
+                act_fp8, w_hi, w_lo, act_scales, sh, sl, block_size=bs, bias=bias
+            )
         output = out_2d.reshape(*input_shape[:-1], out_2d.shape[-1])
 
         ctx.hp_grad_weight = hp_grad_weight

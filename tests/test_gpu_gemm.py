@@ -269,3 +269,27 @@ def test_block_dgrad_matches_oracle(dev, bs, M, D_out, D_in):
     Gd = og.block_deq64(u8(gq), npy(eg), bs, "e5m2")
     refa = Gd @ og.block_deq64(u8(h), npy(eh), bs)
     assert og.rel_fro(npy(dxa), refa) < EXACT
+
+
+# ------------------------------------------------- fused act-quant (a11)
+@pytest.mark.parametrize("bs", [32, 64, 128])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_fused_act_quant_dual_gemm(dev, bs, dtype):
+    """Side outputs bitwise equal to block_quantize_fp8 and the output equal
+    to quant + block dual GEMM (reference tests/test_fused_act_quant_gemm.py
+    :86-144)."""
+    M, N, K_ = 300, 256, 4 * bs
+    g = torch.Generator().manual_seed(bs)
+    x = (torch.randn(M, K_, generator=g) * 3).to(dtype).to(dev)
+    w = torch.randn(N, K_, generator=g) * 0.02
+    h, l, eh, el = K.fused_dual_quantize_fp8(w.to(dev), bs)
+    out, aq, ea = K.fused_act_quant_dual_gemm_forward(x, h, l, eh, el, bs)
+    aq2, ea2 = K.block_quantize_fp8(x, bs)
+    assert torch.equal(aq.view(torch.uint8), aq2.view(torch.uint8)) and torch.equal(ea, ea2)
+    codes, exps = oq.block_quantize(x.float().cpu().numpy(), bs)
+    assert np.array_equal(u8(aq), codes) and np.array_equal(npy(ea), exps)
+    ref = og.block_dual_gemm_nt(codes, exps, u8(h), u8(l), npy(eh), npy(el), bs)
+    assert og.rel_fro(npy(out), ref) < EXACT
+    out2, none1, none2 = K.fused_act_quant_dual_gemm_forward(x, h, l, eh, el, bs,
+                                                             save_side_outputs=False)
+    assert none1 is None and none2 is None and torch.equal(out, out2)
