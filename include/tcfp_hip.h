@@ -174,6 +174,22 @@ int tcfp_block_dual_gemm_dx(const uint8_t* g, int g_fmt, const int8_t* e_g,
                             int block, float* dx, void* workspace, size_t workspace_bytes,
                             void* stream);
 
+/* Block-path weight gradient with an fp32 gradient:
+ *   dw[n, k] = sum_i g[i, n] * 2^ex[k/block, i] * x[i, k]
+ * g [m, n_out] fp32, x [m, k_in] fp8 (x_fmt) with exponents [k_in/block, m],
+ * dw [n_out, k_in] fp32.  Replaces the reference's fp32
+ * `grad_2d.t() @ block_dequantize_fp8(act)` (tcfp/nn/__init__.py:743-750).
+ * The dequantised activation is exact in bf16 and g is split into
+ * g_hi = bf16(g), g_lo = bf16(g - g_hi) (relative representation error
+ * <= 2^-17); both products run as one bf16-MFMA GEMM over the
+ * concatenated contraction [g_hi | g_lo] x [x | x] with fp32 accumulation.
+ *   m % 4 == 0; k_in % block == 0; workspace 16-byte aligned and at least
+ *   tcfp_block_wgrad_workspace_bytes(m, n_out, k_in) bytes. */
+size_t tcfp_block_wgrad_workspace_bytes(int64_t m, int64_t n_out, int64_t k_in);
+int tcfp_block_wgrad(const float* g, int64_t m, int64_t n_out, const uint8_t* x, int x_fmt,
+                     const int8_t* e_x, int64_t k_in, int block, float* dw, void* workspace,
+                     size_t workspace_bytes, void* stream);
+
 /* ---- layout helpers ---------------------------------------------------- */
 
 /* dst[c, r] = src[r, c] for a [rows, cols] byte matrix (ld = cols / rows).

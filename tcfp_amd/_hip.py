@@ -49,6 +49,9 @@ _SIGNATURES = {
                                 _c_void_p, _i64, _i64, _i64, _i32, _c_void_p, _c_void_p,
                                 ctypes.c_size_t, _c_void_p],
     "tcfp_block_dual_gemm_dx_workspace_bytes": [_i64, _i64, _i64],
+    "tcfp_block_wgrad": [_c_void_p, _i64, _i64, _c_void_p, _i32, _c_void_p, _i64, _i32, _c_void_p,
+                         _c_void_p, ctypes.c_size_t, _c_void_p],
+    "tcfp_block_wgrad_workspace_bytes": [_i64, _i64, _i64],
     "tcfp_gemm_set_tile_policy": [_i32],
     "tcfp_transpose_u8": [_c_void_p, _i64, _i64, _c_void_p, _c_void_p],
     "tcfp_selftest_fp8_cvt": [_u32, _u32, _i32, _c_void_p, _c_void_p],
@@ -58,6 +61,7 @@ _RESTYPE = {
     "tcfp_status_string": ctypes.c_char_p,
     "tcfp_workspace_bytes": ctypes.c_size_t,
     "tcfp_block_dual_gemm_dx_workspace_bytes": ctypes.c_size_t,
+    "tcfp_block_wgrad_workspace_bytes": ctypes.c_size_t,
 }
 
 _lib = None

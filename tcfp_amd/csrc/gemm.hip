@@ -924,6 +924,102 @@ __global__ __launch_bounds__(256) void dequant_t_bf16_kernel(
 
 size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
 
+// ---- block wgrad operands ------------------------------------------------
+// dW[n, k] = sum_m g[m, n] * deq(x)[m, k] with fp32 g.  g is split into
+// g_hi = bf16(g) and g_lo = bf16(g - g_hi) (together ~16 significant bits,
+// relative error <= 2^-17), the dequantised activation is exact in bf16,
+// and the two products are one bf16 GEMM over the concatenated contraction:
+//   A' = [g_hi^T | g_lo^T]  [N, 2M],   B' = [x^T | x^T]  [K, 2M].
+
+// A'[c, r] = hi(g[r, c]), A'[c, M + r] = lo(g[r, c]); g [rows, cols] fp32.
+__global__ __launch_bounds__(256) void split_t_bf16_kernel(const float* __restrict__ g,
+                                                           int64_t rows, int64_t cols,
+                                                           uint16_t* __restrict__ out) {
+  __shared__ float tile[64][64 + 1];
+  const int tiles_c = int((cols + 63) / 64);
+  const int64_t r0 = int64_t(blockIdx.x / tiles_c) * 64, c0 = int64_t(blockIdx.x % tiles_c) * 64;
+  const int t = threadIdx.x;
+  {
+    const int lr = t >> 2, lc = (t & 3) * 16;
+    const int64_t r = r0 + lr;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int64_t c = c0 + lc + j;
+      tile[lc + j][lr] = (r < rows && c < cols) ? g[r * cols + c] : 0.0f;
+    }
+  }
+  __syncthreads();
+  const int lc = t >> 2, lr = (t & 3) * 16;
+  const int64_t c = c0 + lc;
+  if (c >= cols) return;
+  uint16_t hi[16], lo[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const float v = tile[lc][lr + j];
+    hi[j] = f32_to_bf16_rne(v);
+    lo[j] = f32_to_bf16_rne(__fsub_rn(v, bf16_to_f32(hi[j])));
+  }
+  uint16_t* oh = out + c * (2 * rows) + r0 + lr;
+  uint16_t* ol = oh + rows;
+  if ((rows % 8) == 0 && r0 + lr + 16 <= rows) {
+    uint32_t wh[8], wl[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      wh[j] = uint32_t(hi[2 * j]) | (uint32_t(hi[2 * j + 1]) << 16);
+      wl[j] = uint32_t(lo[2 * j]) | (uint32_t(lo[2 * j + 1]) << 16);
+    }
+    reinterpret_cast<uint4*>(oh)[0] = make_uint4(wh[0], wh[1], wh[2], wh[3]);
+    reinterpret_cast<uint4*>(oh)[1] = make_uint4(wh[4], wh[5], wh[6], wh[7]);
+    reinterpret_cast<uint4*>(ol)[0] = make_uint4(wl[0], wl[1], wl[2], wl[3]);
+    reinterpret_cast<uint4*>(ol)[1] = make_uint4(wl[4], wl[5], wl[6], wl[7]);
+  } else {
+    for (int j = 0; j < 16; ++j)
+      if (r0 + lr + j < rows) { oh[j] = hi[j]; ol[j] = lo[j]; }
+  }
+}
+
+// B'[c, r] = B'[c, M + r] = bf16(q[r, c] * 2^e[c / bs, r]) (exact).
+template <int FMT>
+__global__ __launch_bounds__(256) void dequant_t_dup_bf16_kernel(
+    const uint8_t* __restrict__ q, const int8_t* __restrict__ e, int64_t rows, int64_t cols,
+    int bs_shift, uint16_t* __restrict__ out) {
+  __shared__ uint16_t tile[64][64 + 2];
+  const int tiles_c = int((cols + 63) / 64);
+  const int64_t r0 = int64_t(blockIdx.x / tiles_c) * 64, c0 = int64_t(blockIdx.x % tiles_c) * 64;
+  const int t = threadIdx.x;
+  {
+    const int lr = t >> 2, lc = (t & 3) * 16;
+    const int64_t r = r0 + lr;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int64_t c = c0 + lc + j;
+      uint16_t v = 0;
+      if (r < rows && c < cols)
+        v = f32_to_bf16_rne(fp8_to_f32<FMT>(q[r * cols + c]) * exp2i(e[(c >> bs_shift) * rows + r]));
+      tile[lc + j][lr] = v;
+    }
+  }
+  __syncthreads();
+  const int lc = t >> 2, lr = (t & 3) * 16;
+  const int64_t c = c0 + lc;
+  if (c >= cols) return;
+  uint16_t* o0 = out + c * (2 * rows) + r0 + lr;
+  uint16_t* o1 = o0 + rows;
+  if ((rows % 8) == 0 && r0 + lr + 16 <= rows) {
+    uint32_t w[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      w[j] = uint32_t(tile[lc][lr + 2 * j]) | (uint32_t(tile[lc][lr + 2 * j + 1]) << 16);
+    reinterpret_cast<uint4*>(o0)[0] = make_uint4(w[0], w[1], w[2], w[3]);
+    reinterpret_cast<uint4*>(o0)[1] = make_uint4(w[4], w[5], w[6], w[7]);
+    reinterpret_cast<uint4*>(o1)[0] = make_uint4(w[0], w[1], w[2], w[3]);
+    reinterpret_cast<uint4*>(o1)[1] = make_uint4(w[4], w[5], w[6], w[7]);
+  } else {
+    for (int j = 0; j < 16; ++j)
+      if (r0 + lr + j < rows) { o0[j] = tile[lc][lr + j]; o1[j] = tile[lc][lr + j]; }
+  }
+}
+
 }  // namespace
 
 extern "C" size_t tcfp_block_dual_gemm_dx_workspace_bytes(int64_t m, int64_t d_out, int64_t d_in) {
@@ -981,5 +1077,52 @@ extern "C" int tcfp_block_dual_gemm_dx(const uint8_t* g, int g_fmt, const int8_t
   ga.lda = 2 * d_out; ga.ldb = 2 * d_out;
   ga.out = dx; ga.ldo = d_in;
   if (w_lo) return launch_gemm<kBF16, kBF16, false, float, 0>(ga, st);
+  return launch_gemm<kBF16, kBF16, true, float, 0>(ga, st);
+}
+
+extern "C" size_t tcfp_block_wgrad_workspace_bytes(int64_t m, int64_t n_out, int64_t k_in) {
+  if (m < 0 || n_out < 0 || k_in < 0) return 0;
+  return align256(size_t(n_out) * size_t(2 * m) * 2) + align256(size_t(k_in) * size_t(2 * m) * 2);
+}
+
+extern "C" int tcfp_block_wgrad(const float* g, int64_t m, int64_t n_out, const uint8_t* x,
+                                int x_fmt, const int8_t* e_x, int64_t k_in, int block, float* dw,
+                                void* workspace, size_t workspace_bytes, void* stream) {
+  if (m < 0 || n_out < 0 || k_in < 0 || n_out > INT32_MAX || k_in > INT32_MAX ||
+      4 * m > INT32_MAX)
+    return TCFP_ERR_SHAPE;
+  if (block != 32 && block != 64 && block != 128) return TCFP_ERR_SHAPE;
+  if (k_in % block != 0 || m % 4 != 0) return TCFP_ERR_SHAPE;
+  if (x_fmt != TCFP_FP8_E4M3 && x_fmt != TCFP_FP8_E5M2) return TCFP_ERR_DTYPE;
+  if (!g || !x || !e_x || !dw) return TCFP_ERR_SHAPE;
+  if (n_out == 0 || k_in == 0) return TCFP_OK;
+  if (!workspace || workspace_bytes < tcfp_block_wgrad_workspace_bytes(m, n_out, k_in))
+    return TCFP_ERR_WORKSPACE;
+  if (!al16(workspace) || !al16(dw)) return TCFP_ERR_ALIGN;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int shift = block == 32 ? 5 : (block == 64 ? 6 : 7);
+  uint8_t* ws = static_cast<uint8_t*>(workspace);
+  uint16_t* ap = reinterpret_cast<uint16_t*>(ws);
+  uint16_t* bp = reinterpret_cast<uint16_t*>(ws + align256(size_t(n_out) * size_t(2 * m) * 2));
+  if (m == 0) {
+    // empty contraction: dW = 0, through the GEMM with K = 0 below
+  } else {
+    const int64_t tg = ((m + 63) / 64) * ((n_out + 63) / 64);
+    const int64_t tx = ((m + 63) / 64) * ((k_in + 63) / 64);
+    if (tg > INT32_MAX || tx > INT32_MAX) return TCFP_ERR_SHAPE;
+    split_t_bf16_kernel<<<unsigned(tg), 256, 0, st>>>(g, m, n_out, ap);
+    if (x_fmt == TCFP_FP8_E5M2)
+      dequant_t_dup_bf16_kernel<TCFP_FP8_E5M2><<<unsigned(tx), 256, 0, st>>>(x, e_x, m, k_in, shift, bp);
+    else
+      dequant_t_dup_bf16_kernel<TCFP_FP8_E4M3><<<unsigned(tx), 256, 0, st>>>(x, e_x, m, k_in, shift, bp);
+    if (hipGetLastError() != hipSuccess) return TCFP_ERR_HIP;
+  }
+  GemmArgs ga{};
+  ga.A = reinterpret_cast<const uint8_t*>(ap);
+  ga.B0 = reinterpret_cast<const uint8_t*>(bp);
+  ga.B1 = ga.B0;
+  ga.M = int(n_out); ga.N = int(k_in); ga.K = int(4 * m);  // bytes of 2M bf16
+  ga.lda = 4 * m; ga.ldb = 4 * m;
+  ga.out = dw; ga.ldo = k_in;
   return launch_gemm<kBF16, kBF16, true, float, 0>(ga, st);
 }

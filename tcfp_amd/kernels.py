@@ -586,6 +586,44 @@ def fused_block_scaled_dual_gemm_backward_dx(
     return out
 
 
+def block_scaled_wgrad(
+    grad: torch.Tensor,
+    act_fp8: torch.Tensor,
+    act_scales: torch.Tensor,
+    block_size: int,
+) -> torch.Tensor:
+    """``grad.t() @ block_dequantize_fp8(act)`` in fp32 accuracy, [N, K].
+
+    The block path's weight gradient (reference ``tcfp/nn/__init__.py:
+    743-750``, an fp32 matmul there).  grad [M, N] (fp32; other dtypes are
+    promoted), act [M, K] FP8 with exponents [K // block_size, M].  The
+    fp32 gradient is split into two bf16 parts and both products run as one
+    bf16-MFMA GEMM; every product is exact and the split's relative
+    representation error is at most 2^-17.  Token counts that are not a
+    multiple of 4 use the dequantise + fp32 matmul form.
+    """
+    M, N = grad.shape
+    M2, Kd = act_fp8.shape
+    assert M == M2, f"token mismatch: grad {tuple(grad.shape)} vs act {tuple(act_fp8.shape)}"
+    dev = _hip.require_gpu(grad, act_fp8, act_scales)
+    g = grad.float().contiguous()
+    if M % 4 != 0:
+        return g.t() @ block_dequantize_fp8(act_fp8, act_scales, block_size)
+    a = act_fp8.contiguous()
+    e = _block_exps(act_scales, M, Kd // block_size, "act_scales")
+    out = torch.empty((N, Kd), dtype=torch.float32, device=dev)
+    nbytes = int(_hip.lib().tcfp_block_wgrad_workspace_bytes(M, N, Kd))
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
+    check(
+        _hip.lib().tcfp_block_wgrad(
+            ptr(g), M, N, ptr(a), _fmt(a.dtype), ptr(e), Kd, block_size, ptr(out), ptr(ws),
+            nbytes, _hip.stream_of(dev),
+        ),
+        "block_wgrad",
+    )
+    return out
+
+
 def set_gemm_tile_policy(policy: str) -> None:
     """Tuning hook: ``"auto"`` (default), ``"large"`` (256 x 128 tiles) or
     ``"small"`` (128 x 64 tiles, two workgroups per CU)."""

@@ -238,10 +238,10 @@ class _TCFP12BlockScaledFunction(torch.autograd.Function):
             ).reshape(ctx.input_shape)
         if need_dw:
             if ctx.hp_grad_weight:
-                act_f = saved_act.to(grad_2d.dtype)
+                grad_weight = grad_2d.t() @ saved_act.to(grad_2d.dtype)
             else:
-                act_f = K.block_dequantize_fp8(saved_act, act_scales, bs).to(grad_2d.dtype)
-            grad_weight = grad_2d.t() @ act_f
+                grad_weight = K.block_scaled_wgrad(grad_2d, saved_act, act_scales, bs)
+                grad_weight = grad_weight.to(grad_2d.dtype)
         if need_db and ctx.has_bias:
             grad_bias = grad_2d.sum(dim=0)
         return (grad_input, grad_weight, grad_bias) + (None,) * 7

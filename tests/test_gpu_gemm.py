@@ -293,3 +293,20 @@ def test_fused_act_quant_dual_gemm(dev, bs, dtype):
     out2, none1, none2 = K.fused_act_quant_dual_gemm_forward(x, h, l, eh, el, bs,
                                                              save_side_outputs=False)
     assert none1 is None and none2 is None and torch.equal(out, out2)
+
+
+# ------------------------------------------------- block wgrad (a14)
+@pytest.mark.parametrize("bs", [32, 64, 128])
+@pytest.mark.parametrize("M,N,K_", [(256, 384, 512), (1024, 256, 1024), (300, 128, 256),
+                                    (8, 64, 128), (302, 64, 128)])
+def test_block_wgrad_fp32_accuracy(dev, bs, M, N, K_):
+    g = torch.Generator().manual_seed(M + N + bs)
+    grad = torch.randn(M, N, generator=g) * 1e-3
+    x = torch.randn(M, K_, generator=g)
+    aq, ea = K.block_quantize_fp8(x.to(dev), bs)
+    dw = K.block_scaled_wgrad(grad.to(dev), aq, ea, bs)
+    assert dw.dtype == torch.float32 and dw.shape == (N, K_)
+    ref = grad.numpy().astype(np.float64).T @ og.block_deq64(u8(aq), npy(ea), bs)
+    err = og.rel_fro(npy(dw), ref)
+    print(f"block wgrad bs={bs} M={M} N={N} K={K_} rel_fro={err:.2e}")
+    assert err < 2e-5  # fp32-level: split-bf16 representation error <= 2^-17
