@@ -73,6 +73,21 @@ int tcfp_quantize_per_tensor(const void* x, int x_dtype, int64_t rows, int64_t c
                              float* scale_out, float* inv_out, void* workspace,
                              void* stream);
 
+/* Per-tensor quantisation that also returns the column sums of x
+ * (col_sum [cols] fp32 = sum over rows), read in the same pass as the
+ * amax.  For the gradient this is the bias gradient the reference computes
+ * separately as grad_2d.sum(0) (tcfp/nn/__init__.py:558) next to the E5M2
+ * quantisation at :494.  Scale rule as tcfp_quantize_per_tensor (no
+ * explicit scale).  cols % 8 == 0; colsum_ws holds
+ * tcfp_colsum_workspace_bytes(rows, cols) bytes of scratch (16-byte
+ * aligned).  The sums are fp32 in a fixed order (per-row-group partials,
+ * then their sum). */
+size_t tcfp_colsum_workspace_bytes(int64_t rows, int64_t cols);
+int tcfp_quantize_per_tensor_colsum(const void* x, int x_dtype, int64_t rows, int64_t cols,
+                                    int fp8_fmt, uint8_t* q, uint8_t* q_t, float* inv_out,
+                                    float* col_sum, void* workspace, void* colsum_ws,
+                                    size_t colsum_ws_bytes, void* stream);
+
 /* Per-tensor dual quantisation with optional error feedback.
  * Replaces the body of _TCFP12TensorCoreFunction.forward that builds
  * W_hi/W_lo (tcfp/nn/__init__.py:343-383, with ErrorFeedbackState

@@ -31,6 +31,10 @@ _SIGNATURES = {
     "tcfp_workspace_bytes": [],
     "tcfp_quantize_per_tensor": [_c_void_p, _i32, _i64, _i64, _i32, _c_void_p, _c_void_p,
                                  _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p],
+    "tcfp_colsum_workspace_bytes": [_i64, _i64],
+    "tcfp_quantize_per_tensor_colsum": [_c_void_p, _i32, _i64, _i64, _i32, _c_void_p, _c_void_p,
+                                        _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+                                        ctypes.c_size_t, _c_void_p],
     "tcfp_dual_quantize_per_tensor": [_c_void_p, _i32, _i64, _i64, _c_void_p, _i32, _i32, _u64,
                                       _u64, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                                       _c_void_p, _c_void_p, _c_void_p, _c_void_p],
@@ -60,6 +64,7 @@ _SIGNATURES = {
 _RESTYPE = {
     "tcfp_status_string": ctypes.c_char_p,
     "tcfp_workspace_bytes": ctypes.c_size_t,
+    "tcfp_colsum_workspace_bytes": ctypes.c_size_t,
     "tcfp_block_dual_gemm_dx_workspace_bytes": ctypes.c_size_t,
     "tcfp_block_wgrad_workspace_bytes": ctypes.c_size_t,
 }

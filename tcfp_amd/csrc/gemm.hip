@@ -375,8 +375,12 @@ struct GemmArgs {
   int tiles_m, tiles_n;
 };
 
-template <int AF, int BF, bool SPLIT, typename OutT, int NW, int BM, int BN, int SCALE>
-__global__ __launch_bounds__(NW * 64, (NW == 4 ? 2 : 1)) void gemm_nt_dma_kernel(GemmArgs g) {
+// NS = LDS stages in flight (2, or 4 for the small tile when one
+// workgroup per CU is resident): the DMA of stage t + NS is issued once
+// every wave has read stage t, so it has NS - 1 stages of MFMA time to land.
+template <int AF, int BF, bool SPLIT, typename OutT, int NW, int BM, int BN, int SCALE, int NS>
+__global__ __launch_bounds__(NW * 64, (NW == 4 && NS == 2 ? 2 : 1)) void gemm_nt_dma_kernel(
+    GemmArgs g) {
   constexpr int WM = NW / 2;        // wave rows
   constexpr int TMW = BM / WM;      // activation rows per wave
   constexpr int MB = TMW / 32;      // 32-row m-blocks per wave
@@ -389,7 +393,8 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 ? 2 : 1)) void gemm_nt_dma_kernel
   constexpr int DI = RPW / 8;       // 1 KiB DMA instructions per wave and stage
   static_assert(RPW % 16 == 0 && BM % RPW == 0 && BN % RPW == 0, "DMA rows must tile regions");
   static_assert(MB >= 1 && NB >= 1, "tile too small for the wave grid");
-  __shared__ __align__(16) uint8_t lds[2 * STAGE];
+  static_assert(NS == 2 || (NS == 4 && SCALE == 0), "deep pipelines carry no exponent loads");
+  __shared__ __align__(16) uint8_t lds[NS * STAGE];
 
   const int M = g.M, N = g.N, K = g.K;
   OutT* __restrict__ out = static_cast<OutT*>(g.out);
@@ -452,7 +457,7 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 ? 2 : 1)) void gemm_nt_dma_kernel
   // end are issued as all-out-of-range loads (zeros into a buffer nobody
   // reads again), so the issue stays branch-free.
   auto issue = [&](int t) {
-    const uint32_t dst = lds_base + uint32_t(t & 1) * STAGE;
+    const uint32_t dst = lds_base + uint32_t(t & (NS - 1)) * STAGE;
     const bool live = t < nt;
     const uint32_t soff = uint32_t(live ? t : 0) * kSK;
     const bool last = t == nt - 1;
@@ -530,7 +535,7 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 ? 2 : 1)) void gemm_nt_dma_kernel
   // Fragments of sub-step h of stage t: [0, NF) weights (slot, n-block),
   // [NF, NF + MB) activations (m-block).
   auto read_frags = [&](v8i* f, int t, int h) {
-    const uint8_t* st = lds + (t & 1) * STAGE;
+    const uint8_t* st = lds + (t & (NS - 1)) * STAGE;
 #pragma unroll
     for (int q = 0; q < NF; ++q) {
       const int rb = (BM + (q / NB) * BN + wn * TNW + (q % NB) * 32) * kRowB;
@@ -573,9 +578,12 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 ? 2 : 1)) void gemm_nt_dma_kernel
   // sched_barrier(0) keeps the scheduler from moving MFMAs across it: MFMAs
   // touch no memory, so without it they drift past the barrier and the LDS
   // reads before it are left with nothing to hide behind.
+  // With NS stages, the DMAs of stages t+2 .. t+NS-1 may stay in flight.
+  constexpr int kInflight = (NS - 2) * DI;
   auto sync_all = [&]() {
     __builtin_amdgcn_sched_barrier(0);
-    __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0), expcnt untouched
+    // vmcnt(kInflight) lgkmcnt(0), expcnt untouched
+    __builtin_amdgcn_s_waitcnt((kInflight & 15) | (7 << 4) | ((kInflight >> 4) << 14));
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
@@ -586,19 +594,19 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 ? 2 : 1)) void gemm_nt_dma_kernel
   int raw[2 * (NF + MB)];   // exponents of the next stage, in flight
   if (nt > 0) {
     load_raw(raw, 0);
-    issue(0);
-    if (nt > 1) issue(1);
-    // wait for stage 0 only: stage 1's DI loads may stay in flight (the
-    // exponent loads were issued before both and are complete too)
-    if (nt > 1) __builtin_amdgcn_s_waitcnt((DI & 15) | (7 << 4) | ((DI >> 4) << 14));
-    else __builtin_amdgcn_s_waitcnt(0x0070);
+#pragma unroll
+    for (int s = 0; s < NS; ++s) issue(s);
+    // wait for stage 0 only: the DMAs of stages 1 .. NS-1 may stay in flight
+    // (the exponent loads were issued before all of them and are complete)
+    constexpr int kPro = (NS - 1) * DI;
+    __builtin_amdgcn_s_waitcnt((kPro & 15) | (7 << 4) | ((kPro >> 4) << 14));
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
     pack(sc, raw);
     read_frags(f0, 0, 0);
   }
   for (int t = 0; t < nt; ++t) {
-    // exponents of stage t + 1: the vmcnt(0) of this stage's barrier covers them
+    // exponents of stage t + 1 (SCALE 1, NS 2): this stage's vmcnt(0) covers them
     load_raw(raw, t + 1);
     __builtin_amdgcn_sched_barrier(0);
     // sub-step 0 of stage t; fragments of sub-step 1 stream in
@@ -607,7 +615,7 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 ? 2 : 1)) void gemm_nt_dma_kernel
     interleave();
     // stage t + 1 landed, every wave has its stage-t fragments: refill t's buffer
     sync_all();
-    issue(t + 2);
+    issue(t + NS);
     __builtin_amdgcn_sched_barrier(0);
     // sub-step 1 of stage t; fragments of stage t + 1 sub-step 0 stream in
     // (after the last stage they read a stale buffer and are never used)
@@ -626,7 +634,7 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 ? 2 : 1)) void gemm_nt_dma_kernel
   constexpr int RB = TNW * EB;               // bytes of one staged tile row
   constexpr int CPR = RB / 16;               // 16-byte chunks per row
   constexpr int RPI = 64 / CPR;              // rows per store instruction
-  static_assert(NW * TMW * RB <= 2 * STAGE, "epilogue staging must fit the operand buffers");
+  static_assert(NW * TMW * RB <= NS * STAGE, "epilogue staging must fit the operand buffers");
   uint8_t* eps = lds + wave * (TMW * RB);    // this wave's staging region
   float c0s = 1.0f, c1s = 1.0f;
   if (SCALE == 0 && g.s_a) {
@@ -694,7 +702,8 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 ? 2 : 1)) void gemm_nt_dma_kernel
 // the out-of-range sentinel must stay beyond every span).
 constexpr int64_t kMaxSpan = (int64_t(1) << 31) - (int64_t(1) << 20);
 
-// Tile policy: 0 = automatic, 1 = always 256 x 128, 2 = always 128 x 64.
+// Tile policy: 0 = automatic, 1 = always 256 x 128, 2 = always 128 x 64,
+// 3 = 128 x 64 with eight waves in the one-round deep-pipeline case.
 int g_tile_policy = 0;
 
 int num_cus() {
@@ -718,7 +727,7 @@ int launch_gemm(GemmArgs ga, hipStream_t st) {
   const int big_tiles = ((m + 255) / 256) * ((n + (SPLIT ? 255 : 127)) / (SPLIT ? 256 : 128));
   // (block-scaled single GEMMs keep two accumulator sets, which only the
   // small tile fits in registers)
-  const bool small = (SCALE == 1 && SPLIT) || g_tile_policy == 2 ||
+  const bool small = (SCALE == 1 && SPLIT) || g_tile_policy >= 2 ||
                      (g_tile_policy == 0 && big_tiles < num_cus());
   const int BMv = small ? 128 : 256, BNv = small ? 64 : 128;
   ga.tiles_m = (m + BMv - 1) / BMv;
@@ -727,10 +736,21 @@ int launch_gemm(GemmArgs ga, hipStream_t st) {
                       (ga.bias == nullptr || (reinterpret_cast<uintptr_t>(ga.bias) & 15) == 0);
   if (dma_ok) {
     const unsigned grid = unsigned(ga.tiles_m) * unsigned(ga.tiles_n);
-    if (small)
-      gemm_nt_dma_kernel<AF, BF, SPLIT, OutT, 4, 128, 64, SCALE><<<grid, 256, 0, st>>>(ga);
-    else if constexpr (!(SCALE == 1 && SPLIT))
-      gemm_nt_dma_kernel<AF, BF, SPLIT, OutT, 8, 256, 128, SCALE><<<grid, 512, 0, st>>>(ga);
+    // a small-tile launch that fits in one round gets the 4-stage pipeline
+    // (one workgroup per CU, 128 KiB of LDS)
+    const bool deep = SCALE == 0 && small && int(grid) <= num_cus();
+    if (small && deep) {
+      if constexpr (SCALE == 0) {
+        if (g_tile_policy == 3)
+          gemm_nt_dma_kernel<AF, BF, SPLIT, OutT, 8, 128, 64, SCALE, 4><<<grid, 512, 0, st>>>(ga);
+        else
+          gemm_nt_dma_kernel<AF, BF, SPLIT, OutT, 4, 128, 64, SCALE, 4><<<grid, 256, 0, st>>>(ga);
+      }
+    } else if (small) {
+      gemm_nt_dma_kernel<AF, BF, SPLIT, OutT, 4, 128, 64, SCALE, 2><<<grid, 256, 0, st>>>(ga);
+    } else if constexpr (!(SCALE == 1 && SPLIT)) {
+      gemm_nt_dma_kernel<AF, BF, SPLIT, OutT, 8, 256, 128, SCALE, 2><<<grid, 512, 0, st>>>(ga);
+    }
     return hipGetLastError() == hipSuccess ? TCFP_OK : TCFP_ERR_HIP;
   }
   if constexpr (SCALE != 0 || AF == kBF16) {
@@ -833,7 +853,7 @@ extern "C" int tcfp_block_dual_gemm(const uint8_t* a, int a_fmt, int64_t lda, co
 }
 
 extern "C" int tcfp_gemm_set_tile_policy(int policy) {
-  if (policy < 0 || policy > 2) return TCFP_ERR_SHAPE;
+  if (policy < 0 || policy > 3) return TCFP_ERR_SHAPE;
   g_tile_policy = policy;
   return TCFP_OK;
 }

@@ -237,6 +237,119 @@ __global__ __launch_bounds__(kThreads) void amax_part_kernel(const InT* __restri
   if (threadIdx.x == 0) part[blockIdx.x] = m;
 }
 
+// ---- amax + column sums (the bias gradient) in one pass ------------------
+// Geometry for x [rows, cols], cols % 8 == 0: a workgroup covers NVW
+// 8-column vectors (a power of two <= 256) with RL = 256 / NVW row lanes,
+// over one group of consecutive rows; it writes the partial max and the
+// partial column sums of its row group to cs_part[rg, cols].
+struct ColsumGeom {
+  int nvw, rl, cb_count, rg_count, rpg;
+};
+
+constexpr int kMaxRowGroups = 256;
+
+inline ColsumGeom colsum_geom(int64_t rows, int64_t cols) {
+  ColsumGeom g;
+  const int64_t nv = cols / 8;
+  int nvw = 1;
+  while (nvw * 2 <= 256 && nvw * 2 <= nv) nvw *= 2;
+  g.nvw = nvw;
+  g.rl = 256 / nvw;
+  g.cb_count = int((nv + nvw - 1) / nvw);
+  int64_t rg = (rows + 4 * g.rl - 1) / (4 * g.rl);  // >= 4 rows per lane
+  const int64_t cap = std::min<int64_t>(kMaxRowGroups, kMaxParts / g.cb_count);
+  if (rg > cap) rg = cap;
+  if (rg < 1) rg = 1;
+  g.rg_count = int(rg);
+  g.rpg = int((rows + rg - 1) / rg);
+  return g;
+}
+
+template <typename InT>
+__global__ __launch_bounds__(kThreads) void amax_colsum_kernel(
+    const InT* __restrict__ x, int64_t rows, int64_t cols, ColsumGeom geo,
+    uint32_t* __restrict__ part, float* __restrict__ cs_part) {
+  __shared__ uint32_t red[kThreads / 64];
+  __shared__ float csum[kThreads * 8];
+  const int cb = blockIdx.x % geo.cb_count, rg = blockIdx.x / geo.cb_count;
+  const int lc = threadIdx.x % geo.nvw, lr = threadIdx.x / geo.nvw;
+  const int64_t cv = int64_t(cb) * geo.nvw + lc;
+  const bool cvalid = cv * 8 < cols;
+  const int64_t r_beg = int64_t(rg) * geo.rpg;
+  const int64_t r_end = std::min<int64_t>(rows, r_beg + geo.rpg);
+  float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  uint32_t m = 0;
+  if (cvalid) {
+    int64_t r = r_beg + lr;
+    for (; r + 3 * geo.rl < r_end; r += 4 * geo.rl) {
+      float v[4][8];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) load8(x + (r + u * geo.rl) * cols + cv * 8, v[u]);
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          acc[j] += v[u][j];
+          m = umax(m, absbits(v[u][j]));
+        }
+    }
+    for (; r < r_end; r += geo.rl) {
+      float v[8];
+      load8(x + r * cols + cv * 8, v);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        acc[j] += v[j];
+        m = umax(m, absbits(v[j]));
+      }
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) csum[threadIdx.x * 8 + j] = acc[j];
+  m = block_umax_all(m, red);  // includes a barrier: csum is complete
+  if (threadIdx.x == 0) part[blockIdx.x] = m;
+  if (lr == 0 && cvalid) {
+    float o[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) o[j] = csum[lc * 8 + j];
+    for (int k = 1; k < geo.rl; ++k)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) o[j] += csum[(k * geo.nvw + lc) * 8 + j];
+    float* dst = cs_part + int64_t(rg) * cols + cv * 8;
+    *reinterpret_cast<float4*>(dst) = make_float4(o[0], o[1], o[2], o[3]);
+    *reinterpret_cast<float4*>(dst + 4) = make_float4(o[4], o[5], o[6], o[7]);
+  }
+}
+
+// out[c] = sum over row groups of cs_part[rg, c]: a workgroup owns 32
+// columns with 8 row lanes, each lane summing every 8th row group with four
+// independent loads in flight, then the lanes meet in LDS (fixed order).
+__global__ __launch_bounds__(kThreads) void colsum_finalize_kernel(const float* __restrict__ cs_part,
+                                                                   int rg_count, int64_t cols,
+                                                                   float* __restrict__ out) {
+  __shared__ float red[8][33];
+  const int lc = threadIdx.x & 31, lr = threadIdx.x >> 5;
+  const int64_t c = int64_t(blockIdx.x) * 32 + lc;
+  float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
+  if (c < cols) {
+    int r = lr;
+    for (; r + 24 < rg_count; r += 32) {
+      s0 += cs_part[int64_t(r) * cols + c];
+      s1 += cs_part[int64_t(r + 8) * cols + c];
+      s2 += cs_part[int64_t(r + 16) * cols + c];
+      s3 += cs_part[int64_t(r + 24) * cols + c];
+    }
+    for (; r < rg_count; r += 8) s0 += cs_part[int64_t(r) * cols + c];
+  }
+  red[lr][lc] = (s0 + s1) + (s2 + s3);
+  __syncthreads();
+  if (lr == 0 && c < cols) {
+    float t = red[0][lc];
+#pragma unroll
+    for (int k = 1; k < 8; ++k) t += red[k][lc];
+    out[c] = t;
+  }
+}
+
 // q = RNE(clamp(x * scale)), flat, two vectors in flight per thread.
 template <typename InT, int FMT>
 __global__ __launch_bounds__(kThreads) void quant_flat_kernel(
@@ -969,10 +1082,14 @@ const char* tcfp_status_string(int status) {
 
 size_t tcfp_workspace_bytes(void) { return sizeof(PartWs); }
 
-int tcfp_quantize_per_tensor(const void* x, int x_dtype, int64_t rows, int64_t cols,
-                             int fp8_fmt, const float* scale_in, uint8_t* q, uint8_t* q_t,
-                             float* scale_out, float* inv_out, void* workspace,
-                             void* stream) {
+}  // extern "C"
+
+namespace {
+
+int quantize_impl(const void* x, int x_dtype, int64_t rows, int64_t cols, int fp8_fmt,
+                  const float* scale_in, uint8_t* q, uint8_t* q_t, float* scale_out,
+                  float* inv_out, void* workspace, float* col_sum, float* cs_ws,
+                  hipStream_t st) {
   if (rows < 0 || cols < 0) return TCFP_ERR_SHAPE;
   if (x_dtype != TCFP_DTYPE_F32 && x_dtype != TCFP_DTYPE_BF16) return TCFP_ERR_DTYPE;
   if (fp8_fmt != TCFP_FP8_E4M3 && fp8_fmt != TCFP_FP8_E5M2) return TCFP_ERR_DTYPE;
@@ -980,12 +1097,28 @@ int tcfp_quantize_per_tensor(const void* x, int x_dtype, int64_t rows, int64_t c
   if (!scale_in && !workspace) return TCFP_ERR_WORKSPACE;
   const int64_t n = rows * cols;
   if (n >= 8 && (reinterpret_cast<uintptr_t>(q) & 7u) != 0) return TCFP_ERR_ALIGN;
-  hipStream_t st = static_cast<hipStream_t>(stream);
   PartWs* ws = static_cast<PartWs*>(workspace);
   const bool bf = x_dtype == TCFP_DTYPE_BF16;
   uint32_t* part = ws ? ws->a : nullptr;
   int g = 0;
-  if (!scale_in) {
+  ColsumGeom geo{};
+  if (col_sum && n > 0) {
+    geo = colsum_geom(rows, cols);
+    g = geo.cb_count * geo.rg_count;
+    if (bf)
+      amax_colsum_kernel<uint16_t><<<g, kThreads, 0, st>>>(static_cast<const uint16_t*>(x), rows,
+                                                           cols, geo, part, cs_ws);
+    else
+      amax_colsum_kernel<float><<<g, kThreads, 0, st>>>(static_cast<const float*>(x), rows, cols,
+                                                        geo, part, cs_ws);
+    colsum_finalize_kernel<<<unsigned((cols + 31) / 32), kThreads, 0, st>>>(cs_ws, geo.rg_count,
+                                                                            cols, col_sum);
+  } else if (col_sum && cols > 0) {
+    // no rows: the column sums are zero
+    colsum_finalize_kernel<<<unsigned((cols + 31) / 32), kThreads, 0, st>>>(cs_ws, 0, cols,
+                                                                            col_sum);
+  }
+  if (!col_sum && !scale_in) {
     g = parts_for((n + 7) / 8);
     if (bf)
       amax_part_kernel<uint16_t, false><<<g, kThreads, 0, st>>>(static_cast<const uint16_t*>(x),
@@ -1027,6 +1160,42 @@ int tcfp_quantize_per_tensor(const void* x, int x_dtype, int64_t rows, int64_t c
     transpose_u8_kernel<<<grid, kThreads, 0, st>>>(q, rows, cols, q_t);
   }
   return launch_status();
+}
+
+}  // namespace
+
+extern "C" {
+
+int tcfp_quantize_per_tensor(const void* x, int x_dtype, int64_t rows, int64_t cols,
+                             int fp8_fmt, const float* scale_in, uint8_t* q, uint8_t* q_t,
+                             float* scale_out, float* inv_out, void* workspace,
+                             void* stream) {
+  return quantize_impl(x, x_dtype, rows, cols, fp8_fmt, scale_in, q, q_t, scale_out, inv_out,
+                       workspace, nullptr, nullptr, static_cast<hipStream_t>(stream));
+}
+
+size_t tcfp_colsum_workspace_bytes(int64_t rows, int64_t cols) {
+  if (rows <= 0 || cols <= 0 || cols % 8 != 0) return 0;
+  return size_t(colsum_geom(rows, cols).rg_count) * size_t(cols) * sizeof(float);
+}
+
+int tcfp_quantize_per_tensor_colsum(const void* x, int x_dtype, int64_t rows, int64_t cols,
+                                    int fp8_fmt, uint8_t* q, uint8_t* q_t, float* inv_out,
+                                    float* col_sum, void* workspace, void* colsum_ws,
+                                    size_t colsum_ws_bytes, void* stream) {
+  if (rows < 0 || cols < 0 || cols % 8 != 0) return TCFP_ERR_SHAPE;
+  if (cols / 8 > int64_t(kMaxParts) * 256) return TCFP_ERR_SHAPE;  // partial slots
+  if (!col_sum) return TCFP_ERR_SHAPE;
+  if (!workspace) return TCFP_ERR_WORKSPACE;
+  if (rows > 0 && cols > 0 &&
+      (!colsum_ws || colsum_ws_bytes < tcfp_colsum_workspace_bytes(rows, cols) ||
+       !aligned16(colsum_ws) || !aligned16(col_sum)))
+    return !colsum_ws || colsum_ws_bytes < tcfp_colsum_workspace_bytes(rows, cols)
+               ? TCFP_ERR_WORKSPACE
+               : TCFP_ERR_ALIGN;
+  return quantize_impl(x, x_dtype, rows, cols, fp8_fmt, nullptr, q, q_t, nullptr, inv_out,
+                       workspace, col_sum, static_cast<float*>(colsum_ws),
+                       static_cast<hipStream_t>(stream));
 }
 
 int tcfp_dual_quantize_per_tensor(const void* w, int w_dtype, int64_t n, int64_t k,

@@ -104,6 +104,43 @@ def quantize_per_tensor(
     return out
 
 
+def quantize_per_tensor_colsum(
+    x: torch.Tensor,
+    fp8_dtype: torch.dtype = torch.float8_e5m2,
+    transpose: bool = False,
+):
+    """Per-tensor FP8 cast (amax scaling, as ``quantize_per_tensor``) that
+    also returns the column sums of the 2-D view, read in the same pass.
+
+    For a gradient this gives the bias gradient (the reference's
+    ``grad_2d.sum(0)``, ``tcfp/nn/__init__.py:558``) alongside the E5M2
+    codes (``:494``).  Returns ``(q, inv, col_sum)`` or, with ``transpose``,
+    ``(q, inv, q_t, col_sum)``.  Needs ``x.shape[-1] % 8 == 0``.
+    """
+    dev = _hip.require_gpu(x)
+    xc = x if x.is_contiguous() else x.contiguous()
+    cols = xc.shape[-1]
+    rows = xc.numel() // cols if cols else 0
+    if cols % 8 != 0:
+        raise ValueError(f"column count ({cols}) must be divisible by 8")
+    q = torch.empty(x.shape, dtype=fp8_dtype, device=dev)
+    q_t = torch.empty((cols, rows), dtype=fp8_dtype, device=dev) if transpose else None
+    inv = torch.empty(1, dtype=torch.float32, device=dev)
+    cs = torch.empty(cols, dtype=torch.float32, device=dev)
+    nbytes = int(_hip.lib().tcfp_colsum_workspace_bytes(rows, cols))
+    cws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=dev)
+    check(
+        _hip.lib().tcfp_quantize_per_tensor_colsum(
+            ptr(xc), _in_dtype(xc), rows, cols, _fmt(fp8_dtype), ptr(q), ptr(q_t), ptr(inv),
+            ptr(cs), ptr(_hip.workspace(dev)), ptr(cws), nbytes, _hip.stream_of(dev),
+        ),
+        "quantize_per_tensor_colsum",
+    )
+    if transpose:
+        return q, inv, q_t, cs
+    return q, inv, cs
+
+
 def dual_quantize_per_tensor(
     weight: torch.Tensor,
     error_buf: torch.Tensor | None = None,
@@ -627,5 +664,5 @@ def block_scaled_wgrad(
 def set_gemm_tile_policy(policy: str) -> None:
     """Tuning hook: ``"auto"`` (default), ``"large"`` (256 x 128 tiles) or
     ``"small"`` (128 x 64 tiles, two workgroups per CU)."""
-    code = {"auto": 0, "large": 1, "small": 2}[policy]
+    code = {"auto": 0, "large": 1, "small": 2, "small8": 3}[policy]
     check(_hip.lib().tcfp_gemm_set_tile_policy(code), "set_gemm_tile_policy")

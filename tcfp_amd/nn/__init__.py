@@ -141,14 +141,21 @@ class _TCFP12TensorCoreFunction(torch.autograd.Function):
             grad_2d = grad_2d.contiguous()
 
         grad_input = grad_weight = grad_bias = None
+        # the bias gradient comes out of the gradient's amax pass when the
+        # gradient is quantised anyway (fp32 sums, as the reference's sum(0))
+        fuse_db = need_db and ctx.has_bias and grad_2d.shape[-1] % 8 == 0
         if need_dx or (need_dw and ctx.fp8_wgrad):
-            if need_dw and ctx.fp8_wgrad:
-                grad_fp8, grad_inv, grad_t = K.quantize_per_tensor(
-                    grad_2d, torch.float8_e5m2, transpose=True
-                )
+            want_t = need_dw and ctx.fp8_wgrad
+            if fuse_db:
+                res = K.quantize_per_tensor_colsum(grad_2d, torch.float8_e5m2, transpose=want_t)
+                grad_bias = res[-1].to(grad_2d.dtype)
+                res = res[:-1]
             else:
-                grad_fp8, grad_inv = K.quantize_per_tensor(grad_2d, torch.float8_e5m2)
-                grad_t = None
+                res = K.quantize_per_tensor(grad_2d, torch.float8_e5m2, transpose=want_t)
+            if want_t:
+                grad_fp8, grad_inv, grad_t = res
+            else:
+                (grad_fp8, grad_inv), grad_t = res, None
             if need_dx:
                 if ctx.abd:
                     gi = K.fp8_gemm_nt(grad_fp8, w_hi_t, grad_inv, inv_hi)
@@ -163,7 +170,7 @@ class _TCFP12TensorCoreFunction(torch.autograd.Function):
                 grad_weight = K.fp8_gemm_nt(grad_t, saved_act, grad_inv, act_inv)
             else:
                 grad_weight = grad_2d.t() @ (saved_act.float() * act_inv).to(grad_2d.dtype)
-        if need_db and ctx.has_bias:
+        if need_db and ctx.has_bias and grad_bias is None:
             grad_bias = grad_2d.sum(dim=0)
         return (grad_input, grad_weight, grad_bias) + (None,) * 12
 

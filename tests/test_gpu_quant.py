@@ -275,3 +275,21 @@ def test_block_dual_quantize_sr(dev):
     assert abs(float((p[m] - frac[m]).mean())) < 0.01
     # unbiased: E[deq(lo)] ~= residual
     assert float(np.abs(p[m] - frac[m]).max()) < 0.2
+
+
+# ------------------------------------------------ quant + column sums (bias grad)
+@pytest.mark.parametrize("shape", [(8192, 1024), (300, 200), (7, 4096), (1000, 24), (0, 64)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_quantize_colsum_codes_and_sums(dev, shape, dtype):
+    g = torch.Generator().manual_seed(shape[0] + shape[1])
+    x = (torch.randn(shape, generator=g) * 1e-3).to(dtype)
+    q, inv, qt, cs = K.quantize_per_tensor_colsum(x.to(dev), torch.float8_e5m2, transpose=True)
+    if shape[0] == 0:
+        assert torch.equal(cs.cpu(), torch.zeros(shape[1]))
+        return
+    codes, inv_o, _ = oq.to_fp8_per_tensor(x.float().numpy(), "bf16" if dtype == torch.bfloat16
+                                           else "f32", ofp8.E5M2)
+    assert np.array_equal(u8(q), codes) and np.array_equal(u8(qt), codes.T)
+    assert inv.item() == float(inv_o)
+    ref = x.double().sum(0).numpy()
+    np.testing.assert_allclose(cs.cpu().numpy(), ref, rtol=1e-5, atol=1e-6 * float(np.abs(x.float().numpy()).sum(0).max()))
