@@ -48,8 +48,9 @@ const char* tcfp_status_string(int status);
 
 /* Bytes of device workspace the per-tensor reductions need.  Reducing
  * kernels store one partial maximum per workgroup there and the kernel that
- * consumes the scale reduces them again, so the workspace needs no
- * initialisation and is never left in a state a later call depends on.
+ * consumes the scale reduces them again.  The single-launch dual
+ * quantisation also keeps three grid-barrier counters there: zero the
+ * workspace once before its first use; every launch leaves them at zero.
  * Calls that may run concurrently (different streams) need different
  * workspaces; calls ordered on one stream can share one. */
 size_t tcfp_workspace_bytes(void);
@@ -89,6 +90,11 @@ int tcfp_quantize_per_tensor_colsum(const void* x, int x_dtype, int64_t rows, in
                                     size_t colsum_ws_bytes, void* stream);
 
 /* Per-tensor dual quantisation with optional error feedback.
+ * Three launches (amax; W_hi + residual amax; W_lo + EF + transposed
+ * codes), each re-reading W and EF.  Optionally (tcfp_dual_quant_set_path)
+ * a single cooperative launch that holds W + EF on chip across the two
+ * grid-wide max reductions when W (as 128 x 128 tiles) fits one or two
+ * tiles per CU and k % 16 == 0.  Both give identical bits.
  * Replaces the body of _TCFP12TensorCoreFunction.forward that builds
  * W_hi/W_lo (tcfp/nn/__init__.py:343-383, with ErrorFeedbackState
  * get_error/update_error, tcfp/core.py:320-326).
@@ -219,6 +225,15 @@ int tcfp_transpose_u8(const uint8_t* src, int64_t rows, int64_t cols, uint8_t* d
  * 256 x 128 tile unless it would leave CUs idle), 1 always 256 x 128,
  * 2 always 128 x 64.  Results do not depend on the policy. */
 int tcfp_gemm_set_tile_policy(int policy);
+
+/* Per-tensor dual quantisation path for all later calls: 0 three launches
+ * (default), 1 a single cooperative launch where it fits. */
+int tcfp_dual_quant_set_path(int path);
+
+/* Copies the workspace's sticky error flag to host *flag (synchronising
+ * the stream): non-zero if a grid-barrier wait of the single-launch dual
+ * quantisation ever gave up (which would also make its results invalid). */
+int tcfp_workspace_error(const void* workspace, int* flag, void* stream);
 
 /* ---- self-test hooks (no reference counterpart) ------------------------ */
 

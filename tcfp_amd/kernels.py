@@ -661,6 +661,26 @@ def block_scaled_wgrad(
     return out
 
 
+def set_dual_quant_path(path: str) -> None:
+    """Tuning/test hook for ``dual_quantize_per_tensor``: ``"three_pass"``
+    (the default) or ``"single_launch"`` (one cooperative launch holding
+    W + EF on chip where it fits; same bits, measured slower)."""
+    code = {"three_pass": 0, "single_launch": 1}[path]
+    check(_hip.lib().tcfp_dual_quant_set_path(code), "set_dual_quant_path")
+
+
+def workspace_error(device: torch.device | None = None) -> int:
+    """Sticky error flag of the reduction workspace (0 = no grid-barrier
+    wait ever gave up)."""
+    import ctypes
+
+    dev = device or torch.device("cuda", torch.cuda.current_device())
+    flag = ctypes.c_int(0)
+    check(_hip.lib().tcfp_workspace_error(ptr(_hip.workspace(dev)), ctypes.byref(flag),
+                                          _hip.stream_of(dev)), "workspace_error")
+    return int(flag.value)
+
+
 def set_gemm_tile_policy(policy: str) -> None:
     """Tuning hook: ``"auto"`` (default), ``"large"`` (256 x 128 tiles) or
     ``"small"`` (128 x 64 tiles, two workgroups per CU)."""

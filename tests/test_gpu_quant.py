@@ -105,14 +105,15 @@ def test_per_tensor_empty(dev):
 
 
 def test_workspace_contents_do_not_matter(dev):
-    """The reduction workspace is scratch: whatever it holds before a call
-    (here all-ones bytes) does not change any output."""
+    """The partial-maximum slots of the reduction workspace are scratch:
+    whatever they hold before a call (here all-ones bytes) changes no output.
+    (The grid-barrier counters after them must stay zero at rest.)"""
     ws = _hip.workspace(dev)
     x = torch.randn(300, 200, generator=torch.Generator().manual_seed(5)).to(dev)
     w = torch.randn(64, 64, generator=torch.Generator().manual_seed(6)).to(dev)
     ref_q = to_fp8_e4m3(x)
     ref_d = K.dual_quantize_per_tensor(w, torch.zeros(64, 64, device=dev))
-    ws.fill_(255)
+    ws[:8192].fill_(255)
     q = to_fp8_e4m3(x)
     d = K.dual_quantize_per_tensor(w, torch.zeros(64, 64, device=dev))
     assert torch.equal(q[0].view(torch.uint8), ref_q[0].view(torch.uint8))
@@ -293,3 +294,31 @@ def test_quantize_colsum_codes_and_sums(dev, shape, dtype):
     assert inv.item() == float(inv_o)
     ref = x.double().sum(0).numpy()
     np.testing.assert_allclose(cs.cpu().numpy(), ref, rtol=1e-5, atol=1e-6 * float(np.abs(x.float().numpy()).sum(0).max()))
+
+
+# ------------------------------------------------ single-launch vs three-pass dual quant
+@pytest.mark.parametrize("shape", [(4096, 1024), (1024, 4096), (128, 128), (300, 208),
+                                   (2048, 2048), (4096, 2048), (100, 96)])
+@pytest.mark.parametrize("wdtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("mode", ["ef", "ef_no_update", "no_ef", "srr"])
+def test_dual_quant_single_launch_matches_three_pass(dev, shape, wdtype, mode):
+    """The cooperative one-launch path and the three-launch path give the
+    same bits (codes, inverse scales, transposed codes, new error)."""
+    g = torch.Generator().manual_seed(shape[0] * 7 + shape[1])
+    W = (torch.randn(shape, generator=g) * 0.02).to(wdtype).to(dev)
+    ef0 = (torch.randn(shape, generator=g) * 1e-5).to(dev)
+    outs = []
+    try:
+        for path in ("three_pass", "single_launch"):
+            K.set_dual_quant_path(path)
+            ef = ef0.clone() if mode.startswith("ef") else None
+            r = K.dual_quantize_per_tensor(W, ef, update_ef=(mode != "ef_no_update"),
+                                           stochastic_lo=(mode == "srr"), transposed=True,
+                                           seed=1234)
+            outs.append([t.view(torch.uint8) if t.dtype.itemsize == 1 else t for t in r]
+                        + ([ef] if ef is not None else []))
+    finally:
+        K.set_dual_quant_path("three_pass")
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
+    assert K.workspace_error(dev) == 0
