@@ -38,5 +38,9 @@ quant.sr_candidates (a5)               deterministic candidate set; the random
                                        draws from torch.rand / tl.rand)
 gemm.* (a6,a7,a9,a10,a12,a13)          float64 textbook matmul of the same
                                        dequantised FP8 operands
+torch_ref.RefTCFP12Function (a1,a2,    the numpy functions above on CPU (codes,
+a6-a9 as one training step)            EF, forward, dX, dW) -- used to hold the
+                                       HIP path's training loss to the
+                                       reference algorithm's
 =====================================  ==========================================
 """

@@ -135,3 +135,37 @@ def test_ef_guard_version_logic_cpu():
     with torch.no_grad():
         lin.weight.add_(1.0)
     assert lin.weight._version != v0
+
+
+def test_ef_state_roundtrip_reference_format(tmp_path):
+    """ef_state.pt has the reference's structure (checkpointing.py:200-224)
+    and restores buffers, EMA dicts, step counts and decay by layer key."""
+    from tcfp_amd.ef_state import ef_state_dict, load_ef_state, save_ef_state
+
+    def model():
+        m = nn.Sequential(nn.Linear(64, 128), nn.GELU(), nn.Linear(128, 64))
+        return convert_to_tcfp(m, use_tensor_cores=True)
+
+    a = model()
+    g = torch.Generator().manual_seed(0)
+    for key, lin in (("0", a[0]), ("2", a[2])):
+        ef = lin._error_state
+        ef._buffers[key] = torch.randn(lin.weight.shape, generator=g)
+        ef._amax_ema[key] = torch.rand(1, generator=g)
+        ef._step_count[key] = 7
+        ef._ema_decay = 0.99
+    snap = ef_state_dict(a)
+    assert set(snap) == {"0", "2"}
+    assert set(snap["0"]) == {"_buffers", "_amax_ema", "_delayed_amax", "_residual_ratio",
+                              "_step_count", "_ema_decay"}
+    save_ef_state(a, tmp_path / "ef_state.pt")
+    b = model()
+    assert load_ef_state(b, tmp_path / "ef_state.pt") == 2
+    for key, la, lb in (("0", a[0], b[0]), ("2", a[2], b[2])):
+        ea, eb = la._error_state, lb._error_state
+        assert torch.equal(ea._buffers[key], eb._buffers[key])
+        assert torch.equal(ea._amax_ema[key], eb._amax_ema[key])
+        assert eb._step_count[key] == 7 and eb._ema_decay == 0.99
+    # unknown keys are skipped, as in the reference
+    from tcfp_amd.ef_state import load_ef_state_dict
+    assert load_ef_state_dict(b, {"nope": snap["0"]}) == 0

@@ -245,3 +245,34 @@ def test_dual_gemm_oracle_closed_forms():
     assert np.allclose(out, brute, rtol=1e-12, atol=0)
     # linear in each scale
     assert np.allclose(og.dual_gemm_nt(a, ofp8.E4M3, lo, hi, 0.5, 2.0, 3.0), 1.5 * brute)
+
+
+def test_torch_ref_step_matches_numpy_oracle():
+    """oracle/torch_ref.py (the torch restatement used for the training-loss
+    parity test) against the numpy oracle on CPU: codes, EF, forward, and
+    the three backward products."""
+    import torch
+
+    from oracle import torch_ref as tr
+
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(48, 64, generator=g).bfloat16()
+    W = torch.randn(32, 64, generator=g) * 0.05
+    b = torch.randn(32, generator=g)
+    ef = {}
+    xr = x.clone().requires_grad_(True)
+    Wr = W.clone().requires_grad_(True)
+    out = tr.RefTCFP12Function.apply(xr, Wr, b, ef, "", True)
+    gout = torch.randn(48, 32, generator=g)
+    out.backward(gout)
+    hi, lo, ih, il, ef_new, _ = oq.dual_quant_per_tensor(W.numpy(), np.zeros((32, 64), np.float32))
+    assert np.array_equal(ef[""].numpy(), ef_new)
+    aq, ai, _ = oq.to_fp8_per_tensor(x.float().numpy(), "bf16")
+    ref = og.dual_gemm_nt(aq, ofp8.E4M3, hi, lo, ai, ih, il) + b.double().numpy()
+    assert og.rel_fro(out.detach().numpy(), ref) < 1e-6
+    gq, gi, _ = oq.to_fp8_per_tensor(gout.numpy(), "f32", ofp8.E5M2)
+    G = ofp8.decode(gq, ofp8.E5M2).astype(np.float64) * gi
+    Wd = ofp8.decode(hi, ofp8.E4M3).astype(np.float64) * ih + ofp8.decode(lo, ofp8.E4M3).astype(np.float64) * il
+    assert og.rel_fro(xr.grad.float().numpy(), G @ Wd) < 1e-2  # dX returned in bf16
+    A = ofp8.decode(aq, ofp8.E4M3).astype(np.float64) * ai
+    assert og.rel_fro(Wr.grad.numpy(), G.T @ A) < 1e-6
