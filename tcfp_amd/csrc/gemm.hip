@@ -379,7 +379,7 @@ struct GemmArgs {
 // workgroup per CU is resident): the DMA of stage t + NS is issued once
 // every wave has read stage t, so it has NS - 1 stages of MFMA time to land.
 template <int AF, int BF, bool SPLIT, typename OutT, int NW, int BM, int BN, int SCALE, int NS>
-__global__ __launch_bounds__(NW * 64, (NW == 4 && NS == 2 ? 2 : 1)) void gemm_nt_dma_kernel(
+__global__ __launch_bounds__(NW * 64, (NW == 4 && NS == 2 && BM == 128 ? 2 : 1)) void gemm_nt_dma_kernel(
     GemmArgs g) {
   constexpr int WM = NW / 2;        // wave rows
   constexpr int TMW = BM / WM;      // activation rows per wave
@@ -727,7 +727,7 @@ int launch_gemm(GemmArgs ga, hipStream_t st) {
   const int big_tiles = ((m + 255) / 256) * ((n + (SPLIT ? 255 : 127)) / (SPLIT ? 256 : 128));
   // (block-scaled single GEMMs keep two accumulator sets, which only the
   // small tile fits in registers)
-  const bool small = (SCALE == 1 && SPLIT) || g_tile_policy >= 2 ||
+  const bool small = (SCALE == 1 && SPLIT) || g_tile_policy == 2 || g_tile_policy == 3 ||
                      (g_tile_policy == 0 && big_tiles < num_cus());
   const int BMv = small ? 128 : 256, BNv = small ? 64 : 128;
   ga.tiles_m = (m + BMv - 1) / BMv;
