@@ -136,8 +136,10 @@ def bench_comparators(t, iters=20):
 
 def bench_block_gemms(iters=20):
     """block-scaled dual GEMM at 4096^3, bs 32/64/128 (int8
-    power-of-two exponents, the reference's block format), plus the single
-    block-scaled GEMM at bs 64.  fp32 out, as the reference's kernels."""
+    power-of-two exponents, the reference's block format, and fp32
+    448/amax block scales, the configuration's literal form), plus the
+    single block-scaled GEMM at bs 64.  fp32 out, as the reference's
+    kernels."""
     import torch
 
     from tcfp_amd import kernels as K
@@ -159,6 +161,12 @@ def bench_block_gemms(iters=20):
             ms = event_time_ms(lambda: K.block_scaled_gemm(a, h, ea, eh, bs), iters, stream)
             res["block64_single_ms"] = ms
             res["block64_single_tflops"] = 2 * n**3 / (ms * 1e-3) / 1e12
+        a, sa = K.block_quantize_fp8(x, bs, scale_format="fp32")
+        h, l, sh, sl = K.fused_dual_quantize_fp8(w, bs, scale_format="fp32")
+        ms = event_time_ms(
+            lambda: K.fused_block_scaled_dual_gemm_forward(a, h, l, sa, sh, sl, bs), iters, stream)
+        res[f"block{bs}_f32s_dual_ms"] = ms
+        res[f"block{bs}_f32s_dual_tflops"] = 4 * n**3 / (ms * 1e-3) / 1e12
     return res
 
 

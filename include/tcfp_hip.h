@@ -139,6 +139,31 @@ int tcfp_block_dual_quantize(const void* w, int w_dtype, int64_t n, int64_t k, i
 int tcfp_block_dequantize(const uint8_t* q, int fp8_fmt, const int8_t* exps, int64_t m,
                           int64_t k, int block, float* out, void* stream);
 
+/* fp32 block scales (non-power-of-two).  The reference quantises blocks
+ * only with power-of-two exponents; these variants apply its per-tensor
+ * rule to_fp8_e4m3 / to_fp8_e5m2 (tcfp/core.py:85-106, 137-158) to each
+ * (row, K-block): scale = FP8_MAX / max(amax, 1e-12) with the reciprocal and
+ * the product rounded to the input dtype, q = RNE(clamp(x * scale)), and
+ * store the fp32 dequantisation multiplier 1 / scale in inv_scales
+ * [k/block, m].  Layout, block sizes and constraints as above. */
+int tcfp_block_quantize_f32s(const void* x, int x_dtype, int64_t m, int64_t k, int block,
+                             int fp8_fmt, uint8_t* q, float* inv_scales, void* stream);
+
+/* Fused block dual quantisation with fp32 block scales: W' = W (+ ef),
+ * hi by the fp32 block rule on W', r = W' - hi * inv_hi, lo by the same rule
+ * on r (RNE, or stochastic as tcfp_block_dual_quantize), and the error
+ * update ef = (W - hi * inv_hi) - lo * inv_lo in place (the reference's
+ * block error update order, tcfp/kernels.py:1867-1873).  A zero residual
+ * block gets zero codes and the 1e-12-clamped multiplier (no sentinel). */
+int tcfp_block_dual_quantize_f32s(const void* w, int w_dtype, int64_t n, int64_t k, int block,
+                                  float* ef, int update_ef, int stochastic_lo, uint64_t seed,
+                                  uint64_t offset, uint8_t* w_hi, uint8_t* w_lo, float* inv_hi,
+                                  float* inv_lo, void* stream);
+
+/* fp8 * inv_scales[c / block, r] -> fp32. */
+int tcfp_block_dequantize_f32s(const uint8_t* q, int fp8_fmt, const float* inv_scales,
+                               int64_t m, int64_t k, int block, float* out, void* stream);
+
 /* ---- GEMMs ------------------------------------------------------------- */
 
 /* Fused dual FP8 GEMM, both operands K-contiguous ("NT"):
@@ -175,6 +200,25 @@ int tcfp_block_dual_gemm(const uint8_t* a, int a_fmt, int64_t lda, const int8_t*
                          const int8_t* e_hi, const int8_t* e_lo, int64_t m, int64_t n,
                          int64_t k, int block, const float* bias, void* out, int out_dtype,
                          int64_t ldo, void* stream);
+
+/* Block-scaled dual FP8 GEMM with fp32 block multipliers (non-power-of-two
+ * block scales, e.g. the 448 / amax rule of tcfp_block_quantize_f32s):
+ *   out[i,j] = sum_kb s_a[kb,i] * ( s_hi[kb,j] * sum_{k in kb} A[i,k] B_hi[j,k]
+ *                                 + s_lo[kb,j] * sum_{k in kb} A[i,k] B_lo[j,k] ) (+ bias[j])
+ * with fp32 dequantisation multipliers s_a [k/block, m], s_hi / s_lo
+ * [k/block, n].  Same operation as tcfp_block_dual_gemm with the reference's
+ * int8 exponents replaced by arbitrary fp32 scales (the reference kernel
+ * multiplies by exp2 of its exponents in-loop, tcfp/kernels.py:577-585,
+ * :757-776); b_lo == NULL gives the single GEMM.  The per-block products
+ * are accumulated on the MFMA and folded into the output with the fp32
+ * multipliers on the VALU.
+ *   block in {32, 64, 128}; k % block == 0; m % 4 == 0; n % 4 == 0;
+ *   s_* 16-byte aligned; other constraints as tcfp_dual_gemm. */
+int tcfp_block_dual_gemm_f32s(const uint8_t* a, int a_fmt, int64_t lda, const float* s_a,
+                              const uint8_t* b_hi, const uint8_t* b_lo, int b_fmt, int64_t ldb,
+                              const float* s_hi, const float* s_lo, int64_t m, int64_t n,
+                              int64_t k, int block, const float* bias, void* out,
+                              int out_dtype, int64_t ldo, void* stream);
 
 /* Block-scaled dual dgrad:
  *   dx[i,k] = sum_n 2^eg[n/block,i] G[i,n] * ( 2^ehi[k/block,n] W_hi[n,k]

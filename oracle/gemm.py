@@ -63,6 +63,17 @@ def block_dual_gemm_nt(a, a_exps, w_hi, w_lo, e_hi, e_lo, bs):
     return A @ W.T
 
 
+def block_dual_gemm_f32s_nt(a, s_a, w_hi, w_lo, s_hi, s_lo, bs, a_fmt=E4M3):
+    """Block dual GEMM with fp32 block multipliers (no sentinel):
+    ``sum_kb s_a (s_hi A W_hi^T + s_lo A W_lo^T)``; ``w_lo=None`` gives the
+    single GEMM."""
+    A = block_scale_deq64(a, s_a, bs, a_fmt)
+    W = block_scale_deq64(w_hi, s_hi, bs)
+    if w_lo is not None:
+        W = W + block_scale_deq64(w_lo, s_lo, bs)
+    return A @ W.T
+
+
 def block_dgrad(g, g_exps, w_hi, w_lo, e_hi, e_lo, bs, g_fmt="e5m2"):
     """``fused_block_scaled_dual_gemm_backward_dx`` (kernels.py:2428-2469)."""
     G = block_deq64(g, g_exps, bs, g_fmt)

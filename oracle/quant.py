@@ -197,6 +197,65 @@ def block_dual_quantize(w: np.ndarray, bs: int, ef: np.ndarray | None = None):
     return hi, lo, e_hi8, e_lo8, ef_new
 
 
+def block_scale_f32(amax: np.ndarray, dtype: str = "f32", fmt: str = E4M3) -> np.ndarray:
+    """fp32 block scales: ``per_tensor_scale``'s rule (core.py:100-101) on
+    each block's amax -- clamp to 1e-12, reciprocal and product with
+    FP8_MAX each rounded to ``dtype``."""
+    a = np.maximum(np.asarray(amax, dtype=F32), _round_dtype(np.array([1e-12], F32), dtype)[0])
+    with np.errstate(divide="ignore", over="ignore", invalid="ignore"):
+        rcp = _round_dtype((F32(1.0) / a).astype(F32), dtype)
+        return _round_dtype((rcp * F32(FP8_MAX[fmt])).astype(F32), dtype).astype(F32)
+
+
+def block_quantize_f32s(x: np.ndarray, bs: int, dtype: str = "f32", fmt: str = E4M3):
+    """Block quantisation with fp32 scales: ``to_fp8_e4m3`` / ``to_fp8_e5m2``
+    (core.py:85-106, :137-158) applied to every (row, K-block).  The
+    reference has no such format (its blocks use power-of-two exponents,
+    kernels.py:205-275); this is the non-power-of-two ``448 / amax`` block
+    scaling run beside it.
+
+    Returns ``(codes [M,K] uint8, inv [K/bs, M] float32)`` where ``inv`` is
+    ``1 / scale``, the block's dequantisation multiplier.
+    """
+    x = np.asarray(x, dtype=F32)
+    xb = _blocks(x, bs)
+    scale = block_scale_f32(np.max(np.abs(xb), axis=-1), dtype, fmt)
+    mx = F32(FP8_MAX[fmt])
+    codes = encode(np.clip(xb * scale[..., None], -mx, mx), fmt).reshape(x.shape)
+    with np.errstate(divide="ignore"):
+        inv = (F32(1.0) / scale).astype(F32)
+    return codes, np.ascontiguousarray(inv.T)
+
+
+def block_dequantize_f32s(codes: np.ndarray, inv: np.ndarray, bs: int,
+                          fmt: str = E4M3) -> np.ndarray:
+    """``fp8 * inv[kb, row]`` in float32."""
+    m, k = codes.shape
+    vals = decode(codes, fmt).reshape(m, k // bs, bs)
+    return (vals * inv.T[..., None].astype(F32)).reshape(m, k).astype(F32)
+
+
+def block_dual_quantize_f32s(w: np.ndarray, bs: int, ef: np.ndarray | None = None):
+    """Dual quantisation with fp32 block scales: the fused block kernel's
+    structure (kernels.py:288-459) with :func:`block_quantize_f32s`'s rule
+    for both components (fp32 rule on ``w + ef`` and on the residual
+    ``r = w' - hi * inv_hi``; no zero-block sentinel) and the block path's
+    error update order ``(w - deq(hi)) - deq(lo)`` (kernels.py:1870-1873).
+
+    Returns ``(hi, lo, inv_hi [K/bs,N], inv_lo [K/bs,N], ef_new|None)``.
+    """
+    w = np.asarray(w, dtype=F32)
+    wc = w + ef if ef is not None else w
+    hi, inv_hi = block_quantize_f32s(wc, bs)
+    deq_hi = block_dequantize_f32s(hi, inv_hi, bs)
+    r = (wc - deq_hi).astype(F32)
+    lo, inv_lo = block_quantize_f32s(r, bs)
+    ef_new = None
+    if ef is not None:
+        ef_new = ((w - deq_hi) - block_dequantize_f32s(lo, inv_lo, bs)).astype(F32)
+    return hi, lo, inv_hi, inv_lo, ef_new
+
+
 def sr_candidates_block(x: np.ndarray):
     """Deterministic part of the in-kernel SR of kernels.py:398-423.
 

@@ -311,6 +311,12 @@ TCFP_DEV void dma16(v4i rsrc, uint32_t voff, uint32_t soff, uint32_t lds) {
                : "memory");
 }
 
+// 16 bytes from a per-lane global address into LDS at lds + 16 * lane
+// (lds wave-uniform); counted by vmcnt like dma16.
+TCFP_DEV void gdma16(const void* src, uint32_t lds) {
+  asm volatile("global_load_lds_dwordx4 %0, off" : : "v"(src), "{m0}"(lds) : "memory");
+}
+
 template <typename OutT>
 TCFP_DEV void store4(OutT* p, float a, float b, float c, float d);
 template <>
@@ -362,13 +368,13 @@ struct GemmArgs {
   const uint8_t* B1;
   int M, N, K;       // K and the leading dimensions count bytes of an
   int64_t lda, ldb;  // operand row: elements for fp8, 2 x elements for bf16
-  const float* s_a;  // per-tensor scalars (SCALE 0)
-  const float* s_0;
+  const float* s_a;  // per-tensor scalars (SCALE 0), or fp32 block multipliers
+  const float* s_0;  // (SCALE 2): [K/bs, M], [K/bs, N], [K/bs, N]
   const float* s_1;
   const int8_t* e_a;  // block exponents (SCALE 1): [K/bs, M], [K/bs, N], [K/bs, N]
   const int8_t* e_0;
   const int8_t* e_1;
-  int bs_shift;  // log2(block size)
+  int bs_shift;  // log2(block size) (SCALE 1 and 2)
   const float* bias;
   void* out;
   int64_t ldo;
@@ -394,7 +400,12 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && NS == 2 && BM == 128 ? 2 : 1))
   static_assert(RPW % 16 == 0 && BM % RPW == 0 && BN % RPW == 0, "DMA rows must tile regions");
   static_assert(MB >= 1 && NB >= 1, "tile too small for the wave grid");
   static_assert(NS == 2 || (NS == 4 && SCALE == 0), "deep pipelines carry no exponent loads");
-  __shared__ __align__(16) uint8_t lds[NS * STAGE];
+  static_assert(SCALE != 2 || (NW == 4 && BM == 128 && BN == 64 && NS == 2),
+                "fp32 block scales use the 128 x 64 tile");
+  // SCALE 2: a three-slot ring of per-stage fp32 scale areas (up to four
+  // K-blocks of 1 KiB) behind the operand stages
+  constexpr int kScB = SCALE == 2 ? 4096 : 0;
+  __shared__ __align__(16) uint8_t lds[NS * STAGE + 3 * kScB];
 
   const int M = g.M, N = g.N, K = g.K;
   OutT* __restrict__ out = static_cast<OutT*>(g.out);
@@ -453,6 +464,28 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && NS == 2 && BM == 128 ? 2 : 1))
   const int nt = (K + kSK - 1) / kSK;
   const int krem = K - (nt - 1) * kSK;  // valid K columns of the last stage
 
+  // ---- fp32 block scales (SCALE 2).  Stage t's K-block b (of kSK / bs) is
+  // brought into ring slot t % 3 by wave b with one 1 KiB global->LDS load:
+  // lanes 0-31 carry the 128 activation-row multipliers, lanes 32-47 the 64
+  // slot-0 and lanes 48-63 the 64 slot-1 weight-row multipliers, 4 floats
+  // each.  Groups past the matrix re-read its last group (M, N % 4 == 0);
+  // their rows are never stored.
+  const float* sc_src = nullptr;
+  int sc_ld = 0;
+  if constexpr (SCALE == 2) {
+    if (lane < 32) {
+      sc_src = g.s_a + min(m0 + 4 * lane, M - 4);
+      sc_ld = M;
+    } else {
+      const int nb = lane < 48 ? n0 : n1;
+      sc_src = (lane < 48 ? g.s_0 : g.s_1) + min(nb + 4 * ((lane - 32) & 15), N - 4);
+      sc_ld = N;
+    }
+  }
+  const uint32_t sc_lds =
+      uint32_t(reinterpret_cast<uintptr_t>((TCFP_LDS uint8_t*)lds)) + uint32_t(NS * STAGE);
+  const int nkb = SCALE == 2 ? (K >> g.bs_shift) : 0;
+
   // DMA of stage t (K columns t*128 ..) into buffer t & 1.  Stages past the
   // end are issued as all-out-of-range loads (zeros into a buffer nobody
   // reads again), so the issue stays branch-free.
@@ -465,6 +498,12 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && NS == 2 && BM == 128 ? 2 : 1))
     for (int i = 0; i < DI; ++i) {
       const int c = (i & 1) ? chunk1 : chunk0;
       dma16(rsrc, (!live || (last && c * 16 >= krem)) ? kOob : voff[i], soff, dst + i * 1024);
+    }
+    if constexpr (SCALE == 2) {
+      if (live && wave < (kSK >> g.bs_shift)) {
+        const int kb = min(((t * kSK) >> g.bs_shift) + wave, nkb - 1);
+        gdma16(sc_src + int64_t(kb) * sc_ld, sc_lds + uint32_t(t % 3) * kScB + uint32_t(wave) * 1024);
+      }
     }
   };
 
@@ -519,9 +558,11 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && NS == 2 && BM == 128 ? 2 : 1))
     }
   };
 
-  // [slot][n-block][m-block].  Block-scaled dual GEMMs keep one set: the
-  // MFMA applies each slot's scales, so W_hi and W_lo products add directly.
-  constexpr int NACC = (SCALE == 1 && !SPLIT) ? 1 : 2;
+  // [slot][n-block][m-block].  Block-scaled dual GEMMs keep one set: with
+  // exponents the MFMA applies each slot's scales, so W_hi and W_lo
+  // products add directly; with fp32 scales each K-block's products are
+  // folded into it on the VALU.
+  constexpr int NACC = (SCALE != 0 && !SPLIT) ? 1 : 2;
   v16f acc[NACC][NB][MB];
 #pragma unroll
   for (int s = 0; s < NACC; ++s)
@@ -597,7 +638,9 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && NS == 2 && BM == 128 ? 2 : 1))
 #pragma unroll
     for (int s = 0; s < NS; ++s) issue(s);
     // wait for stage 0 only: the DMAs of stages 1 .. NS-1 may stay in flight
-    // (the exponent loads were issued before all of them and are complete)
+    // (the exponent loads were issued before all of them and are complete;
+    // a wave that also loads fp32 scales issues one more per stage, which
+    // only makes this wait longer)
     constexpr int kPro = (NS - 1) * DI;
     __builtin_amdgcn_s_waitcnt((kPro & 15) | (7 << 4) | ((kPro >> 4) << 14));
     __builtin_amdgcn_s_barrier();
@@ -605,6 +648,90 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && NS == 2 && BM == 128 ? 2 : 1))
     pack(sc, raw);
     read_frags(f0, 0, 0);
   }
+  if constexpr (SCALE == 2) {
+    // Per K-block partial products p (fresh accumulators), folded into acc
+    // with the block's fp32 multipliers once the block's MFMAs are done:
+    //   acc += s_a[m] * (s_0[n] * p_0 + s_1[n] * p_1)   (dual)
+    //   acc_s += (s_s[n] * s_a[m]) * p_s                 (split single GEMM)
+    // With 32-wide blocks each 64-wide MFMA is issued twice, once per lane
+    // half: the other half's E8M0 scales are set to 2^-127 on both operands,
+    // which scales its products by 2^-254, far below the smallest fp32
+    // subnormal, so they round to zero.
+    v16f p[2][NB][MB];
+    const v16f zero16 = {};
+    auto mfma_p = [&](const v8i* f, auto fresh, int sl) {
+#pragma unroll
+      for (int i = 0; i < MB; ++i)
+#pragma unroll
+        for (int q = 0; q < NF; ++q) {
+          v16f& c = p[q / NB][q % NB][i];
+          if constexpr (decltype(fresh)::value)
+            c = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f[q], f[NF + i], zero16, BF, AF, 0,
+                                                                 sl, 0, sl);
+          else
+            c = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f[q], f[NF + i], c, BF, AF, 0, sl,
+                                                                 0, sl);
+        }
+    };
+    auto fold = [&](int t, int b) {
+      const float* sb = reinterpret_cast<const float*>(lds + NS * STAGE + (t % 3) * kScB + b * 1024);
+      float sa[MB];
+#pragma unroll
+      for (int i = 0; i < MB; ++i) sa[i] = sb[wm * TMW + i * 32 + lr];
+      // lane holds n rows 8 * (r / 4) + 4 * lg + r % 4 of each 32-row block
+#pragma unroll
+      for (int j = 0; j < NB; ++j)
+#pragma unroll
+        for (int gq = 0; gq < 4; ++gq) {
+          const int c = wn * TNW + j * 32 + 8 * gq + 4 * lg;
+          const float4 u4 = *reinterpret_cast<const float4*>(sb + 128 + c);
+          const float4 v4 = *reinterpret_cast<const float4*>(sb + 192 + c);
+          const float w0[4] = {u4.x, u4.y, u4.z, u4.w}, w1[4] = {v4.x, v4.y, v4.z, v4.w};
+#pragma unroll
+          for (int i = 0; i < MB; ++i)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const int r = 4 * gq + e;
+              if constexpr (SPLIT) {
+                acc[0][j][i][r] = __builtin_fmaf(p[0][j][i][r], w0[e] * sa[i], acc[0][j][i][r]);
+                acc[1][j][i][r] = __builtin_fmaf(p[1][j][i][r], w1[e] * sa[i], acc[1][j][i][r]);
+              } else {
+                const float u = __builtin_fmaf(p[1][j][i][r], w1[e], p[0][j][i][r] * w0[e]);
+                acc[0][j][i][r] = __builtin_fmaf(u, sa[i], acc[0][j][i][r]);
+              }
+            }
+        }
+    };
+    const int bsh = g.bs_shift;
+    auto substep = [&](const v8i* f, int t, int h) {
+      if (bsh == 5) {
+        mfma_p(f, std::true_type{}, lg == 0 ? 127 : 0);
+        fold(t, 2 * h);
+        mfma_p(f, std::true_type{}, lg == 1 ? 127 : 0);
+        fold(t, 2 * h + 1);
+      } else if (bsh == 6) {
+        mfma_p(f, std::true_type{}, 127);
+        fold(t, h);
+      } else if (h == 0) {
+        mfma_p(f, std::true_type{}, 127);
+      } else {
+        mfma_p(f, std::false_type{}, 127);
+        fold(t, 0);
+      }
+    };
+    for (int t = 0; t < nt; ++t) {
+      read_frags(f1, t, 1);
+      substep(f0, t, 0);
+      // stage t + 1 and its scales landed, every wave has its stage-t
+      // fragments and is past stage t - 1's scales: refill t's buffer and
+      // ring slot (t + 2) % 3 == (t - 1) % 3
+      sync_all();
+      issue(t + NS);
+      __builtin_amdgcn_sched_barrier(0);
+      read_frags(f0, t + 1, 0);
+      substep(f1, t, 1);
+    }
+  } else {
   for (int t = 0; t < nt; ++t) {
     // exponents of stage t + 1 (SCALE 1, NS 2): this stage's vmcnt(0) covers them
     load_raw(raw, t + 1);
@@ -623,6 +750,7 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && NS == 2 && BM == 128 ? 2 : 1))
     mfmas(f1, sc, 1);
     interleave();
     pack(sc, raw);
+  }
   }
 
   // ---- epilogue -----------------------------------------------------------
@@ -727,7 +855,7 @@ int launch_gemm(GemmArgs ga, hipStream_t st) {
   const int big_tiles = ((m + 255) / 256) * ((n + (SPLIT ? 255 : 127)) / (SPLIT ? 256 : 128));
   // (block-scaled single GEMMs keep two accumulator sets, which only the
   // small tile fits in registers)
-  const bool small = (SCALE == 1 && SPLIT) || g_tile_policy == 2 || g_tile_policy == 3 ||
+  const bool small = (SCALE == 1 && SPLIT) || SCALE == 2 || g_tile_policy == 2 || g_tile_policy == 3 ||
                      (g_tile_policy == 0 && big_tiles < num_cus());
   const int BMv = small ? 128 : 256, BNv = small ? 64 : 128;
   ga.tiles_m = (m + BMv - 1) / BMv;
@@ -748,7 +876,7 @@ int launch_gemm(GemmArgs ga, hipStream_t st) {
       }
     } else if (small) {
       gemm_nt_dma_kernel<AF, BF, SPLIT, OutT, 4, 128, 64, SCALE, 2><<<grid, 256, 0, st>>>(ga);
-    } else if constexpr (!(SCALE == 1 && SPLIT)) {
+    } else if constexpr (!(SCALE == 1 && SPLIT) && SCALE != 2) {
       gemm_nt_dma_kernel<AF, BF, SPLIT, OutT, 8, 256, 128, SCALE, 2><<<grid, 512, 0, st>>>(ga);
     }
     return hipGetLastError() == hipSuccess ? TCFP_OK : TCFP_ERR_HIP;
@@ -849,6 +977,29 @@ extern "C" int tcfp_block_dual_gemm(const uint8_t* a, int a_fmt, int64_t lda, co
   ga.bs_shift = block == 32 ? 5 : (block == 64 ? 6 : 7);
   ga.bias = bias; ga.out = out; ga.ldo = ldo;
   return dispatch_all<1>(a_fmt, b_fmt, b_lo != nullptr, out_dtype, ga,
+                         static_cast<hipStream_t>(stream));
+}
+
+extern "C" int tcfp_block_dual_gemm_f32s(const uint8_t* a, int a_fmt, int64_t lda,
+                                         const float* s_a, const uint8_t* b_hi,
+                                         const uint8_t* b_lo, int b_fmt, int64_t ldb,
+                                         const float* s_hi, const float* s_lo, int64_t m,
+                                         int64_t n, int64_t k, int block, const float* bias,
+                                         void* out, int out_dtype, int64_t ldo, void* stream) {
+  const int rc = check_common(m, n, k, lda, ldb, ldo, a, b_hi, b_lo, out_dtype);
+  if (rc != TCFP_OK) return rc;
+  if (block != 32 && block != 64 && block != 128) return TCFP_ERR_SHAPE;
+  if (k % block != 0 || m % 4 != 0 || n % 4 != 0) return TCFP_ERR_SHAPE;
+  if (!s_a || !s_hi || (b_lo && !s_lo)) return TCFP_ERR_SHAPE;
+  if (!al16(s_a) || !al16(s_hi) || (b_lo && !al16(s_lo))) return TCFP_ERR_ALIGN;
+  if (m == 0 || n == 0) return TCFP_OK;
+  GemmArgs ga{};
+  ga.A = a; ga.B0 = b_hi; ga.B1 = b_lo ? b_lo : b_hi;
+  ga.M = int(m); ga.N = int(n); ga.K = int(k); ga.lda = lda; ga.ldb = ldb;
+  ga.s_a = s_a; ga.s_0 = s_hi; ga.s_1 = b_lo ? s_lo : s_hi;
+  ga.bs_shift = block == 32 ? 5 : (block == 64 ? 6 : 7);
+  ga.bias = bias; ga.out = out; ga.ldo = ldo;
+  return dispatch_all<2>(a_fmt, b_fmt, b_lo != nullptr, out_dtype, ga,
                          static_cast<hipStream_t>(stream));
 }
 

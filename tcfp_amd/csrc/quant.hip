@@ -1107,11 +1107,17 @@ TCFP_DEV void store_words(uint8_t* dst, const uint32_t* words) {
 
 TCFP_DEV uint32_t wbyte(const uint32_t* words, int j) { return (words[j >> 2] >> (8 * (j & 3))) & 0xFFu; }
 
-template <typename InT, int FMT, int BS>
+// Block scale rules.  F32S == false: the reference's power-of-two exponent
+// (int8 [K/bs, rows]).  F32S == true: to_fp8_e4m3's per-tensor rule
+// (tcfp/core.py:99-106) applied to each block -- scale = FP8_MAX / amax with
+// the reciprocal and the product rounded to the input dtype, codes
+// RNE(clamp(x * scale)) -- storing the fp32 inverse scale 1 / scale
+// ([K/bs, rows]), the block's dequantisation multiplier.
+template <typename InT, int FMT, int BS, bool F32S>
 __global__ __launch_bounds__(kThreads) void block_quant_kernel(const InT* __restrict__ x,
                                                                int64_t m, int64_t k,
                                                                uint8_t* __restrict__ q,
-                                                               int8_t* __restrict__ exps) {
+                                                               void* __restrict__ scales) {
   using G = Seg<InT, BS>;
   constexpr int VEC = G::VEC;
   const int64_t kb = blockIdx.y;
@@ -1131,13 +1137,22 @@ __global__ __launch_bounds__(kThreads) void block_quant_kernel(const InT* __rest
   for (int j = 0; j < VEC; ++j) a = umax(a, absbits(v[j]));
   a = seg_umax<G::L>(a);
   const float mx = FMT == TCFP_FP8_E5M2 ? kE5M2Max : kE4M3Max;
-  const int e = block_exponent(__uint_as_float(a), mx);
-  const float mul = exp2i(-e);
+  float mul, inv = 0.0f;
+  int e = 0;
+  if constexpr (F32S) {
+    scale_from_amax(__uint_as_float(a), sizeof(InT) == 2, mx, &mul, &inv);
+  } else {
+    e = block_exponent(__uint_as_float(a), mx);
+    mul = exp2i(-e);
+  }
 #pragma unroll
   for (int j = 0; j < VEC; ++j) v[j] = clampf(v[j] * mul, mx);
   if (valid) {
     encodeN<VEC, FMT>(v, q + off);
-    if (li == 0) exps[kb * m + row] = int8_t(e);
+    if (li == 0) {
+      if constexpr (F32S) static_cast<float*>(scales)[kb * m + row] = inv;
+      else static_cast<int8_t*>(scales)[kb * m + row] = int8_t(e);
+    }
   }
 }
 
@@ -1161,11 +1176,14 @@ TCFP_DEV uint32_t sr_block(float x, float u) {
 
 // Fused block dual quantisation + error update (tcfp/kernels.py:288-459 and
 // :1867-1873).  The error buffer is read and rewritten by the same lane.
-template <typename InT, int BS, bool HAS_EF, bool UPDATE, bool SR>
+// With F32S the two components use the fp32 block rule above on the fp32
+// values w + e and r (no zero-block sentinel: a zero residual gets the
+// clamped 1e-12 amax and zero codes).
+template <typename InT, int BS, bool HAS_EF, bool UPDATE, bool SR, bool F32S>
 __global__ __launch_bounds__(kThreads) void block_dualq_kernel(
     const InT* __restrict__ w, float* __restrict__ ef, int64_t n, int64_t k,
-    uint8_t* __restrict__ hi, uint8_t* __restrict__ lo, int8_t* __restrict__ ehi,
-    int8_t* __restrict__ elo, uint32_t k0, uint32_t k1, uint32_t off0, uint32_t off1) {
+    uint8_t* __restrict__ hi, uint8_t* __restrict__ lo, void* __restrict__ shi,
+    void* __restrict__ slo, uint32_t k0, uint32_t k1, uint32_t off0, uint32_t off1) {
   using G = Seg<InT, BS>;
   constexpr int VEC = G::VEC;
   const int64_t kb = blockIdx.y;
@@ -1199,8 +1217,15 @@ __global__ __launch_bounds__(kThreads) void block_dualq_kernel(
 #pragma unroll
   for (int j = 0; j < VEC; ++j) a = umax(a, absbits(v[j]));
   a = seg_umax<G::L>(a);
-  const int e_hi = block_exponent(__uint_as_float(a), kE4M3Max);
-  const float mul_hi = exp2i(-e_hi), s_hi = exp2i(e_hi);
+  int e_hi = 0;
+  float mul_hi, s_hi;
+  if constexpr (F32S) {
+    scale_from_amax(__uint_as_float(a), false, kE4M3Max, &mul_hi, &s_hi);
+  } else {
+    e_hi = block_exponent(__uint_as_float(a), kE4M3Max);
+    mul_hi = exp2i(-e_hi);
+    s_hi = exp2i(e_hi);
+  }
   float c[VEC];
 #pragma unroll
   for (int j = 0; j < VEC; ++j) c[j] = clampf(v[j] * mul_hi, kE4M3Max);
@@ -1217,9 +1242,15 @@ __global__ __launch_bounds__(kThreads) void block_dualq_kernel(
   // W_lo
   b = seg_umax<G::L>(b);
   const float amax_lo = __uint_as_float(b);
-  const bool zero = amax_lo < 1e-12f;
-  const int e_lo = block_exponent(amax_lo, kE4M3Max);
-  const float mul_lo = zero ? 1.0f : exp2i(-e_lo);
+  const bool zero = !F32S && amax_lo < 1e-12f;
+  int e_lo = 0;
+  float mul_lo, inv_lo = 0.0f;
+  if constexpr (F32S) {
+    scale_from_amax(amax_lo, false, kE4M3Max, &mul_lo, &inv_lo);
+  } else {
+    e_lo = block_exponent(amax_lo, kE4M3Max);
+    mul_lo = zero ? 1.0f : exp2i(-e_lo);
+  }
 #pragma unroll
   for (int j = 0; j < VEC; ++j) c[j] = clampf(r[j] * mul_lo, kE4M3Max);
   uint32_t lc[VEC / 4];
@@ -1241,11 +1272,16 @@ __global__ __launch_bounds__(kThreads) void block_dualq_kernel(
     store_words<VEC>(hi + off, hc);
     store_words<VEC>(lo + off, lc);
     if (li == 0) {
-      ehi[kb * n + row] = int8_t(e_hi);
-      elo[kb * n + row] = int8_t(e_lo_store);
+      if constexpr (F32S) {
+        static_cast<float*>(shi)[kb * n + row] = s_hi;
+        static_cast<float*>(slo)[kb * n + row] = inv_lo;
+      } else {
+        static_cast<int8_t*>(shi)[kb * n + row] = int8_t(e_hi);
+        static_cast<int8_t*>(slo)[kb * n + row] = int8_t(e_lo_store);
+      }
     }
     if constexpr (HAS_EF && UPDATE) {
-      const float s_lo = exp2i(e_lo_store);
+      const float s_lo = F32S ? inv_lo : exp2i(e_lo_store);
       float e[VEC];
 #pragma unroll
       for (int j = 0; j < VEC; ++j) e[j] = (W[j] - dh[j]) - e4m3_to_f32(wbyte(lc, j)) * s_lo;
@@ -1254,16 +1290,19 @@ __global__ __launch_bounds__(kThreads) void block_dualq_kernel(
   }
 }
 
-template <int FMT>
+template <int FMT, bool F32S>
 __global__ __launch_bounds__(kThreads) void block_dequant_kernel(const uint8_t* __restrict__ q,
-                                                                 const int8_t* __restrict__ exps,
+                                                                 const void* __restrict__ scales,
                                                                  int64_t m, int64_t k, int bs,
                                                                  float* __restrict__ out) {
   const int64_t n = m * k;
   const int64_t stride = int64_t(gridDim.x) * kThreads;
   for (int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x; i < n; i += stride) {
     const int64_t r = i / k, c = i - r * k;
-    out[i] = fp8_to_f32<FMT>(q[i]) * exp2i(exps[(c / bs) * m + r]);
+    const int64_t si = (c / bs) * m + r;
+    const float s = F32S ? static_cast<const float*>(scales)[si]
+                         : exp2i(static_cast<const int8_t*>(scales)[si]);
+    out[i] = fp8_to_f32<FMT>(q[i]) * s;
   }
 }
 
@@ -1627,8 +1666,13 @@ int tcfp_dual_quantize_per_tensor(const void* w, int w_dtype, int64_t n, int64_t
   return launch_status();
 }
 
-int tcfp_block_quantize(const void* x, int x_dtype, int64_t m, int64_t k, int block,
-                        int fp8_fmt, uint8_t* q, int8_t* exps, void* stream) {
+}  // extern "C"
+
+namespace {
+
+template <bool F32S>
+int block_quantize_impl(const void* x, int x_dtype, int64_t m, int64_t k, int block, int fp8_fmt,
+                        uint8_t* q, void* scales, hipStream_t st) {
   if (m < 0 || k < 0) return TCFP_ERR_SHAPE;
   if (block != 32 && block != 64 && block != 128) return TCFP_ERR_SHAPE;
   if (k % block != 0) return TCFP_ERR_SHAPE;
@@ -1636,13 +1680,12 @@ int tcfp_block_quantize(const void* x, int x_dtype, int64_t m, int64_t k, int bl
   if (fp8_fmt != TCFP_FP8_E4M3 && fp8_fmt != TCFP_FP8_E5M2) return TCFP_ERR_DTYPE;
   if (!aligned16(x) || !aligned16(q)) return TCFP_ERR_ALIGN;
   if (m == 0 || k == 0) return TCFP_OK;
-  hipStream_t st = static_cast<hipStream_t>(stream);
   const unsigned kbs = unsigned(k / block);
 #define TCFP_BQ(T, F, B)                                                                    \
   do {                                                                                      \
     dim3 grid(unsigned((m + Seg<T, B>::ROWS - 1) / Seg<T, B>::ROWS), kbs);                  \
-    block_quant_kernel<T, F, B><<<grid, kThreads, 0, st>>>(static_cast<const T*>(x), m, k,  \
-                                                           q, exps);                        \
+    block_quant_kernel<T, F, B, F32S><<<grid, kThreads, 0, st>>>(static_cast<const T*>(x),  \
+                                                                 m, k, q, scales);          \
   } while (0)
 #define TCFP_BQ_B(T, F)                                 \
   do {                                                  \
@@ -1660,10 +1703,11 @@ int tcfp_block_quantize(const void* x, int x_dtype, int64_t m, int64_t k, int bl
   return launch_status();
 }
 
-int tcfp_block_dual_quantize(const void* w, int w_dtype, int64_t n, int64_t k, int block,
+template <bool F32S>
+int block_dual_quantize_impl(const void* w, int w_dtype, int64_t n, int64_t k, int block,
                              float* ef, int update_ef, int stochastic_lo, uint64_t seed,
-                             uint64_t offset, uint8_t* w_hi, uint8_t* w_lo, int8_t* e_hi,
-                             int8_t* e_lo, void* stream) {
+                             uint64_t offset, uint8_t* w_hi, uint8_t* w_lo, void* s_hi,
+                             void* s_lo, hipStream_t st) {
   if (n < 0 || k < 0) return TCFP_ERR_SHAPE;
   if (block != 32 && block != 64 && block != 128) return TCFP_ERR_SHAPE;
   if (k % block != 0) return TCFP_ERR_SHAPE;
@@ -1672,7 +1716,6 @@ int tcfp_block_dual_quantize(const void* w, int w_dtype, int64_t n, int64_t k, i
   if (!aligned16(w) || !aligned16(w_hi) || !aligned16(w_lo) || (ef && !aligned16(ef)))
     return TCFP_ERR_ALIGN;
   if (n == 0 || k == 0) return TCFP_OK;
-  hipStream_t st = static_cast<hipStream_t>(stream);
   const unsigned kbs = unsigned(k / block);
   const uint32_t k0 = uint32_t(seed), k1 = uint32_t(seed >> 32);
   const uint32_t o0 = uint32_t(offset), o1 = uint32_t(offset >> 32);
@@ -1680,8 +1723,8 @@ int tcfp_block_dual_quantize(const void* w, int w_dtype, int64_t n, int64_t k, i
 #define TCFP_BDQ(T, B, EF, UP, SR)                                                             \
   do {                                                                                         \
     dim3 grid(unsigned((n + Seg<T, B>::ROWS - 1) / Seg<T, B>::ROWS), kbs);                     \
-    block_dualq_kernel<T, B, EF, UP, SR><<<grid, kThreads, 0, st>>>(                           \
-        static_cast<const T*>(w), ef, n, k, w_hi, w_lo, e_hi, e_lo, k0, k1, o0, o1);           \
+    block_dualq_kernel<T, B, EF, UP, SR, F32S><<<grid, kThreads, 0, st>>>(                     \
+        static_cast<const T*>(w), ef, n, k, w_hi, w_lo, s_hi, s_lo, k0, k1, o0, o1);           \
   } while (0)
 #define TCFP_BDQ_MODE(T, B)                                     \
   do {                                                          \
@@ -1703,18 +1746,64 @@ int tcfp_block_dual_quantize(const void* w, int w_dtype, int64_t n, int64_t k, i
   return launch_status();
 }
 
-int tcfp_block_dequantize(const uint8_t* q, int fp8_fmt, const int8_t* exps, int64_t m,
-                          int64_t k, int block, float* out, void* stream) {
+template <bool F32S>
+int block_dequantize_impl(const uint8_t* q, int fp8_fmt, const void* scales, int64_t m,
+                          int64_t k, int block, float* out, hipStream_t st) {
   if (m < 0 || k < 0 || block <= 0 || k % block != 0) return TCFP_ERR_SHAPE;
   if (fp8_fmt != TCFP_FP8_E4M3 && fp8_fmt != TCFP_FP8_E5M2) return TCFP_ERR_DTYPE;
   if (m == 0 || k == 0) return TCFP_OK;
-  hipStream_t st = static_cast<hipStream_t>(stream);
   const int g = grid_for(m * k, 16);
   if (fp8_fmt == TCFP_FP8_E5M2)
-    block_dequant_kernel<TCFP_FP8_E5M2><<<g, kThreads, 0, st>>>(q, exps, m, k, block, out);
+    block_dequant_kernel<TCFP_FP8_E5M2, F32S><<<g, kThreads, 0, st>>>(q, scales, m, k, block, out);
   else
-    block_dequant_kernel<TCFP_FP8_E4M3><<<g, kThreads, 0, st>>>(q, exps, m, k, block, out);
+    block_dequant_kernel<TCFP_FP8_E4M3, F32S><<<g, kThreads, 0, st>>>(q, scales, m, k, block, out);
   return launch_status();
+}
+
+}  // namespace
+
+extern "C" {
+
+int tcfp_block_quantize(const void* x, int x_dtype, int64_t m, int64_t k, int block,
+                        int fp8_fmt, uint8_t* q, int8_t* exps, void* stream) {
+  return block_quantize_impl<false>(x, x_dtype, m, k, block, fp8_fmt, q, exps,
+                                    static_cast<hipStream_t>(stream));
+}
+
+int tcfp_block_quantize_f32s(const void* x, int x_dtype, int64_t m, int64_t k, int block,
+                             int fp8_fmt, uint8_t* q, float* inv_scales, void* stream) {
+  return block_quantize_impl<true>(x, x_dtype, m, k, block, fp8_fmt, q, inv_scales,
+                                   static_cast<hipStream_t>(stream));
+}
+
+int tcfp_block_dual_quantize(const void* w, int w_dtype, int64_t n, int64_t k, int block,
+                             float* ef, int update_ef, int stochastic_lo, uint64_t seed,
+                             uint64_t offset, uint8_t* w_hi, uint8_t* w_lo, int8_t* e_hi,
+                             int8_t* e_lo, void* stream) {
+  return block_dual_quantize_impl<false>(w, w_dtype, n, k, block, ef, update_ef, stochastic_lo,
+                                         seed, offset, w_hi, w_lo, e_hi, e_lo,
+                                         static_cast<hipStream_t>(stream));
+}
+
+int tcfp_block_dual_quantize_f32s(const void* w, int w_dtype, int64_t n, int64_t k, int block,
+                                  float* ef, int update_ef, int stochastic_lo, uint64_t seed,
+                                  uint64_t offset, uint8_t* w_hi, uint8_t* w_lo, float* inv_hi,
+                                  float* inv_lo, void* stream) {
+  return block_dual_quantize_impl<true>(w, w_dtype, n, k, block, ef, update_ef, stochastic_lo,
+                                        seed, offset, w_hi, w_lo, inv_hi, inv_lo,
+                                        static_cast<hipStream_t>(stream));
+}
+
+int tcfp_block_dequantize(const uint8_t* q, int fp8_fmt, const int8_t* exps, int64_t m,
+                          int64_t k, int block, float* out, void* stream) {
+  return block_dequantize_impl<false>(q, fp8_fmt, exps, m, k, block, out,
+                                      static_cast<hipStream_t>(stream));
+}
+
+int tcfp_block_dequantize_f32s(const uint8_t* q, int fp8_fmt, const float* inv_scales, int64_t m,
+                               int64_t k, int block, float* out, void* stream) {
+  return block_dequantize_impl<true>(q, fp8_fmt, inv_scales, m, k, block, out,
+                                     static_cast<hipStream_t>(stream));
 }
 
 int tcfp_transpose_u8(const uint8_t* src, int64_t rows, int64_t cols, uint8_t* dst,

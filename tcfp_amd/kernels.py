@@ -329,16 +329,35 @@ def fp8_gemm_nt(
 # ---------------------------------------------------------------------------
 
 
+_SCALE_FORMATS = ("exponent", "fp32")
+
+
+def _scale_format(scale_format: str) -> bool:
+    """True for fp32 block multipliers, False for the reference's exponents."""
+    if scale_format not in _SCALE_FORMATS:
+        raise ValueError(f"scale_format must be one of {_SCALE_FORMATS}, got {scale_format!r}")
+    return scale_format == "fp32"
+
+
 def block_quantize_fp8(
     tensor: torch.Tensor,
     block_size: int = 128,
     fp8_dtype: torch.dtype = torch.float8_e4m3fn,
+    *,
+    scale_format: str = "exponent",
 ) -> tuple[torch.Tensor, torch.Tensor]:
-    """Per-(row, K-block) FP8 quantisation; returns ``(fp8 [M,K], int8 exps
-    [K // block_size, M])`` with scale = 2^exp.
+    """Per-(row, K-block) FP8 quantisation; returns ``(fp8 [M,K], scales
+    [K // block_size, M])``.
 
     Reference: ``block_quantize_fp8`` (``tcfp/kernels.py:1675-1722``).
+    ``scale_format="exponent"`` (the reference's format): int8 exponents,
+    block value = fp8 * 2^exp.  ``scale_format="fp32"``: ``to_fp8_e4m3`` /
+    ``to_fp8_e5m2`` (``tcfp/core.py:85-106, 137-158``) applied per block
+    (scale = FP8_MAX / amax, not a power of two); the scales returned are
+    the fp32 dequantisation multipliers ``1 / scale``, block value =
+    fp8 * multiplier.
     """
+    f32s = _scale_format(scale_format)
     dev = _hip.require_gpu(tensor)
     M, K = tensor.shape
     assert K % block_size == 0, f"K ({K}) must be divisible by block_size ({block_size})"
@@ -346,15 +365,15 @@ def block_quantize_fp8(
         raise ValueError(f"block_size must be 32, 64, or 128, got {block_size}")
     x = tensor if tensor.is_contiguous() else tensor.contiguous()
     q = torch.empty((M, K), dtype=fp8_dtype, device=dev)
-    exps = torch.empty((K // block_size, M), dtype=torch.int8, device=dev)
+    scales = torch.empty((K // block_size, M), dtype=torch.float32 if f32s else torch.int8,
+                         device=dev)
+    fn = _hip.lib().tcfp_block_quantize_f32s if f32s else _hip.lib().tcfp_block_quantize
     check(
-        _hip.lib().tcfp_block_quantize(
-            ptr(x), _in_dtype(x), M, K, block_size, _fmt(fp8_dtype), ptr(q), ptr(exps),
-            _hip.stream_of(dev),
-        ),
+        fn(ptr(x), _in_dtype(x), M, K, block_size, _fmt(fp8_dtype), ptr(q), ptr(scales),
+           _hip.stream_of(dev)),
         "block_quantize_fp8",
     )
-    return q, exps
+    return q, scales
 
 
 def block_dequantize_fp8(
@@ -362,19 +381,20 @@ def block_dequantize_fp8(
     block_scales: torch.Tensor,
     block_size: int,
 ) -> torch.Tensor:
-    """``fp8 * 2^exp`` -> fp32 [M, K] (reference ``tcfp/kernels.py:1725-1746``)."""
+    """``fp8 * 2^exp`` (int8 exponents) or ``fp8 * multiplier`` (fp32
+    multipliers) -> fp32 [M, K] (reference ``tcfp/kernels.py:1725-1746``)."""
     dev = _hip.require_gpu(fp8_tensor, block_scales)
     M, K = fp8_tensor.shape
     q = fp8_tensor.contiguous()
     e = block_scales.contiguous()
-    assert e.dtype == torch.int8 and tuple(e.shape) == (K // block_size, M), (
-        f"block_scales must be int8 ({K // block_size}, {M})"
+    assert e.dtype in (torch.int8, torch.float32) and tuple(e.shape) == (K // block_size, M), (
+        f"block_scales must be int8 or float32 ({K // block_size}, {M})"
     )
     out = torch.empty((M, K), dtype=torch.float32, device=dev)
+    fn = (_hip.lib().tcfp_block_dequantize_f32s if e.dtype == torch.float32
+          else _hip.lib().tcfp_block_dequantize)
     check(
-        _hip.lib().tcfp_block_dequantize(
-            ptr(q), _fmt(q.dtype), ptr(e), M, K, block_size, ptr(out), _hip.stream_of(dev)
-        ),
+        fn(ptr(q), _fmt(q.dtype), ptr(e), M, K, block_size, ptr(out), _hip.stream_of(dev)),
         "block_dequantize_fp8",
     )
     return out
@@ -387,6 +407,8 @@ def fused_dual_quantize_fp8(
     stochastic_lo: bool = False,
     update_ef: bool = True,
     seed: int | None = None,
+    *,
+    scale_format: str = "exponent",
 ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
     """W (+ EF) -> ``(w_hi, w_lo, scales_hi, scales_lo)``, one HBM pass.
 
@@ -395,8 +417,11 @@ def fused_dual_quantize_fp8(
     (``:1867-1873``) happens inside the same kernel here; ``error_buf`` is
     modified in place (unless ``update_ef=False``).  Scales are int8
     exponents [K // block_size, N]; W_lo blocks with zero residual carry
-    the -128 sentinel.
+    the -128 sentinel.  ``scale_format="fp32"`` quantises both components
+    with the per-block ``to_fp8_e4m3`` rule of :func:`block_quantize_fp8`
+    and returns fp32 multipliers (no sentinel).
     """
+    f32s = _scale_format(scale_format)
     assert weight.is_contiguous(), "Weight must be contiguous (N, K) row-major"
     N, K = weight.shape
     assert K % block_size == 0, f"K ({K}) must be divisible by block_size ({block_size})"
@@ -417,12 +442,14 @@ def fused_dual_quantize_fp8(
     num_kb = K // block_size
     w_hi = torch.empty((N, K), dtype=torch.float8_e4m3fn, device=dev)
     w_lo = torch.empty((N, K), dtype=torch.float8_e4m3fn, device=dev)
-    sh = torch.empty((num_kb, N), dtype=torch.int8, device=dev)
-    sl = torch.empty((num_kb, N), dtype=torch.int8, device=dev)
+    sdt = torch.float32 if f32s else torch.int8
+    sh = torch.empty((num_kb, N), dtype=sdt, device=dev)
+    sl = torch.empty((num_kb, N), dtype=sdt, device=dev)
     if stochastic_lo and seed is None:
         seed = int(torch.randint(0, 2**62, (1,)).item())
+    fn = _hip.lib().tcfp_block_dual_quantize_f32s if f32s else _hip.lib().tcfp_block_dual_quantize
     check(
-        _hip.lib().tcfp_block_dual_quantize(
+        fn(
             ptr(weight), _in_dtype(weight), N, K, block_size, ptr(error_buf),
             int(bool(update_ef)), int(bool(stochastic_lo)), int(seed or 0), 0, ptr(w_hi),
             ptr(w_lo), ptr(sh), ptr(sl), _hip.stream_of(dev),
@@ -437,9 +464,11 @@ def fused_dual_quantize_fp8(
 # ---------------------------------------------------------------------------
 
 
-def _block_exps(e: torch.Tensor, rows: int, num_kb: int, name: str) -> torch.Tensor:
-    if e.dtype != torch.int8:
-        raise TypeError(f"{name} must be int8 power-of-two exponents, got {e.dtype}")
+def _block_exps(e: torch.Tensor, rows: int, num_kb: int, name: str,
+                dtype: torch.dtype = torch.int8) -> torch.Tensor:
+    if e.dtype != dtype:
+        what = "int8 power-of-two exponents" if dtype == torch.int8 else "float32 multipliers"
+        raise TypeError(f"{name} must be {what} like the other scales, got {e.dtype}")
     if tuple(e.shape) != (num_kb, rows):
         raise ValueError(f"{name} must have shape ({num_kb}, {rows}), got {tuple(e.shape)}")
     return e if e.is_contiguous() else e.contiguous()
@@ -456,17 +485,21 @@ def _block_gemm(a, e_a, b_hi, b_lo, e_hi, e_lo, block_size, bias, out_dtype):
     if block_size not in (32, 64, 128):
         raise ValueError(f"block_size must be 32, 64, or 128, got {block_size}")
     num_kb = k // block_size
-    e_a = _block_exps(e_a, m, num_kb, "scales_a")
-    e_hi = _block_exps(e_hi, n, num_kb, "scales_b")
-    e_lo = _block_exps(e_lo, n, num_kb, "scales_lo") if b_lo is not None else None
+    # int8 exponents (the reference's format) or fp32 multipliers, not mixed
+    sdt = torch.float32 if e_a.dtype == torch.float32 else torch.int8
+    e_a = _block_exps(e_a, m, num_kb, "scales_a", sdt)
+    e_hi = _block_exps(e_hi, n, num_kb, "scales_b", sdt)
+    e_lo = _block_exps(e_lo, n, num_kb, "scales_lo", sdt) if b_lo is not None else None
     if b_lo is not None and b_hi.stride(0) != b_lo.stride(0):
         b_hi, b_lo = b_hi.contiguous(), b_lo.contiguous()
     out = torch.empty((m, n), dtype=out_dtype, device=dev)
     if bias is not None:
         bias = bias.to(torch.float32).contiguous()
         assert bias.shape == (n,), f"bias shape {tuple(bias.shape)} != ({n},)"
+    fn = (_hip.lib().tcfp_block_dual_gemm_f32s if sdt == torch.float32
+          else _hip.lib().tcfp_block_dual_gemm)
     check(
-        _hip.lib().tcfp_block_dual_gemm(
+        fn(
             ptr(a), _fmt(a.dtype), a.stride(0), ptr(e_a), ptr(b_hi), ptr(b_lo),
             _fmt(b_hi.dtype), b_hi.stride(0), ptr(e_hi), ptr(e_lo), m, n, k, block_size,
             ptr(bias), ptr(out), _out_dtype(out_dtype), n, _hip.stream_of(dev),
@@ -490,7 +523,9 @@ def block_scaled_gemm(
     Reference: ``block_scaled_gemm`` (``tcfp/kernels.py:1878-1936``).
     A [M, K], B [N, K] FP8; scales are the int8 exponents
     ``[K // block_size, rows]`` produced by ``block_quantize_fp8``.  The
-    exponents enter the MFMA as hardware E8M0 block scales.
+    exponents enter the MFMA as hardware E8M0 block scales.  fp32
+    multipliers (``scale_format="fp32"``; both operands) are accepted too:
+    ``C = sum_kb sa[kb,m] sb[kb,n] (A_kb @ B_kb^T)``.
     """
     M, K = a_fp8.shape
     N, K2 = b_fp8.shape
@@ -521,6 +556,9 @@ def fused_block_scaled_dual_gemm_forward(
     ``launch_mult`` are scheduling hints of the reference's Triton kernel;
     they do not change the result and are accepted for API compatibility
     (the W_lo skip is output-neutral: skipped blocks hold zero codes).
+    fp32 block multipliers for all three operands (``scale_format="fp32"``
+    quantisers) select the fp32-scale kernel: the same sum with the
+    multipliers in place of 2^exp.
     """
     M, K = act_fp8.shape
     N, K2 = w_hi_fp8.shape

@@ -230,6 +230,69 @@ def test_block_dual_zero_residual_sentinel():
     assert ((el >= -126) | (el == -128)).all()
 
 
+# ----------------------------------- fp32 (non-power-of-two) block scales
+@pytest.mark.parametrize("bs", [32, 64, 128])
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("fmt", [ofp8.E4M3, ofp8.E5M2])
+def test_block_quantize_f32s_is_per_tensor_rule_per_block(bs, dtype, fmt):
+    # each (row, K-block) must equal to_fp8_per_tensor (pinned against torch
+    # above) run on that block alone
+    rng = np.random.default_rng(11 + bs)
+    x = (rng.standard_normal((5, 3 * bs)) * 2.0 ** rng.integers(-12, 12, (5, 3, 1)).repeat(bs, -1)
+         .reshape(5, 3 * bs)).astype(np.float32)
+    if dtype == "bf16":
+        x = ofp8.bf16_round(x)
+    x[2, :bs] = 0.0  # an all-zero block: amax clamps to 1e-12
+    codes, inv = oq.block_quantize_f32s(x, bs, dtype, fmt)
+    assert inv.shape == (3, 5) and inv.dtype == np.float32
+    for r in range(5):
+        for b in range(3):
+            c, i, _ = oq.to_fp8_per_tensor(x[r, b * bs:(b + 1) * bs], dtype, fmt)
+            assert np.array_equal(codes[r, b * bs:(b + 1) * bs], c), (r, b)
+            assert inv[b, r] == i, (r, b)
+    # and the scales are not the power-of-two exponents of the reference format
+    assert not np.all(np.log2(inv) == np.round(np.log2(inv)))
+
+
+@pytest.mark.parametrize("bs", [32, 128])
+def test_block_dual_f32s_is_per_tensor_dual_per_block(bs):
+    # codes and multipliers of every block equal the per-tensor dual quant
+    # (nn/__init__.py:343-383, pinned above) of that block; the error update
+    # follows the block path's (w - deq_hi) - deq_lo order
+    rng = np.random.default_rng(12)
+    w = rng.standard_normal((6, 2 * bs)).astype(np.float32)
+    ef = (rng.standard_normal(w.shape) * 1e-3).astype(np.float32)
+    w[3, :bs] = 0.5  # exact in E4M3: zero residual block
+    ef[3, :bs] = 0.0
+    hi, lo, ih, il, ef_new = oq.block_dual_quantize_f32s(w, bs, ef)
+    for r in range(6):
+        for b in range(2):
+            sl = slice(b * bs, (b + 1) * bs)
+            h2, l2, ih2, il2, ef2, _ = oq.dual_quant_per_tensor(w[r, sl], ef[r, sl])
+            assert np.array_equal(hi[r, sl], h2) and np.array_equal(lo[r, sl], l2), (r, b)
+            assert ih[b, r] == ih2 and il[b, r] == il2, (r, b)
+            # same quantity, other rounding order: within an ulp of |w|
+            assert np.allclose(ef_new[r, sl], ef2, rtol=0, atol=2.0 ** -22), (r, b)
+    assert (lo[3, :bs] == 0).all()
+    deq = oq.block_dequantize_f32s(hi, ih, bs) + oq.block_dequantize_f32s(lo, il, bs)
+    assert np.abs(ef_new - (w - deq)).max() <= 2.0 ** -22
+
+
+def test_block_gemm_f32s_reduces_to_exponent_gemm():
+    # with power-of-two multipliers the fp32-scale GEMM is the reference
+    # format's block GEMM (kernels.py:1939-2028)
+    rng = np.random.default_rng(13)
+    bs = 32
+    a, ea = oq.block_quantize(rng.standard_normal((8, 4 * bs)).astype(np.float32), bs)
+    w = rng.standard_normal((6, 4 * bs)).astype(np.float32)
+    hi, lo, eh, el, _ = oq.block_dual_quantize(w, bs)
+    assert (el != -128).all()
+    got = og.block_dual_gemm_f32s_nt(a, np.exp2(ea.astype(np.float32)), hi, lo,
+                                     np.exp2(eh.astype(np.float32)), np.exp2(el.astype(np.float32)), bs)
+    ref = og.block_dual_gemm_nt(a, ea, hi, lo, eh, el, bs)
+    assert np.allclose(got, ref, rtol=1e-12, atol=0)
+
+
 # ------------------------------------------------------- GEMM oracle
 def test_dual_gemm_oracle_closed_forms():
     rng = np.random.default_rng(8)
