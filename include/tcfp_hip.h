@@ -220,6 +220,22 @@ int tcfp_block_dual_gemm_f32s(const uint8_t* a, int a_fmt, int64_t lda, const fl
                               int64_t k, int block, const float* bias, void* out,
                               int out_dtype, int64_t ldo, void* stream);
 
+/* Weight quantisation + block dual GEMM in one call.  Replaces
+ * fused_wtquant_block_scaled_dual_gemm_forward (tcfp/kernels.py:2152-2323,
+ * kernel :1233-1531): W [n, k] f32/bf16 (+ ef) is dual-quantised as
+ * tcfp_block_dual_quantize (error buffer updated in place, or W_lo
+ * stochastically rounded) into the caller's w_hi / w_lo [n, k] and
+ * e_hi / e_lo [k/block, n], then out = tcfp_block_dual_gemm(a, ...).
+ * Runs as two launches on `stream`: one streaming pass over W and the
+ * GEMM.  w_hi/w_lo are always written (the GEMM reads them).
+ *   constraints as tcfp_block_dual_quantize and tcfp_block_dual_gemm. */
+int tcfp_wtquant_block_dual_gemm(const uint8_t* a, int a_fmt, int64_t lda, const int8_t* e_a,
+                                 const void* w, int w_dtype, int64_t m, int64_t n, int64_t k,
+                                 int block, float* ef, int stochastic_lo, uint64_t seed,
+                                 uint64_t offset, uint8_t* w_hi, uint8_t* w_lo, int8_t* e_hi,
+                                 int8_t* e_lo, const float* bias, void* out, int out_dtype,
+                                 int64_t ldo, void* stream);
+
 /* Block-scaled dual dgrad:
  *   dx[i,k] = sum_n 2^eg[n/block,i] G[i,n] * ( 2^ehi[k/block,n] W_hi[n,k]
  *                                          + 2^elo[k/block,n] W_lo[n,k] )

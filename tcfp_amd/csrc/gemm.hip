@@ -1003,6 +1003,31 @@ extern "C" int tcfp_block_dual_gemm_f32s(const uint8_t* a, int a_fmt, int64_t ld
                          static_cast<hipStream_t>(stream));
 }
 
+// Weight quantisation + block dual GEMM (the reference's single-kernel
+// fused_wtquant_block_scaled_dual_gemm_forward).  Quantising W inside the
+// GEMM would repeat the amax/convert work in every M-tile workgroup; one
+// streaming dual-quant pass (with the error update) followed by the GEMM
+// reads W once and moves only the FP8 codes through HBM again.
+extern "C" int tcfp_wtquant_block_dual_gemm(const uint8_t* a, int a_fmt, int64_t lda,
+                                            const int8_t* e_a, const void* w, int w_dtype,
+                                            int64_t m, int64_t n, int64_t k, int block,
+                                            float* ef, int stochastic_lo, uint64_t seed,
+                                            uint64_t offset, uint8_t* w_hi, uint8_t* w_lo,
+                                            int8_t* e_hi, int8_t* e_lo, const float* bias,
+                                            void* out, int out_dtype, int64_t ldo,
+                                            void* stream) {
+  if (!a || !e_a || !w || !w_hi || !w_lo || !e_hi || !e_lo) return TCFP_ERR_SHAPE;
+  const int rc = check_common(m, n, k, lda, k, ldo, a, w_hi, w_lo, out_dtype);
+  if (rc != TCFP_OK) return rc;
+  if (block != 32 && block != 64 && block != 128) return TCFP_ERR_SHAPE;
+  if (k % block != 0) return TCFP_ERR_SHAPE;
+  const int q = tcfp_block_dual_quantize(w, w_dtype, n, k, block, ef, 1, stochastic_lo, seed,
+                                         offset, w_hi, w_lo, e_hi, e_lo, stream);
+  if (q != TCFP_OK) return q;
+  return tcfp_block_dual_gemm(a, a_fmt, lda, e_a, w_hi, w_lo, TCFP_FP8_E4M3, k, e_hi, e_lo, m, n,
+                              k, block, bias, out, out_dtype, ldo, stream);
+}
+
 extern "C" int tcfp_gemm_set_tile_policy(int policy) {
   if (policy < 0 || policy > 3) return TCFP_ERR_SHAPE;
   g_tile_policy = policy;

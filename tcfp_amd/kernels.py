@@ -610,6 +610,81 @@ def fused_act_quant_dual_gemm_forward(
     return out, None, None
 
 
+def fused_wtquant_block_scaled_dual_gemm_forward(
+    act_fp8: torch.Tensor,
+    weight: torch.Tensor,
+    act_scales: torch.Tensor,
+    block_size: int,
+    error_buf: torch.Tensor | None = None,
+    stochastic_lo: bool = False,
+    save_w_lo: bool = True,
+    sparse_threshold: float = 0.0,
+    persistent: bool = True,
+    launch_mult: int = 1,
+    *,
+    seed: int | None = None,
+    bias: torch.Tensor | None = None,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor | None, torch.Tensor, torch.Tensor | None]:
+    """Weight dual-quantisation (+ EF) and block-scaled dual GEMM.
+
+    Reference: ``fused_wtquant_block_scaled_dual_gemm_forward``
+    (``tcfp/kernels.py:2152-2323``, kernel ``:1233-1531``).  W [N, K]
+    bf16/fp32 (+ ``error_buf``) is dual-quantised exactly as
+    ``fused_dual_quantize_fp8`` (error buffer rewritten in place with
+    ``W - deq(hi) - deq(lo)``, the reference's post-step ``:2311-2319``),
+    then ``out = fused_block_scaled_dual_gemm_forward``.  Returns ``(out
+    fp32 [M, N], w_hi, w_lo | None, scales_hi, scales_lo | None)``; W_lo and
+    its scales are None when ``save_w_lo`` is False (ABD).  One C-ABI call,
+    two launches (the streaming weight pass and the GEMM).
+    ``sparse_threshold``, ``persistent`` and ``launch_mult`` are the
+    reference's scheduling hints and do not change the result.
+    """
+    assert act_fp8.is_contiguous() and weight.is_contiguous(), (
+        "Activations and weight must be contiguous"
+    )
+    M, K = act_fp8.shape
+    N, K2 = weight.shape
+    assert K == K2, f"K mismatch: act ({K}) vs weight ({K2})"
+    assert K % block_size == 0, f"K ({K}) must be divisible by block_size ({block_size})"
+    if stochastic_lo and error_buf is not None:
+        raise ValueError(
+            "stochastic_lo and error_buf are mutually exclusive "
+            "(SRR eliminates the error-feedback buffer)"
+        )
+    if block_size not in (32, 64, 128):
+        raise ValueError(f"block_size must be 32, 64, or 128, got {block_size}")
+    if error_buf is not None:
+        assert error_buf.dtype == torch.float32 and tuple(error_buf.shape) == (N, K), (
+            "error_buf must be float32 with the weight's shape"
+        )
+        assert error_buf.is_contiguous(), "error_buf must be contiguous"
+    dev = _hip.require_gpu(act_fp8, weight, act_scales, error_buf, bias)
+    num_kb = K // block_size
+    e_a = _block_exps(act_scales, M, num_kb, "act_scales")
+    out = torch.empty((M, N), dtype=torch.float32, device=dev)
+    w_hi = torch.empty((N, K), dtype=torch.float8_e4m3fn, device=dev)
+    w_lo = torch.empty((N, K), dtype=torch.float8_e4m3fn, device=dev)
+    s_hi = torch.empty((num_kb, N), dtype=torch.int8, device=dev)
+    s_lo = torch.empty((num_kb, N), dtype=torch.int8, device=dev)
+    if bias is not None:
+        bias = bias.to(torch.float32).contiguous()
+        assert bias.shape == (N,), f"bias shape {tuple(bias.shape)} != ({N},)"
+    if stochastic_lo and seed is None:
+        seed = int(torch.randint(0, 2**62, (1,)).item())
+    check(
+        _hip.lib().tcfp_wtquant_block_dual_gemm(
+            ptr(act_fp8), _fmt(act_fp8.dtype), act_fp8.stride(0), ptr(e_a), ptr(weight),
+            _in_dtype(weight), M, N, K, block_size, ptr(error_buf), int(bool(stochastic_lo)),
+            int(seed or 0), 0, ptr(w_hi), ptr(w_lo), ptr(s_hi), ptr(s_lo), ptr(bias), ptr(out),
+            _out_dtype(torch.float32), N, _hip.stream_of(dev),
+        ),
+        "fused_wtquant_block_scaled_dual_gemm_forward",
+    )
+    if save_w_lo:
+        return out, w_hi, w_lo, s_hi, s_lo
+    return out, w_hi, None, s_hi, None
+
+
 def fused_block_scaled_dual_gemm_backward_dx(
     grad_fp8: torch.Tensor,
     w_hi_fp8: torch.Tensor,

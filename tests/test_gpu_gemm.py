@@ -310,3 +310,55 @@ def test_block_wgrad_fp32_accuracy(dev, bs, M, N, K_):
     err = og.rel_fro(npy(dw), ref)
     print(f"block wgrad bs={bs} M={M} N={N} K={K_} rel_fro={err:.2e}")
     assert err < 2e-5  # fp32-level: split-bf16 representation error <= 2^-17
+
+
+# ------------------------------------- weight quant + block dual GEMM (a16)
+# Mirrors the reference's TestFusedWtQuantDualGemm
+# (tests/test_block_scaling_kernels.py:1038-1291).
+@pytest.mark.parametrize("M,K_,N,bs", [(64, 64, 64, 32), (128, 128, 128, 64), (64, 128, 128, 128),
+                                       (300, 512, 1000, 64)])
+@pytest.mark.parametrize("wdt", [torch.bfloat16, torch.float32])
+def test_wtquant_matches_separate_quant_and_gemm(dev, M, K_, N, bs, wdt):
+    g = torch.Generator().manual_seed(M + N)
+    a, ea = K.block_quantize_fp8(torch.randn(M, K_, generator=g).to(dev), bs)
+    w = torch.randn(N, K_, generator=g).to(wdt).to(dev)
+    out, h, l, sh, sl = K.fused_wtquant_block_scaled_dual_gemm_forward(a, w, ea, bs)
+    assert out.shape == (M, N) and out.dtype == torch.float32
+    assert h.dtype == torch.float8_e4m3fn and sh.dtype == torch.int8
+    assert tuple(sh.shape) == (K_ // bs, N) and tuple(sl.shape) == (K_ // bs, N)
+    h2, l2, sh2, sl2 = K.fused_dual_quantize_fp8(w, bs)
+    assert torch.equal(h.view(torch.uint8), h2.view(torch.uint8))
+    assert torch.equal(l.view(torch.uint8), l2.view(torch.uint8))
+    assert torch.equal(sh, sh2) and torch.equal(sl, sl2)
+    ref = K.fused_block_scaled_dual_gemm_forward(a, h2, l2, ea, sh2, sl2, bs)
+    assert torch.equal(out, ref)
+    oref = og.block_dual_gemm_nt(u8(a), npy(ea), u8(h), u8(l), npy(sh), npy(sl), bs)
+    assert og.rel_fro(npy(out), oref) < EXACT
+
+
+def test_wtquant_abd_ef_and_srr(dev):
+    M, K_, N, bs = 128, 256, 192, 64
+    g = torch.Generator().manual_seed(5)
+    a, ea = K.block_quantize_fp8(torch.randn(M, K_, generator=g).to(dev), bs)
+    w = torch.randn(N, K_, generator=g).to(dev)
+    # ABD: W_lo not returned
+    out, h, l, sh, sl = K.fused_wtquant_block_scaled_dual_gemm_forward(a, w, ea, bs, save_w_lo=False)
+    assert l is None and sl is None and torch.isfinite(out).all()
+    # EF: buffer updated in place to the oracle's W - deq(hi) - deq(lo)
+    ef0 = torch.randn(N, K_, generator=g) * 1e-3
+    ef = ef0.to(dev)
+    out_ef, h, l, sh, sl = K.fused_wtquant_block_scaled_dual_gemm_forward(a, w, ea, bs, error_buf=ef)
+    hi, lo, eh, el, ef_new = oq.block_dual_quantize(npy(w), bs, ef0.numpy())
+    assert np.array_equal(u8(h), hi) and np.array_equal(u8(l), lo)
+    assert np.array_equal(npy(ef).view(np.uint32), ef_new.view(np.uint32))
+    assert not torch.equal(out_ef, out)  # the error term changes the quantised weight
+    # SRR and EF are exclusive; SRR draws lo from the candidates
+    with pytest.raises(ValueError):
+        K.fused_wtquant_block_scaled_dual_gemm_forward(a, w, ea, bs, error_buf=ef,
+                                                        stochastic_lo=True)
+    out_sr, h, l, sh, sl = K.fused_wtquant_block_scaled_dual_gemm_forward(a, w, ea, bs,
+                                                                           stochastic_lo=True,
+                                                                           seed=9)
+    h2, l2, sh2, sl2 = K.fused_dual_quantize_fp8(w, bs, stochastic_lo=True, seed=9)
+    assert torch.equal(l.view(torch.uint8), l2.view(torch.uint8)) and torch.equal(sl, sl2)
+    assert torch.isfinite(out_sr).all()
