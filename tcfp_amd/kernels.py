@@ -31,6 +31,13 @@ def is_hip_available() -> bool:
     return _hip.is_available()
 
 
+def is_triton_available() -> bool:
+    """The reference's gate for its fused-kernel tier
+    (``tcfp/kernels.py:1537-1539``, used at ``tcfp/nn/__init__.py:40-55``);
+    here the tier is the HIP library, so this is :func:`is_hip_available`."""
+    return _hip.is_available()
+
+
 def _fmt(dtype: torch.dtype) -> int:
     try:
         return _FMT[dtype]

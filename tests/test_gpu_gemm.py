@@ -362,3 +362,16 @@ def test_wtquant_abd_ef_and_srr(dev):
     h2, l2, sh2, sl2 = K.fused_dual_quantize_fp8(w, bs, stochastic_lo=True, seed=9)
     assert torch.equal(l.view(torch.uint8), l2.view(torch.uint8)) and torch.equal(sl, sl2)
     assert torch.isfinite(out_sr).all()
+
+
+def test_cuda_ext_surface_routes_to_hip_dual_gemm(dev):
+    from tcfp_amd import cuda_ext
+
+    assert cuda_ext.is_cuda_ext_available() and K.is_triton_available()
+    a, ia = make_act((256, 512), 3, dev)
+    h, l, ih, il = make_pair((384, 512), 4, dev)
+    assert torch.equal(cuda_ext.cuda_ext_dual_gemm_forward(a, h, l, ia, ih, il),
+                       K.fused_dual_gemm_forward(a, h, l, ia, ih, il))
+    g, ig = make_act((256, 384), 5, dev, torch.float8_e5m2)
+    assert torch.equal(cuda_ext.cuda_ext_dual_gemm_backward_dx(g, h, l, ig, ih, il),
+                       K.fused_dual_gemm_backward_dx(g, h, l, ig, ih, il))

@@ -169,3 +169,20 @@ def test_ef_state_roundtrip_reference_format(tmp_path):
     # unknown keys are skipped, as in the reference
     from tcfp_amd.ef_state import load_ef_state_dict
     assert load_ef_state_dict(b, {"nope": snap["0"]}) == 0
+
+
+def test_reference_gate_functions_without_gpu():
+    # the reference's dispatch gates (tcfp/nn/__init__.py:40-66) exist and
+    # report the backend unusable here; the ext entry points fail loudly
+    import torch
+
+    from tcfp_amd import cuda_ext, kernels
+
+    assert kernels.is_triton_available() is False
+    assert cuda_ext.is_cuda_ext_available() is False
+    z = torch.zeros(16, 16)
+    s = torch.ones(1)
+    with pytest.raises(RuntimeError):
+        cuda_ext.cuda_ext_dual_gemm_forward(z, z, z, s, s, s)
+    with pytest.raises(RuntimeError):
+        cuda_ext.cuda_ext_dual_gemm_backward_dx(z, z, z, s, s, s)
