@@ -26,6 +26,8 @@
 // on XCD b % 8, so workgroups are renumbered to give each XCD a contiguous
 // run of tiles, grouped 8 tile-rows deep, which keeps an XCD's A and B
 // panels resident in its own L2.
+#include <algorithm>
+
 #include "common.h"
 
 using namespace tcfp;
@@ -379,6 +381,11 @@ struct GemmArgs {
   void* out;
   int64_t ldo;
   int tiles_m, tiles_n;
+  // split-K (SCALE 0 only): gridDim.y > 1 splits the contraction into
+  // chunks of kc bytes; split y reads K columns [y*kc, y*kc + kc) and writes
+  // its partial output at out + y*split_stride (fp32, no bias)
+  int kc;
+  int64_t split_stride;
 };
 
 // NS = LDS stages in flight (2, or 4 for the small tile when one
@@ -407,8 +414,17 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && NS == 2 && BM == 128 ? 2 : 1))
   constexpr int kScB = SCALE == 2 ? 4096 : 0;
   __shared__ __align__(16) uint8_t lds[NS * STAGE + 3 * kScB];
 
-  const int M = g.M, N = g.N, K = g.K;
+  const int M = g.M, N = g.N;
+  int K = g.K;
   OutT* __restrict__ out = static_cast<OutT*>(g.out);
+  int64_t koff = 0;  // byte offset of this split's first K column
+  if constexpr (SCALE == 0) {
+    if (gridDim.y > 1) {
+      koff = int64_t(blockIdx.y) * g.kc;
+      K = min(g.kc, g.K - int(koff));
+      out += int64_t(blockIdx.y) * g.split_stride;
+    }
+  }
 
   // ---- tile mapping (XCD-aware, grouped) ----
   const int T = g.tiles_m * g.tiles_n;
@@ -437,12 +453,12 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && NS == 2 && BM == 128 ? 2 : 1))
   int64_t ld;
   int rows_left, row_base;
   if (srow0 < BM) {
-    src = g.A + int64_t(m0) * g.lda; ld = g.lda; rows_left = min(M - m0, BM); row_base = srow0;
+    src = g.A + koff + int64_t(m0) * g.lda; ld = g.lda; rows_left = min(M - m0, BM); row_base = srow0;
   } else if (srow0 < BM + BN) {
-    src = g.B0 + int64_t(n0) * g.ldb; ld = g.ldb; rows_left = min(N - n0, BN);
+    src = g.B0 + koff + int64_t(n0) * g.ldb; ld = g.ldb; rows_left = min(N - n0, BN);
     row_base = srow0 - BM;
   } else {
-    src = g.B1 + int64_t(n1) * g.ldb; ld = g.ldb; rows_left = min(N - n1, BN);
+    src = g.B1 + koff + int64_t(n1) * g.ldb; ld = g.ldb; rows_left = min(N - n1, BN);
     row_base = srow0 - BM - BN;
   }
   const uint32_t nrec = rows_left > 0 ? uint32_t(int64_t(rows_left - 1) * ld + K) : 0u;
@@ -863,10 +879,13 @@ int launch_gemm(GemmArgs ga, hipStream_t st) {
   const bool dma_ok = int64_t(BMv) * ga.lda + k < kMaxSpan && int64_t(BNv) * ga.ldb + k < kMaxSpan &&
                       (ga.bias == nullptr || (reinterpret_cast<uintptr_t>(ga.bias) & 15) == 0);
   if (dma_ok) {
-    const unsigned grid = unsigned(ga.tiles_m) * unsigned(ga.tiles_n);
+    // split-K (SCALE 0): gridDim.y = number of K chunks
+    const unsigned splits =
+        (SCALE == 0 && ga.kc > 0 && ga.kc < k) ? unsigned((k + ga.kc - 1) / ga.kc) : 1u;
+    const dim3 grid(unsigned(ga.tiles_m) * unsigned(ga.tiles_n), splits);
     // a small-tile launch that fits in one round gets the 4-stage pipeline
     // (one workgroup per CU, 128 KiB of LDS)
-    const bool deep = SCALE == 0 && small && int(grid) <= num_cus();
+    const bool deep = SCALE == 0 && small && int64_t(grid.x) * splits <= num_cus();
     if (small && deep) {
       if constexpr (SCALE == 0) {
         if (g_tile_policy == 3)
@@ -1276,9 +1295,50 @@ extern "C" int tcfp_block_dual_gemm_dx(const uint8_t* g, int g_fmt, const int8_t
   return launch_gemm<kBF16, kBF16, true, float, 0>(ga, st);
 }
 
+namespace {
+
+// dw[i] = sum_s part[s * stride + i], summed in split order (deterministic);
+// four fp32 per thread (n4 = elements / 4; stride % 4 == 0).
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ part,
+                                                            int splits, int64_t n4,
+                                                            int64_t stride,
+                                                            float* __restrict__ out) {
+  const int64_t step = int64_t(gridDim.x) * 256;
+  for (int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x; i < n4; i += step) {
+    float4 a = reinterpret_cast<const float4*>(part)[i];
+    for (int sp = 1; sp < splits; ++sp) {
+      const float4 b = reinterpret_cast<const float4*>(part + sp * stride)[i];
+      a.x += b.x; a.y += b.y; a.z += b.z; a.w += b.w;
+    }
+    reinterpret_cast<float4*>(out)[i] = a;
+  }
+}
+
+// Split-K factor of the block wgrad GEMM (contraction 2m bf16 = 4m bytes):
+// when the [n_out, k_in] output gives at most half the CUs a 128 x 128
+// tile, split the contraction so every CU gets a workgroup, keeping at
+// least four 128-byte stages per split.  Returns the split count and sets
+// *kc to the split length in bytes (a multiple of 128).
+int64_t wgrad_splits(int64_t m, int64_t n_out, int64_t k_in, int64_t* kc) {
+  const int64_t kbytes = 4 * m;
+  *kc = kbytes;
+  const int64_t tiles = ((n_out + 127) / 128) * ((k_in + 127) / 128);
+  const int64_t cus = num_cus();
+  if (tiles <= 0 || 2 * tiles > cus) return 1;
+  const int64_t s = std::min((cus + tiles - 1) / tiles, kbytes / 512);
+  if (s < 2) return 1;
+  *kc = ((kbytes + s - 1) / s + 127) / 128 * 128;
+  return (kbytes + *kc - 1) / *kc;
+}
+
+}  // namespace
+
 extern "C" size_t tcfp_block_wgrad_workspace_bytes(int64_t m, int64_t n_out, int64_t k_in) {
   if (m < 0 || n_out < 0 || k_in < 0) return 0;
-  return align256(size_t(n_out) * size_t(2 * m) * 2) + align256(size_t(k_in) * size_t(2 * m) * 2);
+  int64_t kc;
+  const int64_t splits = wgrad_splits(m, n_out, k_in, &kc);
+  return align256(size_t(n_out) * size_t(2 * m) * 2) + align256(size_t(k_in) * size_t(2 * m) * 2) +
+         (splits > 1 ? align256(size_t(splits) * size_t(n_out) * size_t(k_in) * 4) : 0);
 }
 
 extern "C" int tcfp_block_wgrad(const float* g, int64_t m, int64_t n_out, const uint8_t* x,
@@ -1320,5 +1380,19 @@ extern "C" int tcfp_block_wgrad(const float* g, int64_t m, int64_t n_out, const 
   ga.M = int(n_out); ga.N = int(k_in); ga.K = int(4 * m);  // bytes of 2M bf16
   ga.lda = 4 * m; ga.ldb = 4 * m;
   ga.out = dw; ga.ldo = k_in;
-  return launch_gemm<kBF16, kBF16, true, float, 0>(ga, st);
+  int64_t kc;
+  const int64_t splits = wgrad_splits(m, n_out, k_in, &kc);
+  if (splits <= 1) return launch_gemm<kBF16, kBF16, true, float, 0>(ga, st);
+  // partial products of each K chunk, then their sum in split order
+  float* part = reinterpret_cast<float*>(ws + align256(size_t(n_out) * size_t(2 * m) * 2) +
+                                         align256(size_t(k_in) * size_t(2 * m) * 2));
+  ga.out = part;
+  ga.kc = int(kc);
+  ga.split_stride = n_out * k_in;
+  const int rc = launch_gemm<kBF16, kBF16, true, float, 0>(ga, st);
+  if (rc != TCFP_OK) return rc;
+  const int64_t n4 = n_out * k_in / 4;
+  const int blocks = int(std::min<int64_t>((n4 + 255) / 256, int64_t(num_cus()) * 8));
+  splitk_reduce_kernel<<<blocks, 256, 0, st>>>(part, int(splits), n4, n_out * k_in, dw);
+  return hipGetLastError() == hipSuccess ? TCFP_OK : TCFP_ERR_HIP;
 }

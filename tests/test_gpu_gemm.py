@@ -297,8 +297,11 @@ def test_fused_act_quant_dual_gemm(dev, bs, dtype):
 
 # ------------------------------------------------- block wgrad (a14)
 @pytest.mark.parametrize("bs", [32, 64, 128])
+# (4096, 256, 256) and (4096, 768, 256) are TinyGPT's wgrads (few output
+# tiles, long contraction: split-K); (1000, 256, 512) has an uneven last split
 @pytest.mark.parametrize("M,N,K_", [(256, 384, 512), (1024, 256, 1024), (300, 128, 256),
-                                    (8, 64, 128), (302, 64, 128)])
+                                    (8, 64, 128), (302, 64, 128), (4096, 256, 256),
+                                    (4096, 768, 256), (1000, 256, 512)])
 def test_block_wgrad_fp32_accuracy(dev, bs, M, N, K_):
     g = torch.Generator().manual_seed(M + N + bs)
     grad = torch.randn(M, N, generator=g) * 1e-3
@@ -310,6 +313,8 @@ def test_block_wgrad_fp32_accuracy(dev, bs, M, N, K_):
     err = og.rel_fro(npy(dw), ref)
     print(f"block wgrad bs={bs} M={M} N={N} K={K_} rel_fro={err:.2e}")
     assert err < 2e-5  # fp32-level: split-bf16 representation error <= 2^-17
+    # the split-K sum runs in a fixed order: repeat calls agree bit for bit
+    assert torch.equal(dw, K.block_scaled_wgrad(grad.to(dev), aq, ea, bs))
 
 
 # ------------------------------------- weight quant + block dual GEMM (a16)
