@@ -626,6 +626,28 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && NS == 2 && BM == 128 ? 2 : 1))
         }
       }
   };
+  // MFMAs of (fragment, m-block) pairs [lo, hi) of sub-step h, pairs in
+  // m-block-major order as in mfmas
+  auto mfmas_range = [&](const v8i* f, const uint32_t* sc, int h, int lo, int hi) {
+#pragma unroll
+    for (int idx = 0; idx < NF * MB; ++idx) {
+      if (idx < lo || idx >= hi) continue;
+      const int i = idx / NF, q = idx % NF;
+      v16f& c = acc[(q / NB) % NACC][q % NB][i];
+      if constexpr (AF == kBF16) {
+        c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bf16_half(f[q], 0), bf16_half(f[NF + i], 0),
+                                                    c, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bf16_half(f[q], 1), bf16_half(f[NF + i], 1),
+                                                    c, 0, 0, 0);
+      } else if constexpr (SCALE == 1) {
+        c = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+            f[q], f[NF + i], c, BF, AF, 0, int(sc[2 * q + h]), 0, int(sc[2 * (NF + i) + h]));
+      } else {
+        c = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f[q], f[NF + i], c, BF, AF, 0, 127,
+                                                             0, 127);
+      }
+    }
+  };
   // NF*MB MFMAs and 2*(NF+MB) LDS reads per sub-step: spread the reads evenly
   auto interleave = [&]() {
     interleave_mfma_lds<NF * MB * (AF == kBF16 ? 2 : 1), 2 * (NF + MB), 0>();
@@ -746,6 +768,29 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && NS == 2 && BM == 128 ? 2 : 1))
       __builtin_amdgcn_sched_barrier(0);
       read_frags(f0, t + 1, 0);
       substep(f1, t, 1);
+    }
+  } else if constexpr (BM == 256 && NS == 2) {
+    // Large tile, one workgroup per CU: its 8 waves meet at every barrier, so
+    // the MFMA pipes drain there.  Half of sub-step 0's MFMAs (operands
+    // already in registers) are held back until after the barrier, and the
+    // refill DMA is issued behind them, so the pipes restart at once.
+    constexpr int NP = NF * MB;
+    constexpr int MPP = AF == kBF16 ? 2 : 1;  // MFMAs per (fragment, m-block) pair
+    for (int t = 0; t < nt; ++t) {
+      load_raw(raw, t + 1);
+      __builtin_amdgcn_sched_barrier(0);
+      read_frags(f1, t, 1);
+      mfmas_range(f0, sc, 0, 0, NP / 2);
+      interleave_mfma_lds<(NP / 2) * MPP, 2 * (NF + MB), 0>();
+      sync_all();
+      mfmas_range(f0, sc, 0, NP / 2, NP);
+      __builtin_amdgcn_sched_barrier(0);
+      issue(t + NS);
+      __builtin_amdgcn_sched_barrier(0);
+      read_frags(f0, t + 1, 0);
+      mfmas(f1, sc, 1);
+      interleave();
+      pack(sc, raw);
     }
   } else {
   for (int t = 0; t < nt; ++t) {
