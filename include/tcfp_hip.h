@@ -303,6 +303,13 @@ int tcfp_workspace_error(const void* workspace, int* flag, void* stream);
 int tcfp_selftest_fp8_cvt(uint32_t lo_bits, uint32_t hi_bits, int fp8_fmt,
                           unsigned long long* mismatches, void* stream);
 
+/* Runs the block stochastic-rounding candidate rule with software FP8
+ * converts and with the hardware converts the kernels use, on every float32
+ * whose bit pattern lies in [lo_bits, hi_bits] (at most 448.0's) and its
+ * negation, at uniform u; counts disagreements into *mismatches. */
+int tcfp_selftest_sr_block(uint32_t lo_bits, uint32_t hi_bits, float u,
+                           unsigned long long* mismatches, void* stream);
+
 /* Fills out[4*i .. 4*i+3] with Philox4x32-10 of counter (i + ctr0, ctr1,
  * ctr2, ctr3) under key (k0, k1), for i < n. */
 int tcfp_selftest_philox(uint32_t ctr0, uint32_t ctr1, uint32_t ctr2, uint32_t ctr3,

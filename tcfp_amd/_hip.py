@@ -75,6 +75,7 @@ _SIGNATURES = {
     "tcfp_workspace_error": [_c_void_p, _c_void_p, _c_void_p],
     "tcfp_transpose_u8": [_c_void_p, _i64, _i64, _c_void_p, _c_void_p],
     "tcfp_selftest_fp8_cvt": [_u32, _u32, _i32, _c_void_p, _c_void_p],
+    "tcfp_selftest_sr_block": [_u32, _u32, ctypes.c_float, _c_void_p, _c_void_p],
     "tcfp_selftest_philox": [_u32, _u32, _u32, _u32, _u32, _u32, _i64, _c_void_p, _c_void_p],
 }
 _RESTYPE = {

@@ -1035,9 +1035,9 @@ __global__ __launch_bounds__(kCoopThreads) void dualq_coop_kernel(
 // L = BS / VEC lanes with one 16-byte load each; a 256-thread workgroup
 // covers 256 / L consecutive rows of one K-block, so the int8 exponents of
 // a workgroup ([K/bs, M] layout) are contiguous.
-template <typename InT, int BS>
+template <typename InT, int BS, int V = 16 / int(sizeof(InT))>
 struct Seg {
-  static constexpr int VEC = 16 / int(sizeof(InT));
+  static constexpr int VEC = V;
   static constexpr int L = BS / VEC;
   static constexpr int ROWS = kThreads / L;
 };
@@ -1156,6 +1156,21 @@ __global__ __launch_bounds__(kThreads) void block_quant_kernel(const InT* __rest
   }
 }
 
+// Stochastic-rounding variants of the dual kernel carry 8 elements per lane
+// so that one Philox call (8 x 16 random bits) serves a lane's elements.
+template <typename InT, int BS, bool SR>
+using DualSeg = Seg<InT, BS, SR ? 8 : 16 / int(sizeof(InT))>;
+
+template <typename InT, int N>
+TCFP_DEV void load_in(const InT* p, float* v) {
+  if constexpr (sizeof(InT) == 4) {
+    loadf<N>(reinterpret_cast<const float*>(p), v);
+  } else {
+    static_assert(N == 8, "bf16 segments load 8 elements");
+    load8(reinterpret_cast<const uint16_t*>(p), v);
+  }
+}
+
 // Block stochastic rounding (tcfp/kernels.py:398-423): the neighbour is
 // found by a quarter-magnitude nudge under a saturating cast.
 TCFP_DEV uint32_t sr_block(float x, float u) {
@@ -1174,6 +1189,35 @@ TCFP_DEV uint32_t sr_block(float x, float u) {
   return exact ? rtn : (u < frac ? other : rtn);
 }
 
+// sr_block on the hardware converts.  Both encodes see clamped inputs
+// (|x| <= 448, the nudged value is clamped), where v_cvt_pk_fp8_f32 is the
+// RNE encoder (bit-identical to the software one over every finite float in
+// range, GPU self-test) and saturation never triggers; v_cvt_f32_fp8 decodes
+// exactly.  tcfp_selftest_sr_block compares the two functions bit for bit.
+TCFP_DEV uint32_t hw_e4m3(float x) {
+  return uint32_t(__builtin_amdgcn_cvt_pk_fp8_f32(x, 0.0f, 0, false)) & 0xFFu;
+}
+TCFP_DEV float hw_e4m3_f32(uint32_t c) { return __builtin_amdgcn_cvt_f32_fp8(int(c), 0); }
+
+TCFP_DEV uint32_t sr_block_hw(float x, float u) {
+  const uint32_t rtn = hw_e4m3(x);
+  const float rtn_f = hw_e4m3_f32(rtn);
+  const float diff = x - rtn_f;
+  const float d = diff >= 0.0f ? 1.0f : -1.0f;
+  const float abs_rtn = fmaxf(fabsf(rtn_f), 1e-12f);
+  const float nud = rtn_f + (d * abs_rtn) * 0.25f;
+  const uint32_t other = hw_e4m3(clampf(nud, kE4M3Max));
+  const float other_f = hw_e4m3_f32(other);
+  const float g = fabsf(other_f - rtn_f);
+  const float gap = fmaxf(g, 1.4e-45f);
+  const float frac = fminf(fabsf(diff) / gap, 1.0f);
+  const bool exact = (fabsf(diff) < 1.4e-45f) || (g < 1.4e-45f);
+  return exact ? rtn : (u < frac ? other : rtn);
+}
+
+// Uniform in [0, 1) from the low 16 bits of v.
+TCFP_DEV float u16_to_unit(uint32_t v) { return float(v & 0xFFFFu) * 1.52587890625e-05f; }
+
 // Fused block dual quantisation + error update (tcfp/kernels.py:288-459 and
 // :1867-1873).  The error buffer is read and rewritten by the same lane.
 // With F32S the two components use the fp32 block rule above on the fp32
@@ -1184,7 +1228,7 @@ __global__ __launch_bounds__(kThreads) void block_dualq_kernel(
     const InT* __restrict__ w, float* __restrict__ ef, int64_t n, int64_t k,
     uint8_t* __restrict__ hi, uint8_t* __restrict__ lo, void* __restrict__ shi,
     void* __restrict__ slo, uint32_t k0, uint32_t k1, uint32_t off0, uint32_t off1) {
-  using G = Seg<InT, BS>;
+  using G = DualSeg<InT, BS, SR>;
   constexpr int VEC = G::VEC;
   const int64_t kb = blockIdx.y;
   const int64_t row = int64_t(blockIdx.x) * G::ROWS + threadIdx.x / G::L;
@@ -1193,7 +1237,7 @@ __global__ __launch_bounds__(kThreads) void block_dualq_kernel(
   const int64_t off = row * k + kb * BS + li * VEC;
   float W[VEC], v[VEC];
   if (valid) {
-    loadv<InT>(w + off, W);
+    load_in<InT, VEC>(w + off, W);
   } else {
 #pragma unroll
     for (int j = 0; j < VEC; ++j) W[j] = 0.0f;
@@ -1255,14 +1299,22 @@ __global__ __launch_bounds__(kThreads) void block_dualq_kernel(
   for (int j = 0; j < VEC; ++j) c[j] = clampf(r[j] * mul_lo, kE4M3Max);
   uint32_t lc[VEC / 4];
   if constexpr (SR) {
-    const int64_t gidx = off;  // element index of c[0] in the [n, k] matrix
+    // elements off .. off + 7 (off % 8 == 0) draw Philox counter off / 8;
+    // element j takes 16 bits of word j / 2
+    static_assert(VEC == 8, "one Philox call per 8 elements");
+    const uint64_t ctr = uint64_t(off) >> 3;
+    const u32x4 rr = philox4x32_10({uint32_t(ctr), uint32_t(ctr >> 32), off0, off1}, k0, k1);
+    const uint32_t words[4] = {rr.x, rr.y, rr.z, rr.w};
 #pragma unroll
-    for (int j = 0; j < VEC; j += 4) {
-      const uint64_t ctr = uint64_t(gidx + j) >> 2;
-      u32x4 rr = philox4x32_10({uint32_t(ctr), uint32_t(ctr >> 32), off0, off1}, k0, k1);
-      lc[j / 4] = sr_block(c[j], u32_to_unit(rr.x)) | (sr_block(c[j + 1], u32_to_unit(rr.y)) << 8) |
-                  (sr_block(c[j + 2], u32_to_unit(rr.z)) << 16) |
-                  (sr_block(c[j + 3], u32_to_unit(rr.w)) << 24);
+    for (int q = 0; q < 2; ++q) {
+      uint32_t word = 0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int j = 4 * q + e;
+        const float u = u16_to_unit(words[j >> 1] >> (16 * (j & 1)));
+        word |= sr_block_hw(c[j], u) << (8 * e);
+      }
+      lc[q] = word;
     }
   } else {
     encode_words<VEC, TCFP_FP8_E4M3>(c, lc);
@@ -1347,6 +1399,23 @@ __global__ __launch_bounds__(kThreads) void selftest_cvt_kernel(uint32_t lo, uin
     const uint32_t h = cvt4_fp8<FMT>(x, -x, 0.f, 0.f) & 0xFFFFu;
     const uint32_t s = f32_to_fp8<FMT>(x) | (f32_to_fp8<FMT>(-x) << 8);
     cnt += (h != s);
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) cnt += __shfl_xor(cnt, o, 64);
+  if ((threadIdx.x & 63) == 0 && cnt) atomicAdd(bad, (unsigned long long)cnt);
+}
+
+// sr_block (software converts) vs sr_block_hw on every float32 whose bit
+// pattern lies in [lo, hi] and its negation, at one uniform u.
+__global__ __launch_bounds__(kThreads) void selftest_sr_kernel(uint32_t lo, uint32_t hi, float u,
+                                                               unsigned long long* bad) {
+  const uint64_t span = uint64_t(hi) - lo + 1;
+  const uint64_t stride = uint64_t(gridDim.x) * kThreads;
+  uint32_t cnt = 0;
+  for (uint64_t i = uint64_t(blockIdx.x) * kThreads + threadIdx.x; i < span; i += stride) {
+    const float x = __uint_as_float(lo + uint32_t(i));
+    cnt += (sr_block(x, u) != sr_block_hw(x, u));
+    cnt += (sr_block(-x, u) != sr_block_hw(-x, u));
   }
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) cnt += __shfl_xor(cnt, o, 64);
@@ -1722,7 +1791,8 @@ int block_dual_quantize_impl(const void* w, int w_dtype, int64_t n, int64_t k, i
   const bool upd = ef && update_ef;
 #define TCFP_BDQ(T, B, EF, UP, SR)                                                             \
   do {                                                                                         \
-    dim3 grid(unsigned((n + Seg<T, B>::ROWS - 1) / Seg<T, B>::ROWS), kbs);                     \
+    using DS = DualSeg<T, B, SR>;                                                              \
+    dim3 grid(unsigned((n + DS::ROWS - 1) / DS::ROWS), kbs);                                   \
     block_dualq_kernel<T, B, EF, UP, SR, F32S><<<grid, kThreads, 0, st>>>(                     \
         static_cast<const T*>(w), ef, n, k, w_hi, w_lo, s_hi, s_lo, k0, k1, o0, o1);           \
   } while (0)
@@ -1827,6 +1897,15 @@ int tcfp_selftest_fp8_cvt(uint32_t lo_bits, uint32_t hi_bits, int fp8_fmt,
     selftest_cvt_kernel<TCFP_FP8_E4M3><<<g, kThreads, 0, st>>>(lo_bits, hi_bits, mismatches);
   else
     return TCFP_ERR_DTYPE;
+  return launch_status();
+}
+
+int tcfp_selftest_sr_block(uint32_t lo_bits, uint32_t hi_bits, float u,
+                           unsigned long long* mismatches, void* stream) {
+  if (hi_bits < lo_bits || hi_bits > 0x43E00000u) return TCFP_ERR_SHAPE;
+  const int g = num_cu() * 8;
+  selftest_sr_kernel<<<g, kThreads, 0, static_cast<hipStream_t>(stream)>>>(lo_bits, hi_bits, u,
+                                                                           mismatches);
   return launch_status();
 }
 

@@ -36,6 +36,17 @@ def test_hw_fp8_convert_matches_software_exhaustively(dev, fmt, top):
     assert bad.item() == 0
 
 
+@pytest.mark.parametrize("u", [0.0, 0.25, 0.5, 0.70710678, 1.0 - 2.0 ** -16])
+def test_sr_block_hardware_converts_match_software(dev, u):
+    # the block SR candidate rule on hardware converts == on software converts,
+    # for every float32 in [0, 448] and its negation
+    bad = torch.zeros(1, dtype=torch.int64, device=dev)
+    _hip.check(_hip.lib().tcfp_selftest_sr_block(0, 0x43E00000, u, bad.data_ptr(),
+                                                 _hip.stream_of(dev)), "selftest")
+    torch.cuda.synchronize()
+    assert bad.item() == 0
+
+
 def test_philox_known_answers(dev):
     # Random123 known-answer vectors for philox4x32-10
     cases = [
