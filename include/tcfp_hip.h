@@ -112,6 +112,32 @@ int tcfp_dual_quantize_per_tensor(const void* w, int w_dtype, int64_t n, int64_t
                                   uint8_t* w_hi_t, uint8_t* w_lo_t, void* workspace,
                                   void* stream);
 
+/* Per-tensor dual quantisation with delayed ("predictive dual-track")
+ * scaling: _TCFP12TensorCoreFunction.forward with delayed_scaling=True
+ * (tcfp/nn/__init__.py:250-309, 343-383; ErrorFeedbackState tcfp/core.py:
+ * 341-403).
+ *   W_hi scale = 448 / D with D = a*amax_prev + b*amax (EMA, three rounded
+ *   fp32 ops; D = amax on the first call, amax_prev == NULL), amax =
+ *   max|W + ef| clamped to 1e-12.
+ *   validate != 0: W_lo scale from the measured residual amax A, and the
+ *   ratio EMA r' = a*ratio_prev + b*(A / D) (r' = A / D when ratio_prev ==
+ *   NULL) is written to *ratio_out.
+ *   validate == 0: W_lo scale = 448 / max(D * ratio_prev, 1e-12) (D / 8
+ *   when ratio_prev == NULL); no residual reduction, so the weight is read
+ *   twice instead of three times.
+ *   a = fp32(ema_decay), b = fp32(1 - ema_decay) as the caller's Python
+ *   float arithmetic rounds them.  *amax_out receives D.  The previous
+ *   state and the outputs must not alias.  Otherwise as
+ *   tcfp_dual_quantize_per_tensor (no stochastic rounding: the reference
+ *   disables delayed scaling under SRR). */
+int tcfp_dual_quantize_per_tensor_delayed(const void* w, int w_dtype, int64_t n, int64_t k,
+                                          float* ef, int update_ef, const float* amax_prev,
+                                          const float* ratio_prev, float ema_decay,
+                                          float one_minus_decay, int validate, float* amax_out,
+                                          float* ratio_out, uint8_t* w_hi, uint8_t* w_lo,
+                                          float* inv_hi, float* inv_lo, uint8_t* w_hi_t,
+                                          uint8_t* w_lo_t, void* workspace, void* stream);
+
 /* ---- per-block quantisation -------------------------------------------- */
 
 /* Per-(row, K-block) FP8 quantisation.  Replaces block_quantize_fp8

@@ -95,6 +95,67 @@ def dual_quant_per_tensor(W: np.ndarray, ef: np.ndarray | None = None):
     return hi, lo, F32(inv_hi), F32(inv_lo), ef_new, residual
 
 
+def _ema_f32(prev, cur, decay: float) -> np.float32:
+    """torch's ``decay * prev + (1 - decay) * cur`` on fp32 scalars: the
+    Python floats are rounded to fp32 and each op rounds (core.py:352-355)."""
+    a, b = F32(decay), F32(1.0 - decay)
+    return F32(F32(a * F32(prev)) + F32(b * F32(cur)))
+
+
+def _scale_of(v) -> np.float32:
+    """``(448 / v).to(float32)`` for an fp32 tensor v: reciprocal, then
+    product (``Tensor.__rtruediv__``)."""
+    return F32(F32(F32(1.0) / F32(v)) * F32(FP8_MAX[E4M3]))
+
+
+def new_delayed_state() -> dict:
+    """The delayed-scaling parts of ``ErrorFeedbackState`` (core.py:309-314)."""
+    return {"amax": {}, "ratio": {}, "steps": {}}
+
+
+def dual_quant_per_tensor_delayed(W: np.ndarray, ef: np.ndarray | None, state: dict,
+                                  name: str, decay: float = 0.999, interval: int = 100):
+    """Per-tensor dual quantisation with delayed (predictive dual-track)
+    scaling: ``_delayed_quantise_w_hi`` / ``_delayed_quantise_w_lo``
+    (nn/__init__.py:250-309, non-NF path) inside the forward's steps 1-4
+    (:343-383), with ErrorFeedbackState's EMA bookkeeping (core.py:341-403).
+
+    ``state`` is updated in place.  Returns ``(hi, lo, inv_hi, inv_lo,
+    ef_new, validated)``.
+    """
+    W = np.asarray(W, dtype=F32)
+    w = W + ef if ef is not None else W
+    # W_hi: scale from the EMA of the clamped amax (first call: the amax)
+    cur = np.maximum(F32(np.max(np.abs(w))), F32(1e-12))
+    key = name + ".w_hi"
+    if key not in state["amax"]:
+        delayed = F32(cur)
+    else:
+        delayed = _ema_f32(state["amax"][key], cur, decay)
+    state["amax"][key] = delayed
+    hi, inv_hi, _ = to_fp8_per_tensor(w, "f32", scale=_scale_of(delayed))
+    residual = (w - decode(hi, E4M3) * inv_hi).astype(F32)
+    # W_lo: measured on validation steps (first call, every `interval`),
+    # predicted from the ratio EMA otherwise
+    skey, rkey = f"{name}.steps", f"{name}.ratio"
+    count = state["steps"].get(skey, 0) + 1
+    state["steps"][skey] = count
+    validate = count == 1 or count % interval == 0
+    if validate:
+        actual = np.maximum(F32(np.max(np.abs(residual))), F32(1e-12))
+        ratio = F32(actual / np.maximum(delayed, F32(1e-12)))
+        state["ratio"][rkey] = ratio if rkey not in state["ratio"] else _ema_f32(
+            state["ratio"][rkey], ratio, decay)
+        lo_amax = actual
+    elif rkey in state["ratio"]:
+        lo_amax = np.maximum(F32(delayed * state["ratio"][rkey]), F32(1e-12))
+    else:
+        lo_amax = np.maximum(F32(delayed / F32(8.0)), F32(1e-12))
+    lo, inv_lo, _ = to_fp8_per_tensor(residual, "f32", scale=_scale_of(lo_amax))
+    ef_new = W - (decode(hi, E4M3) * inv_hi + decode(lo, E4M3) * inv_lo)
+    return hi, lo, F32(inv_hi), F32(inv_lo), ef_new.astype(F32), validate
+
+
 def sr_candidates_per_tensor(x: np.ndarray):
     """Deterministic part of ``stochastic_round_to_fp8_e4m3`` (core.py:418-464).
 

@@ -82,14 +82,18 @@ def ensure_column_major(t: torch.Tensor) -> torch.Tensor:
 
 
 class ErrorFeedbackState:
-    """Per-parameter FP32 error-feedback buffers (``tcfp/core.py:298-326``).
+    """Per-parameter FP32 error-feedback buffers (``tcfp/core.py:298-326``)
+    and the delayed-scaling state (``:328-403``).
 
     ``get_error`` lazily creates a zero buffer shaped like ``like`` (fp32);
     ``update_error`` rebinds the stored tensor.  The HIP dual-quant kernels
     update the stored buffer in place, which is observationally the same
-    for the state machine (``tcfp/nn/__init__.py:375-383``).  The
-    delayed-scaling dictionaries exist for checkpoint-format compatibility
-    (``tcfp/training/checkpointing.py:200-224``) and stay empty here.
+    for the state machine (``tcfp/nn/__init__.py:375-383``).  Under delayed
+    scaling the HIP kernel computes the EMAs on the device and the
+    dictionaries are rebound to its outputs
+    (``kernels.dual_quantize_per_tensor_delayed``); the methods below give
+    the same state transitions with torch ops for callers that drive the
+    state themselves.
     """
 
     def __init__(
@@ -114,6 +118,58 @@ class ErrorFeedbackState:
 
     def update_error(self, name: str, error: torch.Tensor) -> None:
         self._buffers[name] = error.detach()
+
+    def get_amax_ema(self, name: str, current_amax: torch.Tensor) -> torch.Tensor:
+        """EMA of ``current_amax`` (``tcfp/core.py:328-339``)."""
+        if name not in self._amax_ema:
+            self._amax_ema[name] = current_amax.detach().clone()
+        else:
+            self._amax_ema[name] = (
+                self._ema_decay * self._amax_ema[name]
+                + (1 - self._ema_decay) * current_amax.detach()
+            )
+        return self._amax_ema[name]
+
+    def get_delayed_amax(self, name: str, current_amax: torch.Tensor) -> torch.Tensor:
+        """EMA-smoothed amax for delayed scaling; the first call returns
+        ``current_amax`` (``tcfp/core.py:341-356``)."""
+        if name not in self._delayed_amax:
+            self._delayed_amax[name] = current_amax.detach().clone()
+            return current_amax
+        prev = self._delayed_amax[name]
+        self._delayed_amax[name] = (
+            self._ema_decay * prev + (1 - self._ema_decay) * current_amax.detach()
+        )
+        return self._delayed_amax[name]
+
+    def predict_residual_amax(self, name: str, main_amax: torch.Tensor) -> torch.Tensor:
+        """``main_amax * ratio`` (``main_amax / 8`` before any ratio),
+        clamped to 1e-12 (``tcfp/core.py:358-372``)."""
+        ratio_key = f"{name}.ratio"
+        if ratio_key not in self._residual_ratio:
+            return (main_amax / 8.0).clamp(min=1e-12)
+        return (main_amax * self._residual_ratio[ratio_key]).clamp(min=1e-12)
+
+    def update_residual_ratio(self, name: str, main_amax: torch.Tensor,
+                              actual_residual_amax: torch.Tensor) -> None:
+        """EMA of ``amax_lo / amax_hi`` (``tcfp/core.py:374-393``)."""
+        ratio = (actual_residual_amax / main_amax.clamp(min=1e-12)).detach()
+        ratio_key = f"{name}.ratio"
+        if ratio_key not in self._residual_ratio:
+            self._residual_ratio[ratio_key] = ratio
+        else:
+            self._residual_ratio[ratio_key] = (
+                self._ema_decay * self._residual_ratio[ratio_key]
+                + (1 - self._ema_decay) * ratio
+            )
+
+    def should_validate_residual(self, name: str) -> bool:
+        """True on the first call and every ``residual_validation_interval``
+        calls (``tcfp/core.py:395-403``)."""
+        key = f"{name}.steps"
+        count = self._step_count.get(key, 0) + 1
+        self._step_count[key] = count
+        return count == 1 or count % self._residual_validation_interval == 0
 
     def reset(self) -> None:
         self._buffers.clear()

@@ -186,6 +186,38 @@ TCFP_DEV float consumer_scale(const float* scale_in, const uint32_t* part, int g
   return s;
 }
 
+// Delayed ("predictive dual-track") per-tensor scaling of one weight
+// (tcfp/core.py:341-403, tcfp/nn/__init__.py:250-309).  `on == 0` selects
+// the plain per-tensor rule.  The previous EMA values are read from
+// amax_prev / ratio_prev (null: not tracked yet) and the new ones are
+// written to amax_out / ratio_out by workgroup 0 of the last pass, so the
+// state a launch reads is never the state it writes.
+struct Delayed {
+  const float* amax_prev;
+  const float* ratio_prev;
+  float* amax_out;
+  float* ratio_out;
+  float a, b;    // fp32(ema_decay), fp32(1 - ema_decay)
+  int on;
+  int validate;  // measure the residual amax this step (else predict it)
+};
+
+// torch's `d * prev + (1 - d) * cur` on fp32 tensors: three rounded ops.
+TCFP_DEV float ema_f32(float prev, float cur, float a, float b) {
+  return __fadd_rn(__fmul_rn(a, prev), __fmul_rn(b, cur));
+}
+TCFP_DEV float clamp_min_nan(float v, float lo) { return (v != v) ? v : fmaxf(v, lo); }
+// (FP8_MAX / v).to(float32) for an fp32 tensor v: reciprocal, then product;
+// inv = 1 / scale (to_fp8_e4m3 with an explicit scale, tcfp/core.py:99-106).
+TCFP_DEV void scale_of(float v, float fmax, float* s, float* inv) {
+  *s = __fmul_rn(__fdiv_rn(1.0f, v), fmax);
+  *inv = __fdiv_rn(1.0f, *s);
+}
+// get_delayed_amax (tcfp/core.py:341-356) of this step's clamped amax.
+TCFP_DEV float delayed_amax(const Delayed& d, float cur) {
+  return d.amax_prev ? ema_f32(*d.amax_prev, cur, d.a, d.b) : cur;
+}
+
 // Eight elements of x (+ ef) starting at element 8*i.
 template <typename InT, bool HAS_EF>
 TCFP_DEV void load_w8(const InT* __restrict__ x, const float* __restrict__ ef, int64_t i,
@@ -522,12 +554,18 @@ template <typename InT, bool HAS_EF>
 __global__ __launch_bounds__(kThreads) void dualq_hi_kernel(
     const InT* __restrict__ w, const float* __restrict__ ef, int64_t n,
     const uint32_t* __restrict__ pa, int ga, uint8_t* __restrict__ hi, uint32_t* __restrict__ pb,
-    float* inv_hi_out) {
+    float* inv_hi_out, Delayed dl) {
   __shared__ uint32_t red[kThreads / 64];
   __shared__ uint32_t red2[kThreads / 64];
-  const float s_hi =
-      consumer_scale(nullptr, pa, ga, false, kE4M3Max, nullptr, inv_hi_out, red);
-  const float inv_hi = __fdiv_rn(1.0f, s_hi);
+  float s_hi, inv_hi;
+  if (dl.on) {
+    const float cur = clamp_min_nan(reduce_parts(pa, ga, red), 1e-12f);
+    scale_of(delayed_amax(dl, cur), kE4M3Max, &s_hi, &inv_hi);
+    if (blockIdx.x == 0 && threadIdx.x == 0) *inv_hi_out = inv_hi;
+  } else {
+    s_hi = consumer_scale(nullptr, pa, ga, false, kE4M3Max, nullptr, inv_hi_out, red);
+    inv_hi = __fdiv_rn(1.0f, s_hi);
+  }
   uint32_t m = 0;
   const int64_t nvec = n >> 3;
   const int64_t stride = int64_t(gridDim.x) * kThreads;
@@ -641,15 +679,49 @@ TCFP_DEV DualScales dual_scales(const uint32_t* pa, int ga, const uint32_t* pb, 
   return sc;
 }
 
+// Pass-3 scales under delayed scaling: W_hi from the EMA of the amax; W_lo
+// from the measured residual amax on validation steps (updating the
+// amax_lo / amax_hi ratio EMA, tcfp/core.py:374-393) or, otherwise, from
+// the predicted one (delayed * ratio, or delayed / 8 before any ratio,
+// :358-372).  Workgroup 0 writes both inverse scales and the new state.
+TCFP_DEV DualScales dual_scales_delayed(const Delayed& d, const uint32_t* pa, int ga,
+                                        const uint32_t* pb, int gb, float* inv_hi_out,
+                                        float* inv_lo_out, uint32_t* red, uint32_t* red2) {
+  DualScales sc;
+  const float cur = clamp_min_nan(reduce_parts(pa, ga, red), 1e-12f);
+  const float del = delayed_amax(d, cur);
+  scale_of(del, kE4M3Max, &sc.s_hi, &sc.inv_hi);
+  float lo_amax, ratio = 0.0f;
+  if (d.validate) {
+    lo_amax = clamp_min_nan(reduce_parts(pb, gb, red2), 1e-12f);
+    const float r = __fdiv_rn(lo_amax, clamp_min_nan(del, 1e-12f));
+    ratio = d.ratio_prev ? ema_f32(*d.ratio_prev, r, d.a, d.b) : r;
+  } else {
+    lo_amax = clamp_min_nan(d.ratio_prev ? __fmul_rn(del, *d.ratio_prev) : __fdiv_rn(del, 8.0f),
+                            1e-12f);
+  }
+  scale_of(lo_amax, kE4M3Max, &sc.s_lo, &sc.inv_lo);
+  if (blockIdx.x == 0 && threadIdx.x == 0) {
+    *inv_hi_out = sc.inv_hi;
+    *inv_lo_out = sc.inv_lo;
+    *d.amax_out = del;
+    if (d.validate) *d.ratio_out = ratio;
+  }
+  return sc;
+}
+
 // Pass 3 (flat): W_lo codes (RNE or SR) and, optionally, the new error in place.
 template <typename InT, bool HAS_EF, bool UPDATE, bool SR>
 __global__ __launch_bounds__(kThreads) void dualq_lo_kernel(
     const InT* __restrict__ w, float* __restrict__ ef, int64_t n, const uint32_t* __restrict__ pa,
     int ga, const uint32_t* __restrict__ pb, int gb, uint8_t* __restrict__ lo, float* inv_lo_out,
-    uint32_t k0, uint32_t k1, uint32_t off0, uint32_t off1) {
+    uint32_t k0, uint32_t k1, uint32_t off0, uint32_t off1, Delayed dl, float* inv_hi_out,
+    uint8_t* __restrict__ hi) {
   __shared__ uint32_t red[kThreads / 64];
   __shared__ uint32_t red2[kThreads / 64];
-  const DualScales sc = dual_scales(pa, ga, pb, gb, inv_lo_out, red, red2);
+  const DualScales sc =
+      dl.on ? dual_scales_delayed(dl, pa, ga, pb, gb, inv_hi_out, inv_lo_out, red, red2)
+            : dual_scales(pa, ga, pb, gb, inv_lo_out, red, red2);
   const int64_t nvec = n >> 3;
   const int64_t stride = int64_t(gridDim.x) * kThreads;
   auto body = [&](const float W[8], const float v[8], int64_t i) {
@@ -658,6 +730,8 @@ __global__ __launch_bounds__(kThreads) void dualq_lo_kernel(
     dual_codes4<SR>(W, v, sc, i * 8, k0, k1, off0, off1, &hc[0], &lc[0], e);
     dual_codes4<SR>(W + 4, v + 4, sc, i * 8 + 4, k0, k1, off0, off1, &hc[1], &lc[1], e + 4);
     *reinterpret_cast<uint2*>(lo + i * 8) = make_uint2(lc[0], lc[1]);
+    // W_hi codes when no earlier pass wrote them
+    if (hi) *reinterpret_cast<uint2*>(hi + i * 8) = make_uint2(hc[0], hc[1]);
     if constexpr (HAS_EF && UPDATE) store8(ef + i * 8, e);
   };
   int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x;
@@ -678,6 +752,7 @@ __global__ __launch_bounds__(kThreads) void dualq_lo_kernel(
     float v = W;
     if constexpr (HAS_EF) v = W + ef[t];
     const uint32_t hcode = encode1<TCFP_FP8_E4M3>(clampf(v * sc.s_hi, kE4M3Max));
+    if (hi) hi[t] = uint8_t(hcode);
     const float dh = e4m3_to_f32(hcode) * sc.inv_hi;
     const float x = clampf((v - dh) * sc.s_lo, kE4M3Max);
     uint32_t lcode;
@@ -700,14 +775,17 @@ __global__ __launch_bounds__(kThreads) void dualq_lo_t_kernel(
     const InT* __restrict__ w, float* __restrict__ ef, int64_t rows, int64_t cols,
     const uint32_t* __restrict__ pa, int ga, const uint32_t* __restrict__ pb, int gb,
     uint8_t* __restrict__ lo, float* inv_lo_out, uint8_t* __restrict__ hi_t,
-    uint8_t* __restrict__ lo_t, uint32_t k0, uint32_t k1, uint32_t off0, uint32_t off1) {
+    uint8_t* __restrict__ lo_t, uint32_t k0, uint32_t k1, uint32_t off0, uint32_t off1,
+    Delayed dl, float* inv_hi_out, uint8_t* __restrict__ hi) {
   using TL = TileLoad<InT>;
   constexpr int VEC = TL::VEC;
   __shared__ uint32_t red[kThreads / 64];
   __shared__ uint32_t red2[kThreads / 64];
   __shared__ uint32_t tile_h[kTile * kTilePitch];
   __shared__ uint32_t tile_l[kTile * kTilePitch];
-  const DualScales sc = dual_scales(pa, ga, pb, gb, inv_lo_out, red, red2);
+  const DualScales sc =
+      dl.on ? dual_scales_delayed(dl, pa, ga, pb, gb, inv_hi_out, inv_lo_out, red, red2)
+            : dual_scales(pa, ga, pb, gb, inv_lo_out, red, red2);
   const TileGeom tg(cols);
   const int tc = (threadIdx.x % TL::TPR) * VEC;
   const int64_t c = tg.c0 + tc;
@@ -751,6 +829,10 @@ __global__ __launch_bounds__(kThreads) void dualq_lo_t_kernel(
     if (valid) {
       if constexpr (VEC == 4) *reinterpret_cast<uint32_t*>(lo + off) = lc[0];
       else *reinterpret_cast<uint2*>(lo + off) = make_uint2(lc[0], lc[1]);
+      if (hi) {  // W_hi codes when no earlier pass wrote them
+        if constexpr (VEC == 4) *reinterpret_cast<uint32_t*>(hi + off) = hc[0];
+        else *reinterpret_cast<uint2*>(hi + off) = make_uint2(hc[0], hc[1]);
+      }
       if constexpr (HAS_EF && UPDATE) {
 #pragma unroll
         for (int j = 0; j < VEC; j += 4)
@@ -1643,12 +1725,15 @@ int tcfp_quantize_per_tensor_colsum(const void* x, int x_dtype, int64_t rows, in
                        static_cast<hipStream_t>(stream));
 }
 
-int tcfp_dual_quantize_per_tensor(const void* w, int w_dtype, int64_t n, int64_t k,
-                                  float* ef, int update_ef, int stochastic_lo,
-                                  uint64_t seed, uint64_t offset, uint8_t* w_hi,
-                                  uint8_t* w_lo, float* inv_hi, float* inv_lo,
-                                  uint8_t* w_hi_t, uint8_t* w_lo_t, void* workspace,
-                                  void* stream) {
+}  // extern "C"
+
+namespace {
+
+int dual_quantize_impl(const void* w, int w_dtype, int64_t n, int64_t k, float* ef,
+                       int update_ef, int stochastic_lo, uint64_t seed, uint64_t offset,
+                       uint8_t* w_hi, uint8_t* w_lo, float* inv_hi, float* inv_lo,
+                       uint8_t* w_hi_t, uint8_t* w_lo_t, void* workspace, const Delayed& dl,
+                       void* stream) {
   if (n < 0 || k < 0) return TCFP_ERR_SHAPE;
   if (w_dtype != TCFP_DTYPE_F32 && w_dtype != TCFP_DTYPE_BF16) return TCFP_ERR_DTYPE;
   if (!workspace) return TCFP_ERR_WORKSPACE;
@@ -1670,9 +1755,9 @@ int tcfp_dual_quantize_per_tensor(const void* w, int w_dtype, int64_t n, int64_t
   const uint32_t k0 = uint32_t(seed), k1 = uint32_t(seed >> 32);
   const uint32_t o0 = uint32_t(offset), o1 = uint32_t(offset >> 32);
 
-  // one cooperative launch when selected and it fits (SR together with EF
-  // stays on the three-pass path)
-  if (g_force_three_pass == 0 && !(stochastic_lo && has_ef)) {
+  // one cooperative launch when selected and it fits (SR together with EF,
+  // and delayed scaling, stay on the separate passes)
+  if (g_force_three_pass == 0 && !(stochastic_lo && has_ef) && !dl.on) {
     bool done = false;
     if (bf) {
       const uint16_t* wp = static_cast<const uint16_t*>(w);
@@ -1698,21 +1783,28 @@ int tcfp_dual_quantize_per_tensor(const void* w, int w_dtype, int64_t n, int64_t
     if (done) return launch_status();
   }
 
+  // Delayed scaling without validation predicts the residual amax: pass 2
+  // (W_hi codes + residual amax) is skipped and pass 3 writes W_hi too.
+  const bool two_pass = dl.on && !dl.validate;
+  uint8_t* hi3 = two_pass ? w_hi : nullptr;
 #define TCFP_LO(T, EF, UP, SR)                                                                  \
   do {                                                                                          \
     if (tiled)                                                                                  \
       dualq_lo_t_kernel<T, EF, UP, SR><<<unsigned(tiles), kThreads, 0, st>>>(                   \
-          wp, ef, n, k, ws->a, ga, ws->b, gb, w_lo, inv_lo, w_hi_t, w_lo_t, k0, k1, o0, o1);    \
+          wp, ef, n, k, ws->a, ga, ws->b, gb, w_lo, inv_lo, w_hi_t, w_lo_t, k0, k1, o0, o1, dl,  \
+          inv_hi, hi3);                                                                         \
     else                                                                                        \
       dualq_lo_kernel<T, EF, UP, SR><<<gq, kThreads, 0, st>>>(wp, ef, total, ws->a, ga, ws->b, \
-                                                              gb, w_lo, inv_lo, k0, k1, o0, o1); \
+                                                              gb, w_lo, inv_lo, k0, k1, o0, o1, \
+                                                              dl, inv_hi, hi3);                 \
   } while (0)
 #define TCFP_DQ(T, EF)                                                                          \
   do {                                                                                          \
     const T* wp = static_cast<const T*>(w);                                                     \
     amax_part_kernel<T, EF><<<ga, kThreads, 0, st>>>(wp, ef, total, ws->a);                    \
-    dualq_hi_kernel<T, EF><<<gb, kThreads, 0, st>>>(wp, ef, total, ws->a, ga, w_hi, ws->b,     \
-                                                    inv_hi);                                    \
+    if (!two_pass)                                                                              \
+      dualq_hi_kernel<T, EF><<<gb, kThreads, 0, st>>>(wp, ef, total, ws->a, ga, w_hi, ws->b,   \
+                                                      inv_hi, dl);                              \
     if (stochastic_lo) {                                                                        \
       if (upd) TCFP_LO(T, EF, EF, true); else TCFP_LO(T, EF, false, true);                      \
     } else {                                                                                    \
@@ -1733,6 +1825,43 @@ int tcfp_dual_quantize_per_tensor(const void* w, int w_dtype, int64_t n, int64_t
     if (w_lo_t) transpose_u8_kernel<<<grid, kThreads, 0, st>>>(w_lo, n, k, w_lo_t);
   }
   return launch_status();
+}
+
+}  // namespace
+
+extern "C" {
+
+int tcfp_dual_quantize_per_tensor(const void* w, int w_dtype, int64_t n, int64_t k,
+                                  float* ef, int update_ef, int stochastic_lo,
+                                  uint64_t seed, uint64_t offset, uint8_t* w_hi,
+                                  uint8_t* w_lo, float* inv_hi, float* inv_lo,
+                                  uint8_t* w_hi_t, uint8_t* w_lo_t, void* workspace,
+                                  void* stream) {
+  const Delayed off{};
+  return dual_quantize_impl(w, w_dtype, n, k, ef, update_ef, stochastic_lo, seed, offset, w_hi,
+                            w_lo, inv_hi, inv_lo, w_hi_t, w_lo_t, workspace, off, stream);
+}
+
+int tcfp_dual_quantize_per_tensor_delayed(const void* w, int w_dtype, int64_t n, int64_t k,
+                                          float* ef, int update_ef, const float* amax_prev,
+                                          const float* ratio_prev, float ema_decay,
+                                          float one_minus_decay, int validate, float* amax_out,
+                                          float* ratio_out, uint8_t* w_hi, uint8_t* w_lo,
+                                          float* inv_hi, float* inv_lo, uint8_t* w_hi_t,
+                                          uint8_t* w_lo_t, void* workspace, void* stream) {
+  if (!amax_out || (validate && !ratio_out) || !inv_hi || !inv_lo) return TCFP_ERR_SHAPE;
+  if (n * k == 0) return TCFP_ERR_SHAPE;  // the reference's amax of an empty tensor raises
+  Delayed dl{};
+  dl.amax_prev = amax_prev;
+  dl.ratio_prev = ratio_prev;
+  dl.amax_out = amax_out;
+  dl.ratio_out = ratio_out;
+  dl.a = ema_decay;
+  dl.b = one_minus_decay;
+  dl.on = 1;
+  dl.validate = validate ? 1 : 0;
+  return dual_quantize_impl(w, w_dtype, n, k, ef, update_ef, 0, 0, 0, w_hi, w_lo, inv_hi, inv_lo,
+                            w_hi_t, w_lo_t, workspace, dl, stream);
 }
 
 }  // extern "C"

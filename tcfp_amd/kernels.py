@@ -197,6 +197,72 @@ def dual_quantize_per_tensor(
     return w_hi, w_lo, inv_hi, inv_lo
 
 
+def dual_quantize_per_tensor_delayed(
+    weight: torch.Tensor,
+    error_buf: torch.Tensor | None,
+    state,
+    name: str,
+    update_ef: bool = True,
+    transposed: bool = False,
+):
+    """Per-tensor dual quantisation with delayed scaling, updating ``state``.
+
+    ``_delayed_quantise_w_hi`` / ``_delayed_quantise_w_lo`` of the reference
+    (``tcfp/nn/__init__.py:250-309``) on an :class:`ErrorFeedbackState`:
+    the W_hi scale comes from the EMA of the amax (``_delayed_amax[name +
+    ".w_hi"]``), the W_lo scale from the measured residual amax on
+    validation steps (``should_validate_residual``; the ratio EMA
+    ``_residual_ratio[name + ".ratio"]`` is updated) and from the predicted
+    one otherwise.  The state tensors are replaced by new 0-dim fp32
+    tensors, as the reference's EMA rebinds them.  Returns what
+    :func:`dual_quantize_per_tensor` returns.
+    """
+    dev = _hip.require_gpu(weight, error_buf)
+    assert weight.dim() == 2, "weight must be 2-D (N, K)"
+    w = weight if weight.is_contiguous() else weight.contiguous()
+    n, k = w.shape
+    if error_buf is not None:
+        assert error_buf.dtype == torch.float32, "error_buf must be float32"
+        assert error_buf.shape == (n, k), (
+            f"error_buf shape {tuple(error_buf.shape)} != weight shape {(n, k)}"
+        )
+        assert error_buf.is_contiguous(), "error_buf must be contiguous"
+    validate = state.should_validate_residual(name)
+    amax_key, ratio_key = name + ".w_hi", f"{name}.ratio"
+
+    def _scalar_state(t):
+        if t is None:
+            return None
+        return t.detach().to(device=dev, dtype=torch.float32).reshape(()).contiguous()
+
+    prev = _scalar_state(state._delayed_amax.get(amax_key))
+    ratio_prev = _scalar_state(state._residual_ratio.get(ratio_key))
+    amax_out = torch.empty((), dtype=torch.float32, device=dev)
+    ratio_out = torch.empty((), dtype=torch.float32, device=dev) if validate else None
+    w_hi = torch.empty((n, k), dtype=torch.float8_e4m3fn, device=dev)
+    w_lo = torch.empty((n, k), dtype=torch.float8_e4m3fn, device=dev)
+    inv_hi = torch.empty(1, dtype=torch.float32, device=dev)
+    inv_lo = torch.empty(1, dtype=torch.float32, device=dev)
+    w_hi_t = torch.empty((k, n), dtype=torch.float8_e4m3fn, device=dev) if transposed else None
+    w_lo_t = torch.empty((k, n), dtype=torch.float8_e4m3fn, device=dev) if transposed else None
+    decay = float(state._ema_decay)
+    check(
+        _hip.lib().tcfp_dual_quantize_per_tensor_delayed(
+            ptr(w), _in_dtype(w), n, k, ptr(error_buf), int(bool(update_ef)), ptr(prev),
+            ptr(ratio_prev), decay, 1.0 - decay, int(validate), ptr(amax_out), ptr(ratio_out),
+            ptr(w_hi), ptr(w_lo), ptr(inv_hi), ptr(inv_lo), ptr(w_hi_t), ptr(w_lo_t),
+            ptr(_hip.workspace(dev)), _hip.stream_of(dev),
+        ),
+        "dual_quantize_per_tensor_delayed",
+    )
+    state._delayed_amax[amax_key] = amax_out
+    if validate:
+        state._residual_ratio[ratio_key] = ratio_out
+    if transposed:
+        return w_hi, w_lo, inv_hi, inv_lo, w_hi_t, w_lo_t
+    return w_hi, w_lo, inv_hi, inv_lo
+
+
 def transpose_fp8(t: torch.Tensor) -> torch.Tensor:
     """Contiguous transpose of a 2-D 8-bit tensor (HIP, LDS-tiled)."""
     dev = _hip.require_gpu(t)

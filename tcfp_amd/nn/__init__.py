@@ -83,18 +83,23 @@ class _TCFP12TensorCoreFunction(torch.autograd.Function):
     ) -> torch.Tensor:
         if nf_aware_scaling:
             raise NotImplementedError("nf_aware_scaling is not part of this build")
-        if delayed_scaling:
-            raise NotImplementedError("delayed_scaling is not part of this build")
         need_dx = ctx.needs_input_grad[0]
         need_dw = ctx.needs_input_grad[1]
 
-        # 1-4. dual quantisation of W (+ EF read and in-place update)
+        # 1-4. dual quantisation of W (+ EF read and in-place update); with
+        # delayed scaling (and an EF state to hold it) the scales follow the
+        # reference's predictive dual-track rule (nn:250-309, 350-374)
         error_buf = _ef_buffer(error_state, param_name, weight)
-        w_hi, w_lo, inv_hi, inv_lo, w_hi_t, w_lo_t = K.dual_quantize_per_tensor(
-            weight, error_buf, update_ef=update_ef, stochastic_lo=srr, transposed=True
-        ) if need_dx else (*K.dual_quantize_per_tensor(
-            weight, error_buf, update_ef=update_ef, stochastic_lo=srr
-        ), None, None)
+        if delayed_scaling and error_state is not None:
+            res = K.dual_quantize_per_tensor_delayed(
+                weight, error_buf, error_state, param_name, update_ef=update_ef,
+                transposed=need_dx,
+            )
+        else:
+            res = K.dual_quantize_per_tensor(
+                weight, error_buf, update_ef=update_ef, stochastic_lo=srr, transposed=need_dx
+            )
+        w_hi, w_lo, inv_hi, inv_lo, w_hi_t, w_lo_t = res if need_dx else (*res, None, None)
 
         # 5. activation quantisation (and the transposed copy FP8 wgrad reads)
         input_shape = input.shape
@@ -332,8 +337,6 @@ class TCFPLinear(nn.Module):
                 stacklevel=2,
             )
             delayed_scaling = False
-        if delayed_scaling:
-            raise NotImplementedError("delayed_scaling is not part of this build")
 
         self.in_features = in_features
         self.out_features = out_features

@@ -226,3 +226,29 @@ def test_ef_checkpoint_resume_continues_bit_exact(dev, tmp_path):
     for la, lb in ((a[0], b[0]), (a[2], b[2])):
         ka = la._param_name
         assert torch.equal(la._error_state._buffers[ka], lb._error_state._buffers[ka])
+
+
+def test_delayed_scaling_layer(dev):
+    """TCFPLinear(delayed_scaling=True): its first call is the plain
+    per-tensor layer bit for bit (no EMA yet, residual measured); later
+    calls keep the EMA state and train."""
+    torch.manual_seed(11)
+    a = TCFPLinear(256, 512, use_tensor_cores=True, delayed_scaling=True).to(dev)
+    b = TCFPLinear(256, 512, use_tensor_cores=True).to(dev)
+    b.load_state_dict(a.state_dict())
+    x = torch.randn(1024, 256, device=dev).bfloat16()
+    assert torch.equal(a(x), b(x))
+    st = a._error_state
+    assert set(st._delayed_amax) == {a._param_name + ".w_hi"}
+    assert set(st._residual_ratio) == {a._param_name + ".ratio"}
+    opt = torch.optim.AdamW(a.parameters(), lr=1e-3)
+    y = torch.randn(1024, 512, device=dev)
+    losses = []
+    for _ in range(30):
+        loss = (a(x).float() - y).square().mean()
+        opt.zero_grad(set_to_none=True)
+        loss.backward()
+        opt.step()
+        losses.append(loss.item())
+    assert all(np.isfinite(losses)) and losses[-1] < losses[0]
+    assert st._step_count[a._param_name + ".steps"] == 31

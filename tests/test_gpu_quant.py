@@ -333,3 +333,35 @@ def test_dual_quant_single_launch_matches_three_pass(dev, shape, wdtype, mode):
     for a, b in zip(*outs):
         assert torch.equal(a, b)
     assert K.workspace_error(dev) == 0
+
+
+# ---------------------------------------- delayed scaling (PDDS) dual quant
+@pytest.mark.parametrize("wdt", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("transposed", [False, True])
+@pytest.mark.parametrize("shape", [(256, 512), (300, 200), (64, 4096), (33, 1000)])
+def test_delayed_dual_quant_matches_oracle_over_steps(dev, wdt, transposed, shape):
+    from tcfp_amd.core import ErrorFeedbackState
+
+    state = ErrorFeedbackState(ema_decay=0.9, residual_validation_interval=3)
+    ost = oq.new_delayed_state()
+    g = torch.Generator().manual_seed(sum(shape))
+    W = torch.randn(shape, generator=g) * 0.02
+    ef_dev = torch.zeros(shape, device=dev)
+    ef_np = np.zeros(shape, np.float32)
+    for step in range(7):
+        Wd = W.to(wdt)
+        res = K.dual_quantize_per_tensor_delayed(Wd.to(dev), ef_dev, state, "lin",
+                                                 transposed=transposed)
+        hi, lo, ih, il, ef_new, val = oq.dual_quant_per_tensor_delayed(
+            Wd.float().numpy(), ef_np, ost, "lin", decay=0.9, interval=3)
+        tag = f"step {step} validated={val}"
+        assert np.array_equal(u8(res[0]), hi), tag
+        assert np.array_equal(u8(res[1]), lo), tag
+        assert res[2].item() == float(ih) and res[3].item() == float(il), tag
+        assert np.array_equal(ef_dev.cpu().numpy().view(np.uint32), ef_new.view(np.uint32)), tag
+        assert state._delayed_amax["lin.w_hi"].item() == float(ost["amax"]["lin.w_hi"]), tag
+        assert state._residual_ratio["lin.ratio"].item() == float(ost["ratio"]["lin.ratio"]), tag
+        if transposed:
+            assert np.array_equal(u8(res[4]), hi.T) and np.array_equal(u8(res[5]), lo.T), tag
+        ef_np = ef_new
+        W = W + torch.randn(shape, generator=g) * 0.004

@@ -186,3 +186,36 @@ def test_reference_gate_functions_without_gpu():
         cuda_ext.cuda_ext_dual_gemm_forward(z, z, z, s, s, s)
     with pytest.raises(RuntimeError):
         cuda_ext.cuda_ext_dual_gemm_backward_dx(z, z, z, s, s, s)
+
+
+def test_error_feedback_state_delayed_methods_follow_the_oracle():
+    # the torch-op state transitions (reference tcfp/core.py:341-403) give
+    # the same EMA values as the oracle's restatement used for the kernels
+    import numpy as np
+
+    from oracle import quant as oq
+
+    st = ErrorFeedbackState(ema_decay=0.9, residual_validation_interval=3)
+    ost = oq.new_delayed_state()
+    g = torch.Generator().manual_seed(5)
+    W = torch.randn(16, 32, generator=g) * 0.05
+    for step in range(5):
+        cur = W.abs().max().clamp(min=1e-12)
+        delayed = st.get_delayed_amax("w.w_hi", cur)
+        validate = st.should_validate_residual("w")
+        if validate:
+            st.update_residual_ratio("w", delayed, torch.tensor(0.01 * (step + 1)))
+        pred = st.predict_residual_amax("w", delayed)
+        # oracle: the same sequence of amax / measured residual values
+        key = "w.w_hi"
+        ost["amax"][key] = np.float32(cur) if key not in ost["amax"] else oq._ema_f32(
+            ost["amax"][key], np.float32(cur), 0.9)
+        assert float(delayed) == float(ost["amax"][key]), step
+        if validate:
+            r = np.float32(np.float32(0.01 * (step + 1)) / np.float32(delayed))
+            rk = "w.ratio"
+            ost["ratio"][rk] = r if rk not in ost["ratio"] else oq._ema_f32(ost["ratio"][rk], r, 0.9)
+        assert float(pred) == float(max(np.float32(np.float32(delayed) * ost["ratio"]["w.ratio"]),
+                                        np.float32(1e-12))), step
+        assert validate == (step == 0 or (step + 1) % 3 == 0)
+        W = W * 1.1

@@ -177,6 +177,72 @@ def test_sr_candidates_per_tensor():
     assert np.allclose(e[ok], x[ok], rtol=1e-5, atol=1e-6)
 
 
+# ------------------------------------------- delayed scaling (PDDS, f4)
+def test_delayed_first_call_is_the_plain_dual_quant():
+    rng = np.random.default_rng(21)
+    W = (rng.standard_normal((24, 40)) * 0.02).astype(np.float32)
+    ef = (rng.standard_normal(W.shape) * 1e-4).astype(np.float32)
+    st = oq.new_delayed_state()
+    hi, lo, ih, il, ef1, val = oq.dual_quant_per_tensor_delayed(W, ef, st, "w")
+    hi2, lo2, ih2, il2, ef2, _ = oq.dual_quant_per_tensor(W, ef)
+    assert val and np.array_equal(hi, hi2) and np.array_equal(lo, lo2)
+    assert ih == ih2 and il == il2 and np.array_equal(ef1, ef2)
+
+
+def test_delayed_without_memory_is_the_plain_dual_quant_every_step():
+    # decay 0 keeps only the current amax; validating every step measures
+    # the residual: each step must equal the plain per-tensor dual quant
+    rng = np.random.default_rng(22)
+    st = oq.new_delayed_state()
+    W = (rng.standard_normal((16, 32)) * 0.05).astype(np.float32)
+    ef = np.zeros_like(W)
+    for _ in range(4):
+        hi, lo, ih, il, ef_d, val = oq.dual_quant_per_tensor_delayed(W, ef, st, "w", decay=0.0,
+                                                                      interval=1)
+        hi2, lo2, ih2, il2, ef_p, _ = oq.dual_quant_per_tensor(W, ef)
+        assert val and np.array_equal(hi, hi2) and np.array_equal(lo, lo2)
+        assert ih == ih2 and il == il2 and np.array_equal(ef_d, ef_p)
+        ef = ef_d
+        W = (W * np.float32(1.3) + np.float32(0.01)).astype(np.float32)
+
+
+def test_delayed_ema_closed_form():
+    # amax 2 then 4 with decay 0.5: the delayed amax is exactly 3, and the
+    # W_hi scale is torch's reciprocal-then-product of it
+    st = oq.new_delayed_state()
+    W1 = np.full((4, 8), 2.0, np.float32)
+    W2 = np.full((4, 8), -4.0, np.float32)
+    oq.dual_quant_per_tensor_delayed(W1, None, st, "w", decay=0.5)
+    assert st["amax"]["w.w_hi"] == np.float32(2.0)
+    _, _, ih, il, _, val = oq.dual_quant_per_tensor_delayed(W2, None, st, "w", decay=0.5)
+    assert not val and st["amax"]["w.w_hi"] == np.float32(3.0)
+    scale = np.float32(np.float32(1.0) / np.float32(3.0)) * np.float32(448.0)
+    assert ih == np.float32(1.0) / np.float32(scale)
+    # W_lo is predicted, not measured: both residuals are 0 (amax clamps to
+    # 1e-12, ratio 1e-12 / 2), so the predicted residual amax is 1.5e-12
+    # where a measurement would give 1e-12
+    pred = np.float32(np.float32(3.0) * np.float32(np.float32(1e-12) / np.float32(2.0)))
+    scale_lo = np.float32(np.float32(1.0) / pred) * np.float32(448.0)
+    assert il == np.float32(1.0) / np.float32(scale_lo)
+    assert il != np.float32(1.0) / (np.float32(np.float32(1.0) / np.float32(1e-12)) * np.float32(448.0))
+
+
+def test_delayed_prediction_equals_measurement_when_exact():
+    # constant W with a power-of-two amax and decay 0: the ratio measured on
+    # step 1 predicts step 2's residual amax exactly, so the predicted step
+    # must reproduce the measured one bit for bit
+    rng = np.random.default_rng(23)
+    W = (rng.standard_normal((16, 64)) * 0.1).astype(np.float32)
+    W[0, 0] = np.float32(0.5)
+    W = np.clip(W, -0.5, 0.5)
+    st = oq.new_delayed_state()
+    first = oq.dual_quant_per_tensor_delayed(W, None, st, "w", decay=0.0)
+    second = oq.dual_quant_per_tensor_delayed(W, None, st, "w", decay=0.0)
+    assert first[5] and not second[5]
+    for a, b in zip(first[:5], second[:5]):
+        assert np.array_equal(np.asarray(a), np.asarray(b))
+
+
 # ------------------------------------------------------- block quant (a4)
 @pytest.mark.parametrize("bs", [32, 64, 128])
 def test_block_quantize_exponent_and_codes(bs):
