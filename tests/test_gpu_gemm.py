@@ -380,3 +380,48 @@ def test_cuda_ext_surface_routes_to_hip_dual_gemm(dev):
     g, ig = make_act((256, 384), 5, dev, torch.float8_e5m2)
     assert torch.equal(cuda_ext.cuda_ext_dual_gemm_backward_dx(g, h, l, ig, ih, il),
                        K.fused_dual_gemm_backward_dx(g, h, l, ig, ih, il))
+
+
+def test_dual_gemm_empty_rows_and_cols(dev):
+    a, ia = make_act((0, 64), 1, dev)
+    h, l, ih, il = make_pair((32, 64), 2, dev)
+    out = K.fused_dual_gemm_forward(a, h, l, ia, ih, il)
+    assert out.shape == (0, 32)
+    a, ia = make_act((16, 64), 1, dev)
+    h, l, ih, il = make_pair((0, 64), 2, dev)
+    out = K.fused_dual_gemm_forward(a, h, l, ia, ih, il)
+    assert out.shape == (16, 0)
+
+
+def test_c1_single_linear_forward_full_size(dev):
+    """configs[0] at its full size: X [8192, 1024] bf16 N(0,1) (seed 0),
+    W [4096, 1024] fp32 N(0, 0.02) (seed 1), zero EF.  W_hi/W_lo/X codes and
+    scales bit-exact against the oracle; the output within 1e-4 relative
+    Frobenius of the fp32 matmul of the same dequantised operands (the
+    contract is 1e-2), and, as the configuration's literal accuracy
+    reference, within a few percent of X W^T with X unquantised."""
+    from tcfp_amd.nn import TCFPLinear
+
+    x = torch.randn(8192, 1024, generator=torch.Generator().manual_seed(0)).bfloat16()
+    w = torch.randn(4096, 1024, generator=torch.Generator().manual_seed(1)) * 0.02
+    hi, lo, ih, il, _, _ = oq.dual_quant_per_tensor(w.numpy(), np.zeros_like(w.numpy()))
+    xq, xinv, _ = oq.to_fp8_per_tensor(x.float().numpy(), "bf16")
+    h_d, l_d, ih_d, il_d = K.dual_quantize_per_tensor(w.to(dev), torch.zeros(4096, 1024, device=dev))
+    assert np.array_equal(u8(h_d), hi) and np.array_equal(u8(l_d), lo)
+    assert ih_d.item() == float(ih) and il_d.item() == float(il)
+    a_d, ainv_d = K.quantize_per_tensor(x.to(dev))
+    assert np.array_equal(u8(a_d), xq) and ainv_d.item() == float(xinv)
+    lin = TCFPLinear(1024, 4096, bias=False, use_tensor_cores=True).to(dev)
+    with torch.no_grad():
+        lin.weight.copy_(w.to(dev))
+    out = lin(x.to(dev))
+    assert out.dtype == torch.float32 and out.shape == (8192, 4096)
+    A = a_d.float() * ainv_d
+    Wd = h_d.float() * ih_d + l_d.float() * il_d
+    ref = A @ Wd.t()
+    err = (torch.linalg.norm(out - ref) / torch.linalg.norm(ref)).item()
+    lit = x.to(dev).float() @ w.to(dev).t()
+    err_lit = (torch.linalg.norm(out - lit) / torch.linalg.norm(lit)).item()
+    print(f"C1 rel_fro vs dequant fp32 {err:.2e}, vs unquantised X W^T {err_lit:.2e}", flush=True)
+    assert err < EXACT
+    assert err_lit < 5e-2

@@ -365,3 +365,28 @@ def test_delayed_dual_quant_matches_oracle_over_steps(dev, wdt, transposed, shap
             assert np.array_equal(u8(res[4]), hi.T) and np.array_equal(u8(res[5]), lo.T), tag
         ef_np = ef_new
         W = W + torch.randn(shape, generator=g) * 0.004
+
+
+# ------------------------------------------------------------ edge cases
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_nan_propagates_like_torch(dev, dtype):
+    # the reference's amax is NaN-propagating (|t|.max() keeps NaN, clamp
+    # keeps NaN), so one NaN makes the scale and every code NaN
+    x = torch.randn(64, 96).to(dtype)
+    x[7, 11] = float("nan")
+    q, inv = to_fp8_e4m3(x.to(dev))
+    assert torch.isnan(inv).all()
+    codes = u8(q)
+    assert np.all((codes & 0x7F) == 0x7F)
+    h, l, ih, il = K.dual_quantize_per_tensor(x.float().to(dev))
+    assert torch.isnan(ih).all() and np.all((u8(h) & 0x7F) == 0x7F)
+
+
+def test_per_tensor_dual_quant_empty_and_one_element(dev):
+    h, l, ih, il = K.dual_quantize_per_tensor(torch.empty(0, 8, device=dev))
+    assert h.shape == (0, 8) and l.shape == (0, 8)
+    w = torch.tensor([[0.3]], device=dev)
+    h, l, ih, il = K.dual_quantize_per_tensor(w)
+    hi, lo, ih2, il2, _, _ = oq.dual_quant_per_tensor(np.array([[0.3]], np.float32))
+    assert np.array_equal(u8(h), hi) and np.array_equal(u8(l), lo)
+    assert ih.item() == float(ih2) and il.item() == float(il2)
