@@ -297,6 +297,42 @@ int tcfp_block_wgrad(const float* g, int64_t m, int64_t n_out, const uint8_t* x,
                      const int8_t* e_x, int64_t k_in, int block, float* dw, void* workspace,
                      size_t workspace_bytes, void* stream);
 
+/* Block backward, fused operand preparation (no single reference
+ * counterpart: it produces, in one pass over the fp32 gradient g [m, n],
+ * what the reference's backward derives from it separately,
+ * tcfp/nn/__init__.py:700-761):
+ *   g_deq     [m, n] bf16: g block-quantised to E5M2 per (row, n-block of
+ *             `block`) with the block_quantize_fp8 rule (tcfp/kernels.py:
+ *             1675-1722) and dequantised -- the dgrad's G operand;
+ *   g_split_t [n, 2m] bf16: [bf16(g) | bf16(g - bf16(g))] transposed -- the
+ *             wgrad's split fp32 gradient;
+ *   bias_grad [n] fp32: column sums of g (grad.sum(0)), summed per 64-row
+ *             tile and then over tiles in order.
+ * Any output may be NULL.  n % block == 0; bias_grad needs a workspace of
+ * tcfp_block_grad_prep_workspace_bytes(m, n) bytes. */
+size_t tcfp_block_grad_prep_workspace_bytes(int64_t m, int64_t n);
+int tcfp_block_grad_prep(const float* g, int64_t m, int64_t n, int block, uint16_t* g_deq,
+                         uint16_t* g_split_t, float* bias_grad, void* workspace,
+                         size_t workspace_bytes, void* stream);
+
+/* tcfp_block_dual_gemm_dx with the gradient already dequantised to bf16
+ * (g_deq from tcfp_block_grad_prep): same result bit for bit.  Workspace:
+ * tcfp_block_dual_gemm_dx_bf16_workspace_bytes(d_out, d_in). */
+size_t tcfp_block_dual_gemm_dx_bf16_workspace_bytes(int64_t d_out, int64_t d_in);
+int tcfp_block_dual_gemm_dx_bf16(const uint16_t* g_deq, const uint8_t* w_hi, const uint8_t* w_lo,
+                                 const int8_t* e_hi, const int8_t* e_lo, int64_t m, int64_t d_out,
+                                 int64_t d_in, int block, float* dx, void* workspace,
+                                 size_t workspace_bytes, void* stream);
+
+/* tcfp_block_wgrad with the gradient already split and transposed
+ * (g_split_t from tcfp_block_grad_prep): same result bit for bit.
+ * Workspace: tcfp_block_wgrad_presplit_workspace_bytes(m, n_out, k_in). */
+size_t tcfp_block_wgrad_presplit_workspace_bytes(int64_t m, int64_t n_out, int64_t k_in);
+int tcfp_block_wgrad_presplit(const uint16_t* g_split_t, int64_t m, int64_t n_out,
+                              const uint8_t* x, int x_fmt, const int8_t* e_x, int64_t k_in,
+                              int block, float* dw, void* workspace, size_t workspace_bytes,
+                              void* stream);
+
 /* ---- layout helpers ---------------------------------------------------- */
 
 /* dst[c, r] = src[r, c] for a [rows, cols] byte matrix (ld = cols / rows).

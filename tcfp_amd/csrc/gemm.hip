@@ -1140,8 +1140,16 @@ __global__ __launch_bounds__(256) void dequant_rows_bf16_kernel(
 // out[c, r] = bf16(q[r, c] * 2^e[c / bs, r]) through a 64 x 64 LDS tile.
 template <int FMT>
 __global__ __launch_bounds__(256) void dequant_t_bf16_kernel(
-    const uint8_t* __restrict__ q, const int8_t* __restrict__ e, int64_t rows, int64_t cols,
-    int bs_shift, int zero_sentinel, uint16_t* __restrict__ out) {
+    const uint8_t* __restrict__ q0, const int8_t* __restrict__ e0, uint16_t* __restrict__ out0,
+    const uint8_t* __restrict__ q1, const int8_t* __restrict__ e1, uint16_t* __restrict__ out1,
+    int64_t rows, int64_t cols, int bs_shift) {
+  // blockIdx.y 0: matrix 0 (W_hi); 1: matrix 1 (W_lo, whose -128 exponent
+  // marks a zero block)
+  const bool second = blockIdx.y == 1;
+  const uint8_t* __restrict__ q = second ? q1 : q0;
+  const int8_t* __restrict__ e = second ? e1 : e0;
+  uint16_t* __restrict__ out = second ? out1 : out0;
+  const int zero_sentinel = second ? 1 : 0;
   __shared__ uint16_t tile[64][64 + 2];
   const int tiles_c = int((cols + 63) / 64);
   const int64_t r0 = int64_t(blockIdx.x / tiles_c) * 64, c0 = int64_t(blockIdx.x % tiles_c) * 64;
@@ -1282,6 +1290,31 @@ __global__ __launch_bounds__(256) void dequant_t_dup_bf16_kernel(
 
 }  // namespace
 
+namespace {
+
+// W_hi^T, W_lo^T dequantised into bf16 (one launch), then the bf16 dual GEMM
+// A = G [m, d_out] x B = W^T [d_in, d_out] (K counts bytes), fp32 out.
+int dgrad_bf16(const uint16_t* gd, const uint8_t* w_hi, const uint8_t* w_lo, const int8_t* e_hi,
+               const int8_t* e_lo, int64_t m, int64_t d_out, int64_t d_in, int shift, float* dx,
+               uint16_t* wth, uint16_t* wtl, hipStream_t st) {
+  const int64_t tiles = ((d_out + 63) / 64) * ((d_in + 63) / 64);
+  if (tiles > INT32_MAX) return TCFP_ERR_SHAPE;
+  dequant_t_bf16_kernel<TCFP_FP8_E4M3><<<dim3(unsigned(tiles), w_lo ? 2u : 1u), 256, 0, st>>>(
+      w_hi, e_hi, wth, w_lo, e_lo, wtl, d_out, d_in, shift);
+  if (hipGetLastError() != hipSuccess) return TCFP_ERR_HIP;
+  GemmArgs ga{};
+  ga.A = reinterpret_cast<const uint8_t*>(gd);
+  ga.B0 = reinterpret_cast<const uint8_t*>(wth);
+  ga.B1 = reinterpret_cast<const uint8_t*>(w_lo ? wtl : wth);
+  ga.M = int(m); ga.N = int(d_in); ga.K = int(2 * d_out);
+  ga.lda = 2 * d_out; ga.ldb = 2 * d_out;
+  ga.out = dx; ga.ldo = d_in;
+  if (w_lo) return launch_gemm<kBF16, kBF16, false, float, 0>(ga, st);
+  return launch_gemm<kBF16, kBF16, true, float, 0>(ga, st);
+}
+
+}  // namespace
+
 extern "C" size_t tcfp_block_dual_gemm_dx_workspace_bytes(int64_t m, int64_t d_out, int64_t d_in) {
   if (m < 0 || d_out < 0 || d_in < 0) return 0;
   return align256(size_t(m) * size_t(d_out) * 2) + 2 * align256(size_t(d_in) * size_t(d_out) * 2);
@@ -1319,25 +1352,37 @@ extern "C" int tcfp_block_dual_gemm_dx(const uint8_t* g, int g_fmt, const int8_t
       dequant_rows_bf16_kernel<TCFP_FP8_E5M2><<<unsigned(gr), 256, 0, st>>>(g, e_g, m, d_out, shift, 0, gd);
     else
       dequant_rows_bf16_kernel<TCFP_FP8_E4M3><<<unsigned(gr), 256, 0, st>>>(g, e_g, m, d_out, shift, 0, gd);
-    const int64_t tiles = ((d_out + 63) / 64) * ((d_in + 63) / 64);
-    if (tiles > INT32_MAX) return TCFP_ERR_SHAPE;
-    dequant_t_bf16_kernel<TCFP_FP8_E4M3><<<unsigned(tiles), 256, 0, st>>>(w_hi, e_hi, d_out, d_in,
-                                                                           shift, 0, wth);
-    if (w_lo)
-      dequant_t_bf16_kernel<TCFP_FP8_E4M3><<<unsigned(tiles), 256, 0, st>>>(w_lo, e_lo, d_out,
-                                                                             d_in, shift, 1, wtl);
     if (hipGetLastError() != hipSuccess) return TCFP_ERR_HIP;
   }
-  // bf16 dual GEMM: A = G [m, d_out], B = W^T [d_in, d_out]; K counts bytes
-  GemmArgs ga{};
-  ga.A = reinterpret_cast<const uint8_t*>(gd);
-  ga.B0 = reinterpret_cast<const uint8_t*>(wth);
-  ga.B1 = reinterpret_cast<const uint8_t*>(w_lo ? wtl : wth);
-  ga.M = int(m); ga.N = int(d_in); ga.K = int(2 * d_out);
-  ga.lda = 2 * d_out; ga.ldb = 2 * d_out;
-  ga.out = dx; ga.ldo = d_in;
-  if (w_lo) return launch_gemm<kBF16, kBF16, false, float, 0>(ga, st);
-  return launch_gemm<kBF16, kBF16, true, float, 0>(ga, st);
+  return dgrad_bf16(gd, w_hi, w_lo, e_hi, e_lo, m, d_out, d_in, shift, dx, wth, wtl, st);
+}
+
+extern "C" size_t tcfp_block_dual_gemm_dx_bf16_workspace_bytes(int64_t d_out, int64_t d_in) {
+  if (d_out < 0 || d_in < 0) return 0;
+  return 2 * align256(size_t(d_in) * size_t(d_out) * 2);
+}
+
+extern "C" int tcfp_block_dual_gemm_dx_bf16(const uint16_t* g_deq, const uint8_t* w_hi,
+                                            const uint8_t* w_lo, const int8_t* e_hi,
+                                            const int8_t* e_lo, int64_t m, int64_t d_out,
+                                            int64_t d_in, int block, float* dx, void* workspace,
+                                            size_t workspace_bytes, void* stream) {
+  if (m < 0 || d_out < 0 || d_in < 0 || m > INT32_MAX || d_in > INT32_MAX ||
+      2 * d_out > INT32_MAX)
+    return TCFP_ERR_SHAPE;
+  if (block != 32 && block != 64 && block != 128) return TCFP_ERR_SHAPE;
+  if (d_out % block != 0 || d_in % block != 0) return TCFP_ERR_SHAPE;
+  if (!g_deq || !w_hi || !e_hi || (w_lo && !e_lo) || !dx) return TCFP_ERR_SHAPE;
+  if (m == 0 || d_in == 0) return TCFP_OK;
+  if (!workspace || workspace_bytes < tcfp_block_dual_gemm_dx_bf16_workspace_bytes(d_out, d_in))
+    return TCFP_ERR_WORKSPACE;
+  if (!al16(workspace) || !al16(dx) || !al16(g_deq)) return TCFP_ERR_ALIGN;
+  const int shift = block == 32 ? 5 : (block == 64 ? 6 : 7);
+  uint8_t* ws = static_cast<uint8_t*>(workspace);
+  uint16_t* wth = reinterpret_cast<uint16_t*>(ws);
+  uint16_t* wtl = reinterpret_cast<uint16_t*>(ws + align256(size_t(d_in) * size_t(d_out) * 2));
+  return dgrad_bf16(g_deq, w_hi, w_lo, e_hi, e_lo, m, d_out, d_in, shift, dx, wth, wtl,
+                    static_cast<hipStream_t>(stream));
 }
 
 namespace {
@@ -1376,7 +1421,195 @@ int64_t wgrad_splits(int64_t m, int64_t n_out, int64_t k_in, int64_t* kc) {
   return (kbytes + *kc - 1) / *kc;
 }
 
+// The wgrad GEMM over the concatenated contraction: A' = [g_hi | g_lo]^T
+// [n_out, 2m], B' = [x | x]^T [k_in, 2m] (bf16), dw [n_out, k_in] fp32;
+// split-K partials go to `part` when the output is small.
+int wgrad_gemm(const uint16_t* ap, const uint16_t* bp, int64_t m, int64_t n_out, int64_t k_in,
+               float* dw, float* part, hipStream_t st) {
+  GemmArgs ga{};
+  ga.A = reinterpret_cast<const uint8_t*>(ap);
+  ga.B0 = reinterpret_cast<const uint8_t*>(bp);
+  ga.B1 = ga.B0;
+  ga.M = int(n_out); ga.N = int(k_in); ga.K = int(4 * m);  // bytes of 2M bf16
+  ga.lda = 4 * m; ga.ldb = 4 * m;
+  ga.out = dw; ga.ldo = k_in;
+  int64_t kc;
+  const int64_t splits = wgrad_splits(m, n_out, k_in, &kc);
+  if (splits <= 1) return launch_gemm<kBF16, kBF16, true, float, 0>(ga, st);
+  // partial products of each K chunk, then their sum in split order
+  ga.out = part;
+  ga.kc = int(kc);
+  ga.split_stride = n_out * k_in;
+  const int rc = launch_gemm<kBF16, kBF16, true, float, 0>(ga, st);
+  if (rc != TCFP_OK) return rc;
+  const int64_t n4 = n_out * k_in / 4;
+  const int blocks = int(std::min<int64_t>((n4 + 255) / 256, int64_t(num_cus()) * 8));
+  splitk_reduce_kernel<<<blocks, 256, 0, st>>>(part, int(splits), n4, n_out * k_in, dw);
+  return hipGetLastError() == hipSuccess ? TCFP_OK : TCFP_ERR_HIP;
+}
+
+// ---- fused gradient preparation for the block backward ---------------------
+// One pass over the fp32 gradient g [m, n] in 64 x 128 tiles writes, as
+// requested:
+//  * gd [m, n] bf16: g block-quantised to E5M2 per (row, n-block) with the
+//    exponent rule of block_quantize_fp8 (tcfp/kernels.py:205-275) and
+//    dequantised -- the dgrad's G operand;
+//  * gs [n, 2m] bf16: [bf16(g) | bf16(g - bf16(g))] transposed -- the
+//    wgrad's split gradient;
+//  * cpart [ceil(m/64), n] fp32: per-tile column sums (the bias gradient
+//    after colsum_tiles_kernel).
+// n % 32 == 0 (the block sizes divide it).
+template <int BS>
+__global__ __launch_bounds__(256) void grad_prep_kernel(const float* __restrict__ g, int64_t m,
+                                                        int64_t n, uint16_t* __restrict__ gd,
+                                                        uint16_t* __restrict__ gs,
+                                                        float* __restrict__ cpart) {
+  __shared__ float tile[128][64 + 1];  // [column][row]
+  const int tiles_c = int((n + 127) / 128);
+  const int64_t tr = blockIdx.x / tiles_c;
+  const int64_t r0 = tr * 64, c0 = int64_t(blockIdx.x % tiles_c) * 128;
+  const int t = threadIdx.x;
+  // phase 1: row r0 + t/4, columns c0 + 32*(t%4) .. +31 (one 32-wide segment)
+  const int lr = t >> 2, seg = t & 3;
+  const int64_t r = r0 + lr, cb = c0 + seg * 32;
+  const bool in = r < m && cb < n;
+  float v[32];
+  if (in) {
+#pragma unroll
+    for (int j = 0; j < 32; j += 4) {
+      const float4 a = *reinterpret_cast<const float4*>(g + r * n + cb + j);
+      v[j] = a.x; v[j + 1] = a.y; v[j + 2] = a.z; v[j + 3] = a.w;
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 32; ++j) v[j] = 0.0f;
+  }
+  if (gd) {
+    // block amax: a 32-wide segment per lane; 64 / 128-wide blocks span
+    // the 2 / 4 lanes of the same row
+    uint32_t a = 0;
+#pragma unroll
+    for (int j = 0; j < 32; ++j) a = a > (__float_as_uint(v[j]) & 0x7FFFFFFFu) ? a : (__float_as_uint(v[j]) & 0x7FFFFFFFu);
+    if constexpr (BS >= 64) { const uint32_t o = __shfl_xor(a, 1, 64); a = a > o ? a : o; }
+    if constexpr (BS >= 128) { const uint32_t o = __shfl_xor(a, 2, 64); a = a > o ? a : o; }
+    const int e = block_exponent(__uint_as_float(a), kE5M2Max);
+    const float mul = exp2i(-e), sc = exp2i(e);
+    uint32_t w[16];
+#pragma unroll
+    for (int j = 0; j < 32; j += 4) {
+      float c4[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float x = v[j + q] * mul;
+        c4[q] = x > kE5M2Max ? kE5M2Max : (x < -kE5M2Max ? -kE5M2Max : x);
+      }
+      const uint32_t codes = cvt4_fp8<TCFP_FP8_E5M2>(c4[0], c4[1], c4[2], c4[3]);
+      uint16_t b[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        b[q] = f32_to_bf16_rne(fp8_to_f32<TCFP_FP8_E5M2>((codes >> (8 * q)) & 0xFFu) * sc);
+      w[j / 2] = uint32_t(b[0]) | (uint32_t(b[1]) << 16);
+      w[j / 2 + 1] = uint32_t(b[2]) | (uint32_t(b[3]) << 16);
+    }
+    if (in) {
+      uint4* o = reinterpret_cast<uint4*>(gd + r * n + cb);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) o[q] = make_uint4(w[4 * q], w[4 * q + 1], w[4 * q + 2], w[4 * q + 3]);
+    }
+  }
+  if (!gs && !cpart) return;
+#pragma unroll
+  for (int j = 0; j < 32; ++j) tile[seg * 32 + j][lr] = v[j];
+  __syncthreads();
+  // phase 2: column c0 + t/2, rows r0 + 32*(t%2) .. +31
+  const int cc = t >> 1, half = t & 1;
+  const int64_t c = c0 + cc;
+  float sum = 0.0f;
+  uint16_t hi[32], lo[32];
+#pragma unroll
+  for (int j = 0; j < 32; ++j) {
+    const float x = tile[cc][half * 32 + j];
+    sum += x;
+    hi[j] = f32_to_bf16_rne(x);
+    lo[j] = f32_to_bf16_rne(__fsub_rn(x, bf16_to_f32(hi[j])));
+  }
+  if (cpart) {
+    const float other = __shfl_xor(sum, 1, 64);
+    if (half == 0 && c < n) cpart[tr * n + c] = sum + other;
+  }
+  if (gs && c < n) {
+    const int64_t rb = r0 + half * 32;
+    uint16_t* oh = gs + c * (2 * m) + rb;
+    uint16_t* ol = oh + m;
+    if ((m % 8) == 0 && rb + 32 <= m) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        uint32_t wh[4], wl[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          wh[j] = uint32_t(hi[8 * q + 2 * j]) | (uint32_t(hi[8 * q + 2 * j + 1]) << 16);
+          wl[j] = uint32_t(lo[8 * q + 2 * j]) | (uint32_t(lo[8 * q + 2 * j + 1]) << 16);
+        }
+        reinterpret_cast<uint4*>(oh)[q] = make_uint4(wh[0], wh[1], wh[2], wh[3]);
+        reinterpret_cast<uint4*>(ol)[q] = make_uint4(wl[0], wl[1], wl[2], wl[3]);
+      }
+    } else {
+      for (int j = 0; j < 32; ++j)
+        if (rb + j < m) { oh[j] = hi[j]; ol[j] = lo[j]; }
+    }
+  }
+}
+
+// out[c] = sum over row tiles of part[tile, c], in tile order.
+__global__ __launch_bounds__(256) void colsum_tiles_kernel(const float* __restrict__ part,
+                                                           int64_t tiles, int64_t n,
+                                                           float* __restrict__ out) {
+  const int64_t c = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  if (c >= n) return;
+  float s = 0.0f;
+  for (int64_t t = 0; t < tiles; ++t) s += part[t * n + c];
+  out[c] = s;
+}
+
 }  // namespace
+
+extern "C" size_t tcfp_block_grad_prep_workspace_bytes(int64_t m, int64_t n) {
+  if (m < 0 || n < 0) return 0;
+  return align256(size_t((m + 63) / 64) * size_t(n) * 4);
+}
+
+extern "C" int tcfp_block_grad_prep(const float* g, int64_t m, int64_t n, int block,
+                                    uint16_t* g_deq, uint16_t* g_split_t, float* bias_grad,
+                                    void* workspace, size_t workspace_bytes, void* stream) {
+  if (m < 0 || n < 0 || m > INT32_MAX || n > INT32_MAX) return TCFP_ERR_SHAPE;
+  if (block != 32 && block != 64 && block != 128) return TCFP_ERR_SHAPE;
+  if (n % block != 0) return TCFP_ERR_SHAPE;
+  if (!g) return TCFP_ERR_SHAPE;
+  if (bias_grad && (!workspace || workspace_bytes < tcfp_block_grad_prep_workspace_bytes(m, n)))
+    return TCFP_ERR_WORKSPACE;
+  if (!al16(g) || (g_deq && !al16(g_deq)) || (g_split_t && !al16(g_split_t)) ||
+      (workspace && !al16(workspace)))
+    return TCFP_ERR_ALIGN;
+  if (n == 0) return TCFP_OK;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (m == 0) {
+    if (bias_grad) {
+      colsum_tiles_kernel<<<unsigned((n + 255) / 256), 256, 0, st>>>(nullptr, 0, n, bias_grad);
+      return hipGetLastError() == hipSuccess ? TCFP_OK : TCFP_ERR_HIP;
+    }
+    return TCFP_OK;
+  }
+  const int64_t tr = (m + 63) / 64, tc = (n + 127) / 128;
+  if (tr * tc > INT32_MAX) return TCFP_ERR_SHAPE;
+  float* part = bias_grad ? static_cast<float*>(workspace) : nullptr;
+  const unsigned grid = unsigned(tr * tc);
+  if (block == 32) grad_prep_kernel<32><<<grid, 256, 0, st>>>(g, m, n, g_deq, g_split_t, part);
+  else if (block == 64) grad_prep_kernel<64><<<grid, 256, 0, st>>>(g, m, n, g_deq, g_split_t, part);
+  else grad_prep_kernel<128><<<grid, 256, 0, st>>>(g, m, n, g_deq, g_split_t, part);
+  if (bias_grad)
+    colsum_tiles_kernel<<<unsigned((n + 255) / 256), 256, 0, st>>>(part, tr, n, bias_grad);
+  return hipGetLastError() == hipSuccess ? TCFP_OK : TCFP_ERR_HIP;
+}
 
 extern "C" size_t tcfp_block_wgrad_workspace_bytes(int64_t m, int64_t n_out, int64_t k_in) {
   if (m < 0 || n_out < 0 || k_in < 0) return 0;
@@ -1418,26 +1651,48 @@ extern "C" int tcfp_block_wgrad(const float* g, int64_t m, int64_t n_out, const 
       dequant_t_dup_bf16_kernel<TCFP_FP8_E4M3><<<unsigned(tx), 256, 0, st>>>(x, e_x, m, k_in, shift, bp);
     if (hipGetLastError() != hipSuccess) return TCFP_ERR_HIP;
   }
-  GemmArgs ga{};
-  ga.A = reinterpret_cast<const uint8_t*>(ap);
-  ga.B0 = reinterpret_cast<const uint8_t*>(bp);
-  ga.B1 = ga.B0;
-  ga.M = int(n_out); ga.N = int(k_in); ga.K = int(4 * m);  // bytes of 2M bf16
-  ga.lda = 4 * m; ga.ldb = 4 * m;
-  ga.out = dw; ga.ldo = k_in;
-  int64_t kc;
-  const int64_t splits = wgrad_splits(m, n_out, k_in, &kc);
-  if (splits <= 1) return launch_gemm<kBF16, kBF16, true, float, 0>(ga, st);
-  // partial products of each K chunk, then their sum in split order
   float* part = reinterpret_cast<float*>(ws + align256(size_t(n_out) * size_t(2 * m) * 2) +
                                          align256(size_t(k_in) * size_t(2 * m) * 2));
-  ga.out = part;
-  ga.kc = int(kc);
-  ga.split_stride = n_out * k_in;
-  const int rc = launch_gemm<kBF16, kBF16, true, float, 0>(ga, st);
-  if (rc != TCFP_OK) return rc;
-  const int64_t n4 = n_out * k_in / 4;
-  const int blocks = int(std::min<int64_t>((n4 + 255) / 256, int64_t(num_cus()) * 8));
-  splitk_reduce_kernel<<<blocks, 256, 0, st>>>(part, int(splits), n4, n_out * k_in, dw);
-  return hipGetLastError() == hipSuccess ? TCFP_OK : TCFP_ERR_HIP;
+  return wgrad_gemm(ap, bp, m, n_out, k_in, dw, part, st);
+}
+
+extern "C" size_t tcfp_block_wgrad_presplit_workspace_bytes(int64_t m, int64_t n_out,
+                                                           int64_t k_in) {
+  if (m < 0 || n_out < 0 || k_in < 0) return 0;
+  int64_t kc;
+  const int64_t splits = wgrad_splits(m, n_out, k_in, &kc);
+  return align256(size_t(k_in) * size_t(2 * m) * 2) +
+         (splits > 1 ? align256(size_t(splits) * size_t(n_out) * size_t(k_in) * 4) : 0);
+}
+
+extern "C" int tcfp_block_wgrad_presplit(const uint16_t* g_split_t, int64_t m, int64_t n_out,
+                                         const uint8_t* x, int x_fmt, const int8_t* e_x,
+                                         int64_t k_in, int block, float* dw, void* workspace,
+                                         size_t workspace_bytes, void* stream) {
+  if (m < 0 || n_out < 0 || k_in < 0 || n_out > INT32_MAX || k_in > INT32_MAX ||
+      4 * m > INT32_MAX)
+    return TCFP_ERR_SHAPE;
+  if (block != 32 && block != 64 && block != 128) return TCFP_ERR_SHAPE;
+  if (k_in % block != 0 || m % 4 != 0) return TCFP_ERR_SHAPE;
+  if (x_fmt != TCFP_FP8_E4M3 && x_fmt != TCFP_FP8_E5M2) return TCFP_ERR_DTYPE;
+  if (!g_split_t || !x || !e_x || !dw) return TCFP_ERR_SHAPE;
+  if (n_out == 0 || k_in == 0) return TCFP_OK;
+  if (!workspace || workspace_bytes < tcfp_block_wgrad_presplit_workspace_bytes(m, n_out, k_in))
+    return TCFP_ERR_WORKSPACE;
+  if (!al16(workspace) || !al16(dw) || !al16(g_split_t)) return TCFP_ERR_ALIGN;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int shift = block == 32 ? 5 : (block == 64 ? 6 : 7);
+  uint8_t* ws = static_cast<uint8_t*>(workspace);
+  uint16_t* bp = reinterpret_cast<uint16_t*>(ws);
+  if (m > 0) {
+    const int64_t tx = ((m + 63) / 64) * ((k_in + 63) / 64);
+    if (tx > INT32_MAX) return TCFP_ERR_SHAPE;
+    if (x_fmt == TCFP_FP8_E5M2)
+      dequant_t_dup_bf16_kernel<TCFP_FP8_E5M2><<<unsigned(tx), 256, 0, st>>>(x, e_x, m, k_in, shift, bp);
+    else
+      dequant_t_dup_bf16_kernel<TCFP_FP8_E4M3><<<unsigned(tx), 256, 0, st>>>(x, e_x, m, k_in, shift, bp);
+    if (hipGetLastError() != hipSuccess) return TCFP_ERR_HIP;
+  }
+  float* part = reinterpret_cast<float*>(ws + align256(size_t(k_in) * size_t(2 * m) * 2));
+  return wgrad_gemm(g_split_t, bp, m, n_out, k_in, dw, part, st);
 }

@@ -847,6 +847,90 @@ def block_scaled_wgrad(
     return out
 
 
+def block_backward_prep(
+    grad: torch.Tensor,
+    block_size: int,
+    *,
+    dequant: bool = True,
+    split: bool = True,
+    bias: bool = False,
+):
+    """One pass over the fp32 gradient [M, N] for the block backward.
+
+    Returns ``(g_deq, g_split_t, bias_grad)`` (None where not requested):
+    ``g_deq`` [M, N] bf16 is the gradient block-quantised to E5M2 exactly as
+    ``block_quantize_fp8(grad, block_size, float8_e5m2)`` and dequantised
+    (the dgrad operand); ``g_split_t`` [N, 2M] bf16 is the transposed
+    hi/lo split the block wgrad uses; ``bias_grad`` [N] fp32 is
+    ``grad.sum(0)`` summed per 64-row tile.  These replace the quantise,
+    dequantise, split and reduce passes the backward would otherwise make.
+    """
+    M, N = grad.shape
+    assert N % block_size == 0, f"N ({N}) must be divisible by block_size ({block_size})"
+    dev = _hip.require_gpu(grad)
+    g = grad if (grad.dtype == torch.float32 and grad.is_contiguous()) else grad.float().contiguous()
+    g_deq = torch.empty((M, N), dtype=torch.bfloat16, device=dev) if dequant else None
+    g_split = torch.empty((N, 2 * M), dtype=torch.bfloat16, device=dev) if split else None
+    bias_grad = torch.empty((N,), dtype=torch.float32, device=dev) if bias else None
+    nbytes = int(_hip.lib().tcfp_block_grad_prep_workspace_bytes(M, N)) if bias else 0
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev) if bias else None
+    check(
+        _hip.lib().tcfp_block_grad_prep(
+            ptr(g), M, N, block_size, ptr(g_deq), ptr(g_split), ptr(bias_grad), ptr(ws), nbytes,
+            _hip.stream_of(dev),
+        ),
+        "block_backward_prep",
+    )
+    return g_deq, g_split, bias_grad
+
+
+def block_dgrad_from_prep(g_deq, w_hi_fp8, w_lo_fp8, w_hi_scales, w_lo_scales, block_size):
+    """``fused_block_scaled_dual_gemm_backward_dx`` from the bf16 gradient of
+    :func:`block_backward_prep` (same result bit for bit)."""
+    M, D_out = g_deq.shape
+    D_out2, D_in = w_hi_fp8.shape
+    assert D_out == D_out2, f"Shape mismatch: grad({M},{D_out}), w_hi({D_out2},{D_in})"
+    dev = _hip.require_gpu(g_deq, w_hi_fp8, w_lo_fp8)
+    nkb = D_in // block_size
+    wh = w_hi_fp8.contiguous()
+    wl = w_lo_fp8.contiguous() if w_lo_fp8 is not None else None
+    eh = _block_exps(w_hi_scales, D_out, nkb, "w_hi_scales")
+    el = _block_exps(w_lo_scales, D_out, nkb, "w_lo_scales") if wl is not None else None
+    out = torch.empty((M, D_in), dtype=torch.float32, device=dev)
+    nbytes = int(_hip.lib().tcfp_block_dual_gemm_dx_bf16_workspace_bytes(D_out, D_in))
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
+    check(
+        _hip.lib().tcfp_block_dual_gemm_dx_bf16(
+            ptr(g_deq), ptr(wh), ptr(wl), ptr(eh), ptr(el), M, D_out, D_in, block_size, ptr(out),
+            ptr(ws), nbytes, _hip.stream_of(dev),
+        ),
+        "block_dgrad_from_prep",
+    )
+    return out
+
+
+def block_wgrad_from_prep(g_split_t, act_fp8, act_scales, block_size):
+    """``block_scaled_wgrad`` from the split gradient of
+    :func:`block_backward_prep` (same result bit for bit; M % 4 == 0)."""
+    N, M2 = g_split_t.shape
+    M, Kd = act_fp8.shape
+    assert M2 == 2 * M and M % 4 == 0, "split gradient must be [N, 2M] with M % 4 == 0"
+    dev = _hip.require_gpu(g_split_t, act_fp8, act_scales)
+    a = act_fp8.contiguous()
+    e = _block_exps(act_scales, M, Kd // block_size, "act_scales")
+    out = torch.empty((N, Kd), dtype=torch.float32, device=dev)
+    nbytes = int(_hip.lib().tcfp_block_wgrad_presplit_workspace_bytes(M, N, Kd))
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
+    check(
+        _hip.lib().tcfp_block_wgrad_presplit(
+            ptr(g_split_t), M, N, ptr(a), _fmt(a.dtype), ptr(e), Kd, block_size, ptr(out),
+            ptr(ws), nbytes, _hip.stream_of(dev),
+        ),
+        "block_wgrad_from_prep",
+    )
+    return out
+
+
 def set_dual_quant_path(path: str) -> None:
     """Tuning/test hook for ``dual_quantize_per_tensor``: ``"three_pass"``
     (the default) or ``"single_launch"`` (one cooperative launch holding

@@ -241,21 +241,32 @@ class _TCFP12BlockScaledFunction(torch.autograd.Function):
         if not grad_2d.is_contiguous():
             grad_2d = grad_2d.contiguous()
         grad_input = grad_weight = grad_bias = None
-        if need_dx:
-            grad_fp8, grad_scales = K.block_quantize_fp8(
-                grad_2d, block_size=bs, fp8_dtype=torch.float8_e5m2
+        # one pass over the gradient prepares what the reference derives from
+        # it separately (nn:700-761): the E5M2 block-quantised G for the
+        # dgrad (as bf16 values), the split gradient for the fp32-accuracy
+        # wgrad, and the bias gradient
+        fp8_wgrad = need_dw and not ctx.hp_grad_weight and grad_2d.shape[0] % 4 == 0
+        want_db = need_db and ctx.has_bias
+        g_deq = g_split = db = None
+        if need_dx or fp8_wgrad or want_db:
+            g_deq, g_split, db = K.block_backward_prep(
+                grad_2d, bs, dequant=need_dx, split=fp8_wgrad, bias=want_db
             )
-            grad_input = K.fused_block_scaled_dual_gemm_backward_dx(
-                grad_fp8, w_hi, w_lo, grad_scales, sh, sl, block_size=bs
+        if need_dx:
+            grad_input = K.block_dgrad_from_prep(
+                g_deq, w_hi, w_lo, sh, sl, block_size=bs
             ).reshape(ctx.input_shape)
         if need_dw:
             if ctx.hp_grad_weight:
                 grad_weight = grad_2d.t() @ saved_act.to(grad_2d.dtype)
+            elif fp8_wgrad:
+                grad_weight = K.block_wgrad_from_prep(g_split, saved_act, act_scales, bs)
+                grad_weight = grad_weight.to(grad_2d.dtype)
             else:
                 grad_weight = K.block_scaled_wgrad(grad_2d, saved_act, act_scales, bs)
                 grad_weight = grad_weight.to(grad_2d.dtype)
-        if need_db and ctx.has_bias:
-            grad_bias = grad_2d.sum(dim=0)
+        if want_db:
+            grad_bias = db.to(grad_2d.dtype)
         return (grad_input, grad_weight, grad_bias) + (None,) * 7
 
 

@@ -425,3 +425,37 @@ def test_c1_single_linear_forward_full_size(dev):
     print(f"C1 rel_fro vs dequant fp32 {err:.2e}, vs unquantised X W^T {err_lit:.2e}", flush=True)
     assert err < EXACT
     assert err_lit < 5e-2
+
+
+# ---------------------------- fused block-backward gradient preparation
+@pytest.mark.parametrize("bs", [32, 64, 128])
+@pytest.mark.parametrize("M,N,K_", [(300, 256, 512), (4096, 256, 256), (1024, 1024, 768),
+                                    (64, 384, 128), (8, 128, 256)])
+def test_block_backward_prep_matches_separate_passes(dev, bs, M, N, K_):
+    g = torch.Generator().manual_seed(M + N + bs)
+    grad = (torch.randn(M, N, generator=g) * 1e-3).to(dev)
+    grad[:, :bs] *= 1e4  # one block column with a much larger exponent
+    x = torch.randn(M, K_, generator=g).to(dev)
+    aq, ea = K.block_quantize_fp8(x, bs)
+    w = torch.randn(N, K_, generator=g).to(dev) * 0.02
+    h, l, eh, el = K.fused_dual_quantize_fp8(w, bs)
+    g_deq, g_split, db = K.block_backward_prep(grad, bs, dequant=True, split=True, bias=True)
+    # G: exactly the dequantised E5M2 block quantisation
+    gq, ge = K.block_quantize_fp8(grad, bs, torch.float8_e5m2)
+    ref_deq = K.block_dequantize_fp8(gq, ge, bs).bfloat16()
+    assert torch.equal(g_deq, ref_deq)
+    # split: [bf16(g) | bf16(g - bf16(g))] transposed
+    hi = grad.bfloat16()
+    lo = (grad - hi.float()).bfloat16()
+    assert torch.equal(g_split, torch.cat([hi.t(), lo.t()], dim=1))
+    # bias: grad.sum(0) to fp32 summation-order tolerance
+    ref_db = grad.double().sum(0)
+    assert torch.allclose(db.double(), ref_db, rtol=1e-5, atol=1e-6 * ref_db.abs().max().item())
+    # the GEMMs that consume them give the separate path's results bit for bit
+    dx_a = K.fused_block_scaled_dual_gemm_backward_dx(gq, h, l, ge, eh, el, bs)
+    dx_b = K.block_dgrad_from_prep(g_deq, h, l, eh, el, bs)
+    assert torch.equal(dx_a, dx_b)
+    if M % 4 == 0:
+        dw_a = K.block_scaled_wgrad(grad, aq, ea, bs)
+        dw_b = K.block_wgrad_from_prep(g_split, aq, ea, bs)
+        assert torch.equal(dw_a, dw_b)
