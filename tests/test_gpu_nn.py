@@ -67,10 +67,26 @@ def test_ragged_token_count_uses_dequant_wgrad(dev):
 
 
 def test_abd_backward_uses_hi_only(dev):
-    lin = _layer(dev, 128, 64, abd=True)
-    x = torch.randn(32, 128, device=dev, requires_grad=True)
-    lin(x).sum().backward()
-    assert torch.isfinite(x.grad).all()
+    # forward identical to the non-ABD layer (the reference's own check,
+    # tests/test_tensor_cores.py:390-406); dX is the W_hi-only product
+    std = _layer(dev, 128, 64, error_feedback=False)
+    abd = _layer(dev, 128, 64, error_feedback=False, abd=True)
+    abd.load_state_dict(std.state_dict())
+    x = torch.randn(32, 128, device=dev)
+    xs, xa = x.clone().requires_grad_(True), x.clone().requires_grad_(True)
+    ys, ya = std(xs), abd(xa)
+    assert torch.equal(ys, ya)
+    go = torch.randn_like(ya)
+    ys.backward(go)
+    ya.backward(go)
+    hi, lo, ih, il, _, _ = oq.dual_quant_per_tensor(abd.weight.detach().cpu().numpy())
+    gq, ginv, _ = oq.to_fp8_per_tensor(go.cpu().numpy(), "f32", ofp8.E5M2)
+    ref_abd = og.gemm_nt(gq, ofp8.E5M2, np.ascontiguousarray(hi.T), ofp8.E4M3, ginv, ih)
+    ref_std = og.dual_gemm_nt(gq, ofp8.E5M2, np.ascontiguousarray(hi.T), np.ascontiguousarray(lo.T),
+                              ginv, ih, il)
+    assert og.rel_fro(xa.grad.cpu().numpy(), ref_abd) < 1e-4
+    assert og.rel_fro(xs.grad.cpu().numpy(), ref_std) < 1e-4
+    assert not torch.equal(xa.grad, xs.grad)
 
 
 def test_no_input_grad_skips_dgrad(dev):
@@ -180,6 +196,28 @@ def test_block_scaled_srr_and_abd(dev):
     y = lin(x)
     y.square().mean().backward()
     assert torch.isfinite(x.grad).all() and torch.isfinite(lin.weight.grad).all()
+
+
+def test_block_abd_forward_unchanged_and_dx_hi_only(dev):
+    bs = 64
+    std = _layer(dev, 256, 128, scale_block_size=bs, error_feedback=False)
+    abd = _layer(dev, 256, 128, scale_block_size=bs, error_feedback=False, abd=True)
+    abd.load_state_dict(std.state_dict())
+    x = torch.randn(64, 256, device=dev)
+    xs, xa = x.clone().requires_grad_(True), x.clone().requires_grad_(True)
+    ys, ya = std(xs), abd(xa)
+    assert torch.equal(ys, ya)
+    go = torch.randn_like(ya) * 1e-2
+    ys.backward(go)
+    ya.backward(go)
+    hi, lo, eh, el, _ = oq.block_dual_quantize(abd.weight.detach().cpu().numpy(), bs)
+    gq, ge = oq.block_quantize(go.cpu().numpy(), bs, ofp8.E5M2)
+    G = og.block_deq64(gq, ge, bs, ofp8.E5M2)
+    ref_abd = G @ og.block_deq64(hi, eh, bs)
+    ref_std = og.block_dgrad(gq, ge, hi, lo, eh, el, bs)
+    assert og.rel_fro(xa.grad.cpu().numpy(), ref_abd) < 1e-5
+    assert og.rel_fro(xs.grad.cpu().numpy(), ref_std) < 1e-5
+    assert not torch.equal(xa.grad, xs.grad)
 
 
 def test_c4_training_loss_matches_reference_algorithm(dev):
