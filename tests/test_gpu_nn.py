@@ -290,3 +290,59 @@ def test_delayed_scaling_layer(dev):
         losses.append(loss.item())
     assert all(np.isfinite(losses)) and losses[-1] < losses[0]
     assert st._step_count[a._param_name + ".steps"] == 31
+
+
+def test_c5_scaleup_layer_full_size(dev):
+    """configs[4]'s scale-up layer at full size: Linear(4096, 16384) with
+    block-64 scales and SRR at 8192 tokens.  The layer draws its SR key from
+    torch's CPU generator, so re-seeding reproduces the forward's W_hi/W_lo.
+    Block quantisation is per row: sampled rows are checked against the
+    oracle (W_hi and the exponents exactly, W_lo codes within the two SR
+    candidates).  Forward, dX and dW are checked against fp32 matmuls of the
+    same dequantised operands on the GPU."""
+    from tcfp_amd import kernels as K
+
+    bs = 64
+    torch.manual_seed(3)
+    lin = TCFPLinear(4096, 16384, use_tensor_cores=True, scale_block_size=bs, srr=True).to(dev)
+    x = torch.randn(8192, 4096, device=dev, dtype=torch.bfloat16, requires_grad=True)
+    torch.manual_seed(123)
+    out = lin(x)
+    torch.manual_seed(123)
+    seed = int(torch.randint(0, 2**62, (1,)).item())
+    W = lin.weight.detach()
+    h, l, sh, sl = K.fused_dual_quantize_fp8(W, bs, stochastic_lo=True, seed=seed)
+    rows = torch.randint(0, 16384, (6,), generator=torch.Generator().manual_seed(1))
+    for r in rows.tolist():
+        w_r = W[r:r + 1].cpu().numpy()
+        hi, lo_rtn, eh, el, _ = oq.block_dual_quantize(w_r, bs)
+        assert np.array_equal(h[r:r + 1].view(torch.uint8).cpu().numpy(), hi), r
+        assert np.array_equal(sh[:, r:r + 1].cpu().numpy(), eh), r
+        assert np.array_equal(sl[:, r:r + 1].cpu().numpy(), el), r
+        res = (w_r - oq.block_dequantize(hi, eh, bs)).astype(np.float32)
+        xs = np.clip(res * np.repeat(2.0 ** -el.T.astype(np.float64), bs, axis=1), -448,
+                     448).astype(np.float32)
+        rtn, other, _, _ = oq.sr_candidates_block(xs)
+        c = l[r:r + 1].view(torch.uint8).cpu().numpy()
+        assert np.all((c == rtn) | (c == other)), r
+    aq, ea = K.block_quantize_fp8(x.detach(), bs)
+    A = K.block_dequantize_fp8(aq, ea, bs)
+    Wd = K.block_dequantize_fp8(h, sh, bs) + K.block_dequantize_fp8(l, sl, bs)
+    ref = A @ Wd.t()
+    if lin.bias is not None:
+        ref = ref + lin.bias.detach().float()
+    err = (torch.linalg.norm(out.detach() - ref) / torch.linalg.norm(ref)).item()
+    del ref
+    go = torch.randn_like(out) * 1e-3
+    out.backward(go)
+    dw_ref = go.t() @ A
+    dw_err = (torch.linalg.norm(lin.weight.grad - dw_ref) / torch.linalg.norm(dw_ref)).item()
+    del dw_ref
+    gq, ge = K.block_quantize_fp8(go, bs, torch.float8_e5m2)
+    dx_ref = K.block_dequantize_fp8(gq, ge, bs) @ Wd
+    dx_err = (torch.linalg.norm(x.grad.float() - dx_ref) / torch.linalg.norm(dx_ref)).item()
+    print(f"C5 scale-up rel_fro: out {err:.2e}, dW {dw_err:.2e}, dX (bf16) {dx_err:.2e}",
+          flush=True)
+    assert err < 1e-4, err
+    assert dw_err < 2e-5, dw_err
+    assert dx_err < 5e-3, dx_err  # x is bf16: dX is rounded to bf16 (2^-9)
