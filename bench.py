@@ -208,6 +208,11 @@ def bench_dual_quant(iters=20):
     ms = event_time_ms(lambda: K.dual_quantize_per_tensor_delayed(w, ef, st, "w"), iters, stream)
     out["per_tensor_ef_delayed_4096x4096_ms"] = ms
     out["per_tensor_ef_delayed_4096x4096_GBs"] = 14 * n * k / (ms * 1e-3) / 1e9
+    # NF-aware W_hi scaling (sigma = 3): the first pass also sums v and v^2
+    ms = event_time_ms(lambda: K.dual_quantize_per_tensor(w, ef, sigma_factor=3.0), iters,
+                       stream)
+    out["per_tensor_ef_nf_4096x4096_ms"] = ms
+    out["per_tensor_ef_nf_4096x4096_GBs"] = 14 * n * k / (ms * 1e-3) / 1e9
     # block-64 with EF: 14 + 2/64 B/elem
     ms = event_time_ms(lambda: K.fused_dual_quantize_fp8(w, 64, error_buf=ef), iters, stream)
     out["block64_ef_4096x4096_ms"] = ms

@@ -138,6 +138,33 @@ int tcfp_dual_quantize_per_tensor_delayed(const void* w, int w_dtype, int64_t n,
                                           float* inv_hi, float* inv_lo, uint8_t* w_hi_t,
                                           uint8_t* w_lo_t, void* workspace, void* stream);
 
+/* Per-tensor dual quantisation with NF-aware (sigma-based) W_hi scaling:
+ * _TCFP12TensorCoreFunction.forward with nf_aware_scaling=True
+ * (tcfp/nn/__init__.py:350-360 -> to_fp8_e4m3_nf_aware, tcfp/core.py:
+ * 161-193; with delayed scaling, _delayed_quantise_w_hi's NF branch,
+ * :263-275).
+ *   W_hi target T = fp32(sigma_factor) * S, S = std(W + ef) (unbiased,
+ *   computed in fp64 and rounded once to fp32, clamped to 1e-12); T = the
+ *   clamped amax when S < 1e-6.  Fewer than two elements give S = NaN, as
+ *   torch.std does.  W_hi scale = 448 / T (values beyond +-448 saturate).
+ *   stochastic_hi != 0 rounds the W_hi codes stochastically (Philox4x32-10
+ *   keyed by seed / offset, counters apart from W_lo's); stochastic_lo as in
+ *   tcfp_dual_quantize_per_tensor.
+ *   amax_out != NULL selects delayed scaling with the arguments of
+ *   tcfp_dual_quantize_per_tensor_delayed: T replaces the amax in the EMA
+ *   and the residual prediction uses the delayed T.
+ *   Empty weights return TCFP_ERR_SHAPE (the reference's residual amax of
+ *   an empty tensor raises). */
+int tcfp_dual_quantize_per_tensor_nf(const void* w, int w_dtype, int64_t n, int64_t k, float* ef,
+                                     int update_ef, float sigma_factor, int stochastic_hi,
+                                     int stochastic_lo, uint64_t seed, uint64_t offset,
+                                     const float* amax_prev, const float* ratio_prev,
+                                     float ema_decay, float one_minus_decay, int validate,
+                                     float* amax_out, float* ratio_out, uint8_t* w_hi,
+                                     uint8_t* w_lo, float* inv_hi, float* inv_lo,
+                                     uint8_t* w_hi_t, uint8_t* w_lo_t, void* workspace,
+                                     void* stream);
+
 /* ---- per-block quantisation -------------------------------------------- */
 
 /* Per-(row, K-block) FP8 quantisation.  Replaces block_quantize_fp8

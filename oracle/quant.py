@@ -77,16 +77,59 @@ def to_fp8_per_tensor(t: np.ndarray, dtype: str = "f32", fmt: str = E4M3,
     return codes, inv, F32(scale)
 
 
-def dual_quant_per_tensor(W: np.ndarray, ef: np.ndarray | None = None):
+def nf_std_f32(t: np.ndarray) -> np.float32:
+    """``t.std()`` of an fp32 tensor (unbiased, torch's default correction)
+    as the real standard deviation rounded to fp32: float64 mean, float64
+    sum of squared deviations, one rounding at the end.  Fewer than two
+    elements give NaN, as torch.std does.
+    """
+    v = np.asarray(t, dtype=F32).ravel().astype(np.float64)
+    if v.size < 2:
+        return F32(np.nan)
+    d = v - v.mean()
+    return F32(np.sqrt(np.dot(d, d) / (v.size - 1)))
+
+
+def _clamp_min(v, lo: float) -> np.float32:
+    """``clamp(min=lo)`` of an fp32 scalar; NaN passes through."""
+    v = F32(v)
+    return v if np.isnan(v) else np.maximum(v, F32(lo))
+
+
+def nf_target(t: np.ndarray, sigma_factor: float = 3.0) -> np.float32:
+    """The effective max of ``to_fp8_e4m3_nf_aware`` (core.py:181-184):
+    ``sigma_factor * std`` (fp32 product with the fp32-rounded factor), or
+    the clamped amax when the clamped std is below 1e-6 (compared in fp32).
+    """
+    t = np.asarray(t, dtype=F32)
+    std = _clamp_min(nf_std_f32(t), 1e-12)
+    if std < F32(1e-6):
+        return _clamp_min(np.max(np.abs(t)), 1e-12)
+    return F32(F32(sigma_factor) * std)
+
+
+def to_fp8_nf_aware(t: np.ndarray, sigma_factor: float = 3.0):
+    """``to_fp8_e4m3_nf_aware`` without SR (core.py:161-193): the scale is
+    ``(448 / target).to(float32)``, values beyond +-448 saturate.  Returns
+    ``(codes, inv_scale, scale)``."""
+    return to_fp8_per_tensor(t, "f32", scale=_scale_of(nf_target(t, sigma_factor)))
+
+
+def dual_quant_per_tensor(W: np.ndarray, ef: np.ndarray | None = None,
+                          sigma_factor: float | None = None):
     """Per-tensor dual-quant + error feedback (nn/__init__.py:343-383).
 
     ``W`` holds the weight's values as float32.  Returns
     ``(hi, lo, inv_hi, inv_lo, ef_new, residual)``; ``ef_new`` is relative
     to the original W, not to ``W + ef`` (nn/__init__.py:378-383).
+    ``sigma_factor`` selects NF-aware W_hi scaling (nn/__init__.py:356-359).
     """
     W = np.asarray(W, dtype=F32)
     w = W + ef if ef is not None else W
-    hi, inv_hi, _ = to_fp8_per_tensor(w, "f32")
+    if sigma_factor is None:
+        hi, inv_hi, _ = to_fp8_per_tensor(w, "f32")
+    else:
+        hi, inv_hi, _ = to_fp8_nf_aware(w, sigma_factor)
     deq_hi = decode(hi, E4M3) * inv_hi
     residual = w - deq_hi
     lo, inv_lo, _ = to_fp8_per_tensor(residual, "f32")
@@ -114,11 +157,14 @@ def new_delayed_state() -> dict:
 
 
 def dual_quant_per_tensor_delayed(W: np.ndarray, ef: np.ndarray | None, state: dict,
-                                  name: str, decay: float = 0.999, interval: int = 100):
+                                  name: str, decay: float = 0.999, interval: int = 100,
+                                  sigma_factor: float | None = None):
     """Per-tensor dual quantisation with delayed (predictive dual-track)
     scaling: ``_delayed_quantise_w_hi`` / ``_delayed_quantise_w_lo``
-    (nn/__init__.py:250-309, non-NF path) inside the forward's steps 1-4
-    (:343-383), with ErrorFeedbackState's EMA bookkeeping (core.py:341-403).
+    (nn/__init__.py:250-309) inside the forward's steps 1-4 (:343-383), with
+    ErrorFeedbackState's EMA bookkeeping (core.py:341-403).  With
+    ``sigma_factor`` the NF branch (:263-275): the sigma target replaces the
+    amax in the EMA.
 
     ``state`` is updated in place.  Returns ``(hi, lo, inv_hi, inv_lo,
     ef_new, validated)``.
@@ -126,7 +172,10 @@ def dual_quant_per_tensor_delayed(W: np.ndarray, ef: np.ndarray | None, state: d
     W = np.asarray(W, dtype=F32)
     w = W + ef if ef is not None else W
     # W_hi: scale from the EMA of the clamped amax (first call: the amax)
-    cur = np.maximum(F32(np.max(np.abs(w))), F32(1e-12))
+    if sigma_factor is None:
+        cur = np.maximum(F32(np.max(np.abs(w))), F32(1e-12))
+    else:
+        cur = nf_target(w, sigma_factor)
     key = name + ".w_hi"
     if key not in state["amax"]:
         delayed = F32(cur)

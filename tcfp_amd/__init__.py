@@ -8,7 +8,13 @@ and autograd Functions.  All device work runs in hand-written HIP kernels
 (``libtcfp_hip.so``, C ABI in ``include/tcfp_hip.h``).
 """
 from . import core, cuda_ext, kernels, nn  # noqa: F401
-from .core import ErrorFeedbackState, TCFPMode, to_fp8_e4m3, to_fp8_e5m2  # noqa: F401
+from .core import (  # noqa: F401
+    ErrorFeedbackState,
+    TCFPMode,
+    to_fp8_e4m3,
+    to_fp8_e4m3_nf_aware,
+    to_fp8_e5m2,
+)
 from .nn import TCFPLinear, convert_to_tcfp  # noqa: F401
 
 __version__ = "0.1.0"

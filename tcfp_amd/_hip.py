@@ -43,6 +43,12 @@ _SIGNATURES = {
                                               ctypes.c_float, _i32, _c_void_p, _c_void_p,
                                               _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                                               _c_void_p, _c_void_p, _c_void_p, _c_void_p],
+    "tcfp_dual_quantize_per_tensor_nf": [_c_void_p, _i32, _i64, _i64, _c_void_p, _i32,
+                                         ctypes.c_float, _i32, _i32, _u64, _u64, _c_void_p,
+                                         _c_void_p, ctypes.c_float, ctypes.c_float, _i32,
+                                         _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+                                         _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+                                         _c_void_p],
     "tcfp_block_quantize": [_c_void_p, _i32, _i64, _i64, _i32, _i32, _c_void_p, _c_void_p,
                             _c_void_p],
     "tcfp_block_dual_quantize": [_c_void_p, _i32, _i64, _i64, _i32, _c_void_p, _i32, _i32, _u64,

@@ -13,6 +13,7 @@ from enum import Enum, auto
 
 import torch
 
+from . import _hip
 from . import kernels as _k
 
 FP8_E4M3_MAX: float = 448.0
@@ -71,6 +72,36 @@ def to_fp8_e5m2(
     """Per-tensor FP8 E5M2 cast (``tcfp/core.py:137-158``), FP8_MAX = 57344."""
     q, inv = _k.quantize_per_tensor(tensor, torch.float8_e5m2, scale)
     return q, inv
+
+
+def to_fp8_e4m3_nf_aware(
+    tensor: torch.Tensor,
+    sigma_factor: float = 3.0,
+    stochastic: bool = False,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Per-tensor FP8 E4M3 cast with NF-aware (sigma-based) scaling
+    (``tcfp/core.py:161-193``); returns ``(fp8, inv_scale)``, inv_scale (1,).
+
+    ``target = sigma_factor * std(t)`` (unbiased std, clamped to 1e-12), or
+    the clamped amax when that std is below 1e-6; ``scale = 448 / target``;
+    values beyond +-448 saturate; ``stochastic`` rounds each code up or down
+    with probability proportional to its distance.  The std is the real one
+    rounded once to fp32.  Runs the NF-aware dual quantisation kernels and
+    keeps their W_hi half.  An empty tensor gives a NaN scale, as the
+    reference's ``std`` of nothing does.
+    """
+    dev = _hip.require_gpu(tensor)
+    t = tensor if tensor.dtype in (torch.float32, torch.bfloat16) else tensor.float()
+    if t.numel() == 0:
+        return (
+            torch.empty(tensor.shape, dtype=torch.float8_e4m3fn, device=dev),
+            torch.full((1,), float("nan"), dtype=torch.float32, device=dev),
+        )
+    flat = t.contiguous().reshape(1, -1)
+    hi, _, inv_hi, _ = _k.dual_quantize_per_tensor(
+        flat, None, update_ef=False, sigma_factor=sigma_factor, stochastic_hi=stochastic
+    )
+    return hi.reshape(tensor.shape), inv_hi
 
 
 def ensure_column_major(t: torch.Tensor) -> torch.Tensor:

@@ -32,6 +32,14 @@ struct PartWs {
   // error flag set if a barrier wait ever gave up
   uint32_t ctr[4];
   uint32_t pad[60];
+  // NF-aware scaling: per-workgroup shifted sums of the first pass,
+  // sum(v - v0) and sum((v - v0)^2) in fp64 (v0 = the tensor's first element)
+  double s1[kMaxParts];
+  double s2[kMaxParts];
+  // W_hi target (before any EMA) published by workgroup 0 of the W_hi pass
+  // for the residual pass, which then skips re-reducing the partials
+  float hi_tgt;
+  uint32_t pad2[63];
 };
 
 constexpr int kThreads = 256;
@@ -218,6 +226,67 @@ TCFP_DEV float delayed_amax(const Delayed& d, float cur) {
   return d.amax_prev ? ema_f32(*d.amax_prev, cur, d.a, d.b) : cur;
 }
 
+// The W_hi scale rule.  `s1 == nullptr`: the amax rule (tcfp/core.py:100-101).
+// Otherwise NF-aware scaling (to_fp8_e4m3_nf_aware, tcfp/core.py:161-193):
+// the target is sigma * std(v) with the unbiased std (torch.std's default
+// correction), or the amax when that std is below 1e-6; under delayed
+// scaling the target feeds the EMA in place of the amax (tcfp/nn/__init__.py:
+// 263-275).  `sr`: W_hi codes are rounded stochastically (stochastic=True).
+struct HiRule {
+  const double* s1;  // per-workgroup sum(v - v0) of the first pass
+  const double* s2;  // per-workgroup sum((v - v0)^2)
+  int64_t n;         // element count
+  float sigma;       // fp32(sigma_factor): `sigma_factor * std` on an fp32 tensor
+  int sr;
+};
+
+// Workgroup-wide fp64 sum (256 threads) in a fixed order, returned to every
+// thread; `red` holds kThreads / 64 doubles.
+TCFP_DEV double block_dsum_all(double v, double* red) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  double s = red[0];
+#pragma unroll
+  for (int i = 1; i < kThreads / 64; ++i) s += red[i];
+  return s;
+}
+
+// The unbiased standard deviation from the shifted sums: fp64 arithmetic,
+// then one rounding to fp32.  Fewer than two elements give NaN, as torch.std
+// does; a non-finite element gives NaN through the sums.
+TCFP_DEV float std_from_sums(double a1, double a2, int64_t n) {
+  if (n < 2) return __builtin_nanf("");
+  const double nd = double(n);
+  double var = (a2 - a1 * (a1 / nd)) / (nd - 1.0);
+  if (var < 0.0) var = 0.0;  // rounding of a near-constant tensor
+  return float(sqrt(var));
+}
+
+// This step's W_hi target (before any EMA): the clamped amax, or the
+// NF-aware sigma target.  Every workgroup re-reduces the partials in the same
+// order, so all of them agree bit for bit.  `rd` holds 2 * kThreads / 64
+// doubles.
+TCFP_DEV float hi_target(const HiRule& hr, const uint32_t* __restrict__ pa, int ga,
+                         uint32_t* red, double* rd) {
+  if (!hr.s1) return clamp_min_nan(reduce_parts(pa, ga, red), 1e-12f);
+  // all three partial arrays are loaded before any is reduced, so their
+  // latencies overlap
+  uint32_t m = 0;
+  double a1 = 0.0, a2 = 0.0;
+  for (int i = threadIdx.x; i < ga; i += kThreads) {
+    m = umax(m, pa[i]);
+    a1 += hr.s1[i];
+    a2 += hr.s2[i];
+  }
+  const float amax = clamp_min_nan(__uint_as_float(block_umax_all(m, red)), 1e-12f);
+  a1 = block_dsum_all(a1, rd);
+  a2 = block_dsum_all(a2, rd + kThreads / 64);
+  const float sd = clamp_min_nan(std_from_sums(a1, a2, hr.n), 1e-12f);
+  return sd < 1e-6f ? amax : __fmul_rn(hr.sigma, sd);
+}
+
 // Eight elements of x (+ ef) starting at element 8*i.
 template <typename InT, bool HAS_EF>
 TCFP_DEV void load_w8(const InT* __restrict__ x, const float* __restrict__ ef, int64_t i,
@@ -240,13 +309,35 @@ TCFP_DEV void load_w8(const InT* __restrict__ x, const float* __restrict__ ef, i
 
 // Partial max |x (+ ef)| of this workgroup's share -> part[blockIdx.x].
 // Four vectors are loaded before any is reduced, so each thread keeps 64 or
-// 128 bytes in flight.
-template <typename InT, bool HAS_EF>
+// 128 bytes in flight.  STATS (NF-aware scaling) also writes the partial
+// sums of (v - v0) and (v - v0)^2 in fp64 to s1p / s2p, v0 being the first
+// element: the shift keeps the variance free of cancellation when the mean
+// is large against the spread.
+template <typename InT, bool HAS_EF, bool STATS>
 __global__ __launch_bounds__(kThreads) void amax_part_kernel(const InT* __restrict__ x,
                                                              const float* __restrict__ ef,
-                                                             int64_t n, uint32_t* __restrict__ part) {
+                                                             int64_t n, uint32_t* __restrict__ part,
+                                                             double* __restrict__ s1p,
+                                                             double* __restrict__ s2p) {
   __shared__ uint32_t red[kThreads / 64];
+  __shared__ double rd[2 * (kThreads / 64)];
   uint32_t m = 0;
+  double a1 = 0.0, a2 = 0.0, v0 = 0.0;
+  if constexpr (STATS) {
+    if (n > 0) {
+      float f = load1(x);
+      if constexpr (HAS_EF) f = f + ef[0];
+      v0 = double(f);
+    }
+  }
+  auto acc = [&](float v) {
+    m = umax(m, absbits(v));
+    if constexpr (STATS) {
+      const double d = double(v) - v0;
+      a1 += d;
+      a2 = fma(d, d, a2);
+    }
+  };
   const int64_t nvec = n >> 3;
   const int64_t stride = int64_t(gridDim.x) * kThreads;
   int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x;
@@ -257,21 +348,31 @@ __global__ __launch_bounds__(kThreads) void amax_part_kernel(const InT* __restri
 #pragma unroll
     for (int u = 0; u < 4; ++u)
 #pragma unroll
-      for (int j = 0; j < 8; ++j) m = umax(m, absbits(v[u][j]));
+      for (int j = 0; j < 8; ++j) acc(v[u][j]);
   }
   for (; i < nvec; i += stride) {
     float W[8], v[8];
     load_w8<InT, HAS_EF>(x, ef, i, W, v);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) m = umax(m, absbits(v[j]));
+    for (int j = 0; j < 8; ++j) acc(v[j]);
   }
   for (int64_t t = nvec * 8 + int64_t(blockIdx.x) * kThreads + threadIdx.x; t < n; t += stride) {
     float v = load1(x + t);
     if constexpr (HAS_EF) v = v + ef[t];
-    m = umax(m, absbits(v));
+    acc(v);
   }
   m = block_umax_all(m, red);
-  if (threadIdx.x == 0) part[blockIdx.x] = m;
+  if constexpr (STATS) {
+    a1 = block_dsum_all(a1, rd);
+    a2 = block_dsum_all(a2, rd + kThreads / 64);
+  }
+  if (threadIdx.x == 0) {
+    part[blockIdx.x] = m;
+    if constexpr (STATS) {
+      s1p[blockIdx.x] = a1;
+      s2p[blockIdx.x] = a2;
+    }
+  }
 }
 
 // ---- amax + column sums (the bias gradient) in one pass ------------------
@@ -547,25 +648,79 @@ __global__ __launch_bounds__(kThreads) void quant_t_kernel(
 // ===========================================================================
 // Per-tensor dual quantisation (tcfp/nn/__init__.py:343-383)
 // ===========================================================================
-// Pass 1 is amax_part_kernel<InT, HAS_EF> (partials a).
+// Stochastic rounding of an already scaled and clamped value, following
+// stochastic_round_to_fp8_e4m3 (tcfp/core.py:418-464) with torch's cast
+// semantics (a candidate past 448 is the NaN code and is never selected).
+TCFP_DEV uint32_t sr_per_tensor(float x, float u) {
+  const uint32_t lo = f32_to_e4m3(x);
+  const float lo_f = e4m3_to_f32(lo);
+  if (x == lo_f) return lo;
+  const float d = x > lo_f ? 1.0f : (x < lo_f ? -1.0f : 0.0f);
+  uint32_t hi = f32_to_e4m3(lo_f + (d * 0.015625f) * 0.5f);
+  if (e4m3_to_f32(hi) == lo_f) {
+    const float abs_lo = fmaxf(fabsf(lo_f), 0.015625f);
+    hi = f32_to_e4m3(lo_f + (d * abs_lo) * 0.25f);
+  }
+  const float hi_f = e4m3_to_f32(hi);
+  float gap = fabsf(hi_f - lo_f);
+  gap = (gap != gap) ? gap : fmaxf(gap, 1.4e-45f);
+  float frac = fabsf(x - lo_f) / gap;
+  frac = (frac != frac) ? frac : fminf(fmaxf(frac, 0.0f), 1.0f);
+  return (u < frac) ? hi : lo;
+}
+
+// Stochastic W_hi codes (NF-aware scaling with stochastic=True) draw from
+// their own Philox counters, 2^61 + e0 / 4 for the 4-element group at flat
+// element e0 and 3 * 2^61 + t for a tail element t, apart from W_lo's
+// (e0 / 4 and 2^62 + t): the two roundings are independent, and every pass
+// that recomputes W_hi draws the same bits.
+TCFP_DEV uint32_t hi_sr4(const float c[4], int64_t e0, uint32_t k0, uint32_t k1, uint32_t o0,
+                         uint32_t o1) {
+  const uint64_t ctr = (uint64_t(1) << 61) + (uint64_t(e0) >> 2);
+  const u32x4 r = philox4x32_10({uint32_t(ctr), uint32_t(ctr >> 32), o0, o1}, k0, k1);
+  return sr_per_tensor(c[0], u32_to_unit(r.x)) | (sr_per_tensor(c[1], u32_to_unit(r.y)) << 8) |
+         (sr_per_tensor(c[2], u32_to_unit(r.z)) << 16) |
+         (sr_per_tensor(c[3], u32_to_unit(r.w)) << 24);
+}
+TCFP_DEV uint32_t hi_sr1(float c, int64_t t, uint32_t k0, uint32_t k1, uint32_t o0, uint32_t o1) {
+  const uint64_t ctr = (uint64_t(3) << 61) + uint64_t(t);
+  const u32x4 r = philox4x32_10({uint32_t(ctr), uint32_t(ctr >> 32), o0, o1}, k0, k1);
+  return sr_per_tensor(c, u32_to_unit(r.x));
+}
+
+// W_hi codes of the scaled, clamped values c[0..4) at flat element e0.
+TCFP_DEV uint32_t hi_codes4(const float c[4], int64_t e0, bool sr, uint32_t k0, uint32_t k1,
+                            uint32_t o0, uint32_t o1) {
+  return sr ? hi_sr4(c, e0, k0, k1, o0, o1) : encode4<TCFP_FP8_E4M3>(c[0], c[1], c[2], c[3]);
+}
+TCFP_DEV uint32_t hi_code1(float c, int64_t t, bool sr, uint32_t k0, uint32_t k1, uint32_t o0,
+                           uint32_t o1) {
+  return sr ? hi_sr1(c, t, k0, k1, o0, o1) : encode1<TCFP_FP8_E4M3>(c);
+}
+
+// Pass 1 is amax_part_kernel<InT, HAS_EF, STATS> (partials a, and the sums
+// of NF-aware scaling).
 
 // Pass 2: W_hi codes and the partial max |residual| (partials b).
 template <typename InT, bool HAS_EF>
 __global__ __launch_bounds__(kThreads) void dualq_hi_kernel(
     const InT* __restrict__ w, const float* __restrict__ ef, int64_t n,
     const uint32_t* __restrict__ pa, int ga, uint8_t* __restrict__ hi, uint32_t* __restrict__ pb,
-    float* inv_hi_out, Delayed dl) {
+    float* inv_hi_out, Delayed dl, HiRule hr, uint32_t k0, uint32_t k1, uint32_t o0,
+    uint32_t o1, float* tgt_out) {
   __shared__ uint32_t red[kThreads / 64];
   __shared__ uint32_t red2[kThreads / 64];
+  __shared__ double rd[2 * (kThreads / 64)];
   float s_hi, inv_hi;
-  if (dl.on) {
-    const float cur = clamp_min_nan(reduce_parts(pa, ga, red), 1e-12f);
-    scale_of(delayed_amax(dl, cur), kE4M3Max, &s_hi, &inv_hi);
-    if (blockIdx.x == 0 && threadIdx.x == 0) *inv_hi_out = inv_hi;
-  } else {
-    s_hi = consumer_scale(nullptr, pa, ga, false, kE4M3Max, nullptr, inv_hi_out, red);
-    inv_hi = __fdiv_rn(1.0f, s_hi);
+  {
+    const float tgt = hi_target(hr, pa, ga, red, rd);
+    scale_of(dl.on ? delayed_amax(dl, tgt) : tgt, kE4M3Max, &s_hi, &inv_hi);
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+      *inv_hi_out = inv_hi;
+      *tgt_out = tgt;
+    }
   }
+  const bool sr = hr.sr != 0;
   uint32_t m = 0;
   const int64_t nvec = n >> 3;
   const int64_t stride = int64_t(gridDim.x) * kThreads;
@@ -573,7 +728,9 @@ __global__ __launch_bounds__(kThreads) void dualq_hi_kernel(
     float c[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) c[j] = clampf(v[j] * s_hi, kE4M3Max);
-    const uint2 code = encode8<TCFP_FP8_E4M3>(c);
+    const uint2 code = sr ? make_uint2(hi_sr4(c, i * 8, k0, k1, o0, o1),
+                                       hi_sr4(c + 4, i * 8 + 4, k0, k1, o0, o1))
+                          : encode8<TCFP_FP8_E4M3>(c);
     *reinterpret_cast<uint2*>(hi + i * 8) = code;
 #pragma unroll
     for (int j = 0; j < 8; ++j) m = umax(m, absbits(v[j] - e4m3_to_f32(byte_of(code, j)) * inv_hi));
@@ -594,33 +751,12 @@ __global__ __launch_bounds__(kThreads) void dualq_hi_kernel(
   for (int64_t t = nvec * 8 + int64_t(blockIdx.x) * kThreads + threadIdx.x; t < n; t += stride) {
     float v = load1(w + t);
     if constexpr (HAS_EF) v = v + ef[t];
-    const uint32_t code = encode1<TCFP_FP8_E4M3>(clampf(v * s_hi, kE4M3Max));
+    const uint32_t code = hi_code1(clampf(v * s_hi, kE4M3Max), t, sr, k0, k1, o0, o1);
     hi[t] = uint8_t(code);
     m = umax(m, absbits(v - e4m3_to_f32(code) * inv_hi));
   }
   m = block_umax_all(m, red2);
   if (threadIdx.x == 0) pb[blockIdx.x] = m;
-}
-
-// Stochastic rounding of an already scaled and clamped value, following
-// stochastic_round_to_fp8_e4m3 (tcfp/core.py:418-464) with torch's cast
-// semantics (a candidate past 448 is the NaN code and is never selected).
-TCFP_DEV uint32_t sr_per_tensor(float x, float u) {
-  const uint32_t lo = f32_to_e4m3(x);
-  const float lo_f = e4m3_to_f32(lo);
-  if (x == lo_f) return lo;
-  const float d = x > lo_f ? 1.0f : (x < lo_f ? -1.0f : 0.0f);
-  uint32_t hi = f32_to_e4m3(lo_f + (d * 0.015625f) * 0.5f);
-  if (e4m3_to_f32(hi) == lo_f) {
-    const float abs_lo = fmaxf(fabsf(lo_f), 0.015625f);
-    hi = f32_to_e4m3(lo_f + (d * abs_lo) * 0.25f);
-  }
-  const float hi_f = e4m3_to_f32(hi);
-  float gap = fabsf(hi_f - lo_f);
-  gap = (gap != gap) ? gap : fmaxf(gap, 1.4e-45f);
-  float frac = fabsf(x - lo_f) / gap;
-  frac = (frac != frac) ? frac : fminf(fmaxf(frac, 0.0f), 1.0f);
-  return (u < frac) ? hi : lo;
 }
 
 // W_lo codes of 4 consecutive elements starting at flat element `e0`
@@ -648,12 +784,12 @@ struct DualScales {
 // pass 2), W_lo codes, and the new error W - (deq(hi) + deq(lo)).
 template <bool SR>
 TCFP_DEV void dual_codes4(const float W[4], const float v[4], const DualScales& sc, int64_t e0,
-                          uint32_t k0, uint32_t k1, uint32_t o0, uint32_t o1, uint32_t* hcode,
-                          uint32_t* lcode, float err[4]) {
+                          bool srh, uint32_t k0, uint32_t k1, uint32_t o0, uint32_t o1,
+                          uint32_t* hcode, uint32_t* lcode, float err[4]) {
   float c[4], dh[4], x[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) c[j] = clampf(v[j] * sc.s_hi, kE4M3Max);
-  const uint32_t h = encode4<TCFP_FP8_E4M3>(c[0], c[1], c[2], c[3]);
+  const uint32_t h = hi_codes4(c, e0, srh, k0, k1, o0, o1);
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     dh[j] = e4m3_to_f32((h >> (8 * j)) & 0xFFu) * sc.inv_hi;
@@ -669,11 +805,12 @@ TCFP_DEV void dual_codes4(const float W[4], const float v[4], const DualScales& 
   *lcode = l;
 }
 
-TCFP_DEV DualScales dual_scales(const uint32_t* pa, int ga, const uint32_t* pb, int gb,
-                                float* inv_lo_out, uint32_t* red, uint32_t* red2) {
+// `tgt_in`: the W_hi target the W_hi pass published (null: reduce it here).
+TCFP_DEV DualScales dual_scales(const HiRule& hr, const float* tgt_in, const uint32_t* pa, int ga,
+                                const uint32_t* pb, int gb, float* inv_lo_out, uint32_t* red,
+                                uint32_t* red2, double* rd) {
   DualScales sc;
-  sc.s_hi = consumer_scale(nullptr, pa, ga, false, kE4M3Max, nullptr, nullptr, red);
-  sc.inv_hi = __fdiv_rn(1.0f, sc.s_hi);
+  scale_of(tgt_in ? *tgt_in : hi_target(hr, pa, ga, red, rd), kE4M3Max, &sc.s_hi, &sc.inv_hi);
   sc.s_lo = consumer_scale(nullptr, pb, gb, false, kE4M3Max, nullptr, inv_lo_out, red2);
   sc.inv_lo = __fdiv_rn(1.0f, sc.s_lo);
   return sc;
@@ -684,12 +821,12 @@ TCFP_DEV DualScales dual_scales(const uint32_t* pa, int ga, const uint32_t* pb, 
 // amax_lo / amax_hi ratio EMA, tcfp/core.py:374-393) or, otherwise, from
 // the predicted one (delayed * ratio, or delayed / 8 before any ratio,
 // :358-372).  Workgroup 0 writes both inverse scales and the new state.
-TCFP_DEV DualScales dual_scales_delayed(const Delayed& d, const uint32_t* pa, int ga,
-                                        const uint32_t* pb, int gb, float* inv_hi_out,
-                                        float* inv_lo_out, uint32_t* red, uint32_t* red2) {
+TCFP_DEV DualScales dual_scales_delayed(const Delayed& d, const HiRule& hr, const float* tgt_in,
+                                        const uint32_t* pa, int ga, const uint32_t* pb, int gb,
+                                        float* inv_hi_out, float* inv_lo_out, uint32_t* red,
+                                        uint32_t* red2, double* rd) {
   DualScales sc;
-  const float cur = clamp_min_nan(reduce_parts(pa, ga, red), 1e-12f);
-  const float del = delayed_amax(d, cur);
+  const float del = delayed_amax(d, tgt_in ? *tgt_in : hi_target(hr, pa, ga, red, rd));
   scale_of(del, kE4M3Max, &sc.s_hi, &sc.inv_hi);
   float lo_amax, ratio = 0.0f;
   if (d.validate) {
@@ -716,19 +853,22 @@ __global__ __launch_bounds__(kThreads) void dualq_lo_kernel(
     const InT* __restrict__ w, float* __restrict__ ef, int64_t n, const uint32_t* __restrict__ pa,
     int ga, const uint32_t* __restrict__ pb, int gb, uint8_t* __restrict__ lo, float* inv_lo_out,
     uint32_t k0, uint32_t k1, uint32_t off0, uint32_t off1, Delayed dl, float* inv_hi_out,
-    uint8_t* __restrict__ hi) {
+    uint8_t* __restrict__ hi, HiRule hr, const float* tgt_in) {
   __shared__ uint32_t red[kThreads / 64];
   __shared__ uint32_t red2[kThreads / 64];
+  __shared__ double rd[2 * (kThreads / 64)];
   const DualScales sc =
-      dl.on ? dual_scales_delayed(dl, pa, ga, pb, gb, inv_hi_out, inv_lo_out, red, red2)
-            : dual_scales(pa, ga, pb, gb, inv_lo_out, red, red2);
+      dl.on ? dual_scales_delayed(dl, hr, tgt_in, pa, ga, pb, gb, inv_hi_out, inv_lo_out, red,
+                                  red2, rd)
+            : dual_scales(hr, tgt_in, pa, ga, pb, gb, inv_lo_out, red, red2, rd);
+  const bool srh = hr.sr != 0;
   const int64_t nvec = n >> 3;
   const int64_t stride = int64_t(gridDim.x) * kThreads;
   auto body = [&](const float W[8], const float v[8], int64_t i) {
     uint32_t hc[2], lc[2];
     float e[8];
-    dual_codes4<SR>(W, v, sc, i * 8, k0, k1, off0, off1, &hc[0], &lc[0], e);
-    dual_codes4<SR>(W + 4, v + 4, sc, i * 8 + 4, k0, k1, off0, off1, &hc[1], &lc[1], e + 4);
+    dual_codes4<SR>(W, v, sc, i * 8, srh, k0, k1, off0, off1, &hc[0], &lc[0], e);
+    dual_codes4<SR>(W + 4, v + 4, sc, i * 8 + 4, srh, k0, k1, off0, off1, &hc[1], &lc[1], e + 4);
     *reinterpret_cast<uint2*>(lo + i * 8) = make_uint2(lc[0], lc[1]);
     // W_hi codes when no earlier pass wrote them
     if (hi) *reinterpret_cast<uint2*>(hi + i * 8) = make_uint2(hc[0], hc[1]);
@@ -751,7 +891,7 @@ __global__ __launch_bounds__(kThreads) void dualq_lo_kernel(
     const float W = load1(w + t);
     float v = W;
     if constexpr (HAS_EF) v = W + ef[t];
-    const uint32_t hcode = encode1<TCFP_FP8_E4M3>(clampf(v * sc.s_hi, kE4M3Max));
+    const uint32_t hcode = hi_code1(clampf(v * sc.s_hi, kE4M3Max), t, srh, k0, k1, off0, off1);
     if (hi) hi[t] = uint8_t(hcode);
     const float dh = e4m3_to_f32(hcode) * sc.inv_hi;
     const float x = clampf((v - dh) * sc.s_lo, kE4M3Max);
@@ -776,16 +916,19 @@ __global__ __launch_bounds__(kThreads) void dualq_lo_t_kernel(
     const uint32_t* __restrict__ pa, int ga, const uint32_t* __restrict__ pb, int gb,
     uint8_t* __restrict__ lo, float* inv_lo_out, uint8_t* __restrict__ hi_t,
     uint8_t* __restrict__ lo_t, uint32_t k0, uint32_t k1, uint32_t off0, uint32_t off1,
-    Delayed dl, float* inv_hi_out, uint8_t* __restrict__ hi) {
+    Delayed dl, float* inv_hi_out, uint8_t* __restrict__ hi, HiRule hr, const float* tgt_in) {
   using TL = TileLoad<InT>;
   constexpr int VEC = TL::VEC;
   __shared__ uint32_t red[kThreads / 64];
   __shared__ uint32_t red2[kThreads / 64];
+  __shared__ double rd[2 * (kThreads / 64)];
   __shared__ uint32_t tile_h[kTile * kTilePitch];
   __shared__ uint32_t tile_l[kTile * kTilePitch];
   const DualScales sc =
-      dl.on ? dual_scales_delayed(dl, pa, ga, pb, gb, inv_hi_out, inv_lo_out, red, red2)
-            : dual_scales(pa, ga, pb, gb, inv_lo_out, red, red2);
+      dl.on ? dual_scales_delayed(dl, hr, tgt_in, pa, ga, pb, gb, inv_hi_out, inv_lo_out, red,
+                                  red2, rd)
+            : dual_scales(hr, tgt_in, pa, ga, pb, gb, inv_lo_out, red, red2, rd);
+  const bool srh = hr.sr != 0;
   const TileGeom tg(cols);
   const int tc = (threadIdx.x % TL::TPR) * VEC;
   const int64_t c = tg.c0 + tc;
@@ -824,8 +967,8 @@ __global__ __launch_bounds__(kThreads) void dualq_lo_t_kernel(
     float err[VEC];
 #pragma unroll
     for (int j = 0; j < VEC; j += 4)
-      dual_codes4<SR>(W + j, v + j, sc, off + j, k0, k1, off0, off1, &hc[j / 4], &lc[j / 4],
-                      err + j);
+      dual_codes4<SR>(W + j, v + j, sc, off + j, srh, k0, k1, off0, off1, &hc[j / 4],
+                      &lc[j / 4], err + j);
     if (valid) {
       if constexpr (VEC == 4) *reinterpret_cast<uint32_t*>(lo + off) = lc[0];
       else *reinterpret_cast<uint2*>(lo + off) = make_uint2(lc[0], lc[1]);
@@ -1648,11 +1791,11 @@ int quantize_impl(const void* x, int x_dtype, int64_t rows, int64_t cols, int fp
   if (!col_sum && !scale_in) {
     g = parts_for((n + 7) / 8);
     if (bf)
-      amax_part_kernel<uint16_t, false><<<g, kThreads, 0, st>>>(static_cast<const uint16_t*>(x),
-                                                                nullptr, n, part);
+      amax_part_kernel<uint16_t, false, false><<<g, kThreads, 0, st>>>(
+          static_cast<const uint16_t*>(x), nullptr, n, part, nullptr, nullptr);
     else
-      amax_part_kernel<float, false><<<g, kThreads, 0, st>>>(static_cast<const float*>(x),
-                                                             nullptr, n, part);
+      amax_part_kernel<float, false, false><<<g, kThreads, 0, st>>>(
+          static_cast<const float*>(x), nullptr, n, part, nullptr, nullptr);
   }
   const int bfr = bf ? 1 : 0;
   const bool tiled = q_t && n > 0 && cols % 8 == 0;
@@ -1733,7 +1876,7 @@ int dual_quantize_impl(const void* w, int w_dtype, int64_t n, int64_t k, float* 
                        int update_ef, int stochastic_lo, uint64_t seed, uint64_t offset,
                        uint8_t* w_hi, uint8_t* w_lo, float* inv_hi, float* inv_lo,
                        uint8_t* w_hi_t, uint8_t* w_lo_t, void* workspace, const Delayed& dl,
-                       void* stream) {
+                       bool nf, float sigma, bool sr_hi, void* stream) {
   if (n < 0 || k < 0) return TCFP_ERR_SHAPE;
   if (w_dtype != TCFP_DTYPE_F32 && w_dtype != TCFP_DTYPE_BF16) return TCFP_ERR_DTYPE;
   if (!workspace) return TCFP_ERR_WORKSPACE;
@@ -1755,9 +1898,18 @@ int dual_quantize_impl(const void* w, int w_dtype, int64_t n, int64_t k, float* 
   const uint32_t k0 = uint32_t(seed), k1 = uint32_t(seed >> 32);
   const uint32_t o0 = uint32_t(offset), o1 = uint32_t(offset >> 32);
 
+  HiRule hr{};
+  if (nf) {
+    hr.s1 = ws->s1;
+    hr.s2 = ws->s2;
+    hr.n = total;
+    hr.sigma = sigma;
+    hr.sr = sr_hi ? 1 : 0;
+  }
+
   // one cooperative launch when selected and it fits (SR together with EF,
-  // and delayed scaling, stay on the separate passes)
-  if (g_force_three_pass == 0 && !(stochastic_lo && has_ef) && !dl.on) {
+  // delayed scaling and NF-aware scaling stay on the separate passes)
+  if (g_force_three_pass == 0 && !(stochastic_lo && has_ef) && !dl.on && !nf) {
     bool done = false;
     if (bf) {
       const uint16_t* wp = static_cast<const uint16_t*>(w);
@@ -1787,24 +1939,32 @@ int dual_quantize_impl(const void* w, int w_dtype, int64_t n, int64_t k, float* 
   // (W_hi codes + residual amax) is skipped and pass 3 writes W_hi too.
   const bool two_pass = dl.on && !dl.validate;
   uint8_t* hi3 = two_pass ? w_hi : nullptr;
+  // the residual pass takes the W_hi target from the W_hi pass when it ran
+  const float* tgt3 = two_pass ? nullptr : &ws->hi_tgt;
 #define TCFP_LO(T, EF, UP, SR)                                                                  \
   do {                                                                                          \
     if (tiled)                                                                                  \
       dualq_lo_t_kernel<T, EF, UP, SR><<<unsigned(tiles), kThreads, 0, st>>>(                   \
           wp, ef, n, k, ws->a, ga, ws->b, gb, w_lo, inv_lo, w_hi_t, w_lo_t, k0, k1, o0, o1, dl,  \
-          inv_hi, hi3);                                                                         \
+          inv_hi, hi3, hr, tgt3);                                                               \
     else                                                                                        \
       dualq_lo_kernel<T, EF, UP, SR><<<gq, kThreads, 0, st>>>(wp, ef, total, ws->a, ga, ws->b, \
                                                               gb, w_lo, inv_lo, k0, k1, o0, o1, \
-                                                              dl, inv_hi, hi3);                 \
+                                                              dl, inv_hi, hi3, hr, tgt3);       \
   } while (0)
 #define TCFP_DQ(T, EF)                                                                          \
   do {                                                                                          \
     const T* wp = static_cast<const T*>(w);                                                     \
-    amax_part_kernel<T, EF><<<ga, kThreads, 0, st>>>(wp, ef, total, ws->a);                    \
+    if (nf)                                                                                     \
+      amax_part_kernel<T, EF, true><<<ga, kThreads, 0, st>>>(wp, ef, total, ws->a, ws->s1,     \
+                                                             ws->s2);                           \
+    else                                                                                        \
+      amax_part_kernel<T, EF, false><<<ga, kThreads, 0, st>>>(wp, ef, total, ws->a, nullptr,   \
+                                                              nullptr);                         \
     if (!two_pass)                                                                              \
       dualq_hi_kernel<T, EF><<<gb, kThreads, 0, st>>>(wp, ef, total, ws->a, ga, w_hi, ws->b,   \
-                                                      inv_hi, dl);                              \
+                                                      inv_hi, dl, hr, k0, k1, o0, o1,           \
+                                                      &ws->hi_tgt);                             \
     if (stochastic_lo) {                                                                        \
       if (upd) TCFP_LO(T, EF, EF, true); else TCFP_LO(T, EF, false, true);                      \
     } else {                                                                                    \
@@ -1839,7 +1999,8 @@ int tcfp_dual_quantize_per_tensor(const void* w, int w_dtype, int64_t n, int64_t
                                   void* stream) {
   const Delayed off{};
   return dual_quantize_impl(w, w_dtype, n, k, ef, update_ef, stochastic_lo, seed, offset, w_hi,
-                            w_lo, inv_hi, inv_lo, w_hi_t, w_lo_t, workspace, off, stream);
+                            w_lo, inv_hi, inv_lo, w_hi_t, w_lo_t, workspace, off, false, 0.0f,
+                            false, stream);
 }
 
 int tcfp_dual_quantize_per_tensor_delayed(const void* w, int w_dtype, int64_t n, int64_t k,
@@ -1861,7 +2022,36 @@ int tcfp_dual_quantize_per_tensor_delayed(const void* w, int w_dtype, int64_t n,
   dl.on = 1;
   dl.validate = validate ? 1 : 0;
   return dual_quantize_impl(w, w_dtype, n, k, ef, update_ef, 0, 0, 0, w_hi, w_lo, inv_hi, inv_lo,
-                            w_hi_t, w_lo_t, workspace, dl, stream);
+                            w_hi_t, w_lo_t, workspace, dl, false, 0.0f, false, stream);
+}
+
+int tcfp_dual_quantize_per_tensor_nf(const void* w, int w_dtype, int64_t n, int64_t k, float* ef,
+                                     int update_ef, float sigma_factor, int stochastic_hi,
+                                     int stochastic_lo, uint64_t seed, uint64_t offset,
+                                     const float* amax_prev, const float* ratio_prev,
+                                     float ema_decay, float one_minus_decay, int validate,
+                                     float* amax_out, float* ratio_out, uint8_t* w_hi,
+                                     uint8_t* w_lo, float* inv_hi, float* inv_lo,
+                                     uint8_t* w_hi_t, uint8_t* w_lo_t, void* workspace,
+                                     void* stream) {
+  if (!inv_hi || !inv_lo) return TCFP_ERR_SHAPE;
+  // the reference's residual amax of an empty tensor raises
+  if (n * k == 0) return TCFP_ERR_SHAPE;
+  Delayed dl{};
+  if (amax_out) {
+    if (validate && !ratio_out) return TCFP_ERR_SHAPE;
+    dl.amax_prev = amax_prev;
+    dl.ratio_prev = ratio_prev;
+    dl.amax_out = amax_out;
+    dl.ratio_out = ratio_out;
+    dl.a = ema_decay;
+    dl.b = one_minus_decay;
+    dl.on = 1;
+    dl.validate = validate ? 1 : 0;
+  }
+  return dual_quantize_impl(w, w_dtype, n, k, ef, update_ef, stochastic_lo, seed, offset, w_hi,
+                            w_lo, inv_hi, inv_lo, w_hi_t, w_lo_t, workspace, dl, true,
+                            sigma_factor, stochastic_hi != 0, stream);
 }
 
 }  // extern "C"

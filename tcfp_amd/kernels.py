@@ -155,6 +155,8 @@ def dual_quantize_per_tensor(
     stochastic_lo: bool = False,
     transposed: bool = False,
     seed: int | None = None,
+    sigma_factor: float | None = None,
+    stochastic_hi: bool = False,
 ):
     """W (+ error feedback) -> (W_hi, W_lo, inv_hi, inv_lo[, W_hi^T, W_lo^T]).
 
@@ -164,6 +166,12 @@ def dual_quantize_per_tensor(
     in place with ``W - (deq(hi) + deq(lo))``.  ``stochastic_lo`` rounds
     W_lo stochastically (SRR); the Philox key is drawn from torch's CPU
     generator unless ``seed`` is given.
+
+    ``sigma_factor`` selects NF-aware W_hi scaling (``nf_aware_scaling``,
+    reference ``:356-359`` -> ``to_fp8_e4m3_nf_aware``, ``tcfp/core.py:
+    161-193``): the W_hi scale is ``448 / (sigma_factor * std(W + ef))``, or
+    the amax rule when that std is below 1e-6.  ``stochastic_hi`` (only with
+    ``sigma_factor``) rounds the W_hi codes stochastically.
     """
     dev = _hip.require_gpu(weight, error_buf)
     assert weight.dim() == 2, "weight must be 2-D (N, K)"
@@ -181,8 +189,18 @@ def dual_quantize_per_tensor(
     inv_lo = torch.empty(1, dtype=torch.float32, device=dev)
     w_hi_t = torch.empty((k, n), dtype=torch.float8_e4m3fn, device=dev) if transposed else None
     w_lo_t = torch.empty((k, n), dtype=torch.float8_e4m3fn, device=dev) if transposed else None
-    if stochastic_lo and seed is None:
+    if stochastic_hi and sigma_factor is None:
+        raise ValueError("stochastic_hi applies to NF-aware scaling only (pass sigma_factor)")
+    if (stochastic_lo or stochastic_hi) and seed is None:
         seed = int(torch.randint(0, 2**62, (1,)).item())
+    if sigma_factor is not None:
+        _dual_quantize_nf(
+            w, n, k, error_buf, update_ef, sigma_factor, stochastic_hi, stochastic_lo, seed,
+            None, None, 0.0, False, None, None, w_hi, w_lo, inv_hi, inv_lo, w_hi_t, w_lo_t, dev,
+        )
+        if transposed:
+            return w_hi, w_lo, inv_hi, inv_lo, w_hi_t, w_lo_t
+        return w_hi, w_lo, inv_hi, inv_lo
     check(
         _hip.lib().tcfp_dual_quantize_per_tensor(
             ptr(w), _in_dtype(w), n, k, ptr(error_buf), int(bool(update_ef)),
@@ -197,6 +215,29 @@ def dual_quantize_per_tensor(
     return w_hi, w_lo, inv_hi, inv_lo
 
 
+def _dual_quantize_nf(w, n, k, error_buf, update_ef, sigma_factor, stochastic_hi, stochastic_lo,
+                      seed, prev, ratio_prev, decay, validate, amax_out, ratio_out, w_hi, w_lo,
+                      inv_hi, inv_lo, w_hi_t, w_lo_t, dev) -> None:
+    """``tcfp_dual_quantize_per_tensor_nf`` (``amax_out`` None: no delayed
+    scaling)."""
+    if n * k == 0:
+        raise RuntimeError(
+            "NF-aware dual quantisation of an empty weight (the reference's residual amax "
+            "of an empty tensor raises)"
+        )
+    check(
+        _hip.lib().tcfp_dual_quantize_per_tensor_nf(
+            ptr(w), _in_dtype(w), n, k, ptr(error_buf), int(bool(update_ef)),
+            float(sigma_factor), int(bool(stochastic_hi)), int(bool(stochastic_lo)),
+            int(seed or 0), 0, ptr(prev), ptr(ratio_prev), float(decay), 1.0 - float(decay),
+            int(bool(validate)), ptr(amax_out), ptr(ratio_out), ptr(w_hi), ptr(w_lo),
+            ptr(inv_hi), ptr(inv_lo), ptr(w_hi_t), ptr(w_lo_t), ptr(_hip.workspace(dev)),
+            _hip.stream_of(dev),
+        ),
+        "dual_quantize_per_tensor (NF-aware)",
+    )
+
+
 def dual_quantize_per_tensor_delayed(
     weight: torch.Tensor,
     error_buf: torch.Tensor | None,
@@ -204,6 +245,9 @@ def dual_quantize_per_tensor_delayed(
     name: str,
     update_ef: bool = True,
     transposed: bool = False,
+    sigma_factor: float | None = None,
+    stochastic_hi: bool = False,
+    seed: int | None = None,
 ):
     """Per-tensor dual quantisation with delayed scaling, updating ``state``.
 
@@ -215,7 +259,9 @@ def dual_quantize_per_tensor_delayed(
     ``_residual_ratio[name + ".ratio"]`` is updated) and from the predicted
     one otherwise.  The state tensors are replaced by new 0-dim fp32
     tensors, as the reference's EMA rebinds them.  Returns what
-    :func:`dual_quantize_per_tensor` returns.
+    :func:`dual_quantize_per_tensor` returns.  ``sigma_factor`` /
+    ``stochastic_hi``: the NF branch of ``_delayed_quantise_w_hi``
+    (``:263-275``), the sigma target in place of the amax.
     """
     dev = _hip.require_gpu(weight, error_buf)
     assert weight.dim() == 2, "weight must be 2-D (N, K)"
@@ -246,15 +292,26 @@ def dual_quantize_per_tensor_delayed(
     w_hi_t = torch.empty((k, n), dtype=torch.float8_e4m3fn, device=dev) if transposed else None
     w_lo_t = torch.empty((k, n), dtype=torch.float8_e4m3fn, device=dev) if transposed else None
     decay = float(state._ema_decay)
-    check(
-        _hip.lib().tcfp_dual_quantize_per_tensor_delayed(
-            ptr(w), _in_dtype(w), n, k, ptr(error_buf), int(bool(update_ef)), ptr(prev),
-            ptr(ratio_prev), decay, 1.0 - decay, int(validate), ptr(amax_out), ptr(ratio_out),
-            ptr(w_hi), ptr(w_lo), ptr(inv_hi), ptr(inv_lo), ptr(w_hi_t), ptr(w_lo_t),
-            ptr(_hip.workspace(dev)), _hip.stream_of(dev),
-        ),
-        "dual_quantize_per_tensor_delayed",
-    )
+    if stochastic_hi and sigma_factor is None:
+        raise ValueError("stochastic_hi applies to NF-aware scaling only (pass sigma_factor)")
+    if sigma_factor is not None:
+        if stochastic_hi and seed is None:
+            seed = int(torch.randint(0, 2**62, (1,)).item())
+        _dual_quantize_nf(
+            w, n, k, error_buf, update_ef, sigma_factor, stochastic_hi, False, seed, prev,
+            ratio_prev, decay, validate, amax_out, ratio_out, w_hi, w_lo, inv_hi, inv_lo,
+            w_hi_t, w_lo_t, dev,
+        )
+    else:
+        check(
+            _hip.lib().tcfp_dual_quantize_per_tensor_delayed(
+                ptr(w), _in_dtype(w), n, k, ptr(error_buf), int(bool(update_ef)), ptr(prev),
+                ptr(ratio_prev), decay, 1.0 - decay, int(validate), ptr(amax_out),
+                ptr(ratio_out), ptr(w_hi), ptr(w_lo), ptr(inv_hi), ptr(inv_lo), ptr(w_hi_t),
+                ptr(w_lo_t), ptr(_hip.workspace(dev)), _hip.stream_of(dev),
+            ),
+            "dual_quantize_per_tensor_delayed",
+        )
     state._delayed_amax[amax_key] = amax_out
     if validate:
         state._residual_ratio[ratio_key] = ratio_out

@@ -19,9 +19,10 @@ but their bodies call the HIP operator layer (``tcfp_amd.kernels``):
   skipped when autograd does not need it (the reference always computes it;
   the results of the gradients that are returned are unchanged).
 
-The reference's fake-quantise path (``use_tensor_cores=False``, int4/NF4
-residual via ``tcfp.tcfp12``), delayed scaling and NF-aware scaling are not
-part of this build and raise ``NotImplementedError``.
+Delayed scaling and NF-aware scaling run inside the same dual-quant
+kernels.  The reference's fake-quantise path (``use_tensor_cores=False``,
+int4/NF4 residual via ``tcfp.tcfp12``) is not part of this build and raises
+``NotImplementedError``.
 """
 from __future__ import annotations
 
@@ -81,23 +82,26 @@ class _TCFP12TensorCoreFunction(torch.autograd.Function):
         srr: bool = False,
         update_ef: bool = True,
     ) -> torch.Tensor:
-        if nf_aware_scaling:
-            raise NotImplementedError("nf_aware_scaling is not part of this build")
         need_dx = ctx.needs_input_grad[0]
         need_dw = ctx.needs_input_grad[1]
 
         # 1-4. dual quantisation of W (+ EF read and in-place update); with
         # delayed scaling (and an EF state to hold it) the scales follow the
-        # reference's predictive dual-track rule (nn:250-309, 350-374)
+        # reference's predictive dual-track rule (nn:250-309, 350-374);
+        # NF-aware scaling sets the W_hi scale from sigma_factor * std, with
+        # stochastic W_hi rounding when stochastic_rounding (nn:356-359)
         error_buf = _ef_buffer(error_state, param_name, weight)
+        sigma = float(sigma_factor) if nf_aware_scaling else None
+        sr_hi = bool(nf_aware_scaling and stochastic_rounding)
         if delayed_scaling and error_state is not None:
             res = K.dual_quantize_per_tensor_delayed(
                 weight, error_buf, error_state, param_name, update_ef=update_ef,
-                transposed=need_dx,
+                transposed=need_dx, sigma_factor=sigma, stochastic_hi=sr_hi,
             )
         else:
             res = K.dual_quantize_per_tensor(
-                weight, error_buf, update_ef=update_ef, stochastic_lo=srr, transposed=need_dx
+                weight, error_buf, update_ef=update_ef, stochastic_lo=srr, transposed=need_dx,
+                sigma_factor=sigma, stochastic_hi=sr_hi,
             )
         w_hi, w_lo, inv_hi, inv_lo, w_hi_t, w_lo_t = res if need_dx else (*res, None, None)
 
@@ -310,8 +314,6 @@ class TCFPLinear(nn.Module):
                 "TCFPLinear(use_tensor_cores=False) is the fake-quantise path, which is "
                 "not part of this build; pass use_tensor_cores=True"
             )
-        if nf_aware_scaling:
-            raise NotImplementedError("nf_aware_scaling is not part of this build")
         if nf4_residual:
             warnings.warn(
                 "nf4_residual is ignored in tensor core mode — NF4 cannot "
@@ -432,8 +434,18 @@ class TCFPLinear(nn.Module):
         ]
         if self.hp_grad_weight:
             parts.append("hp_grad_weight=True")
+        if self.nf4_residual:
+            parts.append("nf4_residual=True")
+        if self.nf_aware_scaling:
+            parts.append("nf_aware_scaling=True")
+        if self.stochastic_rounding:
+            parts.append("stochastic_rounding=True")
+        if self.delayed_scaling:
+            parts.append("delayed_scaling=True")
         if self.use_fused_kernel:
             parts.append("use_fused_kernel=True")
+        if self.use_cuda_ext:
+            parts.append("use_cuda_ext=True")
         if self.scale_block_size is not None:
             parts.append(f"scale_block_size={self.scale_block_size}")
         if self.abd:

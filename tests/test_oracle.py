@@ -243,6 +243,119 @@ def test_delayed_prediction_equals_measurement_when_exact():
         assert np.array_equal(np.asarray(a), np.asarray(b))
 
 
+# ------------------------------------------------- NF-aware scaling (core.py:161-193)
+def _stdev_exact_f32(x):
+    # statistics.stdev sums the squared deviations exactly (rationals), then
+    # rounds once to double and takes a double sqrt: an independent
+    # implementation of the sample (unbiased) standard deviation
+    import statistics
+
+    return np.float32(statistics.stdev([float(v) for v in np.ravel(x)]))
+
+
+@pytest.mark.parametrize("n", [2, 3, 17, 1000])
+@pytest.mark.parametrize("shift,scale", [(0.0, 1.0), (0.0, 0.02), (100.0, 1e-3), (1.0, 1e-5)])
+def test_nf_std_matches_exact_rational_stdev(n, shift, scale):
+    rng = np.random.default_rng(n + int(shift))
+    x = (rng.standard_normal(n) * scale + shift).astype(np.float32)
+    assert oq.nf_std_f32(x) == _stdev_exact_f32(x)
+
+
+@pytest.mark.parametrize("shape", [(64, 64), (257, 33), (1024, 512)])
+def test_nf_std_matches_torch_std_for_zero_mean_data(shape):
+    import torch
+
+    g = torch.Generator().manual_seed(shape[0])
+    t = torch.randn(shape, generator=g) * 0.02
+    assert oq.nf_std_f32(t.numpy()) == np.float32(t.std().item())
+
+
+def test_nf_std_closed_forms_and_degenerate_sizes():
+    import warnings
+
+    import torch
+
+    # unbiased: var([1, 2, 3, 4]) = 5/3 (the population variance is 5/4)
+    assert oq.nf_std_f32(np.array([1, 2, 3, 4], np.float32)) == np.float32(np.sqrt(5.0 / 3.0))
+    assert oq.nf_std_f32(np.full(10, 0.3, np.float32)) == 0.0
+    with warnings.catch_warnings():
+        warnings.simplefilter("ignore")
+        for v in ([0.5], []):
+            assert np.isnan(torch.tensor(v, dtype=torch.float32).std().item())
+            assert np.isnan(oq.nf_std_f32(np.array(v, np.float32)))
+
+
+@pytest.mark.parametrize("sigma", [3.0, 2.5, 1.1, 3.3])
+def test_nf_target_rule(sigma):
+    import torch
+
+    rng = np.random.default_rng(5)
+    # the product is torch's fp32 tensor * Python float (the factor rounded
+    # to fp32 first), which for some spreads differs from rounding the
+    # double product once
+    seen_double_differs = False
+    for i in range(40):
+        x = (rng.standard_normal((16, 24)) * (0.01 + 0.001 * i)).astype(np.float32)
+        std = oq.nf_std_f32(x)
+        want = np.float32((sigma * torch.tensor(std, dtype=torch.float32)).item())
+        assert oq.nf_target(x, sigma) == want
+        seen_double_differs |= bool(want != np.float32(sigma * np.float64(std)))
+    assert seen_double_differs == (sigma in (1.1, 3.3))
+    # std < 1e-6 (including a constant or zero tensor) falls back to the
+    # clamped amax; one element gives NaN
+    assert oq.nf_target(np.full((4, 4), -0.5, np.float32), sigma) == np.float32(0.5)
+    tiny = (np.float32(0.25) + rng.standard_normal(256).astype(np.float32) * np.float32(1e-7))
+    assert oq.nf_std_f32(tiny) < np.float32(1e-6)
+    assert oq.nf_target(tiny, sigma) == np.float32(np.max(np.abs(tiny)))
+    assert oq.nf_target(np.zeros((3, 3), np.float32), sigma) == np.float32(1e-12)
+    assert np.isnan(oq.nf_target(np.array([[0.3]], np.float32), sigma))
+
+
+def test_nf_aware_quantisation_properties():
+    # the reference's own checks (tests/test_tensor_cores.py:27-68 upstream):
+    # bounded round-trip error and MSE on Gaussian data, finite near-constant
+    rng = np.random.default_rng(42)
+    x = rng.standard_normal((1024, 1024)).astype(np.float32)
+    codes, inv, scale = oq.to_fp8_nf_aware(x)
+    recon = ofp8.decode(codes, "e4m3") * inv
+    assert np.abs(x - recon).mean() / np.abs(x).mean() < 0.15
+    assert np.square(x - recon).mean() / np.square(x).mean() < 0.01
+    # 3 sigma sits below the amax: the scale is larger than the amax rule's
+    # and everything beyond 3 sigma saturates at +-448
+    assert scale > oq.per_tensor_scale(x, "f32")
+    beyond = np.abs(x) * scale > 448
+    assert beyond.any() and np.all((codes[beyond] & 0x7F) == 0x7E)
+    c, inv_c, _ = oq.to_fp8_nf_aware(np.full((64, 64), 0.5, np.float32))
+    assert np.isfinite(inv_c) and np.all((c & 0x7F) == 0x7E)
+
+
+def test_nf_dual_quant_composition():
+    rng = np.random.default_rng(6)
+    W = (rng.standard_normal((48, 80)) * 0.02).astype(np.float32)
+    W[3, 5] = 0.5  # an outlier far beyond 3 sigma
+    ef = (rng.standard_normal(W.shape) * 1e-4).astype(np.float32)
+    hi, lo, ih, il, ef_new, res = oq.dual_quant_per_tensor(W, ef, sigma_factor=3.0)
+    w = W + ef
+    hi2, ih2, _ = oq.to_fp8_nf_aware(w, 3.0)
+    assert np.array_equal(hi, hi2) and ih == ih2
+    # the clipped outlier's excess moves into the residual, which W_lo
+    # quantises with its own amax rule
+    assert np.abs(res).max() == np.abs(res[3, 5]) and res[3, 5] > 0.4
+    lo2, il2, _ = oq.to_fp8_per_tensor(res, "f32")
+    assert np.array_equal(lo, lo2) and il == il2
+    # the delayed NF branch: the first call and every memoryless step equal
+    # the plain NF dual quantisation
+    st = oq.new_delayed_state()
+    for step in range(3):
+        d = oq.dual_quant_per_tensor_delayed(W, ef, st, "w", decay=0.0, interval=1,
+                                             sigma_factor=3.0)
+        p = oq.dual_quant_per_tensor(W, ef, sigma_factor=3.0)
+        assert d[5] and all(np.array_equal(np.asarray(a), np.asarray(b))
+                            for a, b in zip(d[:5], p[:5])), f"step {step}"
+        assert st["amax"]["w.w_hi"] == oq.nf_target(W + ef, 3.0)
+        ef = d[4]
+
+
 # ------------------------------------------------------- block quant (a4)
 @pytest.mark.parametrize("bs", [32, 64, 128])
 def test_block_quantize_exponent_and_codes(bs):
