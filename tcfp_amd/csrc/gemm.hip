@@ -27,6 +27,7 @@
 // run of tiles, grouped 8 tile-rows deep, which keeps an XCD's A and B
 // panels resident in its own L2.
 #include <algorithm>
+#include <type_traits>
 
 #include "common.h"
 
@@ -887,12 +888,269 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && NS == 2 && BM == 128 ? 2 : 1))
   }
 }
 
+// ---------------------------------------------------------------------------
+// Persistent large-tile dual GEMM: per-tensor scales, bf16 output.
+//
+// One workgroup per CU runs tiles b, b + G, b + 2G, ... (G = gridDim.x) of
+// the same grouped, XCD-aware tile order as gemm_nt_dma_kernel, as one
+// stream of K stages, so a tile change costs neither a workgroup launch nor
+// a cold pipeline:
+//  - stage 0 of the next tile is loaded while the current tile's last stage
+//    computes (it takes the buffer stage nt - 2 frees);
+//  - the last stage's buffer is not refilled: the epilogue stages the bf16
+//    output there (every wave finished reading it at that stage's barrier),
+//    reads it back into registers, and the next tile's stage 1 is loaded
+//    into it before the global stores are issued;
+//  - the first barrier of the next tile waits for that stage but not for the
+//    stores (loads and stores retire in issue order under vmcnt), so the
+//    output drains to memory while the next tile computes.
+// The per-stage schedule is the large tile's of gemm_nt_dma_kernel.
+// Launched only for full tiles (M % 256 == 0, N % 128 == 0, K % 128 == 0,
+// K > 128: two stages at least) and a 16-byte aligned output with
+// ldo % 8 == 0: every wave then issues exactly NST store instructions per
+// tile, which the vmcnt accounting above relies on, and no stage is partial.
+template <int AF, int BF>
+__global__ __launch_bounds__(512, 1) void gemm_nt_persist_kernel(GemmArgs g) {
+  constexpr int NW = 8, BM = 256, BN = 128, NS = 2;
+  constexpr int WM = NW / 2, TMW = BM / WM, MB = TMW / 32;
+  constexpr int TNW = BN / 2, NB = TNW / 32, NF = 2 * NB;
+  constexpr int SROWS = BM + 2 * BN;
+  constexpr int STAGE = SROWS * kRowB;
+  constexpr int RPW = SROWS / NW;
+  constexpr int DI = RPW / 8;
+  constexpr int NP = NF * MB;
+  constexpr int RB = TNW * 2;      // bytes of one staged bf16 tile row
+  constexpr int CPR = RB / 16;     // 16-byte chunks per row
+  constexpr int RPI = 64 / CPR;    // rows per store instruction
+  constexpr int NST = TMW / RPI;   // store instructions per wave and tile
+  static_assert(NW * TMW * RB <= STAGE, "epilogue staging must fit one operand buffer");
+  static_assert(NST + DI <= 63, "vmcnt immediate");
+  __shared__ __align__(16) uint8_t lds[NS * STAGE];
+
+  const int M = g.M, N = g.N, K = g.K;
+  uint16_t* __restrict__ out = static_cast<uint16_t*>(g.out);
+  const int T = g.tiles_m * g.tiles_n;
+  const int ntile = (T - int(blockIdx.x) + int(gridDim.x) - 1) / int(gridDim.x);
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  const int lr = lane & 31, lg = lane >> 5;
+
+  // this wave's DMA rows: activation (region 0), slot 0 (1) or slot 1 (2)
+  const int srow0 = wave * RPW;
+  const int region = srow0 < BM ? 0 : (srow0 < BM + BN ? 1 : 2);
+  const int row_base = region == 0 ? srow0 : (region == 1 ? srow0 - BM : srow0 - BM - BN);
+  const uint8_t* const src_base = region == 0 ? g.A : (region == 1 ? g.B0 : g.B1);
+  const int64_t ld = region == 0 ? g.lda : g.ldb;
+  const int region_rows = region == 0 ? BM : BN;
+  const uint32_t nrec = uint32_t(int64_t(region_rows - 1) * ld + K);  // full tiles only
+  const int chunk0 = (lane & 7) ^ swz(lane >> 3);
+  const int chunk1 = (lane & 7) ^ swz(8 + (lane >> 3));
+  uint32_t voff[DI];  // byte offsets of this lane's rows within a tile (tile-independent)
+#pragma unroll
+  for (int i = 0; i < DI; ++i) {
+    const int r = row_base + i * 8 + (lane >> 3);
+    voff[i] = uint32_t(int64_t(r) * ld + ((i & 1) ? chunk1 : chunk0) * 16);
+  }
+  const uint32_t lds0 = uint32_t(reinterpret_cast<uintptr_t>((TCFP_LDS uint8_t*)lds));
+  const uint32_t lds_base = lds0 + uint32_t(srow0) * kRowB;
+  const int nt = K / kSK;
+
+  // tile `it` of this workgroup -> (m0, n0)
+  auto tile_of = [&](int it, int& m0, int& n0) {
+    int l = int(blockIdx.x) + it * int(gridDim.x);
+    if ((T & 7) == 0) l = (l & 7) * (T >> 3) + (l >> 3);
+    constexpr int G = 8;
+    const int per_group = G * g.tiles_n;
+    const int first_m = (l / per_group) * G;
+    const int gm = min(g.tiles_m - first_m, G);
+    m0 = (first_m + (l % per_group) % gm) * BM;
+    n0 = ((l % per_group) / gm) * BN;
+  };
+  auto src_of = [&](int m0, int n0) {
+    return make_rsrc(src_base + int64_t(region == 0 ? m0 : n0) * ld, nrec);
+  };
+  // DMA of stage t of the tile whose operand rows `rs` describes into buffer b
+  auto issue = [&](const v4i& rs, int t, int b) {
+    const uint32_t dst = lds_base + uint32_t(b) * STAGE;
+    const uint32_t soff = uint32_t(t) * kSK;
+#pragma unroll
+    for (int i = 0; i < DI; ++i) dma16(rs, voff[i], soff, dst + i * 1024);
+  };
+
+  int ro[2][2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int q = 0; q < 2; ++q) ro[h][q] = lr * kRowB + (((4 * h + lg + 2 * q) ^ swz(lr)) << 4);
+
+  v16f acc[2][NB][MB];
+  auto zero_acc = [&]() {
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+      for (int j = 0; j < NB; ++j)
+#pragma unroll
+        for (int i = 0; i < MB; ++i)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc[s][j][i][r] = 0.0f;
+  };
+  auto read_frags = [&](v8i* f, int b, int h) {
+    const uint8_t* st = lds + b * STAGE;
+#pragma unroll
+    for (int q = 0; q < NF; ++q) {
+      const int rb = (BM + (q / NB) * BN + wn * TNW + (q % NB) * 32) * kRowB;
+      f[q] = make_frag(lds_read16(st, rb + ro[h][0]), lds_read16(st, rb + ro[h][1]));
+    }
+#pragma unroll
+    for (int i = 0; i < MB; ++i) {
+      const int rb = (wm * TMW + i * 32) * kRowB;
+      f[NF + i] = make_frag(lds_read16(st, rb + ro[h][0]), lds_read16(st, rb + ro[h][1]));
+    }
+  };
+  auto mfmas_range = [&](const v8i* f, int lo, int hi) {
+#pragma unroll
+    for (int idx = 0; idx < NP; ++idx) {
+      if (idx < lo || idx >= hi) continue;
+      const int i = idx / NF, q = idx % NF;
+      v16f& c = acc[q / NB][q % NB][i];
+      c = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f[q], f[NF + i], c, BF, AF, 0, 127, 0,
+                                                           127);
+    }
+  };
+  // every DMA landed except the newest `keep` vector-memory operations
+  // (the previous tile's output stores), every wave's LDS reads are done
+  auto sync_keep = [&](auto keep) {
+    constexpr int k = decltype(keep)::value;
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt((k & 15) | (7 << 4) | ((k >> 4) << 14));
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  float c0s = 1.0f, c1s = 1.0f;
+  if (g.s_a) {
+    const float sa = *g.s_a;
+    c0s = sa * *g.s_0;
+    c1s = sa * *g.s_1;
+  }
+
+  int m0, n0;
+  tile_of(0, m0, n0);
+  v4i cur = src_of(m0, n0);
+  v8i f0[NF + MB], f1[NF + MB];
+  zero_acc();
+  // prologue: stages 0 and 1 of the first tile (nt >= 2 for this kernel)
+  issue(cur, 0, 0);
+  issue(cur, 1, 1);
+  __builtin_amdgcn_s_waitcnt((DI & 15) | (7 << 4) | ((DI >> 4) << 14));
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+  read_frags(f0, 0, 0);
+
+  int cb0 = 0;  // buffer of the current tile's stage 0
+  for (int it = 0; it < ntile; ++it) {
+    const bool more = it + 1 < ntile;
+    v4i nxt = cur;
+    int m1 = 0, n1 = 0;
+    if (more) {
+      tile_of(it + 1, m1, n1);
+      nxt = src_of(m1, n1);
+    }
+    for (int t = 0; t < nt; ++t) {
+      const int b = (cb0 + t) & 1;
+      __builtin_amdgcn_sched_barrier(0);
+      read_frags(f1, b, 1);
+      mfmas_range(f0, 0, NP / 2);
+      interleave_mfma_lds<NP / 2, 2 * (NF + MB), 0>();
+      if (t == 0 && it > 0)
+        sync_keep(std::integral_constant<int, NST>{});
+      else
+        sync_keep(std::integral_constant<int, 0>{});
+      mfmas_range(f0, NP / 2, NP);
+      __builtin_amdgcn_sched_barrier(0);
+      if (t + 2 < nt)
+        issue(cur, t + 2, b);
+      else if (t + 2 == nt && more)
+        issue(nxt, 0, b);  // the next tile's stage 0
+      __builtin_amdgcn_sched_barrier(0);
+      // sub-step 0 of stage t + 1 (after the last stage: the next tile's
+      // stage 0, landed at this barrier; stale and unused after the last tile)
+      read_frags(f0, b ^ 1, 0);
+      mfmas_range(f1, 0, NP);
+      interleave_mfma_lds<NP, 2 * (NF + MB), 0>();
+    }
+
+    // ---- epilogue: stage through the last stage's buffer -------------------
+    const int sb = (cb0 + nt - 1) & 1;
+    uint8_t* eps = lds + sb * STAGE + wave * (TMW * RB);
+    const int nb = n0 + wn * TNW;
+#pragma unroll
+    for (int i = 0; i < MB; ++i)
+#pragma unroll
+      for (int j = 0; j < NB; ++j)
+#pragma unroll
+        for (int gq = 0; gq < 4; ++gq) {
+          const int row = i * 32 + lr, col = j * 32 + gq * 8 + lg * 4;
+          float v[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int r = gq * 4 + q;
+            v[q] = acc[0][j][i][r] * c0s + acc[1][j][i][r] * c1s;
+          }
+          if (g.bias) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) v[q] += g.bias[nb + col + q];
+          }
+          const int byte = col * 2;
+          const int chunk = (byte >> 4) ^ (row & (CPR - 1));
+          store4<uint16_t>(reinterpret_cast<uint16_t*>(eps + row * RB + chunk * 16 + (byte & 15)),
+                           v[0], v[1], v[2], v[3]);
+        }
+    asm volatile("" ::: "memory");
+    // the NST staged chunks of this lane, held in named registers (an array
+    // here is kept in scratch memory across the barrier below)
+    static_assert(NST == 8, "eight store chunks per lane");
+    auto staged = [&](int s) {
+      const int row = s * RPI + lane / CPR, cl = lane % CPR;
+      return *reinterpret_cast<const uint4*>(eps + row * RB + ((cl ^ (row & (CPR - 1))) * 16));
+    };
+    const uint4 d0 = staged(0), d1 = staged(1), d2 = staged(2), d3 = staged(3);
+    const uint4 d4 = staged(4), d5 = staged(5), d6 = staged(6), d7 = staged(7);
+    if (more) {
+      // every wave holds its staged output: the buffer takes the next tile's stage 1
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0), vmcnt and expcnt untouched
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+      issue(nxt, 1, sb);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    auto put = [&](int s, const uint4& d) {
+      const int row = s * RPI + lane / CPR, cl = lane % CPR;
+      uint16_t* o = out + int64_t(m0 + wm * TMW + row) * g.ldo + nb + cl * 8;
+      *reinterpret_cast<uint4*>(o) = d;
+    };
+    put(0, d0); put(1, d1); put(2, d2); put(3, d3);
+    put(4, d4); put(5, d5); put(6, d6); put(7, d7);
+    __builtin_amdgcn_sched_barrier(0);
+    zero_acc();
+    cb0 = sb ^ 1;  // the next tile's stage 0 sits in the other buffer
+    cur = nxt;
+    m0 = m1;
+    n0 = n1;
+  }
+}
+
 // Largest byte span any DMA descriptor may cover (offsets are 32-bit and
 // the out-of-range sentinel must stay beyond every span).
 constexpr int64_t kMaxSpan = (int64_t(1) << 31) - (int64_t(1) << 20);
 
 // Tile policy: 0 = automatic, 1 = always 256 x 128, 2 = always 128 x 64,
-// 3 = 128 x 64 with eight waves in the one-round deep-pipeline case.
+// 3 = 128 x 64 with eight waves in the one-round deep-pipeline case,
+// 4 = 256 x 128 with one workgroup per tile (no persistent launch).
 int g_tile_policy = 0;
 
 int num_cus() {
@@ -941,7 +1199,18 @@ int launch_gemm(GemmArgs ga, hipStream_t st) {
     } else if (small) {
       gemm_nt_dma_kernel<AF, BF, SPLIT, OutT, 4, 128, 64, SCALE, 2><<<grid, 256, 0, st>>>(ga);
     } else if constexpr (!(SCALE == 1 && SPLIT) && SCALE != 2) {
-      gemm_nt_dma_kernel<AF, BF, SPLIT, OutT, 8, 256, 128, SCALE, 2><<<grid, 512, 0, st>>>(ga);
+      // more tiles than CUs, all of them full, bf16 out: one persistent
+      // workgroup per CU runs its tiles back to back
+      bool persist = false;
+      if constexpr (SCALE == 0 && !SPLIT && std::is_same<OutT, uint16_t>::value) {
+        persist = g_tile_policy != 4 && splits == 1 && int64_t(grid.x) > num_cus() &&
+                  m % 256 == 0 && n % 128 == 0 && k % kSK == 0 && k > kSK && ga.ldo % 8 == 0 &&
+                  (reinterpret_cast<uintptr_t>(ga.out) & 15) == 0;
+        if (persist)
+          gemm_nt_persist_kernel<AF, BF><<<unsigned(num_cus()), 512, 0, st>>>(ga);
+      }
+      if (!persist)
+        gemm_nt_dma_kernel<AF, BF, SPLIT, OutT, 8, 256, 128, SCALE, 2><<<grid, 512, 0, st>>>(ga);
     }
     return hipGetLastError() == hipSuccess ? TCFP_OK : TCFP_ERR_HIP;
   }
@@ -1093,7 +1362,7 @@ extern "C" int tcfp_wtquant_block_dual_gemm(const uint8_t* a, int a_fmt, int64_t
 }
 
 extern "C" int tcfp_gemm_set_tile_policy(int policy) {
-  if (policy < 0 || policy > 3) return TCFP_ERR_SHAPE;
+  if (policy < 0 || policy > 4) return TCFP_ERR_SHAPE;
   g_tile_policy = policy;
   return TCFP_OK;
 }

@@ -1009,7 +1009,10 @@ def workspace_error(device: torch.device | None = None) -> int:
 
 
 def set_gemm_tile_policy(policy: str) -> None:
-    """Tuning hook: ``"auto"`` (default), ``"large"`` (256 x 128 tiles) or
-    ``"small"`` (128 x 64 tiles, two workgroups per CU)."""
-    code = {"auto": 0, "large": 1, "small": 2, "small8": 3}[policy]
+    """Tuning hook: ``"auto"`` (default), ``"large"`` (256 x 128 tiles),
+    ``"small"`` (128 x 64 tiles, two workgroups per CU), ``"small8"``
+    (128 x 64 with eight waves where the grid fits one round) or
+    ``"large_nonpersistent"`` (256 x 128 with one workgroup per tile, never
+    the persistent launch).  Results do not depend on the policy."""
+    code = {"auto": 0, "large": 1, "small": 2, "small8": 3, "large_nonpersistent": 4}[policy]
     check(_hip.lib().tcfp_gemm_set_tile_policy(code), "set_gemm_tile_policy")

@@ -156,6 +156,59 @@ def test_tile_policies_agree_bitwise(dev, M, K_, N):
     assert torch.equal(outs[0], outs[2]) and torch.equal(outs[1], outs[3])
 
 
+# ------------------------------------- persistent large-tile launch (C2)
+def _kernel_names(fn):
+    from torch.profiler import ProfilerActivity, profile
+
+    with profile(activities=[ProfilerActivity.CUDA]) as prof:
+        fn()
+        torch.cuda.synchronize()
+    return [e.name for e in prof.events()]
+
+
+@pytest.mark.parametrize("M,N,K_", [(4096, 4096, 4096), (4352, 4096, 256), (8192, 4096, 1024),
+                                    (2048, 8192, 512)])
+@pytest.mark.parametrize("afmt", [torch.float8_e4m3fn, torch.float8_e5m2])
+def test_persistent_dual_gemm_matches_one_workgroup_per_tile(dev, M, N, K_, afmt):
+    """More full 256x128 tiles than CUs with bf16 output runs one persistent
+    workgroup per CU over several tiles (4352 rows: some run three, K = 256:
+    two stages, the fewest it takes).  Each output accumulates in the same
+    K order as with one workgroup per tile, so the bf16 results, bias
+    included, are identical."""
+    print(f"persistent M={M} N={N} K={K_} {afmt}", flush=True)
+    a, sa = make_act((M, K_), 21, dev, afmt)
+    h, l, ih, il = make_pair((N, K_), 22, dev)
+    bias = torch.randn(N, generator=torch.Generator().manual_seed(23)).to(dev)
+    run = lambda: K.fused_dual_gemm_forward(a, h, l, sa, ih, il, bias=bias,
+                                            out_dtype=torch.bfloat16)
+    names = _kernel_names(run)
+    assert any("gemm_nt_persist_kernel" in n for n in names), names
+    p = run()
+    try:
+        K.set_gemm_tile_policy("large_nonpersistent")
+        assert not any("gemm_nt_persist_kernel" in n for n in _kernel_names(run))
+        q = run()
+    finally:
+        K.set_gemm_tile_policy("auto")
+    assert torch.equal(p.view(torch.int16), q.view(torch.int16))
+    if (M, N, K_) == (2048, 8192, 512):
+        fmt = ofp8.E4M3 if afmt == torch.float8_e4m3fn else ofp8.E5M2
+        ref = og.dual_gemm_nt(u8(a), fmt, u8(h), u8(l), sa.item(), ih.item(), il.item())
+        ref = ref + bias.cpu().double().numpy()
+        assert og.rel_fro(p.float().cpu().numpy(), ref) < TOL
+
+
+def test_persistent_launch_not_taken_for_partial_tiles(dev):
+    # edge tiles, a partial K stage or fp32 output keep one workgroup per tile
+    for M, N, K_, od in [(4000, 4096, 1024, torch.bfloat16), (4096, 4096, 1040, torch.bfloat16),
+                         (4096, 4096, 1024, torch.float32)]:
+        a, sa = make_act((M, K_), 24, dev)
+        h, l, ih, il = make_pair((N, K_), 25, dev)
+        names = _kernel_names(lambda: K.fused_dual_gemm_forward(a, h, l, sa, ih, il,
+                                                                out_dtype=od))
+        assert not any("gemm_nt_persist_kernel" in n for n in names), (M, N, K_, od)
+
+
 # ------------------------------------------------- block-scaled (a10, a13)
 def make_block_operands(M, N, K_, bs, dev, seed, act_fp8=torch.float8_e4m3fn):
     g = torch.Generator().manual_seed(seed)
