@@ -390,8 +390,10 @@ int tcfp_workspace_error(const void* workspace, int* flag, void* stream);
 /* ---- self-test hooks (no reference counterpart) ------------------------ */
 
 /* Converts every float32 whose bit pattern lies in [lo_bits, hi_bits] (and
- * its negation) with both the hardware and the software FP8 encoder and
- * counts mismatches into *mismatches (device uint64, accumulated). */
+ * its negation) with both the hardware and the software FP8 encoder, and
+ * decodes all 256 codes with both the hardware and the software decoder
+ * (NaN codes must decode to NaN in both); counts mismatches into
+ * *mismatches (device uint64, accumulated). */
 int tcfp_selftest_fp8_cvt(uint32_t lo_bits, uint32_t hi_bits, int fp8_fmt,
                           unsigned long long* mismatches, void* stream);
 

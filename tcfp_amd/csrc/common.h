@@ -82,7 +82,9 @@ TCFP_DEV uint32_t f32_to_fp8(float x, bool sat = false) {
   else return f32_to_e4m3(x, sat);
 }
 
-TCFP_DEV float e4m3_to_f32(uint32_t c) {
+// Software decoders (exact, from the OCP FP8 definitions): the reference
+// the hardware decoders below are checked against, code by code.
+TCFP_DEV float sw_e4m3_to_f32(uint32_t c) {
   uint32_t s = (c & 0x80u) << 24;
   uint32_t e = (c >> 3) & 0xFu, m = c & 7u;
   uint32_t mag;
@@ -92,7 +94,7 @@ TCFP_DEV float e4m3_to_f32(uint32_t c) {
   return __uint_as_float(s | mag);
 }
 
-TCFP_DEV float e5m2_to_f32(uint32_t c) {
+TCFP_DEV float sw_e5m2_to_f32(uint32_t c) {
   uint32_t s = (c & 0x80u) << 24;
   uint32_t e = (c >> 2) & 0x1Fu, m = c & 3u;
   uint32_t mag;
@@ -101,6 +103,19 @@ TCFP_DEV float e5m2_to_f32(uint32_t c) {
   else mag = ((e + 112u) << 23) | (m << 21);
   return __uint_as_float(s | mag);
 }
+
+template <int FMT>
+TCFP_DEV float sw_fp8_to_f32(uint32_t c) {
+  if constexpr (FMT == TCFP_FP8_E5M2) return sw_e5m2_to_f32(c);
+  else return sw_e4m3_to_f32(c);
+}
+
+// Hardware decoders (v_cvt_f32_fp8 / v_cvt_f32_bf8, byte 0 of c): one
+// instruction.  Every FP8 value is exact in fp32; the GPU self-test checks
+// all 256 codes of both formats against the software decoders (NaN codes
+// decode to a NaN in both).
+TCFP_DEV float e4m3_to_f32(uint32_t c) { return __builtin_amdgcn_cvt_f32_fp8(int(c), 0); }
+TCFP_DEV float e5m2_to_f32(uint32_t c) { return __builtin_amdgcn_cvt_f32_bf8(int(c), 0); }
 
 template <int FMT>
 TCFP_DEV float fp8_to_f32(uint32_t c) {

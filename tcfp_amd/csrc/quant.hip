@@ -1267,10 +1267,20 @@ struct Seg {
   static constexpr int ROWS = kThreads / L;
 };
 
+// Max over each group of L consecutive lanes (L a power of two <= 32),
+// returned to every lane of the group.  DPP permutations inside a row of 16
+// lanes (quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror,
+// row_mirror: after each step every lane holds the max of a group twice as
+// large) need no index arithmetic; the 32-lane step is a ds_swizzle with
+// xor mask 16.  Every lane of the wave executes the reduction.
 template <int L>
 TCFP_DEV uint32_t seg_umax(uint32_t m) {
-#pragma unroll
-  for (int o = L / 2; o > 0; o >>= 1) m = umax(m, __shfl_xor(m, o, 64));
+  if constexpr (L >= 2) m = umax(m, uint32_t(__builtin_amdgcn_update_dpp(0, int(m), 0xB1, 0xF, 0xF, false)));
+  if constexpr (L >= 4) m = umax(m, uint32_t(__builtin_amdgcn_update_dpp(0, int(m), 0x4E, 0xF, 0xF, false)));
+  if constexpr (L >= 8) m = umax(m, uint32_t(__builtin_amdgcn_update_dpp(0, int(m), 0x141, 0xF, 0xF, false)));
+  if constexpr (L >= 16) m = umax(m, uint32_t(__builtin_amdgcn_update_dpp(0, int(m), 0x140, 0xF, 0xF, false)));
+  if constexpr (L >= 32) m = umax(m, uint32_t(__builtin_amdgcn_ds_swizzle(int(m), 0x401F)));
+  static_assert(L >= 1 && L <= 32 && (L & (L - 1)) == 0, "segment of 1..32 lanes");
   return m;
 }
 
@@ -1327,7 +1337,9 @@ TCFP_DEV void encode_words(const float* v, uint32_t* words) {
 template <int N>
 TCFP_DEV void store_words(uint8_t* dst, const uint32_t* words) {
   if constexpr (N == 4) *reinterpret_cast<uint32_t*>(dst) = words[0];
-  else *reinterpret_cast<uint2*>(dst) = make_uint2(words[0], words[1]);
+  else if constexpr (N == 8) *reinterpret_cast<uint2*>(dst) = make_uint2(words[0], words[1]);
+  else *reinterpret_cast<uint4*>(dst) = make_uint4(words[0], words[1], words[2], words[3]);
+  static_assert(N == 4 || N == 8 || N == 16, "4, 8 or 16 codes");
 }
 
 TCFP_DEV uint32_t wbyte(const uint32_t* words, int j) { return (words[j >> 2] >> (8 * (j & 3))) & 0xFFu; }
@@ -1381,37 +1393,46 @@ __global__ __launch_bounds__(kThreads) void block_quant_kernel(const InT* __rest
   }
 }
 
-// Stochastic-rounding variants of the dual kernel carry 8 elements per lane
-// so that one Philox call (8 x 16 random bits) serves a lane's elements.
+// Elements per lane of the dual kernel (each Philox call of the stochastic
+// variants -- 8 x 16 random bits -- serves 8 of them): with stochastic
+// rounding 8 (fp32) or 16 (bf16), otherwise one 16-byte load (4 fp32 or
+// 8 bf16), or 8 fp32 for 32-element blocks.  Measured fastest on MI355X
+// among 4/8/16 elements per lane, contiguous or in interleaved 16-byte
+// chunks (SRR 16384 x 4096: 110 us at 8 fp32 against 116-182 us).
 template <typename InT, int BS, bool SR>
-using DualSeg = Seg<InT, BS, SR ? 8 : 16 / int(sizeof(InT))>;
+using DualSeg = Seg<InT, BS, SR ? 16 / int(sizeof(InT)) * 2 : (BS == 32 ? 8 : 16 / int(sizeof(InT)))>;
 
 template <typename InT, int N>
 TCFP_DEV void load_in(const InT* p, float* v) {
   if constexpr (sizeof(InT) == 4) {
     loadf<N>(reinterpret_cast<const float*>(p), v);
   } else {
-    static_assert(N == 8, "bf16 segments load 8 elements");
-    load8(reinterpret_cast<const uint16_t*>(p), v);
+    static_assert(N % 8 == 0, "bf16 segments load 8 elements at a time");
+#pragma unroll
+    for (int i = 0; i < N; i += 8) load8(reinterpret_cast<const uint16_t*>(p) + i, v + i);
   }
 }
 
 // Block stochastic rounding (tcfp/kernels.py:398-423): the neighbour is
-// found by a quarter-magnitude nudge under a saturating cast.
+// found by a quarter-magnitude nudge under a saturating cast, and is taken
+// with probability |diff| / gap.  The draw u = k * 2^-16 (k a 16-bit
+// integer) is compared as u * gap < |diff|: u has 16 significant bits and
+// gap, the distance between two E4M3 values no more than ~0.6 |rtn| apart,
+// at most 5, so the product is exact and the test is the exact comparison
+// u < |diff| / gap, with no division.  diff == 0 keeps rtn (the product is
+// not below 0); gap == 0 (the nudge rounds back to rtn's value) keeps rtn;
+// a NaN x keeps rtn (its own NaN code) since every comparison is false.
+TCFP_DEV bool sr_take(float diff, float g, float u) { return g != 0.0f && u * g < fabsf(diff); }
+
 TCFP_DEV uint32_t sr_block(float x, float u) {
   const uint32_t rtn = f32_to_e4m3(x, true);
-  const float rtn_f = e4m3_to_f32(rtn);
+  const float rtn_f = sw_e4m3_to_f32(rtn);
   const float diff = x - rtn_f;
-  const float d = diff >= 0.0f ? 1.0f : -1.0f;
-  const float abs_rtn = fmaxf(fabsf(rtn_f), 1e-12f);
-  const float nud = rtn_f + (d * abs_rtn) * 0.25f;
+  const float q = fmaxf(fabsf(rtn_f), 1e-12f) * 0.25f;
+  const float nud = rtn_f + (diff >= 0.0f ? q : -q);
   const uint32_t other = f32_to_e4m3(clampf(nud, kE4M3Max), true);
-  const float other_f = e4m3_to_f32(other);
-  const float g = fabsf(other_f - rtn_f);
-  const float gap = fmaxf(g, 1.4e-45f);
-  const float frac = fminf(fabsf(diff) / gap, 1.0f);
-  const bool exact = (fabsf(diff) < 1.4e-45f) || (g < 1.4e-45f);
-  return exact ? rtn : (u < frac ? other : rtn);
+  const float other_f = sw_e4m3_to_f32(other);
+  return sr_take(diff, fabsf(other_f - rtn_f), u) ? other : rtn;
 }
 
 // sr_block on the hardware converts.  Both encodes see clamped inputs
@@ -1428,20 +1449,50 @@ TCFP_DEV uint32_t sr_block_hw(float x, float u) {
   const uint32_t rtn = hw_e4m3(x);
   const float rtn_f = hw_e4m3_f32(rtn);
   const float diff = x - rtn_f;
-  const float d = diff >= 0.0f ? 1.0f : -1.0f;
-  const float abs_rtn = fmaxf(fabsf(rtn_f), 1e-12f);
-  const float nud = rtn_f + (d * abs_rtn) * 0.25f;
+  const float q = fmaxf(fabsf(rtn_f), 1e-12f) * 0.25f;
+  const float nud = rtn_f + (diff >= 0.0f ? q : -q);
   const uint32_t other = hw_e4m3(clampf(nud, kE4M3Max));
   const float other_f = hw_e4m3_f32(other);
-  const float g = fabsf(other_f - rtn_f);
-  const float gap = fmaxf(g, 1.4e-45f);
-  const float frac = fminf(fabsf(diff) / gap, 1.0f);
-  const bool exact = (fabsf(diff) < 1.4e-45f) || (g < 1.4e-45f);
-  return exact ? rtn : (u < frac ? other : rtn);
+  return sr_take(diff, fabsf(other_f - rtn_f), u) ? other : rtn;
 }
 
-// Uniform in [0, 1) from the low 16 bits of v.
-TCFP_DEV float u16_to_unit(uint32_t v) { return float(v & 0xFFFFu) * 1.52587890625e-05f; }
+// sr_block_hw on four values c[0..4) with packed converts (two values per
+// encode or decode).  Value j draws the 16-bit field j of (r0, r1), low
+// half first, as u = k * 2^-16.  Returns the four codes, value j in byte j.
+// The nudged values are clamped with fmin/fmax: for a NaN c[j] the choice
+// is rtn whatever the candidate is.
+TCFP_DEV uint32_t sr_block_hw4(const float* c, uint32_t r0, uint32_t r1) {
+  typedef float f2 __attribute__((ext_vector_type(2)));
+  const uint32_t rtn = cvt4_fp8<TCFP_FP8_E4M3>(c[0], c[1], c[2], c[3]);
+  const f2 ra = __builtin_amdgcn_cvt_pk_f32_fp8(int(rtn), false);
+  const f2 rb = __builtin_amdgcn_cvt_pk_f32_fp8(int(rtn), true);
+  const float rf[4] = {ra[0], ra[1], rb[0], rb[1]};
+  float diff[4], nud[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    diff[j] = c[j] - rf[j];
+    // the nudge takes diff's sign (for diff == -0 too: the choice is rtn then)
+    const float q = __builtin_copysignf(fmaxf(fabsf(rf[j]), 1e-12f) * 0.25f, diff[j]);
+    nud[j] = fminf(fmaxf(rf[j] + q, -kE4M3Max), kE4M3Max);
+  }
+  const uint32_t oth = cvt4_fp8<TCFP_FP8_E4M3>(nud[0], nud[1], nud[2], nud[3]);
+  const f2 oa = __builtin_amdgcn_cvt_pk_f32_fp8(int(oth), false);
+  const f2 ob = __builtin_amdgcn_cvt_pk_f32_fp8(int(oth), true);
+  const float of[4] = {oa[0], oa[1], ob[0], ob[1]};
+  const uint32_t k[4] = {r0 & 0xFFFFu, r0 >> 16, r1 & 0xFFFFu, r1 >> 16};
+  // sr_take without its gap == 0 guard: a zero gap means the candidate has
+  // rtn's value, and then also rtn's code unless both are zeros, which
+  // happens only with diff == 0 (an exact x), where the strict comparison
+  // already keeps rtn.  (The self-test checks this form against sr_block,
+  // guard included, on every float in range.)
+  uint32_t mask = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const float u = float(k[j]) * 1.52587890625e-05f;
+    if (u * fabsf(of[j] - rf[j]) < fabsf(diff[j])) mask |= 0xFFu << (8 * j);
+  }
+  return (oth & mask) | (rtn & ~mask);
+}
 
 // Fused block dual quantisation + error update (tcfp/kernels.py:288-459 and
 // :1867-1873).  The error buffer is read and rewritten by the same lane.
@@ -1524,22 +1575,15 @@ __global__ __launch_bounds__(kThreads) void block_dualq_kernel(
   for (int j = 0; j < VEC; ++j) c[j] = clampf(r[j] * mul_lo, kE4M3Max);
   uint32_t lc[VEC / 4];
   if constexpr (SR) {
-    // elements off .. off + 7 (off % 8 == 0) draw Philox counter off / 8;
-    // element j takes 16 bits of word j / 2
-    static_assert(VEC == 8, "one Philox call per 8 elements");
-    const uint64_t ctr = uint64_t(off) >> 3;
-    const u32x4 rr = philox4x32_10({uint32_t(ctr), uint32_t(ctr >> 32), off0, off1}, k0, k1);
-    const uint32_t words[4] = {rr.x, rr.y, rr.z, rr.w};
+    // elements 8i .. 8i + 7 of the tensor (flat index) draw Philox counter
+    // i; element 8i + j takes the 16-bit field j of the four output words
+    static_assert(VEC % 8 == 0, "whole Philox calls per lane");
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      uint32_t word = 0;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int j = 4 * q + e;
-        const float u = u16_to_unit(words[j >> 1] >> (16 * (j & 1)));
-        word |= sr_block_hw(c[j], u) << (8 * e);
-      }
-      lc[q] = word;
+    for (int g8 = 0; g8 < VEC / 8; ++g8) {
+      const uint64_t ctr = (uint64_t(off) >> 3) + uint64_t(g8);
+      const u32x4 rr = philox4x32_10({uint32_t(ctr), uint32_t(ctr >> 32), off0, off1}, k0, k1);
+      lc[2 * g8] = sr_block_hw4(c + 8 * g8, rr.x, rr.y);
+      lc[2 * g8 + 1] = sr_block_hw4(c + 8 * g8 + 4, rr.z, rr.w);
     }
   } else {
     encode_words<VEC, TCFP_FP8_E4M3>(c, lc);
@@ -1625,22 +1669,34 @@ __global__ __launch_bounds__(kThreads) void selftest_cvt_kernel(uint32_t lo, uin
     const uint32_t s = f32_to_fp8<FMT>(x) | (f32_to_fp8<FMT>(-x) << 8);
     cnt += (h != s);
   }
+  // workgroup 0 also decodes all 256 codes with both decoders
+  if (blockIdx.x == 0) {
+    const float a = fp8_to_f32<FMT>(threadIdx.x), b = sw_fp8_to_f32<FMT>(threadIdx.x);
+    cnt += !((a != a && b != b) || __float_as_uint(a) == __float_as_uint(b));
+  }
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) cnt += __shfl_xor(cnt, o, 64);
   if ((threadIdx.x & 63) == 0 && cnt) atomicAdd(bad, (unsigned long long)cnt);
 }
 
-// sr_block (software converts) vs sr_block_hw on every float32 whose bit
-// pattern lies in [lo, hi] and its negation, at one uniform u.
+// sr_block (software converts) vs sr_block_hw and the packed sr_block_hw4
+// on every float32 whose bit pattern lies in [lo, hi] and its negation, at
+// one draw: u is truncated to k * 2^-16, the form the kernels draw.
 __global__ __launch_bounds__(kThreads) void selftest_sr_kernel(uint32_t lo, uint32_t hi, float u,
                                                                unsigned long long* bad) {
   const uint64_t span = uint64_t(hi) - lo + 1;
   const uint64_t stride = uint64_t(gridDim.x) * kThreads;
+  const uint32_t k = uint32_t(fminf(fmaxf(u, 0.0f), 0.99999f) * 65536.0f);
+  const float uk = float(k) * 1.52587890625e-05f;
+  const uint32_t r = k | (k << 16);
   uint32_t cnt = 0;
   for (uint64_t i = uint64_t(blockIdx.x) * kThreads + threadIdx.x; i < span; i += stride) {
     const float x = __uint_as_float(lo + uint32_t(i));
-    cnt += (sr_block(x, u) != sr_block_hw(x, u));
-    cnt += (sr_block(-x, u) != sr_block_hw(-x, u));
+    const uint32_t a = sr_block(x, uk), b = sr_block(-x, uk);
+    cnt += (a != sr_block_hw(x, uk));
+    cnt += (b != sr_block_hw(-x, uk));
+    const float c4[4] = {x, -x, -x, x};
+    cnt += (sr_block_hw4(c4, r, r) != (a | (b << 8) | (b << 16) | (a << 24)));
   }
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) cnt += __shfl_xor(cnt, o, 64);

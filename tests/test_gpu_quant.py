@@ -28,7 +28,8 @@ def i8(t):
 # ------------------------------------------------------------ self tests
 @pytest.mark.parametrize("fmt,top", [(0, 0x43E00000), (1, 0x47600000)])
 def test_hw_fp8_convert_matches_software_exhaustively(dev, fmt, top):
-    # every float32 in [0, FP8_MAX] and its negation
+    # every float32 in [0, FP8_MAX] and its negation through both encoders,
+    # and all 256 codes through both decoders
     bad = torch.zeros(1, dtype=torch.int64, device=dev)
     _hip.check(_hip.lib().tcfp_selftest_fp8_cvt(0, top, fmt, bad.data_ptr(),
                                                  _hip.stream_of(dev)), "selftest")
@@ -38,8 +39,9 @@ def test_hw_fp8_convert_matches_software_exhaustively(dev, fmt, top):
 
 @pytest.mark.parametrize("u", [0.0, 0.25, 0.5, 0.70710678, 1.0 - 2.0 ** -16])
 def test_sr_block_hardware_converts_match_software(dev, u):
-    # the block SR candidate rule on hardware converts == on software converts,
-    # for every float32 in [0, 448] and its negation
+    # the block SR rule on hardware converts (scalar and the packed four-value
+    # form the kernels use) == on software converts, for every float32 in
+    # [0, 448] and its negation, at the draw u truncated to k * 2^-16
     bad = torch.zeros(1, dtype=torch.int64, device=dev)
     _hip.check(_hip.lib().tcfp_selftest_sr_block(0, 0x43E00000, u, bad.data_ptr(),
                                                  _hip.stream_of(dev)), "selftest")
