@@ -889,7 +889,7 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && NS == 2 && BM == 128 ? 2 : 1))
 }
 
 // ---------------------------------------------------------------------------
-// Persistent large-tile dual GEMM: per-tensor scales, bf16 output.
+// Persistent large-tile dual GEMM: per-tensor scales, bf16 or fp32 output.
 //
 // One workgroup per CU runs tiles b, b + G, b + 2G, ... (G = gridDim.x) of
 // the same grouped, XCD-aware tile order as gemm_nt_dma_kernel, as one
@@ -909,8 +909,14 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && NS == 2 && BM == 128 ? 2 : 1))
 // K > 128: two stages at least) and a 16-byte aligned output with
 // ldo % 8 == 0: every wave then issues exactly NST store instructions per
 // tile, which the vmcnt accounting above relies on, and no stage is partial.
-template <int AF, int BF>
+//
+// fp32 output (OutT = float) skips the LDS staging: each lane stores its
+// accumulator rows as 16-byte vectors straight from registers (16 stores per
+// wave and tile), and the freed last-stage buffer takes the next tile's
+// stage 1 right at the last stage's barrier.
+template <int AF, int BF, typename OutT>
 __global__ __launch_bounds__(512, 1) void gemm_nt_persist_kernel(GemmArgs g) {
+  constexpr bool F32OUT = std::is_same<OutT, float>::value;
   constexpr int NW = 8, BM = 256, BN = 128, NS = 2;
   constexpr int WM = NW / 2, TMW = BM / WM, MB = TMW / 32;
   constexpr int TNW = BN / 2, NB = TNW / 32, NF = 2 * NB;
@@ -922,13 +928,14 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persist_kernel(GemmArgs g) {
   constexpr int RB = TNW * 2;      // bytes of one staged bf16 tile row
   constexpr int CPR = RB / 16;     // 16-byte chunks per row
   constexpr int RPI = 64 / CPR;    // rows per store instruction
-  constexpr int NST = TMW / RPI;   // store instructions per wave and tile
+  // store instructions per wave and tile
+  constexpr int NST = F32OUT ? MB * NB * 4 : TMW / RPI;
   static_assert(NW * TMW * RB <= STAGE, "epilogue staging must fit one operand buffer");
   static_assert(NST + DI <= 63, "vmcnt immediate");
   __shared__ __align__(16) uint8_t lds[NS * STAGE];
 
   const int M = g.M, N = g.N, K = g.K;
-  uint16_t* __restrict__ out = static_cast<uint16_t*>(g.out);
+  OutT* __restrict__ out = static_cast<OutT*>(g.out);
   const int T = g.tiles_m * g.tiles_n;
   const int ntile = (T - int(blockIdx.x) + int(gridDim.x) - 1) / int(gridDim.x);
 
@@ -1076,6 +1083,8 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persist_kernel(GemmArgs g) {
         issue(cur, t + 2, b);
       else if (t + 2 == nt && more)
         issue(nxt, 0, b);  // the next tile's stage 0
+      else if (F32OUT && more)
+        issue(nxt, 1, b);  // the next tile's stage 1 (no output staging)
       __builtin_amdgcn_sched_barrier(0);
       // sub-step 0 of stage t + 1 (after the last stage: the next tile's
       // stage 0, landed at this barrier; stale and unused after the last tile)
@@ -1084,10 +1093,41 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persist_kernel(GemmArgs g) {
       interleave_mfma_lds<NP, 2 * (NF + MB), 0>();
     }
 
-    // ---- epilogue: stage through the last stage's buffer -------------------
     const int sb = (cb0 + nt - 1) & 1;
-    uint8_t* eps = lds + sb * STAGE + wave * (TMW * RB);
     const int nb = n0 + wn * TNW;
+    if constexpr (F32OUT) {
+      // ---- epilogue: 16-byte stores from the accumulators --------------------
+#pragma unroll
+      for (int i = 0; i < MB; ++i)
+#pragma unroll
+        for (int j = 0; j < NB; ++j)
+#pragma unroll
+          for (int gq = 0; gq < 4; ++gq) {
+            const int row = i * 32 + lr, col = j * 32 + gq * 8 + lg * 4;
+            float v[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const int r = gq * 4 + q;
+              v[q] = acc[0][j][i][r] * c0s + acc[1][j][i][r] * c1s;
+            }
+            if (g.bias) {
+#pragma unroll
+              for (int q = 0; q < 4; ++q) v[q] += g.bias[nb + col + q];
+            }
+            store4<float>(reinterpret_cast<float*>(out) + int64_t(m0 + wm * TMW + row) * g.ldo +
+                              nb + col,
+                          v[0], v[1], v[2], v[3]);
+          }
+      __builtin_amdgcn_sched_barrier(0);
+      zero_acc();
+      cb0 = sb ^ 1;
+      cur = nxt;
+      m0 = m1;
+      n0 = n1;
+      continue;
+    }
+    // ---- epilogue: stage through the last stage's buffer -------------------
+    uint8_t* eps = lds + sb * STAGE + wave * (TMW * RB);
 #pragma unroll
     for (int i = 0; i < MB; ++i)
 #pragma unroll
@@ -1113,7 +1153,7 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persist_kernel(GemmArgs g) {
     asm volatile("" ::: "memory");
     // the NST staged chunks of this lane, held in named registers (an array
     // here is kept in scratch memory across the barrier below)
-    static_assert(NST == 8, "eight store chunks per lane");
+    static_assert(F32OUT || NST == 8, "eight store chunks per lane");
     auto staged = [&](int s) {
       const int row = s * RPI + lane / CPR, cl = lane % CPR;
       return *reinterpret_cast<const uint4*>(eps + row * RB + ((cl ^ (row & (CPR - 1))) * 16));
@@ -1130,7 +1170,7 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persist_kernel(GemmArgs g) {
     __builtin_amdgcn_sched_barrier(0);
     auto put = [&](int s, const uint4& d) {
       const int row = s * RPI + lane / CPR, cl = lane % CPR;
-      uint16_t* o = out + int64_t(m0 + wm * TMW + row) * g.ldo + nb + cl * 8;
+      OutT* o = out + int64_t(m0 + wm * TMW + row) * g.ldo + nb + cl * 8;
       *reinterpret_cast<uint4*>(o) = d;
     };
     put(0, d0); put(1, d1); put(2, d2); put(3, d3);
@@ -1199,15 +1239,15 @@ int launch_gemm(GemmArgs ga, hipStream_t st) {
     } else if (small) {
       gemm_nt_dma_kernel<AF, BF, SPLIT, OutT, 4, 128, 64, SCALE, 2><<<grid, 256, 0, st>>>(ga);
     } else if constexpr (!(SCALE == 1 && SPLIT) && SCALE != 2) {
-      // more tiles than CUs, all of them full, bf16 out: one persistent
-      // workgroup per CU runs its tiles back to back
+      // more tiles than CUs, all of them full: one persistent workgroup
+      // per CU runs its tiles back to back
       bool persist = false;
-      if constexpr (SCALE == 0 && !SPLIT && std::is_same<OutT, uint16_t>::value) {
+      if constexpr (SCALE == 0 && !SPLIT && AF != kBF16) {
         persist = g_tile_policy != 4 && splits == 1 && int64_t(grid.x) > num_cus() &&
                   m % 256 == 0 && n % 128 == 0 && k % kSK == 0 && k > kSK && ga.ldo % 8 == 0 &&
                   (reinterpret_cast<uintptr_t>(ga.out) & 15) == 0;
         if (persist)
-          gemm_nt_persist_kernel<AF, BF><<<unsigned(num_cus()), 512, 0, st>>>(ga);
+          gemm_nt_persist_kernel<AF, BF, OutT><<<unsigned(num_cus()), 512, 0, st>>>(ga);
       }
       if (!persist)
         gemm_nt_dma_kernel<AF, BF, SPLIT, OutT, 8, 256, 128, SCALE, 2><<<grid, 512, 0, st>>>(ga);

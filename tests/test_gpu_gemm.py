@@ -169,18 +169,18 @@ def _kernel_names(fn):
 @pytest.mark.parametrize("M,N,K_", [(4096, 4096, 4096), (4352, 4096, 256), (8192, 4096, 1024),
                                     (2048, 8192, 512)])
 @pytest.mark.parametrize("afmt", [torch.float8_e4m3fn, torch.float8_e5m2])
-def test_persistent_dual_gemm_matches_one_workgroup_per_tile(dev, M, N, K_, afmt):
-    """More full 256x128 tiles than CUs with bf16 output runs one persistent
-    workgroup per CU over several tiles (4352 rows: some run three, K = 256:
-    two stages, the fewest it takes).  Each output accumulates in the same
-    K order as with one workgroup per tile, so the bf16 results, bias
-    included, are identical."""
-    print(f"persistent M={M} N={N} K={K_} {afmt}", flush=True)
+@pytest.mark.parametrize("od", [torch.bfloat16, torch.float32])
+def test_persistent_dual_gemm_matches_one_workgroup_per_tile(dev, M, N, K_, afmt, od):
+    """More full 256x128 tiles than CUs runs one persistent workgroup per CU
+    over several tiles (4352 rows: some run three, K = 256: two stages, the
+    fewest it takes), for bf16 and fp32 output.  Each output accumulates in
+    the same K order as with one workgroup per tile, so the results, bias
+    included, are identical bit for bit."""
+    print(f"persistent M={M} N={N} K={K_} {afmt} {od}", flush=True)
     a, sa = make_act((M, K_), 21, dev, afmt)
     h, l, ih, il = make_pair((N, K_), 22, dev)
     bias = torch.randn(N, generator=torch.Generator().manual_seed(23)).to(dev)
-    run = lambda: K.fused_dual_gemm_forward(a, h, l, sa, ih, il, bias=bias,
-                                            out_dtype=torch.bfloat16)
+    run = lambda: K.fused_dual_gemm_forward(a, h, l, sa, ih, il, bias=bias, out_dtype=od)
     names = _kernel_names(run)
     assert any("gemm_nt_persist_kernel" in n for n in names), names
     p = run()
@@ -190,7 +190,8 @@ def test_persistent_dual_gemm_matches_one_workgroup_per_tile(dev, M, N, K_, afmt
         q = run()
     finally:
         K.set_gemm_tile_policy("auto")
-    assert torch.equal(p.view(torch.int16), q.view(torch.int16))
+    iv = torch.int16 if od == torch.bfloat16 else torch.int32
+    assert torch.equal(p.view(iv), q.view(iv))
     if (M, N, K_) == (2048, 8192, 512):
         fmt = ofp8.E4M3 if afmt == torch.float8_e4m3fn else ofp8.E5M2
         ref = og.dual_gemm_nt(u8(a), fmt, u8(h), u8(l), sa.item(), ih.item(), il.item())
@@ -199,9 +200,9 @@ def test_persistent_dual_gemm_matches_one_workgroup_per_tile(dev, M, N, K_, afmt
 
 
 def test_persistent_launch_not_taken_for_partial_tiles(dev):
-    # edge tiles, a partial K stage or fp32 output keep one workgroup per tile
+    # edge tiles or a partial K stage keep one workgroup per tile
     for M, N, K_, od in [(4000, 4096, 1024, torch.bfloat16), (4096, 4096, 1040, torch.bfloat16),
-                         (4096, 4096, 1024, torch.float32)]:
+                         (4000, 4096, 1024, torch.float32), (4096, 4096, 1040, torch.float32)]:
         a, sa = make_act((M, K_), 24, dev)
         h, l, ih, il = make_pair((N, K_), 25, dev)
         names = _kernel_names(lambda: K.fused_dual_gemm_forward(a, h, l, sa, ih, il,
