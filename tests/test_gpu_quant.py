@@ -265,12 +265,18 @@ def test_block_dual_quantize_sentinel_and_no_ef(dev):
     assert np.array_equal(u8(h), hi) and np.array_equal(u8(l), lo)
 
 
-def test_block_dual_quantize_sr(dev):
+@pytest.mark.parametrize("bs", [32, 64, 128])
+@pytest.mark.parametrize("wdt", [torch.float32, torch.bfloat16])
+def test_block_dual_quantize_sr(dev, bs, wdt):
+    # fp32 weights run 8 elements per lane (one Philox call), bf16 weights 16
+    # (two calls); the segment spans 2..16 lanes across the block sizes
     g = torch.Generator().manual_seed(9)
-    W = torch.randn(64, 256, generator=g)
-    hi, lo_rtn, eh, el, _ = oq.block_dual_quantize(W.numpy(), 64)
-    wb = W.numpy().reshape(64, 4, 64)
-    deq_hi = oq.block_dequantize(hi, eh, 64).reshape(64, 4, 64)
+    W = torch.randn(64, 256, generator=g).to(wdt)
+    Wf = W.float().numpy()
+    nb = 256 // bs
+    hi, lo_rtn, eh, el, _ = oq.block_dual_quantize(Wf, bs)
+    wb = Wf.reshape(64, nb, bs)
+    deq_hi = oq.block_dequantize(hi, eh, bs).reshape(64, nb, bs)
     r = (wb - deq_hi).astype(np.float32)
     x = np.clip(r * (2.0 ** -el.T.astype(np.float64))[..., None], -448, 448).astype(np.float32).reshape(64, 256)
     rtn, other, frac, exact = oq.sr_candidates_block(x)
@@ -278,7 +284,7 @@ def test_block_dual_quantize_sr(dev):
     acc = np.zeros(x.shape)
     n = 200
     for i in range(n):
-        h, l, sh, sl = K.fused_dual_quantize_fp8(W.to(dev), 64, stochastic_lo=True, seed=77 + i)
+        h, l, sh, sl = K.fused_dual_quantize_fp8(W.to(dev), bs, stochastic_lo=True, seed=77 + i)
         assert np.array_equal(u8(h), hi) and np.array_equal(i8(sl), el)
         c = u8(l)
         assert np.all((c == rtn) | (c == other))
