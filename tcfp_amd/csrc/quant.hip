@@ -735,15 +735,21 @@ __global__ __launch_bounds__(kThreads) void dualq_hi_kernel(
 #pragma unroll
     for (int j = 0; j < 8; ++j) m = umax(m, absbits(v[j] - e4m3_to_f32(byte_of(code, j)) * inv_hi));
   };
-  int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x;
-  for (; i + stride < nvec; i += 2 * stride) {
+  // The grid-stride slabs are visited last to first.  Pass 1 (same grid)
+  // visited them first to last, and a vector is handled by the workgroup of
+  // the same index in both passes, i.e. on the same XCD (workgroup b runs on
+  // XCD b % 8), so the slabs pass 1 read last are still in that XCD's L2
+  // when this pass starts; pass 3 goes first to last again.
+  const int64_t i0 = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+  int64_t i = i0 < nvec ? i0 + ((nvec - 1 - i0) / stride) * stride : -1;
+  for (; i - stride >= i0; i -= 2 * stride) {
     float W[2][8], v[2][8];
     load_w8<InT, HAS_EF>(w, ef, i, W[0], v[0]);
-    load_w8<InT, HAS_EF>(w, ef, i + stride, W[1], v[1]);
+    load_w8<InT, HAS_EF>(w, ef, i - stride, W[1], v[1]);
     body(v[0], i);
-    body(v[1], i + stride);
+    body(v[1], i - stride);
   }
-  for (; i < nvec; i += stride) {
+  for (; i >= i0; i -= stride) {
     float W[8], v[8];
     load_w8<InT, HAS_EF>(w, ef, i, W, v);
     body(v, i);

@@ -291,10 +291,15 @@ def test_block_dual_quantize_sr(dev, bs, wdt):
         assert np.all(c[exact] == rtn[exact])
         acc += (c == other) & (other != rtn)
     m = ~exact & (other != rtn)
-    p = acc / n
-    assert abs(float((p[m] - frac[m]).mean())) < 0.01
-    # unbiased: E[deq(lo)] ~= residual
-    assert float(np.abs(p[m] - frac[m]).max()) < 0.2
+    assert m.sum() > 0
+    # unbiased (E[deq(lo)] = residual): the count of round-ups over all
+    # inexact elements matches the sum of their probabilities within 5
+    # binomial standard deviations (bf16 weights leave few inexact residuals,
+    # so the bound scales with how many there are), and no element strays far
+    f = frac[m].astype(np.float64)
+    z = (acc[m].sum() - n * f.sum()) / np.sqrt(max(n * (f * (1 - f)).sum(), 1e-12))
+    assert abs(z) < 5, (int(m.sum()), z)
+    assert float(np.abs(acc[m] / n - f).max()) < 0.2
 
 
 # ------------------------------------------------ quant + column sums (bias grad)
