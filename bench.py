@@ -231,8 +231,13 @@ def bench_dual_quant(iters=20):
     return out
 
 
-def bench_mlp(steps=100, time_iters=20, arms=("tcfp", "bf16")):
-    """1024 -> 4096 -> 1024 GELU MLP, 8192 tokens, MSE, AdamW 1e-3."""
+def bench_mlp(steps=100, time_iters=20, arms=("tcfp", "bf16", "fp32")):
+    """1024 -> 4096 -> 1024 GELU MLP, 8192 tokens, MSE, AdamW 1e-3.
+
+    Arms: TCFP-12 (both linears converted, per-tensor scales with EF), BF16
+    autocast (the target's baseline), and the same model in fp32 (the
+    reference harness's "BF16" baseline is an fp32 model,
+    benchmarks/benchmark_tcfp.py:482-516; context only)."""
     import torch
     import torch.nn as nn
 
@@ -250,13 +255,17 @@ def bench_mlp(steps=100, time_iters=20, arms=("tcfp", "bf16")):
             convert_to_tcfp(m, use_tensor_cores=True)
         return m
 
-    def run(tcfp):
-        m = make(tcfp)
+    xf = x.float()
+
+    def run(arm):
+        m = make(arm == "tcfp")
         opt = torch.optim.AdamW(m.parameters(), lr=1e-3)
 
         def step():
-            if tcfp:
+            if arm == "tcfp":
                 out = m(x)
+            elif arm == "fp32":
+                out = m(xf)
             else:
                 with torch.autocast("cuda", dtype=torch.bfloat16):
                     out = m(x)
@@ -275,15 +284,20 @@ def bench_mlp(steps=100, time_iters=20, arms=("tcfp", "bf16")):
 
     res = {"steps": steps}
     if "tcfp" in arms:
-        l_t, ms_t = run(True)
+        l_t, ms_t = run("tcfp")
         res.update({"tcfp_step_ms": ms_t, "loss_step1_tcfp": l_t[0],
                     f"loss_step{steps}_tcfp": l_t[-1]})
     if "bf16" in arms:
-        l_b, ms_b = run(False)
+        l_b, ms_b = run("bf16")
         res.update({"bf16_autocast_step_ms": ms_b, f"loss_step{steps}_bf16": l_b[-1]})
     if "tcfp" in arms and "bf16" in arms:
         res["speedup_vs_bf16"] = ms_b / ms_t
         res[f"loss_rel_diff_step{steps}"] = abs(l_t[-1] - l_b[-1]) / l_b[-1]
+    if "fp32" in arms:
+        l_f, ms_f = run("fp32")
+        res.update({"fp32_step_ms": ms_f, f"loss_step{steps}_fp32": l_f[-1]})
+        if "tcfp" in arms:
+            res["speedup_vs_fp32"] = ms_f / ms_t
     return res
 
 
@@ -472,8 +486,8 @@ def main():
                     default="all",
                     help="all (default) = headline + every secondary figure; the others run "
                          "one workload (for profiling)")
-    ap.add_argument("--arm", choices=("both", "tcfp", "bf16"), default="both",
-                    help="--part mlp: which model(s) to run")
+    ap.add_argument("--arm", choices=("both", "tcfp", "bf16", "fp32"), default="both",
+                    help="--part mlp: which model(s) to run (both = all three)")
     ap.add_argument("--skip-extras", action="store_true", help="same as --part gemm")
     args = ap.parse_args()
     if args.skip_extras:
@@ -490,7 +504,9 @@ def main():
         fn = {"quant": lambda: bench_dual_quant(), "block": lambda: bench_block_gemms(),
               "c5": lambda: bench_c5(),
               "mlp": lambda: bench_mlp(
-                  steps=args.steps, arms=("tcfp", "bf16") if args.arm == "both" else (args.arm,)), "copy": lambda: bench_copy(args.steps)}
+                  steps=args.steps,
+                  arms=("tcfp", "bf16", "fp32") if args.arm == "both" else (args.arm,)),
+              "copy": lambda: bench_copy(args.steps)}
         log(f"[bench] part {args.part}")
         print(json.dumps({"part": args.part, **fn[args.part]()}), flush=True)
         return
