@@ -231,38 +231,42 @@ def bench_dual_quant(iters=20):
     return out
 
 
-def bench_mlp(steps=100, time_iters=20, arms=("tcfp", "bf16", "fp32")):
+def bench_mlp(steps=100, time_iters=20, arms=("tcfp", "tcfp_fused", "bf16", "fp32")):
     """1024 -> 4096 -> 1024 GELU MLP, 8192 tokens, MSE, AdamW 1e-3.
 
-    Arms: TCFP-12 (both linears converted, per-tensor scales with EF), BF16
-    autocast (the target's baseline), and the same model in fp32 (the
+    Arms: TCFP-12 (both linears converted, per-tensor scales with EF: the
+    drop-in TCFPLinear path), the same with the GELU fused into the
+    quantisation around it (``fuse_tcfp_mlp``; bit-identical results),
+    BF16 autocast (the target's baseline), and the same model in fp32 (the
     reference harness's "BF16" baseline is an fp32 model,
     benchmarks/benchmark_tcfp.py:482-516; context only)."""
     import torch
     import torch.nn as nn
 
-    from tcfp_amd.nn import convert_to_tcfp
+    from tcfp_amd.nn import convert_to_tcfp, fuse_tcfp_mlp
 
     dev = torch.device("cuda:0")
     g = torch.Generator().manual_seed(0)
     x = torch.randn(8192, 1024, generator=g).bfloat16().to(dev)
     y = torch.randn(8192, 1024, generator=g).to(dev)
 
-    def make(tcfp):
+    def make(arm):
         torch.manual_seed(1)
         m = nn.Sequential(nn.Linear(1024, 4096), nn.GELU(), nn.Linear(4096, 1024)).to(dev)
-        if tcfp:
+        if arm.startswith("tcfp"):
             convert_to_tcfp(m, use_tensor_cores=True)
+        if arm == "tcfp_fused":
+            m = fuse_tcfp_mlp(m)
         return m
 
     xf = x.float()
 
     def run(arm):
-        m = make(arm == "tcfp")
+        m = make(arm)
         opt = torch.optim.AdamW(m.parameters(), lr=1e-3)
 
         def step():
-            if arm == "tcfp":
+            if arm.startswith("tcfp"):
                 out = m(x)
             elif arm == "fp32":
                 out = m(xf)
@@ -290,9 +294,16 @@ def bench_mlp(steps=100, time_iters=20, arms=("tcfp", "bf16", "fp32")):
     if "bf16" in arms:
         l_b, ms_b = run("bf16")
         res.update({"bf16_autocast_step_ms": ms_b, f"loss_step{steps}_bf16": l_b[-1]})
+    if "tcfp_fused" in arms:
+        l_u, ms_u = run("tcfp_fused")
+        res.update({"tcfp_fused_step_ms": ms_u, f"loss_step{steps}_tcfp_fused": l_u[-1]})
+        if "tcfp" in arms:
+            res["fused_losses_identical"] = l_u == l_t
     if "tcfp" in arms and "bf16" in arms:
         res["speedup_vs_bf16"] = ms_b / ms_t
         res[f"loss_rel_diff_step{steps}"] = abs(l_t[-1] - l_b[-1]) / l_b[-1]
+    if "tcfp_fused" in arms and "bf16" in arms:
+        res["speedup_fused_vs_bf16"] = ms_b / ms_u
     if "fp32" in arms:
         l_f, ms_f = run("fp32")
         res.update({"fp32_step_ms": ms_f, f"loss_step{steps}_fp32": l_f[-1]})
@@ -486,8 +497,8 @@ def main():
                     default="all",
                     help="all (default) = headline + every secondary figure; the others run "
                          "one workload (for profiling)")
-    ap.add_argument("--arm", choices=("both", "tcfp", "bf16", "fp32"), default="both",
-                    help="--part mlp: which model(s) to run (both = all three)")
+    ap.add_argument("--arm", choices=("both", "tcfp", "tcfp_fused", "bf16", "fp32"),
+                    default="both", help="--part mlp: which model(s) to run (both = all)")
     ap.add_argument("--skip-extras", action="store_true", help="same as --part gemm")
     args = ap.parse_args()
     if args.skip_extras:
@@ -505,7 +516,8 @@ def main():
               "c5": lambda: bench_c5(),
               "mlp": lambda: bench_mlp(
                   steps=args.steps,
-                  arms=("tcfp", "bf16", "fp32") if args.arm == "both" else (args.arm,)),
+                  arms=("tcfp", "tcfp_fused", "bf16", "fp32") if args.arm == "both"
+                  else (args.arm,)),
               "copy": lambda: bench_copy(args.steps)}
         log(f"[bench] part {args.part}")
         print(json.dumps({"part": args.part, **fn[args.part]()}), flush=True)

@@ -89,6 +89,32 @@ int tcfp_quantize_per_tensor_colsum(const void* x, int x_dtype, int64_t rows, in
                                     float* col_sum, void* workspace, void* colsum_ws,
                                     size_t colsum_ws_bytes, void* stream);
 
+/* Producer-fused per-tensor quantisation across a GELU (erf form) between
+ * two TCFP-12 layers.  No single reference function: it replaces the
+ * model's torch GELU followed by the next layer's to_fp8_e4m3 of its input
+ * (tcfp/nn/__init__.py:390 on the GELU output).  h [rows, cols] fp32 is the
+ * first layer's output; act = gelu(h) is written (fp32, as torch's GELU
+ * computes it bit for bit) in the same pass that takes its amax, then act
+ * is quantised by the tcfp_quantize_per_tensor rule (q, optional
+ * transposed q_t, inv_out).  h, act 16-byte aligned. */
+int tcfp_gelu_quantize_per_tensor(const float* h, int64_t rows, int64_t cols, int fp8_fmt,
+                                  float* act, uint8_t* q, uint8_t* q_t, float* inv_out,
+                                  void* workspace, void* stream);
+
+/* The backward counterpart: grad = dGELU/dh * dy (fp32, bit for bit as
+ * torch's GELU backward) is written in the same pass that takes its amax and
+ * its column sums, then quantised as tcfp_quantize_per_tensor_colsum does
+ * (tcfp/nn/__init__.py:494 and :558 applied to the GELU's input gradient,
+ * which the reference gets from torch's GELU backward).  dy, h, grad
+ * [rows, cols] fp32, cols % 8 == 0; colsum_ws as for
+ * tcfp_quantize_per_tensor_colsum. */
+int tcfp_gelu_backward_quantize_per_tensor_colsum(const float* dy, const float* h, int64_t rows,
+                                                  int64_t cols, int fp8_fmt, float* grad,
+                                                  uint8_t* q, uint8_t* q_t, float* inv_out,
+                                                  float* col_sum, void* workspace,
+                                                  void* colsum_ws, size_t colsum_ws_bytes,
+                                                  void* stream);
+
 /* Per-tensor dual quantisation with optional error feedback.
  * Three launches (amax; W_hi + residual amax; W_lo + EF + transposed
  * codes), each re-reading W and EF.  Optionally (tcfp_dual_quant_set_path)

@@ -15,6 +15,6 @@ from .core import (  # noqa: F401
     to_fp8_e4m3_nf_aware,
     to_fp8_e5m2,
 )
-from .nn import TCFPLinear, convert_to_tcfp  # noqa: F401
+from .nn import TCFPLinear, TCFPMLP, convert_to_tcfp, fuse_tcfp_mlp  # noqa: F401
 
 __version__ = "0.1.0"

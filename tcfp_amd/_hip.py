@@ -35,6 +35,12 @@ _SIGNATURES = {
     "tcfp_quantize_per_tensor_colsum": [_c_void_p, _i32, _i64, _i64, _i32, _c_void_p, _c_void_p,
                                         _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                                         ctypes.c_size_t, _c_void_p],
+    "tcfp_gelu_quantize_per_tensor": [_c_void_p, _i64, _i64, _i32, _c_void_p, _c_void_p,
+                                      _c_void_p, _c_void_p, _c_void_p, _c_void_p],
+    "tcfp_gelu_backward_quantize_per_tensor_colsum": [_c_void_p, _c_void_p, _i64, _i64, _i32,
+                                                      _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+                                                      _c_void_p, _c_void_p, _c_void_p,
+                                                      ctypes.c_size_t, _c_void_p],
     "tcfp_dual_quantize_per_tensor": [_c_void_p, _i32, _i64, _i64, _c_void_p, _i32, _i32, _u64,
                                       _u64, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                                       _c_void_p, _c_void_p, _c_void_p, _c_void_p],

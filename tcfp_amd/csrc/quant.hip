@@ -20,10 +20,10 @@ namespace {
 // partial max |x| (as float bits: monotone for non-negative floats, and any
 // NaN sorts above +inf, so torch.max's NaN propagation is kept) into its own
 // slot of a workspace array with a plain store.  The kernel that consumes the
-// scale re-reduces every slot in every workgroup (at most 4 KiB, served from
+// scale re-reduces every slot in every workgroup (at most 8 KiB, served from
 // L2), so the two launches need nothing but stream order: no atomics, no
 // fences, no zero-at-rest requirement, and the result is deterministic.
-constexpr int kMaxParts = 1024;
+constexpr int kMaxParts = 2048;
 struct PartWs {
   uint32_t a[kMaxParts];  // partial amax of the first reduction
   uint32_t b[kMaxParts];  // partial amax of the residual (dual quantisation)
@@ -166,6 +166,20 @@ TCFP_DEV uint32_t block_umax_all(uint32_t m, uint32_t* red) {
   m = red[0];
 #pragma unroll
   for (int i = 1; i < kThreads / 64; ++i) m = umax(m, red[i]);
+  return m;
+}
+
+// Workgroup-wide uint max over NT threads (a multiple of 64), returned to
+// every thread; `red` holds NT / 64 words.
+template <int NT>
+TCFP_DEV uint32_t block_umax_nt(uint32_t m, uint32_t* red) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) m = umax(m, uint32_t(__shfl_xor(int(m), o, 64)));
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+  __syncthreads();
+  m = red[0];
+#pragma unroll
+  for (int i = 1; i < NT / 64; ++i) m = umax(m, red[i]);
   return m;
 }
 
@@ -375,16 +389,76 @@ __global__ __launch_bounds__(kThreads) void amax_part_kernel(const InT* __restri
   }
 }
 
+// ---- GELU producers ---------------------------------------------------------
+// GELU (erf form) exactly as torch evaluates it on fp32 tensors: forward
+// x * 0.5 * (1 + erf(x * sqrt(1/2))), every operation rounded on its own
+// (this file is built without contraction); backward
+// dy * (cdf + x * pdf) with cdf = 0.5 * (1 + erf(x * sqrt(1/2))),
+// pdf = exp(-0.5 * x * x) * (2/sqrt(pi) * sqrt(1/2) * 0.5), the last
+// product and sum as one fused multiply-add.  The constants are the
+// double-precision products rounded once to fp32.  A GPU test holds both
+// bitwise equal to torch.nn.functional.gelu and its gradient.
+constexpr float kSqrtHalf = float(0.70710678118654752440);
+constexpr float kGeluBeta = float(1.12837916709551257390 * 0.70710678118654752440 * 0.5);
+TCFP_DEV float gelu_f32(float x) { return x * 0.5f * (1.0f + erff(x * kSqrtHalf)); }
+TCFP_DEV float gelu_bwd_f32(float x, float dy) {
+  const float cdf = 0.5f * (1.0f + erff(x * kSqrtHalf));
+  const float pdf = expf(-0.5f * x * x) * kGeluBeta;
+  return dy * __builtin_fmaf(x, pdf, cdf);
+}
+
+// act = gelu(h) (written out) and this workgroup's partial max |act| ->
+// part[blockIdx.x], the producer of a per-tensor quantisation of act.
+// 512-thread workgroups: the partial count is capped, and the erf makes the
+// pass VALU-heavy, so each CU needs eight waves per SIMD to overlap the
+// arithmetic with the memory traffic.
+constexpr int kGeluThreads = 512;
+__global__ __launch_bounds__(kGeluThreads) void gelu_amax_kernel(const float* __restrict__ h,
+                                                                 int64_t n, float* __restrict__ act,
+                                                                 uint32_t* __restrict__ part) {
+  __shared__ uint32_t red[kGeluThreads / 64];
+  uint32_t m = 0;
+  const int64_t nvec = n >> 3;
+  const int64_t stride = int64_t(gridDim.x) * kGeluThreads;
+  auto body = [&](const float v[8], int64_t i) {
+    float g[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) g[j] = gelu_f32(v[j]);
+    store8(act + i * 8, g);
+    // the max after the stores, over all eight (measured faster than
+    // folding each value in as it is produced)
+    const uint32_t m01 = umax(absbits(g[0]), absbits(g[1])), m23 = umax(absbits(g[2]), absbits(g[3]));
+    const uint32_t m45 = umax(absbits(g[4]), absbits(g[5])), m67 = umax(absbits(g[6]), absbits(g[7]));
+    m = umax(m, umax(umax(m01, m23), umax(m45, m67)));
+  };
+  // one vector per step: the erf branches per element, and deeper unrolling
+  // measured slower (52 vs 41 us for 32 Mi elements with four in flight)
+  for (int64_t i = int64_t(blockIdx.x) * kGeluThreads + threadIdx.x; i < nvec; i += stride) {
+    float v[8];
+    load8(h + i * 8, v);
+    body(v, i);
+  }
+  for (int64_t t = nvec * 8 + int64_t(blockIdx.x) * kGeluThreads + threadIdx.x; t < n;
+       t += stride) {
+    const float g = gelu_f32(h[t]);
+    act[t] = g;
+    m = umax(m, absbits(g));
+  }
+  m = block_umax_nt<kGeluThreads>(m, red);
+  if (threadIdx.x == 0) part[blockIdx.x] = m;
+}
+
 // ---- amax + column sums (the bias gradient) in one pass ------------------
-// Geometry for x [rows, cols], cols % 8 == 0: a workgroup covers NVW
-// 8-column vectors (a power of two <= 256) with RL = 256 / NVW row lanes,
+// Geometry for x [rows, cols], cols % 8 == 0: a 512-thread workgroup covers
+// NVW 8-column vectors (a power of two <= 256) with RL = 512 / NVW row lanes,
 // over one group of consecutive rows; it writes the partial max and the
 // partial column sums of its row group to cs_part[rg, cols].
 struct ColsumGeom {
   int nvw, rl, cb_count, rg_count, rpg;
 };
 
-constexpr int kMaxRowGroups = 256;
+constexpr int kMaxRowGroups = 512;
+constexpr int kColsumThreads = 512;
 
 inline ColsumGeom colsum_geom(int64_t rows, int64_t cols) {
   ColsumGeom g;
@@ -392,7 +466,7 @@ inline ColsumGeom colsum_geom(int64_t rows, int64_t cols) {
   int nvw = 1;
   while (nvw * 2 <= 256 && nvw * 2 <= nv) nvw *= 2;
   g.nvw = nvw;
-  g.rl = 256 / nvw;
+  g.rl = kColsumThreads / nvw;
   g.cb_count = int((nv + nvw - 1) / nvw);
   int64_t rg = (rows + 4 * g.rl - 1) / (4 * g.rl);  // >= 4 rows per lane
   const int64_t cap = std::min<int64_t>(kMaxRowGroups, kMaxParts / g.cb_count);
@@ -403,12 +477,15 @@ inline ColsumGeom colsum_geom(int64_t rows, int64_t cols) {
   return g;
 }
 
-template <typename InT>
-__global__ __launch_bounds__(kThreads) void amax_colsum_kernel(
+// GELU_BWD: x is the gradient dy of a GELU's output, h its input; the pass
+// works on (and writes to act) the gradient of the input, gelu_bwd(h, dy).
+template <typename InT, bool GELU_BWD = false>
+__global__ __launch_bounds__(kColsumThreads) void amax_colsum_kernel(
     const InT* __restrict__ x, int64_t rows, int64_t cols, ColsumGeom geo,
-    uint32_t* __restrict__ part, float* __restrict__ cs_part) {
-  __shared__ uint32_t red[kThreads / 64];
-  __shared__ float csum[kThreads * 8];
+    uint32_t* __restrict__ part, float* __restrict__ cs_part, const float* __restrict__ h = nullptr,
+    float* __restrict__ act = nullptr) {
+  __shared__ uint32_t red[kColsumThreads / 64];
+  __shared__ float csum[kColsumThreads * 8];
   const int cb = blockIdx.x % geo.cb_count, rg = blockIdx.x / geo.cb_count;
   const int lc = threadIdx.x % geo.nvw, lr = threadIdx.x / geo.nvw;
   const int64_t cv = int64_t(cb) * geo.nvw + lc;
@@ -419,12 +496,27 @@ __global__ __launch_bounds__(kThreads) void amax_colsum_kernel(
   uint32_t m = 0;
   if (cvalid) {
     int64_t r = r_beg + lr;
-    for (; r + 3 * geo.rl < r_end; r += 4 * geo.rl) {
-      float v[4][8];
+    // GELU_BWD: v = gelu_bwd(h, dy), written to act at the same offset
+    auto produce = [&](int64_t off, float* v) {
+      if constexpr (GELU_BWD) {
+        float hv[8];
+        load8(h + off, hv);
 #pragma unroll
-      for (int u = 0; u < 4; ++u) load8(x + (r + u * geo.rl) * cols + cv * 8, v[u]);
+        for (int j = 0; j < 8; ++j) v[j] = gelu_bwd_f32(hv[j], v[j]);
+        store8(act + off, v);
+      }
+    };
+    // rows in flight per lane: 4, or 1 with the GELU producer (two inputs
+    // and its branching erf / exp); each lane still adds its rows in row order
+    constexpr int U = GELU_BWD ? 1 : 4;
+    for (; r + (U - 1) * geo.rl < r_end; r += U * geo.rl) {
+      float v[U][8];
 #pragma unroll
-      for (int u = 0; u < 4; ++u)
+      for (int u = 0; u < U; ++u) load8(x + (r + u * geo.rl) * cols + cv * 8, v[u]);
+#pragma unroll
+      for (int u = 0; u < U; ++u) produce((r + u * geo.rl) * cols + cv * 8, v[u]);
+#pragma unroll
+      for (int u = 0; u < U; ++u)
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
           acc[j] += v[u][j];
@@ -434,6 +526,7 @@ __global__ __launch_bounds__(kThreads) void amax_colsum_kernel(
     for (; r < r_end; r += geo.rl) {
       float v[8];
       load8(x + r * cols + cv * 8, v);
+      produce(r * cols + cv * 8, v);
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         acc[j] += v[j];
@@ -443,7 +536,7 @@ __global__ __launch_bounds__(kThreads) void amax_colsum_kernel(
   }
 #pragma unroll
   for (int j = 0; j < 8; ++j) csum[threadIdx.x * 8 + j] = acc[j];
-  m = block_umax_all(m, red);  // includes a barrier: csum is complete
+  m = block_umax_nt<kColsumThreads>(m, red);  // includes a barrier: csum is complete
   if (threadIdx.x == 0) part[blockIdx.x] = m;
   if (lr == 0 && cvalid) {
     float o[8];
@@ -1818,10 +1911,12 @@ int tcfp_workspace_error(const void* workspace, int* flag, void* stream) {
 
 namespace {
 
+// pre_g > 0: a producer kernel already wrote pre_g partial maxima of x to
+// the workspace (no amax pass here; col_sum must be null).
 int quantize_impl(const void* x, int x_dtype, int64_t rows, int64_t cols, int fp8_fmt,
                   const float* scale_in, uint8_t* q, uint8_t* q_t, float* scale_out,
                   float* inv_out, void* workspace, float* col_sum, float* cs_ws,
-                  hipStream_t st) {
+                  hipStream_t st, int pre_g = 0) {
   if (rows < 0 || cols < 0) return TCFP_ERR_SHAPE;
   if (x_dtype != TCFP_DTYPE_F32 && x_dtype != TCFP_DTYPE_BF16) return TCFP_ERR_DTYPE;
   if (fp8_fmt != TCFP_FP8_E4M3 && fp8_fmt != TCFP_FP8_E5M2) return TCFP_ERR_DTYPE;
@@ -1838,10 +1933,10 @@ int quantize_impl(const void* x, int x_dtype, int64_t rows, int64_t cols, int fp
     geo = colsum_geom(rows, cols);
     g = geo.cb_count * geo.rg_count;
     if (bf)
-      amax_colsum_kernel<uint16_t><<<g, kThreads, 0, st>>>(static_cast<const uint16_t*>(x), rows,
+      amax_colsum_kernel<uint16_t><<<g, kColsumThreads, 0, st>>>(static_cast<const uint16_t*>(x), rows,
                                                            cols, geo, part, cs_ws);
     else
-      amax_colsum_kernel<float><<<g, kThreads, 0, st>>>(static_cast<const float*>(x), rows, cols,
+      amax_colsum_kernel<float><<<g, kColsumThreads, 0, st>>>(static_cast<const float*>(x), rows, cols,
                                                         geo, part, cs_ws);
     colsum_finalize_kernel<<<unsigned((cols + 31) / 32), kThreads, 0, st>>>(cs_ws, geo.rg_count,
                                                                             cols, col_sum);
@@ -1850,7 +1945,9 @@ int quantize_impl(const void* x, int x_dtype, int64_t rows, int64_t cols, int fp
     colsum_finalize_kernel<<<unsigned((cols + 31) / 32), kThreads, 0, st>>>(cs_ws, 0, cols,
                                                                             col_sum);
   }
-  if (!col_sum && !scale_in) {
+  if (pre_g > 0) {
+    g = pre_g;
+  } else if (!col_sum && !scale_in) {
     g = parts_for((n + 7) / 8);
     if (bf)
       amax_part_kernel<uint16_t, false, false><<<g, kThreads, 0, st>>>(
@@ -1928,6 +2025,61 @@ int tcfp_quantize_per_tensor_colsum(const void* x, int x_dtype, int64_t rows, in
   return quantize_impl(x, x_dtype, rows, cols, fp8_fmt, nullptr, q, q_t, nullptr, inv_out,
                        workspace, col_sum, static_cast<float*>(colsum_ws),
                        static_cast<hipStream_t>(stream));
+}
+
+int tcfp_gelu_quantize_per_tensor(const float* h, int64_t rows, int64_t cols, int fp8_fmt,
+                                  float* act, uint8_t* q, uint8_t* q_t, float* inv_out,
+                                  void* workspace, void* stream) {
+  if (rows < 0 || cols < 0) return TCFP_ERR_SHAPE;
+  if (fp8_fmt != TCFP_FP8_E4M3 && fp8_fmt != TCFP_FP8_E5M2) return TCFP_ERR_DTYPE;
+  if (!workspace) return TCFP_ERR_WORKSPACE;
+  if (!aligned16(h) || !aligned16(act) || !inv_out) return TCFP_ERR_ALIGN;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t n = rows * cols;
+  // up to kMaxParts workgroups (measured: 2048 x 512 threads 42 us, 1024 x
+  // 512 threads 44.5 us for 32 Mi elements)
+  const int g = int(std::max<int64_t>(
+      1, std::min<int64_t>(kMaxParts, ((n + 7) / 8 + 2 * kGeluThreads - 1) / (2 * kGeluThreads))));
+  gelu_amax_kernel<<<g, kGeluThreads, 0, st>>>(h, n, act, static_cast<PartWs*>(workspace)->a);
+  return quantize_impl(act, TCFP_DTYPE_F32, rows, cols, fp8_fmt, nullptr, q, q_t, nullptr,
+                       inv_out, workspace, nullptr, nullptr, st, g);
+}
+
+int tcfp_gelu_backward_quantize_per_tensor_colsum(const float* dy, const float* h, int64_t rows,
+                                                  int64_t cols, int fp8_fmt, float* grad,
+                                                  uint8_t* q, uint8_t* q_t, float* inv_out,
+                                                  float* col_sum, void* workspace,
+                                                  void* colsum_ws, size_t colsum_ws_bytes,
+                                                  void* stream) {
+  if (rows < 0 || cols < 0 || cols % 8 != 0) return TCFP_ERR_SHAPE;
+  if (cols / 8 > int64_t(kMaxParts) * 256) return TCFP_ERR_SHAPE;  // partial slots
+  if (fp8_fmt != TCFP_FP8_E4M3 && fp8_fmt != TCFP_FP8_E5M2) return TCFP_ERR_DTYPE;
+  if (!col_sum) return TCFP_ERR_SHAPE;
+  if (!workspace) return TCFP_ERR_WORKSPACE;
+  if (!aligned16(dy) || !aligned16(h) || !aligned16(grad) || !inv_out) return TCFP_ERR_ALIGN;
+  const int64_t n = rows * cols;
+  if (n > 0 && (!colsum_ws || colsum_ws_bytes < tcfp_colsum_workspace_bytes(rows, cols)))
+    return TCFP_ERR_WORKSPACE;
+  if (n > 0 && (!aligned16(colsum_ws) || !aligned16(col_sum))) return TCFP_ERR_ALIGN;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  float* cs_ws = static_cast<float*>(colsum_ws);
+  int g = 0;
+  if (n > 0) {
+    const ColsumGeom geo = colsum_geom(rows, cols);
+    g = geo.cb_count * geo.rg_count;
+    amax_colsum_kernel<float, true><<<g, kColsumThreads, 0, st>>>(
+        dy, rows, cols, geo, static_cast<PartWs*>(workspace)->a, cs_ws, h, grad);
+    colsum_finalize_kernel<<<unsigned((cols + 31) / 32), kThreads, 0, st>>>(cs_ws, geo.rg_count,
+                                                                            cols, col_sum);
+  } else if (cols > 0) {
+    // no rows: the column sums are zero
+    colsum_finalize_kernel<<<unsigned((cols + 31) / 32), kThreads, 0, st>>>(cs_ws, 0, cols,
+                                                                            col_sum);
+  }
+  // an empty tensor has no partials: quantize_impl's own (empty) amax pass
+  // publishes the clamped scale, as for any empty input
+  return quantize_impl(grad, TCFP_DTYPE_F32, rows, cols, fp8_fmt, nullptr, q, q_t, nullptr,
+                       inv_out, workspace, nullptr, nullptr, st, g);
 }
 
 }  // extern "C"

@@ -148,6 +148,94 @@ def quantize_per_tensor_colsum(
     return q, inv, cs
 
 
+def gelu_quantize_per_tensor(
+    h: torch.Tensor,
+    fp8_dtype: torch.dtype = torch.float8_e4m3fn,
+    transpose: bool = False,
+    return_act: bool = False,
+):
+    """``quantize_per_tensor(torch.nn.functional.gelu(h))`` with the GELU
+    fused into the amax pass (the producer of the next layer's activation
+    quantisation, ``tcfp/nn/__init__.py:390`` applied to a GELU output).
+
+    ``h`` is fp32.  ``gelu(h)`` is computed as torch computes it (erf form,
+    bit for bit), written once, and quantised with the per-tensor amax rule.
+    Returns ``(q, inv)``, plus ``q_t`` when ``transpose``, plus the fp32
+    activation when ``return_act``.
+    """
+    dev = _hip.require_gpu(h)
+    if h.dtype != torch.float32:
+        raise AssertionError(f"h must be float32, got {h.dtype}")
+    hc = h if h.is_contiguous() else h.contiguous()
+    cols = hc.shape[-1] if hc.dim() > 0 else 1
+    rows = hc.numel() // cols if cols else 0
+    act = torch.empty(h.shape, dtype=torch.float32, device=dev)
+    q = torch.empty(h.shape, dtype=fp8_dtype, device=dev)
+    q_t = torch.empty((cols, rows), dtype=fp8_dtype, device=dev) if transpose else None
+    inv = torch.empty(1, dtype=torch.float32, device=dev)
+    check(
+        _hip.lib().tcfp_gelu_quantize_per_tensor(
+            ptr(hc), rows, cols, _fmt(fp8_dtype), ptr(act), ptr(q), ptr(q_t), ptr(inv),
+            ptr(_hip.workspace(dev)), _hip.stream_of(dev),
+        ),
+        "gelu_quantize_per_tensor",
+    )
+    out = (q, inv)
+    if transpose:
+        out = out + (q_t,)
+    if return_act:
+        out = out + (act,)
+    return out
+
+
+def gelu_backward_quantize_per_tensor_colsum(
+    dy: torch.Tensor,
+    h: torch.Tensor,
+    fp8_dtype: torch.dtype = torch.float8_e5m2,
+    transpose: bool = False,
+    return_grad: bool = False,
+):
+    """The gradient of a GELU's input, ``g = gelu'(h) * dy`` (as torch's GELU
+    backward computes it, bit for bit), quantised per tensor with its column
+    sums from the same pass (``quantize_per_tensor_colsum(g)``: the E5M2
+    gradient quantisation at ``tcfp/nn/__init__.py:494`` and the bias
+    gradient ``grad_2d.sum(0)`` at ``:558``).
+
+    ``dy`` and ``h`` are fp32 of one shape, last dim divisible by 8.  Returns
+    ``(q, inv, col_sum)`` or, with ``transpose``, ``(q, inv, q_t, col_sum)``;
+    ``return_grad`` appends ``g``.
+    """
+    dev = _hip.require_gpu(dy, h)
+    if dy.dtype != torch.float32 or h.dtype != torch.float32:
+        raise AssertionError("dy and h must be float32")
+    if dy.shape != h.shape:
+        raise AssertionError(f"shape mismatch: dy {tuple(dy.shape)} vs h {tuple(h.shape)}")
+    dc = dy if dy.is_contiguous() else dy.contiguous()
+    hc = h if h.is_contiguous() else h.contiguous()
+    cols = dc.shape[-1]
+    rows = dc.numel() // cols if cols else 0
+    if cols % 8 != 0:
+        raise ValueError(f"column count ({cols}) must be divisible by 8")
+    g = torch.empty(dy.shape, dtype=torch.float32, device=dev)
+    q = torch.empty(dy.shape, dtype=fp8_dtype, device=dev)
+    q_t = torch.empty((cols, rows), dtype=fp8_dtype, device=dev) if transpose else None
+    inv = torch.empty(1, dtype=torch.float32, device=dev)
+    cs = torch.empty(cols, dtype=torch.float32, device=dev)
+    nbytes = int(_hip.lib().tcfp_colsum_workspace_bytes(rows, cols))
+    cws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=dev)
+    check(
+        _hip.lib().tcfp_gelu_backward_quantize_per_tensor_colsum(
+            ptr(dc), ptr(hc), rows, cols, _fmt(fp8_dtype), ptr(g), ptr(q), ptr(q_t), ptr(inv),
+            ptr(cs), ptr(_hip.workspace(dev)), ptr(cws), nbytes, _hip.stream_of(dev),
+        ),
+        "gelu_backward_quantize_per_tensor_colsum",
+    )
+    out = (q, inv, q_t, cs) if transpose else (q, inv, cs)
+    if return_grad:
+        out = out + (g,)
+    return out
+
+
 def dual_quantize_per_tensor(
     weight: torch.Tensor,
     error_buf: torch.Tensor | None = None,

@@ -37,9 +37,12 @@ from ..core import DEFAULT_BLOCK_SIZE, ErrorFeedbackState, TCFPMode
 
 __all__ = [
     "TCFPLinear",
+    "TCFPMLP",
     "convert_to_tcfp",
+    "fuse_tcfp_mlp",
     "_TCFP12TensorCoreFunction",
     "_TCFP12BlockScaledFunction",
+    "_TCFP12FusedMLPFunction",
 ]
 
 
@@ -405,12 +408,7 @@ class TCFPLinear(nn.Module):
         if self._warmup_remaining > 0:
             self._warmup_remaining -= 1
             return F.linear(x, self.weight, self.bias)
-        # EF guard (reference :983-994): update only when the weight changed
-        # since the last update and autograd is recording.
-        ver = self.weight._version
-        update_ef = ver != self._last_weight_version and torch.is_grad_enabled()
-        if update_ef:
-            self._last_weight_version = ver
+        update_ef = self._ef_update_flag()
         if self.scale_block_size is not None:
             return _TCFP12BlockScaledFunction.apply(
                 x, self.weight, self.bias, self.scale_block_size, self.hp_grad_weight,
@@ -421,6 +419,25 @@ class TCFPLinear(nn.Module):
             self.stochastic_rounding, self.hp_grad_weight, self._error_state,
             self._param_name, self.delayed_scaling, self.use_fused_kernel, self.use_cuda_ext,
             self.abd, self.srr, update_ef,
+        )
+
+    def _ef_update_flag(self) -> bool:
+        """EF guard (reference :983-994): update only when the weight changed
+        since the last update and autograd is recording."""
+        ver = self.weight._version
+        update_ef = ver != self._last_weight_version and torch.is_grad_enabled()
+        if update_ef:
+            self._last_weight_version = ver
+        return update_ef
+
+    def _plain_per_tensor(self) -> bool:
+        """True when forward takes the default per-tensor path (EF or not)
+        with no option the fused MLP path leaves out."""
+        return (
+            self.scale_block_size is None and not self.delayed_scaling
+            and not self.nf_aware_scaling and not self.srr and not self.abd
+            and not self.hp_grad_weight and not self._bf16_fallback
+            and self._warmup_remaining == 0
         )
 
     def extra_repr(self) -> str:
@@ -457,6 +474,175 @@ class TCFPLinear(nn.Module):
         if self._bf16_fallback:
             parts.append("bf16_fallback=True")
         return ", ".join(parts)
+
+
+class _TCFP12FusedMLPFunction(torch.autograd.Function):
+    """``TCFPLinear -> GELU -> TCFPLinear`` (both per-tensor, EF as each layer
+    has it) as one autograd node, with the GELU fused into the
+    quantisation on either side of it.
+
+    No reference counterpart: the reference runs ``torch.nn.functional.gelu``
+    between two ``_TCFP12TensorCoreFunction`` calls
+    (``tcfp/nn/__init__.py:325-566``).  Every step here is that sequence's
+    step -- same kernels, same operands, same order of rounding -- except
+    that ``gelu`` is evaluated inside the pass that takes the amax of its
+    output (forward) or of its input gradient (backward, with the bias
+    column sums), and both are evaluated as torch evaluates them, bit for
+    bit.  The outputs, gradients and EF updates are therefore identical to
+    the unfused sequence; the hidden activation and its gradient are each
+    read once less.
+    """
+
+    @staticmethod
+    def forward(  # noqa: PLR0913
+        ctx, x, w1, b1, w2, b2, st1, name1, st2, name2, update_ef1, update_ef2,
+    ):
+        need_dx, need_dw1, need_db1, need_dw2, need_db2 = ctx.needs_input_grad[:5]
+        need_h = need_dx or need_dw1 or need_db1  # a gradient flows into layer 1
+
+        # layer 1 (reference nn:343-425 with the default options)
+        ef1 = _ef_buffer(st1, name1, w1)
+        res = K.dual_quantize_per_tensor(w1, ef1, update_ef=update_ef1, transposed=need_dx)
+        w1_hi, w1_lo, ih1, il1, w1_hi_t, w1_lo_t = res if need_dx else (*res, None, None)
+        input_shape = x.shape
+        x2d = _flatten(x)
+        if need_dw1:
+            a1, a1_inv, a1_t = K.quantize_per_tensor(x2d, transpose=True)
+        else:
+            (a1, a1_inv), a1_t = K.quantize_per_tensor(x2d), None
+        h = K.fused_dual_gemm_forward(a1, w1_hi, w1_lo, a1_inv, ih1, il1, bias=b1)
+
+        # GELU fused into layer 2's activation quantisation (nn:390 on gelu(h))
+        if need_dw2:
+            a2, a2_inv, a2_t = K.gelu_quantize_per_tensor(h, transpose=True)
+        else:
+            (a2, a2_inv), a2_t = K.gelu_quantize_per_tensor(h), None
+
+        # layer 2
+        ef2 = _ef_buffer(st2, name2, w2)
+        res = K.dual_quantize_per_tensor(w2, ef2, update_ef=update_ef2, transposed=need_h)
+        w2_hi, w2_lo, ih2, il2, w2_hi_t, w2_lo_t = res if need_h else (*res, None, None)
+        out = K.fused_dual_gemm_forward(a2, w2_hi, w2_lo, a2_inv, ih2, il2, bias=b2)
+
+        ctx.input_shape = input_shape
+        ctx.has_b1, ctx.has_b2 = b1 is not None, b2 is not None
+        ctx.save_for_backward(
+            a1_t, a1_inv, w1_hi_t, w1_lo_t, ih1, il1,
+            h if need_h else None, a2_t, a2_inv, w2_hi_t, w2_lo_t, ih2, il2,
+        )
+        return out.reshape(*input_shape[:-1], out.shape[-1])
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        (a1_t, a1_inv, w1_hi_t, w1_lo_t, ih1, il1,
+         h, a2_t, a2_inv, w2_hi_t, w2_lo_t, ih2, il2) = ctx.saved_tensors
+        need_dx, need_dw1, need_db1, need_dw2, need_db2 = ctx.needs_input_grad[:5]
+        need_h = need_dx or need_dw1 or need_db1
+        g2 = _flatten(grad_output)
+        if not g2.is_contiguous():
+            g2 = g2.contiguous()
+        grad_x = dw1 = db1 = dw2 = db2 = None
+
+        # layer 2 (nn:462-566): E5M2 grad + bias sums, dual dgrad, FP8 wgrad
+        fuse_db2 = need_db2 and ctx.has_b2 and g2.shape[-1] % 8 == 0
+        dh = None
+        if need_h or need_dw2:
+            if fuse_db2:
+                res = K.quantize_per_tensor_colsum(g2, torch.float8_e5m2, transpose=need_dw2)
+                db2 = res[-1].to(g2.dtype)
+                res = res[:-1]
+            else:
+                res = K.quantize_per_tensor(g2, torch.float8_e5m2, transpose=need_dw2)
+            (q2, g2_inv, q2_t) = res if need_dw2 else (*res, None)
+            if need_h:
+                dh = K._dual_gemm(q2, w2_hi_t, w2_lo_t, g2_inv, ih2, il2, None, torch.float32)
+            if need_dw2:
+                dw2 = K.fp8_gemm_nt(q2_t, a2_t, g2_inv, a2_inv)
+        if need_db2 and ctx.has_b2 and db2 is None:
+            db2 = g2.sum(dim=0)
+
+        # GELU backward fused into layer 1's gradient quantisation (its
+        # amax and bias column sums come from the same pass); layer 1
+        if need_h:
+            res = K.gelu_backward_quantize_per_tensor_colsum(
+                dh, h, torch.float8_e5m2, transpose=need_dw1,
+            )
+            q1, g1_inv, q1_t, cs1 = res if need_dw1 else (res[0], res[1], None, res[2])
+            if need_db1 and ctx.has_b1:
+                db1 = cs1.to(dh.dtype)
+            if need_dx:
+                grad_x = K._dual_gemm(q1, w1_hi_t, w1_lo_t, g1_inv, ih1, il1, None,
+                                      torch.float32).reshape(ctx.input_shape)
+            if need_dw1:
+                dw1 = K.fp8_gemm_nt(q1_t, a1_t, g1_inv, a1_inv)
+        return (grad_x, dw1, db1, dw2, db2) + (None,) * 6
+
+
+class TCFPMLP(nn.Sequential):
+    """``TCFPLinear -> nn.GELU() -> TCFPLinear`` with the GELU fused into the
+    quantisation around it (``_TCFP12FusedMLPFunction``).
+
+    A ``nn.Sequential`` of exactly those three children (same parameter
+    names as the plain sequence, so state dicts and optimizers carry over).
+    When both layers take the default per-tensor path, the GELU is the exact
+    (``approximate="none"``) form, the hidden size is a multiple of 8 and the
+    token count a multiple of 16, forward runs the fused Function, whose
+    results equal the plain sequence's bit for bit; otherwise it runs the
+    plain sequence.  Each layer keeps its own EF state and EF guard.
+    """
+
+    def _fusable(self, x: torch.Tensor) -> bool:
+        if len(self) != 3:
+            return False
+        fc1, act, fc2 = self[0], self[1], self[2]
+        if not (isinstance(fc1, TCFPLinear) and isinstance(fc2, TCFPLinear)):
+            return False
+        if not isinstance(act, nn.GELU) or act.approximate != "none":
+            return False
+        if not (fc1._plain_per_tensor() and fc2._plain_per_tensor()):
+            return False
+        if fc1.out_features != fc2.in_features or fc1.out_features % 8 != 0:
+            return False
+        if x.device.type != "cuda" or x.dtype not in (torch.float32, torch.bfloat16):
+            return False
+        if x.dim() == 0 or x.shape[-1] != fc1.in_features:
+            return False
+        tokens = x.numel() // x.shape[-1]
+        return tokens % 16 == 0 and tokens > 0
+
+    @torch.compiler.disable
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if not self._fusable(x):
+            return super().forward(x)
+        fc1, fc2 = self[0], self[2]
+        u1 = fc1._ef_update_flag()
+        u2 = fc2._ef_update_flag()
+        return _TCFP12FusedMLPFunction.apply(
+            x, fc1.weight, fc1.bias, fc2.weight, fc2.bias,
+            fc1._error_state, fc1._param_name, fc2._error_state, fc2._param_name, u1, u2,
+        )
+
+
+def _is_mlp_triplet(m: nn.Module) -> bool:
+    return (
+        type(m) is nn.Sequential and len(m) == 3
+        and isinstance(m[0], TCFPLinear) and isinstance(m[2], TCFPLinear)
+        and isinstance(m[1], nn.GELU) and m[1].approximate == "none"
+    )
+
+
+def fuse_tcfp_mlp(model: nn.Module) -> nn.Module:
+    """Turn every ``nn.Sequential(TCFPLinear, nn.GELU(), TCFPLinear)`` in
+    ``model`` into a ``TCFPMLP`` holding the same three modules (run it after
+    ``convert_to_tcfp``).  Children are replaced in place; if ``model`` itself
+    is such a sequence, the new ``TCFPMLP`` is returned, else ``model``."""
+    if _is_mlp_triplet(model):
+        return TCFPMLP(*model)
+    for name, child in model.named_children():
+        new = fuse_tcfp_mlp(child)
+        if new is not child:
+            setattr(model, name, new)
+    return model
 
 
 def convert_to_tcfp(

@@ -1,0 +1,198 @@
+"""GPU tests of the producer-fused GELU quantisation and the fused MLP.
+
+The fused path claims bit-identity, so every check here is ``torch.equal``
+on raw bits:
+
+* the GELU (erf form) and its gradient equal torch's on the GPU;
+* the fused quantisation of gelu(h) / of the GELU's input gradient equals
+  the plain per-tensor quantisation (codes, inverse scales, transposed codes,
+  bias column sums) of torch's gelu(h) / gradient;
+* ``TCFPMLP`` (TCFPLinear -> GELU -> TCFPLinear as one autograd node) gives
+  the outputs, gradients and EF buffers of the plain sequence over several
+  AdamW steps.
+"""
+import copy
+
+import pytest
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from tcfp_amd import kernels as K
+from tcfp_amd.nn import TCFPLinear, TCFPMLP, convert_to_tcfp, fuse_tcfp_mlp
+
+pytestmark = pytest.mark.gpu
+
+
+def bits(t):
+    t = t.contiguous()
+    return t.view(torch.int32) if t.dtype == torch.float32 else t.view(torch.uint8)
+
+
+def same_scalar(a, b):
+    a, b = float(a.item()), float(b.item())
+    return a == b or (a != a and b != b)
+
+
+def _specials(t):
+    v = torch.tensor([0.0, -0.0, -0.7518, 10.0, -10.0, 1e-30, 3.5, -3.5])
+    n = min(v.numel(), t.numel())
+    t.view(-1)[:n] = v[:n]
+    return t
+
+
+@pytest.mark.parametrize("shape", [(8192, 4096), (300, 208), (33, 130), (5, 3), (1, 8), (0, 64)])
+def test_gelu_quantize_equals_torch_gelu_then_quantize(dev, shape):
+    print(f"gelu quant {shape}", flush=True)
+    g = torch.Generator().manual_seed(shape[0] * 7 + shape[1])
+    h = _specials(torch.randn(shape, generator=g) * 3).to(dev)
+    q, inv, q_t, act = K.gelu_quantize_per_tensor(h, transpose=True, return_act=True)
+    ref = F.gelu(h)
+    assert torch.equal(bits(act), bits(ref))
+    q2, inv2, q2_t = K.quantize_per_tensor(ref, transpose=True)
+    assert torch.equal(bits(q), bits(q2)) and torch.equal(bits(q_t), bits(q2_t))
+    assert same_scalar(inv, inv2)
+
+
+@pytest.mark.parametrize("shape", [(8192, 4096), (300, 208), (8, 8), (1000, 24), (0, 64)])
+def test_gelu_backward_quantize_colsum_equals_torch(dev, shape):
+    print(f"gelu bwd quant {shape}", flush=True)
+    g = torch.Generator().manual_seed(shape[0] + 11 * shape[1])
+    h = _specials(torch.randn(shape, generator=g) * 3).to(dev)
+    dy = (torch.randn(shape, generator=g) * 1e-3).to(dev)
+    hr = h.clone().requires_grad_(True)
+    F.gelu(hr).backward(dy)
+    ref = hr.grad
+    q, inv, q_t, cs, gr = K.gelu_backward_quantize_per_tensor_colsum(
+        dy, h, transpose=True, return_grad=True)
+    assert torch.equal(bits(gr), bits(ref))
+    q2, inv2, q2_t, cs2 = K.quantize_per_tensor_colsum(ref, torch.float8_e5m2, transpose=True)
+    assert torch.equal(bits(q), bits(q2)) and torch.equal(bits(q_t), bits(q2_t))
+    assert same_scalar(inv, inv2)
+    assert torch.equal(bits(cs), bits(cs2))
+
+
+def test_gelu_quantize_nan_propagates(dev):
+    h = torch.randn(64, 64, device=dev)
+    h[3, 5] = float("nan")
+    q, inv = K.gelu_quantize_per_tensor(h)
+    assert torch.isnan(inv).all()
+
+
+def test_gelu_wrappers_reject_bad_inputs(dev):
+    with pytest.raises(AssertionError, match="float32"):
+        K.gelu_quantize_per_tensor(torch.randn(8, 8, device=dev).bfloat16())
+    with pytest.raises(AssertionError, match="shape"):
+        K.gelu_backward_quantize_per_tensor_colsum(torch.randn(8, 8, device=dev),
+                                                   torch.randn(8, 16, device=dev))
+    with pytest.raises(ValueError, match="divisible"):
+        K.gelu_backward_quantize_per_tensor_colsum(torch.randn(8, 12, device=dev),
+                                                   torch.randn(8, 12, device=dev))
+
+
+def _pair(dev, d_in, d_h, d_out, bias=True, seed=0, **kw):
+    torch.manual_seed(seed)
+    base = nn.Sequential(nn.Linear(d_in, d_h, bias=bias), nn.GELU(),
+                         nn.Linear(d_h, d_out, bias=bias)).to(dev)
+    plain = convert_to_tcfp(copy.deepcopy(base), use_tensor_cores=True, **kw)
+    fused = fuse_tcfp_mlp(convert_to_tcfp(copy.deepcopy(base), use_tensor_cores=True, **kw))
+    assert type(plain) is nn.Sequential and isinstance(fused, TCFPMLP)
+    assert list(plain.state_dict()) == list(fused.state_dict())
+    return plain, fused
+
+
+def _kernel_names(fn):
+    from torch.profiler import ProfilerActivity, profile
+
+    with profile(activities=[ProfilerActivity.CUDA]) as prof:
+        fn()
+        torch.cuda.synchronize()
+    return [e.name for e in prof.events()]
+
+
+def _run_steps(model, x, y, steps, x_grad):
+    opt = torch.optim.AdamW(model.parameters(), lr=1e-3)
+    rec = []
+    for _ in range(steps):
+        xx = x.clone().requires_grad_(x_grad)
+        out = model(xx)
+        loss = (out.float() - y).square().mean()
+        opt.zero_grad(set_to_none=True)
+        loss.backward()
+        r = [out.detach().clone()] + [p.grad.clone() for p in model.parameters()]
+        if x_grad:
+            r.append(xx.grad.clone())
+        rec.append(r)
+        opt.step()
+    efs = [m._error_state._buffers[m._param_name].clone()
+           for m in model.modules() if isinstance(m, TCFPLinear)]
+    return rec, efs
+
+
+@pytest.mark.parametrize("bias", [True, False])
+@pytest.mark.parametrize("x_grad", [False, True])
+@pytest.mark.parametrize("xdtype", [torch.bfloat16, torch.float32])
+def test_fused_mlp_bit_identical_to_plain_sequence(dev, bias, x_grad, xdtype):
+    print(f"fused mlp bias={bias} x_grad={x_grad} {xdtype}", flush=True)
+    plain, fused = _pair(dev, 256, 1024, 384, bias)
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(4, 128, 256, generator=g).to(xdtype).to(dev)
+    y = torch.randn(4, 128, 384, generator=g).to(dev)
+    with torch.no_grad():  # no EF update: the runs below start from the same state
+        names = _kernel_names(lambda: fused(x))
+    assert any("gelu_amax_kernel" in n for n in names), names
+    rp, ep = _run_steps(plain, x, y, 3, x_grad)
+    rf, ef = _run_steps(fused, x, y, 3, x_grad)
+    for step, (a, b) in enumerate(zip(rp, rf)):
+        assert len(a) == len(b)
+        for i, (u, v) in enumerate(zip(a, b)):
+            assert u.dtype == v.dtype and u.shape == v.shape, (step, i)
+            assert torch.equal(u.float().view(torch.int32), v.float().view(torch.int32)), (step, i)
+    for u, v in zip(ep, ef):
+        assert torch.equal(bits(u), bits(v))
+
+
+def test_fused_mlp_c4_shape_one_step(dev):
+    # BASELINE configs[3] shape: 8192 tokens, 1024 -> 4096 -> 1024
+    plain, fused = _pair(dev, 1024, 4096, 1024, seed=3)
+    g = torch.Generator().manual_seed(6)
+    x = torch.randn(8192, 1024, generator=g).bfloat16().to(dev)
+    y = torch.randn(8192, 1024, generator=g).to(dev)
+    rp, ep = _run_steps(plain, x, y, 2, False)
+    rf, ef = _run_steps(fused, x, y, 2, False)
+    for a, b in zip(rp, rf):
+        for u, v in zip(a, b):
+            assert torch.equal(bits(u.float()), bits(v.float()))
+    for u, v in zip(ep, ef):
+        assert torch.equal(bits(u), bits(v))
+
+
+def test_fused_mlp_falls_back_to_plain_sequence(dev):
+    # options the fused path leaves out, a tanh GELU or a ragged token count
+    # run the plain sequence (same results, no fused kernel)
+    cases = [dict(delayed_scaling=True), dict(hp_grad_weight=True)]
+    for kw in cases:
+        plain, fused = _pair(dev, 128, 256, 128, **kw)
+        x = torch.randn(64, 128, device=dev)
+        names = _kernel_names(lambda: fused(x))
+        plain(x)  # the same number of calls on both (EF and scaling state advance per call)
+        assert not any("gelu_amax_kernel" in n for n in names), kw
+        assert torch.equal(bits(fused(x).detach()), bits(plain(x).detach())), kw
+    plain, fused = _pair(dev, 128, 256, 128)
+    assert not any("gelu_amax_kernel" in n
+                   for n in _kernel_names(lambda: fused(torch.randn(40, 128, device=dev))))
+    fused[1] = nn.GELU(approximate="tanh")
+    assert not any("gelu_amax_kernel" in n
+                   for n in _kernel_names(lambda: fused(torch.randn(64, 128, device=dev))))
+
+
+def test_fuse_tcfp_mlp_replaces_nested_sequences(dev):
+    torch.manual_seed(0)
+    model = nn.Module()
+    model.blocks = nn.ModuleList([
+        nn.Sequential(nn.Linear(64, 256), nn.GELU(), nn.Linear(256, 64)) for _ in range(2)])
+    model.head = nn.Sequential(nn.Linear(64, 64), nn.ReLU(), nn.Linear(64, 64))
+    model = fuse_tcfp_mlp(convert_to_tcfp(model.to(dev), use_tensor_cores=True,
+                                          skip_patterns=("none",)))
+    assert all(isinstance(b, TCFPMLP) for b in model.blocks)
+    assert type(model.head) is nn.Sequential
