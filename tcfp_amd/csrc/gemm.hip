@@ -392,9 +392,14 @@ struct GemmArgs {
 // NS = LDS stages in flight (2, or 4 for the small tile when one
 // workgroup per CU is resident): the DMA of stage t + NS is issued once
 // every wave has read stage t, so it has NS - 1 stages of MFMA time to land.
-template <int AF, int BF, bool SPLIT, typename OutT, int NW, int BM, int BN, int SCALE, int NS>
+// F32BS (SCALE 2 only): log2 of the block size, fixed per instantiation so
+// that each block size compiles to one fold schedule.
+template <int AF, int BF, bool SPLIT, typename OutT, int NW, int BM, int BN, int SCALE, int NS,
+          int F32BS = 0>
 __global__ __launch_bounds__(NW * 64, (NW == 4 && NS == 2 && BM == 128 ? 2 : 1)) void gemm_nt_dma_kernel(
     GemmArgs g) {
+  static_assert((SCALE == 2) == (F32BS != 0), "fp32 block scales fix the block size");
+  constexpr int f32_bsh = F32BS;
   constexpr int WM = NW / 2;        // wave rows
   constexpr int TMW = BM / WM;      // activation rows per wave
   constexpr int MB = TMW / 32;      // 32-row m-blocks per wave
@@ -501,7 +506,7 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && NS == 2 && BM == 128 ? 2 : 1))
   }
   const uint32_t sc_lds =
       uint32_t(reinterpret_cast<uintptr_t>((TCFP_LDS uint8_t*)lds)) + uint32_t(NS * STAGE);
-  const int nkb = SCALE == 2 ? (K >> g.bs_shift) : 0;
+  const int nkb = SCALE == 2 ? (K >> f32_bsh) : 0;
 
   // DMA of stage t (K columns t*128 ..) into buffer t & 1.  Stages past the
   // end are issued as all-out-of-range loads (zeros into a buffer nobody
@@ -517,8 +522,8 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && NS == 2 && BM == 128 ? 2 : 1))
       dma16(rsrc, (!live || (last && c * 16 >= krem)) ? kOob : voff[i], soff, dst + i * 1024);
     }
     if constexpr (SCALE == 2) {
-      if (live && wave < (kSK >> g.bs_shift)) {
-        const int kb = min(((t * kSK) >> g.bs_shift) + wave, nkb - 1);
+      if (live && wave < (kSK >> f32_bsh)) {
+        const int kb = min(((t * kSK) >> f32_bsh) + wave, nkb - 1);
         gdma16(sc_src + int64_t(kb) * sc_ld, sc_lds + uint32_t(t % 3) * kScB + uint32_t(wave) * 1024);
       }
     }
@@ -741,14 +746,14 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && NS == 2 && BM == 128 ? 2 : 1))
             }
         }
     };
-    const int bsh = g.bs_shift;
+    constexpr int bsh = f32_bsh;
     auto substep = [&](const v8i* f, int t, int h) {
-      if (bsh == 5) {
+      if constexpr (bsh == 5) {
         mfma_p(f, std::true_type{}, lg == 0 ? 127 : 0);
         fold(t, 2 * h);
         mfma_p(f, std::true_type{}, lg == 1 ? 127 : 0);
         fold(t, 2 * h + 1);
-      } else if (bsh == 6) {
+      } else if constexpr (bsh == 6) {
         mfma_p(f, std::true_type{}, 127);
         fold(t, h);
       } else if (h == 0) {
@@ -1237,7 +1242,16 @@ int launch_gemm(GemmArgs ga, hipStream_t st) {
           gemm_nt_dma_kernel<AF, BF, SPLIT, OutT, 4, 128, 64, SCALE, 4><<<grid, 256, 0, st>>>(ga);
       }
     } else if (small) {
-      gemm_nt_dma_kernel<AF, BF, SPLIT, OutT, 4, 128, 64, SCALE, 2><<<grid, 256, 0, st>>>(ga);
+      if constexpr (SCALE == 2) {
+        if (ga.bs_shift == 5)
+          gemm_nt_dma_kernel<AF, BF, SPLIT, OutT, 4, 128, 64, SCALE, 2, 5><<<grid, 256, 0, st>>>(ga);
+        else if (ga.bs_shift == 6)
+          gemm_nt_dma_kernel<AF, BF, SPLIT, OutT, 4, 128, 64, SCALE, 2, 6><<<grid, 256, 0, st>>>(ga);
+        else
+          gemm_nt_dma_kernel<AF, BF, SPLIT, OutT, 4, 128, 64, SCALE, 2, 7><<<grid, 256, 0, st>>>(ga);
+      } else {
+        gemm_nt_dma_kernel<AF, BF, SPLIT, OutT, 4, 128, 64, SCALE, 2><<<grid, 256, 0, st>>>(ga);
+      }
     } else if constexpr (!(SCALE == 1 && SPLIT) && SCALE != 2) {
       // more tiles than CUs, all of them full: one persistent workgroup
       // per CU runs its tiles back to back
