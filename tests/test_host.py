@@ -219,3 +219,26 @@ def test_error_feedback_state_delayed_methods_follow_the_oracle():
                                         np.float32(1e-12))), step
         assert validate == (step == 0 or (step + 1) % 3 == 0)
         W = W * 1.1
+
+
+def test_fuse_tcfp_mlp_structure_and_cpu_fallback():
+    from tcfp_amd.nn import TCFPMLP, fuse_tcfp_mlp
+
+    torch.manual_seed(0)
+    seq = nn.Sequential(nn.Linear(64, 256), nn.GELU(), nn.Linear(256, 64))
+    keys = list(seq.state_dict())
+    conv = convert_to_tcfp(seq, use_tensor_cores=True)
+    fused = fuse_tcfp_mlp(conv)
+    assert isinstance(fused, TCFPMLP) and list(fused.state_dict()) == keys
+    assert fused[0] is conv[0] and fused[2] is conv[2]  # the same modules, shared parameters
+    # a CPU input is not fusable: the plain sequence runs and raises as
+    # TCFPLinear does without a GPU
+    assert not fused._fusable(torch.randn(16, 64))
+    with pytest.raises(RuntimeError):
+        fused(torch.randn(16, 64))
+    # nested blocks are replaced in place; other sequences are left alone
+    model = nn.Module()
+    model.mlp = nn.Sequential(nn.Linear(64, 128), nn.GELU(), nn.Linear(128, 64))
+    model.other = nn.Sequential(nn.Linear(64, 64), nn.GELU(approximate="tanh"), nn.Linear(64, 64))
+    out = fuse_tcfp_mlp(convert_to_tcfp(model, use_tensor_cores=True, skip_patterns=("none",)))
+    assert out is model and isinstance(model.mlp, TCFPMLP) and type(model.other) is nn.Sequential
