@@ -131,6 +131,23 @@ def bench_comparators(t, iters=20):
     ms = event_time_ms(bf16, iters, stream)
     res["bf16_matmul_ms"] = ms
     res["bf16_matmul_tflops"] = 2 * n**3 / (ms * 1e-3) / 1e12
+
+    # Diagnostic, not a result: the same dual GEMM on all-zero operands
+    # (no bit toggles in the MFMA datapath, so the least power per FLOP)
+    # against C2's data, back to back in this process.  The gap is what
+    # the board's power limit costs the real operands.
+    from tcfp_amd import kernels as K
+
+    az, hz, lz = torch.zeros_like(a), torch.zeros_like(h), torch.zeros_like(l)
+
+    def dual(x, y, z):
+        return lambda: K.fused_dual_gemm_forward(x, y, z, sa, ih, il, out_dtype=torch.bfloat16)
+    for tag, args in (("c2_data", (a, h, l)), ("zero_operands", (az, hz, lz))):
+        f = dual(*args)
+        f()
+        ms = event_time_ms(f, 4 * iters, stream)
+        res[f"dual_{tag}_ms"] = ms
+        res[f"dual_{tag}_tflops"] = 4 * n**3 / (ms * 1e-3) / 1e12
     return res
 
 
