@@ -117,6 +117,32 @@ def test_per_tensor_empty(dev):
     assert q.shape == (0, 16)
 
 
+def test_per_tensor_quant_beyond_int32_elements(dev):
+    # 2^31 + 32768 bf16 elements (4.3 GB): element offsets past 2^31 must
+    # be addressed with 64-bit arithmetic in the amax, flat and transposing
+    # passes.  The tensor's maximum sits in its last element, so a wrapped
+    # index would lose it; codes are checked against the oracle on rows at
+    # the start, across the 2^31 boundary and at the end.
+    rows, cols = 65537, 32768
+    print(f"per-tensor quant {rows}x{cols} bf16", flush=True)
+    g = torch.Generator(device=dev).manual_seed(21)
+    x = torch.randn(rows, cols, generator=g, device=dev, dtype=torch.bfloat16)
+    x[-1, -1] = 1000.0
+    q, inv, qt, s = K.quantize_per_tensor(x, transpose=True, return_scale=True)
+    scale = oq.per_tensor_scale(np.array([1000.0], np.float32), "bf16")
+    assert s.item() == float(scale) and inv.item() == float(np.float32(1) / scale)
+    for r0 in (0, 40000, rows - 2):
+        xs = x[r0:r0 + 2].float().cpu().numpy()
+        codes, _, _ = oq.to_fp8_per_tensor(xs, "bf16", scale=scale)
+        assert np.array_equal(u8(q[r0:r0 + 2]), codes), r0
+        assert np.array_equal(u8(qt[:, r0:r0 + 2]), codes.T), r0
+    # the flat pass (no transposed copy) writes the same codes
+    q2, inv2 = K.quantize_per_tensor(x)
+    assert torch.equal(q2.view(torch.uint8), q.view(torch.uint8)) and torch.equal(inv2, inv)
+    del x, q, qt, q2
+    torch.cuda.empty_cache()
+
+
 def test_workspace_contents_do_not_matter(dev):
     """The partial-maximum slots of the reduction workspace are scratch:
     whatever they hold before a call (here all-ones bytes) changes no output.
