@@ -1733,7 +1733,9 @@ __global__ __launch_bounds__(kThreads) void transpose_u8_kernel(const uint8_t* _
                                                                 int64_t rows, int64_t cols,
                                                                 uint8_t* __restrict__ dst) {
   __shared__ uint8_t tile[64][64 + 4];
-  const int64_t r0 = int64_t(blockIdx.y) * 64, c0 = int64_t(blockIdx.x) * 64;
+  // one workgroup per 64 x 64 tile, tiles numbered row-major on a 1-D grid
+  const int64_t tiles_c = (cols + 63) / 64;
+  const int64_t r0 = int64_t(blockIdx.x) / tiles_c * 64, c0 = int64_t(blockIdx.x) % tiles_c * 64;
   const int t = threadIdx.x;
   const int lr = t >> 2, seg = t & 3;
   const int64_t r = r0 + lr;
@@ -1751,6 +1753,15 @@ __global__ __launch_bounds__(kThreads) void transpose_u8_kernel(const uint8_t* _
       if (rr < rows) dst[c * rows + rr] = tile[seg * 16 + b][lr];
     }
   }
+}
+
+// Launches transpose_u8_kernel over src [rows, cols] -> dst [cols, rows].
+int launch_transpose_u8(const uint8_t* src, int64_t rows, int64_t cols, uint8_t* dst,
+                        hipStream_t st) {
+  const int64_t tiles = ((rows + 63) / 64) * ((cols + 63) / 64);
+  if (tiles > INT32_MAX) return TCFP_ERR_SHAPE;
+  if (tiles > 0) transpose_u8_kernel<<<unsigned(tiles), kThreads, 0, st>>>(src, rows, cols, dst);
+  return TCFP_OK;
 }
 
 // ===========================================================================
@@ -1985,8 +1996,8 @@ int quantize_impl(const void* x, int x_dtype, int64_t rows, int64_t cols, int fp
   }
 #undef TCFP_QF
   if (q_t && n > 0) {
-    const dim3 grid(unsigned((cols + 63) / 64), unsigned((rows + 63) / 64));
-    transpose_u8_kernel<<<grid, kThreads, 0, st>>>(q, rows, cols, q_t);
+    const int rc = launch_transpose_u8(q, rows, cols, q_t, st);
+    if (rc != TCFP_OK) return rc;
   }
   return launch_status();
 }
@@ -2194,9 +2205,8 @@ int dual_quantize_impl(const void* w, int w_dtype, int64_t n, int64_t k, float* 
 #undef TCFP_DQ
 #undef TCFP_LO
   if (!tiled && total > 0 && (w_hi_t || w_lo_t)) {
-    const dim3 grid(unsigned((k + 63) / 64), unsigned((n + 63) / 64));
-    if (w_hi_t) transpose_u8_kernel<<<grid, kThreads, 0, st>>>(w_hi, n, k, w_hi_t);
-    if (w_lo_t) transpose_u8_kernel<<<grid, kThreads, 0, st>>>(w_lo, n, k, w_lo_t);
+    if (w_hi_t && launch_transpose_u8(w_hi, n, k, w_hi_t, st) != TCFP_OK) return TCFP_ERR_SHAPE;
+    if (w_lo_t && launch_transpose_u8(w_lo, n, k, w_lo_t, st) != TCFP_OK) return TCFP_ERR_SHAPE;
   }
   return launch_status();
 }
@@ -2282,6 +2292,7 @@ int block_quantize_impl(const void* x, int x_dtype, int64_t m, int64_t k, int bl
   if (fp8_fmt != TCFP_FP8_E4M3 && fp8_fmt != TCFP_FP8_E5M2) return TCFP_ERR_DTYPE;
   if (!aligned16(x) || !aligned16(q)) return TCFP_ERR_ALIGN;
   if (m == 0 || k == 0) return TCFP_OK;
+  if (k / block > 65535 || m > INT32_MAX) return TCFP_ERR_SHAPE;  // grid limits
   const unsigned kbs = unsigned(k / block);
 #define TCFP_BQ(T, F, B)                                                                    \
   do {                                                                                      \
@@ -2318,6 +2329,7 @@ int block_dual_quantize_impl(const void* w, int w_dtype, int64_t n, int64_t k, i
   if (!aligned16(w) || !aligned16(w_hi) || !aligned16(w_lo) || (ef && !aligned16(ef)))
     return TCFP_ERR_ALIGN;
   if (n == 0 || k == 0) return TCFP_OK;
+  if (k / block > 65535 || n > INT32_MAX) return TCFP_ERR_SHAPE;  // grid limits
   const unsigned kbs = unsigned(k / block);
   const uint32_t k0 = uint32_t(seed), k1 = uint32_t(seed >> 32);
   const uint32_t o0 = uint32_t(offset), o1 = uint32_t(offset >> 32);
@@ -2413,10 +2425,8 @@ int tcfp_transpose_u8(const uint8_t* src, int64_t rows, int64_t cols, uint8_t* d
                       void* stream) {
   if (rows < 0 || cols < 0) return TCFP_ERR_SHAPE;
   if (rows == 0 || cols == 0) return TCFP_OK;
-  dim3 grid(unsigned((cols + 63) / 64), unsigned((rows + 63) / 64));
-  transpose_u8_kernel<<<grid, kThreads, 0, static_cast<hipStream_t>(stream)>>>(src, rows, cols,
-                                                                               dst);
-  return launch_status();
+  const int rc = launch_transpose_u8(src, rows, cols, dst, static_cast<hipStream_t>(stream));
+  return rc != TCFP_OK ? rc : launch_status();
 }
 
 int tcfp_selftest_fp8_cvt(uint32_t lo_bits, uint32_t hi_bits, int fp8_fmt,

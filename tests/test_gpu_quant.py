@@ -143,6 +143,18 @@ def test_per_tensor_quant_beyond_int32_elements(dev):
     torch.cuda.empty_cache()
 
 
+def test_per_tensor_transposed_copy_of_tall_ragged_tensor(dev):
+    # cols % 8 != 0 takes the flat pass and the 64 x 64 byte transpose;
+    # 4194400 rows are more 64-row tiles than a grid's y dimension holds
+    rows, cols = 4194400, 5
+    g = torch.Generator().manual_seed(23)
+    x = torch.randn(rows, cols, generator=g).bfloat16()
+    codes, inv_o, _ = oq.to_fp8_per_tensor(x.float().numpy(), "bf16")
+    q, inv, qt = K.quantize_per_tensor(x.to(dev), transpose=True)
+    assert np.array_equal(u8(q), codes) and inv.item() == float(inv_o)
+    assert np.array_equal(u8(qt), codes.T)
+
+
 def test_workspace_contents_do_not_matter(dev):
     """The partial-maximum slots of the reduction workspace are scratch:
     whatever they hold before a call (here all-ones bytes) changes no output.
