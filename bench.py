@@ -438,8 +438,13 @@ def bench_c5(steps=50, time_iters=10):
                                  / res["bf16"]["loss_last"])
     # scale-up layer
     x = torch.randn(8192, 4096, generator=g).bfloat16().to(dev)
+    from tcfp_amd.nn import set_block_dgrad
+
+    # block64_srr_fp8_dgrad: the same layer with the opt-in FP8 block dgrad
     for arm, kw in (("block64_srr", dict(scale_block_size=64, srr=True)),
+                    ("block64_srr_fp8_dgrad", dict(scale_block_size=64, srr=True)),
                     ("block64_ef", dict(scale_block_size=64)), ("bf16", None)):
+        set_block_dgrad("fp8" if arm.endswith("fp8_dgrad") else "exact")
         torch.manual_seed(2)
         m = nn.Sequential(nn.Linear(4096, 16384), nn.GELU(), nn.Linear(16384, 4096)).to(dev)
         if kw is not None:
@@ -461,6 +466,7 @@ def bench_c5(steps=50, time_iters=10):
                                  "resident_MB": base / 1e6}
         del m
         torch.cuda.empty_cache()
+    set_block_dgrad("exact")
     return res
 
 

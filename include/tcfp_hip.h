@@ -213,6 +213,29 @@ int tcfp_block_dual_quantize(const void* w, int w_dtype, int64_t n, int64_t k, i
                              uint64_t offset, uint8_t* w_hi, uint8_t* w_lo, int8_t* e_hi,
                              int8_t* e_lo, void* stream);
 
+/* Re-blocking of a block dual-quantised weight along its other axis, for an
+ * FP8 block dgrad.  No single reference function: it is the operand step of
+ * the "FP8 block dgrad via a D_out-major re-quantised W^T" that would
+ * replace the reference's fp32 dequantise-then-dot dgrad
+ * (fused_block_scaled_dual_gemm_backward_dx, tcfp/kernels.py:2428-2469,
+ * kernel :2326-2425) when a caller opts in.  W_hi / W_lo [d_out, d_in] with
+ * exponents e_hi / e_lo [d_in/block, d_out] (tcfp_block_dual_quantize's
+ * output) are summed in fp32, v = 2^e_hi W_hi + 2^e_lo W_lo (e_lo = -128:
+ * no lo term), transposed to [d_in, d_out], and dual-quantised again by
+ * the tcfp_block_dual_quantize rule (RNE, no error buffer) along d_out:
+ * wt_hi / wt_lo [d_in, d_out], et_hi / et_lo [d_out/block, d_in], i.e. the
+ * B operands of tcfp_block_dual_gemm for dX = G W with G block-quantised
+ * along d_out.  The re-quantised product differs from the exact one by the
+ * dual-FP8 rounding of v (relative ~2^-9 of each block's maximum).
+ *   w_lo / e_lo may both be NULL (W_hi alone); d_out % block == 0,
+ *   d_in % block == 0; workspace holds
+ *   tcfp_block_requant_t_workspace_bytes(d_out, d_in) bytes (fp32 v^T). */
+size_t tcfp_block_requant_t_workspace_bytes(int64_t d_out, int64_t d_in);
+int tcfp_block_requant_t(const uint8_t* w_hi, const uint8_t* w_lo, const int8_t* e_hi,
+                         const int8_t* e_lo, int64_t d_out, int64_t d_in, int block,
+                         uint8_t* wt_hi, uint8_t* wt_lo, int8_t* et_hi, int8_t* et_lo,
+                         void* workspace, size_t workspace_bytes, void* stream);
+
 /* Block dequantisation fp8 * 2^e -> fp32 (tcfp/kernels.py:1725-1746).
  * A -128 exponent is decoded as 2^-128 like the reference's exp2. */
 int tcfp_block_dequantize(const uint8_t* q, int fp8_fmt, const int8_t* exps, int64_t m,

@@ -307,6 +307,23 @@ def block_dual_quantize(w: np.ndarray, bs: int, ef: np.ndarray | None = None):
     return hi, lo, e_hi8, e_lo8, ef_new
 
 
+def block_requant_t(hi: np.ndarray, lo: np.ndarray | None, e_hi: np.ndarray,
+                    e_lo: np.ndarray | None, bs: int):
+    """A block dual-quantised W [D_out, D_in] re-blocked along D_out (the
+    weight operand of an FP8 block dgrad; the reference has no such step:
+    its dgrad multiplies ``block_dequantize_fp8`` outputs, kernels.py:
+    2326-2425).  ``v = deq(hi) + deq(lo)`` in float32 (kernels.py:1725-1746),
+    then ``fused_dual_quantize_fp8`` of ``v.T`` without EF or SR
+    (kernels.py:1749-1875).  Returns ``(hi_t, lo_t, e_hi_t, e_lo_t)``, codes
+    [D_in, D_out], exponents [D_out/bs, D_in].
+    """
+    v = block_dequantize(hi, e_hi, bs)
+    if lo is not None:
+        v = (v + block_dequantize(lo, e_lo, bs)).astype(F32)
+    hi_t, lo_t, eh_t, el_t, _ = block_dual_quantize(np.ascontiguousarray(v.T), bs)
+    return hi_t, lo_t, eh_t, el_t
+
+
 def block_scale_f32(amax: np.ndarray, dtype: str = "f32", fmt: str = E4M3) -> np.ndarray:
     """fp32 block scales: ``per_tensor_scale``'s rule (core.py:100-101) on
     each block's amax -- clamp to 1e-12, reciprocal and product with

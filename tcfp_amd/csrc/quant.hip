@@ -1764,6 +1764,67 @@ int launch_transpose_u8(const uint8_t* src, int64_t rows, int64_t cols, uint8_t*
   return TCFP_OK;
 }
 
+// out[c, r] = 2^e_hi[c / bs, r] * W_hi[r, c] + 2^e_lo[c / bs, r] * W_lo[r, c]
+// (fp32; an e_lo of -128 marks a zero residual block) for W [rows, cols]
+// E4M3 codes with block exponents along cols: the dual-FP8 weight as one
+// fp32 matrix, transposed through a 64 x 64 LDS tile.  Each thread loads
+// 16 consecutive codes of one row (cols % 16 == 0, so the 16 share one
+// 32/64/128-wide block and one exponent per matrix).
+__global__ __launch_bounds__(kThreads) void dequant_sum_t_kernel(
+    const uint8_t* __restrict__ hi, const uint8_t* __restrict__ lo,
+    const int8_t* __restrict__ e_hi, const int8_t* __restrict__ e_lo, int64_t rows, int64_t cols,
+    int bs_shift, float* __restrict__ out) {
+  __shared__ float tile[64][64 + 1];
+  const int64_t tiles_c = (cols + 63) / 64;
+  const int64_t r0 = int64_t(blockIdx.x) / tiles_c * 64, c0 = int64_t(blockIdx.x) % tiles_c * 64;
+  const int t = threadIdx.x;
+  const int lr = t >> 2, seg = t & 3;
+  const int64_t r = r0 + lr, cs = c0 + seg * 16;
+  float v[16];
+  if (r < rows && cs < cols) {
+    const int64_t kb = cs >> bs_shift;
+    const float sh = exp2i(e_hi[kb * rows + r]);
+    const uint4 qh = *reinterpret_cast<const uint4*>(hi + r * cols + cs);
+    const uint32_t wh[4] = {qh.x, qh.y, qh.z, qh.w};
+#pragma unroll
+    for (int j = 0; j < 16; ++j) v[j] = e4m3_to_f32((wh[j >> 2] >> (8 * (j & 3))) & 0xFFu) * sh;
+    const int el = lo ? int(e_lo[kb * rows + r]) : -128;
+    if (el != -128) {
+      const float sl = exp2i(el);
+      const uint4 ql = *reinterpret_cast<const uint4*>(lo + r * cols + cs);
+      const uint32_t wl[4] = {ql.x, ql.y, ql.z, ql.w};
+#pragma unroll
+      for (int j = 0; j < 16; ++j)
+        v[j] = v[j] + e4m3_to_f32((wl[j >> 2] >> (8 * (j & 3))) & 0xFFu) * sl;
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 16; ++j) v[j] = 0.0f;
+  }
+#pragma unroll
+  for (int j = 0; j < 16; ++j) tile[lr][seg * 16 + j] = v[j];
+  __syncthreads();
+  // 16 lanes write one 256-byte output row segment (16 bytes each), so a
+  // store instruction covers four whole segments
+  const int sub = t & 15, rg = t >> 4;
+  const int64_t rr = r0 + sub * 4;
+#pragma unroll
+  for (int it = 0; it < 4; ++it) {
+    const int oc = it * 16 + rg;
+    const int64_t c = c0 + oc;
+    if (c >= cols) continue;
+    float* o = out + c * rows + rr;
+    if (rr + 4 <= rows && (rows & 3) == 0) {
+      *reinterpret_cast<float4*>(o) = make_float4(tile[sub * 4][oc], tile[sub * 4 + 1][oc],
+                                                  tile[sub * 4 + 2][oc], tile[sub * 4 + 3][oc]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (rr + i < rows) o[i] = tile[sub * 4 + i][oc];
+    }
+  }
+}
+
 // ===========================================================================
 // Self tests
 // ===========================================================================
@@ -2407,6 +2468,38 @@ int tcfp_block_dual_quantize_f32s(const void* w, int w_dtype, int64_t n, int64_t
   return block_dual_quantize_impl<true>(w, w_dtype, n, k, block, ef, update_ef, stochastic_lo,
                                         seed, offset, w_hi, w_lo, inv_hi, inv_lo,
                                         static_cast<hipStream_t>(stream));
+}
+
+size_t tcfp_block_requant_t_workspace_bytes(int64_t d_out, int64_t d_in) {
+  return d_out > 0 && d_in > 0 ? size_t(d_out) * size_t(d_in) * sizeof(float) : 0;
+}
+
+int tcfp_block_requant_t(const uint8_t* w_hi, const uint8_t* w_lo, const int8_t* e_hi,
+                         const int8_t* e_lo, int64_t d_out, int64_t d_in, int block,
+                         uint8_t* wt_hi, uint8_t* wt_lo, int8_t* et_hi, int8_t* et_lo,
+                         void* workspace, size_t workspace_bytes, void* stream) {
+  if (d_out < 0 || d_in < 0) return TCFP_ERR_SHAPE;
+  if (block != 32 && block != 64 && block != 128) return TCFP_ERR_SHAPE;
+  if (d_out % block != 0 || d_in % block != 0) return TCFP_ERR_SHAPE;
+  if (!w_hi || !e_hi || !wt_hi || !wt_lo || !et_hi || !et_lo) return TCFP_ERR_SHAPE;
+  if ((w_lo == nullptr) != (e_lo == nullptr)) return TCFP_ERR_SHAPE;
+  if (!aligned16(w_hi) || (w_lo && !aligned16(w_lo)) || !aligned16(wt_hi) || !aligned16(wt_lo))
+    return TCFP_ERR_ALIGN;
+  if (d_out == 0 || d_in == 0) return TCFP_OK;
+  if (!workspace || workspace_bytes < tcfp_block_requant_t_workspace_bytes(d_out, d_in))
+    return TCFP_ERR_WORKSPACE;
+  if (!aligned16(workspace)) return TCFP_ERR_ALIGN;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t tiles = ((d_out + 63) / 64) * ((d_in + 63) / 64);
+  if (tiles > INT32_MAX) return TCFP_ERR_SHAPE;
+  const int shift = block == 32 ? 5 : (block == 64 ? 6 : 7);
+  float* wt = static_cast<float*>(workspace);
+  dequant_sum_t_kernel<<<unsigned(tiles), kThreads, 0, st>>>(w_hi, w_lo, e_hi, e_lo, d_out, d_in,
+                                                             shift, wt);
+  const int rc = launch_status();
+  if (rc != TCFP_OK) return rc;
+  return block_dual_quantize_impl<false>(wt, TCFP_DTYPE_F32, d_in, d_out, block, nullptr, 0, 0, 0,
+                                         0, wt_hi, wt_lo, et_hi, et_lo, st);
 }
 
 int tcfp_block_dequantize(const uint8_t* q, int fp8_fmt, const int8_t* exps, int64_t m,

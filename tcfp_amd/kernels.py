@@ -1054,6 +1054,63 @@ def block_dgrad_from_prep(g_deq, w_hi_fp8, w_lo_fp8, w_hi_scales, w_lo_scales, b
     return out
 
 
+def block_requant_t(w_hi_fp8, w_lo_fp8, w_hi_scales, w_lo_scales, block_size):
+    """Block dual-quantised W [D_out, D_in] (exponents [D_in // bs, D_out])
+    re-blocked along D_out: ``v = deq(W_hi) + deq(W_lo)`` in fp32, then
+    ``fused_dual_quantize_fp8`` of ``v.T`` (RNE, no error buffer).  Returns
+    ``(wt_hi, wt_lo, et_hi, et_lo)`` with codes [D_in, D_out] and exponents
+    [D_out // bs, D_in]: the weight operands of an FP8 block dgrad
+    (:func:`fp8_block_dgrad`).  ``w_lo_fp8=None`` re-blocks W_hi alone."""
+    D_out, D_in = w_hi_fp8.shape
+    assert D_out % block_size == 0, f"D_out ({D_out}) not divisible by block_size ({block_size})"
+    assert D_in % block_size == 0, f"D_in ({D_in}) not divisible by block_size ({block_size})"
+    if block_size not in (32, 64, 128):
+        raise ValueError(f"block_size must be 32, 64, or 128, got {block_size}")
+    dev = _hip.require_gpu(w_hi_fp8, w_lo_fp8, w_hi_scales, w_lo_scales)
+    if w_hi_fp8.dtype != torch.float8_e4m3fn or (
+            w_lo_fp8 is not None and w_lo_fp8.dtype != torch.float8_e4m3fn):
+        raise TypeError("W_hi / W_lo must be float8_e4m3fn")
+    nkb = D_in // block_size
+    wh = w_hi_fp8.contiguous()
+    wl = w_lo_fp8.contiguous() if w_lo_fp8 is not None else None
+    if wl is not None:
+        assert tuple(wl.shape) == (D_out, D_in), "w_lo shape mismatch"
+    eh = _block_exps(w_hi_scales, D_out, nkb, "w_hi_scales")
+    el = _block_exps(w_lo_scales, D_out, nkb, "w_lo_scales") if wl is not None else None
+    wt_hi = torch.empty((D_in, D_out), dtype=torch.float8_e4m3fn, device=dev)
+    wt_lo = torch.empty((D_in, D_out), dtype=torch.float8_e4m3fn, device=dev)
+    et_hi = torch.empty((D_out // block_size, D_in), dtype=torch.int8, device=dev)
+    et_lo = torch.empty((D_out // block_size, D_in), dtype=torch.int8, device=dev)
+    nbytes = int(_hip.lib().tcfp_block_requant_t_workspace_bytes(D_out, D_in))
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
+    check(
+        _hip.lib().tcfp_block_requant_t(
+            ptr(wh), ptr(wl), ptr(eh), ptr(el), D_out, D_in, block_size, ptr(wt_hi), ptr(wt_lo),
+            ptr(et_hi), ptr(et_lo), ptr(ws), nbytes, _hip.stream_of(dev),
+        ),
+        "block_requant_t",
+    )
+    return wt_hi, wt_lo, et_hi, et_lo
+
+
+def fp8_block_dgrad(grad, w_hi_fp8, w_lo_fp8, w_hi_scales, w_lo_scales, block_size):
+    """Opt-in FP8 block dgrad ``dX ~ grad @ (deq(W_hi) + deq(W_lo))``, fp32
+    [M, D_in]: the gradient block-quantised to E5M2 along D_out (the
+    reference's ``block_quantize_fp8`` of the gradient, ``nn:700-712``),
+    W re-blocked along D_out (:func:`block_requant_t`), then the block dual
+    FP8 GEMM.  The reference multiplies the dequantised operands in fp32
+    (``fused_block_scaled_dual_gemm_backward_dx``); here W carries one more
+    dual-FP8 rounding (relative ~2^-9 of a block's maximum)."""
+    M, D_out = grad.shape
+    assert D_out == w_hi_fp8.shape[0], (
+        f"Shape mismatch: grad({M},{D_out}), w_hi{tuple(w_hi_fp8.shape)}")
+    g_fp8, g_exps = block_quantize_fp8(grad, block_size, torch.float8_e5m2)
+    wt_hi, wt_lo, et_hi, et_lo = block_requant_t(w_hi_fp8, w_lo_fp8, w_hi_scales, w_lo_scales,
+                                                 block_size)
+    return _block_gemm(g_fp8, g_exps, wt_hi, wt_lo, et_hi, et_lo, block_size, None,
+                       torch.float32)
+
+
 def block_wgrad_from_prep(g_split_t, act_fp8, act_scales, block_size):
     """``block_scaled_wgrad`` from the split gradient of
     :func:`block_backward_prep` (same result bit for bit; M % 4 == 0)."""

@@ -40,6 +40,7 @@ __all__ = [
     "TCFPMLP",
     "convert_to_tcfp",
     "fuse_tcfp_mlp",
+    "set_block_dgrad",
     "_TCFP12TensorCoreFunction",
     "_TCFP12BlockScaledFunction",
     "_TCFP12FusedMLPFunction",
@@ -187,6 +188,27 @@ class _TCFP12TensorCoreFunction(torch.autograd.Function):
         return (grad_input, grad_weight, grad_bias) + (None,) * 12
 
 
+_BLOCK_DGRAD = "exact"
+
+
+def set_block_dgrad(mode: str) -> None:
+    """Numerics of the block-scaled layers' input gradient (default
+    ``"exact"``).
+
+    ``"exact"``: the reference's ``dX = deq(G) @ (deq(W_hi) + deq(W_lo))``
+    with every product exact (bf16 MFMA on exactly representable operands),
+    at least as accurate as its fp32 dot.  ``"fp8"``: W re-blocked along
+    D_out and the block dual FP8 GEMM (``kernels.fp8_block_dgrad``), which
+    adds one dual-FP8 rounding of W (relative ~2^-9 of a block's maximum) and
+    runs at FP8 rate.  Read when a layer's forward runs; the backward of that
+    call uses the mode in force then.
+    """
+    global _BLOCK_DGRAD
+    if mode not in ("exact", "fp8"):
+        raise ValueError(f"block dgrad mode must be 'exact' or 'fp8', got {mode!r}")
+    _BLOCK_DGRAD = mode
+
+
 class _TCFP12BlockScaledFunction(torch.autograd.Function):
     """TCFP-12 with per-block (32/64/128 along K) power-of-two scales
     (reference ``tcfp/nn/__init__.py:574-761``)."""
@@ -233,6 +255,7 @@ class _TCFP12BlockScaledFunction(torch.autograd.Function):
         ctx.has_bias = bias is not None
         ctx.bs = bs
         ctx.abd = abd
+        ctx.fp8_dgrad = _BLOCK_DGRAD == "fp8"
         saved_act = input_2d if hp_grad_weight else act_fp8
         saved_act_scales = None if hp_grad_weight else act_scales
         ctx.save_for_backward(saved_act, saved_act_scales, w_hi, None if abd else w_lo, sh,
@@ -255,14 +278,18 @@ class _TCFP12BlockScaledFunction(torch.autograd.Function):
         fp8_wgrad = need_dw and not ctx.hp_grad_weight and grad_2d.shape[0] % 4 == 0
         want_db = need_db and ctx.has_bias
         g_deq = g_split = db = None
-        if need_dx or fp8_wgrad or want_db:
+        exact_dx = need_dx and not ctx.fp8_dgrad
+        if exact_dx or fp8_wgrad or want_db:
             g_deq, g_split, db = K.block_backward_prep(
-                grad_2d, bs, dequant=need_dx, split=fp8_wgrad, bias=want_db
+                grad_2d, bs, dequant=exact_dx, split=fp8_wgrad, bias=want_db
             )
-        if need_dx:
+        if exact_dx:
             grad_input = K.block_dgrad_from_prep(
                 g_deq, w_hi, w_lo, sh, sl, block_size=bs
             ).reshape(ctx.input_shape)
+        elif need_dx:
+            grad_input = K.fp8_block_dgrad(grad_2d, w_hi, w_lo, sh, sl, bs).reshape(
+                ctx.input_shape)
         if need_dw:
             if ctx.hp_grad_weight:
                 grad_weight = grad_2d.t() @ saved_act.to(grad_2d.dtype)

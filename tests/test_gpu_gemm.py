@@ -325,6 +325,74 @@ def test_block_dgrad_matches_oracle(dev, bs, M, D_out, D_in):
     assert og.rel_fro(npy(dxa), refa) < EXACT
 
 
+# ---------------------------------- opt-in FP8 block dgrad (W re-blocked)
+@pytest.mark.parametrize("bs", [32, 64, 128])
+@pytest.mark.parametrize("D_out,D_in", [(128, 256), (384, 128), (512, 1024)])
+def test_block_requant_t_matches_oracle(dev, bs, D_out, D_in):
+    print(f"requant bs={bs} {D_out}x{D_in}", flush=True)
+    g = torch.Generator().manual_seed(D_out * 3 + D_in + bs)
+    w = torch.randn(D_out, D_in, generator=g) * 0.02
+    w[: D_out // 7] *= 300.0  # rows of very different magnitude
+    h, l, eh, el = K.fused_dual_quantize_fp8(w.to(dev), bs)
+    ht, lt, eht, elt = K.block_requant_t(h, l, eh, el, bs)
+    want = oq.block_requant_t(u8(h), u8(l), npy(eh), npy(el), bs)
+    for got, exp in zip((u8(ht), u8(lt), npy(eht), npy(elt)), want):
+        assert np.array_equal(got, exp)
+    # W_hi alone (ABD)
+    ht2, _, eht2, _ = K.block_requant_t(h, None, eh, None, bs)
+    want2 = oq.block_requant_t(u8(h), None, npy(eh), None, bs)
+    assert np.array_equal(u8(ht2), want2[0]) and np.array_equal(npy(eht2), want2[2])
+
+
+@pytest.mark.parametrize("bs", [32, 64, 128])
+@pytest.mark.parametrize("M,D_out,D_in", [(300, 256, 384), (1024, 512, 1024), (4096, 1024, 2048)])
+def test_fp8_block_dgrad_accuracy(dev, bs, M, D_out, D_in):
+    g = torch.Generator().manual_seed(M + 5 * D_out + bs)
+    grad = torch.randn(M, D_out, generator=g) * 1e-3
+    w = torch.randn(D_out, D_in, generator=g) * 0.02
+    gd = grad.to(dev)
+    h, l, eh, el = K.fused_dual_quantize_fp8(w.to(dev), bs)
+    dx = K.fp8_block_dgrad(gd, h, l, eh, el, bs)
+    assert dx.dtype == torch.float32 and dx.shape == (M, D_in)
+    gq, eg = K.block_quantize_fp8(gd, bs, torch.float8_e5m2)
+    # the product of exactly these FP8 operands (the GEMM's own tolerance)
+    ht, lt, eht, elt = oq.block_requant_t(u8(h), u8(l), npy(eh), npy(el), bs)
+    Gd = og.block_deq64(u8(gq), npy(eg), bs, "e5m2")
+    Wt = og.block_deq64(ht, eht, bs) + og.block_deq64(lt, elt, bs, lo_sentinel=True)
+    assert og.rel_fro(npy(dx), Gd @ Wt.T) < EXACT
+    # against the reference's dgrad of the same gradient codes and W
+    exact = og.block_dgrad(u8(gq), npy(eg), u8(h), u8(l), npy(eh), npy(el), bs, "e5m2")
+    err = og.rel_fro(npy(dx), exact)
+    print(f"fp8 block dgrad bs={bs} M={M} rel_fro vs exact {err:.2e}", flush=True)
+    assert err < 1e-2
+
+
+def test_block_layer_fp8_dgrad_mode(dev):
+    from tcfp_amd.nn import TCFPLinear, set_block_dgrad
+
+    torch.manual_seed(0)
+    lin = TCFPLinear(512, 256, use_tensor_cores=True, scale_block_size=64).to(dev)
+    x = torch.randn(1024, 512, device=dev)
+    lin(x)  # the EF update of this weight version: both runs below quantise alike
+    outs = {}
+    try:
+        for mode in ("exact", "fp8"):
+            set_block_dgrad(mode)
+            xx = x.clone().requires_grad_(True)
+            y = lin(xx)
+            y.square().sum().backward()
+            outs[mode] = (y.detach(), xx.grad, lin.weight.grad.clone(), lin.bias.grad.clone())
+            lin.zero_grad(set_to_none=True)
+    finally:
+        set_block_dgrad("exact")
+    (ye, gxe, gwe, gbe), (yf, gxf, gwf, gbf) = outs["exact"], outs["fp8"]
+    assert torch.equal(ye, yf) and torch.equal(gwe, gwf) and torch.equal(gbe, gbf)
+    assert not torch.equal(gxe, gxf)
+    assert og.rel_fro(npy(gxf), npy(gxe)) < 1e-2
+    with pytest.raises(ValueError, match="exact"):
+        set_block_dgrad("tf32")
+
+
 # ------------------------------------------------- fused act-quant (a11)
 @pytest.mark.parametrize("bs", [32, 64, 128])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])

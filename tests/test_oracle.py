@@ -409,6 +409,33 @@ def test_block_dual_zero_residual_sentinel():
     assert ((el >= -126) | (el == -128)).all()
 
 
+@pytest.mark.parametrize("bs", [32, 64, 128])
+def test_block_requant_t_exact_when_representable_and_bounded(bs):
+    rng = np.random.default_rng(bs)
+    # small integers are exact in E4M3 under both blockings: re-blocking
+    # returns the transposed values exactly, with zero residual blocks
+    v = rng.integers(-15, 16, size=(2 * bs, 3 * bs)).astype(np.float32)
+    hi, lo, eh, el, _ = oq.block_dual_quantize(v, bs)
+    ht, lt, eht, elt = oq.block_requant_t(hi, lo, eh, el, bs)
+    assert ht.shape == (3 * bs, 2 * bs) and eht.shape == (2, 3 * bs)
+    assert np.array_equal(oq.block_dequantize(ht, eht, bs), v.T) and (elt == -128).all()
+    # general weights: the result approximates deq(W)^T to within a second
+    # dual-FP8 rounding, |err| <= 2^-7 of the block's maximum
+    w = (rng.standard_normal((4 * bs, 2 * bs)) * 0.02).astype(np.float32)
+    hi, lo, eh, el, _ = oq.block_dual_quantize(w, bs)
+    v = (oq.block_dequantize(hi, eh, bs) + oq.block_dequantize(lo, el, bs)).T
+    ht, lt, eht, elt = oq.block_requant_t(hi, lo, eh, el, bs)
+    got = oq.block_dequantize(ht, eht, bs) + np.where(
+        np.repeat(elt.T, bs, axis=1) == -128, 0.0, oq.block_dequantize(lt, elt, bs))
+    amax = np.repeat(np.abs(v).reshape(v.shape[0], -1, bs).max(-1), bs, axis=1)
+    assert np.all(np.abs(got - v) <= amax * 2.0 ** -7)
+    assert not np.array_equal(ht, hi.T)  # the blocking changed the codes
+    # W_hi alone (ABD)
+    ht2, _, eht2, _ = oq.block_requant_t(hi, None, eh, None, bs)
+    assert np.array_equal(ht2, oq.block_dual_quantize(
+        np.ascontiguousarray(oq.block_dequantize(hi, eh, bs).T), bs)[0])
+
+
 # ----------------------------------- fp32 (non-power-of-two) block scales
 @pytest.mark.parametrize("bs", [32, 64, 128])
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
