@@ -226,15 +226,14 @@ int tcfp_block_dual_quantize(const void* w, int w_dtype, int64_t n, int64_t k, i
  * wt_hi / wt_lo [d_in, d_out], et_hi / et_lo [d_out/block, d_in], i.e. the
  * B operands of tcfp_block_dual_gemm for dX = G W with G block-quantised
  * along d_out.  The re-quantised product differs from the exact one by the
- * dual-FP8 rounding of v (relative ~2^-9 of each block's maximum).
+ * dual-FP8 rounding of v (relative ~2^-9 of each block's maximum).  One pass: v never leaves
+ * the chip.
  *   w_lo / e_lo may both be NULL (W_hi alone); d_out % block == 0,
- *   d_in % block == 0; workspace holds
- *   tcfp_block_requant_t_workspace_bytes(d_out, d_in) bytes (fp32 v^T). */
-size_t tcfp_block_requant_t_workspace_bytes(int64_t d_out, int64_t d_in);
+ *   d_in % block == 0; code pointers 16-byte aligned. */
 int tcfp_block_requant_t(const uint8_t* w_hi, const uint8_t* w_lo, const int8_t* e_hi,
                          const int8_t* e_lo, int64_t d_out, int64_t d_in, int block,
                          uint8_t* wt_hi, uint8_t* wt_lo, int8_t* et_hi, int8_t* et_lo,
-                         void* workspace, size_t workspace_bytes, void* stream);
+                         void* stream);
 
 /* Block dequantisation fp8 * 2^e -> fp32 (tcfp/kernels.py:1725-1746).
  * A -128 exponent is decoded as 2^-128 like the reference's exp2. */

@@ -61,9 +61,7 @@ _SIGNATURES = {
                                  _u64, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p],
     "tcfp_block_dequantize": [_c_void_p, _i32, _c_void_p, _i64, _i64, _i32, _c_void_p, _c_void_p],
     "tcfp_block_requant_t": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i32,
-                             _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
-                             ctypes.c_size_t, _c_void_p],
-    "tcfp_block_requant_t_workspace_bytes": [_i64, _i64],
+                             _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p],
     "tcfp_block_quantize_f32s": [_c_void_p, _i32, _i64, _i64, _i32, _i32, _c_void_p, _c_void_p,
                                  _c_void_p],
     "tcfp_block_dual_quantize_f32s": [_c_void_p, _i32, _i64, _i64, _i32, _c_void_p, _i32, _i32,
@@ -118,7 +116,6 @@ _RESTYPE = {
     "tcfp_block_grad_prep_workspace_bytes": ctypes.c_size_t,
     "tcfp_block_dual_gemm_dx_bf16_workspace_bytes": ctypes.c_size_t,
     "tcfp_block_wgrad_presplit_workspace_bytes": ctypes.c_size_t,
-    "tcfp_block_requant_t_workspace_bytes": ctypes.c_size_t,
 }
 
 _lib = None

@@ -1764,63 +1764,106 @@ int launch_transpose_u8(const uint8_t* src, int64_t rows, int64_t cols, uint8_t*
   return TCFP_OK;
 }
 
-// out[c, r] = 2^e_hi[c / bs, r] * W_hi[r, c] + 2^e_lo[c / bs, r] * W_lo[r, c]
-// (fp32; an e_lo of -128 marks a zero residual block) for W [rows, cols]
-// E4M3 codes with block exponents along cols: the dual-FP8 weight as one
-// fp32 matrix, transposed through a 64 x 64 LDS tile.  Each thread loads
-// 16 consecutive codes of one row (cols % 16 == 0, so the 16 share one
-// 32/64/128-wide block and one exponent per matrix).
-__global__ __launch_bounds__(kThreads) void dequant_sum_t_kernel(
+// Re-blocking of a block dual-quantised weight W [rows, cols] (E4M3 codes,
+// exponents [cols / bs, rows] along cols) along rows, in one pass: a
+// workgroup takes a 128-row x 64-column tile of W_hi and W_lo, forms
+// v = 2^e_hi W_hi + 2^e_lo W_lo in fp32 (an e_lo of -128 marks a zero
+// residual block), holds v transposed in LDS, and dual-quantises each of the
+// 64 transposed rows' 128 values in bs-wide blocks by the block_dualq_kernel
+// rule (RNE, no EF): codes hi_t / lo_t [cols, rows], exponents [rows / bs,
+// cols].  rows % bs == 0 (every block of a tile is whole), cols % 16 == 0.
+template <int BS>
+__global__ __launch_bounds__(kThreads) void requant_t_kernel(
     const uint8_t* __restrict__ hi, const uint8_t* __restrict__ lo,
     const int8_t* __restrict__ e_hi, const int8_t* __restrict__ e_lo, int64_t rows, int64_t cols,
-    int bs_shift, float* __restrict__ out) {
-  __shared__ float tile[64][64 + 1];
-  const int64_t tiles_c = (cols + 63) / 64;
-  const int64_t r0 = int64_t(blockIdx.x) / tiles_c * 64, c0 = int64_t(blockIdx.x) % tiles_c * 64;
+    int bs_shift, uint8_t* __restrict__ hi_t, uint8_t* __restrict__ lo_t,
+    int8_t* __restrict__ et_hi, int8_t* __restrict__ et_lo) {
+  constexpr int TR = 128, TC = 64, VEC = 8, L = BS / VEC;
+  __shared__ float tile[TC][TR + 1];
+  const int64_t tiles_c = (cols + TC - 1) / TC;
+  const int64_t r0 = int64_t(blockIdx.x) / tiles_c * TR, c0 = int64_t(blockIdx.x) % tiles_c * TC;
   const int t = threadIdx.x;
-  const int lr = t >> 2, seg = t & 3;
-  const int64_t r = r0 + lr, cs = c0 + seg * 16;
-  float v[16];
-  if (r < rows && cs < cols) {
-    const int64_t kb = cs >> bs_shift;
-    const float sh = exp2i(e_hi[kb * rows + r]);
-    const uint4 qh = *reinterpret_cast<const uint4*>(hi + r * cols + cs);
-    const uint32_t wh[4] = {qh.x, qh.y, qh.z, qh.w};
+  // ---- v of 16 consecutive codes of one W row per thread and pass (they
+  // share one block along cols, so one exponent per matrix)
+  {
+    const int lr = t >> 2, seg = t & 3;
+    const int64_t cs = c0 + seg * 16;
 #pragma unroll
-    for (int j = 0; j < 16; ++j) v[j] = e4m3_to_f32((wh[j >> 2] >> (8 * (j & 3))) & 0xFFu) * sh;
-    const int el = lo ? int(e_lo[kb * rows + r]) : -128;
-    if (el != -128) {
-      const float sl = exp2i(el);
-      const uint4 ql = *reinterpret_cast<const uint4*>(lo + r * cols + cs);
-      const uint32_t wl[4] = {ql.x, ql.y, ql.z, ql.w};
+    for (int p = 0; p < TR / 64; ++p) {
+      const int tr = p * 64 + lr;
+      const int64_t r = r0 + tr;
+      float v[16];
+      if (r < rows && cs < cols) {
+        const int64_t kb = cs >> bs_shift;
+        const float sh = exp2i(e_hi[kb * rows + r]);
+        const uint4 qh = *reinterpret_cast<const uint4*>(hi + r * cols + cs);
+        const uint32_t wh[4] = {qh.x, qh.y, qh.z, qh.w};
 #pragma unroll
-      for (int j = 0; j < 16; ++j)
-        v[j] = v[j] + e4m3_to_f32((wl[j >> 2] >> (8 * (j & 3))) & 0xFFu) * sl;
+        for (int j = 0; j < 16; ++j) v[j] = e4m3_to_f32(wbyte(wh, j)) * sh;
+        const int el = lo ? int(e_lo[kb * rows + r]) : -128;
+        if (el != -128) {
+          const float sl = exp2i(el);
+          const uint4 ql = *reinterpret_cast<const uint4*>(lo + r * cols + cs);
+          const uint32_t wl[4] = {ql.x, ql.y, ql.z, ql.w};
+#pragma unroll
+          for (int j = 0; j < 16; ++j) v[j] = v[j] + e4m3_to_f32(wbyte(wl, j)) * sl;
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) v[j] = 0.0f;
+      }
+#pragma unroll
+      for (int j = 0; j < 16; ++j) tile[seg * 16 + j][tr] = v[j];
     }
-  } else {
-#pragma unroll
-    for (int j = 0; j < 16; ++j) v[j] = 0.0f;
   }
-#pragma unroll
-  for (int j = 0; j < 16; ++j) tile[lr][seg * 16 + j] = v[j];
   __syncthreads();
-  // 16 lanes write one 256-byte output row segment (16 bytes each), so a
-  // store instruction covers four whole segments
-  const int sub = t & 15, rg = t >> 4;
-  const int64_t rr = r0 + sub * 4;
+  // ---- dual quantisation of the transposed rows: 16 lanes per row (VEC
+  // values each), L lanes per bs-wide block
+  const int part = t & 15;
 #pragma unroll
-  for (int it = 0; it < 4; ++it) {
-    const int oc = it * 16 + rg;
+  for (int p = 0; p < TC / 16; ++p) {
+    const int oc = p * 16 + (t >> 4);
     const int64_t c = c0 + oc;
-    if (c >= cols) continue;
-    float* o = out + c * rows + rr;
-    if (rr + 4 <= rows && (rows & 3) == 0) {
-      *reinterpret_cast<float4*>(o) = make_float4(tile[sub * 4][oc], tile[sub * 4 + 1][oc],
-                                                  tile[sub * 4 + 2][oc], tile[sub * 4 + 3][oc]);
-    } else {
+    const int64_t r = r0 + part * VEC;  // first value of this lane (a row of W)
+    const bool valid = c < cols && r < rows;
+    float v[VEC];
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        if (rr + i < rows) o[i] = tile[sub * 4 + i][oc];
+    for (int j = 0; j < VEC; ++j) v[j] = tile[oc][part * VEC + j];
+    uint32_t a = 0;
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) a = umax(a, absbits(v[j]));
+    a = seg_umax<L>(a);
+    const int eh = block_exponent(__uint_as_float(a), kE4M3Max);
+    const float mul_hi = exp2i(-eh), s_hi = exp2i(eh);
+    float cv[VEC];
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) cv[j] = clampf(v[j] * mul_hi, kE4M3Max);
+    uint32_t hc[VEC / 4];
+    encode_words<VEC, TCFP_FP8_E4M3>(cv, hc);
+    uint32_t b = 0;
+    float res[VEC];
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) {
+      res[j] = v[j] - e4m3_to_f32(wbyte(hc, j)) * s_hi;
+      b = umax(b, absbits(res[j]));
+    }
+    b = seg_umax<L>(b);
+    const float amax_lo = __uint_as_float(b);
+    const bool zero = amax_lo < 1e-12f;
+    const int elo = block_exponent(amax_lo, kE4M3Max);
+    const float mul_lo = zero ? 1.0f : exp2i(-elo);
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) cv[j] = clampf(res[j] * mul_lo, kE4M3Max);
+    uint32_t lc[VEC / 4];
+    encode_words<VEC, TCFP_FP8_E4M3>(cv, lc);
+    if (valid) {
+      store_words<VEC>(hi_t + c * rows + r, hc);
+      store_words<VEC>(lo_t + c * rows + r, lc);
+      if (part % L == 0) {
+        const int64_t kb = r >> bs_shift;
+        et_hi[kb * cols + c] = int8_t(eh);
+        et_lo[kb * cols + c] = int8_t(zero ? -128 : elo);
+      }
     }
   }
 }
@@ -2470,14 +2513,10 @@ int tcfp_block_dual_quantize_f32s(const void* w, int w_dtype, int64_t n, int64_t
                                         static_cast<hipStream_t>(stream));
 }
 
-size_t tcfp_block_requant_t_workspace_bytes(int64_t d_out, int64_t d_in) {
-  return d_out > 0 && d_in > 0 ? size_t(d_out) * size_t(d_in) * sizeof(float) : 0;
-}
-
 int tcfp_block_requant_t(const uint8_t* w_hi, const uint8_t* w_lo, const int8_t* e_hi,
                          const int8_t* e_lo, int64_t d_out, int64_t d_in, int block,
                          uint8_t* wt_hi, uint8_t* wt_lo, int8_t* et_hi, int8_t* et_lo,
-                         void* workspace, size_t workspace_bytes, void* stream) {
+                         void* stream) {
   if (d_out < 0 || d_in < 0) return TCFP_ERR_SHAPE;
   if (block != 32 && block != 64 && block != 128) return TCFP_ERR_SHAPE;
   if (d_out % block != 0 || d_in % block != 0) return TCFP_ERR_SHAPE;
@@ -2486,20 +2525,20 @@ int tcfp_block_requant_t(const uint8_t* w_hi, const uint8_t* w_lo, const int8_t*
   if (!aligned16(w_hi) || (w_lo && !aligned16(w_lo)) || !aligned16(wt_hi) || !aligned16(wt_lo))
     return TCFP_ERR_ALIGN;
   if (d_out == 0 || d_in == 0) return TCFP_OK;
-  if (!workspace || workspace_bytes < tcfp_block_requant_t_workspace_bytes(d_out, d_in))
-    return TCFP_ERR_WORKSPACE;
-  if (!aligned16(workspace)) return TCFP_ERR_ALIGN;
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  const int64_t tiles = ((d_out + 63) / 64) * ((d_in + 63) / 64);
+  const int64_t tiles = ((d_out + 127) / 128) * ((d_in + 63) / 64);
   if (tiles > INT32_MAX) return TCFP_ERR_SHAPE;
-  const int shift = block == 32 ? 5 : (block == 64 ? 6 : 7);
-  float* wt = static_cast<float*>(workspace);
-  dequant_sum_t_kernel<<<unsigned(tiles), kThreads, 0, st>>>(w_hi, w_lo, e_hi, e_lo, d_out, d_in,
-                                                             shift, wt);
-  const int rc = launch_status();
-  if (rc != TCFP_OK) return rc;
-  return block_dual_quantize_impl<false>(wt, TCFP_DTYPE_F32, d_in, d_out, block, nullptr, 0, 0, 0,
-                                         0, wt_hi, wt_lo, et_hi, et_lo, st);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const unsigned g = unsigned(tiles);
+  if (block == 32)
+    requant_t_kernel<32><<<g, kThreads, 0, st>>>(w_hi, w_lo, e_hi, e_lo, d_out, d_in, 5, wt_hi,
+                                                 wt_lo, et_hi, et_lo);
+  else if (block == 64)
+    requant_t_kernel<64><<<g, kThreads, 0, st>>>(w_hi, w_lo, e_hi, e_lo, d_out, d_in, 6, wt_hi,
+                                                 wt_lo, et_hi, et_lo);
+  else
+    requant_t_kernel<128><<<g, kThreads, 0, st>>>(w_hi, w_lo, e_hi, e_lo, d_out, d_in, 7, wt_hi,
+                                                  wt_lo, et_hi, et_lo);
+  return launch_status();
 }
 
 int tcfp_block_dequantize(const uint8_t* q, int fp8_fmt, const int8_t* exps, int64_t m,

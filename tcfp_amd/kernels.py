@@ -1081,12 +1081,10 @@ def block_requant_t(w_hi_fp8, w_lo_fp8, w_hi_scales, w_lo_scales, block_size):
     wt_lo = torch.empty((D_in, D_out), dtype=torch.float8_e4m3fn, device=dev)
     et_hi = torch.empty((D_out // block_size, D_in), dtype=torch.int8, device=dev)
     et_lo = torch.empty((D_out // block_size, D_in), dtype=torch.int8, device=dev)
-    nbytes = int(_hip.lib().tcfp_block_requant_t_workspace_bytes(D_out, D_in))
-    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
     check(
         _hip.lib().tcfp_block_requant_t(
             ptr(wh), ptr(wl), ptr(eh), ptr(el), D_out, D_in, block_size, ptr(wt_hi), ptr(wt_lo),
-            ptr(et_hi), ptr(et_lo), ptr(ws), nbytes, _hip.stream_of(dev),
+            ptr(et_hi), ptr(et_lo), _hip.stream_of(dev),
         ),
         "block_requant_t",
     )
