@@ -344,6 +344,20 @@ def test_block_requant_t_matches_oracle(dev, bs, D_out, D_in):
     assert np.array_equal(u8(ht2), want2[0]) and np.array_equal(npy(eht2), want2[2])
 
 
+@pytest.mark.parametrize("bs,D_out,D_in", [(32, 96, 160), (64, 192, 320), (32, 224, 96),
+                                           (64, 64, 64)])
+def test_block_requant_t_partial_tiles(dev, bs, D_out, D_in):
+    # D_out not a multiple of the 128-row tile, D_in not a multiple of the
+    # 64-column tile: the tail blocks are skipped whole, nothing else moves
+    g = torch.Generator().manual_seed(D_out + D_in)
+    w = torch.randn(D_out, D_in, generator=g) * 0.05
+    h, l, eh, el = K.fused_dual_quantize_fp8(w.to(dev), bs)
+    got = K.block_requant_t(h, l, eh, el, bs)
+    want = oq.block_requant_t(u8(h), u8(l), npy(eh), npy(el), bs)
+    for a, b in zip((u8(got[0]), u8(got[1]), npy(got[2]), npy(got[3])), want):
+        assert np.array_equal(a, b)
+
+
 @pytest.mark.parametrize("bs", [32, 64, 128])
 @pytest.mark.parametrize("M,D_out,D_in", [(300, 256, 384), (1024, 512, 1024), (4096, 1024, 2048)])
 def test_fp8_block_dgrad_accuracy(dev, bs, M, D_out, D_in):
