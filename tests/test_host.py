@@ -242,3 +242,18 @@ def test_fuse_tcfp_mlp_structure_and_cpu_fallback():
     model.other = nn.Sequential(nn.Linear(64, 64), nn.GELU(approximate="tanh"), nn.Linear(64, 64))
     out = fuse_tcfp_mlp(convert_to_tcfp(model, use_tensor_cores=True, skip_patterns=("none",)))
     assert out is model and isinstance(model.mlp, TCFPMLP) and type(model.other) is nn.Sequential
+
+
+def test_set_block_dgrad_modes():
+    import tcfp_amd.nn as tnn
+
+    assert tnn._BLOCK_DGRAD == "exact"  # the reference's numerics by default
+    try:
+        tnn.set_block_dgrad("fp8")
+        assert tnn._BLOCK_DGRAD == "fp8"
+        with pytest.raises(ValueError, match="exact"):
+            tnn.set_block_dgrad("tf32")
+        assert tnn._BLOCK_DGRAD == "fp8"
+    finally:
+        tnn.set_block_dgrad("exact")
+    assert tnn._BLOCK_DGRAD == "exact"
