@@ -48,10 +48,8 @@ const char* tcfp_status_string(int status);
 
 /* Bytes of device workspace the per-tensor reductions need.  Reducing
  * kernels store one partial maximum per workgroup there and the kernel that
- * consumes the scale reduces them again.  The single-launch dual
- * quantisation also keeps three grid-barrier counters there: zero the
- * workspace once before its first use; every launch leaves them at zero.
- * Calls that may run concurrently (different streams) need different
+ * consumes the scale reduces them again.  Its contents need no
+ * initialisation.  Calls that may run concurrently (different streams) need different
  * workspaces; calls ordered on one stream can share one. */
 size_t tcfp_workspace_bytes(void);
 
@@ -117,10 +115,7 @@ int tcfp_gelu_backward_quantize_per_tensor_colsum(const float* dy, const float* 
 
 /* Per-tensor dual quantisation with optional error feedback.
  * Three launches (amax; W_hi + residual amax; W_lo + EF + transposed
- * codes), each re-reading W and EF.  Optionally (tcfp_dual_quant_set_path)
- * a single cooperative launch that holds W + EF on chip across the two
- * grid-wide max reductions when W (as 128 x 128 tiles) fits one or two
- * tiles per CU and k % 16 == 0.  Both give identical bits.
+ * codes), each re-reading W and EF.
  * Replaces the body of _TCFP12TensorCoreFunction.forward that builds
  * W_hi/W_lo (tcfp/nn/__init__.py:343-383, with ErrorFeedbackState
  * get_error/update_error, tcfp/core.py:320-326).
@@ -277,8 +272,11 @@ int tcfp_block_dequantize_f32s(const uint8_t* q, int fp8_fmt, const float* inv_s
  * With b_lo == NULL it is the single scaled GEMM s_a*s_hi*(A B_hi^T): the
  * FP8 wgrad of tcfp/nn/__init__.py:546-555 (A = G^T, B = X^T).
  *   a [m, k] (lda), b_hi/b_lo [n, k] (ldb); k % 16 == 0; lda, ldb % 16 == 0;
- *   pointers 16-byte aligned.  s_* are device fp32 scalars (inverse scales).
- *   out [m, n] (ldo) fp32 or bf16; accumulation is fp32. */
+ *   pointers (bias included) 16-byte aligned.  s_* are device fp32 scalars
+ *   (inverse scales).  out [m, n] (ldo) fp32 or bf16; accumulation is fp32.
+ *   An operand panel of 256 rows must span less than 2 GiB
+ *   (256 * ld + k < 2^31 - 2^20), else TCFP_ERR_SHAPE; the block GEMMs below
+ *   share these constraints. */
 int tcfp_dual_gemm(const uint8_t* a, int a_fmt, int64_t lda, const uint8_t* b_hi,
                    const uint8_t* b_lo, int b_fmt, int64_t ldb, int64_t m, int64_t n,
                    int64_t k, const float* s_a, const float* s_hi, const float* s_lo,
@@ -425,15 +423,6 @@ int tcfp_transpose_u8(const uint8_t* src, int64_t rows, int64_t cols, uint8_t* d
  * small-tile grid fits in one round, 4 256 x 128 with one workgroup per tile
  * (no persistent launch).  Results do not depend on the policy. */
 int tcfp_gemm_set_tile_policy(int policy);
-
-/* Per-tensor dual quantisation path for all later calls: 0 three launches
- * (default), 1 a single cooperative launch where it fits. */
-int tcfp_dual_quant_set_path(int path);
-
-/* Copies the workspace's sticky error flag to host *flag (synchronising
- * the stream): non-zero if a grid-barrier wait of the single-launch dual
- * quantisation ever gave up (which would also make its results invalid). */
-int tcfp_workspace_error(const void* workspace, int* flag, void* stream);
 
 /* ---- self-test hooks (no reference counterpart) ------------------------ */
 

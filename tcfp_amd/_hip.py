@@ -100,8 +100,6 @@ _SIGNATURES = {
                                   _c_void_p, _c_void_p, ctypes.c_size_t, _c_void_p],
     "tcfp_block_wgrad_presplit_workspace_bytes": [_i64, _i64, _i64],
     "tcfp_gemm_set_tile_policy": [_i32],
-    "tcfp_dual_quant_set_path": [_i32],
-    "tcfp_workspace_error": [_c_void_p, _c_void_p, _c_void_p],
     "tcfp_transpose_u8": [_c_void_p, _i64, _i64, _c_void_p, _c_void_p],
     "tcfp_selftest_fp8_cvt": [_u32, _u32, _i32, _c_void_p, _c_void_p],
     "tcfp_selftest_sr_block": [_u32, _u32, ctypes.c_float, _c_void_p, _c_void_p],
@@ -183,10 +181,8 @@ def workspace(device: torch.device) -> torch.Tensor:
     """Reduction scratch for the current stream of ``device``.
 
     Per-tensor reductions pass per-workgroup partial maxima from one launch
-    to the next through it, and the single-launch dual quantisation keeps
-    its grid-barrier counters there (zero when allocated, re-zeroed by the
-    kernel on exit).  Stream order makes one buffer per (device, stream)
-    safe for every call on that stream.
+    to the next through it.  Stream order makes one buffer per (device,
+    stream) safe for every call on that stream.
     """
     idx = device.index if device.index is not None else torch.cuda.current_device()
     key = (idx, stream_of(device))

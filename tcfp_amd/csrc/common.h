@@ -22,6 +22,11 @@ constexpr float kE5M2Max = 57344.0f;
 
 TCFP_DEV float fp8_max(int fmt) { return fmt == TCFP_FP8_E5M2 ? kE5M2Max : kE4M3Max; }
 
+// HIP launch limit along x: gridDim.x * blockDim.x must stay below 2^32.
+inline bool grid_x_fits(int64_t blocks, int threads) {
+  return blocks >= 0 && blocks <= int64_t(UINT32_MAX) / threads;
+}
+
 // ---------------------------------------------------------------------------
 // bfloat16
 // ---------------------------------------------------------------------------

@@ -8,19 +8,14 @@
 // The quantisation kernels emit the transposed copies, so no GEMM needs a
 // transposing operand path.
 //
-// Tiling: a 256-thread workgroup (4 wave64s, one per SIMD) owns a 256 x 128
-// output tile.  Per K step the A tile (256 x BK) is staged once in LDS and
-// shared by the two B tiles (W_hi and W_lo, 128 x BK each) -- the dual GEMM
-// is a single GEMM over [W_hi; W_lo] whose two accumulator halves meet in
-// the epilogue.  Each wave computes 128 x 64 of both halves with
-// v_mfma_scale_f32_32x32x64_f8f6f4 (neutral E8M0 scales), i.e. 4 x 2 x 2
-// 32x32 accumulator tiles (256 fp32 per lane).  In single-GEMM mode the two
-// B slots hold adjacent 128-column halves of one 256-wide tile.
-//
-// LDS rows are 16-byte-chunk XOR-swizzled so that both the 16-byte global
-// -> LDS stores and the 32-byte-per-lane MFMA operand reads are free of
-// bank conflicts.  Two LDS stages with register prefetch overlap the next
-// tile's global loads with the current tile's MFMAs; one barrier per step.
+// Tiling (gemm_nt_dma_kernel below): a workgroup owns a BM x BN output
+// tile per weight slot; per 128-column K stage the activation tile is
+// brought into LDS once by direct global->LDS DMA and shared by the two
+// weight slots (W_hi and W_lo) -- the dual GEMM is a single GEMM over
+// [W_hi; W_lo] whose two accumulator halves meet in the epilogue.  Waves run
+// v_mfma_scale_f32_32x32x64_f8f6f4 on fragments read from XOR-swizzled LDS
+// rows (bank-conflict free).  In single-GEMM mode the two slots hold
+// adjacent column halves of one 2*BN-wide tile.
 //
 // Workgroup -> tile mapping is XCD-aware: the dispatcher places workgroup b
 // on XCD b % 8, so workgroups are renumbered to give each XCD a contiguous
@@ -38,21 +33,6 @@ namespace {
 typedef int v8i __attribute__((ext_vector_type(8)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 
-constexpr int kNT = 256;
-constexpr int kBM = 256;
-constexpr int kBN = 128;
-
-template <int BK>
-struct Lds {
-  static constexpr int CPR = BK / 16;    // 16-byte chunks per row
-  static constexpr int RPW = 256 / BK;   // rows per 256-byte bank window
-  static constexpr int A = kBM * BK;
-  static constexpr int B = kBN * BK;
-  static constexpr int STAGE = A + 2 * B;
-  // byte offset of chunk `ch` of row `r`
-  static TCFP_DEV int off(int r, int ch) { return r * BK + (((ch ^ (r / RPW)) & (CPR - 1)) << 4); }
-};
-
 TCFP_DEV uint4 lds_read16(const uint8_t* base, int off) {
   return *reinterpret_cast<const uint4*>(base + off);
 }
@@ -64,169 +44,6 @@ TCFP_DEV v8i make_frag(uint4 lo, uint4 hi) {
   return f;
 }
 
-template <typename OutT>
-TCFP_DEV void store_out(OutT* p, float v);
-template <>
-TCFP_DEV void store_out<float>(float* p, float v) { *p = v; }
-template <>
-TCFP_DEV void store_out<uint16_t>(uint16_t* p, float v) { *p = f32_to_bf16_rne(v); }
-
-// AF/BF: fp8 format codes of A and B (0 = E4M3, 1 = E5M2), matching the
-// MFMA cbsz/blgp format selectors.  SPLIT = single-GEMM mode.
-template <int AF, int BF, bool SPLIT, int BK, typename OutT>
-__global__ __launch_bounds__(kNT, 1) void gemm_nt_kernel(
-    const uint8_t* __restrict__ A, const uint8_t* __restrict__ B0, const uint8_t* __restrict__ B1,
-    int M, int N, int K, int64_t lda, int64_t ldb, const float* __restrict__ s_a,
-    const float* __restrict__ s_0, const float* __restrict__ s_1, const float* __restrict__ bias,
-    OutT* __restrict__ out, int64_t ldo, int tiles_m, int tiles_n) {
-  using L = Lds<BK>;
-  extern __shared__ __align__(16) uint8_t smem[];
-
-  // ---- tile mapping (XCD-aware, grouped) ----
-  const int T = tiles_m * tiles_n;
-  int l = blockIdx.x;
-  if ((T & 7) == 0) l = (l & 7) * (T >> 3) + (l >> 3);
-  constexpr int G = 8;
-  const int per_group = G * tiles_n;
-  const int first_m = (l / per_group) * G;
-  const int gm = min(tiles_m - first_m, G);
-  const int tm = first_m + (l % per_group) % gm;
-  const int tn = (l % per_group) / gm;
-  const int m0 = tm * kBM;
-  const int n0 = SPLIT ? tn * (2 * kBN) : tn * kBN;
-  const int n1 = SPLIT ? n0 + kBN : n0;  // row base of the second B slot
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
-  const int lr = lane & 31, lg = lane >> 5;
-
-  // ---- global -> register prefetch mapping ----
-  constexpr int A_CH = kBM * L::CPR / kNT;  // 16-byte chunks per thread for A
-  constexpr int B_CH = kBN * L::CPR / kNT;  // ... for each B slot
-  uint4 pa[A_CH], pb0[B_CH], pb1[B_CH];
-
-  auto gload = [&](int kt) {
-    const int kbase = kt * BK;
-#pragma unroll
-    for (int i = 0; i < A_CH; ++i) {
-      const int c = tid + i * kNT;
-      const int r = c / L::CPR, ch = c % L::CPR;
-      const int gr = m0 + r, gk = kbase + ch * 16;
-      pa[i] = (gr < M && gk < K) ? *reinterpret_cast<const uint4*>(A + int64_t(gr) * lda + gk)
-                                 : make_uint4(0, 0, 0, 0);
-    }
-#pragma unroll
-    for (int i = 0; i < B_CH; ++i) {
-      const int c = tid + i * kNT;
-      const int r = c / L::CPR, ch = c % L::CPR;
-      const int gk = kbase + ch * 16;
-      const int g0 = n0 + r, g1 = n1 + r;
-      pb0[i] = (g0 < N && gk < K) ? *reinterpret_cast<const uint4*>(B0 + int64_t(g0) * ldb + gk)
-                                  : make_uint4(0, 0, 0, 0);
-      pb1[i] = (g1 < N && gk < K) ? *reinterpret_cast<const uint4*>(B1 + int64_t(g1) * ldb + gk)
-                                  : make_uint4(0, 0, 0, 0);
-    }
-  };
-  auto lstore = [&](int stage) {
-    uint8_t* base = smem + stage * L::STAGE;
-#pragma unroll
-    for (int i = 0; i < A_CH; ++i) {
-      const int c = tid + i * kNT;
-      *reinterpret_cast<uint4*>(base + L::off(c / L::CPR, c % L::CPR)) = pa[i];
-    }
-#pragma unroll
-    for (int i = 0; i < B_CH; ++i) {
-      const int c = tid + i * kNT;
-      const int o = L::off(c / L::CPR, c % L::CPR);
-      *reinterpret_cast<uint4*>(base + L::A + o) = pb0[i];
-      *reinterpret_cast<uint4*>(base + L::A + L::B + o) = pb1[i];
-    }
-  };
-
-  v16f acc0[4][2], acc1[4][2];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        acc0[i][j][r] = 0.0f;
-        acc1[i][j][r] = 0.0f;
-      }
-
-  const int nk = (K + BK - 1) / BK;
-  if (nk > 0) {
-    gload(0);
-    lstore(0);
-    __syncthreads();
-  }
-  for (int kt = 0; kt < nk; ++kt) {
-    const bool more = kt + 1 < nk;
-    if (more) gload(kt + 1);
-    const uint8_t* base = smem + (kt & 1) * L::STAGE;
-#pragma unroll
-    for (int ks = 0; ks < BK / 64; ++ks) {
-      const int c0 = ks * 4 + 2 * lg;  // this lane's two chunks of the 64-wide step
-      v8i fa[4], fb0[2], fb1[2];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int r = wm * 128 + i * 32 + lr;
-        fa[i] = make_frag(lds_read16(base, L::off(r, c0)), lds_read16(base, L::off(r, c0 + 1)));
-      }
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int r = wn * 64 + j * 32 + lr;
-        fb0[j] = make_frag(lds_read16(base + L::A, L::off(r, c0)),
-                           lds_read16(base + L::A, L::off(r, c0 + 1)));
-        fb1[j] = make_frag(lds_read16(base + L::A + L::B, L::off(r, c0)),
-                           lds_read16(base + L::A + L::B, L::off(r, c0 + 1)));
-      }
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          acc0[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-              fa[i], fb0[j], acc0[i][j], AF, BF, 0, 127, 0, 127);
-          acc1[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-              fa[i], fb1[j], acc1[i][j], AF, BF, 0, 127, 0, 127);
-        }
-    }
-    if (more) lstore((kt + 1) & 1);
-    __syncthreads();
-  }
-
-  // ---- epilogue: scale, combine, store ----
-  const float sa = *s_a;
-  const float c0s = sa * *s_0;
-  const float c1s = sa * *s_1;
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int colw = wn * 64 + j * 32 + lr;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = m0 + wm * 128 + i * 32 + (r >> 2) * 8 + lg * 4 + (r & 3);
-        if (row >= M) continue;
-        OutT* orow = out + int64_t(row) * ldo;
-        if constexpr (SPLIT) {
-          const int ca = n0 + colw, cb = n1 + colw;
-          if (ca < N) store_out<OutT>(orow + ca, acc0[i][j][r] * c0s + (bias ? bias[ca] : 0.0f));
-          if (cb < N) store_out<OutT>(orow + cb, acc1[i][j][r] * c0s + (bias ? bias[cb] : 0.0f));
-        } else {
-          const int col = n0 + colw;
-          if (col < N) {
-            float v = acc0[i][j][r] * c0s + acc1[i][j][r] * c1s;
-            if (bias) v += bias[col];
-            store_out<OutT>(orow + col, v);
-          }
-        }
-      }
-    }
-}
-
-constexpr int kBK = 64;
 
 // ===========================================================================
 // Main kernel: LDS double buffer filled by direct global->LDS DMA
@@ -1224,8 +1041,10 @@ int launch_gemm(GemmArgs ga, hipStream_t st) {
   const int BMv = small ? 128 : 256, BNv = small ? 64 : 128;
   ga.tiles_m = (m + BMv - 1) / BMv;
   ga.tiles_n = (n + (SPLIT ? 2 * BNv : BNv) - 1) / (SPLIT ? 2 * BNv : BNv);
-  const bool dma_ok = int64_t(BMv) * ga.lda + k < kMaxSpan && int64_t(BNv) * ga.ldb + k < kMaxSpan &&
-                      (ga.bias == nullptr || (reinterpret_cast<uintptr_t>(ga.bias) & 15) == 0);
+  if (ga.bias != nullptr && (reinterpret_cast<uintptr_t>(ga.bias) & 15) != 0) return TCFP_ERR_ALIGN;
+  // 512 threads per workgroup at most; the tile index is an int in the kernel
+  if (!grid_x_fits(int64_t(ga.tiles_m) * ga.tiles_n, 512)) return TCFP_ERR_SHAPE;
+  const bool dma_ok = int64_t(BMv) * ga.lda + k < kMaxSpan && int64_t(BNv) * ga.ldb + k < kMaxSpan;
   if (dma_ok) {
     // split-K (SCALE 0): gridDim.y = number of K chunks
     const unsigned splits =
@@ -1268,27 +1087,10 @@ int launch_gemm(GemmArgs ga, hipStream_t st) {
     }
     return hipGetLastError() == hipSuccess ? TCFP_OK : TCFP_ERR_HIP;
   }
-  if constexpr (SCALE != 0 || AF == kBF16) {
-    return TCFP_ERR_SHAPE;  // block-scaled and bf16 GEMMs need spans the DMA path covers
-  } else {
-    const int tiles_m = (m + kBM - 1) / kBM;
-    const int tn_w = SPLIT ? 2 * kBN : kBN;
-    const int tiles_n = (n + tn_w - 1) / tn_w;
-    const int smem = 2 * Lds<kBK>::STAGE;
-    auto kern = gemm_nt_kernel<AF, BF, SPLIT, kBK, OutT>;
-    static bool attr_set = false;
-    if (!attr_set) {
-      if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, smem) != hipSuccess)
-        return TCFP_ERR_HIP;
-      attr_set = true;
-    }
-    kern<<<tiles_m * tiles_n, kNT, smem, st>>>(ga.A, ga.B0, ga.B1, m, n, k, ga.lda, ga.ldb,
-                                               ga.s_a, ga.s_0, ga.s_1, ga.bias,
-                                               static_cast<OutT*>(ga.out), ga.ldo, tiles_m,
-                                               tiles_n);
-    return hipGetLastError() == hipSuccess ? TCFP_OK : TCFP_ERR_HIP;
-  }
+  // Operand panels whose byte span (BM rows of the leading dimension) reaches
+  // 2 GiB do not fit the DMA descriptors' 32-bit offsets: K-contiguous
+  // operands with K < ~8M always fit.
+  return TCFP_ERR_SHAPE;
 }
 
 template <bool SPLIT, typename OutT, int SCALE>
@@ -1621,7 +1423,7 @@ int dgrad_bf16(const uint16_t* gd, const uint8_t* w_hi, const uint8_t* w_lo, con
                const int8_t* e_lo, int64_t m, int64_t d_out, int64_t d_in, int shift, float* dx,
                uint16_t* wth, uint16_t* wtl, hipStream_t st) {
   const int64_t tiles = ((d_out + 63) / 64) * ((d_in + 63) / 64);
-  if (tiles > INT32_MAX) return TCFP_ERR_SHAPE;
+  if (!grid_x_fits(tiles, 256)) return TCFP_ERR_SHAPE;
   dequant_t_bf16_kernel<TCFP_FP8_E4M3><<<dim3(unsigned(tiles), w_lo ? 2u : 1u), 256, 0, st>>>(
       w_hi, e_hi, wth, w_lo, e_lo, wtl, d_out, d_in, shift);
   if (hipGetLastError() != hipSuccess) return TCFP_ERR_HIP;
@@ -1923,7 +1725,7 @@ extern "C" int tcfp_block_grad_prep(const float* g, int64_t m, int64_t n, int bl
     return TCFP_OK;
   }
   const int64_t tr = (m + 63) / 64, tc = (n + 127) / 128;
-  if (tr * tc > INT32_MAX) return TCFP_ERR_SHAPE;
+  if (!grid_x_fits(tr * tc, 256)) return TCFP_ERR_SHAPE;
   float* part = bias_grad ? static_cast<float*>(workspace) : nullptr;
   const unsigned grid = unsigned(tr * tc);
   if (block == 32) grad_prep_kernel<32><<<grid, 256, 0, st>>>(g, m, n, g_deq, g_split_t, part);
@@ -1966,7 +1768,7 @@ extern "C" int tcfp_block_wgrad(const float* g, int64_t m, int64_t n_out, const 
   } else {
     const int64_t tg = ((m + 63) / 64) * ((n_out + 63) / 64);
     const int64_t tx = ((m + 63) / 64) * ((k_in + 63) / 64);
-    if (tg > INT32_MAX || tx > INT32_MAX) return TCFP_ERR_SHAPE;
+    if (!grid_x_fits(tg, 256) || !grid_x_fits(tx, 256)) return TCFP_ERR_SHAPE;
     split_t_bf16_kernel<<<unsigned(tg), 256, 0, st>>>(g, m, n_out, ap);
     if (x_fmt == TCFP_FP8_E5M2)
       dequant_t_dup_bf16_kernel<TCFP_FP8_E5M2><<<unsigned(tx), 256, 0, st>>>(x, e_x, m, k_in, shift, bp);
@@ -2009,7 +1811,7 @@ extern "C" int tcfp_block_wgrad_presplit(const uint16_t* g_split_t, int64_t m, i
   uint16_t* bp = reinterpret_cast<uint16_t*>(ws);
   if (m > 0) {
     const int64_t tx = ((m + 63) / 64) * ((k_in + 63) / 64);
-    if (tx > INT32_MAX) return TCFP_ERR_SHAPE;
+    if (!grid_x_fits(tx, 256)) return TCFP_ERR_SHAPE;
     if (x_fmt == TCFP_FP8_E5M2)
       dequant_t_dup_bf16_kernel<TCFP_FP8_E5M2><<<unsigned(tx), 256, 0, st>>>(x, e_x, m, k_in, shift, bp);
     else

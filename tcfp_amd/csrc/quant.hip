@@ -27,11 +27,6 @@ constexpr int kMaxParts = 2048;
 struct PartWs {
   uint32_t a[kMaxParts];  // partial amax of the first reduction
   uint32_t b[kMaxParts];  // partial amax of the residual (dual quantisation)
-  // grid-barrier counters of the single-launch dual quantisation: zero at
-  // rest (each launch's last workgroup resets them); ctr[3] is a sticky
-  // error flag set if a barrier wait ever gave up
-  uint32_t ctr[4];
-  uint32_t pad[60];
   // NF-aware scaling: per-workgroup shifted sums of the first pass,
   // sum(v - v0) and sum((v - v0)^2) in fp64 (v0 = the tensor's first element)
   double s1[kMaxParts];
@@ -1093,265 +1088,6 @@ __global__ __launch_bounds__(kThreads) void dualq_lo_t_kernel(
   if (lo_t) store_transposed(tile_l, tg, rows, cols, lo_t, threadIdx.x);
 }
 // ===========================================================================
-// Single-launch per-tensor dual quantisation (cooperative grid)
-// ===========================================================================
-//
-// The three passes above read W (+EF) three times because two grid-wide
-// maxima separate them.  Here one workgroup per CU keeps its share of W+EF
-// in registers across two grid barriers: HBM sees W and EF read once and
-// W_hi, W_lo, EF (and the transposed codes) written once.  Work is split in
-// 128 x 128 tiles, TPW per workgroup (tile b, b + G, ...); a thread owns 16
-// consecutive elements of one tile row.  The arithmetic is the three-pass
-// path's, operation for operation, so the outputs are bit-identical.
-//
-// The grid barrier needs every workgroup resident, which the cooperative
-// launch guarantees (it fails instead of launching otherwise, and the
-// caller falls back to the three passes).  Its wait is bounded: after
-// 2^20 polls it sets the workspace's sticky error flag and proceeds, so a
-// broken invariant shows up as a wrong result and an error, never a hang.
-constexpr int kCoopThreads = 1024;
-
-// Everything workgroups exchange across the barrier (the partial maxima)
-// moves through agent-scope atomic stores and loads, which bypass the
-// non-coherent caches, so no cache write-back is needed: the arriving
-// thread only waits until its partial's store is acknowledged
-// (vmcnt(0) also counts stores on this architecture) before it counts
-// itself in.
-TCFP_DEV void grid_barrier(uint32_t* ctr, uint32_t* err, uint32_t G) {
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0)
-    __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    uint32_t spins = 0;
-    while (__hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < G) {
-      __builtin_amdgcn_s_sleep(2);
-      if (++spins > (1u << 20)) {
-        atomicOr(err, 1u);
-        break;
-      }
-    }
-  }
-  __syncthreads();
-}
-
-TCFP_DEV uint32_t block_umax_1024(uint32_t m, uint32_t* red) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) m = umax(m, uint32_t(__shfl_xor(int(m), o, 64)));
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
-  __syncthreads();
-  m = red[0];
-#pragma unroll
-  for (int i = 1; i < kCoopThreads / 64; ++i) m = umax(m, red[i]);
-  return m;
-}
-
-TCFP_DEV float reduce_parts_1024(const uint32_t* p, int g, uint32_t* red) {
-  uint32_t m = 0;
-  for (int i = threadIdx.x; i < g; i += kCoopThreads)
-    m = umax(m, __hip_atomic_load(&p[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-  return __uint_as_float(block_umax_1024(m, red));
-}
-
-template <typename InT>
-TCFP_DEV void load16(const InT* p, float* v);
-template <>
-TCFP_DEV void load16<float>(const float* p, float* v) {
-#pragma unroll
-  for (int i = 0; i < 16; i += 4) {
-    const float4 a = *reinterpret_cast<const float4*>(p + i);
-    v[i] = a.x; v[i + 1] = a.y; v[i + 2] = a.z; v[i + 3] = a.w;
-  }
-}
-template <>
-TCFP_DEV void load16<uint16_t>(const uint16_t* p, float* v) {
-  load8(p, v);
-  load8(p + 8, v + 8);
-}
-
-template <typename InT, bool HAS_EF, bool UPDATE, bool SR, int TPW, bool KEEP_W>
-__global__ __launch_bounds__(kCoopThreads) void dualq_coop_kernel(
-    const InT* __restrict__ w, float* __restrict__ ef, int64_t rows, int64_t cols, int tiles,
-    PartWs* ws, uint8_t* __restrict__ hi, uint8_t* __restrict__ lo, float* inv_hi_out,
-    float* inv_lo_out, uint8_t* __restrict__ hi_t, uint8_t* __restrict__ lo_t, uint32_t k0,
-    uint32_t k1, uint32_t off0, uint32_t off1) {
-  // separate LDS scratch for the two kinds of reduction: a wave may start
-  // the second while another still reads the first's result
-  __shared__ uint32_t red[kCoopThreads / 64];
-  __shared__ uint32_t red_p[kCoopThreads / 64];
-  __shared__ uint32_t tile_h[kTile * kTilePitch];
-  __shared__ uint32_t tile_l[kTile * kTilePitch];
-  // W is kept on chip (one tile per workgroup: 64 KiB of LDS) or re-read
-  __shared__ float4 lds_w[KEEP_W ? kCoopThreads * 4 : 1];
-  static_assert(!KEEP_W || TPW == 1, "W fits on chip for one tile per workgroup");
-  const uint32_t G = gridDim.x;
-  const int tr = threadIdx.x >> 3, tc = (threadIdx.x & 7) * 16;
-  float rv[TPW][16];               // w = W + EF, then the residual
-  uint32_t hc[TPW][4];             // W_hi codes
-  bool valid[TPW];
-  int64_t off[TPW];
-
-  // ---- phase 1: w = W + EF, max |w| ----------------------------------------
-  uint32_t m = 0;
-#pragma unroll
-  for (int i = 0; i < TPW; ++i) {
-    __builtin_amdgcn_sched_barrier(0);
-    const int tile = int(blockIdx.x) + i * int(G);
-    const TileGeom tg(cols, tile < tiles ? tile : 0);
-    const int64_t r = tg.r0 + tr, c = tg.c0 + tc;
-    valid[i] = tile < tiles && r < rows && c < cols;  // cols % 16 == 0: whole run in range
-    off[i] = r * cols + c;
-    float W[16];
-    if (valid[i]) {
-      load16<InT>(w + off[i], W);
-    } else {
-#pragma unroll
-      for (int j = 0; j < 16; ++j) W[j] = 0.0f;
-    }
-    if constexpr (HAS_EF) {
-      float e[16];
-      if (valid[i]) {
-        load16<float>(ef + off[i], e);
-      } else {
-#pragma unroll
-        for (int j = 0; j < 16; ++j) e[j] = 0.0f;
-      }
-#pragma unroll
-      for (int j = 0; j < 16; ++j) rv[i][j] = W[j] + e[j];
-    } else {
-#pragma unroll
-      for (int j = 0; j < 16; ++j) rv[i][j] = W[j];
-    }
-    if constexpr (KEEP_W) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        lds_w[threadIdx.x * 4 + j] = make_float4(W[4 * j], W[4 * j + 1], W[4 * j + 2], W[4 * j + 3]);
-    }
-#pragma unroll
-    for (int j = 0; j < 16; ++j) m = umax(m, absbits(rv[i][j]));
-  }
-  m = block_umax_1024(m, red);
-  if (threadIdx.x == 0)
-    __hip_atomic_store(&ws->a[blockIdx.x], m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  grid_barrier(&ws->ctr[0], &ws->ctr[3], G);
-
-  // ---- phase 2: W_hi codes, residual, max |residual| -----------------------
-  float s_hi, inv_hi;
-  scale_from_amax(reduce_parts_1024(ws->a, int(G), red_p), false, kE4M3Max, &s_hi, &inv_hi);
-  if (blockIdx.x == 0 && threadIdx.x == 0 && inv_hi_out) *inv_hi_out = inv_hi;
-  m = 0;
-#pragma unroll
-  for (int i = 0; i < TPW; ++i) {
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      float c[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) c[j] = clampf(rv[i][4 * q + j] * s_hi, kE4M3Max);
-      hc[i][q] = encode4<TCFP_FP8_E4M3>(c[0], c[1], c[2], c[3]);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float r = rv[i][4 * q + j] - e4m3_to_f32((hc[i][q] >> (8 * j)) & 0xFFu) * inv_hi;
-        rv[i][4 * q + j] = r;
-        m = umax(m, absbits(r));
-      }
-    }
-  }
-  m = block_umax_1024(m, red);
-  if (threadIdx.x == 0)
-    __hip_atomic_store(&ws->b[blockIdx.x], m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  grid_barrier(&ws->ctr[1], &ws->ctr[3], G);
-
-  // ---- phase 3: W_lo codes, new error, codes and transposes ----------------
-  float s_lo, inv_lo;
-  scale_from_amax(reduce_parts_1024(ws->b, int(G), red_p), false, kE4M3Max, &s_lo, &inv_lo);
-  if (blockIdx.x == 0 && threadIdx.x == 0 && inv_lo_out) *inv_lo_out = inv_lo;
-#pragma unroll
-  for (int i = 0; i < TPW; ++i) {
-    // one tile at a time: keeps the scheduler from overlapping the tiles'
-    // temporaries (the registers are the limit here)
-    __builtin_amdgcn_sched_barrier(0);
-    const int tile = int(blockIdx.x) + i * int(G);
-    uint32_t lc[4];
-    // four elements at a time: W (kept or re-read), W_lo codes, new error
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      float dh[4], x[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        dh[j] = e4m3_to_f32((hc[i][q] >> (8 * j)) & 0xFFu) * inv_hi;
-        x[j] = clampf(rv[i][4 * q + j] * s_lo, kE4M3Max);
-      }
-      lc[q] = lo_codes4<SR>(x, off[i] + 4 * q, k0, k1, off0, off1);
-      if constexpr (HAS_EF && UPDATE) {
-        float W[4];
-        if constexpr (KEEP_W) {
-          const float4 a = lds_w[threadIdx.x * 4 + q];
-          W[0] = a.x; W[1] = a.y; W[2] = a.z; W[3] = a.w;
-        } else if (valid[i]) {
-          if constexpr (sizeof(InT) == 4) {
-            const float4 a = *reinterpret_cast<const float4*>(
-                reinterpret_cast<const float*>(w) + off[i] + 4 * q);
-            W[0] = a.x; W[1] = a.y; W[2] = a.z; W[3] = a.w;
-          } else {
-            const uint2 a = *reinterpret_cast<const uint2*>(
-                reinterpret_cast<const uint16_t*>(w) + off[i] + 4 * q);
-            W[0] = __uint_as_float(a.x << 16); W[1] = __uint_as_float(a.x & 0xFFFF0000u);
-            W[2] = __uint_as_float(a.y << 16); W[3] = __uint_as_float(a.y & 0xFFFF0000u);
-          }
-        } else {
-          W[0] = W[1] = W[2] = W[3] = 0.0f;
-        }
-        float e[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          e[j] = W[j] - (dh[j] + e4m3_to_f32((lc[q] >> (8 * j)) & 0xFFu) * inv_lo);
-        if (valid[i])
-          *reinterpret_cast<float4*>(ef + off[i] + 4 * q) = make_float4(e[0], e[1], e[2], e[3]);
-      }
-    }
-    if (valid[i]) {
-      if ((cols & 15) == 0) {
-        *reinterpret_cast<uint4*>(hi + off[i]) = make_uint4(hc[i][0], hc[i][1], hc[i][2], hc[i][3]);
-        *reinterpret_cast<uint4*>(lo + off[i]) = make_uint4(lc[0], lc[1], lc[2], lc[3]);
-      } else {
-        *reinterpret_cast<uint2*>(hi + off[i]) = make_uint2(hc[i][0], hc[i][1]);
-        *reinterpret_cast<uint2*>(hi + off[i] + 8) = make_uint2(hc[i][2], hc[i][3]);
-        *reinterpret_cast<uint2*>(lo + off[i]) = make_uint2(lc[0], lc[1]);
-        *reinterpret_cast<uint2*>(lo + off[i] + 8) = make_uint2(lc[2], lc[3]);
-      }
-    }
-    if (hi_t || lo_t) {
-      if (tile < tiles) {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          tile_h[tr * kTilePitch + tc / 4 + q] = hc[i][q];
-          tile_l[tr * kTilePitch + tc / 4 + q] = lc[q];
-        }
-      }
-      __syncthreads();
-      if (tile < tiles) {
-        const TileGeom tg(cols, tile);
-        if (threadIdx.x < 256) {
-          if (hi_t) store_transposed(tile_h, tg, rows, cols, hi_t, threadIdx.x);
-        } else if (threadIdx.x < 512) {
-          if (lo_t) store_transposed(tile_l, tg, rows, cols, lo_t, threadIdx.x - 256);
-        }
-      }
-      __syncthreads();
-    }
-  }
-
-  // ---- exit: the last workgroup out re-zeroes the barrier counters ---------
-  if (threadIdx.x == 0) {
-    const uint32_t old = atomicAdd(&ws->ctr[2], 1u);
-    if (old == G - 1) {
-      atomicExch(&ws->ctr[0], 0u);
-      atomicExch(&ws->ctr[1], 0u);
-      atomicExch(&ws->ctr[2], 0u);
-    }
-  }
-}
-
-// ===========================================================================
 // Block quantisation (tcfp/kernels.py:205-275)
 // ===========================================================================
 
@@ -1759,7 +1495,7 @@ __global__ __launch_bounds__(kThreads) void transpose_u8_kernel(const uint8_t* _
 int launch_transpose_u8(const uint8_t* src, int64_t rows, int64_t cols, uint8_t* dst,
                         hipStream_t st) {
   const int64_t tiles = ((rows + 63) / 64) * ((cols + 63) / 64);
-  if (tiles > INT32_MAX) return TCFP_ERR_SHAPE;
+  if (!grid_x_fits(tiles, kThreads)) return TCFP_ERR_SHAPE;
   if (tiles > 0) transpose_u8_kernel<<<unsigned(tiles), kThreads, 0, st>>>(src, rows, cols, dst);
   return TCFP_OK;
 }
@@ -1929,61 +1665,6 @@ __global__ __launch_bounds__(kThreads) void selftest_philox_kernel(uint32_t c0, 
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-// Cooperative single-launch dual quantisation; returns false (nothing
-// launched) when the shape or the device does not allow it.
-template <typename T, bool EF, bool UP, bool SR, int TPW>
-bool launch_coop_dualq(const T* w, float* ef, int64_t n, int64_t k, int tiles, int G, PartWs* ws,
-                       uint8_t* hi, uint8_t* lo, float* inv_hi, float* inv_lo, uint8_t* hi_t,
-                       uint8_t* lo_t, uint32_t k0, uint32_t k1, uint32_t o0, uint32_t o1,
-                       hipStream_t st) {
-  constexpr bool KEEP_W = TPW == 1 && EF && UP;
-  auto kern = dualq_coop_kernel<T, EF, UP, SR, TPW, KEEP_W>;
-  void* args[] = {&w, &ef, &n, &k, &tiles, &ws, &hi, &lo, &inv_hi, &inv_lo, &hi_t, &lo_t,
-                  &k0, &k1, &o0, &o1};
-  if (hipLaunchCooperativeKernel(reinterpret_cast<const void*>(kern), dim3(unsigned(G)),
-                                 dim3(kCoopThreads), args, 0, st) != hipSuccess) {
-    (void)hipGetLastError();  // clear: the caller falls back to the three passes
-    return false;
-  }
-  return true;
-}
-
-int g_coop = -1;  // device supports cooperative launches
-// Default: three launches.  Measured on MI355X for 4096 x 1024 with EF:
-// three launches 22 us, the cooperative single launch 47 us (its grid
-// barriers and cooperative dispatch cost more than the two re-reads of W
-// and EF, which hit the 256 MB Infinity Cache at this size).
-int g_force_three_pass = 1;
-
-template <typename T, bool EF, bool UP, bool SR>
-bool try_coop_dualq(const T* w, float* ef, int64_t n, int64_t k, PartWs* ws, uint8_t* hi,
-                    uint8_t* lo, float* inv_hi, float* inv_lo, uint8_t* hi_t, uint8_t* lo_t,
-                    uint32_t k0, uint32_t k1, uint32_t o0, uint32_t o1, hipStream_t st) {
-  if (g_coop < 0) {
-    int dev = 0, v = 0;
-    g_coop = (hipGetDevice(&dev) == hipSuccess &&
-              hipDeviceGetAttribute(&v, hipDeviceAttributeCooperativeLaunch, dev) == hipSuccess &&
-              v)
-                 ? 1
-                 : 0;
-  }
-  if (!g_coop || n <= 0 || k <= 0 || k % 16 != 0) return false;
-  const int64_t tiles = ((n + kTile - 1) / kTile) * ((k + kTile - 1) / kTile);
-  const int G = int(std::min<int64_t>(num_cu(), tiles));
-  const int64_t tpw = (tiles + G - 1) / G;
-  // two tiles per workgroup exceed the register budget when the error is
-  // rewritten; one tile per workgroup covers 256 tiles (e.g. 4096 x 1024)
-  if (tpw > (EF && UP ? 1 : 2) || G > kMaxParts) return false;
-  const int t = int(tiles);
-#define TCFP_COOP(TP) \
-  launch_coop_dualq<T, EF, UP, SR, TP>(w, ef, n, k, t, G, ws, hi, lo, inv_hi, inv_lo, hi_t, lo_t, \
-                                       k0, k1, o0, o1, st)
-  if (tpw == 1) return TCFP_COOP(1);
-  if constexpr (!(EF && UP)) return TCFP_COOP(2);
-  return false;
-#undef TCFP_COOP
-}
-
 }  // namespace
 
 // ===========================================================================
@@ -2005,22 +1686,6 @@ const char* tcfp_status_string(int status) {
 }
 
 size_t tcfp_workspace_bytes(void) { return sizeof(PartWs); }
-
-int tcfp_dual_quant_set_path(int path) {
-  if (path != 0 && path != 1) return TCFP_ERR_SHAPE;
-  g_force_three_pass = path == 0 ? 1 : 0;
-  return TCFP_OK;
-}
-
-int tcfp_workspace_error(const void* workspace, int* flag, void* stream) {
-  if (!workspace || !flag) return TCFP_ERR_SHAPE;
-  const PartWs* ws = static_cast<const PartWs*>(workspace);
-  if (hipMemcpyAsync(flag, &ws->ctr[3], sizeof(int), hipMemcpyDeviceToHost,
-                     static_cast<hipStream_t>(stream)) != hipSuccess ||
-      hipStreamSynchronize(static_cast<hipStream_t>(stream)) != hipSuccess)
-    return TCFP_ERR_HIP;
-  return TCFP_OK;
-}
 
 }  // extern "C"
 
@@ -2075,7 +1740,7 @@ int quantize_impl(const void* x, int x_dtype, int64_t rows, int64_t cols, int fp
   const bool tiled = q_t && n > 0 && cols % 8 == 0;
   if (tiled) {
     const int64_t tiles = ((rows + kTile - 1) / kTile) * ((cols + kTile - 1) / kTile);
-    if (tiles > INT32_MAX) return TCFP_ERR_SHAPE;
+    if (!grid_x_fits(tiles, kThreads)) return TCFP_ERR_SHAPE;
 #define TCFP_QT(T, F)                                                                          \
   quant_t_kernel<T, F><<<unsigned(tiles), kThreads, 0, st>>>(static_cast<const T*>(x), rows,  \
                                                              cols, part, g, bfr, scale_in, q, \
@@ -2223,7 +1888,7 @@ int dual_quantize_impl(const void* w, int w_dtype, int64_t n, int64_t k, float* 
   const bool upd = has_ef && update_ef;
   const bool tiled = (w_hi_t || w_lo_t) && total > 0 && k % 8 == 0;
   const int64_t tiles = ((n + kTile - 1) / kTile) * ((k + kTile - 1) / kTile);
-  if (tiled && tiles > INT32_MAX) return TCFP_ERR_SHAPE;
+  if (tiled && !grid_x_fits(tiles, kThreads)) return TCFP_ERR_SHAPE;
   const uint32_t k0 = uint32_t(seed), k1 = uint32_t(seed >> 32);
   const uint32_t o0 = uint32_t(offset), o1 = uint32_t(offset >> 32);
 
@@ -2234,34 +1899,6 @@ int dual_quantize_impl(const void* w, int w_dtype, int64_t n, int64_t k, float* 
     hr.n = total;
     hr.sigma = sigma;
     hr.sr = sr_hi ? 1 : 0;
-  }
-
-  // one cooperative launch when selected and it fits (SR together with EF,
-  // delayed scaling and NF-aware scaling stay on the separate passes)
-  if (g_force_three_pass == 0 && !(stochastic_lo && has_ef) && !dl.on && !nf) {
-    bool done = false;
-    if (bf) {
-      const uint16_t* wp = static_cast<const uint16_t*>(w);
-      if (stochastic_lo)
-        done = try_coop_dualq<uint16_t, false, false, true>(wp, nullptr, n, k, ws, w_hi, w_lo, inv_hi, inv_lo, w_hi_t, w_lo_t, k0, k1, o0, o1, st);
-      else if (upd)
-        done = try_coop_dualq<uint16_t, true, true, false>(wp, ef, n, k, ws, w_hi, w_lo, inv_hi, inv_lo, w_hi_t, w_lo_t, k0, k1, o0, o1, st);
-      else if (has_ef)
-        done = try_coop_dualq<uint16_t, true, false, false>(wp, ef, n, k, ws, w_hi, w_lo, inv_hi, inv_lo, w_hi_t, w_lo_t, k0, k1, o0, o1, st);
-      else
-        done = try_coop_dualq<uint16_t, false, false, false>(wp, nullptr, n, k, ws, w_hi, w_lo, inv_hi, inv_lo, w_hi_t, w_lo_t, k0, k1, o0, o1, st);
-    } else {
-      const float* wp = static_cast<const float*>(w);
-      if (stochastic_lo)
-        done = try_coop_dualq<float, false, false, true>(wp, nullptr, n, k, ws, w_hi, w_lo, inv_hi, inv_lo, w_hi_t, w_lo_t, k0, k1, o0, o1, st);
-      else if (upd)
-        done = try_coop_dualq<float, true, true, false>(wp, ef, n, k, ws, w_hi, w_lo, inv_hi, inv_lo, w_hi_t, w_lo_t, k0, k1, o0, o1, st);
-      else if (has_ef)
-        done = try_coop_dualq<float, true, false, false>(wp, ef, n, k, ws, w_hi, w_lo, inv_hi, inv_lo, w_hi_t, w_lo_t, k0, k1, o0, o1, st);
-      else
-        done = try_coop_dualq<float, false, false, false>(wp, nullptr, n, k, ws, w_hi, w_lo, inv_hi, inv_lo, w_hi_t, w_lo_t, k0, k1, o0, o1, st);
-    }
-    if (done) return launch_status();
   }
 
   // Delayed scaling without validation predicts the residual amax: pass 2
@@ -2400,7 +2037,9 @@ int block_quantize_impl(const void* x, int x_dtype, int64_t m, int64_t k, int bl
   const unsigned kbs = unsigned(k / block);
 #define TCFP_BQ(T, F, B)                                                                    \
   do {                                                                                      \
-    dim3 grid(unsigned((m + Seg<T, B>::ROWS - 1) / Seg<T, B>::ROWS), kbs);                  \
+    const int64_t gx = (m + Seg<T, B>::ROWS - 1) / Seg<T, B>::ROWS;                         \
+    if (!grid_x_fits(gx, kThreads)) return TCFP_ERR_SHAPE;                                  \
+    dim3 grid(unsigned(gx), kbs);                                                           \
     block_quant_kernel<T, F, B, F32S><<<grid, kThreads, 0, st>>>(static_cast<const T*>(x),  \
                                                                  m, k, q, scales);          \
   } while (0)
@@ -2441,7 +2080,9 @@ int block_dual_quantize_impl(const void* w, int w_dtype, int64_t n, int64_t k, i
 #define TCFP_BDQ(T, B, EF, UP, SR)                                                             \
   do {                                                                                         \
     using DS = DualSeg<T, B, SR>;                                                              \
-    dim3 grid(unsigned((n + DS::ROWS - 1) / DS::ROWS), kbs);                                   \
+    const int64_t gx = (n + DS::ROWS - 1) / DS::ROWS;                                          \
+    if (!grid_x_fits(gx, kThreads)) return TCFP_ERR_SHAPE;                                     \
+    dim3 grid(unsigned(gx), kbs);                                                              \
     block_dualq_kernel<T, B, EF, UP, SR, F32S><<<grid, kThreads, 0, st>>>(                     \
         static_cast<const T*>(w), ef, n, k, w_hi, w_lo, s_hi, s_lo, k0, k1, o0, o1);           \
   } while (0)
@@ -2526,7 +2167,7 @@ int tcfp_block_requant_t(const uint8_t* w_hi, const uint8_t* w_lo, const int8_t*
     return TCFP_ERR_ALIGN;
   if (d_out == 0 || d_in == 0) return TCFP_OK;
   const int64_t tiles = ((d_out + 127) / 128) * ((d_in + 63) / 64);
-  if (tiles > INT32_MAX) return TCFP_ERR_SHAPE;
+  if (!grid_x_fits(tiles, kThreads)) return TCFP_ERR_SHAPE;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const unsigned g = unsigned(tiles);
   if (block == 32)

@@ -61,6 +61,16 @@ def _out_dtype(dtype: torch.dtype) -> int:
     raise TypeError(f"unsupported output dtype {dtype}")
 
 
+def _bias_f32(bias: torch.Tensor, n: int) -> torch.Tensor:
+    """fp32, contiguous, 16-byte aligned copy of the bias (the GEMM epilogue
+    reads it as 16-byte vectors)."""
+    b = bias.to(torch.float32).contiguous()
+    assert b.shape == (n,), f"bias shape {tuple(b.shape)} != ({n},)"
+    if b.data_ptr() % 16 != 0:
+        b = b.clone()
+    return b
+
+
 def _scalar(t: torch.Tensor, name: str) -> torch.Tensor:
     if t.numel() != 1 or t.dtype != torch.float32:
         raise ValueError(f"{name} must be a single-element float32 tensor")
@@ -451,8 +461,7 @@ def _dual_gemm(a, b_hi, b_lo, s_a, s_hi, s_lo, bias, out_dtype):
         b_hi = b_hi.contiguous()
     out = torch.empty((m, n), dtype=out_dtype, device=dev)
     if bias is not None:
-        bias = bias.to(torch.float32).contiguous()
-        assert bias.shape == (n,), f"bias shape {tuple(bias.shape)} != ({n},)"
+        bias = _bias_f32(bias, n)
     check(
         _hip.lib().tcfp_dual_gemm(
             ptr(a), _fmt(a.dtype), a.stride(0), ptr(b_hi), ptr(b_lo), _fmt(b_hi.dtype),
@@ -712,8 +721,7 @@ def _block_gemm(a, e_a, b_hi, b_lo, e_hi, e_lo, block_size, bias, out_dtype):
         b_hi, b_lo = b_hi.contiguous(), b_lo.contiguous()
     out = torch.empty((m, n), dtype=out_dtype, device=dev)
     if bias is not None:
-        bias = bias.to(torch.float32).contiguous()
-        assert bias.shape == (n,), f"bias shape {tuple(bias.shape)} != ({n},)"
+        bias = _bias_f32(bias, n)
     fn = (_hip.lib().tcfp_block_dual_gemm_f32s if sdt == torch.float32
           else _hip.lib().tcfp_block_dual_gemm)
     check(
@@ -885,8 +893,7 @@ def fused_wtquant_block_scaled_dual_gemm_forward(
     s_hi = torch.empty((num_kb, N), dtype=torch.int8, device=dev)
     s_lo = torch.empty((num_kb, N), dtype=torch.int8, device=dev)
     if bias is not None:
-        bias = bias.to(torch.float32).contiguous()
-        assert bias.shape == (N,), f"bias shape {tuple(bias.shape)} != ({N},)"
+        bias = _bias_f32(bias, N)
     if stochastic_lo and seed is None:
         seed = int(torch.randint(0, 2**62, (1,)).item())
     check(
@@ -1129,26 +1136,6 @@ def block_wgrad_from_prep(g_split_t, act_fp8, act_scales, block_size):
         "block_wgrad_from_prep",
     )
     return out
-
-
-def set_dual_quant_path(path: str) -> None:
-    """Tuning/test hook for ``dual_quantize_per_tensor``: ``"three_pass"``
-    (the default) or ``"single_launch"`` (one cooperative launch holding
-    W + EF on chip where it fits; same bits, measured slower)."""
-    code = {"three_pass": 0, "single_launch": 1}[path]
-    check(_hip.lib().tcfp_dual_quant_set_path(code), "set_dual_quant_path")
-
-
-def workspace_error(device: torch.device | None = None) -> int:
-    """Sticky error flag of the reduction workspace (0 = no grid-barrier
-    wait ever gave up)."""
-    import ctypes
-
-    dev = device or torch.device("cuda", torch.cuda.current_device())
-    flag = ctypes.c_int(0)
-    check(_hip.lib().tcfp_workspace_error(ptr(_hip.workspace(dev)), ctypes.byref(flag),
-                                          _hip.stream_of(dev)), "workspace_error")
-    return int(flag.value)
 
 
 def set_gemm_tile_policy(policy: str) -> None:

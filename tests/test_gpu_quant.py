@@ -358,34 +358,6 @@ def test_quantize_colsum_codes_and_sums(dev, shape, dtype):
     np.testing.assert_allclose(cs.cpu().numpy(), ref, rtol=1e-5, atol=1e-6 * float(np.abs(x.float().numpy()).sum(0).max()))
 
 
-# ------------------------------------------------ single-launch vs three-pass dual quant
-@pytest.mark.parametrize("shape", [(4096, 1024), (1024, 4096), (128, 128), (300, 208),
-                                   (2048, 2048), (4096, 2048), (100, 96)])
-@pytest.mark.parametrize("wdtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("mode", ["ef", "ef_no_update", "no_ef", "srr"])
-def test_dual_quant_single_launch_matches_three_pass(dev, shape, wdtype, mode):
-    """The cooperative one-launch path and the three-launch path give the
-    same bits (codes, inverse scales, transposed codes, new error)."""
-    g = torch.Generator().manual_seed(shape[0] * 7 + shape[1])
-    W = (torch.randn(shape, generator=g) * 0.02).to(wdtype).to(dev)
-    ef0 = (torch.randn(shape, generator=g) * 1e-5).to(dev)
-    outs = []
-    try:
-        for path in ("three_pass", "single_launch"):
-            K.set_dual_quant_path(path)
-            ef = ef0.clone() if mode.startswith("ef") else None
-            r = K.dual_quantize_per_tensor(W, ef, update_ef=(mode != "ef_no_update"),
-                                           stochastic_lo=(mode == "srr"), transposed=True,
-                                           seed=1234)
-            outs.append([t.view(torch.uint8) if t.dtype.itemsize == 1 else t for t in r]
-                        + ([ef] if ef is not None else []))
-    finally:
-        K.set_dual_quant_path("three_pass")
-    for a, b in zip(*outs):
-        assert torch.equal(a, b)
-    assert K.workspace_error(dev) == 0
-
-
 # ---------------------------------------- delayed scaling (PDDS) dual quant
 @pytest.mark.parametrize("wdt", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("transposed", [False, True])

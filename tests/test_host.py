@@ -51,6 +51,23 @@ def test_argument_validation_without_launch():
                                         None, None) == 6  # SR + EF
 
 
+def test_grid_limit_is_a_shape_error_without_launch():
+    """1-D grids past HIP's 2^32-thread limit (gridDim.x * 256 threads) are
+    rejected with TCFP_ERR_SHAPE before any launch (the pointers are dummies
+    that are never dereferenced)."""
+    lib = _hip.load_library()
+    p = 4096  # any 16-byte-aligned non-null address
+    limit = (2**32 - 1) // 256  # largest 256-thread grid HIP accepts
+    # re-blocking: ceil(d_out / 128) * ceil(d_in / 64) workgroups
+    d_out, d_in = 128 * 4096, 64 * 4096
+    assert (d_out // 128) * (d_in // 64) == limit + 1
+    assert lib.tcfp_block_requant_t(p, None, p, None, d_out, d_in, 64, p, p, p, p, None) == 1
+    # byte transpose: ceil(rows / 64) * ceil(cols / 64) workgroups
+    rows, cols = 64 * 4096, 64 * 4097
+    assert (rows // 64) * (cols // 64) > limit
+    assert lib.tcfp_transpose_u8(p, rows, cols, p, None) == 1
+
+
 def test_cpu_tensors_fail_loudly():
     with pytest.raises(RuntimeError, match="only on the GPU"):
         to_fp8_e4m3(torch.randn(4, 4))
