@@ -42,6 +42,7 @@ extern "C" {
 #define TCFP_ERR_HIP 4       /* a HIP runtime call failed                  */
 #define TCFP_ERR_WORKSPACE 5 /* workspace missing or too small             */
 #define TCFP_ERR_EXCLUSIVE 6 /* mutually exclusive options requested       */
+#define TCFP_ERR_DEVICE 7    /* stream not on the current device           */
 
 /* Human-readable text for a status code (static storage). */
 const char* tcfp_status_string(int status);
@@ -132,6 +133,26 @@ int tcfp_dual_quantize_per_tensor(const void* w, int w_dtype, int64_t n, int64_t
                                   uint8_t* w_lo, float* inv_hi, float* inv_lo,
                                   uint8_t* w_hi_t, uint8_t* w_lo_t, void* workspace,
                                   void* stream);
+
+/* tcfp_dual_quantize_per_tensor without the workspace argument, for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc).  No counterpart in the
+ * reference.  Same arguments, kernels and results (bit for bit) as
+ * tcfp_dual_quantize_per_tensor; the reduction partials live in a
+ * library-owned static device array of 49408 bytes per GPU (held until the
+ * process ends; the per-tensor reductions need at most that for any weight
+ * size, so no size is rejected for scratch).  The call allocates nothing:
+ * no hipMalloc/hipFree, no allocating library routine; its first call on a
+ * device looks up the array's device address once.  The stream must belong
+ * to the current device (TCFP_ERR_DEVICE otherwise).  Every call on one GPU
+ * shares that array: calls that overlap on one GPU (e.g. on two streams
+ * without ordering between them) race and give wrong scales; calls ordered
+ * on one stream are safe. */
+int tcfp_dual_quantize_per_tensor_noalloc(const void* w, int w_dtype, int64_t n, int64_t k,
+                                          float* ef, int update_ef, int stochastic_lo,
+                                          uint64_t seed, uint64_t offset, uint8_t* w_hi,
+                                          uint8_t* w_lo, float* inv_hi, float* inv_lo,
+                                          uint8_t* w_hi_t, uint8_t* w_lo_t, void* stream);
 
 /* Per-tensor dual quantisation with delayed ("predictive dual-track")
  * scaling: _TCFP12TensorCoreFunction.forward with delayed_scaling=True

@@ -44,6 +44,10 @@ _SIGNATURES = {
     "tcfp_dual_quantize_per_tensor": [_c_void_p, _i32, _i64, _i64, _c_void_p, _i32, _i32, _u64,
                                       _u64, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                                       _c_void_p, _c_void_p, _c_void_p, _c_void_p],
+    "tcfp_dual_quantize_per_tensor_noalloc": [_c_void_p, _i32, _i64, _i64, _c_void_p, _i32,
+                                              _i32, _u64, _u64, _c_void_p, _c_void_p,
+                                              _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+                                              _c_void_p],
     "tcfp_dual_quantize_per_tensor_delayed": [_c_void_p, _i32, _i64, _i64, _c_void_p, _i32,
                                               _c_void_p, _c_void_p, ctypes.c_float,
                                               ctypes.c_float, _i32, _c_void_p, _c_void_p,

@@ -9,6 +9,7 @@
 // thread owns whole 8-element vectors, so the in-place error-feedback update
 // of a vector is done by the thread that read it.
 #include <algorithm>
+#include <mutex>
 
 #include "common.h"
 
@@ -1681,6 +1682,7 @@ const char* tcfp_status_string(int status) {
     case TCFP_ERR_HIP: return "HIP runtime error";
     case TCFP_ERR_WORKSPACE: return "workspace missing";
     case TCFP_ERR_EXCLUSIVE: return "stochastic_lo and error feedback are mutually exclusive";
+    case TCFP_ERR_DEVICE: return "stream is not on the current device";
     default: return "unknown status";
   }
 }
@@ -1966,6 +1968,68 @@ int tcfp_dual_quantize_per_tensor(const void* w, int w_dtype, int64_t n, int64_t
   return dual_quantize_impl(w, w_dtype, n, k, ef, update_ef, stochastic_lo, seed, offset, w_hi,
                             w_lo, inv_hi, inv_lo, w_hi_t, w_lo_t, workspace, off, false, 0.0f,
                             false, stream);
+}
+
+}  // extern "C"
+
+namespace {
+
+// ---- scratch of the no-allocation entry point ----------------------------
+// tcfp_dual_quantize_per_tensor_noalloc keeps its reduction partials in this
+// file-scope device array instead of a caller workspace: one copy per GPU,
+// held until the process ends.  On the host `scratch` names a host-side
+// stand-in, not device memory, so host code never passes it to a kernel: the
+// device address comes from hipGetSymbolAddress, looked up once per device
+// (with that device current, on the first call there) and kept in
+// g_scratch_ptr.  Every call on a GPU shares that GPU's array.  The
+// reduction partials need no initialisation (each launch writes the slots it
+// reads before reading them), so nothing is cleared between calls.
+constexpr size_t kScratchBytes = 49408;  // the per-tensor reductions' PartWs
+static_assert(sizeof(PartWs) <= kScratchBytes, "scratch must hold the reduction workspace");
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of this GPU's scratch; the stream must belong to the
+// current device.
+int scratch_for(hipStream_t st, void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess) return TCFP_ERR_HIP;
+  if (dev < 0 || dev >= kMaxDevices) return TCFP_ERR_DEVICE;
+  if (st != nullptr) {
+    hipDevice_t sd = -1;
+    if (hipStreamGetDevice(st, &sd) != hipSuccess) return TCFP_ERR_HIP;
+    if (sd != dev) return TCFP_ERR_DEVICE;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || ptr == nullptr)
+      return TCFP_ERR_HIP;
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return TCFP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int tcfp_dual_quantize_per_tensor_noalloc(const void* w, int w_dtype, int64_t n, int64_t k,
+                                          float* ef, int update_ef, int stochastic_lo,
+                                          uint64_t seed, uint64_t offset, uint8_t* w_hi,
+                                          uint8_t* w_lo, float* inv_hi, float* inv_lo,
+                                          uint8_t* w_hi_t, uint8_t* w_lo_t, void* stream) {
+  if (tcfp_workspace_bytes() > kScratchBytes) return TCFP_ERR_WORKSPACE;
+  void* ws = nullptr;
+  const int rc = scratch_for(static_cast<hipStream_t>(stream), &ws);
+  if (rc != TCFP_OK) return rc;
+  const Delayed off{};
+  return dual_quantize_impl(w, w_dtype, n, k, ef, update_ef, stochastic_lo, seed, offset, w_hi,
+                            w_lo, inv_hi, inv_lo, w_hi_t, w_lo_t, ws, off, false, 0.0f, false,
+                            stream);
 }
 
 int tcfp_dual_quantize_per_tensor_delayed(const void* w, int w_dtype, int64_t n, int64_t k,
