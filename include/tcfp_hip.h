@@ -73,6 +73,33 @@ int tcfp_quantize_per_tensor(const void* x, int x_dtype, int64_t rows, int64_t c
                              float* scale_out, float* inv_out, void* workspace,
                              void* stream);
 
+/* Per-tensor FP8 E4M3 quantisation with stochastic rounding.  Replaces
+ * tcfp.core.to_fp8_e4m3_sr (tcfp/core.py:109-134), which applies
+ * stochastic_round_to_fp8_e4m3 (tcfp/core.py:418-464) to the scaled values;
+ * with *scale_in == 1 it is that function on already clamped values.
+ *   scale as tcfp_quantize_per_tensor (amax rule, or scale_in);
+ *   c = clamp(x * scale, +-448); code = RNE(c) or its neighbour toward c,
+ *   the neighbour with probability |c - RNE(c)| / gap (the reference's
+ *   candidate rule: nudge 2^-7, retry 0.25 * max(|lo|, 2^-6)); exact values
+ *   keep their code.  Uniforms from Philox4x32-10 keyed by (seed, offset).
+ *   q [rows, cols] (8-byte aligned when >= 8 elements), inv_out (and the
+ *   optional scale_out) device fp32 scalars. */
+int tcfp_quantize_per_tensor_sr(const void* x, int x_dtype, int64_t rows, int64_t cols,
+                                const float* scale_in, uint64_t seed, uint64_t offset,
+                                uint8_t* q, float* scale_out, float* inv_out, void* workspace,
+                                void* stream);
+
+/* Power-of-two block scales.  Replaces tcfp.core.compute_block_scales
+ * (tcfp/core.py:221-252): for each run of `block` elements of the rows of
+ * x [rows, cols] (f32 or bf16), scale = 2^ceil(log2(max(amax, 1e-12) /
+ * fp8_max)) with every step rounded to x's dtype as torch rounds it (bf16:
+ * the quotient and its log2 are rounded to bf16 before the ceil), written
+ * in x's dtype to scales [rows, cols / block] (row-major: the reference's
+ * (..., D // block) layout, not the kernels' [K / block, rows]).  NaN
+ * propagates.  cols % block == 0, fp8_max > 0. */
+int tcfp_block_scales(const void* x, int x_dtype, int64_t rows, int64_t cols, int block,
+                      float fp8_max, void* scales, void* stream);
+
 /* Per-tensor quantisation that also returns the column sums of x
  * (col_sum [cols] fp32 = sum over rows), read in the same pass as the
  * amax.  For the gradient this is the bias gradient the reference computes

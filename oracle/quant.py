@@ -233,6 +233,42 @@ def sr_candidates_per_tensor(x: np.ndarray):
     return lo, hi.astype(np.uint8), frac.astype(F32), exact
 
 
+def compute_block_scales(x: np.ndarray, bs: int, fp8_max: float = 448.0,
+                         dtype: str = "f32") -> np.ndarray:
+    """``compute_block_scales`` (core.py:221-252): ``2^ceil(log2(amax / fp8_max))``
+    per run of ``bs`` elements along the last axis, in the tensor's dtype.
+
+    Every step rounds to ``dtype`` as torch's ops on that dtype do:
+    ``amax.clamp(min=1e-12)`` (the bound itself rounded to the dtype; NaN
+    passes), ``amax / fp8_max`` (fp32 quotient, rounded), ``log2`` (an fp32
+    log2 rounded to the dtype: for bf16 that 8-bit rounding can pull a value
+    just above an integer down onto it), ``ceil`` and ``exp2``.  fp32
+    ``ceil(log2)`` follows :func:`ceil_log2_f32` for normal quotients.
+    Returns float32 arrays holding the dtype's values, shape
+    ``x.shape[:-1] + (x.shape[-1] // bs,)``.
+    """
+    x = np.asarray(x, dtype=F32)
+    *lead, d = x.shape
+    assert d % bs == 0
+    blocks = x.reshape(*lead, d // bs, bs)
+    with np.errstate(invalid="ignore"):
+        amax = np.max(np.abs(blocks), axis=-1) if bs else np.zeros(blocks.shape[:-1], F32)
+    lo = _round_dtype(np.array([1e-12], F32), dtype)[0]
+    amax = np.where(np.isnan(amax), amax, np.maximum(amax, lo)).astype(F32)
+    q = _round_dtype((amax / F32(fp8_max)).astype(F32), dtype)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        l32 = np.log2(q.astype(np.float64)).astype(F32)
+    if dtype == "bf16":
+        e = np.ceil(bf16_round(l32).astype(np.float64))
+    else:
+        normal = np.isfinite(q) & (q >= F32(2.0 ** -126))
+        e = np.where(normal, ceil_log2_f32(np.where(normal, q, F32(1))).astype(np.float64),
+                     np.ceil(l32.astype(np.float64)))
+    with np.errstate(over="ignore"):
+        out = np.exp2(e).astype(F32)
+    return _round_dtype(out, dtype).reshape(*lead, d // bs)
+
+
 def _blocks(x: np.ndarray, bs: int) -> np.ndarray:
     m, k = x.shape
     assert k % bs == 0

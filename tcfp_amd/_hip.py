@@ -31,6 +31,10 @@ _SIGNATURES = {
     "tcfp_workspace_bytes": [],
     "tcfp_quantize_per_tensor": [_c_void_p, _i32, _i64, _i64, _i32, _c_void_p, _c_void_p,
                                  _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p],
+    "tcfp_quantize_per_tensor_sr": [_c_void_p, _i32, _i64, _i64, _c_void_p, _u64, _u64,
+                                    _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p],
+    "tcfp_block_scales": [_c_void_p, _i32, _i64, _i64, _i32, ctypes.c_float, _c_void_p,
+                          _c_void_p],
     "tcfp_colsum_workspace_bytes": [_i64, _i64],
     "tcfp_quantize_per_tensor_colsum": [_c_void_p, _i32, _i64, _i64, _i32, _c_void_p, _c_void_p,
                                         _c_void_p, _c_void_p, _c_void_p, _c_void_p,

@@ -2,9 +2,13 @@
 
 ``to_fp8_e4m3`` / ``to_fp8_e5m2`` keep the reference's exact semantics
 (``tcfp/core.py:85-158``) -- codes and scales bit-identical -- but run as
-HIP kernels (one amax pass, one quantise pass, no host synchronisation).
-``ErrorFeedbackState`` is the reference's per-parameter buffer store
-(``tcfp/core.py:298-326``), keyed by parameter name.
+HIP kernels (one amax pass, one quantise pass, no host synchronisation);
+so do the stochastic-rounding casts (``to_fp8_e4m3_sr``,
+``stochastic_round_to_fp8_e4m3``), ``compute_block_scales`` and the FP8
+matmuls ``fp8_matmul`` / ``fp8_matmul_nn`` (the hand-written FP8 GEMM in
+place of ``torch._scaled_mm``).  ``ErrorFeedbackState`` is the reference's
+per-parameter buffer store (``tcfp/core.py:298-326``), keyed by parameter
+name.
 """
 from __future__ import annotations
 
@@ -24,6 +28,8 @@ FP8_E5M2_MIN: float = -57344.0
 
 DEFAULT_BLOCK_SIZE: int = 32
 VALID_BLOCK_SIZES: tuple[int, ...] = (16, 32, 64, 128)
+
+SCALE_EXPONENT_BIAS: int = 127
 
 
 class TCFPMode(Enum):
@@ -63,6 +69,29 @@ def to_fp8_e4m3(
     """
     q, inv = _k.quantize_per_tensor(tensor, torch.float8_e4m3fn, scale)
     return q, inv
+
+
+def to_fp8_e4m3_sr(
+    tensor: torch.Tensor,
+    scale: torch.Tensor | None = None,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Per-tensor FP8 E4M3 cast with stochastic rounding
+    (``tcfp/core.py:109-134``): the scale of :func:`to_fp8_e4m3`, then
+    :func:`stochastic_round_to_fp8_e4m3` on the scaled, clamped values, so
+    that ``E[dequant(quant(x))] = x``.  Returns ``(fp8, inv_scale)``."""
+    q, inv = _k.quantize_per_tensor_sr(tensor, scale)
+    return q, inv
+
+
+def stochastic_round_to_fp8_e4m3(tensor: torch.Tensor) -> torch.Tensor:
+    """FP8 E4M3 with stochastic rounding of values already in range
+    (``tcfp/core.py:418-464``): each value goes to its round-to-nearest code
+    or that code's neighbour toward it, the neighbour with probability
+    ``|x - lo| / |hi - lo|``; exact values keep their code.  (Values past
+    +-448, outside the reference's contract, saturate here.)"""
+    one = torch.ones(1, dtype=torch.float32, device=tensor.device)
+    q, _ = _k.quantize_per_tensor_sr(tensor, one)
+    return q
 
 
 def to_fp8_e5m2(
@@ -110,6 +139,83 @@ def ensure_column_major(t: torch.Tensor) -> torch.Tensor:
     if t.stride(0) == 1 and t.stride(1) == t.shape[0]:
         return t
     return t.t().contiguous().t()
+
+
+def compute_block_scales(
+    tensor: torch.Tensor,
+    block_size: int = DEFAULT_BLOCK_SIZE,
+    fp8_max: float = FP8_E4M3_MAX,
+) -> torch.Tensor:
+    """Power-of-two block scales ``2^ceil(log2(amax / fp8_max))`` of each
+    run of ``block_size`` elements along the last dimension
+    (``tcfp/core.py:221-252``), shape ``(..., D // block_size)``, in the
+    tensor's dtype (fp32 or bf16; each step rounds as torch's ops on that
+    dtype round)."""
+    *_, D = tensor.shape
+    assert D % block_size == 0, f"D ({D}) must be divisible by block_size ({block_size})"
+    return _k.block_scales(tensor, block_size, fp8_max)
+
+
+def apply_block_scales(
+    tensor: torch.Tensor,
+    scales: torch.Tensor,
+    block_size: int = DEFAULT_BLOCK_SIZE,
+) -> torch.Tensor:
+    """``tensor / scales`` broadcast over each block (``tcfp/core.py:467-490``)."""
+    *batch_dims, D = tensor.shape
+    blocked = tensor.reshape(*batch_dims, D // block_size, block_size)
+    return (blocked / scales.unsqueeze(-1)).reshape(*batch_dims, D)
+
+
+def reverse_block_scales(
+    tensor: torch.Tensor,
+    scales: torch.Tensor,
+    block_size: int = DEFAULT_BLOCK_SIZE,
+) -> torch.Tensor:
+    """``tensor * scales`` broadcast over each block (``tcfp/core.py:493-513``)."""
+    *batch_dims, D = tensor.shape
+    blocked = tensor.reshape(*batch_dims, D // block_size, block_size)
+    return (blocked * scales.unsqueeze(-1)).reshape(*batch_dims, D)
+
+
+def fp8_matmul(
+    a_fp8: torch.Tensor,
+    b_fp8: torch.Tensor,
+    scale_a: torch.Tensor,
+    scale_b: torch.Tensor,
+    out_dtype: torch.dtype = torch.float32,
+) -> torch.Tensor:
+    """``(a_fp8 * scale_a) @ (b_fp8 * scale_b)`` on the FP8 MFMA
+    (``tcfp/core.py:519-553``, where ``torch._scaled_mm`` does it).
+
+    a [M, K], b [K, N] FP8 (E4M3 or E5M2); per-tensor (single-element) fp32
+    scales, i.e. the inverse scales the casts return; fp32 or bf16 output.
+    The GEMM reads both operands K-contiguous, so a row-major b is
+    transposed once (a column-major b is used as is)."""
+    b_t = b_fp8.t()
+    if not b_t.is_contiguous():
+        b_t = _k.transpose_fp8(b_fp8)
+    return _k.fp8_gemm_nt(a_fp8, b_t, scale_a, scale_b, out_dtype=out_dtype)
+
+
+def fp8_matmul_nn(
+    a_fp8: torch.Tensor,
+    b_fp8_t: torch.Tensor,
+    scale_a: torch.Tensor,
+    scale_b: torch.Tensor,
+    out_dtype: torch.dtype = torch.float32,
+) -> torch.Tensor:
+    """:func:`fp8_matmul` with B given transposed, ``b_fp8_t`` [N, K]
+    (``tcfp/core.py:556-578``): ``(a * scale_a) @ (b_fp8_t * scale_b).T``."""
+    return _k.fp8_gemm_nt(a_fp8, b_fp8_t, scale_a, scale_b, out_dtype=out_dtype)
+
+
+def bits_per_value(mode: TCFPMode, block_size: int = DEFAULT_BLOCK_SIZE) -> float:
+    """Effective bits per value (``tcfp/core.py:586-603``): 8 + 4 plus two
+    8-bit block scales amortised over ``block_size`` values."""
+    if mode == TCFPMode.TCFP12:
+        return 8.0 + 4.0 + 2 * (8.0 / block_size)
+    raise ValueError(f"Unknown mode: {mode}")
 
 
 class ErrorFeedbackState:

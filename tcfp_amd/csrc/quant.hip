@@ -1089,6 +1089,101 @@ __global__ __launch_bounds__(kThreads) void dualq_lo_t_kernel(
   if (lo_t) store_transposed(tile_l, tg, rows, cols, lo_t, threadIdx.x);
 }
 // ===========================================================================
+// Per-tensor stochastic rounding (to_fp8_e4m3_sr, tcfp/core.py:109-134)
+// ===========================================================================
+// c = clamp(x * scale) with the per-tensor scale rule (or a given scale),
+// then the stochastic_round_to_fp8_e4m3 rule (tcfp/core.py:418-464) on c:
+// RNE candidate, its neighbour toward c, up with probability |c - lo| / gap.
+// Element e of a 4-element group starting at flat index e0 draws word
+// (e - e0) of Philox4x32-10 counter (e0 / 4, 0, offset); a tail element t
+// (past the last 8-element vector) draws counter 2^62 + t.  The draw of an
+// element depends on its index only, not on the launch shape.
+template <typename InT>
+__global__ __launch_bounds__(kThreads) void quant_sr_kernel(
+    const InT* __restrict__ x, int64_t n, const uint32_t* __restrict__ part, int g, int bf16_rule,
+    const float* __restrict__ scale_in, uint8_t* __restrict__ q, float* scale_out, float* inv_out,
+    uint32_t k0, uint32_t k1, uint32_t o0, uint32_t o1) {
+  __shared__ uint32_t red[kThreads / 64];
+  const float s = consumer_scale(scale_in, part, g, bf16_rule != 0, kE4M3Max, scale_out, inv_out,
+                                 red);
+  const int64_t nvec = n >> 3;
+  const int64_t stride = int64_t(gridDim.x) * kThreads;
+  for (int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x; i < nvec; i += stride) {
+    float v[8];
+    load8(x + i * 8, v);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = clampf(v[j] * s, kE4M3Max);
+    const uint32_t c0 = lo_codes4<true>(v, i * 8, k0, k1, o0, o1);
+    const uint32_t c1 = lo_codes4<true>(v + 4, i * 8 + 4, k0, k1, o0, o1);
+    *reinterpret_cast<uint2*>(q + i * 8) = make_uint2(c0, c1);
+  }
+  for (int64_t t = nvec * 8 + int64_t(blockIdx.x) * kThreads + threadIdx.x; t < n; t += stride) {
+    const float c = clampf(load1(x + t) * s, kE4M3Max);
+    const uint64_t ctr = (uint64_t(1) << 62) + uint64_t(t);
+    const u32x4 r = philox4x32_10({uint32_t(ctr), uint32_t(ctr >> 32), o0, o1}, k0, k1);
+    q[t] = uint8_t(sr_per_tensor(c, u32_to_unit(r.x)));
+  }
+}
+
+// ===========================================================================
+// Power-of-two block scales (compute_block_scales, tcfp/core.py:221-252)
+// ===========================================================================
+// scale = 2^ceil(log2(max(amax, 1e-12) / fp8_max)) per run of `block`
+// elements, every step rounded to the input dtype as torch's ops round it:
+//   fp32: q = amax / fp8_max (IEEE), ceil(log2 q) by the exact integer rule
+//         of a correctly rounded fp32 log2 (ceil_log2_f32), 2^e;
+//   bf16: the 1e-12 bound and q rounded to bf16, log2 q evaluated in fp32
+//         (an fp64 log2 rounded once) and rounded to bf16 -- that 8-bit
+//         rounding can pull a value just above an integer down onto it --
+//         then ceil, 2^e rounded to bf16.
+// NaN propagates; q = 0 gives 0 and q = inf gives inf, as log2/exp2 do.
+TCFP_DEV float pow2_of(float e) {
+  if (e != e) return e;
+  if (e >= 128.0f) return __uint_as_float(0x7F800000u);
+  if (e < -149.0f) return 0.0f;
+  return exp2i(int(e));
+}
+
+TCFP_DEV float block_scale_f32(float amax, float fmax) {
+  if (amax != amax) return amax;
+  const float q = __fdiv_rn(fmaxf(amax, 1e-12f), fmax);
+  if (q != q || q == 0.0f || q == __uint_as_float(0x7F800000u)) return q;
+  if (q >= 1.17549435e-38f) return pow2_of(float(ceil_log2_f32(q)));
+  return pow2_of(ceilf(float(log2(double(q)))));  // subnormal quotient
+}
+
+TCFP_DEV float block_scale_bf16(float amax, float fmax) {
+  if (amax != amax) return amax;
+  const float q = round_bf16(__fdiv_rn(fmaxf(amax, round_bf16(1e-12f)), fmax));
+  if (q != q || q == 0.0f || q == __uint_as_float(0x7F800000u)) return q;
+  const float l = round_bf16(float(log2(double(q))));
+  return round_bf16(pow2_of(ceilf(l)));
+}
+
+TCFP_DEV float abs_load(const float* p) { return fabsf(*p); }
+TCFP_DEV float abs_load(const uint16_t* p) { return fabsf(bf16_to_f32(*p)); }
+TCFP_DEV void store_scale(float* p, float v) { *p = v; }
+TCFP_DEV void store_scale(uint16_t* p, float v) { *p = f32_to_bf16_rne(v); }
+
+// One block per lane: a lane reads its `block` consecutive elements.
+template <typename InT>
+__global__ __launch_bounds__(kThreads) void block_scales_kernel(const InT* __restrict__ x,
+                                                                int64_t nblocks, int block,
+                                                                float fmax,
+                                                                InT* __restrict__ out) {
+  const int64_t stride = int64_t(gridDim.x) * kThreads;
+  for (int64_t b = int64_t(blockIdx.x) * kThreads + threadIdx.x; b < nblocks; b += stride) {
+    const InT* p = x + b * block;
+    float m = 0.0f;
+    for (int i = 0; i < block; ++i) m = nanmax(m, abs_load(p + i));
+    if constexpr (sizeof(InT) == 4)
+      store_scale(out + b, block_scale_f32(m, fmax));
+    else
+      store_scale(out + b, block_scale_bf16(m, fmax));
+  }
+}
+
+// ===========================================================================
 // Block quantisation (tcfp/kernels.py:205-275)
 // ===========================================================================
 
@@ -1783,6 +1878,63 @@ int tcfp_quantize_per_tensor(const void* x, int x_dtype, int64_t rows, int64_t c
                              void* stream) {
   return quantize_impl(x, x_dtype, rows, cols, fp8_fmt, scale_in, q, q_t, scale_out, inv_out,
                        workspace, nullptr, nullptr, static_cast<hipStream_t>(stream));
+}
+
+int tcfp_quantize_per_tensor_sr(const void* x, int x_dtype, int64_t rows, int64_t cols,
+                                const float* scale_in, uint64_t seed, uint64_t offset,
+                                uint8_t* q, float* scale_out, float* inv_out, void* workspace,
+                                void* stream) {
+  if (rows < 0 || cols < 0) return TCFP_ERR_SHAPE;
+  if (x_dtype != TCFP_DTYPE_F32 && x_dtype != TCFP_DTYPE_BF16) return TCFP_ERR_DTYPE;
+  if (!aligned16(x) || !inv_out) return TCFP_ERR_ALIGN;
+  if (!scale_in && !workspace) return TCFP_ERR_WORKSPACE;
+  const int64_t n = rows * cols;
+  if (n >= 8 && (reinterpret_cast<uintptr_t>(q) & 7u) != 0) return TCFP_ERR_ALIGN;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  PartWs* ws = static_cast<PartWs*>(workspace);
+  uint32_t* part = ws ? ws->a : nullptr;
+  const bool bf = x_dtype == TCFP_DTYPE_BF16;
+  int g = 0;
+  if (!scale_in) {
+    g = parts_for((n + 7) / 8);
+    if (bf)
+      amax_part_kernel<uint16_t, false, false><<<g, kThreads, 0, st>>>(
+          static_cast<const uint16_t*>(x), nullptr, n, part, nullptr, nullptr);
+    else
+      amax_part_kernel<float, false, false><<<g, kThreads, 0, st>>>(
+          static_cast<const float*>(x), nullptr, n, part, nullptr, nullptr);
+  }
+  const int gq = grid_for((n + 7) / 8, 8);
+  const uint32_t k0 = uint32_t(seed), k1 = uint32_t(seed >> 32);
+  const uint32_t o0 = uint32_t(offset), o1 = uint32_t(offset >> 32);
+  if (bf)
+    quant_sr_kernel<uint16_t><<<gq, kThreads, 0, st>>>(static_cast<const uint16_t*>(x), n, part,
+                                                       g, 1, scale_in, q, scale_out, inv_out, k0,
+                                                       k1, o0, o1);
+  else
+    quant_sr_kernel<float><<<gq, kThreads, 0, st>>>(static_cast<const float*>(x), n, part, g, 0,
+                                                    scale_in, q, scale_out, inv_out, k0, k1, o0,
+                                                    o1);
+  return launch_status();
+}
+
+int tcfp_block_scales(const void* x, int x_dtype, int64_t rows, int64_t cols, int block,
+                      float fp8_max, void* scales, void* stream) {
+  if (rows < 0 || cols < 0 || block <= 0 || cols % block != 0) return TCFP_ERR_SHAPE;
+  if (!(fp8_max > 0.0f)) return TCFP_ERR_SHAPE;
+  if (x_dtype != TCFP_DTYPE_F32 && x_dtype != TCFP_DTYPE_BF16) return TCFP_ERR_DTYPE;
+  const int64_t nblocks = rows * (cols / block);
+  if (nblocks == 0) return TCFP_OK;
+  if (!x || !scales) return TCFP_ERR_SHAPE;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int gb = grid_for(nblocks, 8);
+  if (x_dtype == TCFP_DTYPE_BF16)
+    block_scales_kernel<uint16_t><<<gb, kThreads, 0, st>>>(
+        static_cast<const uint16_t*>(x), nblocks, block, fp8_max, static_cast<uint16_t*>(scales));
+  else
+    block_scales_kernel<float><<<gb, kThreads, 0, st>>>(
+        static_cast<const float*>(x), nblocks, block, fp8_max, static_cast<float*>(scales));
+  return launch_status();
 }
 
 size_t tcfp_colsum_workspace_bytes(int64_t rows, int64_t cols) {

@@ -121,6 +121,69 @@ def quantize_per_tensor(
     return out
 
 
+def quantize_per_tensor_sr(
+    x: torch.Tensor,
+    scale: torch.Tensor | None = None,
+    seed: int | None = None,
+    return_scale: bool = False,
+):
+    """Per-tensor FP8 E4M3 cast with stochastic rounding (``to_fp8_e4m3_sr``
+    semantics, reference ``tcfp/core.py:109-134`` -> ``stochastic_round_to_
+    fp8_e4m3``, ``:418-464``).  The scale follows the amax rule of
+    :func:`quantize_per_tensor` (or ``scale``); each code is the round-to-
+    nearest candidate or its neighbour toward the scaled value, chosen with
+    the reference's probability from a Philox4x32-10 stream keyed by
+    ``seed`` (drawn from torch's CPU generator when None).  Returns ``(q,
+    inv)`` (plus the fp32 ``scale`` with ``return_scale``)."""
+    dev = _hip.require_gpu(x, scale)
+    xc = x if x.is_contiguous() else x.contiguous()
+    cols = xc.shape[-1] if xc.dim() > 0 else 1
+    rows = xc.numel() // cols if cols else 0
+    q = torch.empty(x.shape, dtype=torch.float8_e4m3fn, device=dev)
+    inv = torch.empty(1, dtype=torch.float32, device=dev)
+    scale_out = torch.empty(1, dtype=torch.float32, device=dev) if return_scale else None
+    s_in = _scalar(scale.to(torch.float32), "scale") if scale is not None else None
+    ws = _hip.workspace(dev) if scale is None else None
+    if seed is None:
+        seed = int(torch.randint(0, 2**62, (1,)).item())
+    check(
+        _hip.lib().tcfp_quantize_per_tensor_sr(
+            ptr(xc), _in_dtype(xc), rows, cols, ptr(s_in), int(seed), 0, ptr(q), ptr(scale_out),
+            ptr(inv), ptr(ws), _hip.stream_of(dev),
+        ),
+        "quantize_per_tensor_sr",
+    )
+    return (q, inv, scale_out) if return_scale else (q, inv)
+
+
+def block_scales(
+    x: torch.Tensor,
+    block_size: int,
+    fp8_max: float = _FP8_E4M3_MAX,
+) -> torch.Tensor:
+    """Power-of-two block scales ``2^ceil(log2(amax / fp8_max))`` per run of
+    ``block_size`` elements along the last axis, in ``x``'s dtype (fp32 or
+    bf16), shape ``x.shape[:-1] + (D // block_size,)`` (reference
+    ``compute_block_scales``, ``tcfp/core.py:221-252``)."""
+    dev = _hip.require_gpu(x)
+    if x.dtype not in (torch.float32, torch.bfloat16):
+        raise TypeError(f"block scales support float32 and bfloat16 tensors, got {x.dtype}")
+    if x.dim() == 0:
+        raise ValueError("block scales need at least one dimension")
+    d = x.shape[-1]
+    xc = x if x.is_contiguous() else x.contiguous()
+    rows = xc.numel() // d if d else 0
+    out = torch.empty((*x.shape[:-1], d // block_size), dtype=x.dtype, device=dev)
+    check(
+        _hip.lib().tcfp_block_scales(
+            ptr(xc), _in_dtype(xc), rows, d, int(block_size), float(fp8_max), ptr(out),
+            _hip.stream_of(dev),
+        ),
+        "block_scales",
+    )
+    return out
+
+
 def quantize_per_tensor_colsum(
     x: torch.Tensor,
     fp8_dtype: torch.dtype = torch.float8_e5m2,
@@ -910,7 +973,7 @@ def fused_wtquant_block_scaled_dual_gemm_forward(
     return out, w_hi, None, s_hi, None
 
 
-def fused_block_scaled_dual_gemm_backward_dx(
+def fused_block_scaled_backward_dx(
     grad_fp8: torch.Tensor,
     w_hi_fp8: torch.Tensor,
     w_lo_fp8: torch.Tensor | None,
@@ -918,11 +981,14 @@ def fused_block_scaled_dual_gemm_backward_dx(
     w_hi_scales: torch.Tensor,
     w_lo_scales: torch.Tensor | None,
     block_size: int,
+    persistent: bool = True,
+    launch_mult: int = 1,
 ) -> torch.Tensor:
     """``dX = deq(grad) @ (deq(W_hi) + deq(W_lo))``, fp32 [M, D_in].
 
-    Reference: ``fused_block_scaled_dual_gemm_backward_dx``
-    (``tcfp/kernels.py:2428-2469``, kernel ``:1051-1205``).  grad [M, D_out]
+    Reference: ``fused_block_scaled_backward_dx`` (``tcfp/kernels.py:
+    2326-2425``, kernel ``:1051-1205``); ``persistent`` / ``launch_mult`` are
+    its scheduling hints and do not change the result.  grad [M, D_out]
     (E5M2 or E4M3) with exponents [D_out // bs, M]; W [D_out, D_in] E4M3
     with exponents [D_in // bs, D_out].  The W exponents change along the
     contraction index, so the operands are dequantised exactly into bf16
@@ -959,6 +1025,22 @@ def fused_block_scaled_dual_gemm_backward_dx(
         "block_dual_gemm_dx",
     )
     return out
+
+
+def fused_block_scaled_dual_gemm_backward_dx(
+    grad_fp8: torch.Tensor,
+    w_hi_fp8: torch.Tensor,
+    w_lo_fp8: torch.Tensor | None,
+    grad_scales: torch.Tensor,
+    w_hi_scales: torch.Tensor,
+    w_lo_scales: torch.Tensor | None,
+    block_size: int,
+) -> torch.Tensor:
+    """Block dgrad dispatcher (reference ``tcfp/kernels.py:2428-2469``): the
+    reference sends it to :func:`fused_block_scaled_backward_dx` whenever its
+    fused tier is available, and here that tier always is."""
+    return fused_block_scaled_backward_dx(grad_fp8, w_hi_fp8, w_lo_fp8, grad_scales, w_hi_scales,
+                                          w_lo_scales, block_size)
 
 
 def block_scaled_wgrad(

@@ -17,6 +17,7 @@ import numpy as np
 import torch
 
 OUT = Path(__file__).with_name("torch_primitives.npz")
+OUT_BLOCK_SCALES = Path(__file__).with_name("torch_block_scales.npz")
 
 
 def main() -> None:
@@ -72,5 +73,41 @@ def main() -> None:
     print("wrote", OUT, OUT.stat().st_size, "bytes")
 
 
+def _block_scales_formula(t: torch.Tensor, bs: int, fp8_max: float) -> torch.Tensor:
+    """The op sequence of the reference's compute_block_scales
+    (tcfp/core.py:243-251), evaluated by torch on the CPU."""
+    *lead, d = t.shape
+    amax = t.reshape(*lead, d // bs, bs).abs().amax(dim=-1).clamp(min=1e-12)
+    return torch.exp2(torch.ceil(torch.log2(amax / fp8_max)))
+
+
+def block_scales() -> None:
+    """torch CPU outputs of the block-scale rule: every positive finite bf16
+    quotient through bf16 log2 / ceil / exp2, and seeded fp32 / bf16 tensors
+    (with zero, tiny, NaN and inf blocks) at block sizes 16..128."""
+    rng = np.random.default_rng(20261202)
+    bits = np.arange(1, 0x7F80, dtype=np.uint32)
+    q = (bits << 16).view(np.float32)
+    qb = torch.from_numpy(q.copy()).bfloat16()
+    pow2_bf16 = torch.exp2(torch.ceil(torch.log2(qb))).float().numpy()
+    out = {"q_bf16": q, "pow2_bf16": pow2_bf16}
+    for dt in ("f32", "bf16"):
+        x = (rng.standard_normal((48, 256)) * 2.0 ** rng.integers(-60, 60, (48, 1))).astype(np.float32)
+        x[0] = 0.0
+        x[1] = 1e-20
+        x[2, 5] = np.nan
+        x[3, 7] = np.inf
+        t = torch.from_numpy(x)
+        if dt == "bf16":
+            t = t.bfloat16()
+        out[f"x_{dt}"] = t.float().numpy()
+        for bs in (16, 32, 64, 128):
+            for fm in (448.0, 57344.0):
+                out[f"s_{dt}_{bs}_{int(fm)}"] = _block_scales_formula(t, bs, fm).float().numpy()
+    np.savez_compressed(OUT_BLOCK_SCALES, **out, torch_version=np.array(torch.__version__))
+    print("wrote", OUT_BLOCK_SCALES, OUT_BLOCK_SCALES.stat().st_size, "bytes")
+
+
 if __name__ == "__main__":
     main()
+    block_scales()

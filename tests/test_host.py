@@ -274,3 +274,79 @@ def test_set_block_dgrad_modes():
     finally:
         tnn.set_block_dgrad("exact")
     assert tnn._BLOCK_DGRAD == "exact"
+
+
+# names a user of the reference imports (tcfp/__init__.py:12-34; tcfp/core.py
+# public functions; the operator layer of tcfp/kernels.py and tcfp/cuda_ext.py
+# that tcfp/nn/__init__.py:40-66 binds; the tcfp.nn surface)
+_REFERENCE_NAMES = {
+    "tcfp": ["ErrorFeedbackState", "FP8Config", "TCFPMode", "ensure_column_major",
+             "fp8_matmul", "to_fp8_e4m3", "to_fp8_e4m3_nf_aware", "to_fp8_e4m3_sr",
+             "to_fp8_e5m2", "__version__"],
+    "tcfp.core": ["FP8_E4M3_MAX", "FP8_E4M3_MIN", "FP8_E4M3_SMALLEST_NORMAL", "FP8_E5M2_MAX",
+                  "FP8_E5M2_MIN", "DEFAULT_BLOCK_SIZE", "VALID_BLOCK_SIZES",
+                  "SCALE_EXPONENT_BIAS", "TCFPMode", "FP8Config", "to_fp8_e4m3",
+                  "to_fp8_e4m3_sr", "to_fp8_e5m2", "to_fp8_e4m3_nf_aware",
+                  "ensure_column_major", "compute_block_scales", "ErrorFeedbackState",
+                  "stochastic_round_to_fp8_e4m3", "apply_block_scales",
+                  "reverse_block_scales", "fp8_matmul", "fp8_matmul_nn", "bits_per_value"],
+    "tcfp.kernels": ["is_triton_available", "fused_dual_gemm_forward",
+                     "fused_dual_gemm_backward_dx", "block_quantize_fp8",
+                     "block_dequantize_fp8", "fused_dual_quantize_fp8", "block_scaled_gemm",
+                     "fused_block_scaled_dual_gemm_forward", "fused_act_quant_dual_gemm_forward",
+                     "fused_wtquant_block_scaled_dual_gemm_forward",
+                     "fused_block_scaled_backward_dx",
+                     "fused_block_scaled_dual_gemm_backward_dx"],
+    "tcfp.cuda_ext": ["is_cuda_ext_available", "cuda_ext_dual_gemm_forward",
+                      "cuda_ext_dual_gemm_backward_dx"],
+    "tcfp.nn": ["TCFPLinear", "convert_to_tcfp", "_TCFP12TensorCoreFunction",
+                "_TCFP12BlockScaledFunction"],
+}
+
+
+def test_reference_import_names_resolve_to_this_build():
+    import importlib
+    import sys
+
+    import tcfp_amd
+
+    for mod_name, names in _REFERENCE_NAMES.items():
+        mod = importlib.import_module(mod_name)
+        # the same module objects, not copies
+        assert mod is sys.modules[mod_name.replace("tcfp", "tcfp_amd", 1)], mod_name
+        missing = [n for n in names if not hasattr(mod, n)]
+        assert not missing, (mod_name, missing)
+    import tcfp
+
+    assert tcfp is tcfp_amd
+    from tcfp.nn import TCFPLinear as A
+
+    assert A is TCFPLinear
+    ns = {}
+    exec("from tcfp import *", ns)
+    assert set(tcfp.__all__) <= set(ns)
+
+
+def test_core_host_helpers_match_reference_behaviour():
+    from tcfp.core import (
+        FP8Config,
+        TCFPMode,
+        apply_block_scales,
+        bits_per_value,
+        reverse_block_scales,
+    )
+
+    assert bits_per_value(TCFPMode.TCFP12) == 12.5
+    assert bits_per_value(TCFPMode.TCFP12, 64) == 12.25
+    cfg = FP8Config()
+    assert cfg.block_size == 32 and cfg.e4m3_for_weights and cfg.e5m2_for_grads
+    # block scaling helpers are plain broadcast arithmetic (CPU tensors here)
+    x = torch.randn(4, 64)
+    s = torch.tensor([[2.0, 0.5]] * 4)
+    y = apply_block_scales(x, s, 32)
+    assert torch.equal(y[:, :32], x[:, :32] / 2.0) and torch.equal(y[:, 32:], x[:, 32:] / 0.5)
+    assert torch.equal(reverse_block_scales(y, s, 32), x)
+    with pytest.raises(AssertionError, match="divisible"):
+        from tcfp.core import compute_block_scales
+
+        compute_block_scales(torch.randn(4, 48), 32)

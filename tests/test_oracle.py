@@ -17,6 +17,7 @@ from oracle import gemm as og
 from oracle import quant as oq
 
 GOLD = np.load(Path(__file__).parent / "golden" / "torch_primitives.npz")
+GOLD_BS = np.load(Path(__file__).parent / "golden" / "torch_block_scales.npz")
 
 
 # ---------------------------------------------------------------- fp8 casts
@@ -357,6 +358,42 @@ def test_nf_dual_quant_composition():
 
 
 # ------------------------------------------------------- block quant (a4)
+# ---------------------------------------------------- compute_block_scales
+def test_block_scales_bf16_log2_rounding_over_every_bf16_quotient():
+    """torch's bf16 ``exp2(ceil(log2(q)))`` for all 32639 positive finite
+    bf16 q: the oracle's fp32 log2 rounded to bf16 reproduces it (a log2
+    kept in fp32 would not: just above an integer it differs)."""
+    q = GOLD_BS["q_bf16"]
+    mine = oq.compute_block_scales(q.reshape(-1, 1), 1, 1.0, "bf16").ravel()
+    keep = q >= np.float32(1.0018652574217413e-12)  # above the clamp
+    assert np.array_equal(mine[keep], GOLD_BS["pow2_bf16"][keep])
+    # the fp32 rule disagrees with the bf16 one on many of these
+    f32 = np.exp2(np.ceil(np.log2(q[keep].astype(np.float64)))).astype(np.float32)
+    assert np.sum(f32 != GOLD_BS["pow2_bf16"][keep]) > 1000
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+@pytest.mark.parametrize("bs", [16, 32, 64, 128])
+@pytest.mark.parametrize("fm", [448.0, 57344.0])
+def test_block_scales_match_torch_formula(dt, bs, fm):
+    """The reference's compute_block_scales op sequence on torch CPU (zero,
+    below-clamp, NaN and inf blocks included) equals the oracle."""
+    x = GOLD_BS[f"x_{dt}"]
+    ref = GOLD_BS[f"s_{dt}_{bs}_{int(fm)}"]
+    mine = oq.compute_block_scales(x, bs, fm, dt)
+    assert mine.shape == ref.shape == (x.shape[0], x.shape[1] // bs)
+    assert np.array_equal(mine, ref, equal_nan=True)
+    # powers of two (or 0 / inf / NaN) that bring each block under fp8_max:
+    # within fp32's log2 rounding margin, or under 2x fp8_max in bf16, whose
+    # 8-bit log2 can round a quotient just above 2^k down to k (the
+    # reference's own test allows that factor, tests/test_core.py:101-108)
+    fin = np.isfinite(ref) & (ref > 0)
+    m, e = np.frexp(ref[fin])
+    assert np.all(m == 0.5)
+    amax = np.abs(x.reshape(x.shape[0], -1, bs)).max(-1)[fin]
+    bound = fm * (1 + 2 ** -17) if dt == "f32" else 2 * fm
+    assert np.all(amax / ref[fin] <= bound)
+
 @pytest.mark.parametrize("bs", [32, 64, 128])
 def test_block_quantize_exponent_and_codes(bs):
     import torch
@@ -545,3 +582,40 @@ def test_torch_ref_step_matches_numpy_oracle():
     assert og.rel_fro(xr.grad.float().numpy(), G @ Wd) < 1e-2  # dX returned in bf16
     A = ofp8.decode(aq, ofp8.E4M3).astype(np.float64) * ai
     assert og.rel_fro(Wr.grad.numpy(), G.T @ A) < 1e-6
+
+
+def test_torch_ref_block_step_matches_numpy_oracle():
+    """oracle/torch_ref.py's block-scaled restatement (the TinyGPT loss
+    parity reference) against the numpy oracle on CPU: codes, exponents,
+    the sentinel, EF, forward and the three backward products."""
+    import torch
+
+    from oracle import torch_ref as tr
+
+    g = torch.Generator().manual_seed(6)
+    x = torch.randn(2, 48, 128, generator=g)
+    W = torch.randn(64, 128, generator=g) * 0.05
+    W[:, :64] = torch.round(W[:, :64] * 64) / 64  # exactly representable: zero residual blocks
+    b = torch.randn(64, generator=g)
+    ef = {}
+    xr = x.clone().requires_grad_(True)
+    Wr = W.clone().requires_grad_(True)
+    out = tr.RefBlockTCFP12Function.apply(xr, Wr, b, ef, "", True, 64)
+    gout = torch.randn(2, 48, 64, generator=g)
+    out.backward(gout)
+    hi, lo, e_hi, e_lo, ef_new = oq.block_dual_quantize(W.numpy(), 64, np.zeros((64, 128), np.float32))
+    assert (e_lo == -128).any() and (e_lo != -128).any()
+    assert np.array_equal(ef[""].numpy(), ef_new)
+    # (+ the zero error buffer: -0.0 + 0.0 is +0.0, as in the kernels)
+    q_hi, s_hi = tr.block_quant(W + torch.zeros_like(W), 64, 448.0, torch.float8_e4m3fn)
+    assert np.array_equal(q_hi.view(torch.uint8).numpy(), hi)
+    assert np.array_equal(s_hi.numpy(), e_hi)
+    aq, ae = oq.block_quantize(x.reshape(-1, 128).numpy(), 64)
+    ref = og.block_dual_gemm_nt(aq, ae, hi, lo, e_hi, e_lo, 64) + b.double().numpy()
+    assert og.rel_fro(out.detach().reshape(-1, 64).numpy(), ref) < 1e-6
+    gq, ge = oq.block_quantize(gout.reshape(-1, 64).numpy(), 64, ofp8.E5M2)
+    dx = og.block_dgrad(gq, ge, hi, lo, e_hi, e_lo, 64)
+    assert og.rel_fro(xr.grad.reshape(-1, 128).numpy(), dx) < 1e-6
+    A = og.block_deq64(aq, ae, 64)
+    dw = gout.reshape(-1, 64).double().numpy().T @ A
+    assert og.rel_fro(Wr.grad.numpy(), dw) < 1e-6
