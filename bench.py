@@ -56,7 +56,9 @@ def event_time_ms(fn, iters, stream, warmup=3):
     return start.elapsed_time(end) / iters
 
 
-def bench_dual_gemm(steps, warmup):
+def c2_tensors():
+    """configs[1] operands resident in HBM: X = seeded bf16 N(0,1) quantised
+    per tensor, W = seeded fp32 N(0,1) dual-quantised (no EF)."""
     import torch
 
     from tcfp_amd import kernels as K
@@ -67,14 +69,44 @@ def bench_dual_gemm(steps, warmup):
     w = torch.randn(n, n, generator=torch.Generator().manual_seed(1)).to(dev)
     a, sa = K.quantize_per_tensor(xb)
     h, l, ih, il = K.dual_quantize_per_tensor(w)
+    torch.cuda.synchronize()
+    return (a, h, l, sa, ih, il, xb, w)
+
+
+def bench_dual_gemm(steps, warmup, t=None, sustained=0):
+    """The headline: ``warmup`` untimed launches, then exactly ``steps``
+    launches timed by wall clock (synchronised on both sides) and by HIP
+    events on the launch stream.
+
+    ``sustained`` > 0 first measures the same kernel back to back over that
+    many launches (HIP events; reported beside the headline).  From an idle
+    GPU -- even 50 ms idle -- the first ~200 launches run 120-143 us while
+    the board's power management ramps up, against 106-110 us back to back
+    (measured per 20 launches); the sustained run puts the headline's
+    timed steps in the working state a training loop keeps the GPU in."""
+    import torch
+
+    from tcfp_amd import kernels as K
+
+    dev = torch.device("cuda:0")
+    if t is None:
+        t = c2_tensors()
+    a, h, l, sa, ih, il, xb, w = t
+    n = a.shape[0]
     out = torch.empty(n, n, dtype=torch.bfloat16, device=dev)
 
     def step():
         return K.fused_dual_gemm_forward(a, h, l, sa, ih, il, out_dtype=torch.bfloat16)
 
+    stream = torch.cuda.current_stream(dev)
+    res = {}
+    if sustained:
+        ms = event_time_ms(step, sustained, stream, warmup=1)
+        res["sustained_launches"] = sustained
+        res["sustained_ms"] = ms
+        res["sustained_tflops"] = 2 * 2 * n**3 / (ms * 1e-3) / 1e12
     for _ in range(warmup):
         out = step()
-    stream = torch.cuda.current_stream(dev)
     torch.cuda.synchronize()
     ev0 = torch.cuda.Event(enable_timing=True)
     ev1 = torch.cuda.Event(enable_timing=True)
@@ -88,67 +120,64 @@ def bench_dual_gemm(steps, warmup):
     wall_ms = (t1 - t0) * 1e3 / steps
     kern_ms = ev0.elapsed_time(ev1) / steps
     flop = 2 * 2 * n**3
-    # parity of the timed output against a torch fp32 dequant matmul
-    ref = (a.float() * sa) @ (h.float() * ih + l.float() * il).t()
-    rel = ((out.float() - ref).norm() / ref.norm()).item()
-    return {
+    res.update({
         "n": n, "flop": flop, "wall_ms": wall_ms, "kern_ms": kern_ms,
         "tflops_wall": flop / (wall_ms * 1e-3) / 1e12,
         "tflops_kern": flop / (kern_ms * 1e-3) / 1e12,
-        "rel_fro": rel, "tensors": (a, h, l, sa, ih, il, xb, w),
-    }
+    })
+    # parity of the timed output against a torch fp32 dequant matmul
+    ref = (a.float() * sa) @ (h.float() * ih + l.float() * il).t()
+    res["rel_fro"] = ((out.float() - ref).norm() / ref.norm()).item()
+    res["tensors"] = t
+    return res
 
 
-def bench_comparators(t, iters=20):
+def bench_comparators(t, iters=200, heat=300, rounds=3):
+    """Library comparators at C2's shape, each measured in the same working
+    state as the dual GEMM: per round, ``heat`` untimed back-to-back calls
+    (the power ramp from idle lasts ~200 launches), then ``iters`` calls
+    timed by HIP events; the median over ``rounds`` interleaved rounds.
+    Arms: this build's dual GEMM on C2's data, hipBLASLt's single
+    ``torch._scaled_mm``, the reference's naive tier (2 x ``_scaled_mm`` +
+    add), BF16 ``torch.matmul``, and -- a diagnostic of the power limit, not
+    a result -- the dual GEMM on all-zero operands (no bit toggles in the
+    MFMA datapath)."""
     import torch
+
+    from tcfp_amd import kernels as K
 
     a, h, l, sa, ih, il, xb, w = t
     stream = torch.cuda.current_stream()
     n = a.shape[0]
-    res = {}
-    try:
-        def naive():
-            o1 = torch._scaled_mm(a, h.t(), scale_a=sa, scale_b=ih, out_dtype=torch.bfloat16)
-            o2 = torch._scaled_mm(a, l.t(), scale_a=sa, scale_b=il, out_dtype=torch.bfloat16)
-            return o1 + o2
-        naive()
-        ms = event_time_ms(naive, iters, stream)
-        res["naive_2x_scaled_mm_add_ms"] = ms
-        res["naive_2x_scaled_mm_add_tflops"] = 4 * n**3 / (ms * 1e-3) / 1e12
-
-        def single():
-            return torch._scaled_mm(a, h.t(), scale_a=sa, scale_b=ih, out_dtype=torch.bfloat16)
-        single()
-        ms = event_time_ms(single, iters, stream)
-        res["scaled_mm_single_ms"] = ms
-        res["scaled_mm_single_tflops"] = 2 * n**3 / (ms * 1e-3) / 1e12
-    except Exception as e:  # library path unavailable on this build
-        res["scaled_mm_error"] = str(e)[:200]
     wb = w.bfloat16()
-
-    def bf16():
-        return xb @ wb.t()
-    bf16()
-    ms = event_time_ms(bf16, iters, stream)
-    res["bf16_matmul_ms"] = ms
-    res["bf16_matmul_tflops"] = 2 * n**3 / (ms * 1e-3) / 1e12
-
-    # Diagnostic, not a result: the same dual GEMM on all-zero operands
-    # (no bit toggles in the MFMA datapath, so the least power per FLOP)
-    # against C2's data, back to back in this process.  The gap is what
-    # the board's power limit costs the real operands.
-    from tcfp_amd import kernels as K
-
     az, hz, lz = torch.zeros_like(a), torch.zeros_like(h), torch.zeros_like(l)
-
-    def dual(x, y, z):
-        return lambda: K.fused_dual_gemm_forward(x, y, z, sa, ih, il, out_dtype=torch.bfloat16)
-    for tag, args in (("c2_data", (a, h, l)), ("zero_operands", (az, hz, lz))):
-        f = dual(*args)
-        f()
-        ms = event_time_ms(f, 4 * iters, stream)
-        res[f"dual_{tag}_ms"] = ms
-        res[f"dual_{tag}_tflops"] = 4 * n**3 / (ms * 1e-3) / 1e12
+    arms = {
+        "dual_c2_data": (4, lambda: K.fused_dual_gemm_forward(a, h, l, sa, ih, il,
+                                                              out_dtype=torch.bfloat16)),
+        "scaled_mm_single": (2, lambda: torch._scaled_mm(a, h.t(), scale_a=sa, scale_b=ih,
+                                                         out_dtype=torch.bfloat16)),
+        "naive_2x_scaled_mm_add": (4, lambda: torch._scaled_mm(
+            a, h.t(), scale_a=sa, scale_b=ih, out_dtype=torch.bfloat16) + torch._scaled_mm(
+            a, l.t(), scale_a=sa, scale_b=il, out_dtype=torch.bfloat16)),
+        "bf16_matmul": (2, lambda: xb @ wb.t()),
+        "dual_zero_operands": (4, lambda: K.fused_dual_gemm_forward(
+            az, hz, lz, sa, ih, il, out_dtype=torch.bfloat16)),
+    }
+    res = {}
+    times = {k: [] for k in arms}
+    for _ in range(rounds):
+        for k, (_, fn) in list(arms.items()):
+            try:
+                times[k].append(event_time_ms(fn, iters, stream, warmup=heat))
+            except Exception as e:  # library path unavailable on this build
+                res[f"{k}_error"] = str(e)[:200]
+                arms.pop(k)
+    for k, (mult, _) in arms.items():
+        ms = statistics.median(times[k])
+        res[f"{k}_ms"] = ms
+        res[f"{k}_tflops"] = mult * n**3 / (ms * 1e-3) / 1e12
+    res["method"] = (f"per arm and round: {heat} untimed calls then {iters} timed (HIP events); "
+                     f"median of {rounds} interleaved rounds")
     return res
 
 
@@ -567,15 +596,17 @@ def main():
         log(f"[bench] part {args.part}")
         print(json.dumps({"part": args.part, **fn[args.part]()}), flush=True)
         return
-    log(f"[bench] dual GEMM 4096^3: warmup {args.warmup}, steps {args.steps}")
-    r = bench_dual_gemm(args.steps, args.warmup)
-    log(f"[bench] dual GEMM: {r['tflops_wall']:.1f} TFLOP/s wall, {r['tflops_kern']:.1f} "
-        f"TFLOP/s events, rel_fro {r['rel_fro']:.2e}")
     extras = {}
     cpu = None
+    t = c2_tensors()
     if args.part == "all":
+        # The secondary parts run first: they bring the GPU out of idle
+        # (clock ramp-up takes longer than a few warm-up launches), so the
+        # headline's timed steps see the clocks of a working GPU.
+        log("[bench] CPU baseline")
+        cpu = cpu_baseline(t)
         log("[bench] comparators")
-        extras["comparators_4096"] = bench_comparators(r["tensors"])
+        extras["comparators_4096"] = bench_comparators(t)
         log("[bench] block-scaled GEMMs (configs[2])")
         extras["block_scaled_4096"] = bench_block_gemms()
         log("[bench] dual quant")
@@ -584,8 +615,14 @@ def main():
         extras["mlp_train_step"] = bench_mlp()
         log("[bench] TinyGPT + scale-up layer (configs[4])")
         extras["c5"] = bench_c5()
-        log("[bench] CPU baseline")
-        cpu = cpu_baseline(r["tensors"])
+    log(f"[bench] dual GEMM 4096^3: warmup {args.warmup}, steps {args.steps}")
+    r = bench_dual_gemm(args.steps, args.warmup, t, sustained=4000)
+    log(f"[bench] dual GEMM: {r['tflops_wall']:.1f} TFLOP/s wall, {r['tflops_kern']:.1f} "
+        f"TFLOP/s events, rel_fro {r['rel_fro']:.2e}")
+    if "sustained_tflops" in r:
+        extras["sustained_back_to_back"] = {"launches": r["sustained_launches"],
+                                            "ms": r["sustained_ms"],
+                                            "tflops": r["sustained_tflops"]}
     achieved = r["tflops_kern"]
     line = {
         "metric": "dual-FP8 GEMM TFLOP/s @4096^3 (% FP8 MFMA peak); MLP train-step ms",

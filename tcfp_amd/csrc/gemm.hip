@@ -849,6 +849,19 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persist_kernel(GemmArgs g) {
                                                            127);
     }
   };
+  // The MFMAs of (fragment, m-block) pairs [lo, hi) stay where they are:
+  // an empty volatile asm that reads and writes their accumulators keeps
+  // the compiler from sinking them past the branches that follow (the
+  // barrier's wait count and the refill DMA depend on the stage), which
+  // would leave the matrix cores idle at every barrier.
+  auto pin_range = [&](int lo, int hi) {
+#pragma unroll
+    for (int idx = 0; idx < NP; ++idx) {
+      if (idx < lo || idx >= hi) continue;
+      const int i = idx / NF, q = idx % NF;
+      asm volatile("" : "+v"(acc[q / NB][q % NB][i]));
+    }
+  };
   // every DMA landed except the newest `keep` vector-memory operations
   // (the previous tile's output stores), every wave's LDS reads are done
   auto sync_keep = [&](auto keep) {
@@ -895,11 +908,13 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persist_kernel(GemmArgs g) {
       read_frags(f1, b, 1);
       mfmas_range(f0, 0, NP / 2);
       interleave_mfma_lds<NP / 2, 2 * (NF + MB), 0>();
+      pin_range(0, NP / 2);
       if (t == 0 && it > 0)
         sync_keep(std::integral_constant<int, NST>{});
       else
         sync_keep(std::integral_constant<int, 0>{});
       mfmas_range(f0, NP / 2, NP);
+      pin_range(NP / 2, NP);
       __builtin_amdgcn_sched_barrier(0);
       if (t + 2 < nt)
         issue(cur, t + 2, b);
