@@ -107,8 +107,13 @@ int tcfp_block_scales(const void* x, int x_dtype, int64_t rows, int64_t cols, in
  * quantisation at :494.  Scale rule as tcfp_quantize_per_tensor (no
  * explicit scale).  cols % 8 == 0; colsum_ws holds
  * tcfp_colsum_workspace_bytes(rows, cols) bytes of scratch (16-byte
- * aligned).  The sums are fp32 in a fixed order (per-row-group partials,
- * then their sum). */
+ * aligned).  The sums are fp32 in one fixed order, shared by every entry
+ * point that returns column sums: per 64-row group q and column c,
+ * y[l] = x[64q + l][c] + x[64q + 32 + l][c] (l < 32; missing rows +0), then
+ * the halving folds y[l] += y[l + d] for l < d, d = 16, 8, 4, 2, 1, give the
+ * group sum y[0]; a finalising pass adds the group sums (its own fixed
+ * order: eight interleaved lanes of four accumulators each, then the lanes
+ * in turn). */
 size_t tcfp_colsum_workspace_bytes(int64_t rows, int64_t cols);
 int tcfp_quantize_per_tensor_colsum(const void* x, int x_dtype, int64_t rows, int64_t cols,
                                     int fp8_fmt, uint8_t* q, uint8_t* q_t, float* inv_out,
@@ -119,13 +124,17 @@ int tcfp_quantize_per_tensor_colsum(const void* x, int x_dtype, int64_t rows, in
  * two TCFP-12 layers.  No single reference function: it replaces the
  * model's torch GELU followed by the next layer's to_fp8_e4m3 of its input
  * (tcfp/nn/__init__.py:390 on the GELU output).  h [rows, cols] fp32 is the
- * first layer's output; act = gelu(h) is written (fp32, as torch's GELU
- * computes it bit for bit) in the same pass that takes its amax, then act
- * is quantised by the tcfp_quantize_per_tensor rule (q, optional
- * transposed q_t, inv_out).  h, act 16-byte aligned. */
+ * first layer's output; gelu(h) (as torch's GELU computes it, bit for bit)
+ * is quantised by the tcfp_quantize_per_tensor rule (q, optional transposed
+ * q_t, inv_out).  Written when not NULL: act = gelu(h) and dgelu = the
+ * derivative factor of torch's GELU backward (cdf(h) + h * pdf(h), so that
+ * dy * dgelu is the backward bit for bit), both [rows, cols] fp32.  One
+ * amax pass, then a quantising pass that recomputes gelu(h) from h.
+ * h, act, dgelu 16-byte aligned.  cols % 8 != 0 takes a flat path that
+ * needs act (written by the amax pass) and no dgelu. */
 int tcfp_gelu_quantize_per_tensor(const float* h, int64_t rows, int64_t cols, int fp8_fmt,
-                                  float* act, uint8_t* q, uint8_t* q_t, float* inv_out,
-                                  void* workspace, void* stream);
+                                  float* act, float* dgelu, uint8_t* q, uint8_t* q_t,
+                                  float* inv_out, void* workspace, void* stream);
 
 /* The backward counterpart: grad = dGELU/dh * dy (fp32, bit for bit as
  * torch's GELU backward) is written in the same pass that takes its amax and
@@ -133,13 +142,72 @@ int tcfp_gelu_quantize_per_tensor(const float* h, int64_t rows, int64_t cols, in
  * (tcfp/nn/__init__.py:494 and :558 applied to the GELU's input gradient,
  * which the reference gets from torch's GELU backward).  dy, h, grad
  * [rows, cols] fp32, cols % 8 == 0; colsum_ws as for
- * tcfp_quantize_per_tensor_colsum. */
+ * tcfp_quantize_per_tensor_colsum.  dy and grad may be the same buffer.
+ * col_sum may be NULL (no sums; colsum_ws unused). */
 int tcfp_gelu_backward_quantize_per_tensor_colsum(const float* dy, const float* h, int64_t rows,
                                                   int64_t cols, int fp8_fmt, float* grad,
                                                   uint8_t* q, uint8_t* q_t, float* inv_out,
                                                   float* col_sum, void* workspace,
                                                   void* colsum_ws, size_t colsum_ws_bytes,
                                                   void* stream);
+
+/* The first layer of a TCFP-12 -> GELU -> TCFP-12 pair with the GELU's
+ * amax taken from the GEMM's epilogue.  No single reference function: it
+ * replaces fused_dual_gemm_forward (tcfp/kernels.py:1545-1601) of the first
+ * layer, the model's torch GELU and the second layer's to_fp8 of its input
+ * (tcfp/nn/__init__.py:390 on the GELU output).
+ *   h = s_a*s_hi * A B_hi^T + s_a*s_lo * A B_lo^T (+ bias), [m, n] fp32
+ *   contiguous, written exactly as tcfp_dual_gemm writes it;
+ *   q (+ q_t) / inv_out / act / dgelu: as tcfp_gelu_quantize_per_tensor
+ *   gives them from h (act and dgelu optional).
+ * Operands and scales as tcfp_dual_gemm (b_lo may be NULL).  On the
+ * persistent launch's shapes (m % 256 == 0, n % 128 == 0, k % 128 == 0,
+ * k > 128, more 256 x 128 tiles than CUs, fp8 operands, b_lo given) the
+ * epilogue records the max of h, and max |gelu(h)| is gelu(max h) whenever
+ * the premises of that rule hold: gelu non-decreasing on [+0, +inf] and
+ * |gelu| below a bound T on the negative numbers, both checked over every
+ * fp32 input once per device (the first call launches the check on its
+ * stream, unless the stream is being captured), and gelu(max h) >= T with
+ * no NaN or -inf in h.  Otherwise a full GELU amax pass runs on the device
+ * in its place.  On any other shape this is tcfp_dual_gemm followed by
+ * tcfp_gelu_quantize_per_tensor.  Same bits in every case. */
+int tcfp_dual_gemm_gelu_quantize(const uint8_t* a, int a_fmt, int64_t lda, const uint8_t* b_hi,
+                                 const uint8_t* b_lo, int b_fmt, int64_t ldb, int64_t m,
+                                 int64_t n, int64_t k, const float* s_a, const float* s_hi,
+                                 const float* s_lo, const float* bias, float* h, float* act,
+                                 float* dgelu, int fp8_fmt, uint8_t* q, uint8_t* q_t,
+                                 float* inv_out, void* workspace, void* stream);
+
+/* State of the premise check of tcfp_dual_gemm_gelu_quantize's amax rule on
+ * the current device: checked (the check has completed), holds (gelu is
+ * non-decreasing on [+0, +inf] for this build), bound (T, the largest
+ * |gelu| over the negative numbers).  Synchronous (a copy from the device).
+ * No reference counterpart. */
+int tcfp_gelu_amax_rule_status(int* checked, int* holds, float* bound);
+
+/* The backward counterpart, with the GELU backward in the dgrad GEMM's
+ * epilogue: replaces fused_dual_gemm_backward_dx (tcfp/kernels.py:1604-1666)
+ * of the second layer, torch's GELU backward, and the first layer's E5M2
+ * gradient quantisation and bias gradient (tcfp/nn/__init__.py:494, :558).
+ *   grad = (s_a*s_hi * A B_hi^T + s_a*s_lo * A B_lo^T) * dgelu, [m, n] fp32
+ *   contiguous (A the quantised output gradient, B the transposed weight
+ *   codes, dgelu the derivative factors tcfp_dual_gemm_gelu_quantize wrote):
+ *   torch's GELU backward of tcfp_dual_gemm's output, bit for bit;
+ *   q (+ q_t) / inv_out / col_sum: grad quantised as
+ *   tcfp_quantize_per_tensor_colsum quantises it.
+ * n % 8 == 0; col_sum may be NULL; colsum_ws as for
+ * tcfp_quantize_per_tensor_colsum.  On the persistent launch's shapes the
+ * epilogue writes grad with its per-workgroup maxima and 64-row column
+ * partials; otherwise the GEMM, a multiply-and-amax pass and the
+ * quantising pass run in turn.  Same bits either way. */
+int tcfp_dual_gemm_dgelu_quantize_colsum(const uint8_t* a, int a_fmt, int64_t lda,
+                                         const uint8_t* b_hi, const uint8_t* b_lo, int b_fmt,
+                                         int64_t ldb, int64_t m, int64_t n, int64_t k,
+                                         const float* s_a, const float* s_hi, const float* s_lo,
+                                         const float* dgelu, float* grad, int fp8_fmt,
+                                         uint8_t* q, uint8_t* q_t, float* inv_out,
+                                         float* col_sum, void* workspace, void* colsum_ws,
+                                         size_t colsum_ws_bytes, void* stream);
 
 /* Per-tensor dual quantisation with optional error feedback.
  * Three launches (amax; W_hi + residual amax; W_lo + EF + transposed

@@ -442,3 +442,48 @@ def sr_candidates_block(x: np.ndarray):
     boundary = np.abs(other_f - rtn_f) < F32(1e-45)
     exact = (np.abs(diff) < F32(1e-45)) | boundary
     return rtn, other, frac.astype(F32), exact
+
+
+def column_sums(x: np.ndarray) -> np.ndarray:
+    """The bias gradient ``grad_2d.sum(0)`` (``tcfp/nn/__init__.py:558``) in
+    the fixed fp32 order of this build's column-sum producers.
+
+    The reference leaves the order to torch's reduction; this build fixes
+    one so that its two producers (the quantising pass and the dgrad GEMM's
+    GELU epilogue) agree bit for bit, and the result agrees with the
+    reference's within fp32 rounding:
+
+    1. per 64-row group (missing rows +0): ``y = x[0:32] + x[32:64]``, then
+       the halving folds ``y = y[:d] + y[d:2d]`` for d = 16, 8, 4, 2, 1;
+    2. the group sums P[q] are added by eight lanes (lane r takes the groups
+       q = r mod 8: four accumulators over q, q + 8, q + 16, q + 24 for each
+       32 groups, then the remaining groups into the first), each lane's
+       ``(s0 + s1) + (s2 + s3)``, then the lanes in turn.
+    """
+    x = np.asarray(x, dtype=F32)
+    rows, cols = x.shape
+    groups = -(-rows // 64)
+    xp = np.zeros((groups * 64, cols), F32)
+    xp[:rows] = x
+    y = xp.reshape(groups, 64, cols)
+    y = y[:, :32] + y[:, 32:]
+    while y.shape[1] > 1:
+        d = y.shape[1] // 2
+        y = y[:, :d] + y[:, d:]
+    p = y[:, 0]
+    lanes = []
+    for lane in range(8):
+        s = [np.zeros(cols, F32) for _ in range(4)]
+        r = lane
+        while r + 24 < groups:
+            for j in range(4):
+                s[j] = s[j] + p[r + 8 * j]
+            r += 32
+        while r < groups:
+            s[0] = s[0] + p[r]
+            r += 8
+        lanes.append((s[0] + s[1]) + (s[2] + s[3]))
+    out = lanes[0]
+    for v in lanes[1:]:
+        out = out + v
+    return out

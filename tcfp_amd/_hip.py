@@ -40,7 +40,7 @@ _SIGNATURES = {
                                         _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                                         ctypes.c_size_t, _c_void_p],
     "tcfp_gelu_quantize_per_tensor": [_c_void_p, _i64, _i64, _i32, _c_void_p, _c_void_p,
-                                      _c_void_p, _c_void_p, _c_void_p, _c_void_p],
+                                      _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p],
     "tcfp_gelu_backward_quantize_per_tensor_colsum": [_c_void_p, _c_void_p, _i64, _i64, _i32,
                                                       _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                                                       _c_void_p, _c_void_p, _c_void_p,
@@ -80,6 +80,16 @@ _SIGNATURES = {
     "tcfp_dual_gemm": [_c_void_p, _i32, _i64, _c_void_p, _c_void_p, _i32, _i64, _i64, _i64, _i64,
                        _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i32, _i64,
                        _c_void_p],
+    "tcfp_dual_gemm_gelu_quantize": [_c_void_p, _i32, _i64, _c_void_p, _c_void_p, _i32, _i64,
+                                     _i64, _i64, _i64, _c_void_p, _c_void_p, _c_void_p,
+                                     _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i32,
+                                     _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p],
+    "tcfp_gelu_amax_rule_status": [_c_void_p, _c_void_p, _c_void_p],
+    "tcfp_dual_gemm_dgelu_quantize_colsum": [_c_void_p, _i32, _i64, _c_void_p, _c_void_p, _i32,
+                                             _i64, _i64, _i64, _i64, _c_void_p, _c_void_p,
+                                             _c_void_p, _c_void_p, _c_void_p, _i32, _c_void_p,
+                                             _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+                                             _c_void_p, ctypes.c_size_t, _c_void_p],
     "tcfp_block_dual_gemm": [_c_void_p, _i32, _i64, _c_void_p, _c_void_p, _c_void_p, _i32, _i64,
                              _c_void_p, _c_void_p, _i64, _i64, _i64, _i32, _c_void_p, _c_void_p,
                              _i32, _i64, _c_void_p],

@@ -35,11 +35,13 @@ COMMON_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
 
-# Per-file extra flags.  The quantisation kernels must match torch's
-# separately rounded elementwise ops bit for bit: no contraction to FMA.
+# Per-file extra flags.  The quantisation kernels and the GEMM epilogues
+# that evaluate GELU must match torch's separately rounded elementwise ops
+# bit for bit (and each other: the erf / exp they inline are compiled with
+# these flags too): no contraction to FMA.
 EXTRA = {
     "quant.hip": ["-ffp-contract=off"],
-    "gemm.hip": [],
+    "gemm.hip": ["-ffp-contract=off"],
 }
 
 

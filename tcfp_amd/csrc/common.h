@@ -27,6 +27,53 @@ inline bool grid_x_fits(int64_t blocks, int threads) {
   return blocks >= 0 && blocks <= int64_t(UINT32_MAX) / threads;
 }
 
+// ---- column sums (bias gradients) -----------------------------------------
+// Every column sum this library computes of a [rows, cols] fp32 tensor x
+// (the producers: the tiled quantisation pass and the dgrad GEMM's GELU
+// epilogue) has one order, so that either producer gives the same bits:
+//  1. per 64-row group q (rows 64q ... 64q + 63, missing rows +0) and column
+//     c: y[l] = x[64q + l][c] + x[64q + 32 + l][c] for l < 32, then halving
+//     folds y[l] = y[l] + y[l + d] for l < d, d = 16, 8, 4, 2, 1, giving
+//     P[q][c] = y[0];
+//  2. the finalising pass (quant.hip) adds the P[q][c] over q.
+constexpr int kColGroup = 64;
+constexpr int kColHalf = kColGroup / 2;
+
+// ---- shared between the GEMM and quantisation sources (quant.hip) --------
+// Slots of per-workgroup partial maxima the per-tensor reduction workspace
+// holds (its first member, at offset 0).
+int max_parts();
+// Per-tensor quantisation of x whose partial maxima (|value| as float bits,
+// NaN above inf) a producer already wrote to the first pre_g workspace
+// slots: the quantising pass of tcfp_quantize_per_tensor, with gelu_in (x
+// is fp32 h, the values are gelu(h)) and col_sum (column sums per 128-row
+// tile in cs_ws, then over the tiles) as in that file.
+int quantize_with_parts(const void* x, int x_dtype, int64_t rows, int64_t cols, int fp8_fmt,
+                        uint8_t* q, uint8_t* q_t, float* inv_out, void* workspace,
+                        float* col_sum, float* cs_ws, void* stream, int pre_g, bool gelu_in);
+// col_sum[c] = the sum over the first `groups` rows of cs_ws ([groups, cols]
+// per-group partials) in the finalising order.
+int colsum_finalize(const float* cs_ws, int64_t groups, int64_t cols, float* col_sum,
+                    void* stream);
+// gelu(h) quantised per tensor (as tcfp_gelu_quantize_per_tensor) with the
+// amax from the GELU amax rule's keys a producer of h wrote, one (int max,
+// uint max) pair per producer workgroup, at keys[2 i], keys[2 i + 1],
+// i < n_keys (keys must not overlap the workspace's first slots).  When the
+// rule does not apply, a full GELU amax pass over h runs in its place (on
+// the device: the launch sequence is the same).  act (gelu(h)) and dgelu
+// (the derivative factor of gelu_and_deriv) are written when not null.
+// cols % 8 == 0.
+int gelu_quantize_from_keys(const float* h, int64_t rows, int64_t cols, int fp8_fmt, float* act,
+                            float* dgelu, uint8_t* q, uint8_t* q_t, float* inv_out,
+                            void* workspace, const uint32_t* keys, int n_keys, void* stream);
+// out = a * b elementwise and the per-tensor quantisation of out with its
+// column sums (tcfp_quantize_per_tensor_colsum, col_sum may be null): the
+// GELU backward from its saved derivative factor (a = dy, b = dgelu).  out
+// may be a.  cols % 8 == 0.
+int mul_quantize_colsum(const float* a, const float* b, int64_t rows, int64_t cols, int fp8_fmt,
+                        float* out, uint8_t* q, uint8_t* q_t, float* inv_out, float* col_sum,
+                        void* workspace, float* cs_ws, void* stream);
+
 // ---------------------------------------------------------------------------
 // bfloat16
 // ---------------------------------------------------------------------------
@@ -188,6 +235,50 @@ TCFP_DEV float exp2i(int e) {
   if (e >= -126) return __uint_as_float(uint32_t(e + 127) << 23);
   return __uint_as_float(1u << (e + 149));
 }
+
+// |v| as float bits: unsigned order is the order of |v|, NaN above inf (the
+// encoding of every partial maximum).
+TCFP_DEV uint32_t absbits(float v) { return __float_as_uint(v) & 0x7FFFFFFFu; }
+TCFP_DEV uint32_t umax(uint32_t a, uint32_t b) { return a > b ? a : b; }
+
+// ---------------------------------------------------------------------------
+// GELU
+// ---------------------------------------------------------------------------
+// GELU (erf form) exactly as torch evaluates it on fp32 tensors: forward
+// x * 0.5 * (1 + erf(x * sqrt(1/2))), every operation rounded on its own
+// (every file that includes this header is built without contraction); backward
+// dy * (cdf + x * pdf) with cdf = 0.5 * (1 + erf(x * sqrt(1/2))),
+// pdf = exp(-0.5 * x * x) * (2/sqrt(pi) * sqrt(1/2) * 0.5), the last
+// product and sum as one fused multiply-add.  The constants are the
+// double-precision products rounded once to fp32.  A GPU test holds both
+// bitwise equal to torch.nn.functional.gelu and its gradient.
+constexpr float kSqrtHalf = float(0.70710678118654752440);
+constexpr float kGeluBeta = float(1.12837916709551257390 * 0.70710678118654752440 * 0.5);
+TCFP_DEV float gelu_f32(float x) { return x * 0.5f * (1.0f + erff(x * kSqrtHalf)); }
+TCFP_DEV float gelu_bwd_f32(float x, float dy) {
+  const float cdf = 0.5f * (1.0f + erff(x * kSqrtHalf));
+  const float pdf = expf(-0.5f * x * x) * kGeluBeta;
+  return dy * __builtin_fmaf(x, pdf, cdf);
+}
+// gelu(x) and the derivative factor d(x) = cdf + x * pdf of gelu_bwd_f32,
+// sharing the erf: gelu_bwd_f32(x, dy) == dy * d(x) bit for bit.
+TCFP_DEV void gelu_and_deriv(float x, float& g, float& d) {
+  const float e = erff(x * kSqrtHalf);
+  g = x * 0.5f * (1.0f + e);
+  const float cdf = 0.5f * (1.0f + e);
+  const float pdf = expf(-0.5f * x * x) * kGeluBeta;
+  d = __builtin_fmaf(x, pdf, cdf);
+}
+
+// Keys of the GELU amax rule.  A producer of h tracks, over its values,
+// the max of the float bits as int32 (the largest h >= +0, or INT32_MIN when
+// every value is negative or -0; +NaN sorts above +inf) and as uint32
+// (>= 0xFF800000 exactly when some value is -inf or a negative NaN).  When
+// gelu is non-decreasing on [+0, +inf] and |gelu| stays below a bound T on
+// the negative numbers (both checked once per device by quant.hip), the
+// max |gelu(h)| is gelu(max h) whenever that is finite, not NaN and >= T.
+constexpr uint32_t kGeluKeyNegNanInf = 0xFF800000u;
+constexpr uint32_t kGeluKeyPosInf = 0x7F800000u;
 
 // ---------------------------------------------------------------------------
 // Philox4x32-10 (Salmon, Moraes, Dror, Shaw: "Parallel random numbers: as

@@ -204,6 +204,16 @@ struct GemmArgs {
   // its partial output at out + y*split_stride (fp32, no bias)
   int kc;
   int64_t split_stride;
+  // GELU epilogues of the persistent fp32 kernel (same leading dimension
+  // ldo as out; EPI 2 ignores bias).  EPI 1 writes out (= h) as EPI 0 and the GELU amax rule's
+  // keys of h (common.h) to part[2 * blockIdx.x], part[2 * blockIdx.x + 1].
+  // EPI 2 reads the GELU derivative factors from aux and writes
+  // aux * value (the GELU backward), with the workgroup's max |written
+  // value| (float bits) at part[blockIdx.x] and, when cs_part is not null,
+  // the 64-row column partials to cs_part ([M / 64, N]).
+  const float* aux;
+  uint32_t* part;
+  float* cs_part;
 };
 
 // NS = LDS stages in flight (2, or 4 for the small tile when one
@@ -736,9 +746,10 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && NS == 2 && BM == 128 ? 2 : 1))
 // accumulator rows as 16-byte vectors straight from registers (16 stores per
 // wave and tile), and the freed last-stage buffer takes the next tile's
 // stage 1 right at the last stage's barrier.
-template <int AF, int BF, typename OutT>
+template <int AF, int BF, typename OutT, int EPI = 0>
 __global__ __launch_bounds__(512, 1) void gemm_nt_persist_kernel(GemmArgs g) {
   constexpr bool F32OUT = std::is_same<OutT, float>::value;
+  static_assert(EPI == 0 || F32OUT, "GELU epilogues write fp32");
   constexpr int NW = 8, BM = 256, BN = 128, NS = 2;
   constexpr int WM = NW / 2, TMW = BM / WM, MB = TMW / 32;
   constexpr int TNW = BN / 2, NB = TNW / 32, NF = 2 * NB;
@@ -754,7 +765,14 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persist_kernel(GemmArgs g) {
   constexpr int NST = F32OUT ? MB * NB * 4 : TMW / RPI;
   static_assert(NW * TMW * RB <= STAGE, "epilogue staging must fit one operand buffer");
   static_assert(NST + DI <= 63, "vmcnt immediate");
+  // EPI 2's column partials: a wave's rows are one 64-row group, its two
+  // m-blocks the group's halves
+  static_assert(EPI != 2 || (TMW == kColGroup && MB == 2), "wave rows vs. column groups");
   __shared__ __align__(16) uint8_t lds[NS * STAGE];
+  // GELU epilogues: EPI 1 the lane's int / uint maxima of the h bits (the
+  // amax rule's keys), EPI 2 its max |value| bits (in amx)
+  uint32_t amx = 0;
+  int32_t kimax = INT32_MIN;
 
   const int M = g.M, N = g.N, K = g.K;
   OutT* __restrict__ out = static_cast<OutT*>(g.out);
@@ -924,8 +942,10 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persist_kernel(GemmArgs g) {
         issue(nxt, 1, b);  // the next tile's stage 1 (no output staging)
       __builtin_amdgcn_sched_barrier(0);
       // sub-step 0 of stage t + 1 (after the last stage: the next tile's
-      // stage 0, landed at this barrier; stale and unused after the last tile)
-      read_frags(f0, b ^ 1, 0);
+      // stage 0, landed at this barrier; stale and unused after the last
+      // tile).  EPI 2 reads it after the epilogue, whose loads need the
+      // registers.
+      if (EPI != 2 || t + 1 < nt) read_frags(f0, b ^ 1, 0);
       mfmas_range(f1, 0, NP);
       interleave_mfma_lds<NP, 2 * (NF + MB), 0>();
     }
@@ -934,27 +954,107 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persist_kernel(GemmArgs g) {
     const int nb = n0 + wn * TNW;
     if constexpr (F32OUT) {
       // ---- epilogue: 16-byte stores from the accumulators --------------------
+      if constexpr (EPI == 2) {
+        // g = value * gelu'(h) factor.  Every factor load of the tile is
+        // issued before any store: a wait for a load also waits for every
+        // vector-memory operation issued before it (the next tile's stage 1,
+        // issued at the last stage, has a head start).
+        float4 dv[MB * NB * 4];
 #pragma unroll
-      for (int i = 0; i < MB; ++i)
+        for (int i = 0; i < MB; ++i)
 #pragma unroll
-        for (int j = 0; j < NB; ++j)
+          for (int j = 0; j < NB; ++j)
 #pragma unroll
-          for (int gq = 0; gq < 4; ++gq) {
-            const int row = i * 32 + lr, col = j * 32 + gq * 8 + lg * 4;
-            float v[4];
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              const int r = gq * 4 + q;
-              v[q] = acc[0][j][i][r] * c0s + acc[1][j][i][r] * c1s;
+            for (int gq = 0; gq < 4; ++gq) {
+              const int64_t o = int64_t(m0 + wm * TMW + i * 32 + lr) * g.ldo + nb + j * 32 +
+                                gq * 8 + lg * 4;
+              dv[(i * NB + j) * 4 + gq] = *reinterpret_cast<const float4*>(g.aux + o);
             }
-            if (g.bias) {
+        // g replaces the first accumulator set in place (the registers of
+        // the second set and of the factors free up as they are consumed)
 #pragma unroll
-              for (int q = 0; q < 4; ++q) v[q] += g.bias[nb + col + q];
+        for (int i = 0; i < MB; ++i)
+#pragma unroll
+          for (int j = 0; j < NB; ++j)
+#pragma unroll
+            for (int gq = 0; gq < 4; ++gq) {
+              const int col = j * 32 + gq * 8 + lg * 4;
+              const int64_t o = int64_t(m0 + wm * TMW + i * 32 + lr) * g.ldo + nb + col;
+              const float4 d = dv[(i * NB + j) * 4 + gq];
+              float v[4];  // (a dgrad: no bias)
+#pragma unroll
+              for (int q = 0; q < 4; ++q) {
+                const int r = gq * 4 + q;
+                v[q] = acc[0][j][i][r] * c0s + acc[1][j][i][r] * c1s;
+              }
+              v[0] = v[0] * d.x;
+              v[1] = v[1] * d.y;
+              v[2] = v[2] * d.z;
+              v[3] = v[3] * d.w;
+              store4<float>(reinterpret_cast<float*>(out) + o, v[0], v[1], v[2], v[3]);
+#pragma unroll
+              for (int q = 0; q < 4; ++q) {
+                amx = umax(amx, absbits(v[q]));
+                acc[0][j][i][gq * 4 + q] = v[q];
+              }
             }
-            store4<float>(reinterpret_cast<float*>(out) + int64_t(m0 + wm * TMW + row) * g.ldo +
-                              nb + col,
-                          v[0], v[1], v[2], v[3]);
+        if (g.cs_part) {
+          // ys[j * 16 + gq * 4 + q]: g(row lr) + g(row 32 + lr) of the lane's
+          // column j * 32 + gq * 8 + lg * 4 + q (the wave's 64-row group)
+          float ys[NB * 16];
+#pragma unroll
+          for (int j = 0; j < NB; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) ys[j * 16 + r] = acc[0][j][0][r] + acc[0][j][1][r];
+          // halving folds over the 32 row lanes (lane bits 4 ... 0): each
+          // step keeps half of the columns and adds the partner lane's
+          // values of them; lane lr ends with the group sum of column k = lr
+#pragma unroll
+          for (int d = 16, len = NB * 16; d >= 1; d >>= 1, len >>= 1) {
+            const bool up = (lr & d) != 0;
+#pragma unroll
+            for (int k = 0; k < len / 2; ++k) {
+              const float give = up ? ys[k] : ys[k + len / 2];
+              const float keep = up ? ys[k + len / 2] : ys[k];
+              ys[k] = keep + __shfl_xor(give, d);
+            }
           }
+          const int col = (lr >> 4) * 32 + ((lr >> 2) & 3) * 8 + lg * 4 + (lr & 3);
+          g.cs_part[int64_t((m0 + wm * TMW) / kColGroup) * N + nb + col] = ys[0];
+        }
+        // the next tile's first fragments (its stage 0 landed at the last
+        // stage's barrier; stale and unused after the last tile)
+        read_frags(f0, sb ^ 1, 0);
+      } else {
+#pragma unroll
+        for (int i = 0; i < MB; ++i)
+#pragma unroll
+          for (int j = 0; j < NB; ++j)
+#pragma unroll
+            for (int gq = 0; gq < 4; ++gq) {
+              const int row = i * 32 + lr, col = j * 32 + gq * 8 + lg * 4;
+              const int64_t o = int64_t(m0 + wm * TMW + row) * g.ldo + nb + col;
+              float v[4];
+#pragma unroll
+              for (int q = 0; q < 4; ++q) {
+                const int r = gq * 4 + q;
+                v[q] = acc[0][j][i][r] * c0s + acc[1][j][i][r] * c1s;
+              }
+              if (g.bias) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) v[q] += g.bias[nb + col + q];
+              }
+              store4<float>(reinterpret_cast<float*>(out) + o, v[0], v[1], v[2], v[3]);
+              if constexpr (EPI == 1) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                  const uint32_t b = __float_as_uint(v[q]);
+                  kimax = max(kimax, int32_t(b));
+                  amx = umax(amx, b);
+                }
+              }
+            }
+      }
       __builtin_amdgcn_sched_barrier(0);
       zero_acc();
       cb0 = sb ^ 1;
@@ -1019,6 +1119,35 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persist_kernel(GemmArgs g) {
     m0 = m1;
     n0 = n1;
   }
+  if constexpr (EPI != 0) {
+    // the workgroup's partials (no DMA is in flight after the last tile)
+    __shared__ uint32_t wmax[2 * NW];
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) {
+      amx = umax(amx, uint32_t(__shfl_xor(int(amx), d)));
+      if constexpr (EPI == 1) kimax = max(kimax, __shfl_xor(kimax, d));
+    }
+    if (lane == 0) {
+      wmax[wave] = amx;
+      wmax[NW + wave] = uint32_t(kimax);
+    }
+    __syncthreads();
+    if (tid == 0) {
+      uint32_t m = wmax[0];
+      int32_t k = int32_t(wmax[NW]);
+#pragma unroll
+      for (int w = 1; w < NW; ++w) {
+        m = umax(m, wmax[w]);
+        k = max(k, int32_t(wmax[NW + w]));
+      }
+      if constexpr (EPI == 1) {
+        g.part[2 * blockIdx.x] = uint32_t(k);
+        g.part[2 * blockIdx.x + 1] = m;
+      } else {
+        g.part[blockIdx.x] = m;
+      }
+    }
+  }
 }
 
 // Largest byte span any DMA descriptor may cover (offsets are 32-bit and
@@ -1042,6 +1171,22 @@ int num_cus() {
       n = 256;
   }
   return n;
+}
+
+bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// The persistent large-tile launch: full 256 x 128 tiles, two K stages at
+// least, more tiles than CUs, no split-K, and every DMA span within the
+// descriptors' reach (tile policies 0 and 1 only).  Per-tensor fp8 dual
+// GEMMs with fp32 or bf16 output.
+bool persist_eligible(const GemmArgs& ga) {
+  if (g_tile_policy != 0 && g_tile_policy != 1) return false;
+  if (ga.M % 256 != 0 || ga.N % 128 != 0 || ga.K % kSK != 0 || ga.K <= kSK) return false;
+  if (ga.kc > 0 && ga.kc < ga.K) return false;
+  if (ga.ldo % 8 != 0 || !al16(ga.out)) return false;
+  if (int64_t(256) * ga.lda + ga.K >= kMaxSpan || int64_t(128) * ga.ldb + ga.K >= kMaxSpan)
+    return false;
+  return int64_t(ga.M / 256) * (ga.N / 128) > num_cus();
 }
 
 template <int AF, int BF, bool SPLIT, typename OutT, int SCALE>
@@ -1091,9 +1236,7 @@ int launch_gemm(GemmArgs ga, hipStream_t st) {
       // per CU runs its tiles back to back
       bool persist = false;
       if constexpr (SCALE == 0 && !SPLIT && AF != kBF16) {
-        persist = g_tile_policy != 4 && splits == 1 && int64_t(grid.x) > num_cus() &&
-                  m % 256 == 0 && n % 128 == 0 && k % kSK == 0 && k > kSK && ga.ldo % 8 == 0 &&
-                  (reinterpret_cast<uintptr_t>(ga.out) & 15) == 0;
+        persist = persist_eligible(ga);
         if (persist)
           gemm_nt_persist_kernel<AF, BF, OutT><<<unsigned(num_cus()), 512, 0, st>>>(ga);
       }
@@ -1128,8 +1271,6 @@ int dispatch_all(int a_fmt, int b_fmt, bool dual, int out_dtype, const GemmArgs&
   return dispatch_fmt<true, uint16_t, SCALE>(a_fmt, b_fmt, ga, st);
 }
 
-bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
-
 int check_common(int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldb, int64_t ldo,
                  const void* a, const void* b_hi, const void* b_lo, int out_dtype) {
   if (m < 0 || n < 0 || k < 0 || m > INT32_MAX || n > INT32_MAX || k > INT32_MAX)
@@ -1160,6 +1301,117 @@ extern "C" int tcfp_dual_gemm(const uint8_t* a, int a_fmt, int64_t lda, const ui
   ga.bias = bias; ga.out = out; ga.ldo = ldo;
   return dispatch_all<0>(a_fmt, b_fmt, b_lo != nullptr, out_dtype, ga,
                          static_cast<hipStream_t>(stream));
+}
+
+namespace {
+
+// One GELU-epilogue persistent launch (EPI 1 or 2) for fp8 operand formats.
+template <int EPI>
+int launch_persist_gelu(int a_fmt, int b_fmt, const GemmArgs& ga, hipStream_t st) {
+  const unsigned grid = unsigned(num_cus());
+#define TCFP_PG(A, B) gemm_nt_persist_kernel<A, B, float, EPI><<<grid, 512, 0, st>>>(ga)
+  if (a_fmt == TCFP_FP8_E4M3 && b_fmt == TCFP_FP8_E4M3) TCFP_PG(0, 0);
+  else if (a_fmt == TCFP_FP8_E5M2 && b_fmt == TCFP_FP8_E4M3) TCFP_PG(1, 0);
+  else if (a_fmt == TCFP_FP8_E4M3 && b_fmt == TCFP_FP8_E5M2) TCFP_PG(0, 1);
+  else if (a_fmt == TCFP_FP8_E5M2 && b_fmt == TCFP_FP8_E5M2) TCFP_PG(1, 1);
+  else return TCFP_ERR_DTYPE;
+#undef TCFP_PG
+  return hipGetLastError() == hipSuccess ? TCFP_OK : TCFP_ERR_HIP;
+}
+
+bool fp8_fmt_ok(int f) { return f == TCFP_FP8_E4M3 || f == TCFP_FP8_E5M2; }
+
+}  // namespace
+
+extern "C" int tcfp_dual_gemm_gelu_quantize(const uint8_t* a, int a_fmt, int64_t lda,
+                                            const uint8_t* b_hi, const uint8_t* b_lo, int b_fmt,
+                                            int64_t ldb, int64_t m, int64_t n, int64_t k,
+                                            const float* s_a, const float* s_hi,
+                                            const float* s_lo, const float* bias, float* h,
+                                            float* act, float* dgelu, int fp8_fmt, uint8_t* q,
+                                            uint8_t* q_t, float* inv_out, void* workspace,
+                                            void* stream) {
+  const int rc = check_common(m, n, k, lda, ldb, n, a, b_hi, b_lo, TCFP_DTYPE_F32);
+  if (rc != TCFP_OK) return rc;
+  if (!s_a || !s_hi || (b_lo && !s_lo)) return TCFP_ERR_SHAPE;
+  if (!fp8_fmt_ok(fp8_fmt)) return TCFP_ERR_DTYPE;
+  if (!workspace) return TCFP_ERR_WORKSPACE;
+  if (!h || !al16(h) || (act && !al16(act)) || (dgelu && !al16(dgelu)) || !inv_out)
+    return TCFP_ERR_ALIGN;
+  if (bias && !al16(bias)) return TCFP_ERR_ALIGN;
+  GemmArgs ga{};
+  ga.A = a; ga.B0 = b_hi; ga.B1 = b_lo;
+  ga.M = int(m); ga.N = int(n); ga.K = int(k); ga.lda = lda; ga.ldb = ldb;
+  ga.s_a = s_a; ga.s_0 = s_hi; ga.s_1 = s_lo;
+  ga.bias = bias; ga.out = h; ga.ldo = n;
+  // the keys go to the workspace's second partial array (the first takes
+  // the amax partials the quantising pass reads)
+  uint32_t* keys = static_cast<uint32_t*>(workspace) + tcfp::max_parts();
+  ga.part = keys;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (b_lo && fp8_fmt_ok(a_fmt) && fp8_fmt_ok(b_fmt) && m > 0 && persist_eligible(ga) &&
+      2 * num_cus() <= tcfp::max_parts()) {
+    ga.tiles_m = int(m / 256);
+    ga.tiles_n = int(n / 128);
+    const int r = launch_persist_gelu<1>(a_fmt, b_fmt, ga, st);
+    if (r != TCFP_OK) return r;
+    return tcfp::gelu_quantize_from_keys(h, m, n, fp8_fmt, act, dgelu, q, q_t, inv_out,
+                                         workspace, keys, num_cus(), stream);
+  }
+  // any other shape: the GEMM, then the GELU amax pass
+  const int r = tcfp_dual_gemm(a, a_fmt, lda, b_hi, b_lo, b_fmt, ldb, m, n, k, s_a, s_hi, s_lo,
+                               bias, h, TCFP_DTYPE_F32, n, stream);
+  if (r != TCFP_OK) return r;
+  return tcfp_gelu_quantize_per_tensor(h, m, n, fp8_fmt, act, dgelu, q, q_t, inv_out, workspace,
+                                       stream);
+}
+
+extern "C" int tcfp_dual_gemm_dgelu_quantize_colsum(
+    const uint8_t* a, int a_fmt, int64_t lda, const uint8_t* b_hi, const uint8_t* b_lo, int b_fmt,
+    int64_t ldb, int64_t m, int64_t n, int64_t k, const float* s_a, const float* s_hi,
+    const float* s_lo, const float* dgelu, float* grad, int fp8_fmt, uint8_t* q, uint8_t* q_t,
+    float* inv_out, float* col_sum, void* workspace, void* colsum_ws, size_t colsum_ws_bytes,
+    void* stream) {
+  const int rc = check_common(m, n, k, lda, ldb, n, a, b_hi, b_lo, TCFP_DTYPE_F32);
+  if (rc != TCFP_OK) return rc;
+  if (!s_a || !s_hi || (b_lo && !s_lo)) return TCFP_ERR_SHAPE;
+  if (!fp8_fmt_ok(fp8_fmt)) return TCFP_ERR_DTYPE;
+  if (n % 8 != 0) return TCFP_ERR_SHAPE;
+  if (!workspace) return TCFP_ERR_WORKSPACE;
+  if (!dgelu || !grad || !al16(dgelu) || !al16(grad) || !inv_out) return TCFP_ERR_ALIGN;
+  const bool sums = col_sum != nullptr && m > 0 && n > 0;
+  if (sums && (!colsum_ws || colsum_ws_bytes < tcfp_colsum_workspace_bytes(m, n)))
+    return TCFP_ERR_WORKSPACE;
+  if (sums && (!al16(colsum_ws) || !al16(col_sum))) return TCFP_ERR_ALIGN;
+  GemmArgs ga{};
+  ga.A = a; ga.B0 = b_hi; ga.B1 = b_lo;
+  ga.M = int(m); ga.N = int(n); ga.K = int(k); ga.lda = lda; ga.ldb = ldb;
+  ga.s_a = s_a; ga.s_0 = s_hi; ga.s_1 = s_lo;
+  ga.out = grad; ga.ldo = n;
+  ga.aux = dgelu;
+  ga.part = static_cast<uint32_t*>(workspace);
+  ga.cs_part = sums ? static_cast<float*>(colsum_ws) : nullptr;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (b_lo && fp8_fmt_ok(a_fmt) && fp8_fmt_ok(b_fmt) && m > 0 && persist_eligible(ga) &&
+      num_cus() <= tcfp::max_parts()) {
+    ga.tiles_m = int(m / 256);
+    ga.tiles_n = int(n / 128);
+    int r = launch_persist_gelu<2>(a_fmt, b_fmt, ga, st);
+    if (r != TCFP_OK) return r;
+    r = tcfp::quantize_with_parts(grad, TCFP_DTYPE_F32, m, n, fp8_fmt, q, q_t, inv_out, workspace,
+                                  nullptr, nullptr, stream, num_cus(), false);
+    if (r != TCFP_OK || !sums) return r;
+    return tcfp::colsum_finalize(static_cast<const float*>(colsum_ws), m / kColGroup, n, col_sum,
+                                 stream);
+  }
+  // any other shape: the GEMM into grad, then grad *= dgelu with the amax,
+  // then the quantising pass with the column sums
+  const int r = tcfp_dual_gemm(a, a_fmt, lda, b_hi, b_lo, b_fmt, ldb, m, n, k, s_a, s_hi, s_lo,
+                               nullptr, grad, TCFP_DTYPE_F32, n, stream);
+  if (r != TCFP_OK) return r;
+  return tcfp::mul_quantize_colsum(grad, dgelu, m, n, fp8_fmt, grad, q, q_t, inv_out,
+                                   sums ? col_sum : nullptr, workspace,
+                                   static_cast<float*>(colsum_ws), stream);
 }
 
 extern "C" int tcfp_block_dual_gemm(const uint8_t* a, int a_fmt, int64_t lda, const int8_t* e_a,

@@ -9,6 +9,7 @@
 // thread owns whole 8-element vectors, so the in-place error-feedback update
 // of a vector is done by the thread that read it.
 #include <algorithm>
+#include <cstring>
 #include <mutex>
 
 #include "common.h"
@@ -35,7 +36,9 @@ struct PartWs {
   // W_hi target (before any EMA) published by workgroup 0 of the W_hi pass
   // for the residual pass, which then skips re-reducing the partials
   float hi_tgt;
-  uint32_t pad2[63];
+  // GELU amax rule: applies (0/1) and the amax bits it gives
+  uint32_t gelu_rule[2];
+  uint32_t pad2[61];
 };
 
 constexpr int kThreads = 256;
@@ -148,9 +151,6 @@ TCFP_DEV void scale_from_amax(float amax, bool bf16_rule, float fmax, float* sca
   }
   *inv = __fdiv_rn(1.0f, *scale);
 }
-
-TCFP_DEV uint32_t absbits(float v) { return __float_as_uint(v) & 0x7FFFFFFFu; }
-TCFP_DEV uint32_t umax(uint32_t a, uint32_t b) { return a > b ? a : b; }
 
 // Workgroup-wide uint max (256 threads), returned to every thread.  `red`
 // is the caller's LDS scratch: one call per array between barriers.
@@ -386,29 +386,22 @@ __global__ __launch_bounds__(kThreads) void amax_part_kernel(const InT* __restri
 }
 
 // ---- GELU producers ---------------------------------------------------------
-// GELU (erf form) exactly as torch evaluates it on fp32 tensors: forward
-// x * 0.5 * (1 + erf(x * sqrt(1/2))), every operation rounded on its own
-// (this file is built without contraction); backward
-// dy * (cdf + x * pdf) with cdf = 0.5 * (1 + erf(x * sqrt(1/2))),
-// pdf = exp(-0.5 * x * x) * (2/sqrt(pi) * sqrt(1/2) * 0.5), the last
-// product and sum as one fused multiply-add.  The constants are the
-// double-precision products rounded once to fp32.  A GPU test holds both
-// bitwise equal to torch.nn.functional.gelu and its gradient.
-constexpr float kSqrtHalf = float(0.70710678118654752440);
-constexpr float kGeluBeta = float(1.12837916709551257390 * 0.70710678118654752440 * 0.5);
-TCFP_DEV float gelu_f32(float x) { return x * 0.5f * (1.0f + erff(x * kSqrtHalf)); }
-TCFP_DEV float gelu_bwd_f32(float x, float dy) {
-  const float cdf = 0.5f * (1.0f + erff(x * kSqrtHalf));
-  const float pdf = expf(-0.5f * x * x) * kGeluBeta;
-  return dy * __builtin_fmaf(x, pdf, cdf);
-}
+// gelu_f32 / gelu_bwd_f32 (common.h) evaluate torch's GELU bit for bit.
 
-// act = gelu(h) (written out) and this workgroup's partial max |act| ->
-// part[blockIdx.x], the producer of a per-tensor quantisation of act.
+// act = gelu(h) (written out unless act is null) and this workgroup's
+// partial max |act| -> part[blockIdx.x], the producer of a per-tensor
+// quantisation of act (which may recompute act from h instead of reading it).
 // 512-thread workgroups: the partial count is capped, and the erf makes the
 // pass VALU-heavy, so each CU needs eight waves per SIMD to overlap the
 // arithmetic with the memory traffic.
 constexpr int kGeluThreads = 512;
+// workgroups of the GELU passes over n elements: up to kMaxParts, two
+// 8-element vectors per thread at least (measured: 2048 x 512 threads 42
+// us, 1024 x 512 threads 44.5 us for 32 Mi elements)
+int gelu_grid(int64_t n) {
+  return int(std::max<int64_t>(
+      1, std::min<int64_t>(kMaxParts, ((n + 7) / 8 + 2 * kGeluThreads - 1) / (2 * kGeluThreads))));
+}
 __global__ __launch_bounds__(kGeluThreads) void gelu_amax_kernel(const float* __restrict__ h,
                                                                  int64_t n, float* __restrict__ act,
                                                                  uint32_t* __restrict__ part) {
@@ -420,7 +413,7 @@ __global__ __launch_bounds__(kGeluThreads) void gelu_amax_kernel(const float* __
     float g[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) g[j] = gelu_f32(v[j]);
-    store8(act + i * 8, g);
+    if (act) store8(act + i * 8, g);
     // the max after the stores, over all eight (measured faster than
     // folding each value in as it is produced)
     const uint32_t m01 = umax(absbits(g[0]), absbits(g[1])), m23 = umax(absbits(g[2]), absbits(g[3]));
@@ -437,117 +430,198 @@ __global__ __launch_bounds__(kGeluThreads) void gelu_amax_kernel(const float* __
   for (int64_t t = nvec * 8 + int64_t(blockIdx.x) * kGeluThreads + threadIdx.x; t < n;
        t += stride) {
     const float g = gelu_f32(h[t]);
-    act[t] = g;
+    if (act) act[t] = g;
     m = umax(m, absbits(g));
   }
   m = block_umax_nt<kGeluThreads>(m, red);
   if (threadIdx.x == 0) part[blockIdx.x] = m;
 }
 
-// ---- amax + column sums (the bias gradient) in one pass ------------------
-// Geometry for x [rows, cols], cols % 8 == 0: a 512-thread workgroup covers
-// NVW 8-column vectors (a power of two <= 256) with RL = 512 / NVW row lanes,
-// over one group of consecutive rows; it writes the partial max and the
-// partial column sums of its row group to cs_part[rg, cols].
-struct ColsumGeom {
-  int nvw, rl, cb_count, rg_count, rpg;
-};
-
-constexpr int kMaxRowGroups = 512;
-constexpr int kColsumThreads = 512;
-
-inline ColsumGeom colsum_geom(int64_t rows, int64_t cols) {
-  ColsumGeom g;
-  const int64_t nv = cols / 8;
-  int nvw = 1;
-  while (nvw * 2 <= 256 && nvw * 2 <= nv) nvw *= 2;
-  g.nvw = nvw;
-  g.rl = kColsumThreads / nvw;
-  g.cb_count = int((nv + nvw - 1) / nvw);
-  int64_t rg = (rows + 4 * g.rl - 1) / (4 * g.rl);  // >= 4 rows per lane
-  const int64_t cap = std::min<int64_t>(kMaxRowGroups, kMaxParts / g.cb_count);
-  if (rg > cap) rg = cap;
-  if (rg < 1) rg = 1;
-  g.rg_count = int(rg);
-  g.rpg = int((rows + rg - 1) / rg);
-  return g;
-}
-
-// GELU_BWD: x is the gradient dy of a GELU's output, h its input; the pass
-// works on (and writes to act) the gradient of the input, gelu_bwd(h, dy).
-template <typename InT, bool GELU_BWD = false>
-__global__ __launch_bounds__(kColsumThreads) void amax_colsum_kernel(
-    const InT* __restrict__ x, int64_t rows, int64_t cols, ColsumGeom geo,
-    uint32_t* __restrict__ part, float* __restrict__ cs_part, const float* __restrict__ h = nullptr,
-    float* __restrict__ act = nullptr) {
-  __shared__ uint32_t red[kColsumThreads / 64];
-  __shared__ float csum[kColsumThreads * 8];
-  const int cb = blockIdx.x % geo.cb_count, rg = blockIdx.x / geo.cb_count;
-  const int lc = threadIdx.x % geo.nvw, lr = threadIdx.x / geo.nvw;
-  const int64_t cv = int64_t(cb) * geo.nvw + lc;
-  const bool cvalid = cv * 8 < cols;
-  const int64_t r_beg = int64_t(rg) * geo.rpg;
-  const int64_t r_end = std::min<int64_t>(rows, r_beg + geo.rpg);
-  float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+// grad = gelu_bwd(h, dy) (written out) and this workgroup's partial max
+// |grad| -> part[blockIdx.x]: the producer of the per-tensor quantisation of
+// a GELU's input gradient.
+// dy and grad may be the same buffer (each element is read, then written,
+// by the same lane).
+__global__ __launch_bounds__(kGeluThreads) void gelu_bwd_amax_kernel(
+    const float* dy, const float* __restrict__ h, int64_t n, float* grad,
+    uint32_t* __restrict__ part) {
+  __shared__ uint32_t red[kGeluThreads / 64];
   uint32_t m = 0;
-  if (cvalid) {
-    int64_t r = r_beg + lr;
-    // GELU_BWD: v = gelu_bwd(h, dy), written to act at the same offset
-    auto produce = [&](int64_t off, float* v) {
-      if constexpr (GELU_BWD) {
-        float hv[8];
-        load8(h + off, hv);
+  const int64_t nvec = n >> 3;
+  const int64_t stride = int64_t(gridDim.x) * kGeluThreads;
+  for (int64_t i = int64_t(blockIdx.x) * kGeluThreads + threadIdx.x; i < nvec; i += stride) {
+    float v[8], hv[8];
+    load8(dy + i * 8, v);
+    load8(h + i * 8, hv);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) v[j] = gelu_bwd_f32(hv[j], v[j]);
-        store8(act + off, v);
-      }
-    };
-    // rows in flight per lane: 4, or 1 with the GELU producer (two inputs
-    // and its branching erf / exp); each lane still adds its rows in row order
-    constexpr int U = GELU_BWD ? 1 : 4;
-    for (; r + (U - 1) * geo.rl < r_end; r += U * geo.rl) {
-      float v[U][8];
+    for (int j = 0; j < 8; ++j) v[j] = gelu_bwd_f32(hv[j], v[j]);
+    store8(grad + i * 8, v);
+    const uint32_t m01 = umax(absbits(v[0]), absbits(v[1])), m23 = umax(absbits(v[2]), absbits(v[3]));
+    const uint32_t m45 = umax(absbits(v[4]), absbits(v[5])), m67 = umax(absbits(v[6]), absbits(v[7]));
+    m = umax(m, umax(umax(m01, m23), umax(m45, m67)));
+  }
+  for (int64_t t = nvec * 8 + int64_t(blockIdx.x) * kGeluThreads + threadIdx.x; t < n;
+       t += stride) {
+    const float v = gelu_bwd_f32(h[t], dy[t]);
+    grad[t] = v;
+    m = umax(m, absbits(v));
+  }
+  m = block_umax_nt<kGeluThreads>(m, red);
+  if (threadIdx.x == 0) part[blockIdx.x] = m;
+}
+
+// out = a * b and this workgroup's partial max |out| -> part[blockIdx.x]
+// (the GELU backward from its saved derivative factor).  out may be a.
+__global__ __launch_bounds__(kGeluThreads) void mul_amax_kernel(const float* a,
+                                                                const float* __restrict__ b,
+                                                                int64_t n, float* out,
+                                                                uint32_t* __restrict__ part) {
+  __shared__ uint32_t red[kGeluThreads / 64];
+  uint32_t m = 0;
+  const int64_t nvec = n >> 3;
+  const int64_t stride = int64_t(gridDim.x) * kGeluThreads;
+  for (int64_t i = int64_t(blockIdx.x) * kGeluThreads + threadIdx.x; i < nvec; i += stride) {
+    float v[8], w[8];
+    load8(a + i * 8, v);
+    load8(b + i * 8, w);
 #pragma unroll
-      for (int u = 0; u < U; ++u) load8(x + (r + u * geo.rl) * cols + cv * 8, v[u]);
+    for (int j = 0; j < 8; ++j) v[j] = v[j] * w[j];
+    store8(out + i * 8, v);
 #pragma unroll
-      for (int u = 0; u < U; ++u) produce((r + u * geo.rl) * cols + cv * 8, v[u]);
-#pragma unroll
-      for (int u = 0; u < U; ++u)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          acc[j] += v[u][j];
-          m = umax(m, absbits(v[u][j]));
-        }
-    }
-    for (; r < r_end; r += geo.rl) {
-      float v[8];
-      load8(x + r * cols + cv * 8, v);
-      produce(r * cols + cv * 8, v);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        acc[j] += v[j];
-        m = umax(m, absbits(v[j]));
-      }
+    for (int j = 0; j < 8; ++j) m = umax(m, absbits(v[j]));
+  }
+  for (int64_t t = nvec * 8 + int64_t(blockIdx.x) * kGeluThreads + threadIdx.x; t < n;
+       t += stride) {
+    const float v = a[t] * b[t];
+    out[t] = v;
+    m = umax(m, absbits(v));
+  }
+  m = block_umax_nt<kGeluThreads>(m, red);
+  if (threadIdx.x == 0) part[blockIdx.x] = m;
+}
+
+// ---- premises of the GELU amax rule ---------------------------------------
+// Checked once per device over every fp32 input: (1) gelu_f32 is
+// non-decreasing on [+0, +inf] (each positive bit pattern against the next);
+// (2) T = max |gelu_f32(x)| over the negative numbers from -0 to the most
+// negative finite value.  The check kernel writes per-workgroup results, a
+// one-workgroup finaliser reduces them and publishes `done` last.
+constexpr int kPremiseWgs = 1024;
+struct GeluPremise {
+  uint32_t done;
+  uint32_t violations;
+  uint32_t t_bits;
+  uint32_t pad;
+  uint32_t wg_viol[kPremiseWgs];
+  uint32_t wg_t[kPremiseWgs];
+};
+__device__ GeluPremise g_gelu_premise;
+
+__global__ __launch_bounds__(kThreads) void gelu_premise_check_kernel() {
+  __shared__ uint32_t red[kThreads / 64];
+  // positive side: bit patterns p in [0, 0x7F800000), each against p + 1
+  constexpr uint32_t kPos = kGeluKeyPosInf;
+  // negative side: -0 ... -FLT_MAX, bit patterns 0x80000000 + [0, 0x7F800000)
+  const uint32_t per = (kPos + uint32_t(kPremiseWgs) * kThreads - 1) / (uint32_t(kPremiseWgs) * kThreads);
+  const uint32_t t0 = (uint32_t(blockIdx.x) * kThreads + threadIdx.x) * per;
+  uint32_t viol = 0, tmax = 0;
+  if (t0 < kPos) {
+    float prev = gelu_f32(__uint_as_float(t0));
+    for (uint32_t k = 0; k < per && t0 + k < kPos; ++k) {
+      const uint32_t p = t0 + k;
+      const float next = gelu_f32(__uint_as_float(p + 1));
+      // a decrease, or a NaN anywhere on the way to +inf, fails the premise
+      viol += (next < prev || next != next || prev != prev) ? 1u : 0u;
+      prev = next;
+      tmax = umax(tmax, absbits(gelu_f32(__uint_as_float(0x80000000u | p))));
     }
   }
-#pragma unroll
-  for (int j = 0; j < 8; ++j) csum[threadIdx.x * 8 + j] = acc[j];
-  m = block_umax_nt<kColsumThreads>(m, red);  // includes a barrier: csum is complete
-  if (threadIdx.x == 0) part[blockIdx.x] = m;
-  if (lr == 0 && cvalid) {
-    float o[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) o[j] = csum[lc * 8 + j];
-    for (int k = 1; k < geo.rl; ++k)
-#pragma unroll
-      for (int j = 0; j < 8; ++j) o[j] += csum[(k * geo.nvw + lc) * 8 + j];
-    float* dst = cs_part + int64_t(rg) * cols + cv * 8;
-    *reinterpret_cast<float4*>(dst) = make_float4(o[0], o[1], o[2], o[3]);
-    *reinterpret_cast<float4*>(dst + 4) = make_float4(o[4], o[5], o[6], o[7]);
+  viol = block_umax_nt<kThreads>(viol, red);  // any violation (the count is not needed)
+  __syncthreads();
+  tmax = block_umax_nt<kThreads>(tmax, red);
+  if (threadIdx.x == 0) {
+    g_gelu_premise.wg_viol[blockIdx.x] = viol;
+    g_gelu_premise.wg_t[blockIdx.x] = tmax;
   }
 }
 
-// out[c] = sum over row groups of cs_part[rg, c]: a workgroup owns 32
+__global__ __launch_bounds__(kThreads) void gelu_premise_finalize_kernel() {
+  __shared__ uint32_t red[kThreads / 64];
+  uint32_t v = 0, t = 0;
+  for (int i = threadIdx.x; i < kPremiseWgs; i += kThreads) {
+    v = umax(v, g_gelu_premise.wg_viol[i]);
+    t = umax(t, g_gelu_premise.wg_t[i]);
+  }
+  v = block_umax_nt<kThreads>(v, red);
+  __syncthreads();
+  t = block_umax_nt<kThreads>(t, red);
+  if (threadIdx.x == 0) {
+    g_gelu_premise.violations = v;
+    g_gelu_premise.t_bits = t;
+    __hip_atomic_store(&g_gelu_premise.done, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+// The GELU amax rule on the keys of h's producer (keys[2 i], keys[2 i + 1],
+// i < n_keys): one workgroup writes rule[0] = 1 and rule[1] = the amax bits
+// when the rule applies, else rule[0] = 0.
+__global__ __launch_bounds__(kThreads) void gelu_rule_decide_kernel(
+    const uint32_t* __restrict__ keys, int n_keys, uint32_t* __restrict__ rule) {
+  __shared__ uint32_t red[kThreads / 64];
+  __shared__ uint32_t red2[kThreads / 64];
+  uint32_t imax_biased = 0, umx = 0;  // int max kept as bits ^ 0x80000000 (unsigned order)
+  for (int i = threadIdx.x; i < n_keys; i += kThreads) {
+    imax_biased = umax(imax_biased, keys[2 * i] ^ 0x80000000u);
+    umx = umax(umx, keys[2 * i + 1]);
+  }
+  imax_biased = block_umax_nt<kThreads>(imax_biased, red);
+  umx = block_umax_nt<kThreads>(umx, red2);
+  if (threadIdx.x != 0) return;
+  const uint32_t imax = imax_biased ^ 0x80000000u;
+  // the premise check ran on this device (agent scope)
+  const bool premises =
+      __hip_atomic_load(&g_gelu_premise.done, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) == 1u &&
+      __hip_atomic_load(&g_gelu_premise.violations, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+          0u;
+  bool ok = false;
+  uint32_t abits = 0;
+  if (premises && umx < kGeluKeyNegNanInf && int32_t(imax) >= 0 && imax <= kGeluKeyPosInf) {
+    abits = absbits(gelu_f32(__uint_as_float(imax)));
+    ok = abits >= __hip_atomic_load(&g_gelu_premise.t_bits, __ATOMIC_RELAXED,
+                                    __HIP_MEMORY_SCOPE_AGENT);
+  }
+  rule[0] = ok ? 1u : 0u;
+  rule[1] = abits;
+}
+
+// Partial maxima of |gelu(h)| for the quantising pass: with the rule
+// (rule[0] == 1) workgroup 0 writes its amax and the others 0; otherwise
+// each workgroup takes its grid-stride share of h.
+__global__ __launch_bounds__(kGeluThreads) void gelu_amax_fallback_kernel(
+    const float* __restrict__ h, int64_t n, const uint32_t* __restrict__ rule,
+    uint32_t* __restrict__ part) {
+  __shared__ uint32_t red[kGeluThreads / 64];
+  if (rule[0] == 1u) {
+    if (threadIdx.x == 0) part[blockIdx.x] = blockIdx.x == 0 ? rule[1] : 0u;
+    return;
+  }
+  uint32_t m = 0;
+  const int64_t nvec = n >> 3;
+  const int64_t stride = int64_t(gridDim.x) * kGeluThreads;
+  for (int64_t i = int64_t(blockIdx.x) * kGeluThreads + threadIdx.x; i < nvec; i += stride) {
+    float v[8];
+    load8(h + i * 8, v);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) m = umax(m, absbits(gelu_f32(v[j])));
+  }
+  for (int64_t t = nvec * 8 + int64_t(blockIdx.x) * kGeluThreads + threadIdx.x; t < n;
+       t += stride)
+    m = umax(m, absbits(gelu_f32(h[t])));
+  m = block_umax_nt<kGeluThreads>(m, red);
+  if (threadIdx.x == 0) part[blockIdx.x] = m;
+}
+
+// out[c] = sum over row groups of cs_part[rg, c] (rg < rg_count): a workgroup owns 32
 // columns with 8 row lanes, each lane summing every 8th row group with four
 // independent loads in flight, then the lanes meet in LDS (fixed order).
 __global__ __launch_bounds__(kThreads) void colsum_finalize_kernel(const float* __restrict__ cs_part,
@@ -692,31 +766,83 @@ TCFP_DEV void loadvec<float>(const float* p, float* v) {
 template <>
 TCFP_DEV void loadvec<uint16_t>(const uint16_t* p, float* v) { load8(p, v); }
 
-template <typename InT, int FMT>
+// GELU_IN: the tile holds h and the pass quantises gelu(h), recomputed
+// here (a producer wrote h and the partial maxima of |gelu(h)|); act_out
+// and dg_out, when not null, receive gelu(h) and its derivative factor.
+// COLSUM: the pass also writes the column sums of the values it quantises
+// (before scaling) per 64-row group to cs_part[group, col], in the order
+// of kColGroup's definition (rows past the end count as +0).  The tile's
+// row lanes hold rows tr = pass * RPI + lane: the folds over row distances
+// of RPI and more stay in a lane's registers, the rest meet in LDS.
+// qt may be null (no transposed copy).
+template <typename InT, int FMT, bool GELU_IN = false, bool COLSUM = false>
 __global__ __launch_bounds__(kThreads) void quant_t_kernel(
     const InT* __restrict__ x, int64_t rows, int64_t cols, const uint32_t* __restrict__ part,
     int g, int bf16_rule, const float* __restrict__ scale_in, uint8_t* __restrict__ q,
-    uint8_t* __restrict__ qt, float* scale_out, float* inv_out) {
+    uint8_t* __restrict__ qt, float* scale_out, float* inv_out,
+    float* __restrict__ cs_part = nullptr, float* __restrict__ act_out = nullptr,
+    float* __restrict__ dg_out = nullptr) {
   using TL = TileLoad<InT>;
   constexpr int VEC = TL::VEC;
   __shared__ uint32_t red[kThreads / 64];
   __shared__ uint32_t tile[kTile * kTilePitch];
+  // passes per half row group; the tile's two row groups, RPI row lanes each
+  constexpr int PH = kColHalf / TL::RPI;
+  static_assert(PH >= 1 && kTile == 2 * kColGroup, "row lanes per pass vs. row groups");
+  __shared__ float csum[COLSUM ? 2 * TL::RPI * kTile : 1];
   const float mx = FMT == TCFP_FP8_E5M2 ? kE5M2Max : kE4M3Max;
   const float s = consumer_scale(scale_in, part, g, bf16_rule != 0, mx, scale_out, inv_out, red);
   const TileGeom tg(cols);
   const int tc = (threadIdx.x % TL::TPR) * VEC;
+  const int rl = threadIdx.x / TL::TPR;
   const int64_t c = tg.c0 + tc;
+  float ys[COLSUM ? PH : 1][VEC];  // x[l] + x[l + 32] of this lane's rows l of the group
 #pragma unroll
   for (int it = 0; it < kTile / TL::RPI; ++it) {
-    const int tr = it * TL::RPI + threadIdx.x / TL::TPR;
+    const int tr = it * TL::RPI + rl;
     const int64_t r = tg.r0 + tr;
     const bool valid = r < rows && c < cols;
     float v[VEC];
     if (valid) {
       loadvec<InT>(x + r * cols + c, v);
+      if constexpr (GELU_IN) {
+        if (dg_out) {
+          float d[VEC];
+#pragma unroll
+          for (int j = 0; j < VEC; ++j) gelu_and_deriv(v[j], v[j], d[j]);
+          *reinterpret_cast<float4*>(dg_out + r * cols + c) = make_float4(d[0], d[1], d[2], d[3]);
+        } else {
+#pragma unroll
+          for (int j = 0; j < VEC; ++j) v[j] = gelu_f32(v[j]);
+        }
+        if (act_out)
+          *reinterpret_cast<float4*>(act_out + r * cols + c) = make_float4(v[0], v[1], v[2], v[3]);
+      }
     } else {
 #pragma unroll
       for (int j = 0; j < VEC; ++j) v[j] = 0.0f;
+    }
+    if constexpr (COLSUM) {
+      const int pg = it % (2 * PH);
+      if (pg < PH) {
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) ys[pg][j] = v[j];
+      } else {
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) ys[pg - PH][j] += v[j];
+      }
+      if (pg == 2 * PH - 1) {
+        // folds over row distances 16 ... RPI (passes PH / 2 ... 1 apart)
+#pragma unroll
+        for (int d = PH / 2; d >= 1; d /= 2)
+#pragma unroll
+          for (int p = 0; p < d; ++p)
+#pragma unroll
+            for (int j = 0; j < VEC; ++j) ys[p][j] += ys[p + d][j];
+        const int grp = it / (2 * PH);
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) csum[(grp * TL::RPI + rl) * kTile + tc + j] = ys[0][j];
+      }
     }
 #pragma unroll
     for (int j = 0; j < VEC; ++j) v[j] = clampf(v[j] * s, mx);
@@ -727,11 +853,27 @@ __global__ __launch_bounds__(kThreads) void quant_t_kernel(
       if constexpr (VEC == 4) *reinterpret_cast<uint32_t*>(q + r * cols + c) = wd[0];
       else *reinterpret_cast<uint2*>(q + r * cols + c) = make_uint2(wd[0], wd[1]);
     }
+    if (qt) {
 #pragma unroll
-    for (int j = 0; j < VEC / 4; ++j) tile[tr * kTilePitch + tc / 4 + j] = wd[j];
+      for (int j = 0; j < VEC / 4; ++j) tile[tr * kTilePitch + tc / 4 + j] = wd[j];
+    }
   }
   __syncthreads();
-  store_transposed(tile, tg, rows, cols, qt, threadIdx.x);
+  if constexpr (COLSUM) {
+    // the folds over row distances RPI / 2 ... 1: one (group, column) per thread
+    static_assert(kThreads == 2 * kTile, "one thread per group column");
+    const int grp = threadIdx.x / kTile, cl = threadIdx.x % kTile;
+    float w[TL::RPI];
+#pragma unroll
+    for (int k = 0; k < TL::RPI; ++k) w[k] = csum[(grp * TL::RPI + k) * kTile + cl];
+#pragma unroll
+    for (int d = TL::RPI / 2; d >= 1; d /= 2)
+#pragma unroll
+      for (int k = 0; k < d; ++k) w[k] += w[k + d];
+    const int64_t cc = tg.c0 + cl, r = tg.r0 + grp * kColGroup;
+    if (cc < cols && r < rows) cs_part[(r / kColGroup) * cols + cc] = w[0];
+  }
+  if (qt) store_transposed(tile, tg, rows, cols, qt, threadIdx.x);
 }
 
 // ===========================================================================
@@ -1788,43 +1930,39 @@ size_t tcfp_workspace_bytes(void) { return sizeof(PartWs); }
 
 namespace {
 
-// pre_g > 0: a producer kernel already wrote pre_g partial maxima of x to
-// the workspace (no amax pass here; col_sum must be null).
+// pre_g > 0: a producer kernel already wrote pre_g partial maxima of the
+// values to quantise to the workspace (no amax pass here).
+// gelu_in: x is fp32 h and the values quantised are gelu(h), recomputed in
+// the quantising pass (cols % 8 == 0).
+// col_sum: the column sums of the values quantised, summed per 128-row tile
+// by the tiled pass into cs_ws [ceil(rows / 128), cols], then over the
+// tiles in order (cols % 8 == 0).
 int quantize_impl(const void* x, int x_dtype, int64_t rows, int64_t cols, int fp8_fmt,
                   const float* scale_in, uint8_t* q, uint8_t* q_t, float* scale_out,
                   float* inv_out, void* workspace, float* col_sum, float* cs_ws,
-                  hipStream_t st, int pre_g = 0) {
+                  hipStream_t st, int pre_g = 0, bool gelu_in = false, float* act_out = nullptr,
+                  float* dg_out = nullptr) {
   if (rows < 0 || cols < 0) return TCFP_ERR_SHAPE;
   if (x_dtype != TCFP_DTYPE_F32 && x_dtype != TCFP_DTYPE_BF16) return TCFP_ERR_DTYPE;
   if (fp8_fmt != TCFP_FP8_E4M3 && fp8_fmt != TCFP_FP8_E5M2) return TCFP_ERR_DTYPE;
   if (!aligned16(x) || !inv_out) return TCFP_ERR_ALIGN;
   if (!scale_in && !workspace) return TCFP_ERR_WORKSPACE;
+  if ((col_sum || gelu_in) && cols % 8 != 0) return TCFP_ERR_SHAPE;
+  if (gelu_in && x_dtype != TCFP_DTYPE_F32) return TCFP_ERR_DTYPE;
+  if (!gelu_in && (act_out || dg_out)) return TCFP_ERR_SHAPE;
+  if ((act_out && !aligned16(act_out)) || (dg_out && !aligned16(dg_out))) return TCFP_ERR_ALIGN;
   const int64_t n = rows * cols;
   if (n >= 8 && (reinterpret_cast<uintptr_t>(q) & 7u) != 0) return TCFP_ERR_ALIGN;
   PartWs* ws = static_cast<PartWs*>(workspace);
   const bool bf = x_dtype == TCFP_DTYPE_BF16;
   uint32_t* part = ws ? ws->a : nullptr;
   int g = 0;
-  ColsumGeom geo{};
-  if (col_sum && n > 0) {
-    geo = colsum_geom(rows, cols);
-    g = geo.cb_count * geo.rg_count;
-    if (bf)
-      amax_colsum_kernel<uint16_t><<<g, kColsumThreads, 0, st>>>(static_cast<const uint16_t*>(x), rows,
-                                                           cols, geo, part, cs_ws);
-    else
-      amax_colsum_kernel<float><<<g, kColsumThreads, 0, st>>>(static_cast<const float*>(x), rows, cols,
-                                                        geo, part, cs_ws);
-    colsum_finalize_kernel<<<unsigned((cols + 31) / 32), kThreads, 0, st>>>(cs_ws, geo.rg_count,
-                                                                            cols, col_sum);
-  } else if (col_sum && cols > 0) {
-    // no rows: the column sums are zero
-    colsum_finalize_kernel<<<unsigned((cols + 31) / 32), kThreads, 0, st>>>(cs_ws, 0, cols,
-                                                                            col_sum);
-  }
   if (pre_g > 0) {
     g = pre_g;
-  } else if (!col_sum && !scale_in) {
+  } else if (!scale_in && gelu_in) {
+    g = gelu_grid(n);
+    gelu_amax_kernel<<<g, kGeluThreads, 0, st>>>(static_cast<const float*>(x), n, nullptr, part);
+  } else if (!scale_in) {
     g = parts_for((n + 7) / 8);
     if (bf)
       amax_part_kernel<uint16_t, false, false><<<g, kThreads, 0, st>>>(
@@ -1834,21 +1972,41 @@ int quantize_impl(const void* x, int x_dtype, int64_t rows, int64_t cols, int fp
           static_cast<const float*>(x), nullptr, n, part, nullptr, nullptr);
   }
   const int bfr = bf ? 1 : 0;
-  const bool tiled = q_t && n > 0 && cols % 8 == 0;
+  const int64_t row_tiles = (rows + kTile - 1) / kTile;
+  const bool tiled = (q_t || col_sum || gelu_in) && n > 0 && cols % 8 == 0;
   if (tiled) {
-    const int64_t tiles = ((rows + kTile - 1) / kTile) * ((cols + kTile - 1) / kTile);
+    const int64_t tiles = int64_t(row_tiles) * ((cols + kTile - 1) / kTile);
     if (!grid_x_fits(tiles, kThreads)) return TCFP_ERR_SHAPE;
-#define TCFP_QT(T, F)                                                                          \
-  quant_t_kernel<T, F><<<unsigned(tiles), kThreads, 0, st>>>(static_cast<const T*>(x), rows,  \
-                                                             cols, part, g, bfr, scale_in, q, \
-                                                             q_t, scale_out, inv_out)
-    if (bf) {
-      if (fp8_fmt == TCFP_FP8_E5M2) TCFP_QT(uint16_t, TCFP_FP8_E5M2); else TCFP_QT(uint16_t, TCFP_FP8_E4M3);
+#define TCFP_QT(T, F, GL, CS)                                                                   \
+  quant_t_kernel<T, F, GL, CS><<<unsigned(tiles), kThreads, 0, st>>>(                          \
+      static_cast<const T*>(x), rows, cols, part, g, bfr, scale_in, q, q_t, scale_out, inv_out, \
+      cs_ws, act_out, dg_out)
+#define TCFP_QT_F(T, GL, CS)                                             \
+  do {                                                                   \
+    if (fp8_fmt == TCFP_FP8_E5M2) TCFP_QT(T, TCFP_FP8_E5M2, GL, CS);     \
+    else TCFP_QT(T, TCFP_FP8_E4M3, GL, CS);                              \
+  } while (0)
+    if (gelu_in) {
+      if (col_sum) TCFP_QT_F(float, true, true); else TCFP_QT_F(float, true, false);
+    } else if (bf) {
+      if (col_sum) TCFP_QT_F(uint16_t, false, true); else TCFP_QT_F(uint16_t, false, false);
     } else {
-      if (fp8_fmt == TCFP_FP8_E5M2) TCFP_QT(float, TCFP_FP8_E5M2); else TCFP_QT(float, TCFP_FP8_E4M3);
+      if (col_sum) TCFP_QT_F(float, false, true); else TCFP_QT_F(float, false, false);
     }
+#undef TCFP_QT_F
 #undef TCFP_QT
+    if (col_sum) {
+      const int64_t groups = (rows + kColGroup - 1) / kColGroup;
+      if (groups > INT32_MAX) return TCFP_ERR_SHAPE;
+      colsum_finalize_kernel<<<unsigned((cols + 31) / 32), kThreads, 0, st>>>(cs_ws, int(groups),
+                                                                              cols, col_sum);
+    }
     return launch_status();
+  }
+  if (col_sum && cols > 0) {
+    // no rows: the column sums are zero
+    colsum_finalize_kernel<<<unsigned((cols + 31) / 32), kThreads, 0, st>>>(cs_ws, 0, cols,
+                                                                            col_sum);
   }
   // flat (also for empty tensors: one workgroup still publishes scale / inv)
   const int gq = grid_for((n + 15) / 16, 8);
@@ -1869,6 +2027,91 @@ int quantize_impl(const void* x, int x_dtype, int64_t rows, int64_t cols, int fp
 }
 
 }  // namespace
+
+namespace tcfp {
+
+int max_parts() { return kMaxParts; }
+
+namespace {
+std::mutex g_premise_mu;
+bool g_premise_launched[64] = {};
+
+// Launches the premise check of the GELU amax rule on `st`, once per device
+// and process.  Not while `st` is being captured (a graph would re-run it on
+// every replay): until a later call launches it, the rule's users take the
+// full pass.
+void launch_gelu_premise_once(hipStream_t st) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return;
+  std::lock_guard<std::mutex> lk(g_premise_mu);
+  if (g_premise_launched[dev]) return;
+  g_premise_launched[dev] = true;
+  gelu_premise_check_kernel<<<kPremiseWgs, kThreads, 0, st>>>();
+  gelu_premise_finalize_kernel<<<1, kThreads, 0, st>>>();
+}
+}  // namespace
+
+int gelu_quantize_from_keys(const float* h, int64_t rows, int64_t cols, int fp8_fmt, float* act,
+                            float* dgelu, uint8_t* q, uint8_t* q_t, float* inv_out,
+                            void* workspace, const uint32_t* keys, int n_keys, void* stream) {
+  if (rows < 0 || cols < 0 || cols % 8 != 0) return TCFP_ERR_SHAPE;
+  if (!workspace) return TCFP_ERR_WORKSPACE;
+  if (n_keys < 1 || n_keys > kMaxParts / 2 || !keys) return TCFP_ERR_SHAPE;
+  const int64_t n = rows * cols;
+  if (n == 0)
+    return quantize_impl(h, TCFP_DTYPE_F32, rows, cols, fp8_fmt, nullptr, q, q_t, nullptr,
+                         inv_out, workspace, nullptr, nullptr, static_cast<hipStream_t>(stream),
+                         0, true, act, dgelu);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  launch_gelu_premise_once(st);
+  PartWs* ws = static_cast<PartWs*>(workspace);
+  gelu_rule_decide_kernel<<<1, kThreads, 0, st>>>(keys, n_keys, ws->gelu_rule);
+  // the full pass (rare) runs on a quarter of the usual grid: with the rule
+  // every workgroup only writes its slot
+  const int g = std::max(1, gelu_grid(n) / 4);
+  gelu_amax_fallback_kernel<<<g, kGeluThreads, 0, st>>>(h, n, ws->gelu_rule, ws->a);
+  return quantize_impl(h, TCFP_DTYPE_F32, rows, cols, fp8_fmt, nullptr, q, q_t, nullptr, inv_out,
+                       workspace, nullptr, nullptr, st, g, true, act, dgelu);
+}
+
+int mul_quantize_colsum(const float* a, const float* b, int64_t rows, int64_t cols, int fp8_fmt,
+                        float* out, uint8_t* q, uint8_t* q_t, float* inv_out, float* col_sum,
+                        void* workspace, float* cs_ws, void* stream) {
+  if (rows < 0 || cols < 0 || cols % 8 != 0) return TCFP_ERR_SHAPE;
+  if (!workspace) return TCFP_ERR_WORKSPACE;
+  if (!aligned16(a) || !aligned16(b) || !aligned16(out)) return TCFP_ERR_ALIGN;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t n = rows * cols;
+  int g = 0;
+  if (n > 0) {
+    g = gelu_grid(n);
+    mul_amax_kernel<<<g, kGeluThreads, 0, st>>>(a, b, n, out, static_cast<PartWs*>(workspace)->a);
+  }
+  return quantize_impl(out, TCFP_DTYPE_F32, rows, cols, fp8_fmt, nullptr, q, q_t, nullptr,
+                       inv_out, workspace, col_sum, cs_ws, st, g);
+}
+
+int colsum_finalize(const float* cs_ws, int64_t groups, int64_t cols, float* col_sum,
+                    void* stream) {
+  if (cols <= 0) return TCFP_OK;
+  if (groups < 0 || groups > INT32_MAX) return TCFP_ERR_SHAPE;
+  colsum_finalize_kernel<<<unsigned((cols + 31) / 32), kThreads, 0,
+                           static_cast<hipStream_t>(stream)>>>(cs_ws, int(groups), cols, col_sum);
+  return launch_status();
+}
+
+int quantize_with_parts(const void* x, int x_dtype, int64_t rows, int64_t cols, int fp8_fmt,
+                        uint8_t* q, uint8_t* q_t, float* inv_out, void* workspace,
+                        float* col_sum, float* cs_ws, void* stream, int pre_g, bool gelu_in) {
+  if (pre_g < 1 || pre_g > kMaxParts || !workspace) return TCFP_ERR_WORKSPACE;
+  return quantize_impl(x, x_dtype, rows, cols, fp8_fmt, nullptr, q, q_t, nullptr, inv_out,
+                       workspace, col_sum, cs_ws, static_cast<hipStream_t>(stream), pre_g,
+                       gelu_in);
+}
+
+}  // namespace tcfp
 
 extern "C" {
 
@@ -1937,9 +2180,21 @@ int tcfp_block_scales(const void* x, int x_dtype, int64_t rows, int64_t cols, in
   return launch_status();
 }
 
+int tcfp_gelu_amax_rule_status(int* checked, int* holds, float* bound) {
+  GeluPremise p;
+  // the header words only (done, violations, t_bits)
+  if (hipMemcpyFromSymbol(&p, HIP_SYMBOL(g_gelu_premise), 4 * sizeof(uint32_t), 0,
+                          hipMemcpyDeviceToHost) != hipSuccess)
+    return TCFP_ERR_HIP;
+  if (checked) *checked = p.done == 1u ? 1 : 0;
+  if (holds) *holds = (p.done == 1u && p.violations == 0u) ? 1 : 0;
+  if (bound) std::memcpy(bound, &p.t_bits, sizeof(float));
+  return TCFP_OK;
+}
+
 size_t tcfp_colsum_workspace_bytes(int64_t rows, int64_t cols) {
   if (rows <= 0 || cols <= 0 || cols % 8 != 0) return 0;
-  return size_t(colsum_geom(rows, cols).rg_count) * size_t(cols) * sizeof(float);
+  return size_t((rows + kColGroup - 1) / kColGroup) * size_t(cols) * sizeof(float);
 }
 
 int tcfp_quantize_per_tensor_colsum(const void* x, int x_dtype, int64_t rows, int64_t cols,
@@ -1947,7 +2202,6 @@ int tcfp_quantize_per_tensor_colsum(const void* x, int x_dtype, int64_t rows, in
                                     float* col_sum, void* workspace, void* colsum_ws,
                                     size_t colsum_ws_bytes, void* stream) {
   if (rows < 0 || cols < 0 || cols % 8 != 0) return TCFP_ERR_SHAPE;
-  if (cols / 8 > int64_t(kMaxParts) * 256) return TCFP_ERR_SHAPE;  // partial slots
   if (!col_sum) return TCFP_ERR_SHAPE;
   if (!workspace) return TCFP_ERR_WORKSPACE;
   if (rows > 0 && cols > 0 &&
@@ -1962,18 +2216,24 @@ int tcfp_quantize_per_tensor_colsum(const void* x, int x_dtype, int64_t rows, in
 }
 
 int tcfp_gelu_quantize_per_tensor(const float* h, int64_t rows, int64_t cols, int fp8_fmt,
-                                  float* act, uint8_t* q, uint8_t* q_t, float* inv_out,
-                                  void* workspace, void* stream) {
+                                  float* act, float* dgelu, uint8_t* q, uint8_t* q_t,
+                                  float* inv_out, void* workspace, void* stream) {
   if (rows < 0 || cols < 0) return TCFP_ERR_SHAPE;
   if (fp8_fmt != TCFP_FP8_E4M3 && fp8_fmt != TCFP_FP8_E5M2) return TCFP_ERR_DTYPE;
   if (!workspace) return TCFP_ERR_WORKSPACE;
-  if (!aligned16(h) || !aligned16(act) || !inv_out) return TCFP_ERR_ALIGN;
+  if (!aligned16(h) || (act && !aligned16(act)) || (dgelu && !aligned16(dgelu)) || !inv_out)
+    return TCFP_ERR_ALIGN;
   hipStream_t st = static_cast<hipStream_t>(stream);
+  if (cols % 8 == 0) {
+    // the amax pass, then the quantising pass recomputes gelu(h) (and its
+    // derivative factor) from h and writes what is asked for
+    return quantize_impl(h, TCFP_DTYPE_F32, rows, cols, fp8_fmt, nullptr, q, q_t, nullptr,
+                         inv_out, workspace, nullptr, nullptr, st, 0, true, act, dgelu);
+  }
+  // ragged rows: the amax pass writes gelu(h), which the flat pass quantises
+  if (!act || dgelu) return TCFP_ERR_SHAPE;
   const int64_t n = rows * cols;
-  // up to kMaxParts workgroups (measured: 2048 x 512 threads 42 us, 1024 x
-  // 512 threads 44.5 us for 32 Mi elements)
-  const int g = int(std::max<int64_t>(
-      1, std::min<int64_t>(kMaxParts, ((n + 7) / 8 + 2 * kGeluThreads - 1) / (2 * kGeluThreads))));
+  const int g = gelu_grid(n);
   gelu_amax_kernel<<<g, kGeluThreads, 0, st>>>(h, n, act, static_cast<PartWs*>(workspace)->a);
   return quantize_impl(act, TCFP_DTYPE_F32, rows, cols, fp8_fmt, nullptr, q, q_t, nullptr,
                        inv_out, workspace, nullptr, nullptr, st, g);
@@ -1986,34 +2246,25 @@ int tcfp_gelu_backward_quantize_per_tensor_colsum(const float* dy, const float* 
                                                   void* colsum_ws, size_t colsum_ws_bytes,
                                                   void* stream) {
   if (rows < 0 || cols < 0 || cols % 8 != 0) return TCFP_ERR_SHAPE;
-  if (cols / 8 > int64_t(kMaxParts) * 256) return TCFP_ERR_SHAPE;  // partial slots
   if (fp8_fmt != TCFP_FP8_E4M3 && fp8_fmt != TCFP_FP8_E5M2) return TCFP_ERR_DTYPE;
-  if (!col_sum) return TCFP_ERR_SHAPE;
   if (!workspace) return TCFP_ERR_WORKSPACE;
   if (!aligned16(dy) || !aligned16(h) || !aligned16(grad) || !inv_out) return TCFP_ERR_ALIGN;
   const int64_t n = rows * cols;
-  if (n > 0 && (!colsum_ws || colsum_ws_bytes < tcfp_colsum_workspace_bytes(rows, cols)))
+  if (col_sum && n > 0 &&
+      (!colsum_ws || colsum_ws_bytes < tcfp_colsum_workspace_bytes(rows, cols)))
     return TCFP_ERR_WORKSPACE;
-  if (n > 0 && (!aligned16(colsum_ws) || !aligned16(col_sum))) return TCFP_ERR_ALIGN;
+  if (col_sum && n > 0 && (!aligned16(colsum_ws) || !aligned16(col_sum))) return TCFP_ERR_ALIGN;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  float* cs_ws = static_cast<float*>(colsum_ws);
   int g = 0;
   if (n > 0) {
-    const ColsumGeom geo = colsum_geom(rows, cols);
-    g = geo.cb_count * geo.rg_count;
-    amax_colsum_kernel<float, true><<<g, kColsumThreads, 0, st>>>(
-        dy, rows, cols, geo, static_cast<PartWs*>(workspace)->a, cs_ws, h, grad);
-    colsum_finalize_kernel<<<unsigned((cols + 31) / 32), kThreads, 0, st>>>(cs_ws, geo.rg_count,
-                                                                            cols, col_sum);
-  } else if (cols > 0) {
-    // no rows: the column sums are zero
-    colsum_finalize_kernel<<<unsigned((cols + 31) / 32), kThreads, 0, st>>>(cs_ws, 0, cols,
-                                                                            col_sum);
+    g = gelu_grid(n);
+    gelu_bwd_amax_kernel<<<g, kGeluThreads, 0, st>>>(dy, h, n, grad,
+                                                     static_cast<PartWs*>(workspace)->a);
   }
   // an empty tensor has no partials: quantize_impl's own (empty) amax pass
   // publishes the clamped scale, as for any empty input
   return quantize_impl(grad, TCFP_DTYPE_F32, rows, cols, fp8_fmt, nullptr, q, q_t, nullptr,
-                       inv_out, workspace, nullptr, nullptr, st, g);
+                       inv_out, workspace, col_sum, static_cast<float*>(colsum_ws), st, g);
 }
 
 }  // extern "C"

@@ -226,15 +226,18 @@ def gelu_quantize_per_tensor(
     fp8_dtype: torch.dtype = torch.float8_e4m3fn,
     transpose: bool = False,
     return_act: bool = False,
+    return_dgelu: bool = False,
 ):
     """``quantize_per_tensor(torch.nn.functional.gelu(h))`` with the GELU
-    fused into the amax pass (the producer of the next layer's activation
-    quantisation, ``tcfp/nn/__init__.py:390`` applied to a GELU output).
+    evaluated inside the amax and quantising passes (the producer of the next
+    layer's activation quantisation, ``tcfp/nn/__init__.py:390`` applied to a
+    GELU output).
 
     ``h`` is fp32.  ``gelu(h)`` is computed as torch computes it (erf form,
-    bit for bit), written once, and quantised with the per-tensor amax rule.
-    Returns ``(q, inv)``, plus ``q_t`` when ``transpose``, plus the fp32
-    activation when ``return_act``.
+    bit for bit) and quantised with the per-tensor amax rule.  Returns
+    ``(q, inv)``, plus ``q_t`` when ``transpose``, plus the fp32 activation
+    when ``return_act``, plus the GELU derivative factor ``d`` (torch's GELU
+    backward is ``dy * d`` bit for bit) when ``return_dgelu``.
     """
     dev = _hip.require_gpu(h)
     if h.dtype != torch.float32:
@@ -242,13 +245,18 @@ def gelu_quantize_per_tensor(
     hc = h if h.is_contiguous() else h.contiguous()
     cols = hc.shape[-1] if hc.dim() > 0 else 1
     rows = hc.numel() // cols if cols else 0
-    act = torch.empty(h.shape, dtype=torch.float32, device=dev)
+    if return_dgelu and cols % 8 != 0:
+        raise ValueError(f"return_dgelu needs a last dim divisible by 8, got {cols}")
+    # a ragged last dim quantises gelu(h) from a stored copy
+    store = return_act or cols % 8 != 0
+    act = torch.empty(h.shape, dtype=torch.float32, device=dev) if store else None
+    dg = torch.empty(h.shape, dtype=torch.float32, device=dev) if return_dgelu else None
     q = torch.empty(h.shape, dtype=fp8_dtype, device=dev)
     q_t = torch.empty((cols, rows), dtype=fp8_dtype, device=dev) if transpose else None
     inv = torch.empty(1, dtype=torch.float32, device=dev)
     check(
         _hip.lib().tcfp_gelu_quantize_per_tensor(
-            ptr(hc), rows, cols, _fmt(fp8_dtype), ptr(act), ptr(q), ptr(q_t), ptr(inv),
+            ptr(hc), rows, cols, _fmt(fp8_dtype), ptr(act), ptr(dg), ptr(q), ptr(q_t), ptr(inv),
             ptr(_hip.workspace(dev)), _hip.stream_of(dev),
         ),
         "gelu_quantize_per_tensor",
@@ -258,6 +266,8 @@ def gelu_quantize_per_tensor(
         out = out + (q_t,)
     if return_act:
         out = out + (act,)
+    if return_dgelu:
+        out = out + (dg,)
     return out
 
 
@@ -534,6 +544,156 @@ def _dual_gemm(a, b_hi, b_lo, s_a, s_hi, s_lo, bias, out_dtype):
         ),
         "dual_gemm",
     )
+    return out
+
+
+def _gemm_operands(a, b_hi, b_lo):
+    a = _gemm_operand(a, "A")
+    b_hi = _gemm_operand(b_hi, "B_hi")
+    b_lo = _gemm_operand(b_lo, "B_lo")
+    if a.shape[1] != b_hi.shape[1] or b_hi.shape != b_lo.shape:
+        raise AssertionError(
+            f"Shape mismatch: A{tuple(a.shape)}, B_hi{tuple(b_hi.shape)}, B_lo{tuple(b_lo.shape)}"
+        )
+    if a.shape[1] % 16 != 0:
+        raise ValueError(f"K ({a.shape[1]}) must be divisible by 16")
+    if b_hi.stride(0) != b_lo.stride(0):
+        b_hi, b_lo = b_hi.contiguous(), b_lo.contiguous()
+    return a, b_hi, b_lo
+
+
+def dual_gemm_gelu_quantize(
+    act_fp8: torch.Tensor,
+    w_hi_fp8: torch.Tensor,
+    w_lo_fp8: torch.Tensor,
+    act_inv: torch.Tensor,
+    w_hi_inv: torch.Tensor,
+    w_lo_inv: torch.Tensor,
+    *,
+    bias: torch.Tensor | None = None,
+    fp8_dtype: torch.dtype = torch.float8_e4m3fn,
+    transpose: bool = False,
+    return_act: bool = False,
+    return_dgelu: bool = False,
+):
+    """``h = fused_dual_gemm_forward(...)`` (fp32) and
+    ``gelu_quantize_per_tensor(h)`` in one call, the GELU's amax taken from
+    the maximum of h the GEMM's epilogue records where the persistent launch
+    runs (the first layer of a TCFP -> GELU -> TCFP pair:
+    ``tcfp/kernels.py:1545-1601``, then ``tcfp/nn/__init__.py:390`` on the
+    GELU output).  Same bits as the two calls.
+
+    Returns ``(h, q, inv)``, then ``q_t`` when ``transpose``, then gelu(h)
+    when ``return_act``, then the GELU derivative factor when
+    ``return_dgelu`` (what ``dual_gemm_dgelu_quantize_colsum`` takes).
+    """
+    dev = _hip.require_gpu(act_fp8, w_hi_fp8, w_lo_fp8, act_inv, w_hi_inv, w_lo_inv, bias)
+    a, b_hi, b_lo = _gemm_operands(act_fp8, w_hi_fp8, w_lo_fp8)
+    m, k = a.shape
+    n = b_hi.shape[0]
+    if return_dgelu and n % 8 != 0:
+        raise ValueError(f"return_dgelu needs N divisible by 8, got {n}")
+    h = torch.empty((m, n), dtype=torch.float32, device=dev)
+    store = return_act or n % 8 != 0
+    act = torch.empty((m, n), dtype=torch.float32, device=dev) if store else None
+    dg = torch.empty((m, n), dtype=torch.float32, device=dev) if return_dgelu else None
+    q = torch.empty((m, n), dtype=fp8_dtype, device=dev)
+    q_t = torch.empty((n, m), dtype=fp8_dtype, device=dev) if transpose else None
+    inv = torch.empty(1, dtype=torch.float32, device=dev)
+    if bias is not None:
+        bias = _bias_f32(bias, n)
+    check(
+        _hip.lib().tcfp_dual_gemm_gelu_quantize(
+            ptr(a), _fmt(a.dtype), a.stride(0), ptr(b_hi), ptr(b_lo), _fmt(b_hi.dtype),
+            b_hi.stride(0), m, n, k, ptr(_scalar(act_inv, "scale_a")),
+            ptr(_scalar(w_hi_inv, "scale_hi")), ptr(_scalar(w_lo_inv, "scale_lo")), ptr(bias),
+            ptr(h), ptr(act), ptr(dg), _fmt(fp8_dtype), ptr(q), ptr(q_t), ptr(inv),
+            ptr(_hip.workspace(dev)), _hip.stream_of(dev),
+        ),
+        "dual_gemm_gelu_quantize",
+    )
+    out = (h, q, inv)
+    if transpose:
+        out = out + (q_t,)
+    if return_act:
+        out = out + (act,)
+    if return_dgelu:
+        out = out + (dg,)
+    return out
+
+
+def gelu_amax_rule_status() -> tuple[bool, bool, float]:
+    """``(checked, holds, bound)`` of the once-per-device premise check of
+    ``dual_gemm_gelu_quantize``'s amax rule (synchronous)."""
+    import ctypes
+
+    c, h, b = ctypes.c_int(0), ctypes.c_int(0), ctypes.c_float(0.0)
+    check(_hip.lib().tcfp_gelu_amax_rule_status(ctypes.addressof(c), ctypes.addressof(h),
+                                                 ctypes.addressof(b)), "gelu_amax_rule_status")
+    return bool(c.value), bool(h.value), float(b.value)
+
+
+def dual_gemm_dgelu_quantize_colsum(
+    grad_fp8: torch.Tensor,
+    w_hi_t: torch.Tensor,
+    w_lo_t: torch.Tensor,
+    grad_inv: torch.Tensor,
+    w_hi_inv: torch.Tensor,
+    w_lo_inv: torch.Tensor,
+    dgelu: torch.Tensor,
+    *,
+    fp8_dtype: torch.dtype = torch.float8_e5m2,
+    transpose: bool = False,
+    col_sum: bool = True,
+    return_grad: bool = False,
+):
+    """The dgrad of the second layer of a TCFP -> GELU -> TCFP pair with the
+    GELU backward in the GEMM's epilogue: ``g = (grad @ W) * dgelu``
+    (``fused_dual_gemm_backward_dx``, ``tcfp/kernels.py:1604-1666``, with the
+    transposed weight codes ``w_*_t`` [d_in, d_out], then torch's GELU
+    backward from the derivative factors ``dual_gemm_gelu_quantize`` /
+    ``gelu_quantize_per_tensor`` return) quantised per tensor with its column
+    sums (``tcfp/nn/__init__.py:494, 558`` on the first layer's gradient).
+    Same bits as ``_dual_gemm`` followed by torch's GELU backward and
+    ``quantize_per_tensor_colsum``.
+
+    Returns ``(q, inv)``, then ``q_t`` when ``transpose``, then the column
+    sums when ``col_sum``, then ``g`` when ``return_grad``.
+    """
+    dev = _hip.require_gpu(grad_fp8, w_hi_t, w_lo_t, grad_inv, w_hi_inv, w_lo_inv, dgelu)
+    a, b_hi, b_lo = _gemm_operands(grad_fp8, w_hi_t, w_lo_t)
+    m, k = a.shape
+    n = b_hi.shape[0]
+    if dgelu.dtype != torch.float32 or tuple(dgelu.shape) != (m, n):
+        raise AssertionError(
+            f"dgelu must be float32 of shape {(m, n)}, got {dgelu.dtype} {tuple(dgelu.shape)}")
+    if n % 8 != 0:
+        raise ValueError(f"column count ({n}) must be divisible by 8")
+    dc = dgelu if dgelu.is_contiguous() else dgelu.contiguous()
+    g = torch.empty((m, n), dtype=torch.float32, device=dev)
+    q = torch.empty((m, n), dtype=fp8_dtype, device=dev)
+    q_t = torch.empty((n, m), dtype=fp8_dtype, device=dev) if transpose else None
+    inv = torch.empty(1, dtype=torch.float32, device=dev)
+    cs = torch.empty(n, dtype=torch.float32, device=dev) if col_sum else None
+    nbytes = int(_hip.lib().tcfp_colsum_workspace_bytes(m, n)) if col_sum else 0
+    cws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=dev) if col_sum else None
+    check(
+        _hip.lib().tcfp_dual_gemm_dgelu_quantize_colsum(
+            ptr(a), _fmt(a.dtype), a.stride(0), ptr(b_hi), ptr(b_lo), _fmt(b_hi.dtype),
+            b_hi.stride(0), m, n, k, ptr(_scalar(grad_inv, "scale_a")),
+            ptr(_scalar(w_hi_inv, "scale_hi")), ptr(_scalar(w_lo_inv, "scale_lo")), ptr(dc),
+            ptr(g), _fmt(fp8_dtype), ptr(q), ptr(q_t), ptr(inv), ptr(cs),
+            ptr(_hip.workspace(dev)), ptr(cws), nbytes, _hip.stream_of(dev),
+        ),
+        "dual_gemm_dgelu_quantize_colsum",
+    )
+    out = (q, inv)
+    if transpose:
+        out = out + (q_t,)
+    if col_sum:
+        out = out + (cs,)
+    if return_grad:
+        out = out + (g,)
     return out
 
 

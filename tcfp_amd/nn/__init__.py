@@ -511,13 +511,17 @@ class _TCFP12FusedMLPFunction(torch.autograd.Function):
     No reference counterpart: the reference runs ``torch.nn.functional.gelu``
     between two ``_TCFP12TensorCoreFunction`` calls
     (``tcfp/nn/__init__.py:325-566``).  Every step here is that sequence's
-    step -- same kernels, same operands, same order of rounding -- except
-    that ``gelu`` is evaluated inside the pass that takes the amax of its
-    output (forward) or of its input gradient (backward, with the bias
-    column sums), and both are evaluated as torch evaluates them, bit for
-    bit.  The outputs, gradients and EF updates are therefore identical to
-    the unfused sequence; the hidden activation and its gradient are each
-    read once less.
+    step -- same operands, same order of rounding -- except that the
+    amax of ``gelu(h)`` comes from the maximum of h recorded in the epilogue
+    of layer 1's GEMM (exact under premises checked once per device, with a
+    full pass otherwise), ``gelu(h)`` is evaluated in layer 2's activation
+    quantisation, which also saves the GELU derivative factors in place of
+    h, and the GELU backward (one multiply by those factors), the amax of
+    its result and the bias column partials run in the epilogue of layer 2's
+    dgrad GEMM.  GELU and its backward are evaluated as torch evaluates
+    them, bit for bit, so outputs, gradients and EF updates are identical to
+    the unfused sequence; the separate GELU and amax passes over the hidden
+    activation and its gradient disappear.
     """
 
     @staticmethod
@@ -537,13 +541,14 @@ class _TCFP12FusedMLPFunction(torch.autograd.Function):
             a1, a1_inv, a1_t = K.quantize_per_tensor(x2d, transpose=True)
         else:
             (a1, a1_inv), a1_t = K.quantize_per_tensor(x2d), None
-        h = K.fused_dual_gemm_forward(a1, w1_hi, w1_lo, a1_inv, ih1, il1, bias=b1)
-
-        # GELU fused into layer 2's activation quantisation (nn:390 on gelu(h))
-        if need_dw2:
-            a2, a2_inv, a2_t = K.gelu_quantize_per_tensor(h, transpose=True)
-        else:
-            (a2, a2_inv), a2_t = K.gelu_quantize_per_tensor(h), None
+        # layer 1's GEMM, whose epilogue records max h for the GELU's amax,
+        # then layer 2's activation quantisation (nn:390 on gelu(h)), which
+        # also writes the GELU derivative factors the backward needs
+        res = K.dual_gemm_gelu_quantize(a1, w1_hi, w1_lo, a1_inv, ih1, il1, bias=b1,
+                                        transpose=need_dw2, return_dgelu=need_h)
+        _, a2, a2_inv = res[:3]
+        a2_t = res[3] if need_dw2 else None
+        dgelu = res[-1] if need_h else None
 
         # layer 2
         ef2 = _ef_buffer(st2, name2, w2)
@@ -555,14 +560,14 @@ class _TCFP12FusedMLPFunction(torch.autograd.Function):
         ctx.has_b1, ctx.has_b2 = b1 is not None, b2 is not None
         ctx.save_for_backward(
             a1_t, a1_inv, w1_hi_t, w1_lo_t, ih1, il1,
-            h if need_h else None, a2_t, a2_inv, w2_hi_t, w2_lo_t, ih2, il2,
+            dgelu, a2_t, a2_inv, w2_hi_t, w2_lo_t, ih2, il2,
         )
         return out.reshape(*input_shape[:-1], out.shape[-1])
 
     @staticmethod
     def backward(ctx, grad_output):
         (a1_t, a1_inv, w1_hi_t, w1_lo_t, ih1, il1,
-         h, a2_t, a2_inv, w2_hi_t, w2_lo_t, ih2, il2) = ctx.saved_tensors
+         dgelu, a2_t, a2_inv, w2_hi_t, w2_lo_t, ih2, il2) = ctx.saved_tensors
         need_dx, need_dw1, need_db1, need_dw2, need_db2 = ctx.needs_input_grad[:5]
         need_h = need_dx or need_dw1 or need_db1
         g2 = _flatten(grad_output)
@@ -572,7 +577,7 @@ class _TCFP12FusedMLPFunction(torch.autograd.Function):
 
         # layer 2 (nn:462-566): E5M2 grad + bias sums, dual dgrad, FP8 wgrad
         fuse_db2 = need_db2 and ctx.has_b2 and g2.shape[-1] % 8 == 0
-        dh = None
+        q2 = g2_inv = None
         if need_h or need_dw2:
             if fuse_db2:
                 res = K.quantize_per_tensor_colsum(g2, torch.float8_e5m2, transpose=need_dw2)
@@ -581,22 +586,23 @@ class _TCFP12FusedMLPFunction(torch.autograd.Function):
             else:
                 res = K.quantize_per_tensor(g2, torch.float8_e5m2, transpose=need_dw2)
             (q2, g2_inv, q2_t) = res if need_dw2 else (*res, None)
-            if need_h:
-                dh = K._dual_gemm(q2, w2_hi_t, w2_lo_t, g2_inv, ih2, il2, None, torch.float32)
             if need_dw2:
                 dw2 = K.fp8_gemm_nt(q2_t, a2_t, g2_inv, a2_inv)
         if need_db2 and ctx.has_b2 and db2 is None:
             db2 = g2.sum(dim=0)
 
-        # GELU backward fused into layer 1's gradient quantisation (its
-        # amax and bias column sums come from the same pass); layer 1
+        # layer 2's dgrad with the GELU backward, its amax and layer 1's
+        # bias column sums in the epilogue, then layer 1's E5M2 gradient
+        # quantisation; layer 1
         if need_h:
-            res = K.gelu_backward_quantize_per_tensor_colsum(
-                dh, h, torch.float8_e5m2, transpose=need_dw1,
+            sums = need_db1 and ctx.has_b1
+            res = K.dual_gemm_dgelu_quantize_colsum(
+                q2, w2_hi_t, w2_lo_t, g2_inv, ih2, il2, dgelu, transpose=need_dw1, col_sum=sums,
             )
-            q1, g1_inv, q1_t, cs1 = res if need_dw1 else (res[0], res[1], None, res[2])
-            if need_db1 and ctx.has_b1:
-                db1 = cs1.to(dh.dtype)
+            q1, g1_inv = res[0], res[1]
+            q1_t = res[2] if need_dw1 else None
+            if sums:
+                db1 = res[-1]
             if need_dx:
                 grad_x = K._dual_gemm(q1, w1_hi_t, w1_lo_t, g1_inv, ih1, il1, None,
                                       torch.float32).reshape(ctx.input_shape)

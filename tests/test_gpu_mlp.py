@@ -13,11 +13,13 @@ on raw bits:
 """
 import copy
 
+import numpy as np
 import pytest
 import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
+from oracle import quant as oq
 from tcfp_amd import kernels as K
 from tcfp_amd.nn import TCFPLinear, TCFPMLP, convert_to_tcfp, fuse_tcfp_mlp
 
@@ -46,12 +48,23 @@ def test_gelu_quantize_equals_torch_gelu_then_quantize(dev, shape):
     print(f"gelu quant {shape}", flush=True)
     g = torch.Generator().manual_seed(shape[0] * 7 + shape[1])
     h = _specials(torch.randn(shape, generator=g) * 3).to(dev)
-    q, inv, q_t, act = K.gelu_quantize_per_tensor(h, transpose=True, return_act=True)
+    dg_ok = shape[-1] % 8 == 0
+    res = K.gelu_quantize_per_tensor(h, transpose=True, return_act=True, return_dgelu=dg_ok)
+    q, inv, q_t, act = res[:4]
     ref = F.gelu(h)
     assert torch.equal(bits(act), bits(ref))
     q2, inv2, q2_t = K.quantize_per_tensor(ref, transpose=True)
     assert torch.equal(bits(q), bits(q2)) and torch.equal(bits(q_t), bits(q2_t))
     assert same_scalar(inv, inv2)
+    if dg_ok:
+        # torch's GELU backward is dy * (derivative factor), bit for bit
+        dy = torch.randn(shape, generator=g).to(dev)
+        hr = h.clone().requires_grad_(True)
+        F.gelu(hr).backward(dy)
+        assert torch.equal(bits(dy * res[-1]), bits(hr.grad))
+        # and without act the same codes
+        q3, inv3 = K.gelu_quantize_per_tensor(h)
+        assert torch.equal(bits(q3), bits(q)) and same_scalar(inv3, inv)
 
 
 @pytest.mark.parametrize("shape", [(8192, 4096), (300, 208), (8, 8), (1000, 24), (0, 64)])
@@ -88,6 +101,129 @@ def test_gelu_wrappers_reject_bad_inputs(dev):
     with pytest.raises(ValueError, match="divisible"):
         K.gelu_backward_quantize_per_tensor_colsum(torch.randn(8, 12, device=dev),
                                                    torch.randn(8, 12, device=dev))
+
+
+# ------------------------------------ GELU and its amax in the GEMM epilogue
+def _fp8_layer(dev, m, k, n, seed, a_dtype=torch.float8_e4m3fn):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(m, k, generator=g) * (1e-3 if a_dtype == torch.float8_e5m2 else 1.0)
+    W = torch.randn(n, k, generator=g) * 0.05
+    a, a_inv = K.quantize_per_tensor(x.to(dev), a_dtype)
+    hi, lo, ih, il = K.dual_quantize_per_tensor(W.to(dev))
+    return a, hi, lo, a_inv, ih, il
+
+
+# (m, k, n): persistent launches (more 256 x 128 tiles than CUs, the C4
+# layer shapes) and shapes that take the unfused fallback
+EPI_SHAPES = [(4096, 256, 4096), (8192, 1024, 4096), (2048, 512, 4224), (300, 64, 208),
+              (512, 256, 1024)]
+
+
+def _bias_case(case, h0, n, dev):
+    """Biases that steer the GELU amax rule: the rule holds ("normal"), or
+    the device falls back to the full pass (every h negative, a NaN, a -inf,
+    or max h so small that gelu(max h) is below the negative-side bound)."""
+    g = torch.Generator().manual_seed(n)
+    b = (torch.randn(n, generator=g) * 0.1).to(dev)
+    if case == "all_negative":
+        b = torch.full((n,), -1e4, device=dev)
+    elif case == "nan":
+        b[5] = float("nan")
+    elif case == "neg_inf":
+        b[7] = float("-inf")
+    elif case == "small_max":
+        b = torch.full((n,), -1e4, device=dev)
+        b[3] = 0.1 - h0[:, 3].max()
+    return b
+
+
+@pytest.mark.parametrize("case", ["normal", "all_negative", "nan", "neg_inf", "small_max"])
+@pytest.mark.parametrize("shape", EPI_SHAPES)
+def test_dual_gemm_gelu_quantize_equals_unfused(dev, shape, case):
+    m, k, n = shape
+    if case != "normal" and m * n > 2**25:
+        pytest.skip("fallback cases at the smaller shapes")
+    print(f"gemm+gelu quant {shape} {case}", flush=True)
+    a, hi, lo, a_inv, ih, il = _fp8_layer(dev, m, k, n, seed=m + k + n)
+    h0 = K._dual_gemm(a, hi, lo, a_inv, ih, il, None, torch.float32)
+    bias = _bias_case(case, h0, n, dev)
+    h, q, inv, q_t, act, dg = K.dual_gemm_gelu_quantize(
+        a, hi, lo, a_inv, ih, il, bias=bias, transpose=True, return_act=True, return_dgelu=True)
+    h_ref = K._dual_gemm(a, hi, lo, a_inv, ih, il, bias, torch.float32)
+    q2, inv2, q2_t, act2, dg2 = K.gelu_quantize_per_tensor(h_ref, transpose=True,
+                                                            return_act=True, return_dgelu=True)
+    assert torch.equal(bits(h), bits(h_ref))
+    assert torch.equal(bits(act), bits(act2)) and torch.equal(bits(dg), bits(dg2))
+    assert torch.equal(bits(q), bits(q2)) and torch.equal(bits(q_t), bits(q2_t))
+    assert same_scalar(inv, inv2)
+    # and against torch's GELU of the same h
+    ref = F.gelu(h_ref)
+    assert torch.equal(bits(act), bits(ref))
+    q3, inv3 = K.quantize_per_tensor(ref)
+    assert torch.equal(bits(q), bits(q3)) and same_scalar(inv, inv3)
+    # without the optional outputs: the same codes
+    h4, q4, inv4 = K.dual_gemm_gelu_quantize(a, hi, lo, a_inv, ih, il, bias=bias)
+    assert torch.equal(bits(q4), bits(q)) and same_scalar(inv4, inv)
+
+
+def test_gelu_amax_rule_premises_hold(dev):
+    a, hi, lo, a_inv, ih, il = _fp8_layer(dev, 4096, 256, 4096, seed=0)
+    K.dual_gemm_gelu_quantize(a, hi, lo, a_inv, ih, il)
+    torch.cuda.synchronize()
+    checked, holds, bound = K.gelu_amax_rule_status()
+    print(f"gelu amax rule: checked={checked} holds={holds} T={bound!r}", flush=True)
+    assert checked and holds
+    # max |gelu| over the negatives: 0.16997 at x = -0.7518
+    x = torch.linspace(-0.80, -0.70, 200001, device=dev)
+    assert abs(bound - float(F.gelu(x).abs().max())) < 1e-6
+
+
+@pytest.mark.parametrize("col_sum", [True, False])
+@pytest.mark.parametrize("shape", EPI_SHAPES + [(1000, 128, 24)])
+def test_dual_gemm_dgelu_quantize_colsum_equals_unfused(dev, shape, col_sum):
+    m, k, n = shape
+    print(f"dgrad+dgelu quant {shape} col_sum={col_sum}", flush=True)
+    a, hi, lo, a_inv, ih, il = _fp8_layer(dev, m, k, n, seed=3 * m + k, a_dtype=torch.float8_e5m2)
+    g = torch.Generator().manual_seed(m * 5 + n)
+    h = _specials(torch.randn(m, n, generator=g) * 3).to(dev)
+    dg = K.gelu_quantize_per_tensor(h, return_dgelu=True)[-1]
+    res = K.dual_gemm_dgelu_quantize_colsum(a, hi, lo, a_inv, ih, il, dg, transpose=True,
+                                            col_sum=col_sum, return_grad=True)
+    dh = K._dual_gemm(a, hi, lo, a_inv, ih, il, None, torch.float32)
+    hr = h.clone().requires_grad_(True)
+    F.gelu(hr).backward(dh)
+    g_ref = hr.grad
+    # the gradient is torch's GELU backward of the dgrad output
+    assert torch.equal(bits(res[-1]), bits(g_ref))
+    q2, inv2, q2_t, cs2 = K.quantize_per_tensor_colsum(g_ref, torch.float8_e5m2, transpose=True)
+    q, inv, q_t = res[:3]
+    assert torch.equal(bits(q), bits(q2)) and torch.equal(bits(q_t), bits(q2_t))
+    assert same_scalar(inv, inv2)
+    if col_sum:
+        assert torch.equal(bits(res[3]), bits(cs2))
+        # the fixed summation order, restated on the CPU
+        assert np.array_equal(res[3].cpu().numpy(), oq.column_sums(g_ref.cpu().numpy()))
+
+
+def test_gemm_epilogue_replaces_the_gelu_passes_at_c4(dev):
+    """At the C4 layer shapes the GELU's amax comes from the persistent
+    GEMM's epilogue, and its backward, amax and bias partials from the dgrad
+    GEMM's: no separate GELU or amax pass over h or its gradient runs."""
+    a, hi, lo, a_inv, ih, il = _fp8_layer(dev, 8192, 1024, 4096, seed=1)
+    fwd = lambda: K.dual_gemm_gelu_quantize(a, hi, lo, a_inv, ih, il, transpose=True,  # noqa: E731
+                                            return_dgelu=True)
+    fwd()
+    torch.cuda.synchronize()  # the premise check has run
+    names = _kernel_names(fwd)
+    assert any("gemm_nt_persist_kernel<0, 0, float, 1>" in n for n in names), names
+    assert not any("gelu_amax_kernel" in n or "amax_part_kernel" in n for n in names), names
+    g8, hi2, lo2, g_inv, ih2, il2 = _fp8_layer(dev, 8192, 1024, 4096, seed=2,
+                                               a_dtype=torch.float8_e5m2)
+    dg = torch.rand(8192, 4096, device=dev)
+    names = _kernel_names(lambda: K.dual_gemm_dgelu_quantize_colsum(
+        g8, hi2, lo2, g_inv, ih2, il2, dg, transpose=True))
+    assert any("gemm_nt_persist_kernel<1, 0, float, 2>" in n for n in names), names
+    assert not any("amax" in n for n in names), names
 
 
 def _pair(dev, d_in, d_h, d_out, bias=True, seed=0, **kw):

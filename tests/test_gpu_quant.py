@@ -356,6 +356,8 @@ def test_quantize_colsum_codes_and_sums(dev, shape, dtype):
     assert inv.item() == float(inv_o)
     ref = x.double().sum(0).numpy()
     np.testing.assert_allclose(cs.cpu().numpy(), ref, rtol=1e-5, atol=1e-6 * float(np.abs(x.float().numpy()).sum(0).max()))
+    # bit for bit in the fixed order (restated in oracle.quant.column_sums)
+    assert np.array_equal(cs.cpu().numpy(), oq.column_sums(x.float().numpy()))
 
 
 # ---------------------------------------- delayed scaling (PDDS) dual quant

@@ -619,3 +619,50 @@ def test_torch_ref_block_step_matches_numpy_oracle():
     A = og.block_deq64(aq, ae, 64)
     dw = gout.reshape(-1, 64).double().numpy().T @ A
     assert og.rel_fro(Wr.grad.numpy(), dw) < 1e-6
+
+
+# ------------------------------------------------------------ column sums
+def _big_and_ones(rows, cols, ones):
+    """2^24 at row 0 of every column; column i has +1 at the rows ones[i]."""
+    x = np.zeros((rows, cols), np.float32)
+    x[0] = 2.0**24
+    for c, rs in enumerate(ones):
+        x[list(rs), c] = 1.0
+    return x
+
+
+def test_column_sums_within_group_tree():
+    """Adding +1 to 2^24 is lost, +2 is kept: which ones survive tells the
+    order.  Halving folds pair rows l, l + 32 first, then l, l + 16, ...:
+    ones at rows 1 and 33 meet each other first (kept, +2) while ones at 32
+    and 48 each meet the 2^24 chain alone (lost).  Row-sequential and
+    adjacent-pair orders give the opposite answers."""
+    x = _big_and_ones(64, 5, [(32, 48), (1, 33), range(1, 64), (2, 3), (16, 48)])
+    got = oq.column_sums(x).astype(np.float64) - 2.0**24
+    # (2, 3): fold 1 is the last, both lost; (16, 48): paired at fold 32 (+2)
+    assert got.tolist() == [0.0, 2.0, 62.0, 0.0, 2.0]
+
+
+def test_column_sums_finalising_order():
+    """Group sums: 2^24 in group 0, ones in groups (16, 24) meet in lane 0's
+    second pair (kept), ones in groups (8, 16) meet 2^24 in the first pair
+    and ones in groups (1, 9) sit in lane 1, added to lane 0's total last."""
+    g = 40
+    x = np.zeros((64 * g, 3), np.float32)
+    x[0] = 2.0**24
+    for c, gs in enumerate([(16, 24), (8, 16), (1, 9)]):
+        for q in gs:
+            x[64 * q, c] = 1.0
+    got = oq.column_sums(x).astype(np.float64) - 2.0**24
+    assert got.tolist() == [2.0, 0.0, 2.0]
+
+
+@pytest.mark.parametrize("shape", [(1, 8), (63, 16), (64, 8), (65, 24), (1000, 24), (4096, 8)])
+def test_column_sums_close_to_exact_and_exact_on_integers(shape):
+    rng = np.random.default_rng(shape[0])
+    x = rng.standard_normal(shape).astype(np.float32)
+    ref = x.astype(np.float64).sum(0)
+    bound = np.abs(x).astype(np.float64).sum(0) * 2.0**-24 * (np.log2(shape[0]) + 10)
+    assert np.all(np.abs(oq.column_sums(x) - ref) <= bound)
+    xi = rng.integers(-1000, 1000, shape).astype(np.float32)  # every partial exact
+    assert np.array_equal(oq.column_sums(xi), xi.astype(np.float64).sum(0).astype(np.float32))
