@@ -496,13 +496,16 @@ int tcfp_block_wgrad(const float* g, int64_t m, int64_t n_out, const uint8_t* x,
  *   g_split_t [n, 2m] bf16: [bf16(g) | bf16(g - bf16(g))] transposed -- the
  *             wgrad's split fp32 gradient;
  *   bias_grad [n] fp32: column sums of g (grad.sum(0)), summed per 64-row
- *             tile and then over tiles in order.
+ *             tile and then over tiles in order;
+ *   g_fp8 [m, n] E5M2 codes with g_exps [n / block, m] int8: the same block
+ *             quantisation as codes (block_quantize_fp8(g, block, e5m2)) --
+ *             the FP8 block dgrad's G operand (both or neither).
  * Any output may be NULL.  n % block == 0; bias_grad needs a workspace of
  * tcfp_block_grad_prep_workspace_bytes(m, n) bytes. */
 size_t tcfp_block_grad_prep_workspace_bytes(int64_t m, int64_t n);
 int tcfp_block_grad_prep(const float* g, int64_t m, int64_t n, int block, uint16_t* g_deq,
-                         uint16_t* g_split_t, float* bias_grad, void* workspace,
-                         size_t workspace_bytes, void* stream);
+                         uint16_t* g_split_t, float* bias_grad, uint8_t* g_fp8, int8_t* g_exps,
+                         void* workspace, size_t workspace_bytes, void* stream);
 
 /* tcfp_block_dual_gemm_dx with the gradient already dequantised to bf16
  * (g_deq from tcfp_block_grad_prep): same result bit for bit.  Workspace:

@@ -108,7 +108,7 @@ _SIGNATURES = {
                          _c_void_p, ctypes.c_size_t, _c_void_p],
     "tcfp_block_wgrad_workspace_bytes": [_i64, _i64, _i64],
     "tcfp_block_grad_prep": [_c_void_p, _i64, _i64, _i32, _c_void_p, _c_void_p, _c_void_p,
-                             _c_void_p, ctypes.c_size_t, _c_void_p],
+                             _c_void_p, _c_void_p, _c_void_p, ctypes.c_size_t, _c_void_p],
     "tcfp_block_grad_prep_workspace_bytes": [_i64, _i64],
     "tcfp_block_dual_gemm_dx_bf16": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64,
                                      _i64, _i64, _i32, _c_void_p, _c_void_p, ctypes.c_size_t,

@@ -204,6 +204,11 @@ struct GemmArgs {
   // its partial output at out + y*split_stride (fp32, no bias)
   int kc;
   int64_t split_stride;
+  // (gemm_nt_dma_kernel) kwrap_b > 0: the B operand rows hold kwrap_b bytes
+  // of contraction and byte k >= kwrap_b reads byte k - kwrap_b (K <= 2
+  // kwrap_b, kwrap_b % 128 == 0): one copy serves a contraction that runs
+  // over the same B columns twice
+  int kwrap_b;
   // GELU epilogues of the persistent fp32 kernel (same leading dimension
   // ldo as out; EPI 2 ignores bias).  EPI 1 writes out (= h) as EPI 0 and the GELU amax rule's
   // keys of h (common.h) to part[2 * blockIdx.x], part[2 * blockIdx.x + 1].
@@ -288,13 +293,16 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && NS == 2 && BM == 128 ? 2 : 1))
   if (srow0 < BM) {
     src = g.A + koff + int64_t(m0) * g.lda; ld = g.lda; rows_left = min(M - m0, BM); row_base = srow0;
   } else if (srow0 < BM + BN) {
-    src = g.B0 + koff + int64_t(n0) * g.ldb; ld = g.ldb; rows_left = min(N - n0, BN);
-    row_base = srow0 - BM;
+    src = g.B0 + (g.kwrap_b ? 0 : koff) + int64_t(n0) * g.ldb; ld = g.ldb;
+    rows_left = min(N - n0, BN); row_base = srow0 - BM;
   } else {
-    src = g.B1 + koff + int64_t(n1) * g.ldb; ld = g.ldb; rows_left = min(N - n1, BN);
-    row_base = srow0 - BM - BN;
+    src = g.B1 + (g.kwrap_b ? 0 : koff) + int64_t(n1) * g.ldb; ld = g.ldb;
+    rows_left = min(N - n1, BN); row_base = srow0 - BM - BN;
   }
-  const uint32_t nrec = rows_left > 0 ? uint32_t(int64_t(rows_left - 1) * ld + K) : 0u;
+  // a wrapping B region addresses contraction bytes koff + t * kSK modulo kwrap_b
+  const uint32_t kwrap = srow0 >= BM ? uint32_t(g.kwrap_b) : 0u;
+  const uint32_t nrec =
+      rows_left > 0 ? uint32_t(int64_t(rows_left - 1) * ld + (kwrap ? int(kwrap) : K)) : 0u;
   const v4i rsrc = make_rsrc(src, nrec);
   // Instruction i fills stage rows srow0 + i*8 .. +8 (1 KiB); lane writes row
   // +lane/8 at physical chunk lane%8.  srow0 is a multiple of 16, so the
@@ -341,7 +349,11 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && NS == 2 && BM == 128 ? 2 : 1))
   auto issue = [&](int t) {
     const uint32_t dst = lds_base + uint32_t(t & (NS - 1)) * STAGE;
     const bool live = t < nt;
-    const uint32_t soff = uint32_t(live ? t : 0) * kSK;
+    uint32_t soff = uint32_t(live ? t : 0) * kSK;
+    if (kwrap) {
+      soff += uint32_t(koff);
+      if (soff >= kwrap) soff -= kwrap;
+    }
     const bool last = t == nt - 1;
 #pragma unroll
     for (int i = 0; i < DI; ++i) {
@@ -1529,12 +1541,13 @@ __global__ __launch_bounds__(256) void dequant_rows_bf16_kernel(
   }
 }
 
-// out[c, r] = bf16(q[r, c] * 2^e[c / bs, r]) through a 64 x 64 LDS tile.
+// out[c, r] = bf16(q[r * ldq + c] * 2^e[c / bs, r]) through a 64 x 64 LDS
+// tile (c < cols: a column range of a wider q when ldq > cols).
 template <int FMT>
 __global__ __launch_bounds__(256) void dequant_t_bf16_kernel(
     const uint8_t* __restrict__ q0, const int8_t* __restrict__ e0, uint16_t* __restrict__ out0,
     const uint8_t* __restrict__ q1, const int8_t* __restrict__ e1, uint16_t* __restrict__ out1,
-    int64_t rows, int64_t cols, int bs_shift) {
+    int64_t rows, int64_t cols, int bs_shift, int64_t ldq) {
   // blockIdx.y 0: matrix 0 (W_hi); 1: matrix 1 (W_lo, whose -128 exponent
   // marks a zero block)
   const bool second = blockIdx.y == 1;
@@ -1556,7 +1569,7 @@ __global__ __launch_bounds__(256) void dequant_t_bf16_kernel(
       if (r < rows && c < cols) {
         const int ex = e[(c >> bs_shift) * rows + r];
         const float sc = (zero_sentinel && ex == -128) ? 0.0f : exp2i(ex);
-        v = f32_to_bf16_rne(fp8_to_f32<FMT>(q[r * cols + c]) * sc);
+        v = f32_to_bf16_rne(fp8_to_f32<FMT>(q[r * ldq + c]) * sc);
       }
       tile[lc + j][lr] = v;
     }
@@ -1638,11 +1651,12 @@ __global__ __launch_bounds__(256) void split_t_bf16_kernel(const float* __restri
   }
 }
 
-// B'[c, r] = B'[c, M + r] = bf16(q[r, c] * 2^e[c / bs, r]) (exact).
+// B'[c, r] = bf16(q[r * ldq + c] * 2^e[c / bs, r]) (exact), and with dup
+// also B'[c, M + r] (rows of 2M); c < cols.
 template <int FMT>
 __global__ __launch_bounds__(256) void dequant_t_dup_bf16_kernel(
     const uint8_t* __restrict__ q, const int8_t* __restrict__ e, int64_t rows, int64_t cols,
-    int bs_shift, uint16_t* __restrict__ out) {
+    int bs_shift, uint16_t* __restrict__ out, int64_t ldq, bool dup) {
   __shared__ uint16_t tile[64][64 + 2];
   const int tiles_c = int((cols + 63) / 64);
   const int64_t r0 = int64_t(blockIdx.x / tiles_c) * 64, c0 = int64_t(blockIdx.x % tiles_c) * 64;
@@ -1655,7 +1669,7 @@ __global__ __launch_bounds__(256) void dequant_t_dup_bf16_kernel(
       const int64_t c = c0 + lc + j;
       uint16_t v = 0;
       if (r < rows && c < cols)
-        v = f32_to_bf16_rne(fp8_to_f32<FMT>(q[r * cols + c]) * exp2i(e[(c >> bs_shift) * rows + r]));
+        v = f32_to_bf16_rne(fp8_to_f32<FMT>(q[r * ldq + c]) * exp2i(e[(c >> bs_shift) * rows + r]));
       tile[lc + j][lr] = v;
     }
   }
@@ -1663,7 +1677,7 @@ __global__ __launch_bounds__(256) void dequant_t_dup_bf16_kernel(
   const int lc = t >> 2, lr = (t & 3) * 16;
   const int64_t c = c0 + lc;
   if (c >= cols) return;
-  uint16_t* o0 = out + c * (2 * rows) + r0 + lr;
+  uint16_t* o0 = out + c * (dup ? 2 * rows : rows) + r0 + lr;
   uint16_t* o1 = o0 + rows;
   if ((rows % 8) == 0 && r0 + lr + 16 <= rows) {
     uint32_t w[8];
@@ -1672,11 +1686,16 @@ __global__ __launch_bounds__(256) void dequant_t_dup_bf16_kernel(
       w[j] = uint32_t(tile[lc][lr + 2 * j]) | (uint32_t(tile[lc][lr + 2 * j + 1]) << 16);
     reinterpret_cast<uint4*>(o0)[0] = make_uint4(w[0], w[1], w[2], w[3]);
     reinterpret_cast<uint4*>(o0)[1] = make_uint4(w[4], w[5], w[6], w[7]);
-    reinterpret_cast<uint4*>(o1)[0] = make_uint4(w[0], w[1], w[2], w[3]);
-    reinterpret_cast<uint4*>(o1)[1] = make_uint4(w[4], w[5], w[6], w[7]);
+    if (dup) {
+      reinterpret_cast<uint4*>(o1)[0] = make_uint4(w[0], w[1], w[2], w[3]);
+      reinterpret_cast<uint4*>(o1)[1] = make_uint4(w[4], w[5], w[6], w[7]);
+    }
   } else {
     for (int j = 0; j < 16; ++j)
-      if (r0 + lr + j < rows) { o0[j] = tile[lc][lr + j]; o1[j] = tile[lc][lr + j]; }
+      if (r0 + lr + j < rows) {
+        o0[j] = tile[lc][lr + j];
+        if (dup) o1[j] = tile[lc][lr + j];
+      }
   }
 }
 
@@ -1684,32 +1703,60 @@ __global__ __launch_bounds__(256) void dequant_t_dup_bf16_kernel(
 
 namespace {
 
-// W_hi^T, W_lo^T dequantised into bf16 (one launch), then the bf16 dual GEMM
-// A = G [m, d_out] x B = W^T [d_in, d_out] (K counts bytes), fp32 out.
+// Dequantised bf16 operand copies of the block backward are made in column
+// chunks whose copies stay within this many bytes (the GEMMs run per chunk
+// into a column range of the output), so the workspace does not grow with
+// the layer; a chunk keeps at least 256 columns.
+constexpr int64_t kOperandChunkBytes = int64_t(64) << 20;
+
+int64_t chunk_cols(int64_t bytes_per_col, int64_t cols) {
+  int64_t c = kOperandChunkBytes / std::max<int64_t>(bytes_per_col, 1) / 256 * 256;
+  c = std::max<int64_t>(c, 256);
+  return std::min(c, cols);
+}
+
+// dx columns per dgrad chunk: W_hi^T and W_lo^T rows of d_out bf16 each
+int64_t dgrad_chunk(int64_t d_out, int64_t d_in) { return chunk_cols(4 * d_out, d_in); }
+
+// Per chunk of dx columns [c0, c0 + n): W_hi^T, W_lo^T rows c0.. dequantised
+// into bf16 (one launch), then the bf16 dual GEMM A = G [m, d_out] x
+// B = W^T [n, d_out] (K counts bytes) into dx[:, c0 ..] (fp32, ld d_in).
 int dgrad_bf16(const uint16_t* gd, const uint8_t* w_hi, const uint8_t* w_lo, const int8_t* e_hi,
                const int8_t* e_lo, int64_t m, int64_t d_out, int64_t d_in, int shift, float* dx,
                uint16_t* wth, uint16_t* wtl, hipStream_t st) {
-  const int64_t tiles = ((d_out + 63) / 64) * ((d_in + 63) / 64);
-  if (!grid_x_fits(tiles, 256)) return TCFP_ERR_SHAPE;
-  dequant_t_bf16_kernel<TCFP_FP8_E4M3><<<dim3(unsigned(tiles), w_lo ? 2u : 1u), 256, 0, st>>>(
-      w_hi, e_hi, wth, w_lo, e_lo, wtl, d_out, d_in, shift);
-  if (hipGetLastError() != hipSuccess) return TCFP_ERR_HIP;
-  GemmArgs ga{};
-  ga.A = reinterpret_cast<const uint8_t*>(gd);
-  ga.B0 = reinterpret_cast<const uint8_t*>(wth);
-  ga.B1 = reinterpret_cast<const uint8_t*>(w_lo ? wtl : wth);
-  ga.M = int(m); ga.N = int(d_in); ga.K = int(2 * d_out);
-  ga.lda = 2 * d_out; ga.ldb = 2 * d_out;
-  ga.out = dx; ga.ldo = d_in;
-  if (w_lo) return launch_gemm<kBF16, kBF16, false, float, 0>(ga, st);
-  return launch_gemm<kBF16, kBF16, true, float, 0>(ga, st);
+  const int64_t cw = dgrad_chunk(d_out, d_in);
+  for (int64_t c0 = 0; c0 < d_in; c0 += cw) {
+    const int64_t n = std::min(cw, d_in - c0);
+    const int64_t tiles = ((d_out + 63) / 64) * ((n + 63) / 64);
+    if (!grid_x_fits(tiles, 256)) return TCFP_ERR_SHAPE;
+    const int64_t eo = (c0 >> shift) * d_out;  // c0 is a multiple of the block
+    dequant_t_bf16_kernel<TCFP_FP8_E4M3><<<dim3(unsigned(tiles), w_lo ? 2u : 1u), 256, 0, st>>>(
+        w_hi + c0, e_hi + eo, wth, w_lo ? w_lo + c0 : nullptr, w_lo ? e_lo + eo : nullptr, wtl,
+        d_out, n, shift, d_in);
+    if (hipGetLastError() != hipSuccess) return TCFP_ERR_HIP;
+    GemmArgs ga{};
+    ga.A = reinterpret_cast<const uint8_t*>(gd);
+    ga.B0 = reinterpret_cast<const uint8_t*>(wth);
+    ga.B1 = reinterpret_cast<const uint8_t*>(w_lo ? wtl : wth);
+    ga.M = int(m); ga.N = int(n); ga.K = int(2 * d_out);
+    ga.lda = 2 * d_out; ga.ldb = 2 * d_out;
+    ga.out = dx + c0; ga.ldo = d_in;
+    const int rc = w_lo ? launch_gemm<kBF16, kBF16, false, float, 0>(ga, st)
+                        : launch_gemm<kBF16, kBF16, true, float, 0>(ga, st);
+    if (rc != TCFP_OK) return rc;
+  }
+  return TCFP_OK;
+}
+
+size_t dgrad_copy_bytes(int64_t d_out, int64_t d_in) {
+  return align256(size_t(dgrad_chunk(d_out, d_in)) * size_t(d_out) * 2);
 }
 
 }  // namespace
 
 extern "C" size_t tcfp_block_dual_gemm_dx_workspace_bytes(int64_t m, int64_t d_out, int64_t d_in) {
   if (m < 0 || d_out < 0 || d_in < 0) return 0;
-  return align256(size_t(m) * size_t(d_out) * 2) + 2 * align256(size_t(d_in) * size_t(d_out) * 2);
+  return align256(size_t(m) * size_t(d_out) * 2) + 2 * dgrad_copy_bytes(d_out, d_in);
 }
 
 extern "C" int tcfp_block_dual_gemm_dx(const uint8_t* g, int g_fmt, const int8_t* e_g,
@@ -1734,7 +1781,7 @@ extern "C" int tcfp_block_dual_gemm_dx(const uint8_t* g, int g_fmt, const int8_t
   uint16_t* gd = reinterpret_cast<uint16_t*>(ws);
   uint16_t* wth = reinterpret_cast<uint16_t*>(ws + align256(size_t(m) * size_t(d_out) * 2));
   uint16_t* wtl = reinterpret_cast<uint16_t*>(reinterpret_cast<uint8_t*>(wth) +
-                                              align256(size_t(d_in) * size_t(d_out) * 2));
+                                              dgrad_copy_bytes(d_out, d_in));
   // dequantised operands
   {
     const int64_t nvec = m * d_out / 8;
@@ -1751,7 +1798,7 @@ extern "C" int tcfp_block_dual_gemm_dx(const uint8_t* g, int g_fmt, const int8_t
 
 extern "C" size_t tcfp_block_dual_gemm_dx_bf16_workspace_bytes(int64_t d_out, int64_t d_in) {
   if (d_out < 0 || d_in < 0) return 0;
-  return 2 * align256(size_t(d_in) * size_t(d_out) * 2);
+  return 2 * dgrad_copy_bytes(d_out, d_in);
 }
 
 extern "C" int tcfp_block_dual_gemm_dx_bf16(const uint16_t* g_deq, const uint8_t* w_hi,
@@ -1772,7 +1819,7 @@ extern "C" int tcfp_block_dual_gemm_dx_bf16(const uint16_t* g_deq, const uint8_t
   const int shift = block == 32 ? 5 : (block == 64 ? 6 : 7);
   uint8_t* ws = static_cast<uint8_t*>(workspace);
   uint16_t* wth = reinterpret_cast<uint16_t*>(ws);
-  uint16_t* wtl = reinterpret_cast<uint16_t*>(ws + align256(size_t(d_in) * size_t(d_out) * 2));
+  uint16_t* wtl = reinterpret_cast<uint16_t*>(ws + dgrad_copy_bytes(d_out, d_in));
   return dgrad_bf16(g_deq, w_hi, w_lo, e_hi, e_lo, m, d_out, d_in, shift, dx, wth, wtl,
                     static_cast<hipStream_t>(stream));
 }
@@ -1781,9 +1828,12 @@ namespace {
 
 // dw[i] = sum_s part[s * stride + i], summed in split order (deterministic);
 // four fp32 per thread (n4 = elements / 4; stride % 4 == 0).
+// The partials are [rows, cols] row-major per split (cols % 4 == 0); out
+// has row stride ldo.
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ part,
                                                             int splits, int64_t n4,
-                                                            int64_t stride,
+                                                            int64_t stride, int64_t cols,
+                                                            int64_t ldo,
                                                             float* __restrict__ out) {
   const int64_t step = int64_t(gridDim.x) * 256;
   for (int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x; i < n4; i += step) {
@@ -1792,7 +1842,8 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
       const float4 b = reinterpret_cast<const float4*>(part + sp * stride)[i];
       a.x += b.x; a.y += b.y; a.z += b.z; a.w += b.w;
     }
-    reinterpret_cast<float4*>(out)[i] = a;
+    const int64_t e = 4 * i, r = e / cols, c = e - r * cols;
+    *reinterpret_cast<float4*>(out + r * ldo + c) = a;
   }
 }
 
@@ -1814,30 +1865,88 @@ int64_t wgrad_splits(int64_t m, int64_t n_out, int64_t k_in, int64_t* kc) {
 }
 
 // The wgrad GEMM over the concatenated contraction: A' = [g_hi | g_lo]^T
-// [n_out, 2m], B' = [x | x]^T [k_in, 2m] (bf16), dw [n_out, k_in] fp32;
+// [n_out, 2m], B' = [x | x]^T [k_in, 2m] (bf16; with `wrap` one copy
+// x^T [k_in, m] read twice), dw [n_out, k_in] fp32 with row stride ldo;
 // split-K partials go to `part` when the output is small.
 int wgrad_gemm(const uint16_t* ap, const uint16_t* bp, int64_t m, int64_t n_out, int64_t k_in,
-               float* dw, float* part, hipStream_t st) {
+               float* dw, int64_t ldo, float* part, bool wrap, hipStream_t st) {
   GemmArgs ga{};
   ga.A = reinterpret_cast<const uint8_t*>(ap);
   ga.B0 = reinterpret_cast<const uint8_t*>(bp);
   ga.B1 = ga.B0;
   ga.M = int(n_out); ga.N = int(k_in); ga.K = int(4 * m);  // bytes of 2M bf16
-  ga.lda = 4 * m; ga.ldb = 4 * m;
-  ga.out = dw; ga.ldo = k_in;
+  ga.lda = 4 * m; ga.ldb = wrap ? 2 * m : 4 * m;
+  ga.kwrap_b = wrap ? int(2 * m) : 0;
+  ga.out = dw; ga.ldo = ldo;
   int64_t kc;
   const int64_t splits = wgrad_splits(m, n_out, k_in, &kc);
   if (splits <= 1) return launch_gemm<kBF16, kBF16, true, float, 0>(ga, st);
-  // partial products of each K chunk, then their sum in split order
+  // partial products of each K chunk ([n_out, k_in] each), then their sum
+  // in split order
   ga.out = part;
+  ga.ldo = k_in;
   ga.kc = int(kc);
   ga.split_stride = n_out * k_in;
   const int rc = launch_gemm<kBF16, kBF16, true, float, 0>(ga, st);
   if (rc != TCFP_OK) return rc;
   const int64_t n4 = n_out * k_in / 4;
   const int blocks = int(std::min<int64_t>((n4 + 255) / 256, int64_t(num_cus()) * 8));
-  splitk_reduce_kernel<<<blocks, 256, 0, st>>>(part, int(splits), n4, n_out * k_in, dw);
+  splitk_reduce_kernel<<<blocks, 256, 0, st>>>(part, int(splits), n4, n_out * k_in, k_in, ldo,
+                                               dw);
   return hipGetLastError() == hipSuccess ? TCFP_OK : TCFP_ERR_HIP;
+}
+
+// One copy of x^T serves both halves of the contraction when its rows (m
+// bf16 = 2m bytes) are whole 128-byte stages.
+bool wgrad_wrap(int64_t m) { return m > 0 && (2 * m) % kSK == 0; }
+// dw columns per wgrad chunk: x^T rows of m bf16 (2m without the wrap)
+int64_t wgrad_chunk(int64_t m, int64_t k_in) {
+  return chunk_cols((wgrad_wrap(m) ? 2 : 4) * std::max<int64_t>(m, 1), k_in);
+}
+size_t wgrad_part_bytes(int64_t m, int64_t n_out, int64_t cols) {
+  int64_t kc;
+  const int64_t splits = wgrad_splits(m, n_out, cols, &kc);
+  return splits > 1 ? align256(size_t(splits) * size_t(n_out) * size_t(cols) * 4) : 0;
+}
+// Workspace of the chunked wgrad: one chunk's x^T copy, then the partials.
+size_t wgrad_copy_bytes(int64_t m, int64_t k_in) {
+  return align256(size_t(wgrad_chunk(m, k_in)) * size_t(wgrad_wrap(m) ? m : 2 * m) * 2);
+}
+size_t wgrad_ws_bytes(int64_t m, int64_t n_out, int64_t k_in) {
+  const int64_t kw = wgrad_chunk(m, k_in);
+  const int64_t rem = kw > 0 ? k_in % kw : 0;
+  return wgrad_copy_bytes(m, k_in) +
+         std::max(wgrad_part_bytes(m, n_out, kw), rem ? wgrad_part_bytes(m, n_out, rem) : 0);
+}
+
+// dw = A'^T-product of the split gradient ap ([n_out, 2m] bf16) with the
+// dequantised activation, per chunk of dw columns: x^T rows c0.. dequantised
+// into the workspace, then the GEMM into dw[:, c0 ..].
+int wgrad_chunked(const uint16_t* ap, int64_t m, int64_t n_out, const uint8_t* x, int x_fmt,
+                  const int8_t* e_x, int64_t k_in, int shift, float* dw, uint8_t* ws,
+                  hipStream_t st) {
+  const bool wrap = wgrad_wrap(m);
+  const int64_t kw = wgrad_chunk(m, k_in);
+  uint16_t* bp = reinterpret_cast<uint16_t*>(ws);
+  float* part = reinterpret_cast<float*>(ws + wgrad_copy_bytes(m, k_in));
+  for (int64_t c0 = 0; c0 < k_in; c0 += kw) {
+    const int64_t n = std::min(kw, k_in - c0);
+    if (m > 0) {
+      const int64_t tx = ((m + 63) / 64) * ((n + 63) / 64);
+      if (!grid_x_fits(tx, 256)) return TCFP_ERR_SHAPE;
+      const int64_t eo = (c0 >> shift) * m;  // c0 is a multiple of the block
+      if (x_fmt == TCFP_FP8_E5M2)
+        dequant_t_dup_bf16_kernel<TCFP_FP8_E5M2><<<unsigned(tx), 256, 0, st>>>(
+            x + c0, e_x + eo, m, n, shift, bp, k_in, !wrap);
+      else
+        dequant_t_dup_bf16_kernel<TCFP_FP8_E4M3><<<unsigned(tx), 256, 0, st>>>(
+            x + c0, e_x + eo, m, n, shift, bp, k_in, !wrap);
+      if (hipGetLastError() != hipSuccess) return TCFP_ERR_HIP;
+    }
+    const int rc = wgrad_gemm(ap, bp, m, n_out, n, dw + c0, k_in, part, wrap, st);
+    if (rc != TCFP_OK) return rc;
+  }
+  return TCFP_OK;
 }
 
 // ---- fused gradient preparation for the block backward ---------------------
@@ -1855,7 +1964,9 @@ template <int BS>
 __global__ __launch_bounds__(256) void grad_prep_kernel(const float* __restrict__ g, int64_t m,
                                                         int64_t n, uint16_t* __restrict__ gd,
                                                         uint16_t* __restrict__ gs,
-                                                        float* __restrict__ cpart) {
+                                                        float* __restrict__ cpart,
+                                                        uint8_t* __restrict__ gq,
+                                                        int8_t* __restrict__ ge) {
   __shared__ float tile[128][64 + 1];  // [column][row]
   const int tiles_c = int((n + 127) / 128);
   const int64_t tr = blockIdx.x / tiles_c;
@@ -1876,7 +1987,7 @@ __global__ __launch_bounds__(256) void grad_prep_kernel(const float* __restrict_
 #pragma unroll
     for (int j = 0; j < 32; ++j) v[j] = 0.0f;
   }
-  if (gd) {
+  if (gd || gq) {
     // block amax: a 32-wide segment per lane; 64 / 128-wide blocks span
     // the 2 / 4 lanes of the same row
     uint32_t a = 0;
@@ -1886,7 +1997,7 @@ __global__ __launch_bounds__(256) void grad_prep_kernel(const float* __restrict_
     if constexpr (BS >= 128) { const uint32_t o = __shfl_xor(a, 2, 64); a = a > o ? a : o; }
     const int e = block_exponent(__uint_as_float(a), kE5M2Max);
     const float mul = exp2i(-e), sc = exp2i(e);
-    uint32_t w[16];
+    uint32_t w[16], cw[8];
 #pragma unroll
     for (int j = 0; j < 32; j += 4) {
       float c4[4];
@@ -1896,6 +2007,7 @@ __global__ __launch_bounds__(256) void grad_prep_kernel(const float* __restrict_
         c4[q] = x > kE5M2Max ? kE5M2Max : (x < -kE5M2Max ? -kE5M2Max : x);
       }
       const uint32_t codes = cvt4_fp8<TCFP_FP8_E5M2>(c4[0], c4[1], c4[2], c4[3]);
+      cw[j / 4] = codes;
       uint16_t b[4];
 #pragma unroll
       for (int q = 0; q < 4; ++q)
@@ -1903,10 +2015,18 @@ __global__ __launch_bounds__(256) void grad_prep_kernel(const float* __restrict_
       w[j / 2] = uint32_t(b[0]) | (uint32_t(b[1]) << 16);
       w[j / 2 + 1] = uint32_t(b[2]) | (uint32_t(b[3]) << 16);
     }
-    if (in) {
+    if (in && gd) {
       uint4* o = reinterpret_cast<uint4*>(gd + r * n + cb);
 #pragma unroll
       for (int q = 0; q < 4; ++q) o[q] = make_uint4(w[4 * q], w[4 * q + 1], w[4 * q + 2], w[4 * q + 3]);
+    }
+    if (in && gq) {
+      // the E5M2 codes [m, n] and the block exponents [n / BS, m] (the lane
+      // at the block's first segment writes it)
+      uint4* o = reinterpret_cast<uint4*>(gq + r * n + cb);
+      o[0] = make_uint4(cw[0], cw[1], cw[2], cw[3]);
+      o[1] = make_uint4(cw[4], cw[5], cw[6], cw[7]);
+      if ((cb & (BS - 1)) == 0) ge[(cb / BS) * m + r] = int8_t(e);
     }
   }
   if (!gs && !cpart) return;
@@ -1972,15 +2092,17 @@ extern "C" size_t tcfp_block_grad_prep_workspace_bytes(int64_t m, int64_t n) {
 
 extern "C" int tcfp_block_grad_prep(const float* g, int64_t m, int64_t n, int block,
                                     uint16_t* g_deq, uint16_t* g_split_t, float* bias_grad,
-                                    void* workspace, size_t workspace_bytes, void* stream) {
+                                    uint8_t* g_fp8, int8_t* g_exps, void* workspace,
+                                    size_t workspace_bytes, void* stream) {
   if (m < 0 || n < 0 || m > INT32_MAX || n > INT32_MAX) return TCFP_ERR_SHAPE;
   if (block != 32 && block != 64 && block != 128) return TCFP_ERR_SHAPE;
   if (n % block != 0) return TCFP_ERR_SHAPE;
   if (!g) return TCFP_ERR_SHAPE;
   if (bias_grad && (!workspace || workspace_bytes < tcfp_block_grad_prep_workspace_bytes(m, n)))
     return TCFP_ERR_WORKSPACE;
+  if ((g_fp8 == nullptr) != (g_exps == nullptr)) return TCFP_ERR_SHAPE;
   if (!al16(g) || (g_deq && !al16(g_deq)) || (g_split_t && !al16(g_split_t)) ||
-      (workspace && !al16(workspace)))
+      (g_fp8 && !al16(g_fp8)) || (workspace && !al16(workspace)))
     return TCFP_ERR_ALIGN;
   if (n == 0) return TCFP_OK;
   hipStream_t st = static_cast<hipStream_t>(stream);
@@ -1995,9 +2117,12 @@ extern "C" int tcfp_block_grad_prep(const float* g, int64_t m, int64_t n, int bl
   if (!grid_x_fits(tr * tc, 256)) return TCFP_ERR_SHAPE;
   float* part = bias_grad ? static_cast<float*>(workspace) : nullptr;
   const unsigned grid = unsigned(tr * tc);
-  if (block == 32) grad_prep_kernel<32><<<grid, 256, 0, st>>>(g, m, n, g_deq, g_split_t, part);
-  else if (block == 64) grad_prep_kernel<64><<<grid, 256, 0, st>>>(g, m, n, g_deq, g_split_t, part);
-  else grad_prep_kernel<128><<<grid, 256, 0, st>>>(g, m, n, g_deq, g_split_t, part);
+  if (block == 32)
+    grad_prep_kernel<32><<<grid, 256, 0, st>>>(g, m, n, g_deq, g_split_t, part, g_fp8, g_exps);
+  else if (block == 64)
+    grad_prep_kernel<64><<<grid, 256, 0, st>>>(g, m, n, g_deq, g_split_t, part, g_fp8, g_exps);
+  else
+    grad_prep_kernel<128><<<grid, 256, 0, st>>>(g, m, n, g_deq, g_split_t, part, g_fp8, g_exps);
   if (bias_grad)
     colsum_tiles_kernel<<<unsigned((n + 255) / 256), 256, 0, st>>>(part, tr, n, bias_grad);
   return hipGetLastError() == hipSuccess ? TCFP_OK : TCFP_ERR_HIP;
@@ -2005,10 +2130,7 @@ extern "C" int tcfp_block_grad_prep(const float* g, int64_t m, int64_t n, int bl
 
 extern "C" size_t tcfp_block_wgrad_workspace_bytes(int64_t m, int64_t n_out, int64_t k_in) {
   if (m < 0 || n_out < 0 || k_in < 0) return 0;
-  int64_t kc;
-  const int64_t splits = wgrad_splits(m, n_out, k_in, &kc);
-  return align256(size_t(n_out) * size_t(2 * m) * 2) + align256(size_t(k_in) * size_t(2 * m) * 2) +
-         (splits > 1 ? align256(size_t(splits) * size_t(n_out) * size_t(k_in) * 4) : 0);
+  return align256(size_t(n_out) * size_t(2 * m) * 2) + wgrad_ws_bytes(m, n_out, k_in);
 }
 
 extern "C" int tcfp_block_wgrad(const float* g, int64_t m, int64_t n_out, const uint8_t* x,
@@ -2029,32 +2151,20 @@ extern "C" int tcfp_block_wgrad(const float* g, int64_t m, int64_t n_out, const 
   const int shift = block == 32 ? 5 : (block == 64 ? 6 : 7);
   uint8_t* ws = static_cast<uint8_t*>(workspace);
   uint16_t* ap = reinterpret_cast<uint16_t*>(ws);
-  uint16_t* bp = reinterpret_cast<uint16_t*>(ws + align256(size_t(n_out) * size_t(2 * m) * 2));
-  if (m == 0) {
-    // empty contraction: dW = 0, through the GEMM with K = 0 below
-  } else {
+  if (m > 0) {  // (an empty contraction gives dW = 0 through the GEMM with K = 0)
     const int64_t tg = ((m + 63) / 64) * ((n_out + 63) / 64);
-    const int64_t tx = ((m + 63) / 64) * ((k_in + 63) / 64);
-    if (!grid_x_fits(tg, 256) || !grid_x_fits(tx, 256)) return TCFP_ERR_SHAPE;
+    if (!grid_x_fits(tg, 256)) return TCFP_ERR_SHAPE;
     split_t_bf16_kernel<<<unsigned(tg), 256, 0, st>>>(g, m, n_out, ap);
-    if (x_fmt == TCFP_FP8_E5M2)
-      dequant_t_dup_bf16_kernel<TCFP_FP8_E5M2><<<unsigned(tx), 256, 0, st>>>(x, e_x, m, k_in, shift, bp);
-    else
-      dequant_t_dup_bf16_kernel<TCFP_FP8_E4M3><<<unsigned(tx), 256, 0, st>>>(x, e_x, m, k_in, shift, bp);
     if (hipGetLastError() != hipSuccess) return TCFP_ERR_HIP;
   }
-  float* part = reinterpret_cast<float*>(ws + align256(size_t(n_out) * size_t(2 * m) * 2) +
-                                         align256(size_t(k_in) * size_t(2 * m) * 2));
-  return wgrad_gemm(ap, bp, m, n_out, k_in, dw, part, st);
+  return wgrad_chunked(ap, m, n_out, x, x_fmt, e_x, k_in, shift, dw,
+                       ws + align256(size_t(n_out) * size_t(2 * m) * 2), st);
 }
 
 extern "C" size_t tcfp_block_wgrad_presplit_workspace_bytes(int64_t m, int64_t n_out,
                                                            int64_t k_in) {
   if (m < 0 || n_out < 0 || k_in < 0) return 0;
-  int64_t kc;
-  const int64_t splits = wgrad_splits(m, n_out, k_in, &kc);
-  return align256(size_t(k_in) * size_t(2 * m) * 2) +
-         (splits > 1 ? align256(size_t(splits) * size_t(n_out) * size_t(k_in) * 4) : 0);
+  return wgrad_ws_bytes(m, n_out, k_in);
 }
 
 extern "C" int tcfp_block_wgrad_presplit(const uint16_t* g_split_t, int64_t m, int64_t n_out,
@@ -2074,17 +2184,6 @@ extern "C" int tcfp_block_wgrad_presplit(const uint16_t* g_split_t, int64_t m, i
   if (!al16(workspace) || !al16(dw) || !al16(g_split_t)) return TCFP_ERR_ALIGN;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int shift = block == 32 ? 5 : (block == 64 ? 6 : 7);
-  uint8_t* ws = static_cast<uint8_t*>(workspace);
-  uint16_t* bp = reinterpret_cast<uint16_t*>(ws);
-  if (m > 0) {
-    const int64_t tx = ((m + 63) / 64) * ((k_in + 63) / 64);
-    if (!grid_x_fits(tx, 256)) return TCFP_ERR_SHAPE;
-    if (x_fmt == TCFP_FP8_E5M2)
-      dequant_t_dup_bf16_kernel<TCFP_FP8_E5M2><<<unsigned(tx), 256, 0, st>>>(x, e_x, m, k_in, shift, bp);
-    else
-      dequant_t_dup_bf16_kernel<TCFP_FP8_E4M3><<<unsigned(tx), 256, 0, st>>>(x, e_x, m, k_in, shift, bp);
-    if (hipGetLastError() != hipSuccess) return TCFP_ERR_HIP;
-  }
-  float* part = reinterpret_cast<float*>(ws + align256(size_t(k_in) * size_t(2 * m) * 2));
-  return wgrad_gemm(g_split_t, bp, m, n_out, k_in, dw, part, st);
+  return wgrad_chunked(g_split_t, m, n_out, x, x_fmt, e_x, k_in, shift, dw,
+                       static_cast<uint8_t*>(workspace), st);
 }

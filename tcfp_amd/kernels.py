@@ -1248,16 +1248,20 @@ def block_backward_prep(
     dequant: bool = True,
     split: bool = True,
     bias: bool = False,
+    fp8: bool = False,
 ):
     """One pass over the fp32 gradient [M, N] for the block backward.
 
-    Returns ``(g_deq, g_split_t, bias_grad)`` (None where not requested):
-    ``g_deq`` [M, N] bf16 is the gradient block-quantised to E5M2 exactly as
+    Returns ``(g_deq, g_split_t, bias_grad)`` (None where not requested),
+    plus ``(g_fp8, g_exps)`` when ``fp8``: ``g_deq`` [M, N] bf16 is the
+    gradient block-quantised to E5M2 exactly as
     ``block_quantize_fp8(grad, block_size, float8_e5m2)`` and dequantised
-    (the dgrad operand); ``g_split_t`` [N, 2M] bf16 is the transposed
-    hi/lo split the block wgrad uses; ``bias_grad`` [N] fp32 is
-    ``grad.sum(0)`` summed per 64-row tile.  These replace the quantise,
-    dequantise, split and reduce passes the backward would otherwise make.
+    (the exact dgrad's operand); ``g_fp8`` / ``g_exps`` are those codes and
+    exponents themselves (the FP8 dgrad's operand); ``g_split_t`` [N, 2M]
+    bf16 is the transposed hi/lo split the block wgrad uses; ``bias_grad``
+    [N] fp32 is ``grad.sum(0)`` summed per 64-row tile.  These replace the
+    quantise, dequantise, split and reduce passes the backward would
+    otherwise make.
     """
     M, N = grad.shape
     assert N % block_size == 0, f"N ({N}) must be divisible by block_size ({block_size})"
@@ -1266,15 +1270,19 @@ def block_backward_prep(
     g_deq = torch.empty((M, N), dtype=torch.bfloat16, device=dev) if dequant else None
     g_split = torch.empty((N, 2 * M), dtype=torch.bfloat16, device=dev) if split else None
     bias_grad = torch.empty((N,), dtype=torch.float32, device=dev) if bias else None
+    g_fp8 = torch.empty((M, N), dtype=torch.float8_e5m2, device=dev) if fp8 else None
+    g_exps = torch.empty((N // block_size, M), dtype=torch.int8, device=dev) if fp8 else None
     nbytes = int(_hip.lib().tcfp_block_grad_prep_workspace_bytes(M, N)) if bias else 0
     ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev) if bias else None
     check(
         _hip.lib().tcfp_block_grad_prep(
-            ptr(g), M, N, block_size, ptr(g_deq), ptr(g_split), ptr(bias_grad), ptr(ws), nbytes,
-            _hip.stream_of(dev),
+            ptr(g), M, N, block_size, ptr(g_deq), ptr(g_split), ptr(bias_grad), ptr(g_fp8),
+            ptr(g_exps), ptr(ws), nbytes, _hip.stream_of(dev),
         ),
         "block_backward_prep",
     )
+    if fp8:
+        return g_deq, g_split, bias_grad, g_fp8, g_exps
     return g_deq, g_split, bias_grad
 
 
@@ -1340,20 +1348,29 @@ def block_requant_t(w_hi_fp8, w_lo_fp8, w_hi_scales, w_lo_scales, block_size):
     return wt_hi, wt_lo, et_hi, et_lo
 
 
-def fp8_block_dgrad(grad, w_hi_fp8, w_lo_fp8, w_hi_scales, w_lo_scales, block_size):
+def fp8_block_dgrad(grad, w_hi_fp8, w_lo_fp8, w_hi_scales, w_lo_scales, block_size, *,
+                    reblocked=None, grad_fp8=None):
     """Opt-in FP8 block dgrad ``dX ~ grad @ (deq(W_hi) + deq(W_lo))``, fp32
     [M, D_in]: the gradient block-quantised to E5M2 along D_out (the
     reference's ``block_quantize_fp8`` of the gradient, ``nn:700-712``),
     W re-blocked along D_out (:func:`block_requant_t`), then the block dual
     FP8 GEMM.  The reference multiplies the dequantised operands in fp32
     (``fused_block_scaled_dual_gemm_backward_dx``); here W carries one more
-    dual-FP8 rounding (relative ~2^-9 of a block's maximum)."""
-    M, D_out = grad.shape
-    assert D_out == w_hi_fp8.shape[0], (
-        f"Shape mismatch: grad({M},{D_out}), w_hi{tuple(w_hi_fp8.shape)}")
-    g_fp8, g_exps = block_quantize_fp8(grad, block_size, torch.float8_e5m2)
-    wt_hi, wt_lo, et_hi, et_lo = block_requant_t(w_hi_fp8, w_lo_fp8, w_hi_scales, w_lo_scales,
-                                                 block_size)
+    dual-FP8 rounding (relative ~2^-9 of a block's maximum).
+
+    ``reblocked`` (the four outputs of :func:`block_requant_t`, e.g. built
+    once in the forward) and ``grad_fp8`` (codes and exponents, e.g. from
+    :func:`block_backward_prep`) skip those steps; ``grad`` and the
+    original weight operands may then be None."""
+    if grad_fp8 is None:
+        g_fp8, g_exps = block_quantize_fp8(grad, block_size, torch.float8_e5m2)
+    else:
+        g_fp8, g_exps = grad_fp8
+    if reblocked is None:
+        assert g_fp8.shape[1] == w_hi_fp8.shape[0], (
+            f"Shape mismatch: grad{tuple(g_fp8.shape)}, w_hi{tuple(w_hi_fp8.shape)}")
+        reblocked = block_requant_t(w_hi_fp8, w_lo_fp8, w_hi_scales, w_lo_scales, block_size)
+    wt_hi, wt_lo, et_hi, et_lo = reblocked
     return _block_gemm(g_fp8, g_exps, wt_hi, wt_lo, et_hi, et_lo, block_size, None,
                        torch.float32)
 

@@ -258,8 +258,12 @@ class _TCFP12BlockScaledFunction(torch.autograd.Function):
         ctx.fp8_dgrad = _BLOCK_DGRAD == "fp8"
         saved_act = input_2d if hp_grad_weight else act_fp8
         saved_act_scales = None if hp_grad_weight else act_scales
-        ctx.save_for_backward(saved_act, saved_act_scales, w_hi, None if abd else w_lo, sh,
-                              None if abd else sl)
+        w_lo_b, sl_b = (None, None) if abd else (w_lo, sl)
+        if ctx.fp8_dgrad and ctx.needs_input_grad[0]:
+            # the FP8 dgrad's weight operand, re-blocked along D_out once per
+            # forward; the backward needs nothing else of W
+            w_hi, w_lo_b, sh, sl_b = K.block_requant_t(w_hi, w_lo_b, sh, sl_b, bs)
+        ctx.save_for_backward(saved_act, saved_act_scales, w_hi, w_lo_b, sh, sl_b)
         return output
 
     @staticmethod
@@ -277,19 +281,19 @@ class _TCFP12BlockScaledFunction(torch.autograd.Function):
         # wgrad, and the bias gradient
         fp8_wgrad = need_dw and not ctx.hp_grad_weight and grad_2d.shape[0] % 4 == 0
         want_db = need_db and ctx.has_bias
-        g_deq = g_split = db = None
+        g_deq = g_split = db = g_codes = None
         exact_dx = need_dx and not ctx.fp8_dgrad
-        if exact_dx or fp8_wgrad or want_db:
-            g_deq, g_split, db = K.block_backward_prep(
-                grad_2d, bs, dequant=exact_dx, split=fp8_wgrad, bias=want_db
+        fp8_dx = need_dx and ctx.fp8_dgrad
+        if exact_dx or fp8_wgrad or want_db or fp8_dx:
+            res = K.block_backward_prep(
+                grad_2d, bs, dequant=exact_dx, split=fp8_wgrad, bias=want_db, fp8=fp8_dx
             )
-        if exact_dx:
-            grad_input = K.block_dgrad_from_prep(
-                g_deq, w_hi, w_lo, sh, sl, block_size=bs
-            ).reshape(ctx.input_shape)
-        elif need_dx:
-            grad_input = K.fp8_block_dgrad(grad_2d, w_hi, w_lo, sh, sl, bs).reshape(
-                ctx.input_shape)
+            g_deq, g_split, db = res[:3]
+            if fp8_dx:
+                g_codes = (res[3], res[4])
+            del res  # (the buffers are released as soon as their users are done)
+        # the wgrad first: its split gradient is released before the dgrad
+        # allocates dX (the two never coexist at the layer's peak)
         if need_dw:
             if ctx.hp_grad_weight:
                 grad_weight = grad_2d.t() @ saved_act.to(grad_2d.dtype)
@@ -299,6 +303,17 @@ class _TCFP12BlockScaledFunction(torch.autograd.Function):
             else:
                 grad_weight = K.block_scaled_wgrad(grad_2d, saved_act, act_scales, bs)
                 grad_weight = grad_weight.to(grad_2d.dtype)
+        g_split = None
+        if exact_dx:
+            grad_input = K.block_dgrad_from_prep(
+                g_deq, w_hi, w_lo, sh, sl, block_size=bs
+            ).reshape(ctx.input_shape)
+        elif need_dx:
+            # (the saved weight operands are the forward's re-blocked ones)
+            grad_input = K.fp8_block_dgrad(None, None, None, None, None, bs,
+                                           reblocked=(w_hi, w_lo, sh, sl),
+                                           grad_fp8=g_codes).reshape(ctx.input_shape)
+        g_deq = g_codes = None
         if want_db:
             grad_bias = db.to(grad_2d.dtype)
         return (grad_input, grad_weight, grad_bias) + (None,) * 7

@@ -575,11 +575,18 @@ def test_block_backward_prep_matches_separate_passes(dev, bs, M, N, K_):
     aq, ea = K.block_quantize_fp8(x, bs)
     w = torch.randn(N, K_, generator=g).to(dev) * 0.02
     h, l, eh, el = K.fused_dual_quantize_fp8(w, bs)
-    g_deq, g_split, db = K.block_backward_prep(grad, bs, dequant=True, split=True, bias=True)
-    # G: exactly the dequantised E5M2 block quantisation
+    g_deq, g_split, db, g8, g8e = K.block_backward_prep(grad, bs, dequant=True, split=True,
+                                                         bias=True, fp8=True)
+    # G: exactly the dequantised E5M2 block quantisation, and its codes
     gq, ge = K.block_quantize_fp8(grad, bs, torch.float8_e5m2)
     ref_deq = K.block_dequantize_fp8(gq, ge, bs).bfloat16()
     assert torch.equal(g_deq, ref_deq)
+    assert torch.equal(g8.view(torch.uint8), gq.view(torch.uint8)) and torch.equal(g8e, ge)
+    # the FP8 dgrad from those codes and a re-blocked weight built beforehand
+    dx8_a = K.fp8_block_dgrad(grad, h, l, eh, el, bs)
+    dx8_b = K.fp8_block_dgrad(None, None, None, None, None, bs,
+                              reblocked=K.block_requant_t(h, l, eh, el, bs), grad_fp8=(g8, g8e))
+    assert torch.equal(dx8_a, dx8_b)
     # split: [bf16(g) | bf16(g - bf16(g))] transposed
     hi = grad.bfloat16()
     lo = (grad - hi.float()).bfloat16()
