@@ -416,6 +416,24 @@ int tcfp_block_dual_gemm(const uint8_t* a, int a_fmt, int64_t lda, const int8_t*
                          int64_t k, int block, const float* bias, void* out, int out_dtype,
                          int64_t ldo, void* stream);
 
+/* Activation block quantisation + block dual FP8 GEMM in one launch.
+ * Replaces fused_act_quant_dual_gemm_forward (tcfp/kernels.py:2031-2149,
+ * kernel :826-1041): act [m, k] (f32 or bf16, row stride lda elements) is
+ * block-quantised to E4M3 along k by tcfp_block_quantize's rule inside the
+ * GEMM, and out [m, n] (fp32, row stride ldo) = the block dual GEMM of those
+ * codes with w_hi / w_lo [n, k] E4M3 and e_hi / e_lo [k/block, n]
+ * (+ bias[j]).  act_fp8 [m, k] (row stride k) and act_scales [k/block, m]
+ * receive the codes and exponents (bitwise tcfp_block_quantize's), or are
+ * both NULL (the reference's save_side_outputs=False).
+ *   block in {32, 64, 128}; k % block == 0; act, w_hi, w_lo, act_fp8 and
+ *   bias 16-byte aligned; lda * element bytes and ldb multiples of 16. */
+int tcfp_act_quant_block_dual_gemm(const void* act, int act_dtype, int64_t lda,
+                                   const uint8_t* w_hi, const uint8_t* w_lo, int64_t ldb,
+                                   const int8_t* e_hi, const int8_t* e_lo, int64_t m, int64_t n,
+                                   int64_t k, int block, const float* bias, float* out,
+                                   int64_t ldo, uint8_t* act_fp8, int8_t* act_scales,
+                                   void* stream);
+
 /* Block-scaled dual FP8 GEMM with fp32 block multipliers (non-power-of-two
  * block scales, e.g. the 448 / amax rule of tcfp_block_quantize_f32s):
  *   out[i,j] = sum_kb s_a[kb,i] * ( s_hi[kb,j] * sum_{k in kb} A[i,k] B_hi[j,k]

@@ -63,6 +63,23 @@ def block_dual_gemm_nt(a, a_exps, w_hi, w_lo, e_hi, e_lo, bs):
     return A @ W.T
 
 
+def lo_threshold_exps(e_lo, threshold, tile=64):
+    """The W_lo sparsity rule of the reference's block GEMMs
+    (``tcfp/kernels.py:766-776``, ``:997-1008``, ``:1497``): for every
+    K-block and every tile of ``tile`` consecutive weight rows, the W_lo
+    part is dropped when the largest W_lo scale of the tile (2^e, 0 for the
+    -128 sentinel) is ``<= threshold``.  Returns the exponents with the
+    dropped blocks set to the sentinel (which ``block_deq64(...,
+    lo_sentinel=True)`` reads as zero)."""
+    e = np.asarray(e_lo).copy()
+    scale = np.where(e == -128, 0.0, np.exp2(e.astype(np.float64)))
+    nkb, n = e.shape
+    for t0 in range(0, n, tile):
+        drop = scale[:, t0:t0 + tile].max(axis=1) <= threshold
+        e[drop, t0:t0 + tile] = -128
+    return e
+
+
 def block_dual_gemm_f32s_nt(a, s_a, w_hi, w_lo, s_hi, s_lo, bs, a_fmt=E4M3):
     """Block dual GEMM with fp32 block multipliers (no sentinel):
     ``sum_kb s_a (s_hi A W_hi^T + s_lo A W_lo^T)``; ``w_lo=None`` gives the

@@ -96,6 +96,9 @@ _SIGNATURES = {
     "tcfp_block_dual_gemm_f32s": [_c_void_p, _i32, _i64, _c_void_p, _c_void_p, _c_void_p, _i32,
                                   _i64, _c_void_p, _c_void_p, _i64, _i64, _i64, _i32, _c_void_p,
                                   _c_void_p, _i32, _i64, _c_void_p],
+    "tcfp_act_quant_block_dual_gemm": [_c_void_p, _i32, _i64, _c_void_p, _c_void_p, _i64,
+                                       _c_void_p, _c_void_p, _i64, _i64, _i64, _i32, _c_void_p,
+                                       _c_void_p, _i64, _c_void_p, _c_void_p, _c_void_p],
     "tcfp_wtquant_block_dual_gemm": [_c_void_p, _i32, _i64, _c_void_p, _c_void_p, _i32, _i64,
                                      _i64, _i64, _i32, _c_void_p, _i32, _u64, _u64, _c_void_p,
                                      _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i32,

@@ -206,21 +206,18 @@ TCFP_DEV uint32_t sw4_fp8(float a, float b, float c, float d) {
 // Subnormal q returns -127 (callers clamp at -126).
 // ---------------------------------------------------------------------------
 TCFP_DEV int ceil_log2_f32(float q) {
-  uint32_t b = __float_as_uint(q);
-  int ef = int((b >> 23) & 0xFFu);
-  if (ef == 0) return -127;
-  int k = ef - 127;
-  uint32_t j = b & 0x7FFFFFu;
-  if (j == 0) return k;
-  int a = k < 0 ? -k : k;
-  int p = 0;
-  if (a != 0) {
-    p = 31 - __clz(a);
-    if (k < 0 && (a & (a - 1)) == 0) p -= 1;
-  }
+  // (written without early returns: every case is a select, so the
+  // compiler emits no divergent branches where lanes hold different q)
+  const uint32_t b = __float_as_uint(q);
+  const int ef = int((b >> 23) & 0xFFu);
+  const int k = ef - 127;
+  const uint32_t j = b & 0x7FFFFFu;
+  const uint32_t a = uint32_t(k < 0 ? -k : k);
+  int p = a != 0u ? 31 - __clz(a) : 0;
+  if (k < 0 && (a & (a - 1u)) == 0u) p -= 1;
   const uint64_t table = 0x16'0B'05'02'01'00'00ull;  // J(p) bytes, p = 0..6
-  uint32_t jmax = p <= 0 ? 0u : uint32_t((table >> (8 * p)) & 0xFFu);
-  return j <= jmax ? k : k + 1;
+  const uint32_t jmax = p <= 0 ? 0u : uint32_t((table >> (8 * p)) & 0xFFu);
+  return ef == 0 ? -127 : k + (j > jmax ? 1 : 0);
 }
 
 // Block exponent rule: max(ceil(log2(max(amax,1e-12) / FP8_MAX)), -126).
@@ -240,6 +237,27 @@ TCFP_DEV float exp2i(int e) {
 // encoding of every partial maximum).
 TCFP_DEV uint32_t absbits(float v) { return __float_as_uint(v) & 0x7FFFFFFFu; }
 TCFP_DEV uint32_t umax(uint32_t a, uint32_t b) { return a > b ? a : b; }
+
+// torch.clamp semantics: NaN passes through.
+TCFP_DEV float clampf(float v, float mx) { return v > mx ? mx : (v < -mx ? -mx : v); }
+
+// Max over each group of L consecutive lanes (L a power of two <= 32),
+// returned to every lane of the group.  DPP permutations inside a row of 16
+// lanes (quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror,
+// row_mirror: after each step every lane holds the max of a group twice as
+// large) need no index arithmetic; the 32-lane step is a ds_swizzle with
+// xor mask 16.  Every lane of the wave executes the reduction.
+template <int L>
+TCFP_DEV uint32_t seg_umax(uint32_t m) {
+  if constexpr (L >= 2) m = umax(m, uint32_t(__builtin_amdgcn_update_dpp(0, int(m), 0xB1, 0xF, 0xF, false)));
+  if constexpr (L >= 4) m = umax(m, uint32_t(__builtin_amdgcn_update_dpp(0, int(m), 0x4E, 0xF, 0xF, false)));
+  if constexpr (L >= 8) m = umax(m, uint32_t(__builtin_amdgcn_update_dpp(0, int(m), 0x141, 0xF, 0xF, false)));
+  if constexpr (L >= 16) m = umax(m, uint32_t(__builtin_amdgcn_update_dpp(0, int(m), 0x140, 0xF, 0xF, false)));
+  if constexpr (L >= 32) m = umax(m, uint32_t(__builtin_amdgcn_ds_swizzle(int(m), 0x401F)));
+  static_assert(L >= 1 && L <= 32 && (L & (L - 1)) == 0, "segment of 1..32 lanes");
+  return m;
+}
+
 
 // ---------------------------------------------------------------------------
 // GELU

@@ -105,6 +105,7 @@ TCFP_DEV v8i make_frag(uint4 lo, uint4 hi) {
 // 64-bank (256 B/clk) LDS.
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef uint32_t v2u __attribute__((ext_vector_type(2)));
 #define TCFP_LDS __attribute__((address_space(3)))
 
 constexpr int kSK = 128;                 // K columns per stage
@@ -113,13 +114,16 @@ constexpr uint32_t kOob = 0x80000000u;   // beyond every descriptor's range
 
 TCFP_DEV int swz(int row) { return (row >> 1) & 7; }
 
+// (the words are wave-uniform; readfirstlane states it for the compiler,
+// whose uniformity analysis can lose track of it in kernels with divergent
+// stores, and the DMA's inline assembly needs them in SGPRs)
 TCFP_DEV v4i make_rsrc(const void* base, uint32_t bytes) {
   const uint64_t a = reinterpret_cast<uint64_t>(base);
   v4i r;
-  r[0] = int(uint32_t(a));
-  r[1] = int(uint32_t(a >> 32) & 0xFFFFu);  // stride 0: raw byte addressing
-  r[2] = int(bytes);                        // num_records: bytes in range
-  r[3] = 0x00020000;                        // gfx9 raw-buffer data format word
+  r[0] = __builtin_amdgcn_readfirstlane(int(uint32_t(a)));
+  r[1] = __builtin_amdgcn_readfirstlane(int(uint32_t(a >> 32) & 0xFFFFu));  // stride 0: raw bytes
+  r[2] = __builtin_amdgcn_readfirstlane(int(bytes));  // num_records: bytes in range
+  r[3] = 0x00020000;                                  // gfx9 raw-buffer data format word
   return r;
 }
 
@@ -182,6 +186,14 @@ TCFP_DEV bf16x8 bf16_half(const v8i& f, int q) {
   return __builtin_bit_cast(bf16x8, h);
 }
 
+// Pairs idx in [lo, hi) of a sub-step's (fragment, m-block) pairs (fragment
+// idx % nf) that remain when the W_lo fragments (>= nb) are left out.
+constexpr int pairs_in(int lo, int hi, int nf, int nb, bool with_lo) {
+  int c = 0;
+  for (int idx = lo; idx < hi; ++idx) c += (with_lo || idx % nf < nb) ? 1 : 0;
+  return c;
+}
+
 struct GemmArgs {
   const uint8_t* A;
   const uint8_t* B0;
@@ -219,18 +231,32 @@ struct GemmArgs {
   const float* aux;
   uint32_t* part;
   float* cs_part;
+  // In-kernel activation quantisation (gemm_nt_dma_kernel AQ != 0): A is the
+  // bf16 / fp32 activation (lda in bytes); the tiles of output column 0
+  // write its E4M3 codes to q_out ([M, K], row stride K) and its exponents
+  // to e_out ([K/bs, M]) when q_out is not null.
+  uint8_t* q_out;
+  int8_t* e_out;
 };
 
 // NS = LDS stages in flight (2, or 4 for the small tile when one
 // workgroup per CU is resident): the DMA of stage t + NS is issued once
 // every wave has read stage t, so it has NS - 1 stages of MFMA time to land.
-// F32BS (SCALE 2 only): log2 of the block size, fixed per instantiation so
-// that each block size compiles to one fold schedule.
+// F32BS (SCALE 2, and AQ): log2 of the block size, fixed per instantiation so
+// that each block size compiles to one fold schedule (one segment reduction).
+// AQ (SCALE 1 dual, 128 x 64 tile): 0 = A is FP8 codes with exponents e_a;
+// 1 / 2 = A is the bf16 / fp32 activation, block-quantised to E4M3 inside
+// the kernel (the reference's fused activation-quant GEMM).
 template <int AF, int BF, bool SPLIT, typename OutT, int NW, int BM, int BN, int SCALE, int NS,
-          int F32BS = 0>
-__global__ __launch_bounds__(NW * 64, (NW == 4 && NS == 2 && BM == 128 ? 2 : 1)) void gemm_nt_dma_kernel(
+          int F32BS = 0, int AQ = 0>
+__global__ __launch_bounds__(NW * 64, (NW == 4 && NS == 2 && BM <= 128 ? 2 : 1)) void gemm_nt_dma_kernel(
     GemmArgs g) {
-  static_assert((SCALE == 2) == (F32BS != 0), "fp32 block scales fix the block size");
+  static_assert((SCALE == 2 || AQ != 0) == (F32BS != 0), "fp32 block scales and AQ fix the block size");
+  // AQ: bf16 activations on the 128 x 64 tile; fp32 ones (twice the bytes
+  // per stage in registers) on a 64 x 64 tile
+  static_assert(AQ == 0 || (SCALE == 1 && !SPLIT && AF == 0 && NS == 2 && NW == 4 && BN == 64 &&
+                            BM == (AQ == 2 ? 64 : 128)),
+                "in-kernel activation quantisation: E4M3 block-scaled dual GEMM, 128/64 x 64 tile");
   constexpr int f32_bsh = F32BS;
   constexpr int WM = NW / 2;        // wave rows
   constexpr int TMW = BM / WM;      // activation rows per wave
@@ -240,7 +266,9 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && NS == 2 && BM == 128 ? 2 : 1))
   constexpr int NF = 2 * NB;        // weight fragments per sub-step
   constexpr int SROWS = BM + 2 * BN;
   constexpr int STAGE = SROWS * kRowB;
-  constexpr int RPW = SROWS / NW;   // stage rows DMA'd by each wave
+  // stage rows DMA'd by each wave (with AQ the waves quantise the activation
+  // rows themselves and DMA only the weight rows)
+  constexpr int RPW = (AQ ? 2 * BN : SROWS) / NW;
   constexpr int DI = RPW / 8;       // 1 KiB DMA instructions per wave and stage
   static_assert(RPW % 16 == 0 && BM % RPW == 0 && BN % RPW == 0, "DMA rows must tile regions");
   static_assert(MB >= 1 && NB >= 1, "tile too small for the wave grid");
@@ -250,7 +278,11 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && NS == 2 && BM == 128 ? 2 : 1))
   // SCALE 2: a three-slot ring of per-stage fp32 scale areas (up to four
   // K-blocks of 1 KiB) behind the operand stages
   constexpr int kScB = SCALE == 2 ? 4096 : 0;
-  __shared__ __align__(16) uint8_t lds[NS * STAGE + 3 * kScB];
+  // AQ: the activation exponents of the two buffered stages, [buffer][32-K
+  // block of the stage][row] (a block of bs >= 32 columns fills
+  // kSK / bs of the four slots)
+  constexpr int kExB = AQ ? 2 * (kSK / 32) * BM : 0;
+  __shared__ __align__(16) uint8_t lds[NS * STAGE + 3 * kScB + kExB];
 
   const int M = g.M, N = g.N;
   int K = g.K;
@@ -286,7 +318,7 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && NS == 2 && BM == 128 ? 2 : 1))
 
   // ---- this wave's DMA source: its RPW stage rows lie in the activation,
   // slot-0 or slot-1 region
-  const int srow0 = wave * RPW;
+  const int srow0 = (AQ ? BM : 0) + wave * RPW;
   const uint8_t* src;
   int64_t ld;
   int rows_left, row_base;
@@ -368,6 +400,127 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && NS == 2 && BM == 128 ? 2 : 1))
     }
   };
 
+  // ---- in-kernel activation quantisation (AQ).  A stage's BM x 128
+  // activation tile is loaded into registers (16 bytes per lane and round,
+  // ALPR lanes per row: consecutive lanes hold consecutive K columns, so a
+  // (row, K-block) segment lies in AL adjacent lanes), block-quantised with
+  // block_quant_kernel's rule -- max |x| over the segment, exponent
+  // max(ceil(log2(amax / 448)), -126), codes RNE(clamp(x * 2^-e, 448)) --
+  // and written as E4M3 codes into the stage's activation rows (swizzled as
+  // the DMA would write them) and as exponents into the stage's exponent
+  // slots.  The tiles of output column 0 also store the codes and
+  // exponents to q_out / e_out.
+  constexpr int AES = AQ == 2 ? 4 : 2;             // input element bytes
+  constexpr int AVEC = 16 / AES;                    // elements per lane and round
+  constexpr int ALPR = kSK / AVEC;                  // lanes per stage row
+  constexpr int ARPI = 64 / ALPR;                   // rows per wave and round
+  constexpr int ARL = AQ ? BM / (NW * ARPI) : 1;    // rounds per stage
+  constexpr int AL = AQ ? (1 << f32_bsh) / AVEC : 1;  // lanes per (row, block) segment
+  uint4 ar[ARL];
+  const int arow = AQ ? wave * ARPI + lane / ALPR : 0;  // tile row of round 0
+  const int acol = AQ ? (lane % ALPR) * AVEC : 0;       // column within the stage
+  const int arows = min(M - m0, BM);
+  const uint32_t anrec =
+      (AQ && arows > 0) ? uint32_t(int64_t(arows - 1) * g.lda + int64_t(K) * AES) : 0u;
+  const __amdgpu_buffer_rsrc_t arsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t*>(g.A) + int64_t(m0) * g.lda, 0, int(anrec), 0x00020000);
+  const uint32_t avoff0 = uint32_t(arow) * uint32_t(g.lda) + uint32_t(acol * AES);
+  const uint32_t astride = uint32_t(NW * ARPI) * uint32_t(g.lda);  // bytes between rounds
+  // loads of stage t's activation (rows past M and columns past K read 0)
+  auto aload = [&](uint4* a4, int t) {
+    if constexpr (AQ != 0) {
+      const uint32_t soff = uint32_t(t) * (kSK * AES);
+      const bool kin = t * kSK + acol < K;
+#pragma unroll
+      for (int r = 0; r < ARL; ++r) {
+        const bool in = kin && arow + r * NW * ARPI < arows;
+        a4[r] = __builtin_bit_cast(
+            uint4, __builtin_amdgcn_raw_buffer_load_b128(arsrc, in ? avoff0 + r * astride : kOob,
+                                                         soff, 0));
+      }
+    }
+  };
+  int8_t* const exs = reinterpret_cast<int8_t*>(lds + NS * STAGE + 3 * kScB);
+  // side outputs through buffer stores: a store beyond the descriptor's
+  // range is dropped, so rows past M and columns past K need no branches
+  const bool side = AQ != 0 && g.q_out != nullptr && tn == 0;
+  const uint32_t qnrec = side && arows > 0 ? uint32_t(int64_t(arows) * K) : 0u;
+  const __amdgpu_buffer_rsrc_t qrsrc = __builtin_amdgcn_make_buffer_rsrc(
+      g.q_out + int64_t(m0) * K, 0, int(qnrec), 0x00020000);
+  const uint32_t enrec = side ? uint32_t(int64_t(K >> f32_bsh) * M) : 0u;
+  const __amdgpu_buffer_rsrc_t ersrc =
+      __builtin_amdgcn_make_buffer_rsrc(g.e_out, 0, int(enrec), 0x00020000);
+  auto aquant = [&](const uint4* a4, int t) {
+    if constexpr (AQ != 0) {
+      uint8_t* st = lds + (t & 1) * STAGE;
+      int8_t* ex = exs + (t & 1) * (kSK / 32) * BM;
+#pragma unroll
+      for (int r = 0; r < ARL; ++r) {
+        const int row = arow + r * NW * ARPI;
+        const uint32_t w[4] = {a4[r].x, a4[r].y, a4[r].z, a4[r].w};
+        float v[AVEC];
+        if constexpr (AQ == 2) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) v[j] = __uint_as_float(w[j]);
+        } else {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            v[2 * j] = __uint_as_float(w[j] << 16);
+            v[2 * j + 1] = __uint_as_float(w[j] & 0xFFFF0000u);
+          }
+        }
+        uint32_t a = 0;
+#pragma unroll
+        for (int j = 0; j < AVEC; ++j) a = umax(a, absbits(v[j]));
+        a = seg_umax<AL>(a);
+        const float amax = __uint_as_float(a);
+        const int e = block_exponent(amax, kE4M3Max);
+        const float mul = exp2i(-e);
+#pragma unroll
+        for (int j = 0; j < AVEC; ++j) v[j] = v[j] * mul;
+        // |x| <= amax, so the clamp changes nothing unless amax * 2^-e
+        // exceeds 448 (or is NaN) somewhere in the wave
+        if (__builtin_amdgcn_ballot_w64(!(amax * mul <= kE4M3Max)) != 0) {
+#pragma unroll
+          for (int j = 0; j < AVEC; ++j) v[j] = clampf(v[j], kE4M3Max);
+        }
+        const int off = row * kRowB + ((((acol >> 4) ^ swz(row))) << 4) + (acol & 15);
+        const int gk = t * kSK + acol;
+        const bool kin = gk < K && row < arows;
+        const uint32_t qoff = kin ? uint32_t(row) * uint32_t(K) + uint32_t(gk) : kOob;
+        if constexpr (AQ == 2) {
+          const uint32_t c = cvt4_fp8<TCFP_FP8_E4M3>(v[0], v[1], v[2], v[3]);
+          *reinterpret_cast<uint32_t*>(st + off) = c;
+          if (side) __builtin_amdgcn_raw_buffer_store_b32(c, qrsrc, qoff, 0, 0);
+        } else {
+          const uint2 c = make_uint2(cvt4_fp8<TCFP_FP8_E4M3>(v[0], v[1], v[2], v[3]),
+                                     cvt4_fp8<TCFP_FP8_E4M3>(v[4], v[5], v[6], v[7]));
+          *reinterpret_cast<uint2*>(st + off) = c;
+          if (side) __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(v2u, c), qrsrc, qoff, 0, 0);
+        }
+        // every lane of the segment writes the (same) exponent: no branch
+        ex[(acol >> f32_bsh) * BM + row] = int8_t(e);
+        if (side) {
+          const uint32_t eoff =
+              kin ? uint32_t(gk >> f32_bsh) * uint32_t(M) + uint32_t(m0 + row) : kOob;
+          __builtin_amdgcn_raw_buffer_store_b8(uint8_t(e), ersrc, eoff, 0, 0);
+        }
+      }
+    }
+  };
+  // activation exponents of stage t from the exponent slots, per
+  // (m-block, sub-step) as load_raw lays them out
+  auto aexps = [&](int* rw_, int t) {
+    if constexpr (AQ != 0) {
+      const int8_t* ex = exs + (t & 1) * (kSK / 32) * BM;
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int i = 0; i < MB; ++i)
+          rw_[2 * (NF + i) + h] = ex[((h * 64 + lg * 32) >> f32_bsh) * BM + wm * TMW + i * 32 + lr];
+    }
+  };
+
   // ---- per-lane LDS read offsets: sub-step h, 16-byte half q of a fragment.
   // The MFMA takes byte j of lane l as K index 16*(l/32) + 32*(j/16) + j%16
   // of its 64-wide step, and the E8M0 scale of lane l covers the 32-wide K
@@ -402,10 +555,12 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && NS == 2 && BM == 128 ? 2 : 1))
           const int8_t* e = (!SPLIT && (q / NB)) ? g.e_1 : g.e_0;
           raw[2 * q + h] = (kin && rw + dq(q) < uint32_t(N)) ? int(e[ow + dq(q)]) : 0;
         }
+        if constexpr (AQ == 0) {
 #pragma unroll
-        for (int i = 0; i < MB; ++i)
-          raw[2 * (NF + i) + h] =
-              (kin && ra + 32 * i < uint32_t(M)) ? int(g.e_a[oa + 32 * i]) : 0;
+          for (int i = 0; i < MB; ++i)
+            raw[2 * (NF + i) + h] =
+                (kin && ra + 32 * i < uint32_t(M)) ? int(g.e_a[oa + 32 * i]) : 0;
+        }
       }
     }
   };
@@ -449,53 +604,69 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && NS == 2 && BM == 128 ? 2 : 1))
       f[NF + i] = make_frag(lds_read16(st, rb + ro[h][0]), lds_read16(st, rb + ro[h][1]));
     }
   };
-  // One sub-step (h) of MFMAs; `sc` holds the stage's E8M0 scales.
-  auto mfmas = [&](const v8i* f, const uint32_t* sc, int h) {
+  // W_lo sparsity (SCALE 1 dual): a stage whose W_lo exponents are the
+  // -128 sentinel on every lane of the wave (E8M0 code 0; the quantisers
+  // write all-zero codes there) contributes nothing, so its W_lo MFMAs are
+  // skipped (tcfp/kernels.py:766-776 with the default threshold 0).
+  constexpr bool kSkipLo = SCALE == 1 && !SPLIT;
+  auto lo_live = [&](const uint32_t* scv) -> bool {
+    if constexpr (kSkipLo) {
+      uint32_t o = 0;
+#pragma unroll
+      for (int q = NB; q < NF; ++q) o |= scv[2 * q] | scv[2 * q + 1];
+      return __builtin_amdgcn_ballot_w64(o != 0u) != 0;
+    } else {
+      return true;
+    }
+  };
+  // One MFMA of weight fragment q and activation fragment i, sub-step h
+  auto mfma1 = [&](const v8i* f, const uint32_t* scv, int h, int q, int i) {
+    v16f& c = acc[(q / NB) % NACC][q % NB][i];
+    if constexpr (AF == kBF16) {
+      // a fragment holds 16 bf16 K values: two K=16 MFMAs
+      c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bf16_half(f[q], 0), bf16_half(f[NF + i], 0),
+                                                  c, 0, 0, 0);
+      c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bf16_half(f[q], 1), bf16_half(f[NF + i], 1),
+                                                  c, 0, 0, 0);
+    } else if constexpr (SCALE == 1) {
+      c = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+          f[q], f[NF + i], c, BF, AF, 0, int(scv[2 * q + h]), 0, int(scv[2 * (NF + i) + h]));
+    } else {
+      c = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f[q], f[NF + i], c, BF, AF, 0, 127,
+                                                           0, 127);
+    }
+  };
+  // One sub-step (h) of MFMAs; `sc` holds the stage's E8M0 scales.  LO
+  // false (a std::integral_constant) leaves out the W_lo fragments.
+  auto mfmas = [&](const v8i* f, const uint32_t* scv, int h, auto lo) {
 #pragma unroll
     for (int i = 0; i < MB; ++i)
 #pragma unroll
       for (int q = 0; q < NF; ++q) {
-        v16f& c = acc[(q / NB) % NACC][q % NB][i];
-        if constexpr (AF == kBF16) {
-          // a fragment holds 16 bf16 K values: two K=16 MFMAs
-          c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bf16_half(f[q], 0), bf16_half(f[NF + i], 0),
-                                                      c, 0, 0, 0);
-          c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bf16_half(f[q], 1), bf16_half(f[NF + i], 1),
-                                                      c, 0, 0, 0);
-        } else if constexpr (SCALE == 1) {
-          c = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-              f[q], f[NF + i], c, BF, AF, 0, int(sc[2 * q + h]), 0, int(sc[2 * (NF + i) + h]));
-        } else {
-          c = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f[q], f[NF + i], c, BF, AF, 0, 127,
-                                                               0, 127);
+        if constexpr (kSkipLo && !decltype(lo)::value) {
+          if (q >= NB) continue;
         }
+        mfma1(f, scv, h, q, i);
       }
   };
   // MFMAs of (fragment, m-block) pairs [lo, hi) of sub-step h, pairs in
   // m-block-major order as in mfmas
-  auto mfmas_range = [&](const v8i* f, const uint32_t* sc, int h, int lo, int hi) {
+  auto mfmas_range = [&](const v8i* f, const uint32_t* scv, int h, int lo, int hi, auto live) {
 #pragma unroll
     for (int idx = 0; idx < NF * MB; ++idx) {
       if (idx < lo || idx >= hi) continue;
       const int i = idx / NF, q = idx % NF;
-      v16f& c = acc[(q / NB) % NACC][q % NB][i];
-      if constexpr (AF == kBF16) {
-        c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bf16_half(f[q], 0), bf16_half(f[NF + i], 0),
-                                                    c, 0, 0, 0);
-        c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bf16_half(f[q], 1), bf16_half(f[NF + i], 1),
-                                                    c, 0, 0, 0);
-      } else if constexpr (SCALE == 1) {
-        c = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-            f[q], f[NF + i], c, BF, AF, 0, int(sc[2 * q + h]), 0, int(sc[2 * (NF + i) + h]));
-      } else {
-        c = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f[q], f[NF + i], c, BF, AF, 0, 127,
-                                                             0, 127);
+      if constexpr (kSkipLo && !decltype(live)::value) {
+        if (q >= NB) continue;
       }
+      mfma1(f, scv, h, q, i);
     }
   };
-  // NF*MB MFMAs and 2*(NF+MB) LDS reads per sub-step: spread the reads evenly
-  auto interleave = [&]() {
-    interleave_mfma_lds<NF * MB * (AF == kBF16 ? 2 : 1), 2 * (NF + MB), 0>();
+  // NF*MB MFMAs (NB*MB without W_lo) and 2*(NF+MB) LDS reads per sub-step:
+  // spread the reads evenly
+  auto interleave = [&](auto lo) {
+    constexpr int nmf = (kSkipLo && !decltype(lo)::value) ? NB * MB : NF * MB;
+    interleave_mfma_lds<nmf * (AF == kBF16 ? 2 : 1), 2 * (NF + MB), 0>();
   };
   // All DMA issued so far has landed and every wave's LDS reads are done
   // (gfx9 s_waitcnt: vmcnt bits [3:0] and [15:14], expcnt [6:4], lgkmcnt [11:8]).
@@ -518,16 +689,27 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && NS == 2 && BM == 128 ? 2 : 1))
   int raw[2 * (NF + MB)];   // exponents of the next stage, in flight
   if (nt > 0) {
     load_raw(raw, 0);
+    if constexpr (AQ != 0) aload(ar, 0);
 #pragma unroll
     for (int s = 0; s < NS; ++s) issue(s);
-    // wait for stage 0 only: the DMAs of stages 1 .. NS-1 may stay in flight
-    // (the exponent loads were issued before all of them and are complete;
-    // a wave that also loads fp32 scales issues one more per stage, which
-    // only makes this wait longer)
-    constexpr int kPro = (NS - 1) * DI;
-    __builtin_amdgcn_s_waitcnt((kPro & 15) | (7 << 4) | ((kPro >> 4) << 14));
+    if constexpr (AQ != 0) {
+      // stage 0's activation into buffer 0 (waiting for its loads waits for
+      // the DMAs issued after them too), then stage 1's loads; the barrier
+      // waits for the LDS writes only
+      aquant(ar, 0);
+      if (nt > 1) aload(ar, 1);
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0), vmcnt and expcnt untouched
+    } else {
+      // wait for stage 0 only: the DMAs of stages 1 .. NS-1 may stay in flight
+      // (the exponent loads were issued before all of them and are complete;
+      // a wave that also loads fp32 scales issues one more per stage, which
+      // only makes this wait longer)
+      constexpr int kPro = (NS - 1) * DI;
+      __builtin_amdgcn_s_waitcnt((kPro & 15) | (7 << 4) | ((kPro >> 4) << 14));
+    }
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
+    if constexpr (AQ != 0) aexps(raw, 0);
     pack(sc, raw);
     read_frags(f0, 0, 0);
   }
@@ -624,17 +806,24 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && NS == 2 && BM == 128 ? 2 : 1))
     for (int t = 0; t < nt; ++t) {
       load_raw(raw, t + 1);
       __builtin_amdgcn_sched_barrier(0);
-      read_frags(f1, t, 1);
-      mfmas_range(f0, sc, 0, 0, NP / 2);
-      interleave_mfma_lds<(NP / 2) * MPP, 2 * (NF + MB), 0>();
-      sync_all();
-      mfmas_range(f0, sc, 0, NP / 2, NP);
-      __builtin_amdgcn_sched_barrier(0);
-      issue(t + NS);
-      __builtin_amdgcn_sched_barrier(0);
-      read_frags(f0, t + 1, 0);
-      mfmas(f1, sc, 1);
-      interleave();
+      // the stage's body with or without its W_lo MFMAs
+      auto body = [&](auto lv) {
+        constexpr bool L = decltype(lv)::value || !kSkipLo;
+        read_frags(f1, t, 1);
+        mfmas_range(f0, sc, 0, 0, NP / 2, lv);
+        interleave_mfma_lds<pairs_in(0, NP / 2, NF, NB, L) * MPP, 2 * (NF + MB), 0>();
+        sync_all();
+        mfmas_range(f0, sc, 0, NP / 2, NP, lv);
+        __builtin_amdgcn_sched_barrier(0);
+        issue(t + NS);
+        __builtin_amdgcn_sched_barrier(0);
+        read_frags(f0, t + 1, 0);
+        mfmas(f1, sc, 1, lv);
+        interleave(lv);
+      };
+      // (no W_lo skip here: a second copy of this body takes the register
+      // headroom of the 256-row tile and spills)
+      body(std::true_type{});
       pack(sc, raw);
     }
   } else {
@@ -642,19 +831,36 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && NS == 2 && BM == 128 ? 2 : 1))
     // exponents of stage t + 1 (SCALE 1, NS 2): this stage's vmcnt(0) covers them
     load_raw(raw, t + 1);
     __builtin_amdgcn_sched_barrier(0);
-    // sub-step 0 of stage t; fragments of sub-step 1 stream in
-    read_frags(f1, t, 1);
-    mfmas(f0, sc, 0);
-    interleave();
-    // stage t + 1 landed, every wave has its stage-t fragments: refill t's buffer
-    sync_all();
-    issue(t + NS);
-    __builtin_amdgcn_sched_barrier(0);
-    // sub-step 1 of stage t; fragments of stage t + 1 sub-step 0 stream in
-    // (after the last stage they read a stale buffer and are never used)
-    read_frags(f0, t + 1, 0);
-    mfmas(f1, sc, 1);
-    interleave();
+    // the stage's body with or without its W_lo MFMAs
+    auto body = [&](auto lv) {
+      // sub-step 0 of stage t; fragments of sub-step 1 stream in
+      read_frags(f1, t, 1);
+      mfmas(f0, sc, 0, lv);
+      interleave(lv);
+      // AQ: the activation of stage t + 1 (loaded during stage t - 1) is
+      // quantised into buffer (t + 1) & 1, which every wave finished
+      // reading at the previous barrier
+      if constexpr (AQ != 0) {
+        if (t + 1 < nt) aquant(ar, t + 1);
+      }
+      // stage t + 1 landed, every wave has its stage-t fragments: refill t's buffer
+      sync_all();
+      issue(t + NS);
+      if constexpr (AQ != 0) {
+        if (t + 2 < nt) aload(ar, t + 2);
+        if (t + 1 < nt) aexps(raw, t + 1);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      // sub-step 1 of stage t; fragments of stage t + 1 sub-step 0 stream in
+      // (after the last stage they read a stale buffer and are never used)
+      read_frags(f0, t + 1, 0);
+      mfmas(f1, sc, 1, lv);
+      interleave(lv);
+    };
+    // (with AQ the stage body is not duplicated: its quantising code is
+    // large, and the narrow GEMMs it serves gain nothing from the skip)
+    if (AQ != 0 || lo_live(sc)) body(std::true_type{});
+    else body(std::false_type{});
     pack(sc, raw);
   }
   }
@@ -1446,6 +1652,66 @@ extern "C" int tcfp_block_dual_gemm(const uint8_t* a, int a_fmt, int64_t lda, co
   ga.bias = bias; ga.out = out; ga.ldo = ldo;
   return dispatch_all<1>(a_fmt, b_fmt, b_lo != nullptr, out_dtype, ga,
                          static_cast<hipStream_t>(stream));
+}
+
+namespace {
+
+// The fused activation-quant GEMM: one launch of the 128 x 64 tile with the
+// activation block-quantised inside (AQ 1 bf16 / 2 fp32, BSH = log2 block).
+template <int AQ, int BSH>
+int launch_actq(GemmArgs ga, hipStream_t st) {
+  constexpr int BMv = AQ == 2 ? 64 : 128;
+  ga.tiles_m = (ga.M + BMv - 1) / BMv;
+  ga.tiles_n = (ga.N + 63) / 64;
+  if (!grid_x_fits(int64_t(ga.tiles_m) * ga.tiles_n, 256)) return TCFP_ERR_SHAPE;
+  const dim3 grid(unsigned(ga.tiles_m) * unsigned(ga.tiles_n));
+  gemm_nt_dma_kernel<0, 0, false, float, 4, BMv, 64, 1, 2, BSH, AQ><<<grid, 256, 0, st>>>(ga);
+  return hipGetLastError() == hipSuccess ? TCFP_OK : TCFP_ERR_HIP;
+}
+
+}  // namespace
+
+extern "C" int tcfp_act_quant_block_dual_gemm(const void* act, int act_dtype, int64_t lda,
+                                              const uint8_t* w_hi, const uint8_t* w_lo,
+                                              int64_t ldb, const int8_t* e_hi,
+                                              const int8_t* e_lo, int64_t m, int64_t n,
+                                              int64_t k, int block, const float* bias,
+                                              float* out, int64_t ldo, uint8_t* act_fp8,
+                                              int8_t* act_scales, void* stream) {
+  if (act_dtype != TCFP_DTYPE_F32 && act_dtype != TCFP_DTYPE_BF16) return TCFP_ERR_DTYPE;
+  if (m < 0 || n < 0 || k < 0 || m > INT32_MAX || n > INT32_MAX || k > INT32_MAX)
+    return TCFP_ERR_SHAPE;
+  if (block != 32 && block != 64 && block != 128) return TCFP_ERR_SHAPE;
+  if (k % block != 0 || lda < k || ldb < k || ldo < n) return TCFP_ERR_SHAPE;
+  if ((act_fp8 == nullptr) != (act_scales == nullptr)) return TCFP_ERR_SHAPE;
+  if (!w_hi || !w_lo || !e_hi || !e_lo) return TCFP_ERR_SHAPE;
+  const int es = act_dtype == TCFP_DTYPE_F32 ? 4 : 2;
+  if ((lda * es) % 16 != 0 || ldb % 16 != 0) return TCFP_ERR_ALIGN;
+  if (!al16(act) || !al16(w_hi) || !al16(w_lo) || (act_fp8 && !al16(act_fp8)))
+    return TCFP_ERR_ALIGN;
+  if (bias && !al16(bias)) return TCFP_ERR_ALIGN;
+  if (m == 0 || n == 0) return TCFP_OK;
+  // the activation rows and the weight rows of a tile must lie within one
+  // buffer descriptor's 32-bit reach
+  if (int64_t(128) * lda * es + k * es >= kMaxSpan || int64_t(64) * ldb + k >= kMaxSpan)
+    return TCFP_ERR_SHAPE;
+  GemmArgs ga{};
+  ga.A = static_cast<const uint8_t*>(act);
+  ga.B0 = w_hi; ga.B1 = w_lo;
+  ga.M = int(m); ga.N = int(n); ga.K = int(k); ga.lda = lda * es; ga.ldb = ldb;
+  ga.e_0 = e_hi; ga.e_1 = e_lo;
+  ga.bs_shift = block == 32 ? 5 : (block == 64 ? 6 : 7);
+  ga.bias = bias; ga.out = out; ga.ldo = ldo;
+  ga.q_out = act_fp8; ga.e_out = act_scales;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (act_dtype == TCFP_DTYPE_BF16) {
+    if (block == 32) return launch_actq<1, 5>(ga, st);
+    if (block == 64) return launch_actq<1, 6>(ga, st);
+    return launch_actq<1, 7>(ga, st);
+  }
+  if (block == 32) return launch_actq<2, 5>(ga, st);
+  if (block == 64) return launch_actq<2, 6>(ga, st);
+  return launch_actq<2, 7>(ga, st);
 }
 
 extern "C" int tcfp_block_dual_gemm_f32s(const uint8_t* a, int a_fmt, int64_t lda,

@@ -102,8 +102,6 @@ TCFP_DEV void store8(float* p, const float v[8]) {
   *reinterpret_cast<float4*>(p + 4) = make_float4(v[4], v[5], v[6], v[7]);
 }
 
-// torch.clamp semantics: NaN passes through.
-TCFP_DEV float clampf(float v, float mx) { return v > mx ? mx : (v < -mx ? -mx : v); }
 
 template <int FMT>
 TCFP_DEV uint2 encode8(const float v[8]) {
@@ -1339,23 +1337,6 @@ struct Seg {
   static constexpr int L = BS / VEC;
   static constexpr int ROWS = kThreads / L;
 };
-
-// Max over each group of L consecutive lanes (L a power of two <= 32),
-// returned to every lane of the group.  DPP permutations inside a row of 16
-// lanes (quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror,
-// row_mirror: after each step every lane holds the max of a group twice as
-// large) need no index arithmetic; the 32-lane step is a ds_swizzle with
-// xor mask 16.  Every lane of the wave executes the reduction.
-template <int L>
-TCFP_DEV uint32_t seg_umax(uint32_t m) {
-  if constexpr (L >= 2) m = umax(m, uint32_t(__builtin_amdgcn_update_dpp(0, int(m), 0xB1, 0xF, 0xF, false)));
-  if constexpr (L >= 4) m = umax(m, uint32_t(__builtin_amdgcn_update_dpp(0, int(m), 0x4E, 0xF, 0xF, false)));
-  if constexpr (L >= 8) m = umax(m, uint32_t(__builtin_amdgcn_update_dpp(0, int(m), 0x141, 0xF, 0xF, false)));
-  if constexpr (L >= 16) m = umax(m, uint32_t(__builtin_amdgcn_update_dpp(0, int(m), 0x140, 0xF, 0xF, false)));
-  if constexpr (L >= 32) m = umax(m, uint32_t(__builtin_amdgcn_ds_swizzle(int(m), 0x401F)));
-  static_assert(L >= 1 && L <= 32 && (L & (L - 1)) == 0, "segment of 1..32 lanes");
-  return m;
-}
 
 template <typename InT>
 TCFP_DEV void loadv(const InT* p, float* v);

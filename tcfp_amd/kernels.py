@@ -982,6 +982,34 @@ def block_scaled_gemm(
     return _block_gemm(a_fp8, scales_a, b_fp8, None, scales_b, None, block_size, None, out_dtype)
 
 
+def _lo_threshold(w_lo: torch.Tensor, lo_scales: torch.Tensor, threshold: float,
+                  block_size: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """The W_lo sparsity rule for ``sparse_threshold > 0``
+    (``tcfp/kernels.py:766-776, 997-1008``): the W_lo part of K-block kb is
+    dropped for a tile of weight rows when the largest of the tile's W_lo
+    scales (2^e, 0 for the -128 sentinel) is at most the threshold.  The
+    reference's tile width is its autotuned ``BLOCK_N`` (64 or 128), so its
+    result depends on the configuration it picked; this build fixes the
+    rule at 64-row tiles.  Dropped blocks become zero codes under the
+    sentinel, which the GEMM skips.  Threshold <= 0 changes nothing (only
+    sentinel blocks qualify, and the GEMM skips wave tiles of those)."""
+    if threshold <= 0.0:
+        return w_lo, lo_scales
+    n = w_lo.shape[0]
+    num_kb = lo_scales.shape[0]
+    sc = torch.where(lo_scales == -128, torch.zeros((), device=lo_scales.device),
+                     torch.exp2(lo_scales.float()))
+    g = (n + 63) // 64
+    pad = torch.zeros((num_kb, g * 64), dtype=sc.dtype, device=sc.device)
+    pad[:, :n] = sc
+    drop = (pad.view(num_kb, g, 64).amax(-1) <= threshold)              # [num_kb, g]
+    drop_rows = drop.repeat_interleave(64, dim=1)[:, :n]                # [num_kb, n]
+    lo_scales = lo_scales.masked_fill(drop_rows, -128)
+    codes = w_lo.view(torch.uint8).reshape(n, num_kb, block_size)
+    codes = codes.masked_fill(drop_rows.t().unsqueeze(-1), 0)
+    return codes.reshape(n, num_kb * block_size).view(w_lo.dtype), lo_scales
+
+
 def fused_block_scaled_dual_gemm_forward(
     act_fp8: torch.Tensor,
     w_hi_fp8: torch.Tensor,
@@ -1001,10 +1029,12 @@ def fused_block_scaled_dual_gemm_forward(
 
     Reference: ``fused_block_scaled_dual_gemm_forward``
     (``tcfp/kernels.py:1939-2028``).  W_lo exponents of -128 (zero residual
-    blocks) contribute nothing.  ``sparse_threshold``, ``persistent`` and
-    ``launch_mult`` are scheduling hints of the reference's Triton kernel;
-    they do not change the result and are accepted for API compatibility
-    (the W_lo skip is output-neutral: skipped blocks hold zero codes).
+    blocks) contribute nothing, and a wave tile whose W_lo exponents are
+    all the sentinel skips its W_lo MFMAs (the reference's sparsity fast
+    path at its default threshold 0).  ``sparse_threshold > 0`` drops the
+    W_lo blocks the reference's rule drops (``_lo_threshold``).
+    ``persistent`` and ``launch_mult`` are scheduling hints of the
+    reference's Triton kernel, accepted and without effect on the result.
     fp32 block multipliers for all three operands (``scale_format="fp32"``
     quantisers) select the fp32-scale kernel: the same sum with the
     multipliers in place of 2^exp.
@@ -1014,6 +1044,9 @@ def fused_block_scaled_dual_gemm_forward(
     assert K == K2 and tuple(w_lo_fp8.shape) == (N, K), (
         f"Shape mismatch: act({M},{K}), w_hi({N},{K2}), w_lo{tuple(w_lo_fp8.shape)}"
     )
+    if sparse_threshold > 0.0 and w_lo_scales.dtype == torch.int8:
+        w_lo_fp8, w_lo_scales = _lo_threshold(w_lo_fp8, w_lo_scales, sparse_threshold,
+                                              block_size)
     return _block_gemm(act_fp8, act_scales, w_hi_fp8, w_lo_fp8, w_hi_scales, w_lo_scales,
                        block_size, bias, out_dtype)
 
@@ -1032,18 +1065,19 @@ def fused_act_quant_dual_gemm_forward(
     *,
     bias: torch.Tensor | None = None,
 ) -> tuple[torch.Tensor, torch.Tensor | None, torch.Tensor | None]:
-    """Activation block-quantisation + block-scaled dual GEMM.
+    """Activation block-quantisation + block-scaled dual GEMM, one launch.
 
     Reference: ``fused_act_quant_dual_gemm_forward`` (``tcfp/kernels.py:
     2031-2149``, kernel ``:826-1041``).  ``act`` [M, K] bf16/fp32 is
     quantised per (row, K-block) to E4M3 with the ``block_quantize_fp8``
-    exponent rule, then multiplied with W_hi/W_lo as
-    ``fused_block_scaled_dual_gemm_forward``.  Returns ``(out fp32 [M, N],
-    act_fp8, act_scales)`` -- the side outputs are bitwise what
+    exponent rule inside the GEMM (each workgroup quantises its activation
+    tile in registers and stages the codes in LDS), then multiplied with
+    W_hi/W_lo as ``fused_block_scaled_dual_gemm_forward``.  Returns ``(out
+    fp32 [M, N], act_fp8, act_scales)`` -- the side outputs, written by the
+    workgroups of the first output-column tile, are bitwise what
     ``block_quantize_fp8`` returns -- or ``(out, None, None)`` when
-    ``save_side_outputs`` is False.  Runs as two HIP launches (block
-    quantisation, then the GEMM with the exponents in the MFMA's scale
-    operands).
+    ``save_side_outputs`` is False (nothing is written for them).
+    ``sparse_threshold`` as ``fused_block_scaled_dual_gemm_forward``.
     """
     M, K = act.shape
     N, K2 = w_hi_fp8.shape
@@ -1051,12 +1085,39 @@ def fused_act_quant_dual_gemm_forward(
         f"Shape mismatch: act({M},{K}), w_hi({N},{K2}), w_lo{tuple(w_lo_fp8.shape)}"
     )
     assert K % block_size == 0, f"K ({K}) must be divisible by block_size ({block_size})"
-    act_fp8, act_scales = block_quantize_fp8(act, block_size)
-    out = _block_gemm(act_fp8, act_scales, w_hi_fp8, w_lo_fp8, w_hi_scales, w_lo_scales,
-                      block_size, bias, torch.float32)
+    if block_size not in (32, 64, 128):
+        raise ValueError(f"block_size must be 32, 64, or 128, got {block_size}")
+    if act.dtype not in (torch.float32, torch.bfloat16):
+        raise TypeError(f"act must be float32 or bfloat16, got {act.dtype}")
+    dev = _hip.require_gpu(act, w_hi_fp8, w_lo_fp8, w_hi_scales, w_lo_scales, bias)
+    num_kb = K // block_size
+    e_hi = _block_exps(w_hi_scales, N, num_kb, "w_hi_scales")
+    e_lo = _block_exps(w_lo_scales, N, num_kb, "w_lo_scales")
+    if sparse_threshold > 0.0:
+        w_lo_fp8, e_lo = _lo_threshold(w_lo_fp8, e_lo, sparse_threshold, block_size)
+    w_hi_fp8 = _gemm_operand(w_hi_fp8, "w_hi")
+    w_lo_fp8 = _gemm_operand(w_lo_fp8, "w_lo")
+    if w_hi_fp8.stride(0) != w_lo_fp8.stride(0):
+        w_hi_fp8, w_lo_fp8 = w_hi_fp8.contiguous(), w_lo_fp8.contiguous()
+    es = act.element_size()
+    if act.stride(1) != 1 or (act.stride(0) * es) % 16 != 0 or act.data_ptr() % 16 != 0:
+        act = act.contiguous()
+    out = torch.empty((M, N), dtype=torch.float32, device=dev)
+    act_fp8 = act_scales = None
     if save_side_outputs:
-        return out, act_fp8, act_scales
-    return out, None, None
+        act_fp8 = torch.empty((M, K), dtype=torch.float8_e4m3fn, device=dev)
+        act_scales = torch.empty((num_kb, M), dtype=torch.int8, device=dev)
+    if bias is not None:
+        bias = _bias_f32(bias, N)
+    check(
+        _hip.lib().tcfp_act_quant_block_dual_gemm(
+            ptr(act), _in_dtype(act), act.stride(0), ptr(w_hi_fp8), ptr(w_lo_fp8),
+            w_hi_fp8.stride(0), ptr(e_hi), ptr(e_lo), M, N, K, block_size, ptr(bias), ptr(out),
+            N, ptr(act_fp8), ptr(act_scales), _hip.stream_of(dev),
+        ),
+        "fused_act_quant_dual_gemm_forward",
+    )
+    return out, act_fp8, act_scales
 
 
 def fused_wtquant_block_scaled_dual_gemm_forward(
@@ -1110,6 +1171,15 @@ def fused_wtquant_block_scaled_dual_gemm_forward(
     dev = _hip.require_gpu(act_fp8, weight, act_scales, error_buf, bias)
     num_kb = K // block_size
     e_a = _block_exps(act_scales, M, num_kb, "act_scales")
+    if sparse_threshold > 0.0:
+        # the threshold rule rewrites W_lo between the two launches
+        w_hi, w_lo, s_hi, s_lo = fused_dual_quantize_fp8(
+            weight, block_size, error_buf=error_buf, stochastic_lo=stochastic_lo, seed=seed)
+        out = fused_block_scaled_dual_gemm_forward(
+            act_fp8, w_hi, w_lo, e_a, s_hi, s_lo, block_size, sparse_threshold, bias=bias)
+        if save_w_lo:
+            return out, w_hi, w_lo, s_hi, s_lo
+        return out, w_hi, None, s_hi, None
     out = torch.empty((M, N), dtype=torch.float32, device=dev)
     w_hi = torch.empty((N, K), dtype=torch.float8_e4m3fn, device=dev)
     w_lo = torch.empty((N, K), dtype=torch.float8_e4m3fn, device=dev)

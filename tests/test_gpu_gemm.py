@@ -408,27 +408,136 @@ def test_block_layer_fp8_dgrad_mode(dev):
 
 
 # ------------------------------------------------- fused act-quant (a11)
+# (M, N, K in blocks): ragged rows and columns, a K that ends mid-stage
+# (3 blocks of 32), several stages, and one row
+ACTQ_SHAPES = [(300, 256, 4), (1, 100, 1), (513, 520, 3), (2048, 512, 16), (130, 64, 8)]
+
+
 @pytest.mark.parametrize("bs", [32, 64, 128])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-def test_fused_act_quant_dual_gemm(dev, bs, dtype):
-    """Side outputs bitwise equal to block_quantize_fp8 and the output equal
-    to quant + block dual GEMM (reference tests/test_fused_act_quant_gemm.py
-    :86-144)."""
-    M, N, K_ = 300, 256, 4 * bs
-    g = torch.Generator().manual_seed(bs)
+@pytest.mark.parametrize("M,N,KB", ACTQ_SHAPES)
+def test_fused_act_quant_dual_gemm(dev, bs, dtype, M, N, KB):
+    """One launch: side outputs bitwise equal to block_quantize_fp8 (and the
+    oracle), the output bitwise equal to block quant + block dual GEMM
+    (same codes through the same MFMA order) and within EXACT of the oracle
+    (reference tests/test_fused_act_quant_gemm.py:86-144)."""
+    K_ = KB * bs
+    g = torch.Generator().manual_seed(bs + M + KB)
     x = (torch.randn(M, K_, generator=g) * 3).to(dtype).to(dev)
     w = torch.randn(N, K_, generator=g) * 0.02
+    bias = torch.randn(N, generator=g).to(dev)
     h, l, eh, el = K.fused_dual_quantize_fp8(w.to(dev), bs)
-    out, aq, ea = K.fused_act_quant_dual_gemm_forward(x, h, l, eh, el, bs)
+    names = [n for n in _kernel_names(lambda: K.fused_act_quant_dual_gemm_forward(
+        x, h, l, eh, el, bs, bias=bias)) if not n.startswith("hip")]
+    assert len(names) == 1 and "gemm_nt_dma_kernel" in names[0], names
+    out, aq, ea = K.fused_act_quant_dual_gemm_forward(x, h, l, eh, el, bs, bias=bias)
     aq2, ea2 = K.block_quantize_fp8(x, bs)
     assert torch.equal(aq.view(torch.uint8), aq2.view(torch.uint8)) and torch.equal(ea, ea2)
     codes, exps = oq.block_quantize(x.float().cpu().numpy(), bs)
     assert np.array_equal(u8(aq), codes) and np.array_equal(npy(ea), exps)
+    two = K.fused_block_scaled_dual_gemm_forward(aq2, h, l, ea2, eh, el, bs, bias=bias)
+    assert torch.equal(out, two)
     ref = og.block_dual_gemm_nt(codes, exps, u8(h), u8(l), npy(eh), npy(el), bs)
+    ref = ref + npy(bias).astype(np.float64)
     assert og.rel_fro(npy(out), ref) < EXACT
-    out2, none1, none2 = K.fused_act_quant_dual_gemm_forward(x, h, l, eh, el, bs,
+    out2, none1, none2 = K.fused_act_quant_dual_gemm_forward(x, h, l, eh, el, bs, bias=bias,
                                                              save_side_outputs=False)
     assert none1 is None and none2 is None and torch.equal(out, out2)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_fused_act_quant_special_values_and_strides(dev, dtype):
+    """Blocks that need the clamp (a log2 boundary just above 448 * 2^k,
+    +-inf, NaN), all-zero blocks, and a row-strided activation view."""
+    bs, M, N = 32, 96, 64
+    K_ = 8 * bs
+    g = torch.Generator().manual_seed(7)
+    base = torch.randn(M, 2 * K_, generator=g)
+    x = base[:, :K_]                                 # row stride 2K
+    x[0, :bs] = 448.0 * 2.0 ** 3 * (1 + 2.0 ** -7)  # exponent rule's boundary
+    x[1, 5] = float("inf")
+    x[2, 40] = float("-inf")
+    x[3, 70] = float("nan")
+    x[4, :] = 0.0
+    x[5, 64:96] = 1e-30
+    xv = base.to(dtype).to(dev)[:, :K_]              # a row-strided view on the GPU
+    xv.copy_(x.to(dtype).to(dev))
+    assert xv.stride(0) == 2 * K_
+    w = torch.randn(N, K_, generator=g) * 0.02
+    h, l, eh, el = K.fused_dual_quantize_fp8(w.to(dev), bs)
+    out, aq, ea = K.fused_act_quant_dual_gemm_forward(xv, h, l, eh, el, bs)
+    aq2, ea2 = K.block_quantize_fp8(xv.contiguous(), bs)
+    assert torch.equal(aq.view(torch.uint8), aq2.view(torch.uint8)) and torch.equal(ea, ea2)
+    # the oracle on the finite rows (its exponent of a block holding inf or
+    # NaN is not defined; the two GPU paths share one rule there)
+    fin = [r for r in range(M) if r not in (1, 2, 3)]
+    codes, exps = oq.block_quantize(xv.float().cpu().numpy()[fin], bs)
+    assert np.array_equal(u8(aq)[fin], codes) and np.array_equal(npy(ea)[:, fin], exps)
+    two = K.fused_block_scaled_dual_gemm_forward(aq2, h, l, ea2, eh, el, bs)
+    assert torch.equal(out.nan_to_num(), two.nan_to_num())
+    assert torch.equal(out.isnan(), two.isnan())
+
+
+# ------------------------------------------------- W_lo sparsity (a10, a11, a16)
+@pytest.mark.parametrize("bs", [32, 64, 128])
+def test_block_dual_gemm_all_sentinel_lo_skip(dev, bs):
+    """All W_lo blocks zero under the -128 sentinel (reference
+    tests/test_block_scaling_kernels.py:643-660): the GEMM skips their MFMAs
+    and equals the W_hi-only product, on the small and the large tile."""
+    M, N, K_ = 512, 256, 8 * bs
+    a, ea, h, l, eh, el = make_block_operands(M, N, K_, bs, dev, 5)
+    l0 = torch.zeros_like(l)
+    el0 = torch.full_like(el, -128)
+    ref = og.block_deq64(u8(a), npy(ea), bs) @ og.block_deq64(u8(h), npy(eh), bs).T
+    outs = []
+    try:
+        for pol in ("large", "small"):
+            K.set_gemm_tile_policy(pol)
+            outs.append(K.fused_block_scaled_dual_gemm_forward(a, h, l0, ea, eh, el0, bs))
+    finally:
+        K.set_gemm_tile_policy("auto")
+    for o in outs:
+        assert og.rel_fro(npy(o), ref) < EXACT
+    assert torch.equal(outs[0], outs[1])
+
+
+@pytest.mark.parametrize("bs", [32, 64, 128])
+def test_block_dual_gemm_partial_sentinel(dev, bs):
+    """Odd K-blocks of W_lo under the sentinel with their codes left in place
+    (reference tests/test_block_scaling_kernels.py:662-696): those blocks
+    contribute nothing."""
+    M, N, K_ = 256, 192, 4 * bs
+    a, ea, h, l, eh, el = make_block_operands(M, N, K_, bs, dev, 6)
+    el = el.clone()
+    el[1::2] = -128
+    out = K.fused_block_scaled_dual_gemm_forward(a, h, l, ea, eh, el, bs)
+    ref = og.block_dual_gemm_nt(u8(a), npy(ea), u8(h), u8(l), npy(eh), npy(el), bs)
+    assert og.rel_fro(npy(out), ref) < EXACT
+
+
+@pytest.mark.parametrize("thr_pow", [-40, -12, -9, 0])
+def test_sparse_threshold_rule(dev, thr_pow):
+    """sparse_threshold > 0 drops W_lo per (64-row tile, K-block) as the
+    oracle's restatement of the reference rule does; the three entry points
+    agree."""
+    bs, M, N, K_ = 64, 128, 200, 512
+    g = torch.Generator().manual_seed(8)
+    x = torch.randn(M, K_, generator=g).to(dev)
+    w = (torch.randn(N, K_, generator=g) * 0.02).to(dev)
+    a, ea = K.block_quantize_fp8(x, bs)
+    h, l, eh, el = K.fused_dual_quantize_fp8(w, bs)
+    thr = 2.0 ** thr_pow
+    e_ref = og.lo_threshold_exps(npy(el), thr)
+    ref = og.block_dual_gemm_nt(u8(a), npy(ea), u8(h), u8(l), npy(eh), e_ref, bs)
+    out = K.fused_block_scaled_dual_gemm_forward(a, h, l, ea, eh, el, bs, sparse_threshold=thr)
+    assert og.rel_fro(npy(out), ref) < EXACT
+    out2, aq, _ = K.fused_act_quant_dual_gemm_forward(x, h, l, eh, el, bs, sparse_threshold=thr)
+    assert torch.equal(aq.view(torch.uint8), a.view(torch.uint8))
+    assert torch.equal(out, out2)
+    out3, *_ = K.fused_wtquant_block_scaled_dual_gemm_forward(a, w, ea, bs, sparse_threshold=thr)
+    assert torch.equal(out, out3)
+    n_drop = int((e_ref != npy(el)).sum())
+    print(f"threshold 2^{thr_pow}: {n_drop} of {el.numel()} W_lo blocks dropped")
 
 
 # ------------------------------------------------- block wgrad (a14)

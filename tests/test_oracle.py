@@ -666,3 +666,24 @@ def test_column_sums_close_to_exact_and_exact_on_integers(shape):
     assert np.all(np.abs(oq.column_sums(x) - ref) <= bound)
     xi = rng.integers(-1000, 1000, shape).astype(np.float32)  # every partial exact
     assert np.array_equal(oq.column_sums(xi), xi.astype(np.float64).sum(0).astype(np.float32))
+
+
+def test_lo_threshold_exps_rule():
+    """Closed cases of the reference's W_lo sparsity rule
+    (tcfp/kernels.py:766-776): a tile of 64 rows is dropped for a K-block
+    only when its largest scale is <= the threshold; the sentinel counts as
+    scale 0; a threshold below every scale drops nothing."""
+    from oracle import gemm as og
+
+    e = np.full((2, 130), -10, dtype=np.int8)
+    e[0, 70] = -5          # tile 1 (rows 64..127) of block 0 holds one larger scale
+    e[1, :64] = -128       # tile 0 of block 1: all sentinel
+    out = og.lo_threshold_exps(e, 2.0 ** -8)
+    assert (out[0, :64] == -128).all()            # tile 0, block 0: max 2^-10 <= 2^-8
+    assert (out[0, 64:128] == e[0, 64:128]).all() # kept: 2^-5 > 2^-8
+    assert (out[0, 128:] == -128).all()           # the partial last tile
+    assert (out[1] == -128).all()
+    assert np.array_equal(og.lo_threshold_exps(e, 2.0 ** -20), e)
+    assert (og.lo_threshold_exps(e, 1.0) == -128).all()
+    # equality counts as dropped (max(scale) <= threshold)
+    assert (og.lo_threshold_exps(np.full((1, 64), -3, np.int8), 0.125) == -128).all()
