@@ -255,7 +255,7 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && NS == 2 && BM <= 128 ? 2 : 1))
   // AQ: bf16 activations on the 128 x 64 tile; fp32 ones (twice the bytes
   // per stage in registers) on a 64 x 64 tile
   static_assert(AQ == 0 || (SCALE == 1 && !SPLIT && AF == 0 && NS == 2 && NW == 4 && BN == 64 &&
-                            BM == (AQ == 2 ? 64 : 128)),
+                            (BM == 64 || (BM == 128 && AQ == 1))),
                 "in-kernel activation quantisation: E4M3 block-scaled dual GEMM, 128/64 x 64 tile");
   constexpr int f32_bsh = F32BS;
   constexpr int WM = NW / 2;        // wave rows
@@ -282,7 +282,9 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && NS == 2 && BM <= 128 ? 2 : 1))
   // block of the stage][row] (a block of bs >= 32 columns fills
   // kSK / bs of the four slots)
   constexpr int kExB = AQ ? 2 * (kSK / 32) * BM : 0;
-  __shared__ __align__(16) uint8_t lds[NS * STAGE + 3 * kScB + kExB];
+  // AQ: per-wave scratch of one float per (row, block) segment of a stage
+  constexpr int kAqS = AQ ? NW * (BM / NW) * (kSK >> F32BS) * 4 : 0;
+  __shared__ __align__(16) uint8_t lds[NS * STAGE + 3 * kScB + kExB + kAqS];
 
   const int M = g.M, N = g.N;
   int K = g.K;
@@ -450,60 +452,117 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && NS == 2 && BM <= 128 ? 2 : 1))
   const uint32_t enrec = side ? uint32_t(int64_t(K >> f32_bsh) * M) : 0u;
   const __amdgpu_buffer_rsrc_t ersrc =
       __builtin_amdgcn_make_buffer_rsrc(g.e_out, 0, int(enrec), 0x00020000);
+  // A wave's stage holds ASEG (row, block) segments.  Their maxima go to
+  // the wave's scratch slots; each lane then turns at most two of them into
+  // an exponent (written to the MFMA's exponent slots and e_out) and a
+  // multiplier 2^-e (written back over the maximum), which the segment's
+  // lanes read for the conversion: one exponent evaluation per segment
+  // instead of one per lane.
+  constexpr int NSB = AQ ? kSK >> f32_bsh : 1;              // blocks per stage row
+  constexpr int ASEG = AQ ? ARL * ARPI * NSB : 1;           // segments per wave and stage
+  float* const aslot = reinterpret_cast<float*>(lds + NS * STAGE + 3 * kScB + kExB) + wave * ASEG;
   auto aquant = [&](const uint4* a4, int t) {
     if constexpr (AQ != 0) {
       uint8_t* st = lds + (t & 1) * STAGE;
       int8_t* ex = exs + (t & 1) * (kSK / 32) * BM;
+      const int sb = acol >> f32_bsh;                        // block of this lane's columns
+      // 1. segment maxima (|x| as bits: unsigned order, NaN above inf)
+      uint32_t am[ARL];
+#pragma unroll
+      for (int r = 0; r < ARL; ++r) {
+        const uint32_t w[4] = {a4[r].x, a4[r].y, a4[r].z, a4[r].w};
+        uint32_t a;
+        if constexpr (AQ == 2) {
+          a = umax(umax(absbits(__uint_as_float(w[0])), absbits(__uint_as_float(w[1]))),
+                   umax(absbits(__uint_as_float(w[2])), absbits(__uint_as_float(w[3]))));
+        } else {
+          // bf16 magnitudes, two per word: max of the 16-bit halves
+          typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+          u16x2 m = __builtin_bit_cast(u16x2, w[0] & 0x7FFF7FFFu);
+#pragma unroll
+          for (int q = 1; q < 4; ++q)
+            m = __builtin_elementwise_max(m, __builtin_bit_cast(u16x2, w[q] & 0x7FFF7FFFu));
+          a = uint32_t(m[0] > m[1] ? m[0] : m[1]) << 16;
+        }
+        am[r] = seg_umax<AL>(a);
+        aslot[(r * ARPI + lane / ALPR) * NSB + sb] = __uint_as_float(am[r]);
+      }
+      // 2. one exponent per segment (lanes past ASEG repeat a segment)
+#pragma unroll
+      for (int i = 0; i < (ASEG + 63) / 64; ++i) {
+        const int sid = (lane + 64 * i) % ASEG;
+        const int e = block_exponent(aslot[sid], kE4M3Max);
+        aslot[sid] = exp2i(-e);
+        const int wr = sid / NSB, b = sid % NSB;
+        const int row = wave * ARPI + wr % ARPI + (wr / ARPI) * NW * ARPI;
+        ex[b * BM + row] = int8_t(e);
+        if (side) {
+          const int gk = t * kSK + (b << f32_bsh);
+          const uint32_t eoff = gk < K && row < arows
+                                    ? uint32_t(gk >> f32_bsh) * uint32_t(M) + uint32_t(m0 + row)
+                                    : kOob;
+          __builtin_amdgcn_raw_buffer_store_b8(uint8_t(e), ersrc, eoff, 0, 0);
+        }
+      }
+      // 3. codes
 #pragma unroll
       for (int r = 0; r < ARL; ++r) {
         const int row = arow + r * NW * ARPI;
+        const float mul = aslot[(r * ARPI + lane / ALPR) * NSB + sb];
         const uint32_t w[4] = {a4[r].x, a4[r].y, a4[r].z, a4[r].w};
-        float v[AVEC];
-        if constexpr (AQ == 2) {
-#pragma unroll
-          for (int j = 0; j < 4; ++j) v[j] = __uint_as_float(w[j]);
-        } else {
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            v[2 * j] = __uint_as_float(w[j] << 16);
-            v[2 * j + 1] = __uint_as_float(w[j] & 0xFFFF0000u);
-          }
-        }
-        uint32_t a = 0;
-#pragma unroll
-        for (int j = 0; j < AVEC; ++j) a = umax(a, absbits(v[j]));
-        a = seg_umax<AL>(a);
-        const float amax = __uint_as_float(a);
-        const int e = block_exponent(amax, kE4M3Max);
-        const float mul = exp2i(-e);
-#pragma unroll
-        for (int j = 0; j < AVEC; ++j) v[j] = v[j] * mul;
         // |x| <= amax, so the clamp changes nothing unless amax * 2^-e
         // exceeds 448 (or is NaN) somewhere in the wave
-        if (__builtin_amdgcn_ballot_w64(!(amax * mul <= kE4M3Max)) != 0) {
+        const bool clamp = __builtin_amdgcn_ballot_w64(!(__uint_as_float(am[r]) * mul <= kE4M3Max)) != 0;
+        uint32_t c[AVEC / 4];
+        if (AQ == 1 && !clamp) {
+          // v_cvt_scalef32_pk_fp8_bf16 with a power-of-two scale 2^e is
+          // RNE(x * 2^-e) for every in-range bf16 x (checked on the GPU
+          // over all bf16 inputs and exponents; it yields NaN, not 448, out
+          // of range -- those waves take the clamping branch)
+          typedef short v2s __attribute__((ext_vector_type(2)));
+          typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
+          // 2^e from 2^-e: both normal for every finite input (-126 <= e <= 120)
+          const float sc = __uint_as_float(0x7F000000u - __float_as_uint(mul));
 #pragma unroll
-          for (int j = 0; j < AVEC; ++j) v[j] = clampf(v[j], kE4M3Max);
+          for (int q = 0; q < AVEC / 4; ++q) {
+            v2s r2 = {0, 0};
+            r2 = __builtin_amdgcn_cvt_scalef32_pk_fp8_bf16(r2, __builtin_bit_cast(v2bf, w[2 * q]), sc, false);
+            r2 = __builtin_amdgcn_cvt_scalef32_pk_fp8_bf16(r2, __builtin_bit_cast(v2bf, w[2 * q + 1]), sc, true);
+            c[q] = __builtin_bit_cast(uint32_t, r2);
+          }
+        } else {
+          float v[AVEC];
+          if constexpr (AQ == 2) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) v[q] = __uint_as_float(w[q]);
+          } else {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              v[2 * q] = __uint_as_float(w[q] << 16);
+              v[2 * q + 1] = __uint_as_float(w[q] & 0xFFFF0000u);
+            }
+          }
+#pragma unroll
+          for (int q = 0; q < AVEC; ++q) v[q] = v[q] * mul;
+          if (clamp) {
+#pragma unroll
+            for (int q = 0; q < AVEC; ++q) v[q] = clampf(v[q], kE4M3Max);
+          }
+#pragma unroll
+          for (int q = 0; q < AVEC / 4; ++q)
+            c[q] = cvt4_fp8<TCFP_FP8_E4M3>(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
         }
         const int off = row * kRowB + ((((acol >> 4) ^ swz(row))) << 4) + (acol & 15);
         const int gk = t * kSK + acol;
-        const bool kin = gk < K && row < arows;
-        const uint32_t qoff = kin ? uint32_t(row) * uint32_t(K) + uint32_t(gk) : kOob;
+        const uint32_t qoff =
+            gk < K && row < arows ? uint32_t(row) * uint32_t(K) + uint32_t(gk) : kOob;
         if constexpr (AQ == 2) {
-          const uint32_t c = cvt4_fp8<TCFP_FP8_E4M3>(v[0], v[1], v[2], v[3]);
-          *reinterpret_cast<uint32_t*>(st + off) = c;
-          if (side) __builtin_amdgcn_raw_buffer_store_b32(c, qrsrc, qoff, 0, 0);
+          *reinterpret_cast<uint32_t*>(st + off) = c[0];
+          if (side) __builtin_amdgcn_raw_buffer_store_b32(c[0], qrsrc, qoff, 0, 0);
         } else {
-          const uint2 c = make_uint2(cvt4_fp8<TCFP_FP8_E4M3>(v[0], v[1], v[2], v[3]),
-                                     cvt4_fp8<TCFP_FP8_E4M3>(v[4], v[5], v[6], v[7]));
-          *reinterpret_cast<uint2*>(st + off) = c;
-          if (side) __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(v2u, c), qrsrc, qoff, 0, 0);
-        }
-        // every lane of the segment writes the (same) exponent: no branch
-        ex[(acol >> f32_bsh) * BM + row] = int8_t(e);
-        if (side) {
-          const uint32_t eoff =
-              kin ? uint32_t(gk >> f32_bsh) * uint32_t(M) + uint32_t(m0 + row) : kOob;
-          __builtin_amdgcn_raw_buffer_store_b8(uint8_t(e), ersrc, eoff, 0, 0);
+          *reinterpret_cast<uint2*>(st + off) = make_uint2(c[0], c[1]);
+          if (side)
+            __builtin_amdgcn_raw_buffer_store_b64(v2u{c[0], c[1]}, qrsrc, qoff, 0, 0);
         }
       }
     }
@@ -1660,12 +1719,19 @@ namespace {
 // activation block-quantised inside (AQ 1 bf16 / 2 fp32, BSH = log2 block).
 template <int AQ, int BSH>
 int launch_actq(GemmArgs ga, hipStream_t st) {
-  constexpr int BMv = AQ == 2 ? 64 : 128;
+  // fp32 activations always, bf16 ones when 128-row tiles would leave CUs
+  // idle: 64-row tiles (twice the workgroups, half the quantisation per
+  // workgroup and stage)
+  const bool rows64 = AQ == 2 || int64_t((ga.M + 127) / 128) * ((ga.N + 63) / 64) < 2 * num_cus();
+  const int BMv = rows64 ? 64 : 128;
   ga.tiles_m = (ga.M + BMv - 1) / BMv;
   ga.tiles_n = (ga.N + 63) / 64;
   if (!grid_x_fits(int64_t(ga.tiles_m) * ga.tiles_n, 256)) return TCFP_ERR_SHAPE;
   const dim3 grid(unsigned(ga.tiles_m) * unsigned(ga.tiles_n));
-  gemm_nt_dma_kernel<0, 0, false, float, 4, BMv, 64, 1, 2, BSH, AQ><<<grid, 256, 0, st>>>(ga);
+  if (rows64)
+    gemm_nt_dma_kernel<0, 0, false, float, 4, 64, 64, 1, 2, BSH, AQ><<<grid, 256, 0, st>>>(ga);
+  else if constexpr (AQ == 1)
+    gemm_nt_dma_kernel<0, 0, false, float, 4, 128, 64, 1, 2, BSH, AQ><<<grid, 256, 0, st>>>(ga);
   return hipGetLastError() == hipSuccess ? TCFP_OK : TCFP_ERR_HIP;
 }
 
