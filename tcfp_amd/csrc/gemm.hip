@@ -516,9 +516,10 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && NS == 2 && BM <= 128 ? 2 : 1))
         uint32_t c[AVEC / 4];
         if (AQ == 1 && !clamp) {
           // v_cvt_scalef32_pk_fp8_bf16 with a power-of-two scale 2^e is
-          // RNE(x * 2^-e) for every in-range bf16 x (checked on the GPU
-          // over all bf16 inputs and exponents; it yields NaN, not 448, out
-          // of range -- those waves take the clamping branch)
+          // RNE(x * 2^-e) for every in-range bf16 x (a GPU test runs every
+          // finite bf16 at every exponent the rule yields against the
+          // multiply-clamp-convert path); out of range it yields NaN, not
+          // 448 -- waves holding such a block take the clamping branch
           typedef short v2s __attribute__((ext_vector_type(2)));
           typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
           // 2^e from 2^-e: both normal for every finite input (-126 <= e <= 120)

@@ -478,6 +478,36 @@ def test_fused_act_quant_special_values_and_strides(dev, dtype):
     assert torch.equal(out.isnan(), two.isnan())
 
 
+def test_fused_act_quant_every_bf16_at_every_exponent(dev):
+    """The fused kernel's bf16 conversion (the scaled hardware convert on
+    waves that need no clamp) against block_quantize_fp8's multiply-clamp-
+    convert: every finite bf16 value x appears in a 32-element block whose
+    maximum 448 * 2^e fixes the exponent e, for every e the rule can produce
+    from finite inputs (-48 .. 120: the 1e-12 floor on the block maximum
+    bounds it below) with |x| <= 448 * 2^e."""
+    allb = (np.arange(65536, dtype=np.uint32) << 16).view(np.float32)
+    allb = allb[np.isfinite(allb)]
+    rows = []
+    for e in range(-48, 121):
+        # (448 * 2^120 overflows; the largest finite bf16 has exponent 120)
+        top = np.float32(448.0) * np.float32(2.0) ** e if e < 120 else allb.max()
+        v = allb[np.abs(allb) <= top]
+        v = np.concatenate([v, np.zeros((-len(v)) % 31, np.float32)]).reshape(-1, 31)
+        rows.append(np.concatenate([np.full((len(v), 1), top, np.float32), v], axis=1))
+    x = torch.from_numpy(np.concatenate(rows)).to(torch.bfloat16).to(dev)
+    assert x.float().abs().amax().isfinite()
+    w = torch.randn(64, 32, generator=torch.Generator().manual_seed(3)) * 0.02
+    h, l, eh, el = K.fused_dual_quantize_fp8(w.to(dev), 32)
+    out, aq, ea = K.fused_act_quant_dual_gemm_forward(x, h, l, eh, el, 32)
+    aq2, ea2 = K.block_quantize_fp8(x, 32)
+    assert torch.equal(ea, ea2)
+    assert torch.equal(aq.view(torch.uint8), aq2.view(torch.uint8))
+    e_expected = torch.cat([torch.full((len(r),), e, dtype=torch.int8)
+                            for e, r in zip(range(-48, 121), rows)]).to(dev)
+    assert torch.equal(ea[0], e_expected)
+    print(f"{x.shape[0]} blocks of 32, exponents -48..120: codes and exponents identical")
+
+
 # ------------------------------------------------- W_lo sparsity (a10, a11, a16)
 @pytest.mark.parametrize("bs", [32, 64, 128])
 def test_block_dual_gemm_all_sentinel_lo_skip(dev, bs):
