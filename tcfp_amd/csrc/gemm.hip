@@ -169,6 +169,17 @@ TCFP_DEV void interleave_mfma_lds() {
   }
 }
 
+// Unscaled FP8 MFMA (per-tensor scales are applied in the epilogue).  The
+// compiler has no separate builtin for v_mfma_f32_32x32x64_f8f6f4: it selects
+// that instruction for the scaled builtin when both scale operands are the
+// literal 0, and the scaled form (an extra instruction word and two scale
+// registers) otherwise.  The GEMM tests would see a scaled form with code 0
+// (2^-127 per operand) at once: every product would vanish.
+template <int BF, int AF>
+TCFP_DEV v16f mfma_plain(const v8i& a, const v8i& b, const v16f& c) {
+  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, BF, AF, 0, 0, 0, 0);
+}
+
 // E8M0 code of a block exponent (bias 127; -128 and anything below -127
 // map to code 0 = 2^-127).
 TCFP_DEV uint32_t e8m0_of(int e) { return e < -127 ? 0u : uint32_t(e + 127); }
@@ -692,8 +703,7 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && NS == 2 && BM <= 128 ? 2 : 1))
       c = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
           f[q], f[NF + i], c, BF, AF, 0, int(scv[2 * q + h]), 0, int(scv[2 * (NF + i) + h]));
     } else {
-      c = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f[q], f[NF + i], c, BF, AF, 0, 127,
-                                                           0, 127);
+      c = mfma_plain<BF, AF>(f[q], f[NF + i], c);
     }
   };
   // One sub-step (h) of MFMAs; `sc` holds the stage's E8M0 scales.  LO
@@ -1141,8 +1151,7 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persist_kernel(GemmArgs g) {
       if (idx < lo || idx >= hi) continue;
       const int i = idx / NF, q = idx % NF;
       v16f& c = acc[q / NB][q % NB][i];
-      c = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f[q], f[NF + i], c, BF, AF, 0, 127, 0,
-                                                           127);
+      c = mfma_plain<BF, AF>(f[q], f[NF + i], c);
     }
   };
   // The MFMAs of (fragment, m-block) pairs [lo, hi) stay where they are:
