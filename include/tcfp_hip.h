@@ -209,6 +209,14 @@ int tcfp_dual_gemm_dgelu_quantize_colsum(const uint8_t* a, int a_fmt, int64_t ld
                                          float* col_sum, void* workspace, void* colsum_ws,
                                          size_t colsum_ws_bytes, void* stream);
 
+/* Tuning switch of tcfp_dual_quantize_per_tensor (and its workspace-free
+ * variant) without delayed or NF-aware scaling, on tensors of 2^23 elements
+ * or more (no counterpart in the reference): on = 1 (default) keeps the
+ * candidates for the residual amax during the amax pass and skips the full
+ * residual pass whenever they decide it; on = 0 always runs the full pass.
+ * Results do not depend on it. */
+int tcfp_dual_quantize_set_candidates(int on);
+
 /* Per-tensor dual quantisation with optional error feedback.
  * Three launches (amax; W_hi + residual amax; W_lo + EF + transposed
  * codes), each re-reading W and EF.

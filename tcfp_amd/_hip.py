@@ -121,6 +121,7 @@ _SIGNATURES = {
                                   _c_void_p, _c_void_p, ctypes.c_size_t, _c_void_p],
     "tcfp_block_wgrad_presplit_workspace_bytes": [_i64, _i64, _i64],
     "tcfp_gemm_set_tile_policy": [_i32],
+    "tcfp_dual_quantize_set_candidates": [_i32],
     "tcfp_transpose_u8": [_c_void_p, _i64, _i64, _c_void_p, _c_void_p],
     "tcfp_selftest_fp8_cvt": [_u32, _u32, _i32, _c_void_p, _c_void_p],
     "tcfp_selftest_sr_block": [_u32, _u32, ctypes.c_float, _c_void_p, _c_void_p],

@@ -383,6 +383,106 @@ __global__ __launch_bounds__(kThreads) void amax_part_kernel(const InT* __restri
   }
 }
 
+// Pass 1 of the dual quantisation under the amax rule on large tensors: the
+// partial max |v| of v = x (+ ef) as amax_part_kernel, and also the
+// "candidates" for the residual amax: every v with |v| >= amax * 4/7 (and
+// some smaller ones) is stored into this workgroup's region of `vals` (cap
+// floats), their number into cnt[blockIdx.x] (more than cap: overflow).
+// The workgroup takes its vectors in rounds of kCandCh per thread; after
+// each round its running maximum M is reduced and the round's values with
+// |v| >= 0.5714 M are stored (M <= amax and 0.5714 < 4/7, so nothing with
+// |v| >= amax * 4/7 is missed), placed by a wave scan of the per-lane
+// counts and one LDS atomic per wave.
+struct CandOut {
+  float* vals;    // region of workgroup b: vals + b * cap
+  uint32_t* cnt;  // per-workgroup count
+  int cap;
+};
+constexpr int kCandCh = 4;
+template <typename InT, bool HAS_EF>
+__global__ __launch_bounds__(kThreads) void amax_cand_kernel(const InT* __restrict__ x,
+                                                             const float* __restrict__ ef,
+                                                             int64_t n, uint32_t* __restrict__ part,
+                                                             CandOut co) {
+  __shared__ uint32_t red[kThreads / 64];
+  __shared__ uint32_t ncand;
+  if (threadIdx.x == 0) ncand = 0;
+  float* const region = co.vals + int64_t(blockIdx.x) * co.cap;
+  const int lane = threadIdx.x & 63;
+  uint32_t mw = 0;  // the workgroup's running maximum (uniform)
+  // store v[j] (j < nv) with |v| >= 0.5714 * the running maximum
+  auto emit = [&](const float* v, int nv) {
+    const float thr = __uint_as_float(mw) * 0.5714f;
+    uint64_t mask = 0;
+    for (int j = 0; j < nv; ++j) mask |= uint64_t(fabsf(v[j]) >= thr) << j;
+    const int c = __builtin_popcountll(mask);
+    int incl = c;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int t = __shfl_up(incl, d, 64);
+      if (lane >= d) incl += t;
+    }
+    const int tot = __shfl(incl, 63, 64);
+    uint32_t base = 0;
+    if (lane == 0 && tot > 0) base = atomicAdd(&ncand, uint32_t(tot));
+    base = uint32_t(__shfl(int(base), 0, 64));
+    uint32_t pos = base + uint32_t(incl - c);
+    while (mask) {
+      const int j = __builtin_ctzll(mask);
+      mask &= mask - 1;
+      if (pos < uint32_t(co.cap)) region[pos] = v[j];
+      ++pos;
+    }
+  };
+  const int64_t nvec = n >> 3;
+  const int64_t stride = int64_t(gridDim.x) * kThreads;
+  const int64_t i0 = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+  const int64_t w0 = int64_t(blockIdx.x) * kThreads;  // the workgroup's first vector
+  // (workgroup-uniform trip count: block_umax_all synchronises)
+  for (int64_t r = 0; w0 + r * kCandCh * stride < nvec; ++r) {
+    float W[kCandCh][8], v[kCandCh][8];
+    int nv = 0;
+    uint32_t mt = 0;
+#pragma unroll
+    for (int u = 0; u < kCandCh; ++u) {
+      const int64_t iv = i0 + (r * kCandCh + u) * stride;
+      if (iv < nvec) {
+        load_w8<InT, HAS_EF>(x, ef, iv, W[u], v[u]);
+        nv = 8 * (u + 1);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[u][j] = 0.0f;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kCandCh; ++u)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) mt = umax(mt, absbits(v[u][j]));
+    mw = umax(mw, block_umax_all(mt, red));
+    emit(&v[0][0], nv);
+    __syncthreads();  // red is reused by the next round's reduction
+  }
+  // the last n % 8 elements (workgroup 0)
+  if (blockIdx.x == 0) {
+    const int64_t t = nvec * 8 + threadIdx.x;
+    float v = 0.0f;
+    uint32_t mt = 0;
+    const bool live = t < n;
+    if (live) {
+      v = load1(x + t);
+      if constexpr (HAS_EF) v = v + ef[t];
+      mt = absbits(v);
+    }
+    mw = umax(mw, block_umax_all(mt, red));
+    emit(&v, live ? 1 : 0);
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    part[blockIdx.x] = mw;
+    co.cnt[blockIdx.x] = ncand;
+  }
+}
+
 // ---- GELU producers ---------------------------------------------------------
 // gelu_f32 / gelu_bwd_f32 (common.h) evaluate torch's GELU bit for bit.
 
@@ -930,13 +1030,65 @@ TCFP_DEV uint32_t hi_code1(float c, int64_t t, bool sr, uint32_t k0, uint32_t k1
 // Pass 1 is amax_part_kernel<InT, HAS_EF, STATS> (partials a, and the sums
 // of NF-aware scaling).
 
+// The residual amax found among pass 1's candidates is the tensor's when
+// every element left out provably has a smaller residual.  Those elements
+// have |v| < amax * 4/7, so v * s_hi < 256 (1 + 2^-22) rounds to a code of
+// at most 256 with an error of at most 8 (E4M3 spacing 16 in [128, 256);
+// just above 256 the error is a few 2^-22), and the computed residual
+// v - code * inv_hi stays below 8.00005 * inv_hi (the roundings of s_hi,
+// inv_hi, the product and the difference add a few 2^-24).  So the candidates decide when their maximum exceeds
+// 8.001 * inv_hi, no workgroup overflowed its region (its partial is
+// 0xFFFFFFFF, a NaN, which no comparison passes) and the amax is finite.
+TCFP_DEV bool cand_decisive(const uint32_t* pa, int ga, const uint32_t* pb2, int gc,
+                            float inv_hi, uint32_t* red, uint32_t* red2) {
+  const uint32_t a = __float_as_uint(reduce_parts(pa, ga, red));
+  const float r = reduce_parts(pb2, gc, red2);
+  return a < 0x7F800000u && r > 8.001f * inv_hi;
+}
+
+// Pass 2 over the candidates only: workgroup b reduces the residuals of
+// the values in regions b, b + G, ... (the arithmetic of dualq_hi_kernel)
+// into pb2[b], or 0xFFFFFFFF when one of them overflowed.  Workgroup 0
+// publishes inv_hi and the W_hi target as dualq_hi_kernel does.
+__global__ __launch_bounds__(kThreads) void cand_resid_kernel(
+    const float* __restrict__ vals, const uint32_t* __restrict__ cnt, int cap,
+    const uint32_t* __restrict__ pa, int ga, uint32_t* __restrict__ pb2, float* inv_hi_out,
+    float* tgt_out) {
+  __shared__ uint32_t red[kThreads / 64];
+  __shared__ uint32_t red2[kThreads / 64];
+  const float tgt = clamp_min_nan(reduce_parts(pa, ga, red), 1e-12f);
+  float s_hi, inv_hi;
+  scale_of(tgt, kE4M3Max, &s_hi, &inv_hi);
+  if (blockIdx.x == 0 && threadIdx.x == 0) {
+    *inv_hi_out = inv_hi;
+    *tgt_out = tgt;
+  }
+  bool ok = true;
+  uint32_t m = 0;
+  for (int b = blockIdx.x; b < ga; b += gridDim.x) {
+    const uint32_t c = cnt[b];
+    if (c > uint32_t(cap)) {
+      ok = false;
+      continue;
+    }
+    const float* v = vals + int64_t(b) * cap;
+    for (uint32_t k = threadIdx.x; k < c; k += kThreads) {
+      const float x = v[k];
+      const uint32_t code = encode1<TCFP_FP8_E4M3>(clampf(x * s_hi, kE4M3Max));
+      m = umax(m, absbits(x - e4m3_to_f32(code) * inv_hi));
+    }
+  }
+  m = block_umax_all(m, red2);
+  if (threadIdx.x == 0) pb2[blockIdx.x] = ok ? m : 0xFFFFFFFFu;
+}
+
 // Pass 2: W_hi codes and the partial max |residual| (partials b).
 template <typename InT, bool HAS_EF>
 __global__ __launch_bounds__(kThreads) void dualq_hi_kernel(
     const InT* __restrict__ w, const float* __restrict__ ef, int64_t n,
     const uint32_t* __restrict__ pa, int ga, uint8_t* __restrict__ hi, uint32_t* __restrict__ pb,
     float* inv_hi_out, Delayed dl, HiRule hr, uint32_t k0, uint32_t k1, uint32_t o0,
-    uint32_t o1, float* tgt_out) {
+    uint32_t o1, float* tgt_out, const uint32_t* __restrict__ cand_b2 = nullptr, int gc = 0) {
   __shared__ uint32_t red[kThreads / 64];
   __shared__ uint32_t red2[kThreads / 64];
   __shared__ double rd[2 * (kThreads / 64)];
@@ -949,6 +1101,9 @@ __global__ __launch_bounds__(kThreads) void dualq_hi_kernel(
       *tgt_out = tgt;
     }
   }
+  // after a candidate pass (which then leaves W_hi to pass 3): nothing to
+  // do when the candidates decided the residual amax
+  if (cand_b2 && cand_decisive(pa, ga, cand_b2, gc, inv_hi, red, red2)) return;
   const bool sr = hr.sr != 0;
   uint32_t m = 0;
   const int64_t nvec = n >> 3;
@@ -960,7 +1115,7 @@ __global__ __launch_bounds__(kThreads) void dualq_hi_kernel(
     const uint2 code = sr ? make_uint2(hi_sr4(c, i * 8, k0, k1, o0, o1),
                                        hi_sr4(c + 4, i * 8 + 4, k0, k1, o0, o1))
                           : encode8<TCFP_FP8_E4M3>(c);
-    *reinterpret_cast<uint2*>(hi + i * 8) = code;
+    if (hi) *reinterpret_cast<uint2*>(hi + i * 8) = code;
 #pragma unroll
     for (int j = 0; j < 8; ++j) m = umax(m, absbits(v[j] - e4m3_to_f32(byte_of(code, j)) * inv_hi));
   };
@@ -987,7 +1142,7 @@ __global__ __launch_bounds__(kThreads) void dualq_hi_kernel(
     float v = load1(w + t);
     if constexpr (HAS_EF) v = v + ef[t];
     const uint32_t code = hi_code1(clampf(v * s_hi, kE4M3Max), t, sr, k0, k1, o0, o1);
-    hi[t] = uint8_t(code);
+    if (hi) hi[t] = uint8_t(code);
     m = umax(m, absbits(v - e4m3_to_f32(code) * inv_hi));
   }
   m = block_umax_all(m, red2);
@@ -1041,11 +1196,18 @@ TCFP_DEV void dual_codes4(const float W[4], const float v[4], const DualScales& 
 }
 
 // `tgt_in`: the W_hi target the W_hi pass published (null: reduce it here).
+// `pb2` (after a candidate pass): the gc candidates' residual partials,
+// used in place of pb when they decide the residual amax.
 TCFP_DEV DualScales dual_scales(const HiRule& hr, const float* tgt_in, const uint32_t* pa, int ga,
                                 const uint32_t* pb, int gb, float* inv_lo_out, uint32_t* red,
-                                uint32_t* red2, double* rd) {
+                                uint32_t* red2, double* rd, const uint32_t* pb2 = nullptr,
+                                int gc = 0) {
   DualScales sc;
   scale_of(tgt_in ? *tgt_in : hi_target(hr, pa, ga, red, rd), kE4M3Max, &sc.s_hi, &sc.inv_hi);
+  if (pb2 && cand_decisive(pa, ga, pb2, gc, sc.inv_hi, red, red2)) {
+    pb = pb2;
+    gb = gc;
+  }
   sc.s_lo = consumer_scale(nullptr, pb, gb, false, kE4M3Max, nullptr, inv_lo_out, red2);
   sc.inv_lo = __fdiv_rn(1.0f, sc.s_lo);
   return sc;
@@ -1088,14 +1250,14 @@ __global__ __launch_bounds__(kThreads) void dualq_lo_kernel(
     const InT* __restrict__ w, float* __restrict__ ef, int64_t n, const uint32_t* __restrict__ pa,
     int ga, const uint32_t* __restrict__ pb, int gb, uint8_t* __restrict__ lo, float* inv_lo_out,
     uint32_t k0, uint32_t k1, uint32_t off0, uint32_t off1, Delayed dl, float* inv_hi_out,
-    uint8_t* __restrict__ hi, HiRule hr, const float* tgt_in) {
+    uint8_t* __restrict__ hi, HiRule hr, const float* tgt_in, const uint32_t* pb2, int gc) {
   __shared__ uint32_t red[kThreads / 64];
   __shared__ uint32_t red2[kThreads / 64];
   __shared__ double rd[2 * (kThreads / 64)];
   const DualScales sc =
       dl.on ? dual_scales_delayed(dl, hr, tgt_in, pa, ga, pb, gb, inv_hi_out, inv_lo_out, red,
                                   red2, rd)
-            : dual_scales(hr, tgt_in, pa, ga, pb, gb, inv_lo_out, red, red2, rd);
+            : dual_scales(hr, tgt_in, pa, ga, pb, gb, inv_lo_out, red, red2, rd, pb2, gc);
   const bool srh = hr.sr != 0;
   const int64_t nvec = n >> 3;
   const int64_t stride = int64_t(gridDim.x) * kThreads;
@@ -1151,7 +1313,8 @@ __global__ __launch_bounds__(kThreads) void dualq_lo_t_kernel(
     const uint32_t* __restrict__ pa, int ga, const uint32_t* __restrict__ pb, int gb,
     uint8_t* __restrict__ lo, float* inv_lo_out, uint8_t* __restrict__ hi_t,
     uint8_t* __restrict__ lo_t, uint32_t k0, uint32_t k1, uint32_t off0, uint32_t off1,
-    Delayed dl, float* inv_hi_out, uint8_t* __restrict__ hi, HiRule hr, const float* tgt_in) {
+    Delayed dl, float* inv_hi_out, uint8_t* __restrict__ hi, HiRule hr, const float* tgt_in,
+    const uint32_t* pb2, int gc) {
   using TL = TileLoad<InT>;
   constexpr int VEC = TL::VEC;
   __shared__ uint32_t red[kThreads / 64];
@@ -1162,7 +1325,7 @@ __global__ __launch_bounds__(kThreads) void dualq_lo_t_kernel(
   const DualScales sc =
       dl.on ? dual_scales_delayed(dl, hr, tgt_in, pa, ga, pb, gb, inv_hi_out, inv_lo_out, red,
                                   red2, rd)
-            : dual_scales(hr, tgt_in, pa, ga, pb, gb, inv_lo_out, red, red2, rd);
+            : dual_scales(hr, tgt_in, pa, ga, pb, gb, inv_lo_out, red, red2, rd, pb2, gc);
   const bool srh = hr.sr != 0;
   const TileGeom tg(cols);
   const int tc = (threadIdx.x % TL::TPR) * VEC;
@@ -2252,6 +2415,10 @@ int tcfp_gelu_backward_quantize_per_tensor_colsum(const float* dy, const float* 
 
 namespace {
 
+// Candidate pass of the per-tensor dual quantisation (set by
+// tcfp_dual_quantize_set_candidates; on by default).
+int g_cand_on = 1;
+
 int dual_quantize_impl(const void* w, int w_dtype, int64_t n, int64_t k, float* ef,
                        int update_ef, int stochastic_lo, uint64_t seed, uint64_t offset,
                        uint8_t* w_hi, uint8_t* w_lo, float* inv_hi, float* inv_lo,
@@ -2290,19 +2457,34 @@ int dual_quantize_impl(const void* w, int w_dtype, int64_t n, int64_t k, float* 
   // Delayed scaling without validation predicts the residual amax: pass 2
   // (W_hi codes + residual amax) is skipped and pass 3 writes W_hi too.
   const bool two_pass = dl.on && !dl.validate;
-  uint8_t* hi3 = two_pass ? w_hi : nullptr;
+  // The amax rule on a large tensor: pass 1 also keeps the candidates for
+  // the residual amax in W_lo's buffer (one region of `cap` floats per
+  // workgroup; W_lo is written last), a pass over them finds the residual
+  // amax, and the full residual pass exits at once when they decide it
+  // (cand_decisive); pass 3 then writes W_hi.
+  const bool cand = g_cand_on && !nf && !dl.on && total >= (int64_t(1) << 23);
+  const int cap = cand ? int(std::min<int64_t>(total / ga / 4, INT32_MAX)) : 0;
+  // the candidate pass runs one workgroup per region, the full residual
+  // pass behind it one per CU (it only does work when the candidates do not
+  // decide); pass 3 reads gc or gbx partials
+  const int gc = cand ? ga : 0;
+  const int gbx = cand ? num_cu() : gb;
+  uint32_t* const cand_cnt = reinterpret_cast<uint32_t*>(ws->s2);
+  uint32_t* const cand_b2 = reinterpret_cast<uint32_t*>(ws->s1);
+  const uint32_t* pb2 = cand ? cand_b2 : nullptr;
+  uint8_t* hi3 = (two_pass || cand) ? w_hi : nullptr;
   // the residual pass takes the W_hi target from the W_hi pass when it ran
   const float* tgt3 = two_pass ? nullptr : &ws->hi_tgt;
 #define TCFP_LO(T, EF, UP, SR)                                                                  \
   do {                                                                                          \
     if (tiled)                                                                                  \
       dualq_lo_t_kernel<T, EF, UP, SR><<<unsigned(tiles), kThreads, 0, st>>>(                   \
-          wp, ef, n, k, ws->a, ga, ws->b, gb, w_lo, inv_lo, w_hi_t, w_lo_t, k0, k1, o0, o1, dl,  \
-          inv_hi, hi3, hr, tgt3);                                                               \
+          wp, ef, n, k, ws->a, ga, ws->b, gbx, w_lo, inv_lo, w_hi_t, w_lo_t, k0, k1, o0, o1,     \
+          dl, inv_hi, hi3, hr, tgt3, pb2, gc);                                                  \
     else                                                                                        \
-      dualq_lo_kernel<T, EF, UP, SR><<<gq, kThreads, 0, st>>>(wp, ef, total, ws->a, ga, ws->b, \
-                                                              gb, w_lo, inv_lo, k0, k1, o0, o1, \
-                                                              dl, inv_hi, hi3, hr, tgt3);       \
+      dualq_lo_kernel<T, EF, UP, SR><<<gq, kThreads, 0, st>>>(                                  \
+          wp, ef, total, ws->a, ga, ws->b, gbx, w_lo, inv_lo, k0, k1, o0, o1, dl, inv_hi, hi3,   \
+          hr, tgt3, pb2, gc);                                                                   \
   } while (0)
 #define TCFP_DQ(T, EF)                                                                          \
   do {                                                                                          \
@@ -2310,13 +2492,21 @@ int dual_quantize_impl(const void* w, int w_dtype, int64_t n, int64_t k, float* 
     if (nf)                                                                                     \
       amax_part_kernel<T, EF, true><<<ga, kThreads, 0, st>>>(wp, ef, total, ws->a, ws->s1,     \
                                                              ws->s2);                           \
+    else if (cand)                                                                              \
+      amax_cand_kernel<T, EF><<<ga, kThreads, 0, st>>>(                                         \
+          wp, ef, total, ws->a, CandOut{reinterpret_cast<float*>(w_lo), cand_cnt, cap});        \
     else                                                                                        \
       amax_part_kernel<T, EF, false><<<ga, kThreads, 0, st>>>(wp, ef, total, ws->a, nullptr,   \
                                                               nullptr);                         \
+    if (cand)                                                                                   \
+      cand_resid_kernel<<<gc, kThreads, 0, st>>>(reinterpret_cast<const float*>(w_lo),         \
+                                                 cand_cnt, cap, ws->a, ga, cand_b2, inv_hi,     \
+                                                 &ws->hi_tgt);                                  \
     if (!two_pass)                                                                              \
-      dualq_hi_kernel<T, EF><<<gb, kThreads, 0, st>>>(wp, ef, total, ws->a, ga, w_hi, ws->b,   \
-                                                      inv_hi, dl, hr, k0, k1, o0, o1,           \
-                                                      &ws->hi_tgt);                             \
+      dualq_hi_kernel<T, EF><<<gbx, kThreads, 0, st>>>(wp, ef, total, ws->a, ga,               \
+                                                       cand ? nullptr : w_hi, ws->b, inv_hi,   \
+                                                       dl, hr, k0, k1, o0, o1, &ws->hi_tgt,    \
+                                                       pb2, gc);                               \
     if (stochastic_lo) {                                                                        \
       if (upd) TCFP_LO(T, EF, EF, true); else TCFP_LO(T, EF, false, true);                      \
     } else {                                                                                    \
@@ -2341,6 +2531,12 @@ int dual_quantize_impl(const void* w, int w_dtype, int64_t n, int64_t k, float* 
 }  // namespace
 
 extern "C" {
+
+int tcfp_dual_quantize_set_candidates(int on) {
+  if (on != 0 && on != 1) return TCFP_ERR_SHAPE;
+  g_cand_on = on;
+  return TCFP_OK;
+}
 
 int tcfp_dual_quantize_per_tensor(const void* w, int w_dtype, int64_t n, int64_t k,
                                   float* ef, int update_ef, int stochastic_lo,

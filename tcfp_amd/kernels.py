@@ -1475,3 +1475,13 @@ def set_gemm_tile_policy(policy: str) -> None:
     the persistent launch).  Results do not depend on the policy."""
     code = {"auto": 0, "large": 1, "small": 2, "small8": 3, "large_nonpersistent": 4}[policy]
     check(_hip.lib().tcfp_gemm_set_tile_policy(code), "set_gemm_tile_policy")
+
+
+def set_dual_quant_candidates(on: bool) -> None:
+    """Tuning hook of the per-tensor dual quantisation on tensors of 2^23
+    elements or more: True (default) keeps the candidates for the residual
+    amax in the amax pass and skips the full residual pass whenever they
+    decide it; False always runs the full pass.  Results do not depend on
+    it."""
+    check(_hip.lib().tcfp_dual_quantize_set_candidates(int(bool(on))),
+          "set_dual_quant_candidates")

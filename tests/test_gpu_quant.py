@@ -197,6 +197,57 @@ def test_dual_quant_per_tensor_ef_steps_bitexact(dev, shape, wdtype):
         Wd = W.to(dev)
 
 
+def _cand_case(name, shape, g):
+    w = torch.randn(shape, generator=g) * 0.02
+    if name == "overflow":       # every |v| near the max: all are candidates
+        w = torch.sign(w) * (1.0 + 1e-3 * torch.rand(shape, generator=g))
+    elif name == "exact":        # E4M3-representable: every residual is zero
+        codes = torch.randint(0, 126, shape, generator=g, dtype=torch.uint8)
+        w = codes.view(torch.float8_e4m3fn).float() * 2.0 ** -7
+    elif name == "outlier":      # one value far above the rest
+        w[3, 5] = 1e4
+    elif name == "nan":
+        w[7, 11] = float("nan")
+    elif name == "inf":
+        w[2, 9] = float("inf")
+    return w
+
+
+@pytest.mark.parametrize("name", ["normal", "overflow", "exact", "outlier", "nan", "inf"])
+@pytest.mark.parametrize("shape,wdtype", [((4096, 2048), torch.float32),
+                                          ((2049, 4097), torch.float32),
+                                          ((4096, 2048), torch.bfloat16)])
+def test_dual_quant_candidate_pass_matches_full_pass(dev, name, shape, wdtype):
+    """The candidate residual pass (tensors of 2^23+ elements) against the
+    full residual pass on the same inputs, bit for bit: codes, both inverse
+    scales, the transposed codes and the EF update, on data where the
+    candidates decide (normal) and where the full pass must run (a region
+    overflows, every residual is zero, one outlier, NaN, inf); and against
+    the oracle on the finite cases."""
+    g = torch.Generator().manual_seed(len(name) + shape[1])
+    w = _cand_case(name, shape, g).to(wdtype).to(dev)
+    ef0 = (torch.randn(shape, generator=g) * 1e-4).to(dev)
+    outs = []
+    try:
+        for on in (True, False):
+            K.set_dual_quant_candidates(on)
+            ef = ef0.clone()
+            res = K.dual_quantize_per_tensor(w, ef, transposed=True)
+            outs.append([r.view(torch.uint8) if r.dtype.itemsize == 1 else r for r in res] + [ef])
+    finally:
+        K.set_dual_quant_candidates(True)
+    for x, y in zip(*outs):
+        assert torch.equal(x.nan_to_num(), y.nan_to_num()) and torch.equal(x.isnan(), y.isnan())
+    if name in ("nan", "inf"):
+        return
+    hi, lo, ih, il, ef_new, _ = oq.dual_quant_per_tensor(w.float().cpu().numpy(),
+                                                         ef0.cpu().numpy())
+    h, l, ihd, ild, ht, lt, efd = outs[0]
+    assert np.array_equal(h.cpu().numpy(), hi) and np.array_equal(l.cpu().numpy(), lo)
+    assert ihd.item() == float(ih) and ild.item() == float(il)
+    assert np.array_equal(efd.cpu().numpy(), ef_new)
+
+
 def test_dual_quant_no_update_leaves_ef(dev):
     W = torch.randn(64, 64, device=dev) * 0.02
     ef = torch.randn(64, 64, device=dev) * 1e-4
