@@ -1351,6 +1351,12 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persist_kernel(GemmArgs g) {
       continue;
     }
     // ---- epilogue: stage through the last stage's buffer -------------------
+    // (the lane index is laundered here, so the compiler derives the
+    // epilogue's lane-dependent offsets after the K loop instead of keeping
+    // them live across it, where no register is free for them)
+    int lane_e = lane;
+    asm volatile("" : "+v"(lane_e));
+    const int lr_e = lane_e & 31, lg_e = lane_e >> 5;
     uint8_t* eps = lds + sb * STAGE + wave * (TMW * RB);
 #pragma unroll
     for (int i = 0; i < MB; ++i)
@@ -1358,7 +1364,7 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persist_kernel(GemmArgs g) {
       for (int j = 0; j < NB; ++j)
 #pragma unroll
         for (int gq = 0; gq < 4; ++gq) {
-          const int row = i * 32 + lr, col = j * 32 + gq * 8 + lg * 4;
+          const int row = i * 32 + lr_e, col = j * 32 + gq * 8 + lg_e * 4;
           float v[4];
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
@@ -1379,7 +1385,7 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persist_kernel(GemmArgs g) {
     // here is kept in scratch memory across the barrier below)
     static_assert(F32OUT || NST == 8, "eight store chunks per lane");
     auto staged = [&](int s) {
-      const int row = s * RPI + lane / CPR, cl = lane % CPR;
+      const int row = s * RPI + lane_e / CPR, cl = lane_e % CPR;
       return *reinterpret_cast<const uint4*>(eps + row * RB + ((cl ^ (row & (CPR - 1))) * 16));
     };
     const uint4 d0 = staged(0), d1 = staged(1), d2 = staged(2), d3 = staged(3);
@@ -1393,7 +1399,7 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persist_kernel(GemmArgs g) {
     }
     __builtin_amdgcn_sched_barrier(0);
     auto put = [&](int s, const uint4& d) {
-      const int row = s * RPI + lane / CPR, cl = lane % CPR;
+      const int row = s * RPI + lane_e / CPR, cl = lane_e % CPR;
       OutT* o = out + int64_t(m0 + wm * TMW + row) * g.ldo + nb + cl * 8;
       *reinterpret_cast<uint4*>(o) = d;
     };
