@@ -56,6 +56,12 @@ def test_gelu_quantize_equals_torch_gelu_then_quantize(dev, shape):
     q2, inv2, q2_t = K.quantize_per_tensor(ref, transpose=True)
     assert torch.equal(bits(q), bits(q2)) and torch.equal(bits(q_t), bits(q2_t))
     assert same_scalar(inv, inv2)
+    # and directly against the oracle's to_fp8_e4m3 of torch's gelu(h)
+    if ref.numel() and torch.isfinite(ref).all():
+        oc, oinv, _ = oq.to_fp8_per_tensor(ref.cpu().numpy(), "f32")
+        assert np.array_equal(q.view(torch.uint8).cpu().numpy(), oc)
+        assert np.array_equal(q_t.view(torch.uint8).cpu().numpy(), oc.T)
+        assert float(inv.item()) == float(oinv)
     if dg_ok:
         # torch's GELU backward is dy * (derivative factor), bit for bit
         dy = torch.randn(shape, generator=g).to(dev)
@@ -83,6 +89,14 @@ def test_gelu_backward_quantize_colsum_equals_torch(dev, shape):
     assert torch.equal(bits(q), bits(q2)) and torch.equal(bits(q_t), bits(q2_t))
     assert same_scalar(inv, inv2)
     assert torch.equal(bits(cs), bits(cs2))
+    # and directly against the oracle: to_fp8_e5m2 of torch's GELU backward,
+    # and the column sums in this build's fixed order
+    if ref.numel():
+        r = ref.cpu().numpy()
+        oc, oinv, _ = oq.to_fp8_per_tensor(r, "f32", "e5m2")
+        assert np.array_equal(q.view(torch.uint8).cpu().numpy(), oc)
+        assert float(inv.item()) == float(oinv)
+        assert np.array_equal(cs.cpu().numpy(), oq.column_sums(r))
 
 
 def test_gelu_quantize_nan_propagates(dev):
