@@ -256,10 +256,15 @@ class _TCFP12BlockScaledFunction(torch.autograd.Function):
         ctx.bs = bs
         ctx.abd = abd
         ctx.fp8_dgrad = _BLOCK_DGRAD == "fp8"
-        saved_act = input_2d if hp_grad_weight else act_fp8
-        saved_act_scales = None if hp_grad_weight else act_scales
+        # only what the backward will use is kept: the activation codes for
+        # dW, the weight codes for dX
+        need_dx, need_dw = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+        saved_act = (input_2d if hp_grad_weight else act_fp8) if need_dw else None
+        saved_act_scales = None if (hp_grad_weight or not need_dw) else act_scales
         w_lo_b, sl_b = (None, None) if abd else (w_lo, sl)
-        if ctx.fp8_dgrad and ctx.needs_input_grad[0]:
+        if not need_dx:
+            w_hi = w_lo_b = sh = sl_b = None
+        elif ctx.fp8_dgrad:
             # the FP8 dgrad's weight operand, re-blocked along D_out once per
             # forward; the backward needs nothing else of W
             w_hi, w_lo_b, sh, sl_b = K.block_requant_t(w_hi, w_lo_b, sh, sl_b, bs)
