@@ -192,7 +192,17 @@ def ptr(t: torch.Tensor | None) -> int | None:
     return None if t is None else t.data_ptr()
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_of(device: torch.device) -> int:
+    """Raw handle of torch's current stream on ``device`` (the stream every
+    op here enqueues on).  torch's own raw-stream query costs ~0.1 us
+    against ~2 us for ``torch.cuda.current_stream``; both give the same
+    handle."""
+    if _raw_stream is not None:
+        idx = device.index
+        return _raw_stream(torch.cuda.current_device() if idx is None else idx)
     return torch.cuda.current_stream(device).cuda_stream
 
 

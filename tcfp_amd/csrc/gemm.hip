@@ -2420,15 +2420,28 @@ __global__ __launch_bounds__(256) void grad_prep_kernel(const float* __restrict_
   }
 }
 
-// out[c] = sum over row tiles of part[tile, c], in tile order.
+// out[c] = sum over row tiles of part[tile, c]: a workgroup takes 16
+// columns, its 16 lanes per column sum the tiles t = lane, lane + 16, ... in
+// order, and the 16 lane sums are added in lane order (a fixed order: the
+// result is deterministic).  Sixteen-way parallel along the tiles, so the
+// chain of dependent loads per thread is tiles / 16 long.
 __global__ __launch_bounds__(256) void colsum_tiles_kernel(const float* __restrict__ part,
                                                            int64_t tiles, int64_t n,
                                                            float* __restrict__ out) {
-  const int64_t c = int64_t(blockIdx.x) * 256 + threadIdx.x;
-  if (c >= n) return;
+  __shared__ float red[16][17];
+  const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
+  const int64_t c = int64_t(blockIdx.x) * 16 + tx;
   float s = 0.0f;
-  for (int64_t t = 0; t < tiles; ++t) s += part[t * n + c];
-  out[c] = s;
+  if (c < n)
+    for (int64_t t = ty; t < tiles; t += 16) s += part[t * n + c];
+  red[ty][tx] = s;
+  __syncthreads();
+  if (ty == 0 && c < n) {
+    float a = red[0][tx];
+#pragma unroll
+    for (int k = 1; k < 16; ++k) a += red[k][tx];
+    out[c] = a;
+  }
 }
 
 }  // namespace
@@ -2456,7 +2469,7 @@ extern "C" int tcfp_block_grad_prep(const float* g, int64_t m, int64_t n, int bl
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (m == 0) {
     if (bias_grad) {
-      colsum_tiles_kernel<<<unsigned((n + 255) / 256), 256, 0, st>>>(nullptr, 0, n, bias_grad);
+      colsum_tiles_kernel<<<unsigned((n + 15) / 16), 256, 0, st>>>(nullptr, 0, n, bias_grad);
       return hipGetLastError() == hipSuccess ? TCFP_OK : TCFP_ERR_HIP;
     }
     return TCFP_OK;
@@ -2472,7 +2485,7 @@ extern "C" int tcfp_block_grad_prep(const float* g, int64_t m, int64_t n, int bl
   else
     grad_prep_kernel<128><<<grid, 256, 0, st>>>(g, m, n, g_deq, g_split_t, part, g_fp8, g_exps);
   if (bias_grad)
-    colsum_tiles_kernel<<<unsigned((n + 255) / 256), 256, 0, st>>>(part, tr, n, bias_grad);
+    colsum_tiles_kernel<<<unsigned((n + 15) / 16), 256, 0, st>>>(part, tr, n, bias_grad);
   return hipGetLastError() == hipSuccess ? TCFP_OK : TCFP_ERR_HIP;
 }
 
