@@ -1034,10 +1034,21 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && NS == 2 && BM <= 128 ? 2 : 1))
 // accumulator rows as 16-byte vectors straight from registers (16 stores per
 // wave and tile), and the freed last-stage buffer takes the next tile's
 // stage 1 right at the last stage's barrier.
-template <int AF, int BF, typename OutT, int EPI = 0>
+//
+// SCALE 1: block exponents (E8M0 MFMA scale operands, one accumulator set
+// for W_hi and W_lo).  A lane's 12 exponent bytes of a stage are buffer
+// loads at a 32-bit lane offset fixed per tile and a uniform per-stage
+// offset (full tiles: no bounds predicates), issued at the top of the
+// stage before and waited for at its barrier, which waits for every
+// earlier load anyway; the E8M0 codes are formed at the end of the stage,
+// after the refill DMA, without a further wait (a wait there would also
+// wait for that DMA).
+template <int AF, int BF, typename OutT, int EPI = 0, int SCALE = 0>
 __global__ __launch_bounds__(512, 1) void gemm_nt_persist_kernel(GemmArgs g) {
   constexpr bool F32OUT = std::is_same<OutT, float>::value;
   static_assert(EPI == 0 || F32OUT, "GELU epilogues write fp32");
+  static_assert(SCALE == 0 || (SCALE == 1 && EPI == 0), "block exponents: plain epilogue only");
+  constexpr int NACC = SCALE == 1 ? 1 : 2;
   constexpr int NW = 8, BM = 256, BN = 128, NS = 2;
   constexpr int WM = NW / 2, TMW = BM / WM, MB = TMW / 32;
   constexpr int TNW = BN / 2, NB = TNW / 32, NF = 2 * NB;
@@ -1057,6 +1068,12 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persist_kernel(GemmArgs g) {
   // m-blocks the group's halves
   static_assert(EPI != 2 || (TMW == kColGroup && MB == 2), "wave rows vs. column groups");
   __shared__ __align__(16) uint8_t lds[NS * STAGE];
+  // the tile's bias columns: loaded at the top of stage max(nt - 2, 0) by
+  // the first BN threads and stored here after that stage's barrier (which
+  // waits for every earlier load), read by the epilogue after the last
+  // stage's barrier.  Loaded in the epilogue itself, each wait for the bias
+  // would also wait for the next tile's DMA and the stores before it.
+  __shared__ __align__(16) float bias_s[BN];
   // GELU epilogues: EPI 1 the lane's int / uint maxima of the h bits (the
   // amax rule's keys), EPI 2 its max |value| bits (in amx)
   uint32_t amx = 0;
@@ -1121,16 +1138,80 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persist_kernel(GemmArgs g) {
 #pragma unroll
     for (int q = 0; q < 2; ++q) ro[h][q] = lr * kRowB + (((4 * h + lg + 2 * q) ^ swz(lr)) << 4);
 
-  v16f acc[2][NB][MB];
+  v16f acc[NACC][NB][MB];
   auto zero_acc = [&]() {
 #pragma unroll
-    for (int s = 0; s < 2; ++s)
+    for (int s = 0; s < NACC; ++s)
 #pragma unroll
       for (int j = 0; j < NB; ++j)
 #pragma unroll
         for (int i = 0; i < MB; ++i)
 #pragma unroll
           for (int r = 0; r < 16; ++r) acc[s][j][i][r] = 0.0f;
+  };
+  // output value r of accumulator block (j, i)
+  auto accv = [&](int j, int i, int r, float c0, float c1) -> float {
+    if constexpr (SCALE == 1) return acc[0][j][i][r];
+    else return acc[0][j][i][r] * c0 + acc[NACC - 1][j][i][r] * c1;
+  };
+
+  // ---- block exponents (SCALE 1).  Weight fragment q reads row
+  // n0 + wn * TNW + 32 * (q % NB) + lr of e_0 (q < NB, W_hi) or e_1 (W_lo),
+  // activation fragment i row m0 + wm * TMW + 32 * i + lr of e_a; sub-step
+  // h of stage t covers K block t * (kSK >> bs) + ((64 h + 32 lg) >> bs) for
+  // this lane's 32-column half lg.
+  const int bsh = SCALE == 1 ? g.bs_shift : 0;
+  const uint32_t kbs = uint32_t(kSK >> bsh);  // K blocks per stage
+  const uint32_t kbl0 = uint32_t((32 * lg) >> bsh), kbl1 = uint32_t((64 + 32 * lg) >> bsh);
+  const uint32_t nkb = SCALE == 1 ? uint32_t(K >> bsh) : 0u;
+  const __amdgpu_buffer_rsrc_t er0 = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<int8_t*>(g.e_0), 0, int(nkb * uint32_t(N)), 0x00020000);
+  const __amdgpu_buffer_rsrc_t er1 = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<int8_t*>(g.e_1), 0, int(nkb * uint32_t(N)), 0x00020000);
+  const __amdgpu_buffer_rsrc_t era = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<int8_t*>(g.e_a), 0, int(nkb * uint32_t(M)), 0x00020000);
+  // lane offsets of a tile's sub-step 0 / 1 exponents: weight, activation
+  struct EOff { uint32_t w0, w1, a0, a1; };
+  auto eoff_of = [&](int m0, int n0) {
+    const uint32_t rw = uint32_t(n0 + wn * TNW + lr), ra = uint32_t(m0 + wm * TMW + lr);
+    return EOff{kbl0 * uint32_t(N) + rw, kbl1 * uint32_t(N) + rw, kbl0 * uint32_t(M) + ra,
+                kbl1 * uint32_t(M) + ra};
+  };
+  // raw bytes of stage t: [2 q + h] weight fragment q, [2 (NF + i) + h]
+  // activation fragment i
+  uint32_t raw[SCALE == 1 ? 2 * (NF + MB) : 1];
+  uint32_t sc[SCALE == 1 ? 2 * (NF + MB) : 1];
+  auto load_raw = [&](const EOff& eo, int t) {
+    if constexpr (SCALE == 1) {
+      const int sw = int(uint32_t(t) * kbs * uint32_t(N)), sa = int(uint32_t(t) * kbs * uint32_t(M));
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const uint32_t ow = h ? eo.w1 : eo.w0, oa = h ? eo.a1 : eo.a0;
+#pragma unroll
+        for (int q = 0; q < NF; ++q)
+          raw[2 * q + h] = __builtin_amdgcn_raw_buffer_load_b8(q < NB ? er0 : er1,
+                                                               int(ow + 32u * (q % NB)), sw, 0);
+#pragma unroll
+        for (int i = 0; i < MB; ++i)
+          raw[2 * (NF + i) + h] = __builtin_amdgcn_raw_buffer_load_b8(era, int(oa + 32u * i), sa, 0);
+      }
+    }
+  };
+  // the loads have landed (a use here makes the compiler wait at this point)
+  auto hold_raw = [&]() {
+    if constexpr (SCALE == 1) {
+#pragma unroll
+      for (int f = 0; f < 2 * (NF + MB); ++f) asm volatile("" : "+v"(raw[f]));
+    }
+  };
+  // E8M0 code of an int8 exponent byte u: (u ^ 128) - 1 saturated at 0 maps
+  // e = -128 .. 127 to 0 (2^-127, the sentinel too), 0, 1, ..., 254
+  auto pack = [&]() {
+    if constexpr (SCALE == 1) {
+#pragma unroll
+      for (int f = 0; f < 2 * (NF + MB); ++f)
+        sc[f] = __builtin_elementwise_sub_sat(raw[f] ^ 128u, 1u);
+    }
   };
   auto read_frags = [&](v8i* f, int b, int h) {
     const uint8_t* st = lds + b * STAGE;
@@ -1145,13 +1226,17 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persist_kernel(GemmArgs g) {
       f[NF + i] = make_frag(lds_read16(st, rb + ro[h][0]), lds_read16(st, rb + ro[h][1]));
     }
   };
-  auto mfmas_range = [&](const v8i* f, int lo, int hi) {
+  auto mfmas_range = [&](const v8i* f, int h, int lo, int hi) {
 #pragma unroll
     for (int idx = 0; idx < NP; ++idx) {
       if (idx < lo || idx >= hi) continue;
       const int i = idx / NF, q = idx % NF;
-      v16f& c = acc[q / NB][q % NB][i];
-      c = mfma_plain<BF, AF>(f[q], f[NF + i], c);
+      v16f& c = acc[(q / NB) % NACC][q % NB][i];
+      if constexpr (SCALE == 1)
+        c = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+            f[q], f[NF + i], c, BF, AF, 0, int(sc[2 * q + h]), 0, int(sc[2 * (NF + i) + h]));
+      else
+        c = mfma_plain<BF, AF>(f[q], f[NF + i], c);
     }
   };
   // The MFMAs of (fragment, m-block) pairs [lo, hi) stay where they are:
@@ -1164,7 +1249,7 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persist_kernel(GemmArgs g) {
     for (int idx = 0; idx < NP; ++idx) {
       if (idx < lo || idx >= hi) continue;
       const int i = idx / NF, q = idx % NF;
-      asm volatile("" : "+v"(acc[q / NB][q % NB][i]));
+      asm volatile("" : "+v"(acc[(q / NB) % NACC][q % NB][i]));
     }
   };
   // every DMA landed except the newest `keep` vector-memory operations
@@ -1179,7 +1264,7 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persist_kernel(GemmArgs g) {
   };
 
   float c0s = 1.0f, c1s = 1.0f;
-  if (g.s_a) {
+  if (SCALE == 0 && g.s_a) {
     const float sa = *g.s_a;
     c0s = sa * *g.s_0;
     c1s = sa * *g.s_1;
@@ -1188,37 +1273,62 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persist_kernel(GemmArgs g) {
   int m0, n0;
   tile_of(0, m0, n0);
   v4i cur = src_of(m0, n0);
+  EOff eo = eoff_of(m0, n0);
   v8i f0[NF + MB], f1[NF + MB];
   zero_acc();
-  // prologue: stages 0 and 1 of the first tile (nt >= 2 for this kernel)
+  // prologue: stages 0 and 1 of the first tile (nt >= 2 for this kernel),
+  // after stage 0's exponents (complete at the wait, which leaves only the
+  // newest DI operations in flight)
+  load_raw(eo, 0);
   issue(cur, 0, 0);
   issue(cur, 1, 1);
   __builtin_amdgcn_s_waitcnt((DI & 15) | (7 << 4) | ((DI >> 4) << 14));
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
+  hold_raw();
+  pack();
   read_frags(f0, 0, 0);
 
   int cb0 = 0;  // buffer of the current tile's stage 0
   for (int it = 0; it < ntile; ++it) {
     const bool more = it + 1 < ntile;
     v4i nxt = cur;
+    EOff eo_n = eo;
     int m1 = 0, n1 = 0;
     if (more) {
       tile_of(it + 1, m1, n1);
       nxt = src_of(m1, n1);
+      if constexpr (SCALE == 1) eo_n = eoff_of(m1, n1);
     }
     for (int t = 0; t < nt; ++t) {
       const int b = (cb0 + t) & 1;
       __builtin_amdgcn_sched_barrier(0);
+      // exponents of the next stage (after the last: the next tile's stage
+      // 0), waited for after this stage's barrier.  (One load site: loads
+      // in two branches land in different registers, and the copy where
+      // they merge would wait for them right here.  In a tile's first
+      // stage the wait also covers the previous tile's output stores.)
+      if constexpr (SCALE == 1) {
+        const bool last = t + 1 == nt;
+        if (!last || more) {
+          const EOff e = last ? eo_n : eo;
+          load_raw(e, last ? 0 : t + 1);
+        }
+      }
+      const bool bias_stage = g.bias != nullptr && t == (nt > 2 ? nt - 2 : 0) && tid < BN;
+      float bv = 0.0f;
+      if (bias_stage) bv = g.bias[n0 + tid];
       read_frags(f1, b, 1);
-      mfmas_range(f0, 0, NP / 2);
+      mfmas_range(f0, 0, 0, NP / 2);
       interleave_mfma_lds<NP / 2, 2 * (NF + MB), 0>();
       pin_range(0, NP / 2);
       if (t == 0 && it > 0)
         sync_keep(std::integral_constant<int, NST>{});
       else
         sync_keep(std::integral_constant<int, 0>{});
-      mfmas_range(f0, NP / 2, NP);
+      hold_raw();
+      if (bias_stage) bias_s[tid] = bv;
+      mfmas_range(f0, 0, NP / 2, NP);
       pin_range(NP / 2, NP);
       __builtin_amdgcn_sched_barrier(0);
       if (t + 2 < nt)
@@ -1233,8 +1343,9 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persist_kernel(GemmArgs g) {
       // tile).  EPI 2 reads it after the epilogue, whose loads need the
       // registers.
       if (EPI != 2 || t + 1 < nt) read_frags(f0, b ^ 1, 0);
-      mfmas_range(f1, 0, NP);
+      mfmas_range(f1, 1, 0, NP);
       interleave_mfma_lds<NP, 2 * (NF + MB), 0>();
+      pack();  // the next stage's E8M0 codes (its sub-step 1 MFMAs are issued)
     }
 
     const int sb = (cb0 + nt - 1) & 1;
@@ -1272,7 +1383,7 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persist_kernel(GemmArgs g) {
 #pragma unroll
               for (int q = 0; q < 4; ++q) {
                 const int r = gq * 4 + q;
-                v[q] = acc[0][j][i][r] * c0s + acc[1][j][i][r] * c1s;
+                v[q] = accv(j, i, r, c0s, c1s);
               }
               v[0] = v[0] * d.x;
               v[1] = v[1] * d.y;
@@ -1325,11 +1436,14 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persist_kernel(GemmArgs g) {
 #pragma unroll
               for (int q = 0; q < 4; ++q) {
                 const int r = gq * 4 + q;
-                v[q] = acc[0][j][i][r] * c0s + acc[1][j][i][r] * c1s;
+                v[q] = accv(j, i, r, c0s, c1s);
               }
               if (g.bias) {
-#pragma unroll
-                for (int q = 0; q < 4; ++q) v[q] += g.bias[nb + col + q];
+                const float4 b4 = *reinterpret_cast<const float4*>(bias_s + wn * TNW + col);
+                v[0] += b4.x;
+                v[1] += b4.y;
+                v[2] += b4.z;
+                v[3] += b4.w;
               }
               store4<float>(reinterpret_cast<float*>(out) + o, v[0], v[1], v[2], v[3]);
               if constexpr (EPI == 1) {
@@ -1346,6 +1460,7 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persist_kernel(GemmArgs g) {
       zero_acc();
       cb0 = sb ^ 1;
       cur = nxt;
+      eo = eo_n;
       m0 = m1;
       n0 = n1;
       continue;
@@ -1369,11 +1484,14 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persist_kernel(GemmArgs g) {
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
             const int r = gq * 4 + q;
-            v[q] = acc[0][j][i][r] * c0s + acc[1][j][i][r] * c1s;
+            v[q] = accv(j, i, r, c0s, c1s);
           }
           if (g.bias) {
-#pragma unroll
-            for (int q = 0; q < 4; ++q) v[q] += g.bias[nb + col + q];
+            const float4 b4 = *reinterpret_cast<const float4*>(bias_s + wn * TNW + col);
+            v[0] += b4.x;
+            v[1] += b4.y;
+            v[2] += b4.z;
+            v[3] += b4.w;
           }
           const int byte = col * 2;
           const int chunk = (byte >> 4) ^ (row & (CPR - 1));
@@ -1409,6 +1527,7 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persist_kernel(GemmArgs g) {
     zero_acc();
     cb0 = sb ^ 1;  // the next tile's stage 0 sits in the other buffer
     cur = nxt;
+    eo = eo_n;
     m0 = m1;
     n0 = n1;
   }
@@ -1470,8 +1589,8 @@ bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 // The persistent large-tile launch: full 256 x 128 tiles, two K stages at
 // least, more tiles than CUs, no split-K, and every DMA span within the
-// descriptors' reach (tile policies 0 and 1 only).  Per-tensor fp8 dual
-// GEMMs with fp32 or bf16 output.
+// descriptors' reach (tile policies 0 and 1 only).  fp8 dual GEMMs with
+// per-tensor scales or block exponents, fp32 or bf16 output.
 bool persist_eligible(const GemmArgs& ga) {
   if (g_tile_policy != 0 && g_tile_policy != 1) return false;
   if (ga.M % 256 != 0 || ga.N % 128 != 0 || ga.K % kSK != 0 || ga.K <= kSK) return false;
@@ -1528,10 +1647,13 @@ int launch_gemm(GemmArgs ga, hipStream_t st) {
       // more tiles than CUs, all of them full: one persistent workgroup
       // per CU runs its tiles back to back
       bool persist = false;
-      if constexpr (SCALE == 0 && !SPLIT && AF != kBF16) {
-        persist = persist_eligible(ga);
+      if constexpr (!SPLIT && AF != kBF16) {
+        // (block exponents: 32-bit exponent offsets)
+        persist = persist_eligible(ga) &&
+                  (SCALE == 0 || int64_t(ga.K >> ga.bs_shift) * (ga.M > ga.N ? ga.M : ga.N) <
+                                     int64_t(INT32_MAX));
         if (persist)
-          gemm_nt_persist_kernel<AF, BF, OutT><<<unsigned(num_cus()), 512, 0, st>>>(ga);
+          gemm_nt_persist_kernel<AF, BF, OutT, 0, SCALE><<<unsigned(num_cus()), 512, 0, st>>>(ga);
       }
       if (!persist)
         gemm_nt_dma_kernel<AF, BF, SPLIT, OutT, 8, 256, 128, SCALE, 2><<<grid, 512, 0, st>>>(ga);

@@ -210,6 +210,41 @@ def test_persistent_launch_not_taken_for_partial_tiles(dev):
         assert not any("gemm_nt_persist_kernel" in n for n in names), (M, N, K_, od)
 
 
+@pytest.mark.parametrize("bs", [32, 64, 128])
+@pytest.mark.parametrize("M,N,K_,od", [(4352, 2048, 256, torch.float32),
+                                       (2048, 8192, 512, torch.float32),
+                                       (4352, 2048, 384, torch.bfloat16)])
+@pytest.mark.parametrize("afmt", [torch.float8_e4m3fn, torch.float8_e5m2])
+def test_persistent_block_dual_gemm_matches_one_workgroup_per_tile(dev, bs, M, N, K_, od, afmt):
+    """Block-exponent dual GEMMs with more full 256x128 tiles than CUs run
+    the persistent kernel (E8M0 scale operands, exponents loaded per stage
+    at per-tile lane offsets).  Its MFMAs accumulate in the K order of the
+    one-workgroup-per-tile kernel, so the results, bias included, are
+    identical bit for bit; one shape is also held to the oracle."""
+    print(f"persistent block bs={bs} M={M} N={N} K={K_} {od} {afmt}", flush=True)
+    a, ea, h, l, eh, el = make_block_operands(M, N, K_, bs, dev, 31, act_fp8=afmt)
+    bias = torch.randn(N, generator=torch.Generator().manual_seed(32)).to(dev)
+    run = lambda: K.fused_block_scaled_dual_gemm_forward(a, h, l, ea, eh, el, bs, bias=bias,
+                                                          out_dtype=od)
+    assert any("gemm_nt_persist_kernel" in n for n in _kernel_names(run))
+    p = run()
+    try:
+        K.set_gemm_tile_policy("large_nonpersistent")
+        assert not any("gemm_nt_persist_kernel" in n for n in _kernel_names(run))
+        q = run()
+    finally:
+        K.set_gemm_tile_policy("auto")
+    iv = torch.int16 if od == torch.bfloat16 else torch.int32
+    assert torch.equal(p.view(iv), q.view(iv))
+    if (M, N, K_) == (2048, 8192, 512):
+        fmt = ofp8.E4M3 if afmt == torch.float8_e4m3fn else ofp8.E5M2
+        A = og.block_deq64(u8(a), npy(ea), bs, fmt)
+        W = og.block_deq64(u8(h), npy(eh), bs) + og.block_deq64(u8(l), npy(el), bs,
+                                                                  lo_sentinel=True)
+        ref = A @ W.T + bias.cpu().double().numpy()
+        assert og.rel_fro(npy(p), ref) < EXACT
+
+
 # ------------------------------------------------- block-scaled (a10, a13)
 def make_block_operands(M, N, K_, bs, dev, seed, act_fp8=torch.float8_e4m3fn):
     g = torch.Generator().manual_seed(seed)
