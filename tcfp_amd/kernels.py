@@ -1029,9 +1029,9 @@ def fused_block_scaled_dual_gemm_forward(
 
     Reference: ``fused_block_scaled_dual_gemm_forward``
     (``tcfp/kernels.py:1939-2028``).  W_lo exponents of -128 (zero residual
-    blocks) contribute nothing, and a wave tile whose W_lo exponents are
-    all the sentinel skips its W_lo MFMAs (the reference's sparsity fast
-    path at its default threshold 0).  ``sparse_threshold > 0`` drops the
+    blocks) contribute nothing, and on the 128 x 64 tile a wave tile whose
+    W_lo exponents are all the sentinel skips its W_lo MFMAs (the
+    reference's sparsity fast path at its default threshold 0).  ``sparse_threshold > 0`` drops the
     W_lo blocks the reference's rule drops (``_lo_threshold``).
     ``persistent`` and ``launch_mult`` are scheduling hints of the
     reference's Triton kernel, accepted and without effect on the result.
