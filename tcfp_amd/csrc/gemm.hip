@@ -2027,13 +2027,36 @@ __global__ __launch_bounds__(256) void dequant_rows_bf16_kernel(
   }
 }
 
+// Byte B of w decoded (the decoders take the byte select directly).
+template <int FMT, int B>
+TCFP_DEV float fp8_byte_to_f32(uint32_t w) {
+  if constexpr (FMT == TCFP_FP8_E5M2) return __builtin_amdgcn_cvt_f32_bf8(int(w), B);
+  else return __builtin_amdgcn_cvt_f32_fp8(int(w), B);
+}
+
+// The 16 codes of a 16-byte row piece times sc, as bf16, into column j of
+// the transposing tile: tile[lc + j][lr].
+template <int FMT>
+TCFP_DEV void deq16_to_tile(const uint4 w, float sc, uint16_t (*tile)[64 + 2], int lc, int lr) {
+  const uint32_t words[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    tile[lc + 4 * i + 0][lr] = f32_to_bf16_rne(fp8_byte_to_f32<FMT, 0>(words[i]) * sc);
+    tile[lc + 4 * i + 1][lr] = f32_to_bf16_rne(fp8_byte_to_f32<FMT, 1>(words[i]) * sc);
+    tile[lc + 4 * i + 2][lr] = f32_to_bf16_rne(fp8_byte_to_f32<FMT, 2>(words[i]) * sc);
+    tile[lc + 4 * i + 3][lr] = f32_to_bf16_rne(fp8_byte_to_f32<FMT, 3>(words[i]) * sc);
+  }
+}
+
 // out[c, r] = bf16(q[r * ldq + c] * 2^e[c / bs, r]) through a 64 x 64 LDS
-// tile (c < cols: a column range of a wider q when ldq > cols).
+// tile (c < cols: a column range of a wider q when ldq > cols).  vec: q is
+// 16-byte aligned and ldq % 16 == 0, so a full tile's thread reads its 16
+// codes (one exponent block: bs >= 32) with one load.
 template <int FMT>
 __global__ __launch_bounds__(256) void dequant_t_bf16_kernel(
     const uint8_t* __restrict__ q0, const int8_t* __restrict__ e0, uint16_t* __restrict__ out0,
     const uint8_t* __restrict__ q1, const int8_t* __restrict__ e1, uint16_t* __restrict__ out1,
-    int64_t rows, int64_t cols, int bs_shift, int64_t ldq) {
+    int64_t rows, int64_t cols, int bs_shift, int64_t ldq, bool vec) {
   // blockIdx.y 0: matrix 0 (W_hi); 1: matrix 1 (W_lo, whose -128 exponent
   // marks a zero block)
   const bool second = blockIdx.y == 1;
@@ -2045,7 +2068,13 @@ __global__ __launch_bounds__(256) void dequant_t_bf16_kernel(
   const int tiles_c = int((cols + 63) / 64);
   const int64_t r0 = int64_t(blockIdx.x / tiles_c) * 64, c0 = int64_t(blockIdx.x % tiles_c) * 64;
   const int t = threadIdx.x;
-  {
+  if (vec && r0 + 64 <= rows && c0 + 64 <= cols) {
+    const int lr = t >> 2, lc = (t & 3) * 16;
+    const int64_t r = r0 + lr;
+    const uint4 w = *reinterpret_cast<const uint4*>(q + r * ldq + c0 + lc);
+    const int ex = e[((c0 + lc) >> bs_shift) * rows + r];
+    deq16_to_tile<FMT>(w, (zero_sentinel && ex == -128) ? 0.0f : exp2i(ex), tile, lc, lr);
+  } else {
     const int lr = t >> 2, lc = (t & 3) * 16;
     const int64_t r = r0 + lr;
 #pragma unroll
@@ -2138,16 +2167,21 @@ __global__ __launch_bounds__(256) void split_t_bf16_kernel(const float* __restri
 }
 
 // B'[c, r] = bf16(q[r * ldq + c] * 2^e[c / bs, r]) (exact), and with dup
-// also B'[c, M + r] (rows of 2M); c < cols.
+// also B'[c, M + r] (rows of 2M); c < cols.  vec as in dequant_t_bf16_kernel.
 template <int FMT>
 __global__ __launch_bounds__(256) void dequant_t_dup_bf16_kernel(
     const uint8_t* __restrict__ q, const int8_t* __restrict__ e, int64_t rows, int64_t cols,
-    int bs_shift, uint16_t* __restrict__ out, int64_t ldq, bool dup) {
+    int bs_shift, uint16_t* __restrict__ out, int64_t ldq, bool dup, bool vec) {
   __shared__ uint16_t tile[64][64 + 2];
   const int tiles_c = int((cols + 63) / 64);
   const int64_t r0 = int64_t(blockIdx.x / tiles_c) * 64, c0 = int64_t(blockIdx.x % tiles_c) * 64;
   const int t = threadIdx.x;
-  {
+  if (vec && r0 + 64 <= rows && c0 + 64 <= cols) {
+    const int lr = t >> 2, lc = (t & 3) * 16;
+    const int64_t r = r0 + lr;
+    const uint4 w = *reinterpret_cast<const uint4*>(q + r * ldq + c0 + lc);
+    deq16_to_tile<FMT>(w, exp2i(e[((c0 + lc) >> bs_shift) * rows + r]), tile, lc, lr);
+  } else {
     const int lr = t >> 2, lc = (t & 3) * 16;
     const int64_t r = r0 + lr;
 #pragma unroll
@@ -2216,9 +2250,10 @@ int dgrad_bf16(const uint16_t* gd, const uint8_t* w_hi, const uint8_t* w_lo, con
     const int64_t tiles = ((d_out + 63) / 64) * ((n + 63) / 64);
     if (!grid_x_fits(tiles, 256)) return TCFP_ERR_SHAPE;
     const int64_t eo = (c0 >> shift) * d_out;  // c0 is a multiple of the block
+    const bool vec = al16(w_hi + c0) && (!w_lo || al16(w_lo + c0)) && d_in % 16 == 0;
     dequant_t_bf16_kernel<TCFP_FP8_E4M3><<<dim3(unsigned(tiles), w_lo ? 2u : 1u), 256, 0, st>>>(
         w_hi + c0, e_hi + eo, wth, w_lo ? w_lo + c0 : nullptr, w_lo ? e_lo + eo : nullptr, wtl,
-        d_out, n, shift, d_in);
+        d_out, n, shift, d_in, vec);
     if (hipGetLastError() != hipSuccess) return TCFP_ERR_HIP;
     GemmArgs ga{};
     ga.A = reinterpret_cast<const uint8_t*>(gd);
@@ -2421,12 +2456,13 @@ int wgrad_chunked(const uint16_t* ap, int64_t m, int64_t n_out, const uint8_t* x
       const int64_t tx = ((m + 63) / 64) * ((n + 63) / 64);
       if (!grid_x_fits(tx, 256)) return TCFP_ERR_SHAPE;
       const int64_t eo = (c0 >> shift) * m;  // c0 is a multiple of the block
+      const bool vec = al16(x + c0) && k_in % 16 == 0;
       if (x_fmt == TCFP_FP8_E5M2)
         dequant_t_dup_bf16_kernel<TCFP_FP8_E5M2><<<unsigned(tx), 256, 0, st>>>(
-            x + c0, e_x + eo, m, n, shift, bp, k_in, !wrap);
+            x + c0, e_x + eo, m, n, shift, bp, k_in, !wrap, vec);
       else
         dequant_t_dup_bf16_kernel<TCFP_FP8_E4M3><<<unsigned(tx), 256, 0, st>>>(
-            x + c0, e_x + eo, m, n, shift, bp, k_in, !wrap);
+            x + c0, e_x + eo, m, n, shift, bp, k_in, !wrap, vec);
       if (hipGetLastError() != hipSuccess) return TCFP_ERR_HIP;
     }
     const int rc = wgrad_gemm(ap, bp, m, n_out, n, dw + c0, k_in, part, wrap, st);
