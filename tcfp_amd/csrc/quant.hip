@@ -1494,6 +1494,31 @@ __global__ __launch_bounds__(kThreads) void block_scales_kernel(const InT* __res
 // L = BS / VEC lanes with one 16-byte load each; a 256-thread workgroup
 // covers 256 / L consecutive rows of one K-block, so the int8 exponents of
 // a workgroup ([K/bs, M] layout) are contiguous.
+// (row group, K-block) of this workgroup in the block quantisers' grids.
+//  kfast (a 1-D grid of row groups x kbs items): K-blocks fastest, and
+//    workgroup b (dispatched to XCD b % 8) takes item (b % 8) * T/8 + b / 8:
+//    each XCD walks its own contiguous run of whole row groups, so the
+//    workgroups resident at once cover a few MB and the two halves of a
+//    128-byte line (64-byte row pieces: bf16 at block 32) stay in one L2.
+//    From 64 MB of input: 8192 x 16384 fp32 at block 64 ran 127 us against
+//    205 us in row-group order.
+//  otherwise (grid x = row group, y = K-block): row groups fastest, one
+//    K-block of many rows at a time, ~1 us faster on 32 MB inputs.
+TCFP_DEV void block_item(int64_t kbs64, bool kfast, uint32_t& rg, int64_t& kb) {
+  if (kfast) {
+    const uint32_t b = blockIdx.x, t = gridDim.x, kbs = uint32_t(kbs64);
+    const uint32_t i = (t & 7u) == 0 ? (b & 7u) * (t >> 3) + (b >> 3) : b;
+    rg = i / kbs;
+    kb = i - rg * kbs;
+  } else {
+    rg = blockIdx.x;
+    kb = blockIdx.y;
+  }
+}
+
+// Inputs of at least this many bytes take the K-fastest order above.
+constexpr int64_t kKFastBytes = int64_t(64) << 20;
+
 template <typename InT, int BS, int V = 16 / int(sizeof(InT))>
 struct Seg {
   static constexpr int VEC = V;
@@ -1571,11 +1596,14 @@ template <typename InT, int FMT, int BS, bool F32S>
 __global__ __launch_bounds__(kThreads) void block_quant_kernel(const InT* __restrict__ x,
                                                                int64_t m, int64_t k,
                                                                uint8_t* __restrict__ q,
-                                                               void* __restrict__ scales) {
+                                                               void* __restrict__ scales,
+                                                               bool kfast) {
   using G = Seg<InT, BS>;
   constexpr int VEC = G::VEC;
-  const int64_t kb = blockIdx.y;
-  const int64_t row = int64_t(blockIdx.x) * G::ROWS + threadIdx.x / G::L;
+  uint32_t rg;
+  int64_t kb;
+  block_item(k / BS, kfast, rg, kb);
+  const int64_t row = int64_t(rg) * G::ROWS + threadIdx.x / G::L;
   const int li = threadIdx.x % G::L;
   const bool valid = row < m;
   const int64_t off = row * k + kb * BS + li * VEC;
@@ -1720,11 +1748,13 @@ template <typename InT, int BS, bool HAS_EF, bool UPDATE, bool SR, bool F32S>
 __global__ __launch_bounds__(kThreads) void block_dualq_kernel(
     const InT* __restrict__ w, float* __restrict__ ef, int64_t n, int64_t k,
     uint8_t* __restrict__ hi, uint8_t* __restrict__ lo, void* __restrict__ shi,
-    void* __restrict__ slo, uint32_t k0, uint32_t k1, uint32_t off0, uint32_t off1) {
+    void* __restrict__ slo, uint32_t k0, uint32_t k1, uint32_t off0, uint32_t off1, bool kfast) {
   using G = DualSeg<InT, BS, SR>;
   constexpr int VEC = G::VEC;
-  const int64_t kb = blockIdx.y;
-  const int64_t row = int64_t(blockIdx.x) * G::ROWS + threadIdx.x / G::L;
+  uint32_t rg;
+  int64_t kb;
+  block_item(k / BS, kfast, rg, kb);
+  const int64_t row = int64_t(rg) * G::ROWS + threadIdx.x / G::L;
   const int li = threadIdx.x % G::L;
   const bool valid = row < n;
   const int64_t off = row * k + kb * BS + li * VEC;
@@ -2677,15 +2707,17 @@ int block_quantize_impl(const void* x, int x_dtype, int64_t m, int64_t k, int bl
   if (fp8_fmt != TCFP_FP8_E4M3 && fp8_fmt != TCFP_FP8_E5M2) return TCFP_ERR_DTYPE;
   if (!aligned16(x) || !aligned16(q)) return TCFP_ERR_ALIGN;
   if (m == 0 || k == 0) return TCFP_OK;
-  if (k / block > 65535 || m > INT32_MAX) return TCFP_ERR_SHAPE;  // grid limits
+  if (m > INT32_MAX) return TCFP_ERR_SHAPE;
   const unsigned kbs = unsigned(k / block);
+  // (grid y holds at most 65535 K-blocks)
+  const bool kfast = m * k * (x_dtype == TCFP_DTYPE_F32 ? 4 : 2) >= kKFastBytes || kbs > 65535u;
 #define TCFP_BQ(T, F, B)                                                                    \
   do {                                                                                      \
-    const int64_t gx = (m + Seg<T, B>::ROWS - 1) / Seg<T, B>::ROWS;                         \
-    if (!grid_x_fits(gx, kThreads)) return TCFP_ERR_SHAPE;                                  \
-    dim3 grid(unsigned(gx), kbs);                                                           \
+    const int64_t rgs = (m + Seg<T, B>::ROWS - 1) / Seg<T, B>::ROWS;                        \
+    if (!grid_x_fits(kfast ? rgs * kbs : rgs, kThreads)) return TCFP_ERR_SHAPE;              \
+    const dim3 grid = kfast ? dim3(unsigned(rgs * kbs)) : dim3(unsigned(rgs), kbs);         \
     block_quant_kernel<T, F, B, F32S><<<grid, kThreads, 0, st>>>(static_cast<const T*>(x),  \
-                                                                 m, k, q, scales);          \
+                                                                 m, k, q, scales, kfast);   \
   } while (0)
 #define TCFP_BQ_B(T, F)                                 \
   do {                                                  \
@@ -2716,19 +2748,21 @@ int block_dual_quantize_impl(const void* w, int w_dtype, int64_t n, int64_t k, i
   if (!aligned16(w) || !aligned16(w_hi) || !aligned16(w_lo) || (ef && !aligned16(ef)))
     return TCFP_ERR_ALIGN;
   if (n == 0 || k == 0) return TCFP_OK;
-  if (k / block > 65535 || n > INT32_MAX) return TCFP_ERR_SHAPE;  // grid limits
+  if (n > INT32_MAX) return TCFP_ERR_SHAPE;
   const unsigned kbs = unsigned(k / block);
+  // (grid y holds at most 65535 K-blocks)
+  const bool kfast = n * k * (w_dtype == TCFP_DTYPE_F32 ? 4 : 2) >= kKFastBytes || kbs > 65535u;
   const uint32_t k0 = uint32_t(seed), k1 = uint32_t(seed >> 32);
   const uint32_t o0 = uint32_t(offset), o1 = uint32_t(offset >> 32);
   const bool upd = ef && update_ef;
 #define TCFP_BDQ(T, B, EF, UP, SR)                                                             \
   do {                                                                                         \
     using DS = DualSeg<T, B, SR>;                                                              \
-    const int64_t gx = (n + DS::ROWS - 1) / DS::ROWS;                                          \
-    if (!grid_x_fits(gx, kThreads)) return TCFP_ERR_SHAPE;                                     \
-    dim3 grid(unsigned(gx), kbs);                                                              \
+    const int64_t rgs = (n + DS::ROWS - 1) / DS::ROWS;                                         \
+    if (!grid_x_fits(kfast ? rgs * kbs : rgs, kThreads)) return TCFP_ERR_SHAPE;                 \
+    const dim3 grid = kfast ? dim3(unsigned(rgs * kbs)) : dim3(unsigned(rgs), kbs);            \
     block_dualq_kernel<T, B, EF, UP, SR, F32S><<<grid, kThreads, 0, st>>>(                     \
-        static_cast<const T*>(w), ef, n, k, w_hi, w_lo, s_hi, s_lo, k0, k1, o0, o1);           \
+        static_cast<const T*>(w), ef, n, k, w_hi, w_lo, s_hi, s_lo, k0, k1, o0, o1, kfast);    \
   } while (0)
 #define TCFP_BDQ_MODE(T, B)                                     \
   do {                                                          \
