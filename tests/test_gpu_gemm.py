@@ -740,7 +740,10 @@ def test_c1_single_linear_forward_full_size(dev):
 # ---------------------------- fused block-backward gradient preparation
 @pytest.mark.parametrize("bs", [32, 64, 128])
 @pytest.mark.parametrize("M,N,K_", [(300, 256, 512), (4096, 256, 256), (1024, 1024, 768),
-                                    (64, 384, 128), (8, 128, 256)])
+                                    (64, 384, 128), (8, 128, 256),
+                                    # N >= 8192: the grouped tile order (whole and
+                                    # partial 16-row-tile groups, an odd tile count)
+                                    (1100, 8192, 128), (200, 8320, 128)])
 def test_block_backward_prep_matches_separate_passes(dev, bs, M, N, K_):
     g = torch.Generator().manual_seed(M + N + bs)
     grad = (torch.randn(M, N, generator=g) * 1e-3).to(dev)

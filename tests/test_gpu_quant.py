@@ -391,6 +391,62 @@ def test_block_dual_quantize_sr(dev, bs, wdt):
     assert float(np.abs(acc[m] / n - f).max()) < 0.2
 
 
+# ------------------- block quantisers on inputs of 64 MB and more (work order)
+@pytest.mark.parametrize("shape,dtype,bs,fp8", [
+    ((4100, 4160), torch.float32, 64, torch.float8_e4m3fn),
+    ((8192, 4096), torch.bfloat16, 32, torch.float8_e5m2)])
+def test_block_quantize_large_input_bitexact(dev, shape, dtype, bs, fp8):
+    """From 64 MB of input the block quantisers run K-blocks fastest in
+    XCD-contiguous runs (4100 x 4160 fp32: an odd workgroup count and a
+    partial row group; bf16 at block 32: 64-byte row pieces).  Codes and
+    exponents stay the oracle's bit for bit."""
+    g = torch.Generator().manual_seed(shape[0] + bs)
+    x = (torch.randn(shape, generator=g) *
+         2.0 ** torch.randint(-8, 8, (shape[0], 1), generator=g)).to(dtype)
+    assert x.numel() * x.element_size() >= 64 << 20
+    fmt = ofp8.E4M3 if fp8 == torch.float8_e4m3fn else ofp8.E5M2
+    codes, exps = oq.block_quantize(x.float().numpy(), bs, fmt)
+    q, e = K.block_quantize_fp8(x.to(dev), bs, fp8)
+    assert np.array_equal(i8(e), exps)
+    assert np.array_equal(u8(q), codes)
+
+
+def test_block_dual_quantize_large_input_ef_bitexact(dev):
+    """Block-64 dual quantisation with EF of a 64 MB weight (the K-fastest
+    order): codes, exponents and the new EF equal the oracle's."""
+    g = torch.Generator().manual_seed(5)
+    W = torch.randn(4096, 4096, generator=g) * 0.02
+    ef_o = (np.random.default_rng(5).standard_normal((4096, 4096)) * 1e-4).astype(np.float32)
+    ef_d = torch.from_numpy(ef_o.copy()).to(dev)
+    hi, lo, eh, el, ef_new = oq.block_dual_quantize(W.numpy(), 64, ef_o)
+    h, l, sh, sl = K.fused_dual_quantize_fp8(W.to(dev), 64, error_buf=ef_d)
+    assert np.array_equal(u8(h), hi) and np.array_equal(u8(l), lo)
+    assert np.array_equal(i8(sh), eh) and np.array_equal(i8(sl), el)
+    assert np.array_equal(ef_d.cpu().numpy(), ef_new)
+
+
+def test_block_dual_quantize_large_input_sr(dev):
+    """SRR on a 64 MB weight (the K-fastest order): W_hi and both exponent
+    arrays equal the oracle's, and every W_lo code is one of the two
+    stochastic-rounding candidates (the nearest where the residual is exact)."""
+    g = torch.Generator().manual_seed(6)
+    W = torch.randn(4096, 4096, generator=g) * 0.02
+    Wf = W.numpy()
+    bs, nb = 64, 4096 // 64
+    hi, lo_rtn, eh, el, _ = oq.block_dual_quantize(Wf, bs)
+    h, l, sh, sl = K.fused_dual_quantize_fp8(W.to(dev), bs, stochastic_lo=True, seed=11)
+    assert np.array_equal(u8(h), hi)
+    assert np.array_equal(i8(sh), eh) and np.array_equal(i8(sl), el)
+    deq_hi = oq.block_dequantize(hi, eh, bs).reshape(4096, nb, bs)
+    r = (Wf.reshape(4096, nb, bs) - deq_hi).astype(np.float32)
+    x = np.clip(r * (2.0 ** -el.T.astype(np.float64))[..., None], -448, 448)
+    rtn, other, frac, exact = oq.sr_candidates_block(x.astype(np.float32).reshape(4096, 4096))
+    c = u8(l)
+    assert np.all((c == rtn) | (c == other))
+    assert np.all(c[exact] == rtn[exact])
+    assert ((c == other) & (other != rtn)).any()
+
+
 # ------------------------------------------------ quant + column sums (bias grad)
 @pytest.mark.parametrize("shape", [(8192, 1024), (300, 200), (7, 4096), (1000, 24), (0, 64)])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
