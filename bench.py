@@ -1,6 +1,6 @@
 """Benchmark of the TCFP-12 hot path on one MI355X.
 
-    python bench.py [--steps K] [--warmup W] [--gpus 1] [--part all|gemm|quant|block|mlp|c5|copy]
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--part all|gemm|quant|block|mlp|c5|copy|scaled_mm]
 
 Headline (BASELINE.json ``metric``, configs[1]): the fused dual-FP8 GEMM
 ``out = X W_hi^T s_x s_hi + X W_lo^T s_x s_lo`` at M = N = K = 4096,
@@ -130,6 +130,19 @@ def bench_dual_gemm(steps, warmup, t=None, sustained=0):
     res["rel_fro"] = ((out.float() - ref).norm() / ref.norm()).item()
     res["tensors"] = t
     return res
+
+
+def bench_scaled_mm(steps, warmup):
+    """hipBLASLt's single ``torch._scaled_mm`` on C2's operands (the
+    comparator arm of ``bench_comparators``) alone: ``warmup`` untimed calls,
+    then ``steps`` timed by HIP events -- a workload for counter runs."""
+    import torch
+
+    a, h, l, sa, ih, il, xb, w = c2_tensors()
+    ms = event_time_ms(lambda: torch._scaled_mm(a, h.t(), scale_a=sa, scale_b=ih,
+                                                out_dtype=torch.bfloat16),
+                       steps, torch.cuda.current_stream(), warmup=warmup)
+    return {"scaled_mm_single_ms": ms, "tflops": 2 * a.shape[0] ** 3 / ms / 1e9}
 
 
 def bench_comparators(t, iters=200, heat=300, rounds=3):
@@ -567,7 +580,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--part", choices=("all", "gemm", "quant", "block", "mlp", "c5", "copy"),
+    ap.add_argument("--part", choices=("all", "gemm", "quant", "block", "mlp", "c5", "copy",
+                                       "scaled_mm"),
                     default="all",
                     help="all (default) = headline + every secondary figure; the others run "
                          "one workload (for profiling)")
@@ -592,7 +606,8 @@ def main():
                   steps=args.steps,
                   arms=("tcfp", "tcfp_fused", "bf16", "fp32") if args.arm == "both"
                   else (args.arm,)),
-              "copy": lambda: bench_copy(args.steps)}
+              "copy": lambda: bench_copy(args.steps),
+              "scaled_mm": lambda: bench_scaled_mm(args.steps, args.warmup)}
         log(f"[bench] part {args.part}")
         print(json.dumps({"part": args.part, **fn[args.part]()}), flush=True)
         return
