@@ -147,13 +147,50 @@ def test_tile_policies_agree_bitwise(dev, M, K_, N):
     h, l, ih, il = make_pair((N, K_), 8, dev)
     outs = []
     try:
-        for pol in ("large", "small"):
+        for pol in ("large", "small", "small8"):
             K.set_gemm_tile_policy(pol)
             outs.append(K.fused_dual_gemm_forward(a, h, l, sa, ih, il))
             outs.append(K.fp8_gemm_nt(a, h, sa, ih))
     finally:
         K.set_gemm_tile_policy("auto")
-    assert torch.equal(outs[0], outs[2]) and torch.equal(outs[1], outs[3])
+    for i in (2, 4):
+        assert torch.equal(outs[0], outs[i]) and torch.equal(outs[1], outs[i + 1]), i
+
+
+@pytest.mark.parametrize("afmt", [torch.float8_e4m3fn, torch.float8_e5m2])
+@pytest.mark.parametrize("od", [torch.float32, torch.bfloat16])
+def test_small_tile_two_stage_launch(dev, afmt, od):
+    """2048 x 2048 outputs: the 256x128 tiles (128) would leave CUs idle and
+    the 128x64 tiles (512) take two rounds, so the small tile runs its
+    two-stage pipeline (the four-stage one needs a single round).  The dual
+    GEMM with bias and the single GEMM (2048 x 4096: 512 tiles of 128 x
+    2 x 64), held to the float64 oracle and bit for bit to the large tile."""
+    print(f"small two-stage {afmt} {od}", flush=True)
+    M, K_, N = 2048, 512, 2048
+    fmt = ofp8.E4M3 if afmt == torch.float8_e4m3fn else ofp8.E5M2
+    a, sa = make_act((M, K_), 31, dev, afmt)
+    h, l, ih, il = make_pair((N, K_), 32, dev)
+    bias = torch.randn(N, generator=torch.Generator().manual_seed(33)).to(dev)
+    h2, _, ih2, _ = make_pair((4096, K_), 34, dev)
+    dual = lambda: K.fused_dual_gemm_forward(a, h, l, sa, ih, il, bias=bias, out_dtype=od)
+    single = lambda: K.fp8_gemm_nt(a, h2, sa, ih2, out_dtype=od)
+    for fn in (dual, single):
+        names = _kernel_names(fn)
+        assert any("128, 64, 0, 2, 0, 0>" in n for n in names), names
+    p, s = dual(), single()
+    tol = EXACT if od == torch.float32 else TOL
+    ref = og.dual_gemm_nt(u8(a), fmt, u8(h), u8(l), sa.item(), ih.item(), il.item())
+    ref = ref + bias.cpu().double().numpy()
+    assert og.rel_fro(p.float().cpu().numpy(), ref) < tol
+    ref_s = og.gemm_nt(u8(a), fmt, u8(h2), ofp8.E4M3, sa.item(), ih2.item())
+    assert og.rel_fro(s.float().cpu().numpy(), ref_s) < tol
+    try:
+        K.set_gemm_tile_policy("large")
+        q, t = dual(), single()
+    finally:
+        K.set_gemm_tile_policy("auto")
+    iv = torch.int16 if od == torch.bfloat16 else torch.int32
+    assert torch.equal(p.view(iv), q.view(iv)) and torch.equal(s.view(iv), t.view(iv))
 
 
 # ------------------------------------- persistent large-tile launch (C2)
