@@ -2122,6 +2122,7 @@ int quantize_impl(const void* x, int x_dtype, int64_t rows, int64_t cols, int fp
   if (!aligned16(x) || !inv_out) return TCFP_ERR_ALIGN;
   if (!scale_in && !workspace) return TCFP_ERR_WORKSPACE;
   if ((col_sum || gelu_in) && cols % 8 != 0) return TCFP_ERR_SHAPE;
+  if (col_sum && gelu_in) return TCFP_ERR_SHAPE;
   if (gelu_in && x_dtype != TCFP_DTYPE_F32) return TCFP_ERR_DTYPE;
   if (!gelu_in && (act_out || dg_out)) return TCFP_ERR_SHAPE;
   if ((act_out && !aligned16(act_out)) || (dg_out && !aligned16(dg_out))) return TCFP_ERR_ALIGN;
@@ -2161,7 +2162,7 @@ int quantize_impl(const void* x, int x_dtype, int64_t rows, int64_t cols, int fp
     else TCFP_QT(T, TCFP_FP8_E4M3, GL, CS);                              \
   } while (0)
     if (gelu_in) {
-      if (col_sum) TCFP_QT_F(float, true, true); else TCFP_QT_F(float, true, false);
+      TCFP_QT_F(float, true, false);  // (no entry point asks for column sums of gelu(h))
     } else if (bf) {
       if (col_sum) TCFP_QT_F(uint16_t, false, true); else TCFP_QT_F(uint16_t, false, false);
     } else {

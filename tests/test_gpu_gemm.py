@@ -376,23 +376,26 @@ def test_block_dual_gemm_bf16_out_bias_and_policies(dev):
 @pytest.mark.parametrize("bs", [32, 64, 128])
 @pytest.mark.parametrize("M,D_out,D_in", [(64, 128, 256), (300, 256, 384), (1024, 512, 1024),
                                           (33, 384, 128)])
-def test_block_dgrad_matches_oracle(dev, bs, M, D_out, D_in):
+@pytest.mark.parametrize("gfmt", ["e5m2", "e4m3"])
+def test_block_dgrad_matches_oracle(dev, bs, M, D_out, D_in, gfmt):
+    # (the reference's gradients are E5M2; the entry point takes either code)
     g = torch.Generator().manual_seed(M + D_out + bs)
     grad = torch.randn(M, D_out, generator=g) * 1e-3
     grad[: max(1, M // 9)] *= 1e4
     w = torch.randn(D_out, D_in, generator=g) * 0.02
-    gq, eg = K.block_quantize_fp8(grad.to(dev), bs, torch.float8_e5m2)
+    gdt = torch.float8_e5m2 if gfmt == "e5m2" else torch.float8_e4m3fn
+    gq, eg = K.block_quantize_fp8(grad.to(dev), bs, gdt)
     h, l, eh, el = K.fused_dual_quantize_fp8(w.to(dev), bs)
     dx = K.fused_block_scaled_dual_gemm_backward_dx(gq, h, l, eg, eh, el, bs)
     assert dx.dtype == torch.float32 and dx.shape == (M, D_in)
-    ref = og.block_dgrad(u8(gq), npy(eg), u8(h), u8(l), npy(eh), npy(el), bs, "e5m2")
+    ref = og.block_dgrad(u8(gq), npy(eg), u8(h), u8(l), npy(eh), npy(el), bs, gfmt)
     err = og.rel_fro(npy(dx), ref)
     print(f"block dgrad bs={bs} M={M} D_out={D_out} D_in={D_in} rel_fro={err:.2e}")
     # exact bf16 operands, fp32 accumulation
     assert err < EXACT
     # ABD: W_hi only
     dxa = K.fused_block_scaled_dual_gemm_backward_dx(gq, h, None, eg, eh, None, bs)
-    Gd = og.block_deq64(u8(gq), npy(eg), bs, "e5m2")
+    Gd = og.block_deq64(u8(gq), npy(eg), bs, gfmt)
     refa = Gd @ og.block_deq64(u8(h), npy(eh), bs)
     assert og.rel_fro(npy(dxa), refa) < EXACT
 
@@ -649,14 +652,16 @@ def test_sparse_threshold_rule(dev, thr_pow):
 @pytest.mark.parametrize("M,N,K_", [(256, 384, 512), (1024, 256, 1024), (300, 128, 256),
                                     (8, 64, 128), (302, 64, 128), (4096, 256, 256),
                                     (4096, 768, 256), (1000, 256, 512)])
-def test_block_wgrad_fp32_accuracy(dev, bs, M, N, K_):
+@pytest.mark.parametrize("afmt", ["e4m3", "e5m2"])
+def test_block_wgrad_fp32_accuracy(dev, bs, M, N, K_, afmt):
     g = torch.Generator().manual_seed(M + N + bs)
     grad = torch.randn(M, N, generator=g) * 1e-3
     x = torch.randn(M, K_, generator=g)
-    aq, ea = K.block_quantize_fp8(x.to(dev), bs)
+    adt = torch.float8_e4m3fn if afmt == "e4m3" else torch.float8_e5m2
+    aq, ea = K.block_quantize_fp8(x.to(dev), bs, adt)
     dw = K.block_scaled_wgrad(grad.to(dev), aq, ea, bs)
     assert dw.dtype == torch.float32 and dw.shape == (N, K_)
-    ref = grad.numpy().astype(np.float64).T @ og.block_deq64(u8(aq), npy(ea), bs)
+    ref = grad.numpy().astype(np.float64).T @ og.block_deq64(u8(aq), npy(ea), bs, afmt)
     err = og.rel_fro(npy(dw), ref)
     print(f"block wgrad bs={bs} M={M} N={N} K={K_} rel_fro={err:.2e}")
     assert err < 2e-5  # fp32-level: split-bf16 representation error <= 2^-17

@@ -346,3 +346,29 @@ def test_fuse_tcfp_mlp_replaces_nested_sequences(dev):
                                           skip_patterns=("none",)))
     assert all(isinstance(b, TCFPMLP) for b in model.blocks)
     assert type(model.head) is nn.Sequential
+
+
+@pytest.mark.parametrize("shape", [(300, 208), (1000, 24)])
+def test_gelu_e5m2_and_colsum_e4m3_quantisation(dev, shape):
+    """The entry points take either FP8 format (the layers use E4M3 for
+    gelu(h) and E5M2 for gradients): gelu(h) quantised to E5M2, and the
+    column-sum quantisation to E4M3 from fp32 and bf16, held to the
+    oracle's casts and column sums."""
+    print(f"gelu e5m2 / colsum e4m3 {shape}", flush=True)
+    g = torch.Generator().manual_seed(shape[0] + 3 * shape[1])
+    h = (torch.randn(shape, generator=g) * 3).to(dev)
+    q, inv, q_t = K.gelu_quantize_per_tensor(h, torch.float8_e5m2, transpose=True)
+    ref = F.gelu(h).cpu().numpy()
+    oc, oinv, _ = oq.to_fp8_per_tensor(ref, "f32", "e5m2")
+    assert np.array_equal(q.view(torch.uint8).cpu().numpy(), oc)
+    assert np.array_equal(q_t.view(torch.uint8).cpu().numpy(), oc.T)
+    assert float(inv.item()) == float(oinv)
+    for dt, tag in ((torch.float32, "f32"), (torch.bfloat16, "bf16")):
+        x = torch.randn(shape, generator=g).to(dt).to(dev)
+        q, inv, q_t, cs = K.quantize_per_tensor_colsum(x, torch.float8_e4m3fn, transpose=True)
+        xn = x.float().cpu().numpy()
+        oc, oinv, _ = oq.to_fp8_per_tensor(xn, tag, "e4m3")
+        assert np.array_equal(q.view(torch.uint8).cpu().numpy(), oc), tag
+        assert np.array_equal(q_t.view(torch.uint8).cpu().numpy(), oc.T), tag
+        assert float(inv.item()) == float(oinv), tag
+        assert np.array_equal(cs.cpu().numpy(), oq.column_sums(xn)), tag
