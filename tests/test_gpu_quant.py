@@ -292,6 +292,42 @@ def test_dual_quant_sr_candidates_and_unbiased(dev):
     assert float(np.abs(p[m] - frac[m]).max()) < 0.2
 
 
+@pytest.mark.parametrize("wdtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("update", [True, False])
+@pytest.mark.parametrize("transposed", [False, True])
+def test_dual_quant_sr_with_error_feedback(dev, wdtype, update, transposed):
+    """Stochastic W_lo with an error-feedback buffer: the reference's
+    Function allows both (nn/__init__.py:363-383; its layer never enables
+    both).  W_hi, the scales and the candidate pair follow W + ef, and the
+    new error is W - (deq(hi) + deq(lo)) of the codes drawn."""
+    g = torch.Generator().manual_seed(5)
+    W = torch.randn(128, 256, generator=g).to(wdtype)
+    ef0 = torch.randn(128, 256, generator=g) * 1e-3
+    Wf = W.float().numpy()
+    hi_o, _, ih_o, il_o, _, res = oq.dual_quant_per_tensor(Wf, ef0.numpy())
+    scale_lo = oq.per_tensor_scale(res, "f32")
+    x = np.clip(res * scale_lo, -448, 448).astype(np.float32)
+    lo_c, hi_c, frac, exact = oq.sr_candidates_per_tensor(x)
+    ef = ef0.clone().to(dev)
+    out = K.dual_quantize_per_tensor(W.to(dev), ef, update_ef=update, stochastic_lo=True,
+                                     seed=77, transposed=transposed)
+    h, l, ih, il = out[:4]
+    assert np.array_equal(u8(h), hi_o)
+    assert ih.item() == float(ih_o) and il.item() == float(il_o)
+    c = u8(l)
+    assert np.all((c == lo_c) | (c == hi_c)), "SR picked a code outside the candidate pair"
+    assert np.all(c[exact] == lo_c[exact])
+    assert 0 < int((c != lo_c).sum()) < c.size
+    if transposed:
+        assert np.array_equal(u8(out[4]), hi_o.T) and np.array_equal(u8(out[5]), c.T)
+    if update:
+        deq_hi = ofp8.decode(hi_o, ofp8.E4M3).astype(np.float32) * np.float32(ih_o)
+        deq_lo = ofp8.decode(c, ofp8.E4M3).astype(np.float32) * np.float32(il_o)
+        assert np.array_equal(ef.cpu().numpy(), Wf - (deq_hi + deq_lo))
+    else:
+        assert torch.equal(ef.cpu(), ef0)
+
+
 # ------------------------------------------------------ block quant (a4)
 @pytest.mark.parametrize("bs", [32, 64, 128])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
@@ -342,6 +378,12 @@ def test_block_dual_quantize_ef_bitexact(dev, bs, wdtype, shape):
         assert np.array_equal(i8(sh), eh) and np.array_equal(i8(sl), el)
         assert np.array_equal(ef_d.cpu().numpy(), ef_new), f"step {step}"
         ef_o = ef_new
+    # update_ef=False: the same codes from W + ef, the buffer untouched
+    hi, lo, eh, el, _ = oq.block_dual_quantize(W.float().numpy(), bs, ef_o)
+    h, l, sh, sl = K.fused_dual_quantize_fp8(W.to(dev), bs, error_buf=ef_d, update_ef=False)
+    assert np.array_equal(u8(h), hi) and np.array_equal(u8(l), lo)
+    assert np.array_equal(i8(sh), eh) and np.array_equal(i8(sl), el)
+    assert np.array_equal(ef_d.cpu().numpy(), ef_o)
 
 
 def test_block_dual_quantize_sentinel_and_no_ef(dev):
