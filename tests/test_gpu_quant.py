@@ -248,31 +248,36 @@ def test_dual_quant_candidate_pass_matches_full_pass(dev, name, shape, wdtype):
     assert np.array_equal(efd.cpu().numpy(), ef_new)
 
 
-def test_dual_quant_no_update_leaves_ef(dev):
-    W = torch.randn(64, 64, device=dev) * 0.02
+@pytest.mark.parametrize("wdtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("transposed", [False, True])
+def test_dual_quant_no_update_leaves_ef(dev, wdtype, transposed):
+    W = (torch.randn(64, 64, device=dev) * 0.02).to(wdtype)
     ef = torch.randn(64, 64, device=dev) * 1e-4
     before = ef.clone()
-    a = K.dual_quantize_per_tensor(W, ef, update_ef=False)
+    a = K.dual_quantize_per_tensor(W, ef, update_ef=False, transposed=transposed)
     assert torch.equal(ef, before)
-    b = K.dual_quantize_per_tensor(W, before.clone(), update_ef=True)
+    b = K.dual_quantize_per_tensor(W, before.clone(), update_ef=True, transposed=transposed)
     assert all(torch.equal(x.view(torch.uint8) if x.dtype.itemsize == 1 else x,
                            y.view(torch.uint8) if y.dtype.itemsize == 1 else y)
                for x, y in zip(a, b))
 
 
-def test_dual_quant_no_ef_matches_zero_ef(dev):
-    W = torch.randn(96, 160, device=dev)
-    a = K.dual_quantize_per_tensor(W, None)
-    b = K.dual_quantize_per_tensor(W, torch.zeros_like(W))
+@pytest.mark.parametrize("wdtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("transposed", [False, True])
+def test_dual_quant_no_ef_matches_zero_ef(dev, wdtype, transposed):
+    W = torch.randn(96, 160, device=dev).to(wdtype)
+    a = K.dual_quantize_per_tensor(W, None, transposed=transposed)
+    b = K.dual_quantize_per_tensor(W, torch.zeros(96, 160, device=dev), transposed=transposed)
     for x, y in zip(a, b):
         assert torch.equal(x.view(torch.uint8) if x.dtype.itemsize == 1 else x,
                            y.view(torch.uint8) if y.dtype.itemsize == 1 else y)
 
 
-def test_dual_quant_sr_candidates_and_unbiased(dev):
+@pytest.mark.parametrize("wdtype", [torch.float32, torch.bfloat16])
+def test_dual_quant_sr_candidates_and_unbiased(dev, wdtype):
     g = torch.Generator().manual_seed(3)
-    W = torch.randn(128, 256, generator=g)
-    hi_o, lo_rtn, ih_o, il_o, _, res = oq.dual_quant_per_tensor(W.numpy(), None)
+    W = torch.randn(128, 256, generator=g).to(wdtype)
+    hi_o, lo_rtn, ih_o, il_o, _, res = oq.dual_quant_per_tensor(W.float().numpy(), None)
     scale_lo = oq.per_tensor_scale(res, "f32")
     x = np.clip(res * scale_lo, -448, 448).astype(np.float32)
     lo_c, hi_c, frac, exact = oq.sr_candidates_per_tensor(x)
