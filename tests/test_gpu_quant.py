@@ -472,6 +472,25 @@ def test_block_dual_quantize_large_input_ef_bitexact(dev):
     assert np.array_equal(ef_d.cpu().numpy(), ef_new)
 
 
+@pytest.mark.parametrize("bs", [32, 64, 128])
+@pytest.mark.parametrize("wdtype", [torch.float32, torch.bfloat16])
+def test_block_dual_quantize_large_input_no_update(dev, bs, wdtype):
+    """update_ef=False on a 64 MB weight (the K-fastest order): the codes
+    and exponents of the updating call, the buffer untouched."""
+    print(f"block dq large no-update bs={bs} {wdtype}", flush=True)
+    rows = 4096 if wdtype == torch.float32 else 8192
+    g = torch.Generator().manual_seed(bs)
+    W = (torch.randn(rows, 4096, generator=g) * 0.02).to(wdtype).to(dev)
+    ef = torch.randn(rows, 4096, generator=g).mul_(1e-4).to(dev)
+    keep = ef.clone()
+    a = K.fused_dual_quantize_fp8(W, bs, error_buf=ef, update_ef=False)
+    assert torch.equal(ef, keep)
+    b = K.fused_dual_quantize_fp8(W, bs, error_buf=keep, update_ef=True)
+    assert not torch.equal(ef, keep)
+    for x, y in zip(a, b):
+        assert torch.equal(x.view(torch.uint8), y.view(torch.uint8))
+
+
 def test_block_dual_quantize_large_input_sr(dev):
     """SRR on a 64 MB weight (the K-fastest order): W_hi and both exponent
     arrays equal the oracle's, and every W_lo code is one of the two
