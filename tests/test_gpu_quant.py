@@ -474,21 +474,31 @@ def test_block_dual_quantize_large_input_ef_bitexact(dev):
 
 @pytest.mark.parametrize("bs", [32, 64, 128])
 @pytest.mark.parametrize("wdtype", [torch.float32, torch.bfloat16])
-def test_block_dual_quantize_large_input_no_update(dev, bs, wdtype):
-    """update_ef=False on a 64 MB weight (the K-fastest order): the codes
-    and exponents of the updating call, the buffer untouched."""
-    print(f"block dq large no-update bs={bs} {wdtype}", flush=True)
+@pytest.mark.parametrize("fmt", ["exponent", "fp32"])
+def test_block_dual_quantize_large_input_no_update(dev, bs, wdtype, fmt):
+    """update_ef=False on a 64 MB weight (the K-fastest order), with either
+    scale format: the codes and scales of the updating call, the buffer
+    untouched.  With fp32 multipliers, SRR keeps W_hi and both scale arrays
+    of the round-to-nearest call and changes only some W_lo codes."""
+    print(f"block dq large no-update bs={bs} {wdtype} {fmt}", flush=True)
     rows = 4096 if wdtype == torch.float32 else 8192
     g = torch.Generator().manual_seed(bs)
     W = (torch.randn(rows, 4096, generator=g) * 0.02).to(wdtype).to(dev)
     ef = torch.randn(rows, 4096, generator=g).mul_(1e-4).to(dev)
     keep = ef.clone()
-    a = K.fused_dual_quantize_fp8(W, bs, error_buf=ef, update_ef=False)
+    a = K.fused_dual_quantize_fp8(W, bs, error_buf=ef, update_ef=False, scale_format=fmt)
     assert torch.equal(ef, keep)
-    b = K.fused_dual_quantize_fp8(W, bs, error_buf=keep, update_ef=True)
+    b = K.fused_dual_quantize_fp8(W, bs, error_buf=keep, update_ef=True, scale_format=fmt)
     assert not torch.equal(ef, keep)
     for x, y in zip(a, b):
         assert torch.equal(x.view(torch.uint8), y.view(torch.uint8))
+    if fmt == "fp32":
+        rne = K.fused_dual_quantize_fp8(W, bs, scale_format=fmt)
+        sr = K.fused_dual_quantize_fp8(W, bs, stochastic_lo=True, seed=9, scale_format=fmt)
+        for i in (0, 2, 3):
+            assert torch.equal(sr[i].view(torch.uint8), rne[i].view(torch.uint8)), i
+        moved = (sr[1].view(torch.uint8) != rne[1].view(torch.uint8)).float().mean().item()
+        assert 0.0 < moved < 0.75, moved
 
 
 def test_block_dual_quantize_large_input_sr(dev):
