@@ -249,6 +249,28 @@ def test_dual_quant_candidate_pass_matches_full_pass(dev, name, shape, wdtype):
 
 
 @pytest.mark.parametrize("wdtype", [torch.float32, torch.bfloat16])
+def test_dual_quant_candidate_pass_without_ef(dev, wdtype):
+    """The candidate residual pass with no error-feedback buffer (2^23+
+    elements): the full pass's codes and scales, and the oracle's."""
+    g = torch.Generator().manual_seed(17)
+    w = (torch.randn(4096, 2048, generator=g) * 0.02).to(wdtype).to(dev)
+    outs = []
+    try:
+        for on in (True, False):
+            K.set_dual_quant_candidates(on)
+            outs.append([r.view(torch.uint8) if r.dtype.itemsize == 1 else r
+                         for r in K.dual_quantize_per_tensor(w, None)])
+    finally:
+        K.set_dual_quant_candidates(True)
+    for x, y in zip(*outs):
+        assert torch.equal(x, y)
+    hi, lo, ih, il, _, _ = oq.dual_quant_per_tensor(w.float().cpu().numpy(), None)
+    h, l, ihd, ild = outs[0]
+    assert np.array_equal(h.cpu().numpy(), hi) and np.array_equal(l.cpu().numpy(), lo)
+    assert ihd.item() == float(ih) and ild.item() == float(il)
+
+
+@pytest.mark.parametrize("wdtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("transposed", [False, True])
 def test_dual_quant_no_update_leaves_ef(dev, wdtype, transposed):
     W = (torch.randn(64, 64, device=dev) * 0.02).to(wdtype)
