@@ -194,6 +194,21 @@ def test_small_tile_two_stage_launch(dev, afmt, od):
 
 
 # ------------------------------------- persistent large-tile launch (C2)
+@pytest.mark.parametrize("afmt", [torch.float8_e4m3fn, torch.float8_e5m2])
+@pytest.mark.parametrize("M,N,K_", [(256, 384, 512), (2048, 4096, 256)])
+def test_single_gemm_e5m2_b_operand(dev, afmt, M, N, K_):
+    """The C ABI takes either FP8 format for both operands (the layers
+    only pass E4M3 weights): B in E5M2 with either A, one-round and
+    two-round small-tile grids, against the float64 oracle."""
+    print(f"gemm B=e5m2 A={afmt} {M}x{N}x{K_}", flush=True)
+    a, sa = make_act((M, K_), 41, dev, afmt)
+    b, sb = make_act((N, K_), 42, dev, torch.float8_e5m2)
+    out = K.fp8_gemm_nt(a, b, sa, sb)
+    fa = ofp8.E4M3 if afmt == torch.float8_e4m3fn else ofp8.E5M2
+    ref = og.gemm_nt(u8(a), fa, u8(b), ofp8.E5M2, sa.item(), sb.item())
+    assert og.rel_fro(out.cpu().numpy(), ref) < EXACT
+
+
 def _kernel_names(fn):
     from torch.profiler import ProfilerActivity, profile
 
