@@ -214,7 +214,10 @@ int tcfp_dual_gemm_dgelu_quantize_colsum(const uint8_t* a, int a_fmt, int64_t ld
  * or more (no counterpart in the reference): on = 1 (default) keeps the
  * candidates for the residual amax during the amax pass and skips the full
  * residual pass whenever they decide it; on = 0 always runs the full pass.
- * Results do not depend on it. */
+ * Results do not depend on it.  While the candidates are kept, the
+ * caller's w_lo buffer (all n * k bytes of it, as up to n * k / 4 fp32
+ * values) holds them between the amax pass and the W_lo pass (see the w_lo
+ * note of tcfp_dual_quantize_per_tensor). */
 int tcfp_dual_quantize_set_candidates(int on);
 
 /* Per-tensor dual quantisation with optional error feedback.
@@ -229,7 +232,15 @@ int tcfp_dual_quantize_set_candidates(int on);
  *           e_new = W - (hi*inv_hi + lo*inv_lo).
  *   stochastic_lo  round W_lo stochastically (SRR, tcfp/core.py:109-134,
  *           418-464) with Philox4x32-10 keyed by (seed, offset).
- *   w_hi_t, w_lo_t optional [k, n] transposed codes (dgrad operands). */
+ *   w_hi_t, w_lo_t optional [k, n] transposed codes (dgrad operands).
+ *   w_lo    is also scratch during the call: on tensors of 2^23 elements or
+ *           more (candidate pass on, the default; no delayed or NF-aware
+ *           scaling) the amax pass stores fp32 candidate values in it, which
+ *           the final pass overwrites with the W_lo codes.  So w_lo must not
+ *           alias any input (w, ef) and must not be read, on any stream,
+ *           before the call's work on `stream` has completed; a persistent
+ *           w_lo buffer shared with concurrent readers needs
+ *           tcfp_dual_quantize_set_candidates(0). */
 int tcfp_dual_quantize_per_tensor(const void* w, int w_dtype, int64_t n, int64_t k,
                                   float* ef, int update_ef, int stochastic_lo,
                                   uint64_t seed, uint64_t offset, uint8_t* w_hi,
@@ -250,7 +261,8 @@ int tcfp_dual_quantize_per_tensor(const void* w, int w_dtype, int64_t n, int64_t
  * to the current device (TCFP_ERR_DEVICE otherwise).  Every call on one GPU
  * shares that array: calls that overlap on one GPU (e.g. on two streams
  * without ordering between them) race and give wrong scales; calls ordered
- * on one stream are safe. */
+ * on one stream are safe.  w_lo is scratch during the call as in
+ * tcfp_dual_quantize_per_tensor (same aliasing rule). */
 int tcfp_dual_quantize_per_tensor_noalloc(const void* w, int w_dtype, int64_t n, int64_t k,
                                           float* ef, int update_ef, int stochastic_lo,
                                           uint64_t seed, uint64_t offset, uint8_t* w_hi,

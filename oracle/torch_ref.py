@@ -108,10 +108,13 @@ class RefTCFPLinear(nn.Linear):
         return RefTCFP12Function.apply(x, self.weight, self.bias, self.ef, "", upd)
 
 
-def gelu_mlp_step_losses(make_linear, d_in, d_hidden, tokens, steps, seed, device):
+def gelu_mlp_step_losses(make_linear, d_in, d_hidden, tokens, steps, seed, device,
+                         autocast_bf16=False):
     """Losses of ``steps`` AdamW(lr 1e-3) steps of Linear -> GELU -> Linear
     on seeded bf16 inputs and an MSE target, with ``make_linear(i, o)``
-    building the linears (weights re-initialised from ``seed``)."""
+    building the linears (weights re-initialised from ``seed``).
+    ``autocast_bf16``: run the forward under ``torch.autocast(bfloat16)``
+    (the BF16 mixed-precision baseline with ``nn.Linear``)."""
     g = torch.Generator().manual_seed(seed)
     x = torch.randn(tokens, d_in, generator=g).bfloat16().to(device)
     y = torch.randn(tokens, d_in, generator=g).to(device)
@@ -124,7 +127,10 @@ def gelu_mlp_step_losses(make_linear, d_in, d_hidden, tokens, steps, seed, devic
     opt = torch.optim.AdamW(model.parameters(), lr=1e-3)
     losses = []
     for _ in range(steps):
-        loss = (model(x).float() - y).square().mean()
+        with torch.autocast(device.type if isinstance(device, torch.device) else "cuda",
+                            dtype=torch.bfloat16, enabled=autocast_bf16):
+            out = model(x)
+        loss = (out.float() - y).square().mean()
         opt.zero_grad(set_to_none=True)
         loss.backward()
         opt.step()

@@ -410,11 +410,14 @@ __global__ __launch_bounds__(kThreads) void amax_cand_kernel(const InT* __restri
   float* const region = co.vals + int64_t(blockIdx.x) * co.cap;
   const int lane = threadIdx.x & 63;
   uint32_t mw = 0;  // the workgroup's running maximum (uniform)
-  // store v[j] (j < nv) with |v| >= 0.5714 * the running maximum
+  // store v[j] (j < nv) with |v| >= 0.5714 * the running maximum.  Zeros
+  // are never stored: their residual is zero, below any decisive maximum,
+  // and while the running maximum is still 0 they would all pass (a zero
+  // head of a tensor would fill the region and force the full pass).
   auto emit = [&](const float* v, int nv) {
     const float thr = __uint_as_float(mw) * 0.5714f;
     uint64_t mask = 0;
-    for (int j = 0; j < nv; ++j) mask |= uint64_t(fabsf(v[j]) >= thr) << j;
+    for (int j = 0; j < nv; ++j) mask |= uint64_t(fabsf(v[j]) >= thr && v[j] != 0.0f) << j;
     const int c = __builtin_popcountll(mask);
     int incl = c;
 #pragma unroll

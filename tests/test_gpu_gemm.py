@@ -836,3 +836,47 @@ def test_block_backward_prep_matches_separate_passes(dev, bs, M, N, K_):
         dw_a = K.block_scaled_wgrad(grad, aq, ea, bs)
         dw_b = K.block_wgrad_from_prep(g_split, aq, ea, bs)
         assert torch.equal(dw_a, dw_b)
+
+
+@pytest.mark.parametrize("bs", [32, 64, 128])
+def test_c3_4096_cubed_block_exponents_against_torch_fp32(dev, bs):
+    """configs[2] at full size with the reference's block format: 4096^3
+    block dual GEMM with int8 power-of-two exponents (E8M0 MFMA scales,
+    persistent kernel) at bs 32 / 64 / 128, against torch's fp32 matmul of
+    the dequantised operands (the reference's contract,
+    tests/test_block_scaling_kernels.py:210-240)."""
+    M = N = K_ = 4096
+    g = torch.Generator(device=dev).manual_seed(100 + bs)
+    x = torch.randn(M, K_, device=dev, generator=g, dtype=torch.bfloat16)
+    w = torch.randn(N, K_, device=dev, generator=g, dtype=torch.bfloat16)
+    print(f"[c3 e8m0] bs={bs} 4096^3", flush=True)
+    a, ea = K.block_quantize_fp8(x, bs)
+    h, l, eh, el = K.fused_dual_quantize_fp8(w, bs)
+    out = K.fused_block_scaled_dual_gemm_forward(a, h, l, ea, eh, el, bs)
+    A = K.block_dequantize_fp8(a, ea, bs)
+    W = K.block_dequantize_fp8(h, eh, bs) + K.block_dequantize_fp8(l, el, bs)
+    ref = A @ W.t()
+    err = (torch.linalg.norm(out - ref) / torch.linalg.norm(ref)).item()
+    print(f"C3 e8m0 bs={bs} rel_fro vs fp32 matmul {err:.2e}", flush=True)
+    assert err < EXACT
+    # the reference's own bound on the same comparison
+    assert torch.allclose(out, ref, atol=1e-3 * float(ref.abs().max()), rtol=0)
+
+
+def test_c3_4096_cubed_single_block64_against_torch_fp32(dev):
+    """configs[2]'s single-component block-64 FP8 GEMM at full size (4096^3,
+    int8 exponents on both operands) against torch's fp32 matmul of the
+    dequantised operands."""
+    M = N = K_ = 4096
+    bs = 64
+    g = torch.Generator(device=dev).manual_seed(7)
+    x = torch.randn(M, K_, device=dev, generator=g, dtype=torch.bfloat16)
+    w = torch.randn(N, K_, device=dev, generator=g, dtype=torch.bfloat16)
+    print("[c3 single] bs=64 4096^3", flush=True)
+    a, ea = K.block_quantize_fp8(x, bs)
+    b, eb = K.block_quantize_fp8(w, bs)
+    out = K.block_scaled_gemm(a, b, ea, eb, bs)
+    ref = K.block_dequantize_fp8(a, ea, bs) @ K.block_dequantize_fp8(b, eb, bs).t()
+    err = (torch.linalg.norm(out - ref) / torch.linalg.norm(ref)).item()
+    print(f"C3 single block-64 rel_fro vs fp32 matmul {err:.2e}", flush=True)
+    assert err < EXACT

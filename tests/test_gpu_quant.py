@@ -210,10 +210,13 @@ def _cand_case(name, shape, g):
         w[7, 11] = float("nan")
     elif name == "inf":
         w[2, 9] = float("inf")
+    elif name == "zerohead":     # a zero first quarter (zero-initialised rows)
+        w[: shape[0] // 4] = 0.0
     return w
 
 
-@pytest.mark.parametrize("name", ["normal", "overflow", "exact", "outlier", "nan", "inf"])
+@pytest.mark.parametrize("name", ["normal", "overflow", "exact", "outlier", "nan", "inf",
+                                  "zerohead"])
 @pytest.mark.parametrize("shape,wdtype", [((4096, 2048), torch.float32),
                                           ((2049, 4097), torch.float32),
                                           ((4096, 2048), torch.bfloat16)])

@@ -51,9 +51,11 @@ def test_noalloc_dual_quant_matches_workspace_entry_point(wdtype, mode):
     stream = torch.cuda.current_stream(dev).cuda_stream
     ws = torch.empty(int(_hip.lib().tcfp_workspace_bytes()), dtype=torch.uint8, device=dev)
     g = torch.Generator().manual_seed(7)
-    # the second call is smaller, and its amax is far below the first's: a
-    # stale partial of the first call would change its scales
-    for shape, mag in (((4096, 1024), 1.0), ((300, 208), 0.01)):
+    # the first shape has 2^23 elements, so the candidate residual pass runs
+    # (its counts and partials also live in the static array); the second
+    # call is smaller, and its amax is far below the first's: a stale
+    # partial of the first call would change its scales
+    for shape, mag in (((4096, 2048), 1.0), ((300, 208), 0.01)):
         print(f"[noalloc] shape={shape} dtype={wdtype} mode={mode}", flush=True)
         W = (torch.randn(shape, generator=g) * mag).to(wdtype).to(dev)
         ef0 = (torch.randn(shape, generator=g) * 1e-3 * mag).to(dev)
@@ -75,6 +77,28 @@ def test_noalloc_dual_quant_matches_workspace_entry_point(wdtype, mode):
         # first call would be ~100x off); bf16 rounding of the scale allowed
         amax = (W.float() + (ef0 if mode == "ef" else 0)).abs().max().clamp(min=1e-12)
         assert float(b["inv_hi"]) == pytest.approx(float(amax) / 448.0, rel=2e-2)
+
+
+def test_noalloc_call_allocates_no_device_memory():
+    """After a warm-up call, further calls leave the device's free memory
+    (hipMemGetInfo, through torch.cuda.mem_get_info) unchanged: the entry
+    point allocates nothing, on the candidate path (2^23 elements) and the
+    plain one."""
+    dev = torch.device("cuda", 0)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    g = torch.Generator().manual_seed(11)
+    for shape in ((4096, 2048), (512, 384)):
+        print(f"[noalloc] allocation check shape={shape}", flush=True)
+        W = torch.randn(shape, generator=g).to(dev)
+        ef = torch.zeros(shape, device=dev)
+        o = _outputs(*shape, dev)
+        _call(True, W, ef, o, stream)
+        torch.cuda.synchronize()
+        free0 = torch.cuda.mem_get_info(dev)[0]
+        for _ in range(3):
+            _call(True, W, ef, o, stream)
+        torch.cuda.synchronize()
+        assert torch.cuda.mem_get_info(dev)[0] == free0, shape
 
 
 def test_noalloc_rejects_a_bad_shape_before_launching():
