@@ -1047,13 +1047,23 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && NS == 2 && BM <= 128 ? 2 : 1))
 // earlier load anyway; the E8M0 codes are formed at the end of the stage,
 // after the refill DMA, without a further wait (a wait there would also
 // wait for that DMA).
-template <int AF, int BF, typename OutT, int EPI = 0, int SCALE = 0, int ND = 8>
+template <int AF, int BF, typename OutT, int EPI = 0, int SCALE = 0, int ND = 8, int BNT = 128>
 __global__ __launch_bounds__(512, 1) void gemm_nt_persist_kernel(GemmArgs g) {
   constexpr bool F32OUT = std::is_same<OutT, float>::value;
   static_assert(EPI == 0 || F32OUT, "GELU epilogues write fp32");
   static_assert(SCALE == 0 || (SCALE == 1 && EPI == 0), "block exponents: plain epilogue only");
   constexpr int NACC = SCALE == 1 ? 1 : 2;
-  constexpr int NW = 8, BM = 256, BN = 128, NS = 2;
+  constexpr int NW = 8, BM = 256, BN = BNT, NS = 2;
+  // BN = 64 (EPI 2 only): the GELU derivative factors of the tile (256 x 64
+  // fp32, 64 KiB) are brought into LDS beside the two 48 KiB operand stages
+  // in pieces during the tile's K stages, so the epilogue reads them from
+  // LDS.  With the 256 x 128 tile (2 x 64 KiB of stages) there is no room
+  // for its 128 KiB of factors, and loading them in the epilogue, every CU
+  // at once, left the matrix cores idle: 8192 x 4096 x 1024 ran 120.9 us
+  // against 74.4 us with the loads taken out (timing copy).
+  constexpr bool DGL = BNT == 64;
+  static_assert(BNT == 128 || (BNT == 64 && EPI == 2 && SCALE == 0 && F32OUT),
+                "the 256 x 64 tile serves the GELU backward epilogue");
   constexpr int WM = NW / 2, TMW = BM / WM, MB = TMW / 32;
   constexpr int TNW = BN / 2, NB = TNW / 32, NF = 2 * NB;
   constexpr int SROWS = BM + 2 * BN;
@@ -1069,7 +1079,10 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persist_kernel(GemmArgs g) {
   // but 8192^3 784 -> 860 us (a DMA wave's 16 loads per stage arrive later
   // on long contractions); the dispatcher takes ND = 4 for K <= 4096.
   // Block exponents keep every wave loading (each loads its own exponents).
-  static_assert(ND == 8 || (ND == 4 && SCALE == 0), "DMA waves: all, or half with per-tensor scales");
+  // (BN = 64: six DMA waves of 64 rows each, four for the activation rows
+  // and one per weight slot)
+  static_assert(BNT == 128 ? (ND == 8 || (ND == 4 && SCALE == 0)) : ND == 6,
+                "DMA waves: all, or half with per-tensor scales; six for the 256 x 64 tile");
   constexpr int RPW = SROWS / ND;
   constexpr int DI = RPW / 8;
   constexpr int NP = NF * MB;
@@ -1078,13 +1091,12 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persist_kernel(GemmArgs g) {
   constexpr int RPI = 64 / CPR;    // rows per store instruction
   // store instructions per wave and tile
   constexpr int NST = F32OUT ? MB * NB * 4 : TMW / RPI;
-  static_assert(NW * TMW * RB <= STAGE, "epilogue staging must fit one operand buffer");
+  static_assert(F32OUT || NW * TMW * RB <= STAGE, "epilogue staging must fit one operand buffer");
   // (a DMA wave holds at most two stages' DMA and one tile's stores in flight)
   static_assert(NST + 2 * DI <= 63, "vmcnt immediate");
   // EPI 2's column partials: a wave's rows are one 64-row group, its two
   // m-blocks the group's halves
   static_assert(EPI != 2 || (TMW == kColGroup && MB == 2), "wave rows vs. column groups");
-  __shared__ __align__(16) uint8_t lds[NS * STAGE];
   // The tile's bias columns (block exponents): loaded at the top of stage
   // max(nt - 2, 0) by the first BN threads and stored here after that
   // stage's barrier (which waits for every earlier load), read by the
@@ -1095,7 +1107,13 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persist_kernel(GemmArgs g) {
   // direct loads: there the staging code measured 2-4% slower with fp32
   // output and ~1% slower at 4096^3 with bf16 output and no bias.
   constexpr bool kBiasLds = SCALE == 1;
-  __shared__ __align__(16) float bias_s[kBiasLds ? BN : 4];
+  // one LDS array: the operand stages, then the bias columns (block
+  // exponents), then the derivative factors (DGL)
+  constexpr int kBiasB = kBiasLds ? BN * 4 : 0;
+  constexpr int kDgB = DGL ? BM * BN * 4 : 0;
+  __shared__ __align__(16) uint8_t lds[NS * STAGE + kBiasB + kDgB];
+  float* const bias_s = reinterpret_cast<float*>(lds + NS * STAGE);
+  const float* const dgl = reinterpret_cast<const float*>(lds + NS * STAGE + kBiasB);
   // GELU epilogues: EPI 1 the lane's int / uint maxima of the h bits (the
   // amax rule's keys), EPI 2 its max |value| bits (in amx)
   uint32_t amx = 0;
@@ -1160,6 +1178,33 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persist_kernel(GemmArgs g) {
 #pragma unroll
     for (int i = 0; i < DI; ++i)
       dma16(rs, ((i & 1) ? voff1 : voff0) + uint32_t(i) * row8, soff, dst + i * 1024);
+  };
+  // DGL: the current tile's derivative factors into LDS.  Piece p (1 KiB:
+  // tile rows 4p .. 4p + 3, 16 lanes per row) lands at dgl + p KiB with
+  // each row's 16-byte chunk c at chunk c ^ (row & 15), so the epilogue's
+  // reads (32 rows, one chunk each) spread over every bank.  The waves that
+  // issue no operand DMA (ND .. NW - 1) load them: they wait for memory
+  // only at the tile's last barrier, so the pieces -- read from HBM -- have
+  // the whole tile to land.  (Issued by the DMA waves, each stage's barrier
+  // waited for that stage's pieces: no faster than the epilogue loads.)
+  // Wave ND + w issues pieces w, w + (NW - ND), ..., its k-th at stage
+  // k % (nt - 1).
+  constexpr int NDG = NW - ND;  // factor-loading waves
+  const uint32_t dg_lds0 = lds0 + uint32_t(NS * STAGE + kBiasB);
+  const uint32_t ldo_b = uint32_t(g.ldo) * 4u;
+  const int dg_np = (DGL && !dma_wave) ? (BM / 4 - (wave - ND) + NDG - 1) / NDG : 0;
+  const uint32_t dg_nrec = uint32_t(int64_t(BM - 1) * g.ldo * 4 + BN * 4);
+  auto issue_dg = [&](const v4i& rs, int t) {
+    if constexpr (DGL) {
+      const int span = nt - 1;  // nt >= 2
+      if (t >= span) return;
+      for (int k = t; k < dg_np; k += span) {
+        const int p = (wave - ND) + NDG * k;
+        const int row = 4 * p + (lane >> 4);
+        const uint32_t vo = uint32_t(row) * ldo_b + uint32_t(((lane & 15) ^ (row & 15)) * 16);
+        dma16(rs, vo, 0u, dg_lds0 + uint32_t(p) * 1024u);
+      }
+    }
   };
 
   int ro[2][2];
@@ -1284,12 +1329,15 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persist_kernel(GemmArgs g) {
   };
   // every DMA landed except the newest `keep` vector-memory operations
   // (the previous tile's output stores), every wave's LDS reads are done.
-  // A wave that issues no DMA waits for its LDS reads only.
-  auto sync_keep = [&](auto keep) {
+  // A wave that issues no operand DMA waits for its LDS reads only, except
+  // (DGL) at the tile's last barrier (`fin`), where its factor loads land.
+  auto sync_keep = [&](auto keep, bool fin) {
     constexpr int k = decltype(keep)::value;
     __builtin_amdgcn_sched_barrier(0);
     if (dma_wave)
       __builtin_amdgcn_s_waitcnt((k & 15) | (7 << 4) | ((k >> 4) << 14));
+    else if (DGL && fin)
+      __builtin_amdgcn_s_waitcnt(0 | (7 << 4));  // vmcnt(0) lgkmcnt(0)
     else
       __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0), vmcnt and expcnt untouched
     __builtin_amdgcn_s_barrier();
@@ -1326,6 +1374,8 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persist_kernel(GemmArgs g) {
   int cb0 = 0;  // buffer of the current tile's stage 0
   for (int it = 0; it < ntile; ++it) {
     const bool more = it + 1 < ntile;
+    v4i dgr{};
+    if constexpr (DGL) dgr = make_rsrc(g.aux + int64_t(m0) * g.ldo + n0, dg_nrec);
     v4i nxt = cur;
     EOff eo_n = eo;
     int m1 = 0, n1 = 0;
@@ -1358,9 +1408,9 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persist_kernel(GemmArgs g) {
       interleave_mfma_lds<NP / 2, 2 * (NF + MB), 0>();
       pin_range(0, NP / 2);
       if (t == 0 && it > 0)
-        sync_keep(std::integral_constant<int, NST>{});
+        sync_keep(std::integral_constant<int, NST>{}, t + 1 == nt);
       else
-        sync_keep(std::integral_constant<int, 0>{});
+        sync_keep(std::integral_constant<int, 0>{}, t + 1 == nt);
       hold_raw();
       if (bias_stage) bias_s[tid] = bv;
       mfmas_range(f0, 0, NP / 2, NP);
@@ -1372,6 +1422,7 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persist_kernel(GemmArgs g) {
         issue(nxt, 0, b);  // the next tile's stage 0
       else if (F32OUT && more)
         issue(nxt, 1, b);  // the next tile's stage 1 (no output staging)
+      issue_dg(dgr, t);
       __builtin_amdgcn_sched_barrier(0);
       // sub-step 0 of stage t + 1 (after the last stage: the next tile's
       // stage 0, landed at this barrier; stale and unused after the last
@@ -1399,9 +1450,16 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persist_kernel(GemmArgs g) {
           for (int j = 0; j < NB; ++j)
 #pragma unroll
             for (int gq = 0; gq < 4; ++gq) {
-              const int64_t o = int64_t(m0 + wm * TMW + i * 32 + lr) * g.ldo + nb + j * 32 +
-                                gq * 8 + lg * 4;
-              dv[(i * NB + j) * 4 + gq] = *reinterpret_cast<const float4*>(g.aux + o);
+              if constexpr (DGL) {
+                const int row = wm * TMW + i * 32 + lr;
+                const int c = (wn * TNW + j * 32 + gq * 8 + lg * 4) >> 2;
+                dv[(i * NB + j) * 4 + gq] =
+                    *reinterpret_cast<const float4*>(dgl + row * BN + ((c ^ (row & 15)) << 2));
+              } else {
+                const int64_t o = int64_t(m0 + wm * TMW + i * 32 + lr) * g.ldo + nb + j * 32 +
+                                  gq * 8 + lg * 4;
+                dv[(i * NB + j) * 4 + gq] = *reinterpret_cast<const float4*>(g.aux + o);
+              }
             }
         // g replaces the first accumulator set in place (the registers of
         // the second set and of the factors free up as they are consumed)
@@ -1441,19 +1499,29 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persist_kernel(GemmArgs g) {
             for (int r = 0; r < 16; ++r) ys[j * 16 + r] = acc[0][j][0][r] + acc[0][j][1][r];
           // halving folds over the 32 row lanes (lane bits 4 ... 0): each
           // step keeps half of the columns and adds the partner lane's
-          // values of them; lane lr ends with the group sum of column k = lr
+          // values of them (row distances 16 ... 1, as kColGroup's order
+          // sums them); with NB = 2 lane lr ends with the group sum of
+          // column lr, with NB = 1 (16 columns per lane half) the last step
+          // adds the partner's value of the same column and lanes lr, lr ^ 1
+          // both hold it
 #pragma unroll
           for (int d = 16, len = NB * 16; d >= 1; d >>= 1, len >>= 1) {
             const bool up = (lr & d) != 0;
+            if (len >= 2) {
 #pragma unroll
-            for (int k = 0; k < len / 2; ++k) {
-              const float give = up ? ys[k] : ys[k + len / 2];
-              const float keep = up ? ys[k + len / 2] : ys[k];
-              ys[k] = keep + __shfl_xor(give, d);
+              for (int k = 0; k < len / 2; ++k) {
+                const float give = up ? ys[k] : ys[k + len / 2];
+                const float keep = up ? ys[k + len / 2] : ys[k];
+                ys[k] = keep + __shfl_xor(give, d);
+              }
+            } else {
+              ys[0] = ys[0] + __shfl_xor(ys[0], d);
             }
           }
-          const int col = (lr >> 4) * 32 + ((lr >> 2) & 3) * 8 + lg * 4 + (lr & 3);
-          g.cs_part[int64_t((m0 + wm * TMW) / kColGroup) * N + nb + col] = ys[0];
+          const int col = NB == 2 ? (lr >> 4) * 32 + ((lr >> 2) & 3) * 8 + lg * 4 + (lr & 3)
+                                  : ((lr >> 3) & 3) * 8 + lg * 4 + ((lr >> 1) & 3);
+          if (NB == 2 || (lr & 1) == 0)
+            g.cs_part[int64_t((m0 + wm * TMW) / kColGroup) * N + nb + col] = ys[0];
         }
         // the next tile's first fragments (its stage 0 landed at the last
         // stage's barrier; stale and unused after the last tile)
@@ -1577,8 +1645,11 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persist_kernel(GemmArgs g) {
     n0 = n1;
   }
   if constexpr (EPI != 0) {
-    // the workgroup's partials (no DMA is in flight after the last tile)
-    __shared__ uint32_t wmax[2 * NW];
+    // the workgroup's partials (no DMA is in flight after the last tile; the
+    // barrier retires every wave's last LDS reads before the operand
+    // buffer takes the per-wave maxima)
+    uint32_t* const wmax = reinterpret_cast<uint32_t*>(lds);
+    __syncthreads();
 #pragma unroll
     for (int d = 32; d >= 1; d >>= 1) {
       amx = umax(amx, uint32_t(__shfl_xor(int(amx), d)));
@@ -1973,23 +2044,45 @@ extern "C" int tcfp_dual_gemm(const uint8_t* a, int a_fmt, int64_t lda, const ui
 namespace {
 
 // One GELU-epilogue persistent launch (EPI 1 or 2) for fp8 operand formats.
+// One GELU-epilogue persistent launch for the formats the fused MLP passes:
+// EPI 1 (layer 1's forward) E4M3 activations, EPI 2 (layer 2's dgrad) E5M2
+// gradients, E4M3 weights (other formats take the unfused path).  EPI 2
+// runs the 256 x 64 tile with its derivative factors in LDS when `narrow`
+// (tiles_n counts 64-column tiles then), else the 256 x 128 tile.
 template <int EPI>
-int launch_persist_gelu(int a_fmt, int b_fmt, const GemmArgs& ga, hipStream_t st) {
+int launch_persist_gelu(const GemmArgs& ga, bool narrow, hipStream_t st) {
   const unsigned grid = unsigned(num_cus());
-#define TCFP_PG(A, B)                                                               \
-  do {                                                                              \
-    if (ga.K <= kPersistHalfDmaMaxK)                                                \
-      gemm_nt_persist_kernel<A, B, float, EPI, 0, 4><<<grid, 512, 0, st>>>(ga);    \
-    else                                                                            \
-      gemm_nt_persist_kernel<A, B, float, EPI><<<grid, 512, 0, st>>>(ga);          \
-  } while (0)
-  if (a_fmt == TCFP_FP8_E4M3 && b_fmt == TCFP_FP8_E4M3) TCFP_PG(0, 0);
-  else if (a_fmt == TCFP_FP8_E5M2 && b_fmt == TCFP_FP8_E4M3) TCFP_PG(1, 0);
-  else if (a_fmt == TCFP_FP8_E4M3 && b_fmt == TCFP_FP8_E5M2) TCFP_PG(0, 1);
-  else if (a_fmt == TCFP_FP8_E5M2 && b_fmt == TCFP_FP8_E5M2) TCFP_PG(1, 1);
-  else return TCFP_ERR_DTYPE;
-#undef TCFP_PG
+  constexpr int AF = EPI == 1 ? TCFP_FP8_E4M3 : TCFP_FP8_E5M2;
+  bool done = false;
+  if constexpr (EPI == 2) {
+    if (narrow) {
+      gemm_nt_persist_kernel<AF, 0, float, EPI, 0, 6, 64><<<grid, 512, 0, st>>>(ga);
+      done = true;
+    }
+  }
+  if (done) {
+  } else if (ga.K <= kPersistHalfDmaMaxK)
+    gemm_nt_persist_kernel<AF, 0, float, EPI, 0, 4><<<grid, 512, 0, st>>>(ga);
+  else
+    gemm_nt_persist_kernel<AF, 0, float, EPI><<<grid, 512, 0, st>>>(ga);
   return hipGetLastError() == hipSuccess ? TCFP_OK : TCFP_ERR_HIP;
+}
+
+// The EPI 2 launch on the 256 x 64 tile: full tiles, more of them than CUs,
+// and every operand, output and factor span within a descriptor's reach;
+// contractions up to 2048 only.  Its main loop issues half the MFMAs per
+// barrier of the 256 x 128 tile's: measured in one process (bit-identical
+// results, call incl. the quantising pass), 8192 x 4096 x 1024 160.5 against
+// 163.8 us, 8192 x 4096 x 4096 357.4 against 310.2 us.
+bool dgelu_narrow_eligible(const GemmArgs& ga) {
+  if (g_tile_policy != 0) return false;
+  if (ga.M % 256 != 0 || ga.N % 64 != 0 || ga.K % kSK != 0 || ga.K <= kSK || ga.K > 2048)
+    return false;
+  if (ga.ldo % 8 != 0 || !al16(ga.out) || !al16(ga.aux)) return false;
+  if (int64_t(256) * ga.lda + ga.K >= kMaxSpan || int64_t(64) * ga.ldb + ga.K >= kMaxSpan ||
+      int64_t(255) * ga.ldo * 4 + 256 >= kMaxSpan)
+    return false;
+  return int64_t(ga.M / 256) * (ga.N / 64) > num_cus();
 }
 
 bool fp8_fmt_ok(int f) { return f == TCFP_FP8_E4M3 || f == TCFP_FP8_E5M2; }
@@ -2022,11 +2115,11 @@ extern "C" int tcfp_dual_gemm_gelu_quantize(const uint8_t* a, int a_fmt, int64_t
   uint32_t* keys = static_cast<uint32_t*>(workspace) + tcfp::max_parts();
   ga.part = keys;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (b_lo && fp8_fmt_ok(a_fmt) && fp8_fmt_ok(b_fmt) && m > 0 && persist_eligible(ga) &&
-      2 * num_cus() <= tcfp::max_parts()) {
+  if (b_lo && a_fmt == TCFP_FP8_E4M3 && b_fmt == TCFP_FP8_E4M3 && m > 0 &&
+      persist_eligible(ga) && 2 * num_cus() <= tcfp::max_parts()) {
     ga.tiles_m = int(m / 256);
     ga.tiles_n = int(n / 128);
-    const int r = launch_persist_gelu<1>(a_fmt, b_fmt, ga, st);
+    const int r = launch_persist_gelu<1>(ga, false, st);
     if (r != TCFP_OK) return r;
     return tcfp::gelu_quantize_from_keys(h, m, n, fp8_fmt, act, dgelu, q, q_t, inv_out,
                                          workspace, keys, num_cus(), stream);
@@ -2065,11 +2158,12 @@ extern "C" int tcfp_dual_gemm_dgelu_quantize_colsum(
   ga.part = static_cast<uint32_t*>(workspace);
   ga.cs_part = sums ? static_cast<float*>(colsum_ws) : nullptr;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (b_lo && fp8_fmt_ok(a_fmt) && fp8_fmt_ok(b_fmt) && m > 0 && persist_eligible(ga) &&
-      num_cus() <= tcfp::max_parts()) {
+  const bool narrow = dgelu_narrow_eligible(ga);
+  if (b_lo && a_fmt == TCFP_FP8_E5M2 && b_fmt == TCFP_FP8_E4M3 && m > 0 &&
+      (narrow || persist_eligible(ga)) && num_cus() <= tcfp::max_parts()) {
     ga.tiles_m = int(m / 256);
-    ga.tiles_n = int(n / 128);
-    int r = launch_persist_gelu<2>(a_fmt, b_fmt, ga, st);
+    ga.tiles_n = int(n / (narrow ? 64 : 128));
+    int r = launch_persist_gelu<2>(ga, narrow, st);
     if (r != TCFP_OK) return r;
     r = tcfp::quantize_with_parts(grad, TCFP_DTYPE_F32, m, n, fp8_fmt, q, q_t, inv_out, workspace,
                                   nullptr, nullptr, stream, num_cus(), false);

@@ -229,14 +229,14 @@ def test_gemm_epilogue_replaces_the_gelu_passes_at_c4(dev):
     fwd()
     torch.cuda.synchronize()  # the premise check has run
     names = _kernel_names(fwd)
-    assert any("gemm_nt_persist_kernel<0, 0, float, 1, 0, 4>" in n for n in names), names
+    assert any("gemm_nt_persist_kernel<0, 0, float, 1, 0, 4, 128>" in n for n in names), names
     assert not any("gelu_amax_kernel" in n or "amax_part_kernel" in n for n in names), names
     g8, hi2, lo2, g_inv, ih2, il2 = _fp8_layer(dev, 8192, 1024, 4096, seed=2,
                                                a_dtype=torch.float8_e5m2)
     dg = torch.rand(8192, 4096, device=dev)
     names = _kernel_names(lambda: K.dual_gemm_dgelu_quantize_colsum(
         g8, hi2, lo2, g_inv, ih2, il2, dg, transpose=True))
-    assert any("gemm_nt_persist_kernel<1, 0, float, 2, 0, 4>" in n for n in names), names
+    assert any("gemm_nt_persist_kernel<1, 0, float, 2, 0, 6, 64>" in n for n in names), names
     assert not any("amax" in n for n in names), names
 
 
@@ -372,3 +372,31 @@ def test_gelu_e5m2_and_colsum_e4m3_quantisation(dev, shape):
         assert np.array_equal(q_t.view(torch.uint8).cpu().numpy(), oc.T), tag
         assert float(inv.item()) == float(oinv), tag
         assert np.array_equal(cs.cpu().numpy(), oq.column_sums(xn)), tag
+
+
+@pytest.mark.parametrize("m,k,n", [(8192, 1024, 4096), (4096, 512, 2048), (2048, 256, 8192),
+                                   (8192, 2048, 4096)])
+def test_dgelu_epilogue_narrow_tile_matches_wide(dev, m, k, n):
+    """Layer 2's dgrad with the GELU backward in its epilogue: the 256 x 64
+    tile with the derivative factors brought into LDS during the K loop
+    (taken for K <= 2048) against the 256 x 128 tile that loads them in the
+    epilogue (tile policy "large"), bit for bit: gradient, codes, transposed
+    codes, inverse scale and bias column sums; and the kernel each takes."""
+    print(f"dgelu narrow vs wide {m}x{k}x{n}", flush=True)
+    a, hi, lo, a_inv, ih, il = _fp8_layer(dev, m, k, n, seed=m + 7 * k,
+                                          a_dtype=torch.float8_e5m2)
+    dg = torch.rand(m, n, generator=torch.Generator().manual_seed(n)).to(dev) * 1.2 - 0.15
+    run = lambda: K.dual_gemm_dgelu_quantize_colsum(a, hi, lo, a_inv, ih, il, dg,  # noqa: E731
+                                                    transpose=True, col_sum=True,
+                                                    return_grad=True)
+    names = _kernel_names(run)
+    assert any("gemm_nt_persist_kernel<1, 0, float, 2, 0, 6, 64>" in x for x in names), names
+    p = run()
+    try:
+        K.set_gemm_tile_policy("large")
+        assert not any(", 6, 64>" in x for x in _kernel_names(run))
+        q = run()
+    finally:
+        K.set_gemm_tile_policy("auto")
+    for x, y in zip(p, q):
+        assert torch.equal(bits(x), bits(y))
