@@ -61,7 +61,8 @@ size_t tcfp_workspace_bytes(void);
  * (tcfp/core.py:137-158), used for activations at tcfp/nn/__init__.py:390
  * and gradients at :494.
  *   scale_in  optional device fp32 scalar: use it instead of the amax rule.
- *   q         [rows, cols] fp8 codes.
+ *   q         [rows, cols] fp8 codes; may be NULL when q_t is given and
+ *             cols % 8 == 0 (only the transposed copy is written).
  *   q_t       optional [cols, rows] transposed codes (wgrad operand).
  *   scale_out optional device fp32 scalar receiving the scale used.
  *   inv_out   device fp32 scalar receiving 1/scale.
@@ -195,8 +196,10 @@ int tcfp_gelu_amax_rule_status(int* checked, int* holds, float* bound);
  *   torch's GELU backward of tcfp_dual_gemm's output, bit for bit;
  *   q (+ q_t) / inv_out / col_sum: grad quantised as
  *   tcfp_quantize_per_tensor_colsum quantises it.
- * n % 8 == 0; col_sum may be NULL; colsum_ws as for
- * tcfp_quantize_per_tensor_colsum.  On the persistent launch's shapes the
+ * n % 8 == 0; col_sum may be NULL; q may be NULL when q_t is given;
+ * colsum_ws as for tcfp_quantize_per_tensor_colsum.  On the persistent
+ * launch's shapes (the 256 x 64 tile with the factors staged in LDS for
+ * k <= 2048, else the 256 x 128 tile) the
  * epilogue writes grad with its per-workgroup maxima and 64-row column
  * partials; otherwise the GEMM, a multiply-and-amax pass and the
  * quantising pass run in turn.  Same bits either way. */
@@ -208,6 +211,51 @@ int tcfp_dual_gemm_dgelu_quantize_colsum(const uint8_t* a, int a_fmt, int64_t ld
                                          uint8_t* q, uint8_t* q_t, float* inv_out,
                                          float* col_sum, void* workspace, void* colsum_ws,
                                          size_t colsum_ws_bytes, void* stream);
+
+/* ---- batched per-tensor quantisation ------------------------------------ */
+
+#define TCFP_JOB_DUAL 0 /* dual quantisation of a weight (W + EF -> W_hi, W_lo)  */
+#define TCFP_JOB_ACT 1  /* per-tensor quantisation of an activation / gradient */
+
+/* One tensor of tcfp_quantize_batch.  x [rows, cols] (f32 or bf16),
+ * cols % 8 == 0, rows, cols > 0.
+ *   TCFP_JOB_DUAL: as tcfp_dual_quantize_per_tensor without stochastic
+ *     rounding: ef optional (updated in place when update_ef), q / q_lo the
+ *     W_hi / W_lo codes, inv / inv_lo their inverse scales, q_t / q_lo_t
+ *     optional transposed copies.
+ *   TCFP_JOB_ACT: as tcfp_quantize_per_tensor without an explicit scale:
+ *     fp8_fmt, q (may be NULL when q_t is given), q_t optional, inv. */
+typedef struct tcfp_quant_job {
+  int kind;
+  const void* x;
+  int x_dtype;
+  int64_t rows;
+  int64_t cols;
+  float* ef;
+  int update_ef;
+  int fp8_fmt;
+  uint8_t* q;
+  uint8_t* q_t;
+  float* inv;
+  uint8_t* q_lo;
+  uint8_t* q_lo_t;
+  float* inv_lo;
+} tcfp_quant_job;
+
+/* Workspace bytes tcfp_quantize_batch needs for `count` jobs. */
+size_t tcfp_quantize_batch_workspace_bytes(int count);
+
+/* Up to 4 independent per-tensor quantisations in three launches in all,
+ * instead of two (activation) or three (weight) each: the amax passes of
+ * every job share one launch, the W_hi passes of the weights a second, and
+ * the final passes (W_lo + EF + transposed codes; activation codes) a third.
+ * Results are those of the single-tensor entry points, bit for bit.  No
+ * reference counterpart: it serves TCFPMLP's forward, whose two weights and
+ * input the reference quantises one call at a time (tcfp/nn/__init__.py:
+ * 343-390, once per layer).  workspace: tcfp_quantize_batch_workspace_bytes
+ * (count) bytes, any contents; jobs must not alias each other's outputs. */
+int tcfp_quantize_batch(int count, const tcfp_quant_job* jobs, void* workspace,
+                        size_t workspace_bytes, void* stream);
 
 /* Tuning switch of tcfp_dual_quantize_per_tensor (and its workspace-free
  * variant) without delayed or NF-aware scaling, on tensors of 2^23 elements

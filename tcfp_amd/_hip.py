@@ -25,6 +25,21 @@ _i32 = ctypes.c_int
 _u32 = ctypes.c_uint32
 _u64 = ctypes.c_uint64
 
+JOB_DUAL = 0
+JOB_ACT = 1
+
+
+class QuantJob(ctypes.Structure):
+    """``tcfp_quant_job`` (include/tcfp_hip.h): one tensor of
+    ``tcfp_quantize_batch``."""
+
+    _fields_ = [
+        ("kind", _i32), ("x", _c_void_p), ("x_dtype", _i32), ("rows", _i64), ("cols", _i64),
+        ("ef", _c_void_p), ("update_ef", _i32), ("fp8_fmt", _i32), ("q", _c_void_p),
+        ("q_t", _c_void_p), ("inv", _c_void_p), ("q_lo", _c_void_p), ("q_lo_t", _c_void_p),
+        ("inv_lo", _c_void_p),
+    ]
+
 # name -> argtypes (all return int status unless listed in _RESTYPE)
 _SIGNATURES = {
     "tcfp_status_string": [_i32],
@@ -120,6 +135,8 @@ _SIGNATURES = {
     "tcfp_block_wgrad_presplit": [_c_void_p, _i64, _i64, _c_void_p, _i32, _c_void_p, _i64, _i32,
                                   _c_void_p, _c_void_p, ctypes.c_size_t, _c_void_p],
     "tcfp_block_wgrad_presplit_workspace_bytes": [_i64, _i64, _i64],
+    "tcfp_quantize_batch_workspace_bytes": [_i32],
+    "tcfp_quantize_batch": [_i32, ctypes.POINTER(QuantJob), _c_void_p, ctypes.c_size_t, _c_void_p],
     "tcfp_gemm_set_tile_policy": [_i32],
     "tcfp_dual_quantize_set_candidates": [_i32],
     "tcfp_transpose_u8": [_c_void_p, _i64, _i64, _c_void_p, _c_void_p],
@@ -136,6 +153,7 @@ _RESTYPE = {
     "tcfp_block_grad_prep_workspace_bytes": ctypes.c_size_t,
     "tcfp_block_dual_gemm_dx_bf16_workspace_bytes": ctypes.c_size_t,
     "tcfp_block_wgrad_presplit_workspace_bytes": ctypes.c_size_t,
+    "tcfp_quantize_batch_workspace_bytes": ctypes.c_size_t,
 }
 
 _lib = None
@@ -223,6 +241,24 @@ def workspace(device: torch.device) -> torch.Tensor:
         nbytes = int(lib().tcfp_workspace_bytes())
         ws = torch.zeros(nbytes, dtype=torch.uint8, device=device)
         _ws[key] = ws
+    return ws
+
+
+_bws: dict[tuple[int, int], torch.Tensor] = {}
+MAX_BATCH_JOBS = 4
+
+
+def batch_workspace(device: torch.device) -> torch.Tensor:
+    """``tcfp_quantize_batch``'s reduction scratch (room for its largest
+    batch) for the current stream of ``device``; stream order makes one per
+    (device, stream) safe."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    key = (idx, stream_of(device))
+    ws = _bws.get(key)
+    if ws is None:
+        nbytes = int(lib().tcfp_quantize_batch_workspace_bytes(MAX_BATCH_JOBS))
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=device)
+        _bws[key] = ws
     return ws
 
 

@@ -1068,21 +1068,14 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persist_kernel(GemmArgs g) {
   constexpr int TNW = BN / 2, NB = TNW / 32, NF = 2 * NB;
   constexpr int SROWS = BM + 2 * BN;
   constexpr int STAGE = SROWS * kRowB;
-  // ND = waves that issue the operand DMA (8: all; 4: the first four, each
-  // with twice the rows).  vmcnt retires loads and stores in issue order, so
-  // a wave that stores its part of tile j's output and then refills a stage
-  // buffer for tile j + 1 waits for those stores at the next barrier; with
-  // ND = 4 the other four waves never wait for memory at a barrier and their
-  // stores drain while the next tile computes.  Measured in one process
-  // (bit-identical results): 4096^3 bf16 out 100.6 -> 98.9 us, 8192 x 4096 x
-  // 1024 fp32 out + bias 76.4 -> 75.0 us and with E5M2 A 72.3 -> 70.2 us,
-  // but 8192^3 784 -> 860 us (a DMA wave's 16 loads per stage arrive later
-  // on long contractions); the dispatcher takes ND = 4 for K <= 4096.
-  // Block exponents keep every wave loading (each loads its own exponents).
-  // (BN = 64: six DMA waves of 64 rows each, four for the activation rows
-  // and one per weight slot)
-  static_assert(BNT == 128 ? (ND == 8 || (ND == 4 && SCALE == 0)) : ND == 6,
-                "DMA waves: all, or half with per-tensor scales; six for the 256 x 64 tile");
+  // ND = waves that issue the operand DMA: all eight for the 256 x 128
+  // tile; six of 64 rows each for the 256 x 64 tile (four for the
+  // activation rows, one per weight slot), whose other two waves bring in
+  // the GELU derivative factors.  (Four DMA waves with twice the rows each,
+  // letting the other four waves' output stores drain past the barriers,
+  // gained <= 1 us on standalone 8192 x 4096 x 1024 GEMMs but cost 7 us per
+  // step of the fused MLP training step, measured in one process.)
+  static_assert(BNT == 128 ? ND == 8 : ND == 6, "DMA waves: all eight; six for the 256 x 64 tile");
   constexpr int RPW = SROWS / ND;
   constexpr int DI = RPW / 8;
   constexpr int NP = NF * MB;
@@ -1678,191 +1671,9 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persist_kernel(GemmArgs g) {
   }
 }
 
-// ---------------------------------------------------------------------------
-// Single FP8 GEMM with a long contraction and few output tiles (the FP8
-// wgrad: K = the token count, a [D_out, D_in] output of at most one 128 x
-// 128 tile per CU).  The four-wave 128 x 128 tile runs one wave per SIMD,
-// and nothing covers that wave's barrier and LDS waits.  Here eight waves
-// share the tile in two groups of four: group g computes the whole tile
-// over the K stages t with t % 2 == g, each wave a 64 x 64 block, so every
-// SIMD holds one wave of each group and a round (one stage per group, one
-// barrier) issues twice the MFMAs of a four-wave stage.  Four 32 KiB stage
-// buffers: a round's two stages plus the next round's, whose DMA is issued
-// half-way through the previous round.  At the end both groups' partial
-// tiles go to LDS and every wave sums a slice of rows (group 0's partial +
-// group 1's, in that order), scales and stores full 512-byte rows.
-// Full tiles only: M, N multiples of 128, K a multiple of 256.
-template <int AF, int BF>
-__global__ __launch_bounds__(512, 1) void gemm_nt_ksplit_kernel(GemmArgs g) {
-  constexpr int BM = 128, BN = 128;      // tile: activation ("A") rows x weight ("B") rows
-  constexpr int SROWS = BM + BN;
-  constexpr int STAGE = SROWS * kRowB;   // 32 KiB
-  constexpr int NBUF = 4;
-  constexpr int MB = 2, NB = 2;          // 32-row blocks per wave: A, B
-  constexpr int NFR = NB + MB;           // fragments per sub-step: [0, NB) B, [NB, NFR) A
-  constexpr int RPW = SROWS / 4;         // stage rows DMA'd by each wave of a group
-  constexpr int DI = RPW / 8;            // 1 KiB DMA instructions per wave and stage
-  static_assert(NBUF * STAGE >= 2 * BM * BN * 4, "the partial tiles must fit the stage buffers");
-  __shared__ __align__(16) uint8_t lds[NBUF * STAGE];
-
-  const int M = g.M, N = g.N, K = g.K;
-  const int T = g.tiles_m * g.tiles_n;
-  int l = blockIdx.x;
-  if ((T & 7) == 0) l = (l & 7) * (T >> 3) + (l >> 3);
-  constexpr int G = 4;
-  const int per_group = G * g.tiles_n;
-  const int first_m = (l / per_group) * G;
-  const int gm = min(g.tiles_m - first_m, G);
-  const int m0 = (first_m + (l % per_group) % gm) * BM;
-  const int n0 = ((l % per_group) / gm) * BN;
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int grp = wave >> 2, wq = wave & 3;
-  const int wm = wq >> 1, wn = wq & 1;
-  const int lr = lane & 31, lg = lane >> 5;
-
-  // DMA: wave wq of a group fills stage rows wq*RPW .. +RPW of its group's
-  // stages (rows [0, BM) activation, [BM, BM + BN) weight)
-  const int srow0 = wq * RPW;
-  const bool in_a = srow0 < BM;
-  const uint8_t* src = in_a ? g.A + int64_t(m0) * g.lda : g.B0 + int64_t(n0) * g.ldb;
-  const int64_t ld = in_a ? g.lda : g.ldb;
-  const int row_base = in_a ? srow0 : srow0 - BM;
-  const v4i rsrc = make_rsrc(src, uint32_t(int64_t((in_a ? BM : BN) - 1) * ld + K));
-  const int chunk0 = (lane & 7) ^ swz(lane >> 3);
-  const int chunk1 = (lane & 7) ^ swz(8 + (lane >> 3));
-  uint32_t voff[DI];
-#pragma unroll
-  for (int i = 0; i < DI; ++i)
-    voff[i] = uint32_t(int64_t(row_base + i * 8 + (lane >> 3)) * ld + ((i & 1) ? chunk1 : chunk0) * 16);
-  const uint32_t lds_base =
-      uint32_t(reinterpret_cast<uintptr_t>((TCFP_LDS uint8_t*)lds)) + uint32_t(srow0) * kRowB;
-  const int nr = K / (2 * kSK);  // rounds
-  // stage s = 2 r + grp of round r lives in buffer s % NBUF; past the last
-  // round the DMA reads nothing (every lane out of range)
-  auto issue = [&](int r) {
-    const int s = 2 * r + grp;
-    const bool live = r < nr;
-    const uint32_t dst = lds_base + uint32_t(s & (NBUF - 1)) * STAGE;
-    const uint32_t soff = uint32_t(live ? s : 0) * kSK;
-#pragma unroll
-    for (int i = 0; i < DI; ++i) dma16(rsrc, live ? voff[i] : kOob, soff, dst + i * 1024);
-  };
-
-  int ro[2][2];
-#pragma unroll
-  for (int h = 0; h < 2; ++h)
-#pragma unroll
-    for (int q = 0; q < 2; ++q) ro[h][q] = lr * kRowB + (((4 * h + lg + 2 * q) ^ swz(lr)) << 4);
-  auto read_frags = [&](v8i* f, int r, int h) {
-    const uint8_t* st = lds + ((2 * r + grp) & (NBUF - 1)) * STAGE;
-#pragma unroll
-    for (int q = 0; q < NB; ++q) {
-      const int rb = (BM + wn * 64 + q * 32) * kRowB;
-      f[q] = make_frag(lds_read16(st, rb + ro[h][0]), lds_read16(st, rb + ro[h][1]));
-    }
-#pragma unroll
-    for (int i = 0; i < MB; ++i) {
-      const int rb = (wm * 64 + i * 32) * kRowB;
-      f[NB + i] = make_frag(lds_read16(st, rb + ro[h][0]), lds_read16(st, rb + ro[h][1]));
-    }
-  };
-  v16f acc[NB][MB];
-#pragma unroll
-  for (int j = 0; j < NB; ++j)
-#pragma unroll
-    for (int i = 0; i < MB; ++i)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) acc[j][i][e] = 0.0f;
-  auto mfmas = [&](const v8i* f) {
-#pragma unroll
-    for (int i = 0; i < MB; ++i)
-#pragma unroll
-      for (int q = 0; q < NB; ++q) acc[q][i] = mfma_plain<BF, AF>(f[q], f[NB + i], acc[q][i]);
-  };
-  // every DMA this wave issued has landed and every wave's LDS reads are done
-  auto sync_all = [&]() {
-    __builtin_amdgcn_sched_barrier(0);
-    __builtin_amdgcn_s_waitcnt(0 | (7 << 4));  // vmcnt(0) lgkmcnt(0)
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_sched_barrier(0);
-  };
-
-  v8i f0[NFR], f1[NFR];
-  // prologue: rounds 0 and 1; wait for round 0 only
-  issue(0);
-  issue(1);
-  __builtin_amdgcn_s_waitcnt((DI & 15) | (7 << 4) | ((DI >> 4) << 14));
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-  read_frags(f0, 0, 0);
-  for (int r = 0; r < nr; ++r) {
-    read_frags(f1, r, 1);
-    mfmas(f0);
-    interleave_mfma_lds<NB * MB, 2 * NFR, 0>();
-    // round r + 1 landed, every wave has its round-r fragments: refill
-    // round r's buffers with round r + 2
-    sync_all();
-    issue(r + 2);
-    __builtin_amdgcn_sched_barrier(0);
-    read_frags(f0, r + 1, 0);  // (stale after the last round, never used)
-    mfmas(f1);
-    interleave_mfma_lds<NB * MB, 2 * NFR, 0>();
-  }
-
-  // ---- epilogue: both groups' partial tiles through LDS --------------------
-  // partial p of group grp: [BM rows][BN cols] fp32 at lds + grp * BM*BN*4,
-  // row r's 16-byte chunk c at chunk c ^ (r & 31)
-  constexpr int RB = BN * 4;           // bytes per partial row
-  constexpr int CPR = RB / 16;         // 32 chunks per row
-  sync_all();
-  float* part = reinterpret_cast<float*>(lds + grp * (BM * RB));
-#pragma unroll
-  for (int i = 0; i < MB; ++i)
-#pragma unroll
-    for (int j = 0; j < NB; ++j)
-#pragma unroll
-      for (int gq = 0; gq < 4; ++gq) {
-        const int row = wm * 64 + i * 32 + lr;
-        const int col = wn * 64 + j * 32 + gq * 8 + lg * 4;
-        const int ch = (col >> 2) ^ (row & (CPR - 1));
-        *reinterpret_cast<float4*>(part + row * BN + ch * 4) =
-            make_float4(acc[j][i][gq * 4], acc[j][i][gq * 4 + 1], acc[j][i][gq * 4 + 2],
-                        acc[j][i][gq * 4 + 3]);
-      }
-  __syncthreads();
-  const float cs = (g.s_a ? *g.s_a : 1.0f) * (g.s_0 ? *g.s_0 : 1.0f);
-  const float* p0 = reinterpret_cast<const float*>(lds);
-  const float* p1 = reinterpret_cast<const float*>(lds + BM * RB);
-  float* __restrict__ out = static_cast<float*>(g.out);
-  // wave w stores rows w*16 .. +16, two rows per instruction
-#pragma unroll
-  for (int it = 0; it < BM / 16; ++it) {
-    const int row = wave * (BM / 8) + it * 2 + (lane >> 5);
-    const int cl = lane & 31;
-    const int o = row * BN + ((cl ^ (row & (CPR - 1))) * 4);
-    const float4 a = *reinterpret_cast<const float4*>(p0 + o);
-    const float4 b = *reinterpret_cast<const float4*>(p1 + o);
-    float v[4] = {(a.x + b.x) * cs, (a.y + b.y) * cs, (a.z + b.z) * cs, (a.w + b.w) * cs};
-    const int n = n0 + cl * 4;
-    if (g.bias) {
-#pragma unroll
-      for (int q = 0; q < 4; ++q) v[q] += g.bias[n + q];
-    }
-    *reinterpret_cast<float4*>(out + int64_t(m0 + row) * g.ldo + n) = make_float4(v[0], v[1], v[2], v[3]);
-  }
-}
-
 // Largest byte span any DMA descriptor may cover (offsets are 32-bit and
 // the out-of-range sentinel must stay beyond every span).
 constexpr int64_t kMaxSpan = (int64_t(1) << 31) - (int64_t(1) << 20);
-
-// Contractions up to this length take the persistent per-tensor kernel with
-// four DMA waves (gemm_nt_persist_kernel's ND).
-constexpr int kPersistHalfDmaMaxK = 4096;
 
 // Tile policy: 0 = automatic, 1 = always 256 x 128, 2 = always 128 x 64,
 // 3 = 128 x 64 with eight waves in the one-round deep-pipeline case,
@@ -1899,22 +1710,6 @@ bool persist_eligible(const GemmArgs& ga) {
   return int64_t(ga.M / 256) * (ga.N / 128) > num_cus();
 }
 
-// The two-group split-K single GEMM (gemm_nt_ksplit_kernel, FP8 operands): fp32 output,
-// full 128 x 128 tiles, an even number of K stages (two per round), 16-byte
-// aligned output rows (tile policy automatic).
-template <bool SPLIT, typename OutT>
-bool ksplit_eligible(const GemmArgs& ga) {
-  if constexpr (!SPLIT || !std::is_same<OutT, float>::value) {
-    return false;
-  } else {
-    if (g_tile_policy != 0) return false;
-    if (ga.M % 128 != 0 || ga.N % 128 != 0 || ga.K % (2 * kSK) != 0 || ga.K < 2 * kSK)
-      return false;
-    if (ga.ldo % 4 != 0 || !al16(ga.out)) return false;
-    return int64_t(128) * ga.lda + ga.K < kMaxSpan && int64_t(128) * ga.ldb + ga.K < kMaxSpan;
-  }
-}
-
 template <int AF, int BF, bool SPLIT, typename OutT, int SCALE>
 int launch_gemm(GemmArgs ga, hipStream_t st) {
   const int m = ga.M, n = ga.N, k = ga.K;
@@ -1941,11 +1736,7 @@ int launch_gemm(GemmArgs ga, hipStream_t st) {
     const bool deep = SCALE == 0 && small && int64_t(grid.x) * splits <= num_cus();
     if (small && deep) {
       if constexpr (SCALE == 0) {
-        // (FP8 operands only: the two-group kernel has no bf16 MFMA path)
-        const bool ks = AF != kBF16 && splits == 1 && ksplit_eligible<SPLIT, OutT>(ga);
-        if (ks) {
-          if constexpr (AF != kBF16) gemm_nt_ksplit_kernel<AF, BF><<<grid, 512, 0, st>>>(ga);
-        } else if (g_tile_policy == 3)
+        if (g_tile_policy == 3)
           gemm_nt_dma_kernel<AF, BF, SPLIT, OutT, 8, 128, 64, SCALE, 4><<<grid, 512, 0, st>>>(ga);
         else
           gemm_nt_dma_kernel<AF, BF, SPLIT, OutT, 4, 128, 64, SCALE, 4><<<grid, 256, 0, st>>>(ga);
@@ -1970,13 +1761,8 @@ int launch_gemm(GemmArgs ga, hipStream_t st) {
         persist = persist_eligible(ga) &&
                   (SCALE == 0 || int64_t(ga.K >> ga.bs_shift) * (ga.M > ga.N ? ga.M : ga.N) <
                                      int64_t(INT32_MAX));
-        if (persist) {
-          if (SCALE == 0 && ga.K <= kPersistHalfDmaMaxK)
-            gemm_nt_persist_kernel<AF, BF, OutT, 0, SCALE, SCALE == 0 ? 4 : 8>
-                <<<unsigned(num_cus()), 512, 0, st>>>(ga);
-          else
-            gemm_nt_persist_kernel<AF, BF, OutT, 0, SCALE><<<unsigned(num_cus()), 512, 0, st>>>(ga);
-        }
+        if (persist)
+          gemm_nt_persist_kernel<AF, BF, OutT, 0, SCALE><<<unsigned(num_cus()), 512, 0, st>>>(ga);
       }
       if (!persist)
         gemm_nt_dma_kernel<AF, BF, SPLIT, OutT, 8, 256, 128, SCALE, 2><<<grid, 512, 0, st>>>(ga);
@@ -2060,11 +1846,7 @@ int launch_persist_gelu(const GemmArgs& ga, bool narrow, hipStream_t st) {
       done = true;
     }
   }
-  if (done) {
-  } else if (ga.K <= kPersistHalfDmaMaxK)
-    gemm_nt_persist_kernel<AF, 0, float, EPI, 0, 4><<<grid, 512, 0, st>>>(ga);
-  else
-    gemm_nt_persist_kernel<AF, 0, float, EPI><<<grid, 512, 0, st>>>(ga);
+  if (!done) gemm_nt_persist_kernel<AF, 0, float, EPI><<<grid, 512, 0, st>>>(ga);
   return hipGetLastError() == hipSuccess ? TCFP_OK : TCFP_ERR_HIP;
 }
 

@@ -185,9 +185,12 @@ TCFP_DEV float reduce_parts(const uint32_t* __restrict__ p, int g, uint32_t* red
 }
 
 // The scale a per-tensor consumer kernel works with: the explicit one, or
-// the amax rule over the partials.  Workgroup 0 publishes (scale, inv).
+// the amax rule over the partials.  Workgroup 0 publishes (scale, inv);
+// `bid` is the workgroup's index when a launch serves several tensors
+// (-1: blockIdx.x).
 TCFP_DEV float consumer_scale(const float* scale_in, const uint32_t* part, int g, bool bf16_rule,
-                              float fmax, float* scale_out, float* inv_out, uint32_t* red) {
+                              float fmax, float* scale_out, float* inv_out, uint32_t* red,
+                              int bid = -1) {
   float s, inv;
   if (scale_in) {
     s = *scale_in;
@@ -195,7 +198,7 @@ TCFP_DEV float consumer_scale(const float* scale_in, const uint32_t* part, int g
   } else {
     scale_from_amax(reduce_parts(part, g, red), bf16_rule, fmax, &s, &inv);
   }
-  if (blockIdx.x == 0 && threadIdx.x == 0) {
+  if ((bid < 0 ? int(blockIdx.x) : bid) == 0 && threadIdx.x == 0) {
     if (scale_out) *scale_out = s;
     if (inv_out) *inv_out = inv;
   }
@@ -321,14 +324,16 @@ TCFP_DEV void load_w8(const InT* __restrict__ x, const float* __restrict__ ef, i
 // sums of (v - v0) and (v - v0)^2 in fp64 to s1p / s2p, v0 being the first
 // element: the shift keeps the variance free of cancellation when the mean
 // is large against the spread.
+// (body: workgroup `bid` of `nbk`; a batched launch runs it for one of
+// several tensors)
 template <typename InT, bool HAS_EF, bool STATS>
-__global__ __launch_bounds__(kThreads) void amax_part_kernel(const InT* __restrict__ x,
+TCFP_DEV void amax_part_body(const InT* __restrict__ x,
                                                              const float* __restrict__ ef,
                                                              int64_t n, uint32_t* __restrict__ part,
                                                              double* __restrict__ s1p,
-                                                             double* __restrict__ s2p) {
-  __shared__ uint32_t red[kThreads / 64];
-  __shared__ double rd[2 * (kThreads / 64)];
+                                                             double* __restrict__ s2p,
+                                                             const int bid, const int nbk,
+                                                             uint32_t* red, double* rd) {
   uint32_t m = 0;
   double a1 = 0.0, a2 = 0.0, v0 = 0.0;
   if constexpr (STATS) {
@@ -347,8 +352,8 @@ __global__ __launch_bounds__(kThreads) void amax_part_kernel(const InT* __restri
     }
   };
   const int64_t nvec = n >> 3;
-  const int64_t stride = int64_t(gridDim.x) * kThreads;
-  int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+  const int64_t stride = int64_t(nbk) * kThreads;
+  int64_t i = int64_t(bid) * kThreads + threadIdx.x;
   for (; i + 3 * stride < nvec; i += 4 * stride) {
     float W[4][8], v[4][8];
 #pragma unroll
@@ -364,7 +369,7 @@ __global__ __launch_bounds__(kThreads) void amax_part_kernel(const InT* __restri
 #pragma unroll
     for (int j = 0; j < 8; ++j) acc(v[j]);
   }
-  for (int64_t t = nvec * 8 + int64_t(blockIdx.x) * kThreads + threadIdx.x; t < n; t += stride) {
+  for (int64_t t = nvec * 8 + int64_t(bid) * kThreads + threadIdx.x; t < n; t += stride) {
     float v = load1(x + t);
     if constexpr (HAS_EF) v = v + ef[t];
     acc(v);
@@ -375,12 +380,24 @@ __global__ __launch_bounds__(kThreads) void amax_part_kernel(const InT* __restri
     a2 = block_dsum_all(a2, rd + kThreads / 64);
   }
   if (threadIdx.x == 0) {
-    part[blockIdx.x] = m;
+    part[bid] = m;
     if constexpr (STATS) {
-      s1p[blockIdx.x] = a1;
-      s2p[blockIdx.x] = a2;
+      s1p[bid] = a1;
+      s2p[bid] = a2;
     }
   }
+}
+
+template <typename InT, bool HAS_EF, bool STATS>
+__global__ __launch_bounds__(kThreads) void amax_part_kernel(const InT* __restrict__ x,
+                                                             const float* __restrict__ ef,
+                                                             int64_t n, uint32_t* __restrict__ part,
+                                                             double* __restrict__ s1p,
+                                                             double* __restrict__ s2p) {
+  __shared__ uint32_t red[kThreads / 64];
+  __shared__ double rd[2 * (kThreads / 64)];
+  amax_part_body<InT, HAS_EF, STATS>(x, ef, n, part, s1p, s2p, int(blockIdx.x), int(gridDim.x),
+                                     red, rd);
 }
 
 // Pass 1 of the dual quantisation under the amax rule on large tensors: the
@@ -664,46 +681,55 @@ __global__ __launch_bounds__(kThreads) void gelu_premise_finalize_kernel() {
 }
 
 // The GELU amax rule on the keys of h's producer (keys[2 i], keys[2 i + 1],
-// i < n_keys): one workgroup writes rule[0] = 1 and rule[1] = the amax bits
-// when the rule applies, else rule[0] = 0.
-__global__ __launch_bounds__(kThreads) void gelu_rule_decide_kernel(
-    const uint32_t* __restrict__ keys, int n_keys, uint32_t* __restrict__ rule) {
-  __shared__ uint32_t red[kThreads / 64];
-  __shared__ uint32_t red2[kThreads / 64];
+// i < n_keys), then the partial maxima of |gelu(h)| for the quantising
+// pass, in one launch.  Every workgroup reduces the keys (2 * n_keys words,
+// L2 hits) to the same decision.  When the rule applies, workgroup 0 writes
+// the amax it gives to part[0] and the others 0 (no pass over h); otherwise
+// each workgroup takes its grid-stride share of h.  Workgroup 0 also
+// records the decision in rule[0] (1: applied) and rule[1] (its amax bits).
+__global__ __launch_bounds__(kGeluThreads) void gelu_amax_rule_kernel(
+    const uint32_t* __restrict__ keys, int n_keys, const float* __restrict__ h, int64_t n,
+    uint32_t* __restrict__ rule, uint32_t* __restrict__ part) {
+  __shared__ uint32_t red[kGeluThreads / 64];
+  __shared__ uint32_t red2[kGeluThreads / 64];
   uint32_t imax_biased = 0, umx = 0;  // int max kept as bits ^ 0x80000000 (unsigned order)
-  for (int i = threadIdx.x; i < n_keys; i += kThreads) {
+  for (int i = threadIdx.x; i < n_keys; i += kGeluThreads) {
     imax_biased = umax(imax_biased, keys[2 * i] ^ 0x80000000u);
     umx = umax(umx, keys[2 * i + 1]);
   }
-  imax_biased = block_umax_nt<kThreads>(imax_biased, red);
-  umx = block_umax_nt<kThreads>(umx, red2);
-  if (threadIdx.x != 0) return;
-  const uint32_t imax = imax_biased ^ 0x80000000u;
-  // the premise check ran on this device (agent scope)
-  const bool premises =
-      __hip_atomic_load(&g_gelu_premise.done, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) == 1u &&
-      __hip_atomic_load(&g_gelu_premise.violations, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-          0u;
-  bool ok = false;
-  uint32_t abits = 0;
-  if (premises && umx < kGeluKeyNegNanInf && int32_t(imax) >= 0 && imax <= kGeluKeyPosInf) {
-    abits = absbits(gelu_f32(__uint_as_float(imax)));
-    ok = abits >= __hip_atomic_load(&g_gelu_premise.t_bits, __ATOMIC_RELAXED,
-                                    __HIP_MEMORY_SCOPE_AGENT);
+  imax_biased = block_umax_nt<kGeluThreads>(imax_biased, red);
+  umx = block_umax_nt<kGeluThreads>(umx, red2);
+  // thread 0 decides and hands the decision to the workgroup through LDS
+  // (its acquire load of the premise flag invalidates caches: one per
+  // workgroup, not one per thread)
+  __shared__ uint32_t dec[2];
+  if (threadIdx.x == 0) {
+    const uint32_t imax = imax_biased ^ 0x80000000u;
+    // the premise check ran on this device (agent scope)
+    const bool premises =
+        __hip_atomic_load(&g_gelu_premise.done, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) ==
+            1u &&
+        __hip_atomic_load(&g_gelu_premise.violations, __ATOMIC_RELAXED,
+                          __HIP_MEMORY_SCOPE_AGENT) == 0u;
+    bool ok = false;
+    uint32_t abits = 0;
+    if (premises && umx < kGeluKeyNegNanInf && int32_t(imax) >= 0 && imax <= kGeluKeyPosInf) {
+      abits = absbits(gelu_f32(__uint_as_float(imax)));
+      ok = abits >= __hip_atomic_load(&g_gelu_premise.t_bits, __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT);
+    }
+    dec[0] = ok ? 1u : 0u;
+    dec[1] = abits;
+    if (blockIdx.x == 0) {
+      rule[0] = dec[0];
+      rule[1] = abits;
+    }
   }
-  rule[0] = ok ? 1u : 0u;
-  rule[1] = abits;
-}
-
-// Partial maxima of |gelu(h)| for the quantising pass: with the rule
-// (rule[0] == 1) workgroup 0 writes its amax and the others 0; otherwise
-// each workgroup takes its grid-stride share of h.
-__global__ __launch_bounds__(kGeluThreads) void gelu_amax_fallback_kernel(
-    const float* __restrict__ h, int64_t n, const uint32_t* __restrict__ rule,
-    uint32_t* __restrict__ part) {
-  __shared__ uint32_t red[kGeluThreads / 64];
-  if (rule[0] == 1u) {
-    if (threadIdx.x == 0) part[blockIdx.x] = blockIdx.x == 0 ? rule[1] : 0u;
+  __syncthreads();
+  const bool ok = dec[0] != 0u;
+  const uint32_t abits = dec[1];
+  if (ok) {
+    if (threadIdx.x == 0) part[blockIdx.x] = blockIdx.x == 0 ? abits : 0u;
     return;
   }
   uint32_t m = 0;
@@ -718,6 +744,7 @@ __global__ __launch_bounds__(kGeluThreads) void gelu_amax_fallback_kernel(
   for (int64_t t = nvec * 8 + int64_t(blockIdx.x) * kGeluThreads + threadIdx.x; t < n;
        t += stride)
     m = umax(m, absbits(gelu_f32(h[t])));
+  __syncthreads();  // red is reused
   m = block_umax_nt<kGeluThreads>(m, red);
   if (threadIdx.x == 0) part[blockIdx.x] = m;
 }
@@ -875,25 +902,25 @@ TCFP_DEV void loadvec<uint16_t>(const uint16_t* p, float* v) { load8(p, v); }
 // of kColGroup's definition (rows past the end count as +0).  The tile's
 // row lanes hold rows tr = pass * RPI + lane: the folds over row distances
 // of RPI and more stay in a lane's registers, the rest meet in LDS.
-// qt may be null (no transposed copy).
+// qt may be null (no transposed copy), and so may q when qt is not (only
+// the transposed copy is written).
+// (body: tile `bid`; nbk unused)
 template <typename InT, int FMT, bool GELU_IN = false, bool COLSUM = false>
-__global__ __launch_bounds__(kThreads) void quant_t_kernel(
+TCFP_DEV void quant_t_body(
     const InT* __restrict__ x, int64_t rows, int64_t cols, const uint32_t* __restrict__ part,
     int g, int bf16_rule, const float* __restrict__ scale_in, uint8_t* __restrict__ q,
     uint8_t* __restrict__ qt, float* scale_out, float* inv_out,
-    float* __restrict__ cs_part = nullptr, float* __restrict__ act_out = nullptr,
-    float* __restrict__ dg_out = nullptr) {
+    float* __restrict__ cs_part, float* __restrict__ act_out,
+    float* __restrict__ dg_out, const int bid, const int nbk, uint32_t* red, uint32_t* tile,
+    float* csum) {
   using TL = TileLoad<InT>;
   constexpr int VEC = TL::VEC;
-  __shared__ uint32_t red[kThreads / 64];
-  __shared__ uint32_t tile[kTile * kTilePitch];
   // passes per half row group; the tile's two row groups, RPI row lanes each
   constexpr int PH = kColHalf / TL::RPI;
   static_assert(PH >= 1 && kTile == 2 * kColGroup, "row lanes per pass vs. row groups");
-  __shared__ float csum[COLSUM ? 2 * TL::RPI * kTile : 1];
   const float mx = FMT == TCFP_FP8_E5M2 ? kE5M2Max : kE4M3Max;
-  const float s = consumer_scale(scale_in, part, g, bf16_rule != 0, mx, scale_out, inv_out, red);
-  const TileGeom tg(cols);
+  const float s = consumer_scale(scale_in, part, g, bf16_rule != 0, mx, scale_out, inv_out, red, bid);
+  const TileGeom tg(cols, bid);
   const int tc = (threadIdx.x % TL::TPR) * VEC;
   const int rl = threadIdx.x / TL::TPR;
   const int64_t c = tg.c0 + tc;
@@ -950,7 +977,7 @@ __global__ __launch_bounds__(kThreads) void quant_t_kernel(
     uint32_t wd[VEC / 4];
 #pragma unroll
     for (int j = 0; j < VEC; j += 4) wd[j / 4] = encode4<FMT>(v[j], v[j + 1], v[j + 2], v[j + 3]);
-    if (valid) {
+    if (valid && q) {
       if constexpr (VEC == 4) *reinterpret_cast<uint32_t*>(q + r * cols + c) = wd[0];
       else *reinterpret_cast<uint2*>(q + r * cols + c) = make_uint2(wd[0], wd[1]);
     }
@@ -975,6 +1002,21 @@ __global__ __launch_bounds__(kThreads) void quant_t_kernel(
     if (cc < cols && r < rows) cs_part[(r / kColGroup) * cols + cc] = w[0];
   }
   if (qt) store_transposed(tile, tg, rows, cols, qt, threadIdx.x);
+}
+
+template <typename InT, int FMT, bool GELU_IN = false, bool COLSUM = false>
+__global__ __launch_bounds__(kThreads) void quant_t_kernel(
+    const InT* __restrict__ x, int64_t rows, int64_t cols, const uint32_t* __restrict__ part,
+    int g, int bf16_rule, const float* __restrict__ scale_in, uint8_t* __restrict__ q,
+    uint8_t* __restrict__ qt, float* scale_out, float* inv_out,
+    float* __restrict__ cs_part = nullptr, float* __restrict__ act_out = nullptr,
+    float* __restrict__ dg_out = nullptr) {
+  __shared__ uint32_t red[kThreads / 64];
+  __shared__ uint32_t tile[kTile * kTilePitch];
+  __shared__ float csum[COLSUM ? 2 * TileLoad<InT>::RPI * kTile : 1];
+  quant_t_body<InT, FMT, GELU_IN, COLSUM>(x, rows, cols, part, g, bf16_rule, scale_in, q, qt,
+                                          scale_out, inv_out, cs_part, act_out, dg_out,
+                                          int(blockIdx.x), int(gridDim.x), red, tile, csum);
 }
 
 // ===========================================================================
@@ -1086,20 +1128,19 @@ __global__ __launch_bounds__(kThreads) void cand_resid_kernel(
 }
 
 // Pass 2: W_hi codes and the partial max |residual| (partials b).
+// (body: workgroup `bid` of `nbk`)
 template <typename InT, bool HAS_EF>
-__global__ __launch_bounds__(kThreads) void dualq_hi_kernel(
+TCFP_DEV void dualq_hi_body(
     const InT* __restrict__ w, const float* __restrict__ ef, int64_t n,
     const uint32_t* __restrict__ pa, int ga, uint8_t* __restrict__ hi, uint32_t* __restrict__ pb,
     float* inv_hi_out, Delayed dl, HiRule hr, uint32_t k0, uint32_t k1, uint32_t o0,
-    uint32_t o1, float* tgt_out, const uint32_t* __restrict__ cand_b2 = nullptr, int gc = 0) {
-  __shared__ uint32_t red[kThreads / 64];
-  __shared__ uint32_t red2[kThreads / 64];
-  __shared__ double rd[2 * (kThreads / 64)];
+    uint32_t o1, float* tgt_out, const uint32_t* __restrict__ cand_b2, int gc, const int bid,
+    const int nbk, uint32_t* red, uint32_t* red2, double* rd) {
   float s_hi, inv_hi;
   {
     const float tgt = hi_target(hr, pa, ga, red, rd);
     scale_of(dl.on ? delayed_amax(dl, tgt) : tgt, kE4M3Max, &s_hi, &inv_hi);
-    if (blockIdx.x == 0 && threadIdx.x == 0) {
+    if (bid == 0 && threadIdx.x == 0) {
       *inv_hi_out = inv_hi;
       *tgt_out = tgt;
     }
@@ -1110,7 +1151,7 @@ __global__ __launch_bounds__(kThreads) void dualq_hi_kernel(
   const bool sr = hr.sr != 0;
   uint32_t m = 0;
   const int64_t nvec = n >> 3;
-  const int64_t stride = int64_t(gridDim.x) * kThreads;
+  const int64_t stride = int64_t(nbk) * kThreads;
   auto body = [&](const float v[8], int64_t i) {
     float c[8];
 #pragma unroll
@@ -1127,7 +1168,7 @@ __global__ __launch_bounds__(kThreads) void dualq_hi_kernel(
   // the same index in both passes, i.e. on the same XCD (workgroup b runs on
   // XCD b % 8), so the slabs pass 1 read last are still in that XCD's L2
   // when this pass starts; pass 3 goes first to last again.
-  const int64_t i0 = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+  const int64_t i0 = int64_t(bid) * kThreads + threadIdx.x;
   int64_t i = i0 < nvec ? i0 + ((nvec - 1 - i0) / stride) * stride : -1;
   for (; i - stride >= i0; i -= 2 * stride) {
     float W[2][8], v[2][8];
@@ -1141,7 +1182,7 @@ __global__ __launch_bounds__(kThreads) void dualq_hi_kernel(
     load_w8<InT, HAS_EF>(w, ef, i, W, v);
     body(v, i);
   }
-  for (int64_t t = nvec * 8 + int64_t(blockIdx.x) * kThreads + threadIdx.x; t < n; t += stride) {
+  for (int64_t t = nvec * 8 + int64_t(bid) * kThreads + threadIdx.x; t < n; t += stride) {
     float v = load1(w + t);
     if constexpr (HAS_EF) v = v + ef[t];
     const uint32_t code = hi_code1(clampf(v * s_hi, kE4M3Max), t, sr, k0, k1, o0, o1);
@@ -1149,7 +1190,21 @@ __global__ __launch_bounds__(kThreads) void dualq_hi_kernel(
     m = umax(m, absbits(v - e4m3_to_f32(code) * inv_hi));
   }
   m = block_umax_all(m, red2);
-  if (threadIdx.x == 0) pb[blockIdx.x] = m;
+  if (threadIdx.x == 0) pb[bid] = m;
+}
+
+template <typename InT, bool HAS_EF>
+__global__ __launch_bounds__(kThreads) void dualq_hi_kernel(
+    const InT* __restrict__ w, const float* __restrict__ ef, int64_t n,
+    const uint32_t* __restrict__ pa, int ga, uint8_t* __restrict__ hi, uint32_t* __restrict__ pb,
+    float* inv_hi_out, Delayed dl, HiRule hr, uint32_t k0, uint32_t k1, uint32_t o0,
+    uint32_t o1, float* tgt_out, const uint32_t* __restrict__ cand_b2 = nullptr, int gc = 0) {
+  __shared__ uint32_t red[kThreads / 64];
+  __shared__ uint32_t red2[kThreads / 64];
+  __shared__ double rd[2 * (kThreads / 64)];
+  dualq_hi_body<InT, HAS_EF>(w, ef, n, pa, ga, hi, pb, inv_hi_out, dl, hr, k0, k1, o0, o1,
+                             tgt_out, cand_b2, gc, int(blockIdx.x), int(gridDim.x), red, red2,
+                             rd);
 }
 
 // W_lo codes of 4 consecutive elements starting at flat element `e0`
@@ -1204,14 +1259,14 @@ TCFP_DEV void dual_codes4(const float W[4], const float v[4], const DualScales& 
 TCFP_DEV DualScales dual_scales(const HiRule& hr, const float* tgt_in, const uint32_t* pa, int ga,
                                 const uint32_t* pb, int gb, float* inv_lo_out, uint32_t* red,
                                 uint32_t* red2, double* rd, const uint32_t* pb2 = nullptr,
-                                int gc = 0) {
+                                int gc = 0, int bid = -1) {
   DualScales sc;
   scale_of(tgt_in ? *tgt_in : hi_target(hr, pa, ga, red, rd), kE4M3Max, &sc.s_hi, &sc.inv_hi);
   if (pb2 && cand_decisive(pa, ga, pb2, gc, sc.inv_hi, red, red2)) {
     pb = pb2;
     gb = gc;
   }
-  sc.s_lo = consumer_scale(nullptr, pb, gb, false, kE4M3Max, nullptr, inv_lo_out, red2);
+  sc.s_lo = consumer_scale(nullptr, pb, gb, false, kE4M3Max, nullptr, inv_lo_out, red2, bid);
   sc.inv_lo = __fdiv_rn(1.0f, sc.s_lo);
   return sc;
 }
@@ -1224,7 +1279,7 @@ TCFP_DEV DualScales dual_scales(const HiRule& hr, const float* tgt_in, const uin
 TCFP_DEV DualScales dual_scales_delayed(const Delayed& d, const HiRule& hr, const float* tgt_in,
                                         const uint32_t* pa, int ga, const uint32_t* pb, int gb,
                                         float* inv_hi_out, float* inv_lo_out, uint32_t* red,
-                                        uint32_t* red2, double* rd) {
+                                        uint32_t* red2, double* rd, int bid = -1) {
   DualScales sc;
   const float del = delayed_amax(d, tgt_in ? *tgt_in : hi_target(hr, pa, ga, red, rd));
   scale_of(del, kE4M3Max, &sc.s_hi, &sc.inv_hi);
@@ -1238,7 +1293,7 @@ TCFP_DEV DualScales dual_scales_delayed(const Delayed& d, const HiRule& hr, cons
                             1e-12f);
   }
   scale_of(lo_amax, kE4M3Max, &sc.s_lo, &sc.inv_lo);
-  if (blockIdx.x == 0 && threadIdx.x == 0) {
+  if ((bid < 0 ? int(blockIdx.x) : bid) == 0 && threadIdx.x == 0) {
     *inv_hi_out = sc.inv_hi;
     *inv_lo_out = sc.inv_lo;
     *d.amax_out = del;
@@ -1310,27 +1365,24 @@ __global__ __launch_bounds__(kThreads) void dualq_lo_kernel(
 
 // Pass 3 (tiled, cols % 8 == 0): as dualq_lo_kernel on 128 x 128 tiles, and
 // also writes the transposed W_hi and W_lo codes (the dgrad operands).
+// (body: tile `bid`; nbk unused)
 template <typename InT, bool HAS_EF, bool UPDATE, bool SR>
-__global__ __launch_bounds__(kThreads) void dualq_lo_t_kernel(
+TCFP_DEV void dualq_lo_t_body(
     const InT* __restrict__ w, float* __restrict__ ef, int64_t rows, int64_t cols,
     const uint32_t* __restrict__ pa, int ga, const uint32_t* __restrict__ pb, int gb,
     uint8_t* __restrict__ lo, float* inv_lo_out, uint8_t* __restrict__ hi_t,
     uint8_t* __restrict__ lo_t, uint32_t k0, uint32_t k1, uint32_t off0, uint32_t off1,
     Delayed dl, float* inv_hi_out, uint8_t* __restrict__ hi, HiRule hr, const float* tgt_in,
-    const uint32_t* pb2, int gc) {
+    const uint32_t* pb2, int gc, const int bid, const int nbk, uint32_t* red, uint32_t* red2,
+    double* rd, uint32_t* tile_h, uint32_t* tile_l) {
   using TL = TileLoad<InT>;
   constexpr int VEC = TL::VEC;
-  __shared__ uint32_t red[kThreads / 64];
-  __shared__ uint32_t red2[kThreads / 64];
-  __shared__ double rd[2 * (kThreads / 64)];
-  __shared__ uint32_t tile_h[kTile * kTilePitch];
-  __shared__ uint32_t tile_l[kTile * kTilePitch];
   const DualScales sc =
       dl.on ? dual_scales_delayed(dl, hr, tgt_in, pa, ga, pb, gb, inv_hi_out, inv_lo_out, red,
-                                  red2, rd)
-            : dual_scales(hr, tgt_in, pa, ga, pb, gb, inv_lo_out, red, red2, rd, pb2, gc);
+                                  red2, rd, bid)
+            : dual_scales(hr, tgt_in, pa, ga, pb, gb, inv_lo_out, red, red2, rd, pb2, gc, bid);
   const bool srh = hr.sr != 0;
-  const TileGeom tg(cols);
+  const TileGeom tg(cols, bid);
   const int tc = (threadIdx.x % TL::TPR) * VEC;
   const int64_t c = tg.c0 + tc;
 #pragma unroll 2
@@ -1393,6 +1445,25 @@ __global__ __launch_bounds__(kThreads) void dualq_lo_t_kernel(
   __syncthreads();
   if (hi_t) store_transposed(tile_h, tg, rows, cols, hi_t, threadIdx.x);
   if (lo_t) store_transposed(tile_l, tg, rows, cols, lo_t, threadIdx.x);
+}
+
+template <typename InT, bool HAS_EF, bool UPDATE, bool SR>
+__global__ __launch_bounds__(kThreads) void dualq_lo_t_kernel(
+    const InT* __restrict__ w, float* __restrict__ ef, int64_t rows, int64_t cols,
+    const uint32_t* __restrict__ pa, int ga, const uint32_t* __restrict__ pb, int gb,
+    uint8_t* __restrict__ lo, float* inv_lo_out, uint8_t* __restrict__ hi_t,
+    uint8_t* __restrict__ lo_t, uint32_t k0, uint32_t k1, uint32_t off0, uint32_t off1,
+    Delayed dl, float* inv_hi_out, uint8_t* __restrict__ hi, HiRule hr, const float* tgt_in,
+    const uint32_t* pb2, int gc) {
+  __shared__ uint32_t red[kThreads / 64];
+  __shared__ uint32_t red2[kThreads / 64];
+  __shared__ double rd[2 * (kThreads / 64)];
+  __shared__ uint32_t tile_h[kTile * kTilePitch];
+  __shared__ uint32_t tile_l[kTile * kTilePitch];
+  dualq_lo_t_body<InT, HAS_EF, UPDATE, SR>(w, ef, rows, cols, pa, ga, pb, gb, lo, inv_lo_out,
+                                           hi_t, lo_t, k0, k1, off0, off1, dl, inv_hi_out, hi,
+                                           hr, tgt_in, pb2, gc, int(blockIdx.x),
+                                           int(gridDim.x), red, red2, rd, tile_h, tile_l);
 }
 // ===========================================================================
 // Per-tensor stochastic rounding (to_fp8_e4m3_sr, tcfp/core.py:109-134)
@@ -2152,6 +2223,9 @@ int quantize_impl(const void* x, int x_dtype, int64_t rows, int64_t cols, int fp
   const int bfr = bf ? 1 : 0;
   const int64_t row_tiles = (rows + kTile - 1) / kTile;
   const bool tiled = (q_t || col_sum || gelu_in) && n > 0 && cols % 8 == 0;
+  // the codes may be left out only where the tiled pass writes the
+  // transposed copy instead
+  if (!q && n > 0 && !(tiled && q_t)) return TCFP_ERR_SHAPE;
   if (tiled) {
     const int64_t tiles = int64_t(row_tiles) * ((cols + kTile - 1) / kTile);
     if (!grid_x_fits(tiles, kThreads)) return TCFP_ERR_SHAPE;
@@ -2245,11 +2319,10 @@ int gelu_quantize_from_keys(const float* h, int64_t rows, int64_t cols, int fp8_
   hipStream_t st = static_cast<hipStream_t>(stream);
   launch_gelu_premise_once(st);
   PartWs* ws = static_cast<PartWs*>(workspace);
-  gelu_rule_decide_kernel<<<1, kThreads, 0, st>>>(keys, n_keys, ws->gelu_rule);
   // the full pass (rare) runs on a quarter of the usual grid: with the rule
   // every workgroup only writes its slot
   const int g = std::max(1, gelu_grid(n) / 4);
-  gelu_amax_fallback_kernel<<<g, kGeluThreads, 0, st>>>(h, n, ws->gelu_rule, ws->a);
+  gelu_amax_rule_kernel<<<g, kGeluThreads, 0, st>>>(keys, n_keys, h, n, ws->gelu_rule, ws->a);
   return quantize_impl(h, TCFP_DTYPE_F32, rows, cols, fp8_fmt, nullptr, q, q_t, nullptr, inv_out,
                        workspace, nullptr, nullptr, st, g, true, act, dgelu);
 }
@@ -2563,6 +2636,208 @@ int dual_quantize_impl(const void* w, int w_dtype, int64_t n, int64_t k, float* 
 }
 
 }  // namespace
+
+namespace {
+
+// ---- batched per-tensor quantisation (tcfp_quantize_batch) ----------------
+// Each job keeps its own reduction workspace; a launch's workgroups are split
+// among the jobs (job j owns [off[j], off[j + 1])) and each runs the
+// single-tensor pass's body on its share.  In the amax and W_hi passes every
+// job's share starts at a multiple of 8 workgroups, so a vector is handled
+// on the same XCD (workgroup b runs on XCD b % 8) in both passes, as in the
+// single-tensor launches.
+constexpr int kMaxBatchJobs = 4;
+struct BatchJob {
+  const void* x;
+  float* ef;
+  int64_t rows, cols;
+  int bf16, dual, has_ef, update, fmt;
+  uint8_t* q;
+  uint8_t* q_t;
+  float* inv;
+  uint8_t* q_lo;
+  uint8_t* q_lo_t;
+  float* inv_lo;
+  PartWs* ws;
+  int g1, g2;  // workgroups of the amax and W_hi passes
+};
+struct BatchArgs {
+  BatchJob j[kMaxBatchJobs];
+  int nj;
+  int off[3][kMaxBatchJobs + 1];  // per pass: each job's first workgroup; [nj] = grid
+};
+
+// the job that workgroup blockIdx.x of pass p serves, and its index there
+TCFP_DEV int batch_job(const BatchArgs& a, int p, int* bid) {
+  int j = 0;
+  while (j + 1 < a.nj && int(blockIdx.x) >= a.off[p][j + 1]) ++j;
+  *bid = int(blockIdx.x) - a.off[p][j];
+  return j;
+}
+
+__global__ __launch_bounds__(kThreads) void batch_amax_kernel(BatchArgs a) {
+  __shared__ uint32_t red[kThreads / 64];
+  __shared__ double rd[2 * (kThreads / 64)];
+  int bid;
+  const int j = batch_job(a, 0, &bid);
+  const BatchJob& b = a.j[j];
+  const int nbk = a.off[0][j + 1] - a.off[0][j];
+  if (bid >= b.g1) return;  // (the padding up to a multiple of 8)
+  const int64_t n = b.rows * b.cols;
+  if (b.bf16) {
+    const uint16_t* x = static_cast<const uint16_t*>(b.x);
+    if (b.has_ef) amax_part_body<uint16_t, true, false>(x, b.ef, n, b.ws->a, nullptr, nullptr, bid, b.g1, red, rd);
+    else amax_part_body<uint16_t, false, false>(x, nullptr, n, b.ws->a, nullptr, nullptr, bid, b.g1, red, rd);
+  } else {
+    const float* x = static_cast<const float*>(b.x);
+    if (b.has_ef) amax_part_body<float, true, false>(x, b.ef, n, b.ws->a, nullptr, nullptr, bid, b.g1, red, rd);
+    else amax_part_body<float, false, false>(x, nullptr, n, b.ws->a, nullptr, nullptr, bid, b.g1, red, rd);
+  }
+  (void)nbk;
+}
+
+__global__ __launch_bounds__(kThreads) void batch_hi_kernel(BatchArgs a) {
+  __shared__ uint32_t red[kThreads / 64];
+  __shared__ uint32_t red2[kThreads / 64];
+  __shared__ double rd[2 * (kThreads / 64)];
+  int bid;
+  const BatchJob& b = a.j[batch_job(a, 1, &bid)];
+  if (bid >= b.g2) return;
+  const int64_t n = b.rows * b.cols;
+  const Delayed off{};
+  const HiRule hr{};
+#define TCFP_BHI(T, EF)                                                                        \
+  dualq_hi_body<T, EF>(static_cast<const T*>(b.x), EF ? b.ef : nullptr, n, b.ws->a, b.g1, b.q, \
+                       b.ws->b, b.inv, off, hr, 0, 0, 0, 0, &b.ws->hi_tgt, nullptr, 0, bid,   \
+                       b.g2, red, red2, rd)
+  if (b.bf16) {
+    if (b.has_ef) TCFP_BHI(uint16_t, true); else TCFP_BHI(uint16_t, false);
+  } else {
+    if (b.has_ef) TCFP_BHI(float, true); else TCFP_BHI(float, false);
+  }
+#undef TCFP_BHI
+}
+
+__global__ __launch_bounds__(kThreads) void batch_final_kernel(BatchArgs a) {
+  __shared__ uint32_t red[kThreads / 64];
+  __shared__ uint32_t red2[kThreads / 64];
+  __shared__ double rd[2 * (kThreads / 64)];
+  __shared__ uint32_t tile_h[kTile * kTilePitch];
+  __shared__ uint32_t tile_l[kTile * kTilePitch];
+  int bid;
+  const int j = batch_job(a, 2, &bid);
+  const BatchJob& b = a.j[j];
+  const int nbk = a.off[2][j + 1] - a.off[2][j];
+  if (b.dual) {
+    const Delayed off{};
+    const HiRule hr{};
+#define TCFP_BLO(T, EF, UP)                                                                    \
+  dualq_lo_t_body<T, EF, UP, false>(static_cast<const T*>(b.x), EF ? b.ef : nullptr, b.rows,    \
+                                    b.cols, b.ws->a, b.g1, b.ws->b, b.g2, b.q_lo, b.inv_lo,     \
+                                    b.q_t, b.q_lo_t, 0, 0, 0, 0, off, nullptr, nullptr, hr,     \
+                                    &b.ws->hi_tgt, nullptr, 0, bid, nbk, red, red2, rd, tile_h, \
+                                    tile_l)
+    if (b.bf16) {
+      if (!b.has_ef) TCFP_BLO(uint16_t, false, false);
+      else if (b.update) TCFP_BLO(uint16_t, true, true);
+      else TCFP_BLO(uint16_t, true, false);
+    } else {
+      if (!b.has_ef) TCFP_BLO(float, false, false);
+      else if (b.update) TCFP_BLO(float, true, true);
+      else TCFP_BLO(float, true, false);
+    }
+#undef TCFP_BLO
+  } else {
+    float* const cs = reinterpret_cast<float*>(tile_l);  // (no column sums: unused)
+#define TCFP_BQ(T, F)                                                                          \
+  quant_t_body<T, F, false, false>(static_cast<const T*>(b.x), b.rows, b.cols, b.ws->a, b.g1,  \
+                                   b.bf16, nullptr, b.q, b.q_t, nullptr, b.inv, nullptr,       \
+                                   nullptr, nullptr, bid, nbk, red, tile_h, cs)
+    if (b.bf16) {
+      if (b.fmt == TCFP_FP8_E5M2) TCFP_BQ(uint16_t, TCFP_FP8_E5M2);
+      else TCFP_BQ(uint16_t, TCFP_FP8_E4M3);
+    } else {
+      if (b.fmt == TCFP_FP8_E5M2) TCFP_BQ(float, TCFP_FP8_E5M2);
+      else TCFP_BQ(float, TCFP_FP8_E4M3);
+    }
+#undef TCFP_BQ
+  }
+}
+
+size_t batch_ws_bytes(int count) {
+  return count > 0 ? size_t(count) * ((sizeof(PartWs) + 255) & ~size_t(255)) : 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t tcfp_quantize_batch_workspace_bytes(int count) {
+  return count < 1 || count > kMaxBatchJobs ? 0 : batch_ws_bytes(count);
+}
+
+int tcfp_quantize_batch(int count, const tcfp_quant_job* jobs, void* workspace,
+                        size_t workspace_bytes, void* stream) {
+  if (count < 1 || count > kMaxBatchJobs || !jobs) return TCFP_ERR_SHAPE;
+  if (!workspace || workspace_bytes < batch_ws_bytes(count)) return TCFP_ERR_WORKSPACE;
+  if (!aligned16(workspace)) return TCFP_ERR_ALIGN;
+  BatchArgs a{};
+  a.nj = count;
+  int o[3] = {0, 0, 0};
+  for (int j = 0; j < count; ++j) {
+    const tcfp_quant_job& s = jobs[j];
+    BatchJob& b = a.j[j];
+    if (s.kind != TCFP_JOB_DUAL && s.kind != TCFP_JOB_ACT) return TCFP_ERR_SHAPE;
+    if (s.rows <= 0 || s.cols <= 0 || s.cols % 8 != 0) return TCFP_ERR_SHAPE;
+    if (s.x_dtype != TCFP_DTYPE_F32 && s.x_dtype != TCFP_DTYPE_BF16) return TCFP_ERR_DTYPE;
+    if (!s.x || !s.inv || !aligned16(s.x) || (s.ef && !aligned16(s.ef))) return TCFP_ERR_ALIGN;
+    const bool dual = s.kind == TCFP_JOB_DUAL;
+    if (dual) {
+      if (!s.q || !s.q_lo || !s.inv_lo || !aligned16(s.q) || !aligned16(s.q_lo))
+        return TCFP_ERR_ALIGN;
+    } else {
+      if (s.fp8_fmt != TCFP_FP8_E4M3 && s.fp8_fmt != TCFP_FP8_E5M2) return TCFP_ERR_DTYPE;
+      if (!s.q && !s.q_t) return TCFP_ERR_SHAPE;
+      if (s.q && (reinterpret_cast<uintptr_t>(s.q) & 7u) != 0) return TCFP_ERR_ALIGN;
+    }
+    const int64_t n = s.rows * s.cols;
+    const int64_t tiles = ((s.rows + kTile - 1) / kTile) * ((s.cols + kTile - 1) / kTile);
+    b.x = s.x;
+    b.ef = dual ? s.ef : nullptr;
+    b.rows = s.rows;
+    b.cols = s.cols;
+    b.bf16 = s.x_dtype == TCFP_DTYPE_BF16 ? 1 : 0;
+    b.dual = dual ? 1 : 0;
+    b.has_ef = b.ef ? 1 : 0;
+    b.update = (b.ef && s.update_ef) ? 1 : 0;
+    b.fmt = s.fp8_fmt;
+    b.q = s.q;
+    b.q_t = s.q_t;
+    b.inv = s.inv;
+    b.q_lo = dual ? s.q_lo : nullptr;
+    b.q_lo_t = dual ? s.q_lo_t : nullptr;
+    b.inv_lo = dual ? s.inv_lo : nullptr;
+    b.ws = reinterpret_cast<PartWs*>(static_cast<uint8_t*>(workspace) +
+                                     size_t(j) * ((sizeof(PartWs) + 255) & ~size_t(255)));
+    b.g1 = parts_for((n + 7) / 8);
+    b.g2 = dual ? parts_for((n + 7) / 8) : 0;
+    a.off[0][j] = o[0];
+    a.off[1][j] = o[1];
+    a.off[2][j] = o[2];
+    o[0] += (b.g1 + 7) / 8 * 8;
+    o[1] += (b.g2 + 7) / 8 * 8;
+    if (tiles > INT32_MAX - o[2]) return TCFP_ERR_SHAPE;
+    o[2] += int(tiles);
+  }
+  for (int p = 0; p < 3; ++p) a.off[p][count] = o[p];
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  batch_amax_kernel<<<unsigned(o[0]), kThreads, 0, st>>>(a);
+  if (o[1] > 0) batch_hi_kernel<<<unsigned(o[1]), kThreads, 0, st>>>(a);
+  batch_final_kernel<<<unsigned(o[2]), kThreads, 0, st>>>(a);
+  return launch_status();
+}
+
+}  // extern "C"
 
 extern "C" {
 

@@ -386,6 +386,61 @@ def dual_quantize_per_tensor(
     return w_hi, w_lo, inv_hi, inv_lo
 
 
+def quantize_batch(dual=(), act=()):
+    """Several independent per-tensor quantisations in three launches in all
+    (``tcfp_quantize_batch``; no reference counterpart).
+
+    ``dual``: ``(weight, error_buf, update_ef, transposed)`` tuples, each
+    quantised as ``dual_quantize_per_tensor(weight, error_buf, update_ef,
+    transposed=transposed)`` (no stochastic rounding); ``act``: ``(x,
+    fp8_dtype, transpose)`` tuples, each as ``quantize_per_tensor(x,
+    fp8_dtype, transpose=transpose)`` (2-D ``x``).  Returns the two lists
+    of result tuples, bit for bit those calls' results.  Tensors the batch
+    does not take (empty, a last dimension not divisible by 8, more than
+    four in all) are quantised by those calls instead.
+    """
+    dual, act = list(dual), list(act)
+    fits = (0 < len(dual) + len(act) <= _hip.MAX_BATCH_JOBS
+            and all(w.dim() == 2 and w.numel() > 0 and w.shape[1] % 8 == 0 for w, *_ in dual)
+            and all(x.dim() == 2 and x.numel() > 0 and x.shape[1] % 8 == 0 for x, *_ in act))
+    if not fits:
+        return ([dual_quantize_per_tensor(w, e, u, transposed=t) for w, e, u, t in dual],
+                [quantize_per_tensor(x, f, transpose=t) for x, f, t in act])
+    dev = _hip.require_gpu(*[t for w, e, _, _ in dual for t in (w, e)],
+                           *[x for x, _, _ in act])
+    jobs = (_hip.QuantJob * (len(dual) + len(act)))()
+    res_d, res_a = [], []
+    for i, (w, e, u, t) in enumerate(dual):
+        w = w if w.is_contiguous() else w.contiguous()
+        n, k = w.shape
+        if e is not None:
+            assert e.dtype == torch.float32, "error_buf must be float32"
+            assert e.shape == (n, k), f"error_buf shape {tuple(e.shape)} != weight shape {(n, k)}"
+            assert e.is_contiguous(), "error_buf must be contiguous"
+        hi = torch.empty((n, k), dtype=torch.float8_e4m3fn, device=dev)
+        lo = torch.empty((n, k), dtype=torch.float8_e4m3fn, device=dev)
+        ih = torch.empty(1, dtype=torch.float32, device=dev)
+        il = torch.empty(1, dtype=torch.float32, device=dev)
+        ht = torch.empty((k, n), dtype=torch.float8_e4m3fn, device=dev) if t else None
+        lt = torch.empty((k, n), dtype=torch.float8_e4m3fn, device=dev) if t else None
+        jobs[i] = _hip.QuantJob(_hip.JOB_DUAL, ptr(w), _in_dtype(w), n, k, ptr(e), int(bool(u)),
+                                0, ptr(hi), ptr(ht), ptr(ih), ptr(lo), ptr(lt), ptr(il))
+        res_d.append((hi, lo, ih, il, ht, lt) if t else (hi, lo, ih, il))
+    for i, (x, f, t) in enumerate(act, start=len(dual)):
+        x = x if x.is_contiguous() else x.contiguous()
+        rows, cols = x.shape
+        q = torch.empty((rows, cols), dtype=f, device=dev)
+        qt = torch.empty((cols, rows), dtype=f, device=dev) if t else None
+        inv = torch.empty(1, dtype=torch.float32, device=dev)
+        jobs[i] = _hip.QuantJob(_hip.JOB_ACT, ptr(x), _in_dtype(x), rows, cols, None, 0, _fmt(f),
+                                ptr(q), ptr(qt), ptr(inv), None, None, None)
+        res_a.append((q, inv, qt) if t else (q, inv))
+    ws = _hip.batch_workspace(dev)
+    check(_hip.lib().tcfp_quantize_batch(len(jobs), jobs, ptr(ws), ws.numel(),
+                                         _hip.stream_of(dev)), "quantize_batch")
+    return res_d, res_a
+
+
 def _dual_quantize_nf(w, n, k, error_buf, update_ef, sigma_factor, stochastic_hi, stochastic_lo,
                       seed, prev, ratio_prev, decay, validate, amax_out, ratio_out, w_hi, w_lo,
                       inv_hi, inv_lo, w_hi_t, w_lo_t, dev) -> None:
@@ -646,6 +701,7 @@ def dual_gemm_dgelu_quantize_colsum(
     transpose: bool = False,
     col_sum: bool = True,
     return_grad: bool = False,
+    codes: bool = True,
 ):
     """The dgrad of the second layer of a TCFP -> GELU -> TCFP pair with the
     GELU backward in the GEMM's epilogue: ``g = (grad @ W) * dgelu``
@@ -658,8 +714,12 @@ def dual_gemm_dgelu_quantize_colsum(
     ``quantize_per_tensor_colsum``.
 
     Returns ``(q, inv)``, then ``q_t`` when ``transpose``, then the column
-    sums when ``col_sum``, then ``g`` when ``return_grad``.
+    sums when ``col_sum``, then ``g`` when ``return_grad``.  ``codes=False``
+    (with ``transpose``) writes only the transposed codes; ``q`` is then
+    None.
     """
+    if not codes and not transpose:
+        raise ValueError("codes=False needs transpose=True (the codes are written one way or both)")
     dev = _hip.require_gpu(grad_fp8, w_hi_t, w_lo_t, grad_inv, w_hi_inv, w_lo_inv, dgelu)
     a, b_hi, b_lo = _gemm_operands(grad_fp8, w_hi_t, w_lo_t)
     m, k = a.shape
@@ -671,7 +731,7 @@ def dual_gemm_dgelu_quantize_colsum(
         raise ValueError(f"column count ({n}) must be divisible by 8")
     dc = dgelu if dgelu.is_contiguous() else dgelu.contiguous()
     g = torch.empty((m, n), dtype=torch.float32, device=dev)
-    q = torch.empty((m, n), dtype=fp8_dtype, device=dev)
+    q = torch.empty((m, n), dtype=fp8_dtype, device=dev) if codes else None
     q_t = torch.empty((n, m), dtype=fp8_dtype, device=dev) if transpose else None
     inv = torch.empty(1, dtype=torch.float32, device=dev)
     cs = torch.empty(n, dtype=torch.float32, device=dev) if col_sum else None

@@ -551,16 +551,19 @@ class _TCFP12FusedMLPFunction(torch.autograd.Function):
         need_dx, need_dw1, need_db1, need_dw2, need_db2 = ctx.needs_input_grad[:5]
         need_h = need_dx or need_dw1 or need_db1  # a gradient flows into layer 1
 
-        # layer 1 (reference nn:343-425 with the default options)
+        # both layers' dual quantisation (nn:343-383) and layer 1's
+        # activation quantisation (nn:390): independent per-tensor
+        # quantisations, run as one batch (three launches in all)
         ef1 = _ef_buffer(st1, name1, w1)
-        res = K.dual_quantize_per_tensor(w1, ef1, update_ef=update_ef1, transposed=need_dx)
-        w1_hi, w1_lo, ih1, il1, w1_hi_t, w1_lo_t = res if need_dx else (*res, None, None)
+        ef2 = _ef_buffer(st2, name2, w2)
         input_shape = x.shape
         x2d = _flatten(x)
-        if need_dw1:
-            a1, a1_inv, a1_t = K.quantize_per_tensor(x2d, transpose=True)
-        else:
-            (a1, a1_inv), a1_t = K.quantize_per_tensor(x2d), None
+        (res, res2), (ra,) = K.quantize_batch(
+            dual=[(w1, ef1, update_ef1, need_dx), (w2, ef2, update_ef2, need_h)],
+            act=[(x2d, torch.float8_e4m3fn, need_dw1)],
+        )
+        w1_hi, w1_lo, ih1, il1, w1_hi_t, w1_lo_t = res if need_dx else (*res, None, None)
+        a1, a1_inv, a1_t = ra if need_dw1 else (*ra, None)
         # layer 1's GEMM, whose epilogue records max h for the GELU's amax,
         # then layer 2's activation quantisation (nn:390 on gelu(h)), which
         # also writes the GELU derivative factors the backward needs
@@ -571,9 +574,7 @@ class _TCFP12FusedMLPFunction(torch.autograd.Function):
         dgelu = res[-1] if need_h else None
 
         # layer 2
-        ef2 = _ef_buffer(st2, name2, w2)
-        res = K.dual_quantize_per_tensor(w2, ef2, update_ef=update_ef2, transposed=need_h)
-        w2_hi, w2_lo, ih2, il2, w2_hi_t, w2_lo_t = res if need_h else (*res, None, None)
+        w2_hi, w2_lo, ih2, il2, w2_hi_t, w2_lo_t = res2 if need_h else (*res2, None, None)
         out = K.fused_dual_gemm_forward(a2, w2_hi, w2_lo, a2_inv, ih2, il2, bias=b2)
 
         ctx.input_shape = input_shape
@@ -616,8 +617,11 @@ class _TCFP12FusedMLPFunction(torch.autograd.Function):
         # quantisation; layer 1
         if need_h:
             sums = need_db1 and ctx.has_b1
+            # (layer 1's gradient codes feed its dX, their transposed copy its
+            # dW: the codes are written only when dX is needed)
             res = K.dual_gemm_dgelu_quantize_colsum(
                 q2, w2_hi_t, w2_lo_t, g2_inv, ih2, il2, dgelu, transpose=need_dw1, col_sum=sums,
+                codes=need_dx or not need_dw1,
             )
             q1, g1_inv = res[0], res[1]
             q1_t = res[2] if need_dw1 else None

@@ -229,7 +229,7 @@ def test_gemm_epilogue_replaces_the_gelu_passes_at_c4(dev):
     fwd()
     torch.cuda.synchronize()  # the premise check has run
     names = _kernel_names(fwd)
-    assert any("gemm_nt_persist_kernel<0, 0, float, 1, 0, 4, 128>" in n for n in names), names
+    assert any("gemm_nt_persist_kernel<0, 0, float, 1, 0, 8, 128>" in n for n in names), names
     assert not any("gelu_amax_kernel" in n or "amax_part_kernel" in n for n in names), names
     g8, hi2, lo2, g_inv, ih2, il2 = _fp8_layer(dev, 8192, 1024, 4096, seed=2,
                                                a_dtype=torch.float8_e5m2)

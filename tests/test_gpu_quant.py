@@ -623,3 +623,56 @@ def test_per_tensor_dual_quant_empty_and_one_element(dev):
     hi, lo, ih2, il2, _, _ = oq.dual_quant_per_tensor(np.array([[0.3]], np.float32))
     assert np.array_equal(u8(h), hi) and np.array_equal(u8(l), lo)
     assert ih.item() == float(ih2) and il.item() == float(il2)
+
+
+@pytest.mark.parametrize("case", ["mlp", "mixed", "big", "fallback"])
+def test_quantize_batch_equals_single_calls(dev, case):
+    """tcfp_quantize_batch (three launches for every tensor of the batch)
+    against the single-tensor entry points on the same inputs, bit for bit:
+    codes, transposed codes, inverse scales and updated EF buffers.  Cases:
+    the C4 MLP's two weights and input; fp32 / bf16 weights with and
+    without EF, update off, ragged rows, E5M2 activations; a 2^23-element
+    weight (the single call takes the candidate pass); a last dimension not
+    divisible by 8 (the batch hands it to the single calls)."""
+    g = torch.Generator().manual_seed(len(case))
+    if case == "mlp":
+        shapes = [((4096, 1024), torch.float32, True, True, False),
+                  ((1024, 4096), torch.float32, True, True, True)]
+        acts = [((8192, 1024), torch.bfloat16, torch.float8_e4m3fn, True)]
+    elif case == "mixed":
+        shapes = [((300, 200), torch.bfloat16, True, False, True),
+                  ((384, 96), torch.float32, False, False, False),
+                  ((130, 1000), torch.float32, True, True, True)]
+        acts = [((333, 136), torch.float32, torch.float8_e5m2, True)]
+    elif case == "big":
+        shapes = [((4096, 2048), torch.float32, True, True, True)]
+        acts = [((2048, 512), torch.float32, torch.float8_e5m2, False)]
+    else:
+        shapes = [((64, 100), torch.float32, True, True, False)]
+        acts = [((32, 36), torch.float32, torch.float8_e4m3fn, True)]
+    dual, efs_a, efs_b = [], [], []
+    for shape, wdt, has_ef, upd, tr in shapes:
+        w = (torch.randn(shape, generator=g) * 0.02).to(wdt).to(dev)
+        e = (torch.randn(shape, generator=g) * 1e-4).to(dev) if has_ef else None
+        efs_a.append(e.clone() if e is not None else None)
+        efs_b.append(e.clone() if e is not None else None)
+        dual.append((w, tr, upd))
+    act = [((torch.randn(s, generator=g) * 3).to(dt).to(dev), f, tr) for s, dt, f, tr in acts]
+    print(f"[batch] {case}", flush=True)
+    rd, ra = K.quantize_batch(dual=[(w, e, u, t) for (w, t, u), e in zip(dual, efs_a)], act=act)
+    for (w, t, u), e, r in zip(dual, efs_b, rd):
+        ref = K.dual_quantize_per_tensor(w, e, update_ef=u, transposed=t)
+        assert len(r) == len(ref)
+        for x, y in zip(r, ref):
+            x = x.view(torch.uint8) if x.dtype.itemsize == 1 else x
+            y = y.view(torch.uint8) if y.dtype.itemsize == 1 else y
+            assert torch.equal(x, y), (case, tuple(w.shape))
+    for ea, eb in zip(efs_a, efs_b):
+        if ea is not None:
+            assert torch.equal(ea, eb)
+    for (x, f, t), r in zip(act, ra):
+        ref = K.quantize_per_tensor(x, f, transpose=t)
+        for p, q in zip(r, ref):
+            p = p.view(torch.uint8) if p.dtype.itemsize == 1 else p
+            q = q.view(torch.uint8) if q.dtype.itemsize == 1 else q
+            assert torch.equal(p, q), (case, tuple(x.shape))

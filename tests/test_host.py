@@ -350,3 +350,32 @@ def test_core_host_helpers_match_reference_behaviour():
         from tcfp.core import compute_block_scales
 
         compute_block_scales(torch.randn(4, 48), 32)
+
+
+def test_quantize_batch_validation_without_launch():
+    """tcfp_quantize_batch: the job struct's layout (tcfp_quant_job, 104
+    bytes on x86-64), its workspace size, and the argument checks that
+    return before anything is launched (pointers are dummies)."""
+    import ctypes
+
+    lib = _hip.load_library()
+    assert ctypes.sizeof(_hip.QuantJob) == 104
+    assert _hip.QuantJob.rows.offset == 24 and _hip.QuantJob.inv_lo.offset == 96
+    one = lib.tcfp_quantize_batch_workspace_bytes(1)
+    assert one >= lib.tcfp_workspace_bytes()
+    assert lib.tcfp_quantize_batch_workspace_bytes(4) == 4 * one
+    assert lib.tcfp_quantize_batch_workspace_bytes(0) == 0
+    assert lib.tcfp_quantize_batch_workspace_bytes(5) == 0
+    p = 4096
+    jobs = (_hip.QuantJob * 1)()
+    assert lib.tcfp_quantize_batch(0, jobs, p, one, None) == 1
+    assert lib.tcfp_quantize_batch(5, jobs, p, one, None) == 1
+    jobs[0] = _hip.QuantJob(_hip.JOB_DUAL, p, 0, 4, 16, None, 0, 0, p, None, p, p, None, p)
+    assert lib.tcfp_quantize_batch(1, jobs, None, 0, None) == 5  # no workspace
+    assert lib.tcfp_quantize_batch(1, jobs, p, one - 1, None) == 5  # too small
+    jobs[0] = _hip.QuantJob(7, p, 0, 4, 16, None, 0, 0, p, None, p, p, None, p)
+    assert lib.tcfp_quantize_batch(1, jobs, p, one, None) == 1  # kind
+    jobs[0] = _hip.QuantJob(_hip.JOB_DUAL, p, 0, 4, 12, None, 0, 0, p, None, p, p, None, p)
+    assert lib.tcfp_quantize_batch(1, jobs, p, one, None) == 1  # cols % 8
+    jobs[0] = _hip.QuantJob(_hip.JOB_ACT, p, 0, 4, 16, None, 0, 5, p, None, p, None, None, None)
+    assert lib.tcfp_quantize_batch(1, jobs, p, one, None) == 2  # fp8 format
