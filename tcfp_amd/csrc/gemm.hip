@@ -1185,7 +1185,7 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persist_kernel(GemmArgs g) {
   constexpr int NDG = NW - ND;  // factor-loading waves
   const uint32_t dg_lds0 = lds0 + uint32_t(NS * STAGE + kBiasB);
   const uint32_t ldo_b = uint32_t(g.ldo) * 4u;
-  const int dg_np = (DGL && !dma_wave) ? (BM / 4 - (wave - ND) + NDG - 1) / NDG : 0;
+  const int dg_np = (DGL && !dma_wave) ? (BM / 4 - (wave - ND) + NDG - 1) / (NDG > 0 ? NDG : 1) : 0;
   const uint32_t dg_nrec = uint32_t(int64_t(BM - 1) * g.ldo * 4 + BN * 4);
   auto issue_dg = [&](const v4i& rs, int t) {
     if constexpr (DGL) {
@@ -1736,9 +1736,12 @@ int launch_gemm(GemmArgs ga, hipStream_t st) {
     const bool deep = SCALE == 0 && small && int64_t(grid.x) * splits <= num_cus();
     if (small && deep) {
       if constexpr (SCALE == 0) {
-        if (g_tile_policy == 3)
-          gemm_nt_dma_kernel<AF, BF, SPLIT, OutT, 8, 128, 64, SCALE, 4><<<grid, 512, 0, st>>>(ga);
-        else
+        // (the eight-wave tuning policy serves FP8 operands; bf16 takes the
+        // four-wave tile under every policy)
+        if (AF != kBF16 && g_tile_policy == 3) {
+          if constexpr (AF != kBF16)
+            gemm_nt_dma_kernel<AF, BF, SPLIT, OutT, 8, 128, 64, SCALE, 4><<<grid, 512, 0, st>>>(ga);
+        } else
           gemm_nt_dma_kernel<AF, BF, SPLIT, OutT, 4, 128, 64, SCALE, 4><<<grid, 256, 0, st>>>(ga);
       }
     } else if (small) {

@@ -499,8 +499,11 @@ def test_block_layer_fp8_dgrad_mode(dev):
 
 # ------------------------------------------------- fused act-quant (a11)
 # (M, N, K in blocks): ragged rows and columns, a K that ends mid-stage
-# (3 blocks of 32), several stages, and one row
-ACTQ_SHAPES = [(300, 256, 4), (1, 100, 1), (513, 520, 3), (2048, 512, 16), (130, 64, 8)]
+# (3 blocks of 32), several stages, and one row; 4096 x 1024 fills twice as
+# many 128-row tiles as CUs, which bf16 activations take (64-row tiles
+# otherwise)
+ACTQ_SHAPES = [(300, 256, 4), (1, 100, 1), (513, 520, 3), (2048, 512, 16), (130, 64, 8),
+               (4096, 1024, 2)]
 
 
 @pytest.mark.parametrize("bs", [32, 64, 128])
@@ -520,6 +523,8 @@ def test_fused_act_quant_dual_gemm(dev, bs, dtype, M, N, KB):
     names = [n for n in _kernel_names(lambda: K.fused_act_quant_dual_gemm_forward(
         x, h, l, eh, el, bs, bias=bias)) if not n.startswith("hip")]
     assert len(names) == 1 and "gemm_nt_dma_kernel" in names[0], names
+    rows = 128 if dtype == torch.bfloat16 and (M // 128) * (N // 64) >= 512 else 64
+    assert f"4, {rows}, 64, 1, 2, {bs.bit_length() - 1}," in names[0], names
     out, aq, ea = K.fused_act_quant_dual_gemm_forward(x, h, l, eh, el, bs, bias=bias)
     aq2, ea2 = K.block_quantize_fp8(x, bs)
     assert torch.equal(aq.view(torch.uint8), aq2.view(torch.uint8)) and torch.equal(ea, ea2)
