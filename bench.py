@@ -244,50 +244,116 @@ def bench_copy(steps):
     return {"copy_bytes_each_way": 256 << 20, "launches": steps}
 
 
-def bench_dual_quant(iters=20):
+def rotated_time_ms(calls, rounds, stream):
+    """Average time per call over ``rounds`` passes of ``calls`` (one call
+    per independent set of inputs and outputs), HIP events on ``stream``:
+    with the sets together well beyond the 256 MB Infinity Cache every call
+    reads its operands from HBM (the cold figure).  One untimed pass
+    first."""
+    import torch
+
+    for fn in calls:
+        fn()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(rounds):
+        for fn in calls:
+            fn()
+    end.record(stream)
+    end.synchronize()
+    return start.elapsed_time(end) / (rounds * len(calls))
+
+
+COLD_BYTES = 768 << 20  # working set of the cold protocol: 3 x the Infinity Cache
+
+
+def bench_dual_quant(iters=20, cold_rounds=4):
+    """The quantisation kernels at the sizes the configs use, each timed two
+    ways: warm (``iters`` back-to-back calls on one set of buffers, which
+    can stay in the 256 MB Infinity Cache) and cold (calls rotating over
+    independent buffer sets totalling >= 768 MB, ``rotated_time_ms``).
+    GB/s = algorithmic bytes (each input read once, each output written
+    once) / time."""
     import torch
 
     from tcfp_amd import kernels as K
+    from tcfp_amd.core import ErrorFeedbackState
 
     dev = torch.device("cuda:0")
     stream = torch.cuda.current_stream(dev)
     out = {}
+
+    def row(name, make, alg_bytes, set_bytes):
+        """make(i) -> a zero-argument call on buffer set i."""
+        f0 = make(0)
+        ms = event_time_ms(f0, iters, stream)
+        nsets = max(2, -(-COLD_BYTES // set_bytes))
+        calls = [f0] + [make(i) for i in range(1, nsets)]
+        cold = rotated_time_ms(calls, cold_rounds, stream)
+        out[f"{name}_ms"] = ms
+        out[f"{name}_GBs"] = alg_bytes / (ms * 1e-3) / 1e9
+        out[f"{name}_cold_ms"] = cold
+        out[f"{name}_cold_GBs"] = alg_bytes / (cold * 1e-3) / 1e9
+        out[f"{name}_cold_sets"] = nsets
+        del calls
+        torch.cuda.empty_cache()
+
     n, k = 4096, 4096
-    w = torch.randn(n, k, device=dev) * 0.02
-    ef = torch.zeros(n, k, device=dev)
-    # per-tensor with EF (update in place): 14 algorithmic B/elem
-    ms = event_time_ms(lambda: K.dual_quantize_per_tensor(w, ef), iters, stream)
-    out["per_tensor_ef_4096x4096_ms"] = ms
-    out["per_tensor_ef_4096x4096_GBs"] = 14 * n * k / (ms * 1e-3) / 1e9
+    ne = n * k
+
+    def wef(i, rows=n):
+        g = torch.Generator(device=dev).manual_seed(100 + i)
+        return (torch.randn(rows, k, device=dev, generator=g) * 0.02,
+                torch.zeros(rows, k, device=dev))
+
+    # per-tensor with EF (update in place): 14 algorithmic B/elem (W and EF
+    # read, EF written, two code arrays); a set holds W, EF and the codes
+    def per_tensor(i):
+        w, ef = wef(i)
+        return lambda: K.dual_quantize_per_tensor(w, ef)
+
+    row("per_tensor_ef_4096x4096", per_tensor, 14 * ne, 10 * ne)
+
     # the same with delayed scaling on a non-validation step (the residual
     # amax is predicted: two passes over W + EF instead of three)
-    from tcfp_amd.core import ErrorFeedbackState
+    def delayed(i):
+        w, ef = wef(i)
+        st = ErrorFeedbackState(residual_validation_interval=10**9)
+        K.dual_quantize_per_tensor_delayed(w, ef, st, "w")  # the first call validates
+        return lambda: K.dual_quantize_per_tensor_delayed(w, ef, st, "w")
 
-    st = ErrorFeedbackState(residual_validation_interval=10**9)
-    K.dual_quantize_per_tensor_delayed(w, ef, st, "w")  # first call validates
-    ms = event_time_ms(lambda: K.dual_quantize_per_tensor_delayed(w, ef, st, "w"), iters, stream)
-    out["per_tensor_ef_delayed_4096x4096_ms"] = ms
-    out["per_tensor_ef_delayed_4096x4096_GBs"] = 14 * n * k / (ms * 1e-3) / 1e9
+    row("per_tensor_ef_delayed_4096x4096", delayed, 14 * ne, 10 * ne)
+
     # NF-aware W_hi scaling (sigma = 3): the first pass also sums v and v^2
-    ms = event_time_ms(lambda: K.dual_quantize_per_tensor(w, ef, sigma_factor=3.0), iters,
-                       stream)
-    out["per_tensor_ef_nf_4096x4096_ms"] = ms
-    out["per_tensor_ef_nf_4096x4096_GBs"] = 14 * n * k / (ms * 1e-3) / 1e9
+    def nf(i):
+        w, ef = wef(i)
+        return lambda: K.dual_quantize_per_tensor(w, ef, sigma_factor=3.0)
+
+    row("per_tensor_ef_nf_4096x4096", nf, 14 * ne, 10 * ne)
+
     # block-64 with EF: 14 + 2/64 B/elem
-    ms = event_time_ms(lambda: K.fused_dual_quantize_fp8(w, 64, error_buf=ef), iters, stream)
-    out["block64_ef_4096x4096_ms"] = ms
-    out["block64_ef_4096x4096_GBs"] = (14 + 2 / 64) * n * k / (ms * 1e-3) / 1e9
+    def block64(i):
+        w, ef = wef(i)
+        return lambda: K.fused_dual_quantize_fp8(w, 64, error_buf=ef)
+
+    row("block64_ef_4096x4096", block64, (14 + 2 / 64) * ne, 10 * ne)
+
     # SRR block-64 on the C5 scale-up weight [16384, 4096]: 6 + 2/64 B/elem
-    w2 = torch.randn(16384, 4096, device=dev) * 0.02
-    ms = event_time_ms(lambda: K.fused_dual_quantize_fp8(w2, 64, stochastic_lo=True, seed=1),
-                       iters, stream)
-    out["block64_srr_16384x4096_ms"] = ms
-    out["block64_srr_16384x4096_GBs"] = (6 + 2 / 64) * 16384 * 4096 / (ms * 1e-3) / 1e9
-    # act quant bf16 [8192, 1024] -> e4m3 (+ transposed copy): 2 + 1 (+1) B/elem
-    x = torch.randn(8192, 1024, device=dev).bfloat16()
-    ms = event_time_ms(lambda: K.quantize_per_tensor(x), iters, stream)
-    out["act_quant_bf16_8192x1024_ms"] = ms
-    out["act_quant_bf16_8192x1024_GBs"] = 3 * x.numel() / (ms * 1e-3) / 1e9
+    def srr(i):
+        g = torch.Generator(device=dev).manual_seed(200 + i)
+        w2 = torch.randn(16384, 4096, device=dev, generator=g) * 0.02
+        return lambda: K.fused_dual_quantize_fp8(w2, 64, stochastic_lo=True, seed=1)
+
+    row("block64_srr_16384x4096", srr, (6 + 2 / 64) * 16384 * 4096, 6 * 16384 * 4096)
+
+    # act quant bf16 [8192, 1024] -> e4m3: 2 + 1 B/elem
+    def act(i):
+        g = torch.Generator(device=dev).manual_seed(300 + i)
+        x = torch.randn(8192, 1024, device=dev, generator=g).bfloat16()
+        return lambda: K.quantize_per_tensor(x)
+
+    row("act_quant_bf16_8192x1024", act, 3 * 8192 * 1024, 3 * 8192 * 1024)
     return out
 
 
