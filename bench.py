@@ -547,13 +547,17 @@ def bench_c5(steps=50, time_iters=10):
                                  / res["bf16"]["loss_last"])
     # scale-up layer
     x = torch.randn(8192, 4096, generator=g).bfloat16().to(dev)
-    from tcfp_amd.nn import set_block_dgrad
+    from tcfp_amd.nn import set_block_dgrad, set_block_wgrad
 
-    # block64_srr_fp8_dgrad: the same layer with the opt-in FP8 block dgrad
+    # the same layer with the opt-in FP8 block dgrad and / or the opt-in
+    # single-pass bf16 wgrad
     for arm, kw in (("block64_srr", dict(scale_block_size=64, srr=True)),
                     ("block64_srr_fp8_dgrad", dict(scale_block_size=64, srr=True)),
+                    ("block64_srr_bf16_wgrad", dict(scale_block_size=64, srr=True)),
+                    ("block64_srr_fp8_dgrad_bf16_wgrad", dict(scale_block_size=64, srr=True)),
                     ("block64_ef", dict(scale_block_size=64)), ("bf16", None)):
-        set_block_dgrad("fp8" if arm.endswith("fp8_dgrad") else "exact")
+        set_block_dgrad("fp8" if "fp8_dgrad" in arm else "exact")
+        set_block_wgrad("bf16" if "bf16_wgrad" in arm else "split")
         torch.manual_seed(2)
         m = nn.Sequential(nn.Linear(4096, 16384), nn.GELU(), nn.Linear(16384, 4096)).to(dev)
         if kw is not None:
@@ -576,7 +580,92 @@ def bench_c5(steps=50, time_iters=10):
         del m
         torch.cuda.empty_cache()
     set_block_dgrad("exact")
+    set_block_wgrad("split")
     return res
+
+
+def bench_c5_memory():
+    """Peak-memory breakdown of the C5 scale-up layer's forward + backward
+    (``Linear(4096,16384) -> GELU -> Linear(16384,4096)``, 8192 tokens):
+    the caching allocator's event history of one call is replayed, and the
+    allocations live at the highest point are grouped by the code that made
+    them (the innermost frame in this package or this file, else the
+    innermost frame).  Per arm: peak MB, resident MB (weights, EF buffers,
+    optimizer-free), and the live tensors at the peak."""
+    import torch
+    import torch.nn as nn
+
+    from tcfp_amd.nn import convert_to_tcfp, set_block_dgrad, set_block_wgrad
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(8192, 4096, generator=g).bfloat16().to(dev)
+    out = {}
+    for arm, kw, dg, wg in (
+            ("block64_srr", dict(scale_block_size=64, srr=True), "exact", "split"),
+            ("block64_srr_fp8_dgrad_bf16_wgrad", dict(scale_block_size=64, srr=True), "fp8",
+             "bf16"),
+            ("bf16", None, "exact", "split")):
+        set_block_dgrad(dg)
+        set_block_wgrad(wg)
+        torch.manual_seed(2)
+        m = nn.Sequential(nn.Linear(4096, 16384), nn.GELU(), nn.Linear(16384, 4096)).to(dev)
+        if kw is not None:
+            convert_to_tcfp(m, use_tensor_cores=True, **kw)
+
+        def fb():
+            with torch.autocast("cuda", dtype=torch.bfloat16, enabled=kw is None):
+                y = m(x)
+            y.float().square().mean().backward()
+
+        fb()
+        for p in m.parameters():
+            p.grad = None
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+        live = {}
+        for blk in torch.cuda.memory._snapshot()["segments"]:
+            for b in blk["blocks"]:
+                if b["state"] == "active_allocated":
+                    live[b["address"]] = (b["size"], "resident")
+        resident = sum(v[0] for v in live.values())
+        torch.cuda.memory._record_memory_history(max_entries=200000)
+        fb()
+        torch.cuda.synchronize()
+        snap = torch.cuda.memory._snapshot()
+        torch.cuda.memory._record_memory_history(enabled=None)
+
+        def where(frames):
+            for f in frames:
+                fn = f.get("filename", "")
+                if "tcfp_amd" in fn or fn.endswith("bench.py"):
+                    return f"{fn.split('/')[-1]}:{f.get('name')}:{f.get('line')}"
+            f = frames[0] if frames else {}
+            return f"{f.get('filename', '?').split('/')[-1]}:{f.get('name', '?')}"
+
+        cur = dict(live)
+        total = resident
+        best, best_live = total, dict(cur)
+        for ev in snap["device_traces"][dev.index or 0]:
+            a = ev["action"]
+            if a == "alloc":
+                cur[ev["addr"]] = (ev["size"], where(ev.get("frames", [])))
+                total += ev["size"]
+                if total > best:
+                    best, best_live = total, dict(cur)
+            elif a == "free_completed" and ev["addr"] in cur:
+                total -= cur.pop(ev["addr"])[0]
+        groups = {}
+        for size, w in best_live.values():
+            groups[w] = groups.get(w, 0) + size
+        top = sorted(groups.items(), key=lambda kv: -kv[1])
+        out[arm] = {"peak_MB": best / 1e6, "resident_MB": resident / 1e6,
+                    "at_peak_MB": {k: round(v / 1e6, 1) for k, v in top if v >= 1e6}}
+        del m
+        torch.cuda.empty_cache()
+    set_block_dgrad("exact")
+    set_block_wgrad("split")
+    return out
 
 
 def cpu_baseline(t, reps=5):
@@ -646,8 +735,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--part", choices=("all", "gemm", "quant", "block", "mlp", "c5", "copy",
-                                       "scaled_mm"),
+    ap.add_argument("--part", choices=("all", "gemm", "quant", "block", "mlp", "c5", "c5mem",
+                                       "copy", "scaled_mm"),
                     default="all",
                     help="all (default) = headline + every secondary figure; the others run "
                          "one workload (for profiling)")
@@ -667,7 +756,7 @@ def main():
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     if args.part != "all" and args.part != "gemm":
         fn = {"quant": lambda: bench_dual_quant(), "block": lambda: bench_block_gemms(),
-              "c5": lambda: bench_c5(),
+              "c5": lambda: bench_c5(), "c5mem": lambda: bench_c5_memory(),
               "mlp": lambda: bench_mlp(
                   steps=args.steps,
                   arms=("tcfp", "tcfp_fused", "bf16", "fp32") if args.arm == "both"

@@ -580,7 +580,9 @@ int tcfp_block_wgrad(const float* g, int64_t m, int64_t n_out, const uint8_t* x,
  *             `block`) with the block_quantize_fp8 rule (tcfp/kernels.py:
  *             1675-1722) and dequantised -- the dgrad's G operand;
  *   g_split_t [n, 2m] bf16: [bf16(g) | bf16(g - bf16(g))] transposed -- the
- *             wgrad's split fp32 gradient;
+ *             wgrad's split fp32 gradient (split_lo 1); with split_lo 0
+ *             [n, m] bf16: bf16(g) transposed, the single-pass wgrad's
+ *             operand;
  *   bias_grad [n] fp32: column sums of g (grad.sum(0)), summed per 64-row
  *             tile and then over tiles in order;
  *   g_fp8 [m, n] E5M2 codes with g_exps [n / block, m] int8: the same block
@@ -590,8 +592,8 @@ int tcfp_block_wgrad(const float* g, int64_t m, int64_t n_out, const uint8_t* x,
  * tcfp_block_grad_prep_workspace_bytes(m, n) bytes. */
 size_t tcfp_block_grad_prep_workspace_bytes(int64_t m, int64_t n);
 int tcfp_block_grad_prep(const float* g, int64_t m, int64_t n, int block, uint16_t* g_deq,
-                         uint16_t* g_split_t, float* bias_grad, uint8_t* g_fp8, int8_t* g_exps,
-                         void* workspace, size_t workspace_bytes, void* stream);
+                         uint16_t* g_split_t, int split_lo, float* bias_grad, uint8_t* g_fp8,
+                         int8_t* g_exps, void* workspace, size_t workspace_bytes, void* stream);
 
 /* tcfp_block_dual_gemm_dx with the gradient already dequantised to bf16
  * (g_deq from tcfp_block_grad_prep): same result bit for bit.  Workspace:
@@ -603,13 +605,18 @@ int tcfp_block_dual_gemm_dx_bf16(const uint16_t* g_deq, const uint8_t* w_hi, con
                                  size_t workspace_bytes, void* stream);
 
 /* tcfp_block_wgrad with the gradient already split and transposed
- * (g_split_t from tcfp_block_grad_prep): same result bit for bit.
- * Workspace: tcfp_block_wgrad_presplit_workspace_bytes(m, n_out, k_in). */
-size_t tcfp_block_wgrad_presplit_workspace_bytes(int64_t m, int64_t n_out, int64_t k_in);
-int tcfp_block_wgrad_presplit(const uint16_t* g_split_t, int64_t m, int64_t n_out,
-                              const uint8_t* x, int x_fmt, const int8_t* e_x, int64_t k_in,
-                              int block, float* dw, void* workspace, size_t workspace_bytes,
-                              void* stream);
+ * (g_split_t [n_out, 2m] from tcfp_block_grad_prep with split_lo 1): same
+ * result bit for bit.  With split_lo 0, g_split_t is [n_out, m] (bf16(g)
+ * transposed) and dW = bf16(g)^T deq(x): one bf16 pass instead of two,
+ * relative error ~2^-9 per gradient element (the reference's wgrad
+ * contract is 1e-2 relative; m % 64 == 0).  Workspace:
+ * tcfp_block_wgrad_presplit_workspace_bytes(m, n_out, k_in, split_lo). */
+size_t tcfp_block_wgrad_presplit_workspace_bytes(int64_t m, int64_t n_out, int64_t k_in,
+                                                 int split_lo);
+int tcfp_block_wgrad_presplit(const uint16_t* g_split_t, int split_lo, int64_t m,
+                              int64_t n_out, const uint8_t* x, int x_fmt, const int8_t* e_x,
+                              int64_t k_in, int block, float* dw, void* workspace,
+                              size_t workspace_bytes, void* stream);
 
 /* ---- layout helpers ---------------------------------------------------- */
 

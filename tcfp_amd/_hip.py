@@ -125,16 +125,16 @@ _SIGNATURES = {
     "tcfp_block_wgrad": [_c_void_p, _i64, _i64, _c_void_p, _i32, _c_void_p, _i64, _i32, _c_void_p,
                          _c_void_p, ctypes.c_size_t, _c_void_p],
     "tcfp_block_wgrad_workspace_bytes": [_i64, _i64, _i64],
-    "tcfp_block_grad_prep": [_c_void_p, _i64, _i64, _i32, _c_void_p, _c_void_p, _c_void_p,
+    "tcfp_block_grad_prep": [_c_void_p, _i64, _i64, _i32, _c_void_p, _c_void_p, _i32, _c_void_p,
                              _c_void_p, _c_void_p, _c_void_p, ctypes.c_size_t, _c_void_p],
     "tcfp_block_grad_prep_workspace_bytes": [_i64, _i64],
     "tcfp_block_dual_gemm_dx_bf16": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64,
                                      _i64, _i64, _i32, _c_void_p, _c_void_p, ctypes.c_size_t,
                                      _c_void_p],
     "tcfp_block_dual_gemm_dx_bf16_workspace_bytes": [_i64, _i64],
-    "tcfp_block_wgrad_presplit": [_c_void_p, _i64, _i64, _c_void_p, _i32, _c_void_p, _i64, _i32,
-                                  _c_void_p, _c_void_p, ctypes.c_size_t, _c_void_p],
-    "tcfp_block_wgrad_presplit_workspace_bytes": [_i64, _i64, _i64],
+    "tcfp_block_wgrad_presplit": [_c_void_p, _i32, _i64, _i64, _c_void_p, _i32, _c_void_p, _i64,
+                                  _i32, _c_void_p, _c_void_p, ctypes.c_size_t, _c_void_p],
+    "tcfp_block_wgrad_presplit_workspace_bytes": [_i64, _i64, _i64, _i32],
     "tcfp_quantize_batch_workspace_bytes": [_i32],
     "tcfp_quantize_batch": [_i32, ctypes.POINTER(QuantJob), _c_void_p, ctypes.c_size_t, _c_void_p],
     "tcfp_gemm_set_tile_policy": [_i32],

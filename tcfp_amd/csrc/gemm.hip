@@ -2489,13 +2489,14 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
   }
 }
 
-// Split-K factor of the block wgrad GEMM (contraction 2m bf16 = 4m bytes):
-// when the [n_out, k_in] output gives at most half the CUs a 128 x 128
-// tile, split the contraction so every CU gets a workgroup, keeping at
-// least four 128-byte stages per split.  Returns the split count and sets
-// *kc to the split length in bytes (a multiple of 128).
-int64_t wgrad_splits(int64_t m, int64_t n_out, int64_t k_in, int64_t* kc) {
-  const int64_t kbytes = 4 * m;
+// Split-K factor of the block wgrad GEMM (contraction 2m bf16 = 4m bytes;
+// m bf16 = 2m bytes without the low half, `lo` false): when the [n_out,
+// k_in] output gives at most half the CUs a 128 x 128 tile, split the
+// contraction so every CU gets a workgroup, keeping at least four 128-byte
+// stages per split.  Returns the split count and sets *kc to the split
+// length in bytes (a multiple of 128).
+int64_t wgrad_splits(int64_t m, int64_t n_out, int64_t k_in, int64_t* kc, bool lo = true) {
+  const int64_t kbytes = (lo ? 4 : 2) * m;
   *kc = kbytes;
   const int64_t tiles = ((n_out + 127) / 128) * ((k_in + 127) / 128);
   const int64_t cus = num_cus();
@@ -2509,19 +2510,27 @@ int64_t wgrad_splits(int64_t m, int64_t n_out, int64_t k_in, int64_t* kc) {
 // The wgrad GEMM over the concatenated contraction: A' = [g_hi | g_lo]^T
 // [n_out, 2m], B' = [x | x]^T [k_in, 2m] (bf16; with `wrap` one copy
 // x^T [k_in, m] read twice), dw [n_out, k_in] fp32 with row stride ldo;
-// split-K partials go to `part` when the output is small.
+// split-K partials go to `part` when the output is small.  Without the low
+// half (`lo` false): A' = g_hi^T [n_out, m] against one copy x^T [k_in, m].
 int wgrad_gemm(const uint16_t* ap, const uint16_t* bp, int64_t m, int64_t n_out, int64_t k_in,
-               float* dw, int64_t ldo, float* part, bool wrap, hipStream_t st) {
+               float* dw, int64_t ldo, float* part, bool wrap, hipStream_t st, bool lo = true) {
   GemmArgs ga{};
   ga.A = reinterpret_cast<const uint8_t*>(ap);
   ga.B0 = reinterpret_cast<const uint8_t*>(bp);
   ga.B1 = ga.B0;
-  ga.M = int(n_out); ga.N = int(k_in); ga.K = int(4 * m);  // bytes of 2M bf16
-  ga.lda = 4 * m; ga.ldb = wrap ? 2 * m : 4 * m;
-  ga.kwrap_b = wrap ? int(2 * m) : 0;
+  ga.M = int(n_out); ga.N = int(k_in);
+  if (lo) {
+    ga.K = int(4 * m);  // bytes of 2M bf16
+    ga.lda = 4 * m; ga.ldb = wrap ? 2 * m : 4 * m;
+    ga.kwrap_b = wrap ? int(2 * m) : 0;
+  } else {
+    ga.K = int(2 * m);
+    ga.lda = 2 * m; ga.ldb = 2 * m;
+    ga.kwrap_b = 0;
+  }
   ga.out = dw; ga.ldo = ldo;
   int64_t kc;
-  const int64_t splits = wgrad_splits(m, n_out, k_in, &kc);
+  const int64_t splits = wgrad_splits(m, n_out, k_in, &kc, lo);
   if (splits <= 1) return launch_gemm<kBF16, kBF16, true, float, 0>(ga, st);
   // partial products of each K chunk ([n_out, k_in] each), then their sum
   // in split order
@@ -2541,36 +2550,43 @@ int wgrad_gemm(const uint16_t* ap, const uint16_t* bp, int64_t m, int64_t n_out,
 // One copy of x^T serves both halves of the contraction when its rows (m
 // bf16 = 2m bytes) are whole 128-byte stages.
 bool wgrad_wrap(int64_t m) { return m > 0 && (2 * m) % kSK == 0; }
-// dw columns per wgrad chunk: x^T rows of m bf16 (2m without the wrap)
-int64_t wgrad_chunk(int64_t m, int64_t k_in) {
-  return chunk_cols((wgrad_wrap(m) ? 2 : 4) * std::max<int64_t>(m, 1), k_in);
+// x^T copy rows: m bf16 (one copy serves both halves, or there is no low
+// half), 2m otherwise
+bool wgrad_one_copy(int64_t m, bool lo) { return !lo || wgrad_wrap(m); }
+// dw columns per wgrad chunk
+int64_t wgrad_chunk(int64_t m, int64_t k_in, bool lo = true) {
+  return chunk_cols((wgrad_one_copy(m, lo) ? 2 : 4) * std::max<int64_t>(m, 1), k_in);
 }
-size_t wgrad_part_bytes(int64_t m, int64_t n_out, int64_t cols) {
+size_t wgrad_part_bytes(int64_t m, int64_t n_out, int64_t cols, bool lo = true) {
   int64_t kc;
-  const int64_t splits = wgrad_splits(m, n_out, cols, &kc);
+  const int64_t splits = wgrad_splits(m, n_out, cols, &kc, lo);
   return splits > 1 ? align256(size_t(splits) * size_t(n_out) * size_t(cols) * 4) : 0;
 }
 // Workspace of the chunked wgrad: one chunk's x^T copy, then the partials.
-size_t wgrad_copy_bytes(int64_t m, int64_t k_in) {
-  return align256(size_t(wgrad_chunk(m, k_in)) * size_t(wgrad_wrap(m) ? m : 2 * m) * 2);
+size_t wgrad_copy_bytes(int64_t m, int64_t k_in, bool lo = true) {
+  return align256(size_t(wgrad_chunk(m, k_in, lo)) * size_t(wgrad_one_copy(m, lo) ? m : 2 * m) *
+                  2);
 }
-size_t wgrad_ws_bytes(int64_t m, int64_t n_out, int64_t k_in) {
-  const int64_t kw = wgrad_chunk(m, k_in);
+size_t wgrad_ws_bytes(int64_t m, int64_t n_out, int64_t k_in, bool lo = true) {
+  const int64_t kw = wgrad_chunk(m, k_in, lo);
   const int64_t rem = kw > 0 ? k_in % kw : 0;
-  return wgrad_copy_bytes(m, k_in) +
-         std::max(wgrad_part_bytes(m, n_out, kw), rem ? wgrad_part_bytes(m, n_out, rem) : 0);
+  return wgrad_copy_bytes(m, k_in, lo) +
+         std::max(wgrad_part_bytes(m, n_out, kw, lo),
+                  rem ? wgrad_part_bytes(m, n_out, rem, lo) : 0);
 }
 
-// dw = A'^T-product of the split gradient ap ([n_out, 2m] bf16) with the
-// dequantised activation, per chunk of dw columns: x^T rows c0.. dequantised
-// into the workspace, then the GEMM into dw[:, c0 ..].
+// dw = A'^T-product of the split gradient ap ([n_out, 2m] bf16; [n_out, m]
+// without the low half) with the dequantised activation, per chunk of dw
+// columns: x^T rows c0.. dequantised into the workspace, then the GEMM into
+// dw[:, c0 ..].
 int wgrad_chunked(const uint16_t* ap, int64_t m, int64_t n_out, const uint8_t* x, int x_fmt,
                   const int8_t* e_x, int64_t k_in, int shift, float* dw, uint8_t* ws,
-                  hipStream_t st) {
+                  hipStream_t st, bool lo = true) {
   const bool wrap = wgrad_wrap(m);
-  const int64_t kw = wgrad_chunk(m, k_in);
+  const bool dup = !wgrad_one_copy(m, lo);
+  const int64_t kw = wgrad_chunk(m, k_in, lo);
   uint16_t* bp = reinterpret_cast<uint16_t*>(ws);
-  float* part = reinterpret_cast<float*>(ws + wgrad_copy_bytes(m, k_in));
+  float* part = reinterpret_cast<float*>(ws + wgrad_copy_bytes(m, k_in, lo));
   for (int64_t c0 = 0; c0 < k_in; c0 += kw) {
     const int64_t n = std::min(kw, k_in - c0);
     if (m > 0) {
@@ -2580,13 +2596,13 @@ int wgrad_chunked(const uint16_t* ap, int64_t m, int64_t n_out, const uint8_t* x
       const bool vec = al16(x + c0) && k_in % 16 == 0;
       if (x_fmt == TCFP_FP8_E5M2)
         dequant_t_dup_bf16_kernel<TCFP_FP8_E5M2><<<unsigned(tx), 256, 0, st>>>(
-            x + c0, e_x + eo, m, n, shift, bp, k_in, !wrap, vec);
+            x + c0, e_x + eo, m, n, shift, bp, k_in, dup, vec);
       else
         dequant_t_dup_bf16_kernel<TCFP_FP8_E4M3><<<unsigned(tx), 256, 0, st>>>(
-            x + c0, e_x + eo, m, n, shift, bp, k_in, !wrap, vec);
+            x + c0, e_x + eo, m, n, shift, bp, k_in, dup, vec);
       if (hipGetLastError() != hipSuccess) return TCFP_ERR_HIP;
     }
-    const int rc = wgrad_gemm(ap, bp, m, n_out, n, dw + c0, k_in, part, wrap, st);
+    const int rc = wgrad_gemm(ap, bp, m, n_out, n, dw + c0, k_in, part, wrap, st, lo);
     if (rc != TCFP_OK) return rc;
   }
   return TCFP_OK;
@@ -2599,7 +2615,8 @@ int wgrad_chunked(const uint16_t* ap, int64_t m, int64_t n_out, const uint8_t* x
 //    exponent rule of block_quantize_fp8 (tcfp/kernels.py:205-275) and
 //    dequantised -- the dgrad's G operand;
 //  * gs [n, 2m] bf16: [bf16(g) | bf16(g - bf16(g))] transposed -- the
-//    wgrad's split gradient;
+//    wgrad's split gradient (with `lo` false gs [n, m]: bf16(g) transposed,
+//    the single-pass wgrad's operand);
 //  * cpart [ceil(m/64), n] fp32: per-tile column sums (the bias gradient
 //    after colsum_tiles_kernel).
 // n % 32 == 0 (the block sizes divide it).
@@ -2609,7 +2626,8 @@ __global__ __launch_bounds__(256) void grad_prep_kernel(const float* __restrict_
                                                         uint16_t* __restrict__ gs,
                                                         float* __restrict__ cpart,
                                                         uint8_t* __restrict__ gq,
-                                                        int8_t* __restrict__ ge, bool grouped) {
+                                                        int8_t* __restrict__ ge, bool grouped,
+                                                        bool lo) {
   __shared__ float tile[128][64 + 1];  // [column][row]
   const int tiles_c = int((n + 127) / 128);
   int64_t tr, c0;
@@ -2699,13 +2717,13 @@ __global__ __launch_bounds__(256) void grad_prep_kernel(const float* __restrict_
   const int cc = t >> 1, half = t & 1;
   const int64_t c = c0 + cc;
   float sum = 0.0f;
-  uint16_t hi[32], lo[32];
+  uint16_t hi[32], lo_v[32];
 #pragma unroll
   for (int j = 0; j < 32; ++j) {
     const float x = tile[cc][half * 32 + j];
     sum += x;
     hi[j] = f32_to_bf16_rne(x);
-    lo[j] = f32_to_bf16_rne(__fsub_rn(x, bf16_to_f32(hi[j])));
+    lo_v[j] = f32_to_bf16_rne(__fsub_rn(x, bf16_to_f32(hi[j])));
   }
   if (cpart) {
     const float other = __shfl_xor(sum, 1, 64);
@@ -2713,7 +2731,7 @@ __global__ __launch_bounds__(256) void grad_prep_kernel(const float* __restrict_
   }
   if (gs && c < n) {
     const int64_t rb = r0 + half * 32;
-    uint16_t* oh = gs + c * (2 * m) + rb;
+    uint16_t* oh = gs + c * (lo ? 2 * m : m) + rb;
     uint16_t* ol = oh + m;
     if ((m % 8) == 0 && rb + 32 <= m) {
 #pragma unroll
@@ -2722,14 +2740,17 @@ __global__ __launch_bounds__(256) void grad_prep_kernel(const float* __restrict_
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           wh[j] = uint32_t(hi[8 * q + 2 * j]) | (uint32_t(hi[8 * q + 2 * j + 1]) << 16);
-          wl[j] = uint32_t(lo[8 * q + 2 * j]) | (uint32_t(lo[8 * q + 2 * j + 1]) << 16);
+          wl[j] = uint32_t(lo_v[8 * q + 2 * j]) | (uint32_t(lo_v[8 * q + 2 * j + 1]) << 16);
         }
         reinterpret_cast<uint4*>(oh)[q] = make_uint4(wh[0], wh[1], wh[2], wh[3]);
-        reinterpret_cast<uint4*>(ol)[q] = make_uint4(wl[0], wl[1], wl[2], wl[3]);
+        if (lo) reinterpret_cast<uint4*>(ol)[q] = make_uint4(wl[0], wl[1], wl[2], wl[3]);
       }
     } else {
       for (int j = 0; j < 32; ++j)
-        if (rb + j < m) { oh[j] = hi[j]; ol[j] = lo[j]; }
+        if (rb + j < m) {
+          oh[j] = hi[j];
+          if (lo) ol[j] = lo_v[j];
+        }
     }
   }
 }
@@ -2766,7 +2787,8 @@ extern "C" size_t tcfp_block_grad_prep_workspace_bytes(int64_t m, int64_t n) {
 }
 
 extern "C" int tcfp_block_grad_prep(const float* g, int64_t m, int64_t n, int block,
-                                    uint16_t* g_deq, uint16_t* g_split_t, float* bias_grad,
+                                    uint16_t* g_deq, uint16_t* g_split_t, int split_lo,
+                                    float* bias_grad,
                                     uint8_t* g_fp8, int8_t* g_exps, void* workspace,
                                     size_t workspace_bytes, void* stream) {
   if (m < 0 || n < 0 || m > INT32_MAX || n > INT32_MAX) return TCFP_ERR_SHAPE;
@@ -2776,6 +2798,7 @@ extern "C" int tcfp_block_grad_prep(const float* g, int64_t m, int64_t n, int bl
   if (bias_grad && (!workspace || workspace_bytes < tcfp_block_grad_prep_workspace_bytes(m, n)))
     return TCFP_ERR_WORKSPACE;
   if ((g_fp8 == nullptr) != (g_exps == nullptr)) return TCFP_ERR_SHAPE;
+  if (split_lo != 0 && split_lo != 1) return TCFP_ERR_SHAPE;
   if (!al16(g) || (g_deq && !al16(g_deq)) || (g_split_t && !al16(g_split_t)) ||
       (g_fp8 && !al16(g_fp8)) || (workspace && !al16(workspace)))
     return TCFP_ERR_ALIGN;
@@ -2797,13 +2820,13 @@ extern "C" int tcfp_block_grad_prep(const float* g, int64_t m, int64_t n, int bl
   const bool grouped = n >= 8192;
   if (block == 32)
     grad_prep_kernel<32><<<grid, 256, 0, st>>>(g, m, n, g_deq, g_split_t, part, g_fp8, g_exps,
-                                                  grouped);
+                                                  grouped, split_lo != 0);
   else if (block == 64)
     grad_prep_kernel<64><<<grid, 256, 0, st>>>(g, m, n, g_deq, g_split_t, part, g_fp8, g_exps,
-                                                  grouped);
+                                                  grouped, split_lo != 0);
   else
     grad_prep_kernel<128><<<grid, 256, 0, st>>>(g, m, n, g_deq, g_split_t, part, g_fp8, g_exps,
-                                                  grouped);
+                                                  grouped, split_lo != 0);
   if (bias_grad)
     colsum_tiles_kernel<<<unsigned((n + 15) / 16), 256, 0, st>>>(part, tr, n, bias_grad);
   return hipGetLastError() == hipSuccess ? TCFP_OK : TCFP_ERR_HIP;
@@ -2843,28 +2866,31 @@ extern "C" int tcfp_block_wgrad(const float* g, int64_t m, int64_t n_out, const 
 }
 
 extern "C" size_t tcfp_block_wgrad_presplit_workspace_bytes(int64_t m, int64_t n_out,
-                                                           int64_t k_in) {
+                                                           int64_t k_in, int split_lo) {
   if (m < 0 || n_out < 0 || k_in < 0) return 0;
-  return wgrad_ws_bytes(m, n_out, k_in);
+  return wgrad_ws_bytes(m, n_out, k_in, split_lo != 0);
 }
 
-extern "C" int tcfp_block_wgrad_presplit(const uint16_t* g_split_t, int64_t m, int64_t n_out,
-                                         const uint8_t* x, int x_fmt, const int8_t* e_x,
-                                         int64_t k_in, int block, float* dw, void* workspace,
-                                         size_t workspace_bytes, void* stream) {
+extern "C" int tcfp_block_wgrad_presplit(const uint16_t* g_split_t, int split_lo, int64_t m,
+                                         int64_t n_out, const uint8_t* x, int x_fmt,
+                                         const int8_t* e_x, int64_t k_in, int block, float* dw,
+                                         void* workspace, size_t workspace_bytes, void* stream) {
   if (m < 0 || n_out < 0 || k_in < 0 || n_out > INT32_MAX || k_in > INT32_MAX ||
       4 * m > INT32_MAX)
     return TCFP_ERR_SHAPE;
   if (block != 32 && block != 64 && block != 128) return TCFP_ERR_SHAPE;
   if (k_in % block != 0 || m % 4 != 0) return TCFP_ERR_SHAPE;
+  // (the single pass contracts over whole 128-byte stages)
+  if (split_lo != 1 && (split_lo != 0 || m % 64 != 0)) return TCFP_ERR_SHAPE;
   if (x_fmt != TCFP_FP8_E4M3 && x_fmt != TCFP_FP8_E5M2) return TCFP_ERR_DTYPE;
   if (!g_split_t || !x || !e_x || !dw) return TCFP_ERR_SHAPE;
   if (n_out == 0 || k_in == 0) return TCFP_OK;
-  if (!workspace || workspace_bytes < tcfp_block_wgrad_presplit_workspace_bytes(m, n_out, k_in))
+  if (!workspace ||
+      workspace_bytes < tcfp_block_wgrad_presplit_workspace_bytes(m, n_out, k_in, split_lo))
     return TCFP_ERR_WORKSPACE;
   if (!al16(workspace) || !al16(dw) || !al16(g_split_t)) return TCFP_ERR_ALIGN;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int shift = block == 32 ? 5 : (block == 64 ? 6 : 7);
   return wgrad_chunked(g_split_t, m, n_out, x, x_fmt, e_x, k_in, shift, dw,
-                       static_cast<uint8_t*>(workspace), st);
+                       static_cast<uint8_t*>(workspace), st, split_lo != 0);
 }

@@ -1379,6 +1379,7 @@ def block_backward_prep(
     split: bool = True,
     bias: bool = False,
     fp8: bool = False,
+    split_lo: bool = True,
 ):
     """One pass over the fp32 gradient [M, N] for the block backward.
 
@@ -1388,7 +1389,8 @@ def block_backward_prep(
     ``block_quantize_fp8(grad, block_size, float8_e5m2)`` and dequantised
     (the exact dgrad's operand); ``g_fp8`` / ``g_exps`` are those codes and
     exponents themselves (the FP8 dgrad's operand); ``g_split_t`` [N, 2M]
-    bf16 is the transposed hi/lo split the block wgrad uses; ``bias_grad``
+    bf16 is the transposed hi/lo split the block wgrad uses (``split_lo``
+    False: [N, M], the transposed bf16(grad) of the single-pass wgrad); ``bias_grad``
     [N] fp32 is ``grad.sum(0)`` summed per 64-row tile.  These replace the
     quantise, dequantise, split and reduce passes the backward would
     otherwise make.
@@ -1398,7 +1400,8 @@ def block_backward_prep(
     dev = _hip.require_gpu(grad)
     g = grad if (grad.dtype == torch.float32 and grad.is_contiguous()) else grad.float().contiguous()
     g_deq = torch.empty((M, N), dtype=torch.bfloat16, device=dev) if dequant else None
-    g_split = torch.empty((N, 2 * M), dtype=torch.bfloat16, device=dev) if split else None
+    g_split = (torch.empty((N, 2 * M if split_lo else M), dtype=torch.bfloat16, device=dev)
+               if split else None)
     bias_grad = torch.empty((N,), dtype=torch.float32, device=dev) if bias else None
     g_fp8 = torch.empty((M, N), dtype=torch.float8_e5m2, device=dev) if fp8 else None
     g_exps = torch.empty((N // block_size, M), dtype=torch.int8, device=dev) if fp8 else None
@@ -1406,7 +1409,8 @@ def block_backward_prep(
     ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev) if bias else None
     check(
         _hip.lib().tcfp_block_grad_prep(
-            ptr(g), M, N, block_size, ptr(g_deq), ptr(g_split), ptr(bias_grad), ptr(g_fp8),
+            ptr(g), M, N, block_size, ptr(g_deq), ptr(g_split), int(split_lo), ptr(bias_grad),
+            ptr(g_fp8),
             ptr(g_exps), ptr(ws), nbytes, _hip.stream_of(dev),
         ),
         "block_backward_prep",
@@ -1507,19 +1511,23 @@ def fp8_block_dgrad(grad, w_hi_fp8, w_lo_fp8, w_hi_scales, w_lo_scales, block_si
 
 def block_wgrad_from_prep(g_split_t, act_fp8, act_scales, block_size):
     """``block_scaled_wgrad`` from the split gradient of
-    :func:`block_backward_prep` (same result bit for bit; M % 4 == 0)."""
+    :func:`block_backward_prep` (same result bit for bit; M % 4 == 0).  A
+    [N, M] operand (``split_lo=False``) gives the single-pass wgrad
+    ``bf16(grad)^T deq(act)`` (M % 64 == 0)."""
     N, M2 = g_split_t.shape
     M, Kd = act_fp8.shape
-    assert M2 == 2 * M and M % 4 == 0, "split gradient must be [N, 2M] with M % 4 == 0"
+    lo = M2 == 2 * M
+    assert (lo and M % 4 == 0) or (M2 == M and M % 64 == 0), (
+        "split gradient must be [N, 2M] with M % 4 == 0 or [N, M] with M % 64 == 0")
     dev = _hip.require_gpu(g_split_t, act_fp8, act_scales)
     a = act_fp8.contiguous()
     e = _block_exps(act_scales, M, Kd // block_size, "act_scales")
     out = torch.empty((N, Kd), dtype=torch.float32, device=dev)
-    nbytes = int(_hip.lib().tcfp_block_wgrad_presplit_workspace_bytes(M, N, Kd))
+    nbytes = int(_hip.lib().tcfp_block_wgrad_presplit_workspace_bytes(M, N, Kd, int(lo)))
     ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
     check(
         _hip.lib().tcfp_block_wgrad_presplit(
-            ptr(g_split_t), M, N, ptr(a), _fmt(a.dtype), ptr(e), Kd, block_size, ptr(out),
+            ptr(g_split_t), int(lo), M, N, ptr(a), _fmt(a.dtype), ptr(e), Kd, block_size, ptr(out),
             ptr(ws), nbytes, _hip.stream_of(dev),
         ),
         "block_wgrad_from_prep",

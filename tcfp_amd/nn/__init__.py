@@ -41,6 +41,7 @@ __all__ = [
     "convert_to_tcfp",
     "fuse_tcfp_mlp",
     "set_block_dgrad",
+    "set_block_wgrad",
     "_TCFP12TensorCoreFunction",
     "_TCFP12BlockScaledFunction",
     "_TCFP12FusedMLPFunction",
@@ -209,6 +210,28 @@ def set_block_dgrad(mode: str) -> None:
     _BLOCK_DGRAD = mode
 
 
+_BLOCK_WGRAD = "split"
+
+
+def set_block_wgrad(mode: str) -> None:
+    """Numerics of the block-scaled layers' weight gradient (default
+    ``"split"``).
+
+    ``"split"``: the reference's ``dW = G^T @ deq(X)`` with G in fp32,
+    computed as two exact bf16 passes over ``[bf16(G) | bf16(G - bf16(G))]``
+    (the reference's fp32 product to within fp32 accumulation).
+    ``"bf16"``: one pass over ``bf16(G)`` (relative error ~2^-9 per gradient
+    element, within the reference's 1e-2 GEMM contract): half the MFMA
+    work, and the gradient's low half is never stored.  Token counts that
+    are not a multiple of 64 keep the split.  Read when a layer's forward
+    runs, like :func:`set_block_dgrad`.
+    """
+    global _BLOCK_WGRAD
+    if mode not in ("split", "bf16"):
+        raise ValueError(f"block wgrad mode must be 'split' or 'bf16', got {mode!r}")
+    _BLOCK_WGRAD = mode
+
+
 class _TCFP12BlockScaledFunction(torch.autograd.Function):
     """TCFP-12 with per-block (32/64/128 along K) power-of-two scales
     (reference ``tcfp/nn/__init__.py:574-761``)."""
@@ -256,6 +279,7 @@ class _TCFP12BlockScaledFunction(torch.autograd.Function):
         ctx.bs = bs
         ctx.abd = abd
         ctx.fp8_dgrad = _BLOCK_DGRAD == "fp8"
+        ctx.bf16_wgrad = _BLOCK_WGRAD == "bf16"
         # only what the backward will use is kept: the activation codes for
         # dW, the weight codes for dX
         need_dx, need_dw = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
@@ -291,7 +315,8 @@ class _TCFP12BlockScaledFunction(torch.autograd.Function):
         fp8_dx = need_dx and ctx.fp8_dgrad
         if exact_dx or fp8_wgrad or want_db or fp8_dx:
             res = K.block_backward_prep(
-                grad_2d, bs, dequant=exact_dx, split=fp8_wgrad, bias=want_db, fp8=fp8_dx
+                grad_2d, bs, dequant=exact_dx, split=fp8_wgrad, bias=want_db, fp8=fp8_dx,
+                split_lo=not (ctx.bf16_wgrad and grad_2d.shape[0] % 64 == 0),
             )
             g_deq, g_split, db = res[:3]
             if fp8_dx:

@@ -841,6 +841,19 @@ def test_block_backward_prep_matches_separate_passes(dev, bs, M, N, K_):
         dw_a = K.block_scaled_wgrad(grad, aq, ea, bs)
         dw_b = K.block_wgrad_from_prep(g_split, aq, ea, bs)
         assert torch.equal(dw_a, dw_b)
+    # the single-pass operand: bf16(g) transposed, the split's first half
+    g_hi = K.block_backward_prep(grad, bs, dequant=False, split=True, split_lo=False)[1]
+    assert torch.equal(g_hi, hi.t().contiguous())
+    if M % 64 == 0:
+        # the single-pass wgrad: bf16(g)^T deq(x) with fp32 accumulation,
+        # and within 2^-9-level error of the fp32 gradient's product
+        dw_1 = K.block_wgrad_from_prep(g_hi, aq, ea, bs)
+        A = K.block_dequantize_fp8(aq, ea, bs).double()
+        ref_hi = hi.double().t() @ A
+        ref = grad.double().t() @ A
+        rel = lambda a, b: (torch.linalg.norm(a.double() - b) / torch.linalg.norm(b)).item()  # noqa: E731
+        assert rel(dw_1, ref_hi) < 1e-5
+        assert rel(dw_1, ref) < 4e-3
 
 
 @pytest.mark.parametrize("bs", [32, 64, 128])

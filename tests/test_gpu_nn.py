@@ -302,6 +302,43 @@ def test_delayed_scaling_layer(dev):
     assert st._step_count[a._param_name + ".steps"] == 31
 
 
+def test_c5_scaleup_single_pass_wgrad(dev):
+    """``set_block_wgrad("bf16")`` on the C5 scale-up layer at full size
+    (Linear(4096, 16384), block 64 + SRR, 8192 tokens): the output and dX
+    are those of the default split wgrad bit for bit, and dW -- one bf16
+    pass over bf16(G) -- is within 4e-3 relative Frobenius of the fp32
+    product G^T deq(X) (the reference's GEMM contract is 1e-2)."""
+    from tcfp_amd import kernels as K
+    from tcfp_amd.nn import set_block_wgrad
+
+    bs = 64
+    grads = {}
+    for mode in ("split", "bf16"):
+        set_block_wgrad(mode)
+        try:
+            torch.manual_seed(3)
+            lin = TCFPLinear(4096, 16384, use_tensor_cores=True, scale_block_size=bs,
+                             srr=True).to(dev)
+            x = torch.randn(8192, 4096, device=dev, dtype=torch.bfloat16, requires_grad=True)
+            torch.manual_seed(123)
+            out = lin(x)
+            go = torch.randn(out.shape, generator=torch.Generator(device=dev).manual_seed(5),
+                             device=dev) * 1e-3
+            out.backward(go)
+            grads[mode] = (out.detach(), x.grad, lin.weight.grad)
+        finally:
+            set_block_wgrad("split")
+    print("[c5 scale-up] single-pass wgrad", flush=True)
+    assert torch.equal(grads["split"][0], grads["bf16"][0])
+    assert torch.equal(grads["split"][1], grads["bf16"][1])
+    aq, ea = K.block_quantize_fp8(x.detach(), bs)
+    dw_ref = go.t() @ K.block_dequantize_fp8(aq, ea, bs)
+    err = lambda a: (torch.linalg.norm(a - dw_ref) / torch.linalg.norm(dw_ref)).item()  # noqa: E731
+    e1, e2 = err(grads["bf16"][2]), err(grads["split"][2])
+    print(f"dW rel_fro: single pass {e1:.2e}, split {e2:.2e}", flush=True)
+    assert e1 < 4e-3 and e2 < 2e-5
+
+
 @pytest.mark.parametrize("d_in,d_out", [(4096, 16384), (16384, 4096)])
 def test_c5_scaleup_layer_full_size(dev, d_in, d_out):
     """configs[4]'s scale-up layers at full size: Linear(4096, 16384) and
