@@ -268,6 +268,27 @@ def rotated_time_ms(calls, rounds, stream):
 COLD_BYTES = 768 << 20  # working set of the cold protocol: 3 x the Infinity Cache
 
 
+def bench_dual_quant_cold(rounds=10):
+    """Only the cold rotation of the per-tensor dual-quant + EF row at
+    4096^2 (five W + EF sets, 640 MB), for profiling its kernels and
+    traffic under the cold protocol."""
+    import torch
+
+    from tcfp_amd import kernels as K
+
+    dev = torch.device("cuda:0")
+    sets = []
+    for i in range(5):
+        g = torch.Generator(device=dev).manual_seed(100 + i)
+        sets.append((torch.randn(4096, 4096, device=dev, generator=g) * 0.02,
+                     torch.zeros(4096, 4096, device=dev)))
+    calls = [lambda w=w, ef=ef: K.dual_quantize_per_tensor(w, ef) for w, ef in sets]
+    ms = rotated_time_ms(calls, rounds, torch.cuda.current_stream(dev))
+    return {"per_tensor_ef_4096x4096_cold_ms": ms,
+            "per_tensor_ef_4096x4096_cold_GBs": 14 * 4096 * 4096 / (ms * 1e-3) / 1e9,
+            "calls": rounds * len(calls) + len(calls)}
+
+
 def bench_dual_quant(iters=20, cold_rounds=4):
     """The quantisation kernels at the sizes the configs use, each timed two
     ways: warm (``iters`` back-to-back calls on one set of buffers, which
@@ -735,8 +756,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--part", choices=("all", "gemm", "quant", "block", "mlp", "c5", "c5mem",
-                                       "copy", "scaled_mm"),
+    ap.add_argument("--part", choices=("all", "gemm", "quant", "quantcold", "block", "mlp", "c5",
+                                       "c5mem", "copy", "scaled_mm"),
                     default="all",
                     help="all (default) = headline + every secondary figure; the others run "
                          "one workload (for profiling)")
@@ -757,6 +778,7 @@ def main():
     if args.part != "all" and args.part != "gemm":
         fn = {"quant": lambda: bench_dual_quant(), "block": lambda: bench_block_gemms(),
               "c5": lambda: bench_c5(), "c5mem": lambda: bench_c5_memory(),
+              "quantcold": lambda: bench_dual_quant_cold(max(1, args.steps // 20)),
               "mlp": lambda: bench_mlp(
                   steps=args.steps,
                   arms=("tcfp", "tcfp_fused", "bf16", "fp32") if args.arm == "both"
