@@ -1047,12 +1047,22 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && NS == 2 && BM <= 128 ? 2 : 1))
 // earlier load anyway; the E8M0 codes are formed at the end of the stage,
 // after the refill DMA, without a further wait (a wait there would also
 // wait for that DMA).
-template <int AF, int BF, typename OutT, int EPI = 0, int SCALE = 0, int ND = 8, int BNT = 128>
+//
+// SPL (single GEMM, 256 x 64 slots): the two weight slots are two adjacent
+// 64-row blocks of one B (the launcher points B1 / e_1 64 rows past B0 /
+// e_0), each with its own accumulator set, written to the two 64-column
+// halves of a 256 x 128 output tile.  Block-scaled single GEMMs keep two
+// accumulator sets, which the 256 x 128 slots' registers do not hold; the
+// 256 x 64 slots' do.
+template <int AF, int BF, typename OutT, int EPI = 0, int SCALE = 0, int ND = 8, int BNT = 128,
+          bool SPL = false>
 __global__ __launch_bounds__(512, 1) void gemm_nt_persist_kernel(GemmArgs g) {
   constexpr bool F32OUT = std::is_same<OutT, float>::value;
   static_assert(EPI == 0 || F32OUT, "GELU epilogues write fp32");
   static_assert(SCALE == 0 || (SCALE == 1 && EPI == 0), "block exponents: plain epilogue only");
-  constexpr int NACC = SCALE == 1 ? 1 : 2;
+  static_assert(!SPL || (BNT == 64 && EPI == 0 && F32OUT), "single GEMM: 256 x 64 slots, fp32");
+  constexpr int NACC = (SCALE == 1 && !SPL) ? 1 : 2;
+  constexpr int NSL = SPL ? 2 : 1;  // output column blocks per tile
   constexpr int NW = 8, BM = 256, BN = BNT, NS = 2;
   // BN = 64 (EPI 2 only): the GELU derivative factors of the tile (256 x 64
   // fp32, 64 KiB) are brought into LDS beside the two 48 KiB operand stages
@@ -1061,9 +1071,9 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persist_kernel(GemmArgs g) {
   // for its 128 KiB of factors, and loading them in the epilogue, every CU
   // at once, left the matrix cores idle: 8192 x 4096 x 1024 ran 120.9 us
   // against 74.4 us with the loads taken out (timing copy).
-  constexpr bool DGL = BNT == 64;
-  static_assert(BNT == 128 || (BNT == 64 && EPI == 2 && SCALE == 0 && F32OUT),
-                "the 256 x 64 tile serves the GELU backward epilogue");
+  constexpr bool DGL = BNT == 64 && EPI == 2;
+  static_assert(BNT == 128 || (BNT == 64 && EPI == 2 && SCALE == 0 && F32OUT) || SPL,
+                "the 256 x 64 tile serves the GELU backward epilogue and single GEMMs");
   constexpr int WM = NW / 2, TMW = BM / WM, MB = TMW / 32;
   constexpr int TNW = BN / 2, NB = TNW / 32, NF = 2 * NB;
   constexpr int SROWS = BM + 2 * BN;
@@ -1083,7 +1093,7 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persist_kernel(GemmArgs g) {
   constexpr int CPR = RB / 16;     // 16-byte chunks per row
   constexpr int RPI = 64 / CPR;    // rows per store instruction
   // store instructions per wave and tile
-  constexpr int NST = F32OUT ? MB * NB * 4 : TMW / RPI;
+  constexpr int NST = F32OUT ? NSL * MB * NB * 4 : TMW / RPI;
   static_assert(F32OUT || NW * TMW * RB <= STAGE, "epilogue staging must fit one operand buffer");
   // (a DMA wave holds at most two stages' DMA and one tile's stores in flight)
   static_assert(NST + 2 * DI <= 63, "vmcnt immediate");
@@ -1102,7 +1112,7 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persist_kernel(GemmArgs g) {
   constexpr bool kBiasLds = SCALE == 1;
   // one LDS array: the operand stages, then the bias columns (block
   // exponents), then the derivative factors (DGL)
-  constexpr int kBiasB = kBiasLds ? BN * 4 : 0;
+  constexpr int kBiasB = kBiasLds ? NSL * BN * 4 : 0;
   constexpr int kDgB = DGL ? BM * BN * 4 : 0;
   __shared__ __align__(16) uint8_t lds[NS * STAGE + kBiasB + kDgB];
   float* const bias_s = reinterpret_cast<float*>(lds + NS * STAGE);
@@ -1158,7 +1168,7 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persist_kernel(GemmArgs g) {
     const int first_m = (l / per_group) * G;
     const int gm = min(g.tiles_m - first_m, G);
     m0 = (first_m + (l % per_group) % gm) * BM;
-    n0 = ((l % per_group) / gm) * BN;
+    n0 = ((l % per_group) / gm) * (NSL * BN);
   };
   auto src_of = [&](int m0, int n0) {
     return make_rsrc(src_base + int64_t(region == 0 ? m0 : n0) * ld, nrec);
@@ -1393,7 +1403,7 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persist_kernel(GemmArgs g) {
         }
       }
       const bool bias_stage =
-          kBiasLds && g.bias != nullptr && t == (nt > 2 ? nt - 2 : 0) && tid < BN;
+          kBiasLds && g.bias != nullptr && t == (nt > 2 ? nt - 2 : 0) && tid < NSL * BN;
       float bv = 0.0f;
       if (bias_stage) bv = g.bias[n0 + tid];
       read_frags(f1, b, 1);
@@ -1520,19 +1530,25 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persist_kernel(GemmArgs g) {
         // stage's barrier; stale and unused after the last tile)
         read_frags(f0, sb ^ 1, 0);
       } else {
+        // (SPL: output column block sl of the tile from accumulator set sl)
+#pragma unroll
+        for (int sl = 0; sl < NSL; ++sl)
 #pragma unroll
         for (int i = 0; i < MB; ++i)
 #pragma unroll
           for (int j = 0; j < NB; ++j)
 #pragma unroll
             for (int gq = 0; gq < 4; ++gq) {
-              const int row = i * 32 + lr, col = j * 32 + gq * 8 + lg * 4;
+              const int row = i * 32 + lr, col = sl * BN + j * 32 + gq * 8 + lg * 4;
               const int64_t o = int64_t(m0 + wm * TMW + row) * g.ldo + nb + col;
               float v[4];
 #pragma unroll
               for (int q = 0; q < 4; ++q) {
                 const int r = gq * 4 + q;
-                v[q] = accv(j, i, r, c0s, c1s);
+                if constexpr (SPL)
+                  v[q] = SCALE == 1 ? acc[sl][j][i][r] : acc[sl][j][i][r] * c0s;
+                else
+                  v[q] = accv(j, i, r, c0s, c1s);
               }
               if (g.bias) {
                 if constexpr (kBiasLds) {
@@ -1713,6 +1729,24 @@ bool persist_eligible(const GemmArgs& ga) {
 template <int AF, int BF, bool SPLIT, typename OutT, int SCALE>
 int launch_gemm(GemmArgs ga, hipStream_t st) {
   const int m = ga.M, n = ga.N, k = ga.K;
+  if constexpr (SCALE == 1 && SPLIT && AF != kBF16 && std::is_same<OutT, float>::value) {
+    // block-scaled single GEMM with more full 256 x 128 tiles than CUs: the
+    // persistent kernel with the two weight slots on adjacent 64-row blocks
+    // (32-bit exponent offsets)
+    if (persist_eligible(ga) &&
+        int64_t(k >> ga.bs_shift) * (m > n ? m : n) < int64_t(INT32_MAX)) {
+      if (ga.bias != nullptr && (reinterpret_cast<uintptr_t>(ga.bias) & 15) != 0)
+        return TCFP_ERR_ALIGN;
+      GemmArgs gp = ga;
+      gp.B1 = ga.B0 + 64 * ga.ldb;
+      gp.e_1 = ga.e_0 + 64;
+      gp.tiles_m = m / 256;
+      gp.tiles_n = n / 128;
+      gemm_nt_persist_kernel<AF, BF, float, 0, 1, 6, 64, true>
+          <<<unsigned(num_cus()), 512, 0, st>>>(gp);
+      return hipGetLastError() == hipSuccess ? TCFP_OK : TCFP_ERR_HIP;
+    }
+  }
   // large tile unless it would leave CUs idle
   const int big_tiles = ((m + 255) / 256) * ((n + (SPLIT ? 255 : 127)) / (SPLIT ? 256 : 128));
   // (block-scaled single GEMMs keep two accumulator sets, which only the

@@ -893,6 +893,8 @@ def test_c3_4096_cubed_single_block64_against_torch_fp32(dev):
     print("[c3 single] bs=64 4096^3", flush=True)
     a, ea = K.block_quantize_fp8(x, bs)
     b, eb = K.block_quantize_fp8(w, bs)
+    names = _kernel_names(lambda: K.block_scaled_gemm(a, b, ea, eb, bs))
+    assert any("gemm_nt_persist_kernel<0, 0, float, 0, 1, 6, 64, true>" in n for n in names), names
     out = K.block_scaled_gemm(a, b, ea, eb, bs)
     ref = K.block_dequantize_fp8(a, ea, bs) @ K.block_dequantize_fp8(b, eb, bs).t()
     err = (torch.linalg.norm(out - ref) / torch.linalg.norm(ref)).item()

@@ -42,13 +42,16 @@ PATHS = {
     "large": ("large_nonpersistent", SMALL, "8, 256, 128, {S}, 2, "),
     "persist": ("auto", BIG, None),
     "small": ("auto", SMALL, "4, 128, 64, {S}, 2, "),  # block scales: two stages
+    # block-scaled single GEMM, fp32 output: the persistent kernel with the
+    # two weight slots on adjacent 64-row blocks
+    "persist_spl": ("auto", BIG, None),
 }
 # (scale kind, dual) -> the tile paths the dispatcher has for it
 SCALE_PATHS = {
     ("pt", True): ["deep", "small8", "small2", "large", "persist"],
     ("pt", False): ["deep", "small8", "small2", "large"],
     ("e8m0", True): ["small", "large", "persist"],
-    ("e8m0", False): ["small"],
+    ("e8m0", False): ["small", "persist_spl"],
     ("f32s", True): ["small"],
     ("f32s", False): ["small"],
 }
@@ -58,6 +61,8 @@ def _cases():
     for (kind, dual), paths in SCALE_PATHS.items():
         for path in paths:
             for od in OUT:
+                if path == "persist_spl" and od != "f32":
+                    continue
                 for af in (0, 1):
                     for bf in (0, 1):
                         bss = (32, 64, 128) if kind == "f32s" else ((64,) if kind == "e8m0" else (0,))
@@ -145,8 +150,10 @@ def test_gemm_instantiation_against_float64(dev, kind, bs, dual, path, od, af, b
     ref += f64(bias)[None, :]
 
     split = "false" if dual else "true"
-    if frag is None:
-        want = f"gemm_nt_persist_kernel<{af}, {bf}, {out_name}, 0, {scale_id}, 8, 128>"
+    if path == "persist_spl":
+        want = f"gemm_nt_persist_kernel<{af}, {bf}, float, 0, 1, 6, 64, true>"
+    elif frag is None:
+        want = f"gemm_nt_persist_kernel<{af}, {bf}, {out_name}, 0, {scale_id}, 8, 128, false>"
     else:
         want = f"gemm_nt_dma_kernel<{af}, {bf}, {split}, {out_name}, " + frag.format(S=scale_id)
         if kind == "f32s":

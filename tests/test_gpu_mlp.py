@@ -229,14 +229,14 @@ def test_gemm_epilogue_replaces_the_gelu_passes_at_c4(dev):
     fwd()
     torch.cuda.synchronize()  # the premise check has run
     names = _kernel_names(fwd)
-    assert any("gemm_nt_persist_kernel<0, 0, float, 1, 0, 8, 128>" in n for n in names), names
+    assert any("gemm_nt_persist_kernel<0, 0, float, 1, 0, 8, 128, false>" in n for n in names), names
     assert not any("gelu_amax_kernel" in n or "amax_part_kernel" in n for n in names), names
     g8, hi2, lo2, g_inv, ih2, il2 = _fp8_layer(dev, 8192, 1024, 4096, seed=2,
                                                a_dtype=torch.float8_e5m2)
     dg = torch.rand(8192, 4096, device=dev)
     names = _kernel_names(lambda: K.dual_gemm_dgelu_quantize_colsum(
         g8, hi2, lo2, g_inv, ih2, il2, dg, transpose=True))
-    assert any("gemm_nt_persist_kernel<1, 0, float, 2, 0, 6, 64>" in n for n in names), names
+    assert any("gemm_nt_persist_kernel<1, 0, float, 2, 0, 6, 64, false>" in n for n in names), names
     assert not any("amax" in n for n in names), names
 
 
@@ -390,7 +390,7 @@ def test_dgelu_epilogue_narrow_tile_matches_wide(dev, m, k, n):
                                                     transpose=True, col_sum=True,
                                                     return_grad=True)
     names = _kernel_names(run)
-    assert any("gemm_nt_persist_kernel<1, 0, float, 2, 0, 6, 64>" in x for x in names), names
+    assert any("gemm_nt_persist_kernel<1, 0, float, 2, 0, 6, 64, false>" in x for x in names), names
     p = run()
     try:
         K.set_gemm_tile_policy("large")
