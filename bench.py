@@ -268,6 +268,42 @@ def rotated_time_ms(calls, rounds, stream):
 COLD_BYTES = 768 << 20  # working set of the cold protocol: 3 x the Infinity Cache
 
 
+def bench_quant_in_consumer(iters=50, rounds=5):
+    """Quantisation inside the consuming GEMM against a separate pass, at
+    the C4 gradient's consumer shapes: this build's in-GEMM activation
+    quantisation (the block-scaled act-quant GEMM, a11) against
+    ``block_quantize_fp8`` + the block dual GEMM on the same operands (the
+    results are identical; the in-GEMM form re-quantises each activation
+    panel once per output-column tile).  Median of ``rounds``."""
+    import torch
+
+    from tcfp_amd import kernels as K
+
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream(dev)
+    bs = 64
+    out = {}
+    for (m, n, k) in ((8192, 4096, 1024), (8192, 1024, 4096), (8192, 512, 1024)):
+        g = torch.Generator(device=dev).manual_seed(1)
+        x = torch.randn(m, k, device=dev, generator=g)
+        w = torch.randn(n, k, device=dev, generator=g) * 0.02
+        h, l, eh, el = K.fused_dual_quantize_fp8(w, bs)
+
+        def fused():
+            return K.fused_act_quant_dual_gemm_forward(x, h, l, eh, el, bs,
+                                                       save_side_outputs=False)[0]
+
+        def sep():
+            aq, ea = K.block_quantize_fp8(x, bs)
+            return K.fused_block_scaled_dual_gemm_forward(aq, h, l, ea, eh, el, bs)
+
+        same = bool(torch.equal(fused(), sep()))
+        tf = sorted(event_time_ms(fused, iters, stream) for _ in range(rounds))[rounds // 2]
+        ts = sorted(event_time_ms(sep, iters, stream) for _ in range(rounds))[rounds // 2]
+        out[f"{m}x{n}x{k}_fp32"] = {"in_gemm_ms": tf, "separate_ms": ts, "identical": same}
+    return out
+
+
 def bench_dual_quant_cold(rounds=10):
     """Only the cold rotation of the per-tensor dual-quant + EF row at
     4096^2 (five W + EF sets, 640 MB), for profiling its kernels and
@@ -756,8 +792,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--part", choices=("all", "gemm", "quant", "quantcold", "block", "mlp", "c5",
-                                       "c5mem", "copy", "scaled_mm"),
+    ap.add_argument("--part", choices=("all", "gemm", "quant", "quantcold", "quantfuse", "block",
+                                       "mlp", "c5", "c5mem", "copy", "scaled_mm"),
                     default="all",
                     help="all (default) = headline + every secondary figure; the others run "
                          "one workload (for profiling)")
@@ -779,6 +815,7 @@ def main():
         fn = {"quant": lambda: bench_dual_quant(), "block": lambda: bench_block_gemms(),
               "c5": lambda: bench_c5(), "c5mem": lambda: bench_c5_memory(),
               "quantcold": lambda: bench_dual_quant_cold(max(1, args.steps // 20)),
+              "quantfuse": lambda: bench_quant_in_consumer(),
               "mlp": lambda: bench_mlp(
                   steps=args.steps,
                   arms=("tcfp", "tcfp_fused", "bf16", "fp32") if args.arm == "both"
