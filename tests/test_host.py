@@ -379,3 +379,23 @@ def test_quantize_batch_validation_without_launch():
     assert lib.tcfp_quantize_batch(1, jobs, p, one, None) == 1  # cols % 8
     jobs[0] = _hip.QuantJob(_hip.JOB_ACT, p, 0, 4, 16, None, 0, 5, p, None, p, None, None, None)
     assert lib.tcfp_quantize_batch(1, jobs, p, one, None) == 2  # fp8 format
+
+
+def test_single_pass_wgrad_arguments_without_launch():
+    """The split_lo argument of tcfp_block_grad_prep and
+    tcfp_block_wgrad_presplit: 0 or 1 only, and the single pass (0) only
+    for token counts that are a multiple of 64 -- checked before anything
+    is launched (dummy pointers); the single pass's workspace is no larger
+    than the split's."""
+    lib = _hip.load_library()
+    p = 4096
+    # (g, m, n, block, g_deq, g_split_t, split_lo, bias_grad, g_fp8, g_exps, ws, ws_bytes, stream)
+    assert lib.tcfp_block_grad_prep(p, 128, 256, 64, None, p, 2, None, None, None, None, 0,
+                                    None) == 1
+    # (g_split_t, split_lo, m, n_out, x, x_fmt, e_x, k_in, block, dw, ws, ws_bytes, stream)
+    ws1 = lib.tcfp_block_wgrad_presplit_workspace_bytes(128, 256, 512, 1)
+    ws0 = lib.tcfp_block_wgrad_presplit_workspace_bytes(128, 256, 512, 0)
+    assert 0 < ws0 <= ws1
+    assert lib.tcfp_block_wgrad_presplit(p, 2, 128, 256, p, 0, p, 512, 64, p, p, ws1, None) == 1
+    assert lib.tcfp_block_wgrad_presplit(p, 0, 100, 256, p, 0, p, 512, 64, p, p, ws1, None) == 1
+    assert lib.tcfp_block_wgrad_presplit(p, 0, 128, 256, p, 0, p, 512, 64, p, p, 0, None) == 5
