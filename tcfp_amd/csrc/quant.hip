@@ -2681,7 +2681,6 @@ __global__ __launch_bounds__(kThreads) void batch_amax_kernel(BatchArgs a) {
   int bid;
   const int j = batch_job(a, 0, &bid);
   const BatchJob& b = a.j[j];
-  const int nbk = a.off[0][j + 1] - a.off[0][j];
   if (bid >= b.g1) return;  // (the padding up to a multiple of 8)
   const int64_t n = b.rows * b.cols;
   if (b.bf16) {
@@ -2693,7 +2692,6 @@ __global__ __launch_bounds__(kThreads) void batch_amax_kernel(BatchArgs a) {
     if (b.has_ef) amax_part_body<float, true, false>(x, b.ef, n, b.ws->a, nullptr, nullptr, bid, b.g1, red, rd);
     else amax_part_body<float, false, false>(x, nullptr, n, b.ws->a, nullptr, nullptr, bid, b.g1, red, rd);
   }
-  (void)nbk;
 }
 
 __global__ __launch_bounds__(kThreads) void batch_hi_kernel(BatchArgs a) {
