@@ -1188,10 +1188,13 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persist_kernel(GemmArgs g) {
   // reads (32 rows, one chunk each) spread over every bank.  The waves that
   // issue no operand DMA (ND .. NW - 1) load them: they wait for memory
   // only at the tile's last barrier, so the pieces -- read from HBM -- have
-  // the whole tile to land.  (Issued by the DMA waves, each stage's barrier
-  // waited for that stage's pieces: no faster than the epilogue loads.)
-  // Wave ND + w issues pieces w, w + (NW - ND), ..., its k-th at stage
-  // k % (nt - 1).
+  // the rest of the tile to land.  (Issued by the DMA waves, each stage's
+  // barrier waited for that stage's pieces: no faster than the epilogue
+  // loads.)  Wave ND + w issues pieces w, w + (NW - ND), ..., its k-th at
+  // stage k % min(nt - 1, 2): all of them in the tile's first two stages.
+  // Spread over every stage, the last pieces left about one stage before
+  // the last barrier and every tile waited there for an HBM round trip
+  // (8192 x 4096 x 1024: 120.7 us, 86.2 us with no factor loads at all).
   constexpr int NDG = NW - ND;  // factor-loading waves
   const uint32_t dg_lds0 = lds0 + uint32_t(NS * STAGE + kBiasB);
   const uint32_t ldo_b = uint32_t(g.ldo) * 4u;
@@ -1199,7 +1202,7 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persist_kernel(GemmArgs g) {
   const uint32_t dg_nrec = uint32_t(int64_t(BM - 1) * g.ldo * 4 + BN * 4);
   auto issue_dg = [&](const v4i& rs, int t) {
     if constexpr (DGL) {
-      const int span = nt - 1;  // nt >= 2
+      const int span = nt - 1 < 2 ? nt - 1 : 2;  // nt >= 2
       if (t >= span) return;
       for (int k = t; k < dg_np; k += span) {
         const int p = (wave - ND) + NDG * k;
