@@ -964,6 +964,26 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && NS == 2 && BM <= 128 ? 2 : 1))
 #pragma unroll
   for (int s = 0; s < (SPLIT ? 2 : 1); ++s) {
     const int nb = (s ? n1 : n0) + wn * TNW;  // first output column of this tile
+    // the lane's bias columns, loaded once for all its rows (16-byte loads
+    // where the four columns are in range; the pointer is 16-byte aligned).
+    // Not with fp32 block scales, whose single-GEMM block-32 variant has no
+    // registers to spare for them.
+    constexpr bool kBiasHoist = SCALE != 2;
+    float4 bq[kBiasHoist ? NB * 4 : 1];
+    if (kBiasHoist && g.bias) {
+#pragma unroll
+      for (int j = 0; j < NB; ++j)
+#pragma unroll
+        for (int gq = 0; gq < 4; ++gq) {
+          const int c = nb + j * 32 + gq * 8 + lg * 4;
+          if (c + 3 < N) {
+            bq[j * 4 + gq] = *reinterpret_cast<const float4*>(g.bias + c);
+          } else {
+            bq[j * 4 + gq] = make_float4(c < N ? g.bias[c] : 0.0f, c + 1 < N ? g.bias[c + 1] : 0.0f,
+                                         c + 2 < N ? g.bias[c + 2] : 0.0f, 0.0f);
+          }
+        }
+    }
 #pragma unroll
     for (int i = 0; i < MB; ++i)
 #pragma unroll
@@ -980,8 +1000,16 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && NS == 2 && BM <= 128 ? 2 : 1))
             else v[q] = acc[0][j][i][r] * c0s + acc[NACC - 1][j][i][r] * c1s;
           }
           if (g.bias) {
+            if constexpr (kBiasHoist) {
+              const float4 b4 = bq[j * 4 + gq];
+              v[0] += b4.x;
+              v[1] += b4.y;
+              v[2] += b4.z;
+              v[3] += b4.w;
+            } else {
 #pragma unroll
-            for (int q = 0; q < 4; ++q) v[q] += nb + col + q < N ? g.bias[nb + col + q] : 0.0f;
+              for (int q = 0; q < 4; ++q) v[q] += nb + col + q < N ? g.bias[nb + col + q] : 0.0f;
+            }
           }
           // 16-byte chunk index within the row, XOR-permuted by row
           const int byte = col * EB;
