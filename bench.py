@@ -268,6 +268,51 @@ def rotated_time_ms(calls, rounds, stream):
 COLD_BYTES = 768 << 20  # working set of the cold protocol: 3 x the Infinity Cache
 
 
+def bench_gemm_sweep(iters=50, rounds=3):
+    """Per-tensor dual FP8 GEMM over the configs' shapes and a K sweep
+    (M x N x K, fp32 and bf16 output, E4M3 operands, no bias), plus the
+    single FP8 GEMM at the wgrad shapes: median of ``rounds`` event-timed
+    runs of ``iters`` back-to-back launches each.  The K sweep separates
+    the main loop's rate (the slope) from a GEMM's fixed cost (the
+    intercept: prologue and the output written)."""
+    import torch
+
+    from tcfp_amd import kernels as K
+
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream(dev)
+    out = {}
+
+    def timed(fn):
+        return sorted(event_time_ms(fn, iters, stream) for _ in range(rounds))[rounds // 2]
+
+    shapes = [(8192, 4096, k) for k in (1024, 2048, 4096, 8192)] + \
+             [(8192, 1024, k) for k in (1024, 2048, 4096, 8192)] + [(4096, 4096, 4096)]
+    # out of the idle-to-busy clock ramp first (1500 back-to-back launches)
+    g = torch.Generator(device=dev).manual_seed(1)
+    a, sa = K.quantize_per_tensor(torch.randn(4096, 4096, device=dev, generator=g))
+    h, l, ih, il = K.dual_quantize_per_tensor(torch.randn(4096, 4096, device=dev, generator=g))
+    for _ in range(1500):
+        K.fused_dual_gemm_forward(a, h, l, sa, ih, il, out_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    for (m, n, k) in shapes:
+        g = torch.Generator(device=dev).manual_seed(m + n + k)
+        a, sa = K.quantize_per_tensor(torch.randn(m, k, device=dev, generator=g))
+        h, l, ih, il = K.dual_quantize_per_tensor(torch.randn(n, k, device=dev, generator=g))
+        for od in (torch.float32, torch.bfloat16):
+            ms = timed(lambda: K.fused_dual_gemm_forward(a, h, l, sa, ih, il, out_dtype=od))
+            key = f"dual_{m}x{n}x{k}_{'f32' if od == torch.float32 else 'bf16'}"
+            out[key] = {"ms": ms, "tflops": 4.0 * m * n * k / (ms * 1e-3) / 1e12}
+    for (m, n, k) in ((4096, 1024, 8192), (1024, 4096, 8192)):
+        g = torch.Generator(device=dev).manual_seed(m + n + k)
+        a, sa = K.quantize_per_tensor(torch.randn(m, k, device=dev, generator=g),
+                                      torch.float8_e5m2)
+        b, sb = K.quantize_per_tensor(torch.randn(n, k, device=dev, generator=g))
+        ms = timed(lambda: K.fp8_gemm_nt(a, b, sa, sb))
+        out[f"single_{m}x{n}x{k}_f32"] = {"ms": ms, "tflops": 2.0 * m * n * k / (ms * 1e-3) / 1e12}
+    return out
+
+
 def bench_quant_in_consumer(iters=50, rounds=5):
     """Quantisation inside the consuming GEMM against a separate pass, at
     the C4 gradient's consumer shapes: this build's in-GEMM activation
@@ -792,8 +837,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--part", choices=("all", "gemm", "quant", "quantcold", "quantfuse", "block",
-                                       "mlp", "c5", "c5mem", "copy", "scaled_mm"),
+    ap.add_argument("--part", choices=("all", "gemm", "quant", "quantcold", "quantfuse", "sweep",
+                                       "block", "mlp", "c5", "c5mem", "copy", "scaled_mm"),
                     default="all",
                     help="all (default) = headline + every secondary figure; the others run "
                          "one workload (for profiling)")
@@ -816,6 +861,7 @@ def main():
               "c5": lambda: bench_c5(), "c5mem": lambda: bench_c5_memory(),
               "quantcold": lambda: bench_dual_quant_cold(max(1, args.steps // 20)),
               "quantfuse": lambda: bench_quant_in_consumer(),
+              "sweep": lambda: bench_gemm_sweep(),
               "mlp": lambda: bench_mlp(
                   steps=args.steps,
                   arms=("tcfp", "tcfp_fused", "bf16", "fp32") if args.arm == "both"
