@@ -630,8 +630,9 @@ int tcfp_transpose_u8(const uint8_t* src, int64_t rows, int64_t cols, uint8_t* d
 
 /* GEMM tile selection for all later calls in the process: 0 automatic (the
  * 256 x 128 tile unless it would leave CUs idle; FP8 dual GEMMs with more
- * full tiles than CUs run one persistent workgroup per CU), 1 always
- * 256 x 128, 2 always 128 x 64, 3 128 x 64 with eight waves where the
+ * full tiles than CUs run one persistent workgroup per CU; block-scaled
+ * single GEMMs with at least as many full 256 x 256 tiles as CUs take that
+ * tile), 1 always 256 x 128, 2 always 128 x 64, 3 128 x 64 with eight waves where the
  * small-tile grid fits in one round (FP8 operands; bf16 ones keep four
  * waves), 4 256 x 128 with one workgroup per tile (no persistent launch).
  * Results do not depend on the policy. */

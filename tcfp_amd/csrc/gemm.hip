@@ -1088,9 +1088,16 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persist_kernel(GemmArgs g) {
   constexpr bool F32OUT = std::is_same<OutT, float>::value;
   static_assert(EPI == 0 || F32OUT, "GELU epilogues write fp32");
   static_assert(SCALE == 0 || (SCALE == 1 && EPI == 0), "block exponents: plain epilogue only");
-  static_assert(!SPL || (BNT == 64 && EPI == 0 && F32OUT), "single GEMM: 256 x 64 slots, fp32");
+  static_assert(!SPL || (EPI == 0 && F32OUT), "single GEMM: fp32, plain epilogue");
   constexpr int NACC = (SCALE == 1 && !SPL) ? 1 : 2;
   constexpr int NSL = SPL ? 2 : 1;  // output column blocks per tile
+  // ROLL (single GEMM, 256 x 128 slots: a 256 x 256 output tile): the two
+  // accumulator sets take 128 registers, so the weight fragments are not
+  // double-buffered: each is re-read for the next sub-step as soon as its
+  // MFMAs are issued (four weight and two activation fragments per wave in
+  // flight besides the current two activation fragments, 64 registers
+  // instead of 96).
+  constexpr bool ROLL = SPL && BNT == 128;
   constexpr int NW = 8, BM = 256, BN = BNT, NS = 2;
   // BN = 64 (EPI 2 only): the GELU derivative factors of the tile (256 x 64
   // fp32, 64 KiB) are brought into LDS beside the two 48 KiB operand stages
@@ -1102,6 +1109,7 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persist_kernel(GemmArgs g) {
   constexpr bool DGL = BNT == 64 && EPI == 2;
   static_assert(BNT == 128 || (BNT == 64 && EPI == 2 && SCALE == 0 && F32OUT) || SPL,
                 "the 256 x 64 tile serves the GELU backward epilogue and single GEMMs");
+  static_assert(!ROLL || SCALE == 1, "the rolling schedule serves block-scaled single GEMMs");
   constexpr int WM = NW / 2, TMW = BM / WM, MB = TMW / 32;
   constexpr int TNW = BN / 2, NB = TNW / 32, NF = 2 * NB;
   constexpr int SROWS = BM + 2 * BN;
@@ -1290,7 +1298,7 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persist_kernel(GemmArgs g) {
   // activation fragment i
   uint32_t raw[SCALE == 1 ? 2 * (NF + MB) : 1];
   uint32_t sc[SCALE == 1 ? 2 * (NF + MB) : 1];
-  auto load_raw = [&](const EOff& eo, int t) {
+  auto load_raw = [&](uint32_t* raw, const EOff& eo, int t) {
     if constexpr (SCALE == 1) {
       const int sw = int(uint32_t(t) * kbs * uint32_t(N)), sa = int(uint32_t(t) * kbs * uint32_t(M));
 #pragma unroll
@@ -1307,7 +1315,7 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persist_kernel(GemmArgs g) {
     }
   };
   // the loads have landed (a use here makes the compiler wait at this point)
-  auto hold_raw = [&]() {
+  auto hold_raw = [&](uint32_t* raw) {
     if constexpr (SCALE == 1) {
 #pragma unroll
       for (int f = 0; f < 2 * (NF + MB); ++f) asm volatile("" : "+v"(raw[f]));
@@ -1315,38 +1323,53 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persist_kernel(GemmArgs g) {
   };
   // E8M0 code of an int8 exponent byte u: (u ^ 128) - 1 saturated at 0 maps
   // e = -128 .. 127 to 0 (2^-127, the sentinel too), 0, 1, ..., 254
-  auto pack = [&]() {
+  auto pack = [&](const uint32_t* raw) {
     if constexpr (SCALE == 1) {
 #pragma unroll
       for (int f = 0; f < 2 * (NF + MB); ++f)
         sc[f] = __builtin_elementwise_sub_sat(raw[f] ^ 128u, 1u);
     }
   };
-  auto read_frags = [&](v8i* f, int b, int h) {
+  // fragment x of sub-step h from buffer b: weight fragment x (x < NF) or
+  // activation fragment x - NF
+  auto read_one = [&](v8i& f, int b, int h, int x) {
     const uint8_t* st = lds + b * STAGE;
+    const int rb = x < NF ? (BM + (x / NB) * BN + wn * TNW + (x % NB) * 32) * kRowB
+                          : (wm * TMW + (x - NF) * 32) * kRowB;
+    f = make_frag(lds_read16(st, rb + ro[h][0]), lds_read16(st, rb + ro[h][1]));
+  };
+  auto read_frags = [&](v8i* f, int b, int h) {
 #pragma unroll
-    for (int q = 0; q < NF; ++q) {
-      const int rb = (BM + (q / NB) * BN + wn * TNW + (q % NB) * 32) * kRowB;
-      f[q] = make_frag(lds_read16(st, rb + ro[h][0]), lds_read16(st, rb + ro[h][1]));
-    }
-#pragma unroll
-    for (int i = 0; i < MB; ++i) {
-      const int rb = (wm * TMW + i * 32) * kRowB;
-      f[NF + i] = make_frag(lds_read16(st, rb + ro[h][0]), lds_read16(st, rb + ro[h][1]));
-    }
+    for (int x = 0; x < NF + MB; ++x) read_one(f[x], b, h, x);
+  };
+  // weight fragment q times activation fragment i of sub-step h
+  auto mfma_one = [&](const v8i& fq, const v8i& fi, int h, int q, int i) {
+    v16f& c = acc[(q / NB) % NACC][q % NB][i];
+    if constexpr (SCALE == 1)
+      c = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+          fq, fi, c, BF, AF, 0, int(sc[2 * q + h]), 0, int(sc[2 * (NF + i) + h]));
+    else
+      c = mfma_plain<BF, AF>(fq, fi, c);
   };
   auto mfmas_range = [&](const v8i* f, int h, int lo, int hi) {
 #pragma unroll
     for (int idx = 0; idx < NP; ++idx) {
       if (idx < lo || idx >= hi) continue;
       const int i = idx / NF, q = idx % NF;
-      v16f& c = acc[(q / NB) % NACC][q % NB][i];
-      if constexpr (SCALE == 1)
-        c = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-            f[q], f[NF + i], c, BF, AF, 0, int(sc[2 * q + h]), 0, int(sc[2 * (NF + i) + h]));
-      else
-        c = mfma_plain<BF, AF>(f[q], f[NF + i], c);
+      mfma_one(f[q], f[NF + i], h, q, i);
     }
+  };
+  // ROLL: the MFMAs of weight fragment q with both activation fragments
+  // fa[NF .. NF + MB), then the fragment's register takes (weight
+  // fragment q of sub-step h_next from buffer b_next)
+  auto mfma_roll = [&](v8i* fw, const v8i* fa, int h, int q, int b_next, int h_next) {
+#pragma unroll
+    for (int i = 0; i < MB; ++i) mfma_one(fw[q], fa[NF + i], h, q, i);
+#pragma unroll
+    for (int i = 0; i < MB; ++i) asm volatile("" : "+v"(acc[(q / NB) % NACC][q % NB][i]));
+    __builtin_amdgcn_sched_barrier(0);
+    if (b_next >= 0) read_one(fw[q], b_next, h_next, q);
+    __builtin_amdgcn_sched_barrier(0);
   };
   // The MFMAs of (fragment, m-block) pairs [lo, hi) stay where they are:
   // an empty volatile asm that reads and writes their accumulators keeps
@@ -1395,14 +1418,14 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persist_kernel(GemmArgs g) {
   // prologue: stages 0 and 1 of the first tile (nt >= 2 for this kernel),
   // after stage 0's exponents (complete at the wait, which leaves only the
   // newest DI operations in flight)
-  load_raw(eo, 0);
+  load_raw(raw, eo, 0);
   issue(cur, 0, 0);
   issue(cur, 1, 1);
   __builtin_amdgcn_s_waitcnt((DI & 15) | (7 << 4) | ((DI >> 4) << 14));
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
-  hold_raw();
-  pack();
+  hold_raw(raw);
+  pack(raw);
   read_frags(f0, 0, 0);
 
   int cb0 = 0;  // buffer of the current tile's stage 0
@@ -1425,18 +1448,63 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persist_kernel(GemmArgs g) {
       // 0), waited for after this stage's barrier.  (One load site: loads
       // in two branches land in different registers, and the copy where
       // they merge would wait for them right here.  In a tile's first
-      // stage the wait also covers the previous tile's output stores.)
+      // stage the wait also covers the previous tile's output stores:
+      // issuing these loads in the previous tile's epilogue, before its
+      // stores, measured no faster for dual GEMMs and 3-9% slower for the
+      // 256 x 256 single GEMM.)
       if constexpr (SCALE == 1) {
         const bool last = t + 1 == nt;
         if (!last || more) {
           const EOff e = last ? eo_n : eo;
-          load_raw(e, last ? 0 : t + 1);
+          load_raw(raw, e, last ? 0 : t + 1);
         }
       }
       const bool bias_stage =
           kBiasLds && g.bias != nullptr && t == (nt > 2 ? nt - 2 : 0) && tid < NSL * BN;
       float bv = 0.0f;
       if (bias_stage) bv = g.bias[n0 + tid];
+      if constexpr (ROLL) {
+        // sub-step 1's activation fragments, then sub-step 0 weight fragment
+        // by weight fragment, each register re-read for sub-step 1 behind
+        // its MFMAs.  All of sub-step 1's MFMAs follow the barrier (PRE = 0;
+        // with one or two of its weight fragments before the barrier the
+        // 4096^3 single block-64 GEMM ran 66.5 / 68.5 us against 63.8 us).
+#pragma unroll
+        for (int i = 0; i < MB; ++i) read_one(f1[NF + i], b, 1, NF + i);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int q = 0; q < NF; ++q) mfma_roll(f0, f0, 0, q, b, 1);
+        constexpr int PRE = 0;  // sub-step 1 weight fragments before the barrier
+#pragma unroll
+        for (int q = 0; q < PRE; ++q) mfma_roll(f0, f1, 1, q, -1, 0);
+        if (t == 0 && it > 0)
+          sync_keep(std::integral_constant<int, NST>{}, false);
+        else
+          sync_keep(std::integral_constant<int, 0>{}, false);
+        hold_raw(raw);
+        if (bias_stage) bias_s[tid] = bv;
+        // the next weight fragment's MFMAs refill the pipes after the
+        // barrier, then the refill DMA and sub-step 0 of stage t + 1 (after
+        // the last stage: the next tile's stage 0, landed at this barrier;
+        // stale and unused after the last tile) into the free registers
+        mfma_roll(f0, f1, 1, PRE, -1, 0);
+        if (t + 2 < nt)
+          issue(cur, t + 2, b);
+        else if (t + 2 == nt && more)
+          issue(nxt, 0, b);
+        else if (more)
+          issue(nxt, 1, b);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < MB; ++i) read_one(f0[NF + i], b ^ 1, 0, NF + i);
+#pragma unroll
+        for (int q = 0; q <= PRE; ++q) read_one(f0[q], b ^ 1, 0, q);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int q = PRE + 1; q < NF; ++q) mfma_roll(f0, f1, 1, q, b ^ 1, 0);
+        pack(raw);
+        continue;
+      }
       read_frags(f1, b, 1);
       mfmas_range(f0, 0, 0, NP / 2);
       interleave_mfma_lds<NP / 2, 2 * (NF + MB), 0>();
@@ -1445,7 +1513,7 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persist_kernel(GemmArgs g) {
         sync_keep(std::integral_constant<int, NST>{}, t + 1 == nt);
       else
         sync_keep(std::integral_constant<int, 0>{}, t + 1 == nt);
-      hold_raw();
+      hold_raw(raw);
       if (bias_stage) bias_s[tid] = bv;
       mfmas_range(f0, 0, NP / 2, NP);
       pin_range(NP / 2, NP);
@@ -1465,13 +1533,14 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persist_kernel(GemmArgs g) {
       if (EPI != 2 || t + 1 < nt) read_frags(f0, b ^ 1, 0);
       mfmas_range(f1, 1, 0, NP);
       interleave_mfma_lds<NP, 2 * (NF + MB), 0>();
-      pack();  // the next stage's E8M0 codes (its sub-step 1 MFMAs are issued)
+      pack(raw);  // the next stage's E8M0 codes (its sub-step 1 MFMAs are issued)
     }
 
     const int sb = (cb0 + nt - 1) & 1;
     const int nb = n0 + wn * TNW;
     if constexpr (F32OUT) {
       // ---- epilogue: 16-byte stores from the accumulators --------------------
+      // (the next tile's stage 1 exponents first: the stores follow)
       if constexpr (EPI == 2) {
         // g = value * gelu'(h) factor.  Every factor load of the tile is
         // issued before any store: a wait for a load also waits for every
@@ -1722,7 +1791,8 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persist_kernel(GemmArgs g) {
 // the out-of-range sentinel must stay beyond every span).
 constexpr int64_t kMaxSpan = (int64_t(1) << 31) - (int64_t(1) << 20);
 
-// Tile policy: 0 = automatic, 1 = always 256 x 128, 2 = always 128 x 64,
+// Tile policy: 0 = automatic (block-scaled single GEMMs may take 256 x 256
+// tiles), 1 = always 256 x 128, 2 = always 128 x 64,
 // 3 = 128 x 64 with eight waves in the one-round deep-pipeline case,
 // 4 = 256 x 128 with one workgroup per tile (no persistent launch).
 int g_tile_policy = 0;
@@ -1762,13 +1832,24 @@ int launch_gemm(GemmArgs ga, hipStream_t st) {
   const int m = ga.M, n = ga.N, k = ga.K;
   if constexpr (SCALE == 1 && SPLIT && AF != kBF16 && std::is_same<OutT, float>::value) {
     // block-scaled single GEMM with more full 256 x 128 tiles than CUs: the
-    // persistent kernel with the two weight slots on adjacent 64-row blocks
-    // (32-bit exponent offsets)
+    // persistent kernel with the two weight slots on adjacent weight-row
+    // blocks (32-bit exponent offsets) -- 128-row slots (256 x 256 output
+    // tiles) when there are at least as many of those as CUs (automatic
+    // tile policy), else 64-row slots (256 x 128 output tiles)
     if (persist_eligible(ga) &&
         int64_t(k >> ga.bs_shift) * (m > n ? m : n) < int64_t(INT32_MAX)) {
       if (ga.bias != nullptr && (reinterpret_cast<uintptr_t>(ga.bias) & 15) != 0)
         return TCFP_ERR_ALIGN;
       GemmArgs gp = ga;
+      if (g_tile_policy == 0 && n % 256 == 0 && int64_t(m / 256) * (n / 256) >= num_cus()) {
+        gp.B1 = ga.B0 + 128 * ga.ldb;
+        gp.e_1 = ga.e_0 + 128;
+        gp.tiles_m = m / 256;
+        gp.tiles_n = n / 256;
+        gemm_nt_persist_kernel<AF, BF, float, 0, 1, 8, 128, true>
+            <<<unsigned(num_cus()), 512, 0, st>>>(gp);
+        return hipGetLastError() == hipSuccess ? TCFP_OK : TCFP_ERR_HIP;
+      }
       gp.B1 = ga.B0 + 64 * ga.ldb;
       gp.e_1 = ga.e_0 + 64;
       gp.tiles_m = m / 256;

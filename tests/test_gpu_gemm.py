@@ -297,6 +297,44 @@ def test_persistent_block_dual_gemm_matches_one_workgroup_per_tile(dev, bs, M, N
         assert og.rel_fro(npy(p), ref) < EXACT
 
 
+@pytest.mark.parametrize("bs", [32, 64, 128])
+@pytest.mark.parametrize("M,N,K_", [(4096, 4096, 256), (2048, 8192, 384), (4352, 4096, 256)])
+@pytest.mark.parametrize("afmt", [torch.float8_e4m3fn, torch.float8_e5m2])
+def test_single_block_gemm_256x256_tiles_match_256x128(dev, bs, M, N, K_, afmt):
+    """Block-scaled single GEMMs with at least as many full 256 x 256 tiles
+    as CUs run the persistent kernel on 128-row weight slots (two
+    accumulator sets, weight fragments re-read behind their MFMAs); the
+    256 x 128 tile policy runs 64-row slots.  Both issue the same MFMAs on
+    the same 32 x 32 output blocks in the same K order, so the results, bias
+    included, are identical bit for bit; one shape is also held to the
+    oracle."""
+    print(f"single block 256x256 bs={bs} M={M} N={N} K={K_} {afmt}", flush=True)
+    g = torch.Generator().manual_seed(40 + bs)
+    x = torch.randn(M, K_, generator=g)
+    x[: M // 7] *= 300.0
+    w = torch.randn(N, K_, generator=g) * 0.02
+    a, ea = K.block_quantize_fp8(x.to(dev), bs, afmt)
+    b, eb = K.block_quantize_fp8(w.to(dev), bs)
+    bias = torch.randn(N, generator=torch.Generator().manual_seed(41)).to(dev)
+    run = lambda: K._block_gemm(a, ea, b, None, eb, None, bs, bias, torch.float32)
+    names = _kernel_names(run)
+    assert any("gemm_nt_persist_kernel" in n and "8, 128, true>" in n for n in names), names
+    p = run()
+    try:
+        K.set_gemm_tile_policy("large")
+        names = _kernel_names(run)
+        assert any("gemm_nt_persist_kernel" in n and "6, 64, true>" in n for n in names), names
+        q = run()
+    finally:
+        K.set_gemm_tile_policy("auto")
+    assert torch.equal(p.view(torch.int32), q.view(torch.int32))
+    if (M, N, K_) == (4096, 4096, 256) and bs == 64:
+        fmt = ofp8.E4M3 if afmt == torch.float8_e4m3fn else ofp8.E5M2
+        ref = (og.block_deq64(u8(a), npy(ea), bs, fmt) @ og.block_deq64(u8(b), npy(eb), bs).T
+               + bias.cpu().double().numpy())
+        assert og.rel_fro(npy(p), ref) < EXACT
+
+
 # ------------------------------------------------- block-scaled (a10, a13)
 def make_block_operands(M, N, K_, bs, dev, seed, act_fp8=torch.float8_e4m3fn):
     g = torch.Generator().manual_seed(seed)
@@ -894,7 +932,8 @@ def test_c3_4096_cubed_single_block64_against_torch_fp32(dev):
     a, ea = K.block_quantize_fp8(x, bs)
     b, eb = K.block_quantize_fp8(w, bs)
     names = _kernel_names(lambda: K.block_scaled_gemm(a, b, ea, eb, bs))
-    assert any("gemm_nt_persist_kernel<0, 0, float, 0, 1, 6, 64, true>" in n for n in names), names
+    # (256 x 256 tiles, one per CU, on the 256-CU MI355X)
+    assert any("gemm_nt_persist_kernel<0, 0, float, 0, 1, 8, 128, true>" in n for n in names), names
     out = K.block_scaled_gemm(a, b, ea, eb, bs)
     ref = K.block_dequantize_fp8(a, ea, bs) @ K.block_dequantize_fp8(b, eb, bs).t()
     err = (torch.linalg.norm(out - ref) / torch.linalg.norm(ref)).item()

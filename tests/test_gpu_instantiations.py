@@ -43,15 +43,17 @@ PATHS = {
     "persist": ("auto", BIG, None),
     "small": ("auto", SMALL, "4, 128, 64, {S}, 2, "),  # block scales: two stages
     # block-scaled single GEMM, fp32 output: the persistent kernel with the
-    # two weight slots on adjacent 64-row blocks
+    # two weight slots on adjacent 64-row blocks, or 128-row blocks where
+    # there are at least as many 256 x 256 tiles as CUs
     "persist_spl": ("auto", BIG, None),
+    "persist_spl128": ("auto", (4096, 4096, 256), None),
 }
 # (scale kind, dual) -> the tile paths the dispatcher has for it
 SCALE_PATHS = {
     ("pt", True): ["deep", "small8", "small2", "large", "persist"],
     ("pt", False): ["deep", "small8", "small2", "large"],
     ("e8m0", True): ["small", "large", "persist"],
-    ("e8m0", False): ["small", "persist_spl"],
+    ("e8m0", False): ["small", "persist_spl", "persist_spl128"],
     ("f32s", True): ["small"],
     ("f32s", False): ["small"],
 }
@@ -61,7 +63,7 @@ def _cases():
     for (kind, dual), paths in SCALE_PATHS.items():
         for path in paths:
             for od in OUT:
-                if path == "persist_spl" and od != "f32":
+                if path.startswith("persist_spl") and od != "f32":
                     continue
                 for af in (0, 1):
                     for bf in (0, 1):
@@ -152,6 +154,8 @@ def test_gemm_instantiation_against_float64(dev, kind, bs, dual, path, od, af, b
     split = "false" if dual else "true"
     if path == "persist_spl":
         want = f"gemm_nt_persist_kernel<{af}, {bf}, float, 0, 1, 6, 64, true>"
+    elif path == "persist_spl128":
+        want = f"gemm_nt_persist_kernel<{af}, {bf}, float, 0, 1, 8, 128, true>"
     elif frag is None:
         want = f"gemm_nt_persist_kernel<{af}, {bf}, {out_name}, 0, {scale_id}, 8, 128, false>"
     else:
