@@ -632,10 +632,13 @@ int tcfp_transpose_u8(const uint8_t* src, int64_t rows, int64_t cols, uint8_t* d
  * 256 x 128 tile unless it would leave CUs idle; FP8 dual GEMMs with more
  * full tiles than CUs run one persistent workgroup per CU; block-scaled
  * single GEMMs with at least as many full 256 x 256 tiles as CUs take that
- * tile), 1 always 256 x 128, 2 always 128 x 64, 3 128 x 64 with eight waves where the
+ * tile; per-tensor dual GEMMs with bf16 output and K >= 8192 the persistent
+ * 256 x 128 tile with four waves, one per SIMD), 1 always 256 x 128, 2 always
+ * 128 x 64, 3 128 x 64 with eight waves where the
  * small-tile grid fits in one round (FP8 operands; bf16 ones keep four
- * waves), 4 256 x 128 with one workgroup per tile (no persistent launch).
- * Results do not depend on the policy. */
+ * waves), 4 256 x 128 with one workgroup per tile (no persistent launch),
+ * 5 the four-wave persistent 256 x 128 tile for per-tensor dual GEMMs with
+ * bf16 output (the others as 0).  Results do not depend on the policy. */
 int tcfp_gemm_set_tile_policy(int policy);
 
 /* ---- self-test hooks (no reference counterpart) ------------------------ */

@@ -1084,7 +1084,8 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && NS == 2 && BM <= 128 ? 2 : 1))
 // 256 x 64 slots' do.
 template <int AF, int BF, typename OutT, int EPI = 0, int SCALE = 0, int ND = 8, int BNT = 128,
           bool SPL = false>
-__global__ __launch_bounds__(512, 1) void gemm_nt_persist_kernel(GemmArgs g) {
+__global__ __launch_bounds__(BNT == 128 && ND == 4 ? 256 : 512, 1) void gemm_nt_persist_kernel(
+    GemmArgs g) {
   constexpr bool F32OUT = std::is_same<OutT, float>::value;
   static_assert(EPI == 0 || F32OUT, "GELU epilogues write fp32");
   static_assert(SCALE == 0 || (SCALE == 1 && EPI == 0), "block exponents: plain epilogue only");
@@ -1098,7 +1099,10 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persist_kernel(GemmArgs g) {
   // flight besides the current two activation fragments, 64 registers
   // instead of 96).
   constexpr bool ROLL = SPL && BNT == 128;
-  constexpr int NW = 8, BM = 256, BN = BNT, NS = 2;
+  // W4 (ND = 4 with 256 x 128 slots): four waves, one per SIMD, each
+  // owning 128 activation rows x 64 weight rows of both slots
+  constexpr bool W4 = BNT == 128 && ND == 4;
+  constexpr int NW = W4 ? 4 : 8, BM = 256, BN = BNT, NS = 2;
   // BN = 64 (EPI 2 only): the GELU derivative factors of the tile (256 x 64
   // fp32, 64 KiB) are brought into LDS beside the two 48 KiB operand stages
   // in pieces during the tile's K stages, so the epilogue reads them from
@@ -1121,10 +1125,16 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persist_kernel(GemmArgs g) {
   // letting the other four waves' output stores drain past the barriers,
   // gained <= 1 us on standalone 8192 x 4096 x 1024 GEMMs but cost 7 us per
   // step of the fused MLP training step, measured in one process.)
-  static_assert(BNT == 128 ? ND == 8 : ND == 6, "DMA waves: all eight; six for the 256 x 64 tile");
+  static_assert(BNT == 128 ? (ND == 8 || ND == 4) : ND == 6,
+                "DMA waves: all of them; six for the 256 x 64 tile");
+  static_assert(!W4 || (SCALE == 0 && EPI == 0 && !SPL && !F32OUT),
+                "the four-wave tile serves per-tensor dual GEMMs with bf16 output");
   constexpr int RPW = SROWS / ND;
   constexpr int DI = RPW / 8;
   constexpr int NP = NF * MB;
+  // (W4: two DMA instructions behind each of half a sub-step's MFMAs, one
+  // fragment read behind each of the other half's)
+  static_assert(!W4 || (DI == NP && NF + MB == NP / 2), "four-wave stage layout");
   constexpr int RB = TNW * 2;      // bytes of one staged bf16 tile row
   constexpr int CPR = RB / 16;     // 16-byte chunks per row
   constexpr int RPI = 64 / CPR;    // rows per store instruction
@@ -1150,7 +1160,10 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persist_kernel(GemmArgs g) {
   // exponents), then the derivative factors (DGL)
   constexpr int kBiasB = kBiasLds ? NSL * BN * 4 : 0;
   constexpr int kDgB = DGL ? BM * BN * 4 : 0;
-  __shared__ __align__(16) uint8_t lds[NS * STAGE + kBiasB + kDgB];
+  // W4: 1 KiB that the refill DMA of a stage with nothing to load writes
+  // (zeros from an out-of-range offset), so that its issue needs no branch
+  constexpr int kDumB = W4 ? 1024 : 0;
+  __shared__ __align__(16) uint8_t lds[NS * STAGE + kBiasB + kDgB + kDumB];
   float* const bias_s = reinterpret_cast<float*>(lds + NS * STAGE);
   const float* const dgl = reinterpret_cast<const float*>(lds + NS * STAGE + kBiasB);
   // GELU epilogues: EPI 1 the lane's int / uint maxima of the h bits (the
@@ -1170,7 +1183,7 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persist_kernel(GemmArgs g) {
   const int lr = lane & 31, lg = lane >> 5;
 
   // this wave's DMA rows: activation (region 0), slot 0 (1) or slot 1 (2)
-  const bool dma_wave = wave < ND;
+  const bool dma_wave = W4 || wave < ND;
   const int srow0 = (dma_wave ? wave : 0) * RPW;
   const int region = srow0 < BM ? 0 : (srow0 < BM + BN ? 1 : 2);
   const int row_base = region == 0 ? srow0 : (region == 1 ? srow0 - BM : srow0 - BM - BN);
@@ -1214,9 +1227,14 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persist_kernel(GemmArgs g) {
     if (!dma_wave) return;
     const uint32_t dst = lds_base + uint32_t(b) * STAGE;
     const uint32_t soff = uint32_t(t) * kSK;
+    // (W4: the lane offsets laundered here too -- precomputed, its sixteen
+    // instruction offsets were spilled, and each reload waited for every
+    // DMA before it)
+    uint32_t vb0 = voff0, vb1 = voff1;
+    if constexpr (W4) asm volatile("" : "+v"(vb0), "+v"(vb1));
 #pragma unroll
     for (int i = 0; i < DI; ++i)
-      dma16(rs, ((i & 1) ? voff1 : voff0) + uint32_t(i) * row8, soff, dst + i * 1024);
+      dma16(rs, ((i & 1) ? vb1 : vb0) + uint32_t(i) * row8, soff, dst + i * 1024);
   };
   // DGL: the current tile's derivative factors into LDS.  Piece p (1 KiB:
   // tile rows 4p .. 4p + 3, 16 lanes per row) lands at dgl + p KiB with
@@ -1463,6 +1481,92 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persist_kernel(GemmArgs g) {
           kBiasLds && g.bias != nullptr && t == (nt > 2 ? nt - 2 : 0) && tid < NSL * BN;
       float bv = 0.0f;
       if (bias_stage) bv = g.bias[n0 + tid];
+      if constexpr (W4) {
+        // One wave per SIMD: nothing else hides a stall, so the stage is
+        // one fixed sequence.  Sub-step 0's first half with the fragments
+        // of sub-step 1 read behind its MFMAs (RDP per MFMA); the barrier;
+        // the refill DMA behind the next MFMAs (DMP instructions per MFMA),
+        // the fragments of sub-step 0 of stage t + 1 behind the MFMAs after
+        // it (one per MFMA; after the last stage: the next tile's stage 0,
+        // stale after the last tile).  A stage with nothing to load (the
+        // last: its buffer stages the output) still issues the refill
+        // instructions, re-reading stage 0 of the tile into a dummy KiB, so
+        // that the issue needs no branch.
+        constexpr int RDP = 2, DMP = 1;
+        // The refill's parameters -- the next tile's stage 0 when t + 2 ==
+        // nt (nxt == cur when there is none: the dummy then re-reads the
+        // current tile's stage 0) -- are formed behind the first MFMA whose
+        // slot carries no reads: formed at the top of the stage, their ~30
+        // scalar instructions delayed its first MFMA.  (The lane offsets
+        // are laundered per stage, so that the sixteen instruction offsets
+        // are formed one add each instead of being kept in sixteen
+        // registers across the kernel.)
+        v4i drs;
+        uint32_t dsoff = 0, dbase = 0, dstep = 0, vb0 = 0, vb1 = 0;
+        auto dma_params = [&]() {
+          const bool in_tile = t + 2 < nt;
+          const bool live = t + 2 < nt + int(more);
+          drs = in_tile ? cur : nxt;
+          dsoff = in_tile ? uint32_t(t + 2) * kSK : 0u;
+          dbase = live ? lds_base + uint32_t(b) * STAGE : lds0 + uint32_t(NS * STAGE);
+          dstep = live ? 1024u : 0u;
+          vb0 = voff0;
+          vb1 = voff1;
+          asm volatile("" : "+v"(vb0), "+v"(vb1));
+        };
+        constexpr int JP = (NF + MB + RDP - 1) / RDP;  // the first pre-barrier slot without reads
+        static_assert(JP < NP / 2, "a pre-barrier slot for the refill parameters");
+        // after pre-barrier MFMA j: sub-step 1 fragments j * RDP .. + RDP
+        auto pre_op = [&](int j) {
+          __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+          for (int u = 0; u < RDP; ++u)
+            if (j * RDP + u < NF + MB) read_one(f1[j * RDP + u], b, 1, j * RDP + u);
+          if (j == JP) dma_params();
+          __builtin_amdgcn_sched_barrier(0);
+        };
+        // after post-barrier MFMA j: refill instructions j * DMP .. + DMP,
+        // then (j >= DI / DMP) fragment j - DI / DMP of stage t + 1
+        auto post_op = [&](int j) {
+          __builtin_amdgcn_sched_barrier(0);
+          if (j < DI / DMP) {
+#pragma unroll
+            for (int u = 0; u < DMP; ++u) {
+              const int i = j * DMP + u;
+              dma16(drs, ((i & 1) ? vb1 : vb0) + uint32_t(i) * row8, dsoff,
+                    dbase + uint32_t(i) * dstep);
+            }
+          } else if (j - DI / DMP < NF + MB) {
+            read_one(f0[j - DI / DMP], b ^ 1, 0, j - DI / DMP);
+          }
+          __builtin_amdgcn_sched_barrier(0);
+        };
+        static_assert(NF + MB <= RDP * (NP / 2), "sub-step 1's fragments within sub-step 0's first half");
+        static_assert(DI / DMP + NF + MB <= NP + NP / 2, "refill and reads within the stage");
+#pragma unroll
+        for (int idx = 0; idx < NP / 2; ++idx) {
+          mfma_one(f0[idx % NF], f0[NF + idx / NF], 0, idx % NF, idx / NF);
+          pre_op(idx);
+        }
+#pragma unroll
+        for (int idx = 0; idx < NP / 2; ++idx)
+          asm volatile("" : "+a"(acc[(idx % NF / NB) % NACC][idx % NF % NB][idx / NF]));
+        if (t == 0 && it > 0)
+          sync_keep(std::integral_constant<int, NST>{}, false);
+        else
+          sync_keep(std::integral_constant<int, 0>{}, false);
+#pragma unroll
+        for (int idx = NP / 2; idx < NP; ++idx) {
+          mfma_one(f0[idx % NF], f0[NF + idx / NF], 0, idx % NF, idx / NF);
+          post_op(idx - NP / 2);
+        }
+#pragma unroll
+        for (int idx = 0; idx < NP; ++idx) {
+          mfma_one(f1[idx % NF], f1[NF + idx / NF], 1, idx % NF, idx / NF);
+          post_op(NP / 2 + idx);
+        }
+        continue;
+      }
       if constexpr (ROLL) {
         // sub-step 1's activation fragments, then sub-step 0 weight fragment
         // by weight fragment, each register re-read for sub-step 1 behind
@@ -1723,13 +1827,18 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persist_kernel(GemmArgs g) {
     asm volatile("" ::: "memory");
     // the NST staged chunks of this lane, held in named registers (an array
     // here is kept in scratch memory across the barrier below)
-    static_assert(F32OUT || NST == 8, "eight store chunks per lane");
+    static_assert(F32OUT || NST == 8 || NST == 16, "eight or sixteen store chunks per lane");
     auto staged = [&](int s) {
       const int row = s * RPI + lane_e / CPR, cl = lane_e % CPR;
       return *reinterpret_cast<const uint4*>(eps + row * RB + ((cl ^ (row & (CPR - 1))) * 16));
     };
     const uint4 d0 = staged(0), d1 = staged(1), d2 = staged(2), d3 = staged(3);
     const uint4 d4 = staged(4), d5 = staged(5), d6 = staged(6), d7 = staged(7);
+    uint4 d8{}, d9{}, d10{}, d11{}, d12{}, d13{}, d14{}, d15{};
+    if constexpr (NST == 16) {
+      d8 = staged(8), d9 = staged(9), d10 = staged(10), d11 = staged(11);
+      d12 = staged(12), d13 = staged(13), d14 = staged(14), d15 = staged(15);
+    }
     if (more) {
       // every wave holds its staged output: the buffer takes the next tile's stage 1
       __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0), vmcnt and expcnt untouched
@@ -1745,6 +1854,10 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persist_kernel(GemmArgs g) {
     };
     put(0, d0); put(1, d1); put(2, d2); put(3, d3);
     put(4, d4); put(5, d5); put(6, d6); put(7, d7);
+    if constexpr (NST == 16) {
+      put(8, d8); put(9, d9); put(10, d10); put(11, d11);
+      put(12, d12); put(13, d13); put(14, d14); put(15, d15);
+    }
     __builtin_amdgcn_sched_barrier(0);
     zero_acc();
     cb0 = sb ^ 1;  // the next tile's stage 0 sits in the other buffer
@@ -1792,9 +1905,11 @@ __global__ __launch_bounds__(512, 1) void gemm_nt_persist_kernel(GemmArgs g) {
 constexpr int64_t kMaxSpan = (int64_t(1) << 31) - (int64_t(1) << 20);
 
 // Tile policy: 0 = automatic (block-scaled single GEMMs may take 256 x 256
-// tiles), 1 = always 256 x 128, 2 = always 128 x 64,
+// tiles; per-tensor dual GEMMs with bf16 output and K >= 8192 the
+// four-wave persistent tile), 1 = always 256 x 128, 2 = always 128 x 64,
 // 3 = 128 x 64 with eight waves in the one-round deep-pipeline case,
-// 4 = 256 x 128 with one workgroup per tile (no persistent launch).
+// 4 = 256 x 128 with one workgroup per tile (no persistent launch),
+// 5 = the four-wave persistent 256 x 128 tile (per-tensor dual, bf16 out).
 int g_tile_policy = 0;
 
 int num_cus() {
@@ -1818,7 +1933,7 @@ bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 // descriptors' reach (tile policies 0 and 1 only).  fp8 dual GEMMs with
 // per-tensor scales or block exponents, fp32 or bf16 output.
 bool persist_eligible(const GemmArgs& ga) {
-  if (g_tile_policy != 0 && g_tile_policy != 1) return false;
+  if (g_tile_policy != 0 && g_tile_policy != 1 && g_tile_policy != 5) return false;
   if (ga.M % 256 != 0 || ga.N % 128 != 0 || ga.K % kSK != 0 || ga.K <= kSK) return false;
   if (ga.kc > 0 && ga.kc < ga.K) return false;
   if (ga.ldo % 8 != 0 || !al16(ga.out)) return false;
@@ -1910,8 +2025,20 @@ int launch_gemm(GemmArgs ga, hipStream_t st) {
         persist = persist_eligible(ga) &&
                   (SCALE == 0 || int64_t(ga.K >> ga.bs_shift) * (ga.M > ga.N ? ga.M : ga.N) <
                                      int64_t(INT32_MAX));
-        if (persist)
+        if (persist) {
+          if constexpr (SCALE == 0 && std::is_same<OutT, uint16_t>::value) {
+            // the four-wave tile (one wave per SIMD, 128 x 64 x 2 per wave):
+            // a K loop ~5% shorter in shader cycles at a ~2% lower clock
+            // (power cap) and a longer per-tile epilogue, so it is taken
+            // where the K loop dominates (measured: 4096^2 x 8192 185.7 vs
+            // 187.8 us, x 16384 352.8 vs 370.3 us; 4096^3 level)
+            if (g_tile_policy == 5 || (g_tile_policy == 0 && ga.K >= 8192)) {
+              gemm_nt_persist_kernel<AF, BF, OutT, 0, 0, 4><<<unsigned(num_cus()), 256, 0, st>>>(ga);
+              return hipGetLastError() == hipSuccess ? TCFP_OK : TCFP_ERR_HIP;
+            }
+          }
           gemm_nt_persist_kernel<AF, BF, OutT, 0, SCALE><<<unsigned(num_cus()), 512, 0, st>>>(ga);
+        }
       }
       if (!persist)
         gemm_nt_dma_kernel<AF, BF, SPLIT, OutT, 8, 256, 128, SCALE, 2><<<grid, 512, 0, st>>>(ga);
@@ -2250,7 +2377,7 @@ extern "C" int tcfp_wtquant_block_dual_gemm(const uint8_t* a, int a_fmt, int64_t
 }
 
 extern "C" int tcfp_gemm_set_tile_policy(int policy) {
-  if (policy < 0 || policy > 4) return TCFP_ERR_SHAPE;
+  if (policy < 0 || policy > 5) return TCFP_ERR_SHAPE;
   g_tile_policy = policy;
   return TCFP_OK;
 }

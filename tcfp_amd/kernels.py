@@ -1540,8 +1540,11 @@ def set_gemm_tile_policy(policy: str) -> None:
     ``"small"`` (128 x 64 tiles, two workgroups per CU), ``"small8"``
     (128 x 64 with eight waves where the grid fits one round) or
     ``"large_nonpersistent"`` (256 x 128 with one workgroup per tile, never
-    the persistent launch).  Results do not depend on the policy."""
-    code = {"auto": 0, "large": 1, "small": 2, "small8": 3, "large_nonpersistent": 4}[policy]
+    the persistent launch) or ``"large4"`` (the persistent 256 x 128 tile
+    with four waves, one per SIMD, for per-tensor dual GEMMs with bf16
+    output).  Results do not depend on the policy."""
+    code = {"auto": 0, "large": 1, "small": 2, "small8": 3, "large_nonpersistent": 4,
+            "large4": 5}[policy]
     check(_hip.lib().tcfp_gemm_set_tile_policy(code), "set_gemm_tile_policy")
 
 

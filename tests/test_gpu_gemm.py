@@ -297,6 +297,38 @@ def test_persistent_block_dual_gemm_matches_one_workgroup_per_tile(dev, bs, M, N
         assert og.rel_fro(npy(p), ref) < EXACT
 
 
+@pytest.mark.parametrize("M,N,K_", [(2048, 4608, 256), (4352, 2048, 384), (4096, 4096, 1024),
+                                     (2048, 4608, 8192)])
+@pytest.mark.parametrize("afmt", [torch.float8_e4m3fn, torch.float8_e5m2])
+def test_four_wave_tile_matches_eight_wave(dev, M, N, K_, afmt):
+    """Per-tensor dual GEMMs with bf16 output on the persistent 256 x 128
+    tile with four waves (one per SIMD, 128 activation rows x 64 weight
+    rows of both slots per wave; policy "large4", and the automatic choice
+    at K >= 8192) against the eight-wave kernel (policy "large"): the same
+    MFMAs on the same 32 x 32 blocks in the same K order, so the outputs,
+    bias included, are identical bit for bit."""
+    print(f"four-wave M={M} N={N} K={K_} {afmt}", flush=True)
+    a, sa = make_act((M, K_), 50, dev, afmt)
+    h, l, ih, il = make_pair((N, K_), 51, dev)
+    bias = torch.randn(N, generator=torch.Generator().manual_seed(52)).to(dev)
+    run = lambda: K.fused_dual_gemm_forward(a, h, l, sa, ih, il, bias=bias,
+                                            out_dtype=torch.bfloat16)
+    w4 = "0, 0, 4, 128, false>"
+    try:
+        K.set_gemm_tile_policy("large4")
+        assert any("gemm_nt_persist_kernel" in n and w4 in n for n in _kernel_names(run))
+        p = run()
+        K.set_gemm_tile_policy("large")
+        names = _kernel_names(run)
+        assert any("gemm_nt_persist_kernel" in n and "0, 0, 8, 128, false>" in n for n in names)
+        q = run()
+    finally:
+        K.set_gemm_tile_policy("auto")
+    assert torch.equal(p.view(torch.int16), q.view(torch.int16))
+    auto_w4 = any("gemm_nt_persist_kernel" in n and w4 in n for n in _kernel_names(run))
+    assert auto_w4 == (K_ >= 8192)
+
+
 @pytest.mark.parametrize("bs", [32, 64, 128])
 @pytest.mark.parametrize("M,N,K_", [(4096, 4096, 256), (2048, 8192, 384), (4352, 4096, 256)])
 @pytest.mark.parametrize("afmt", [torch.float8_e4m3fn, torch.float8_e5m2])

@@ -47,10 +47,12 @@ PATHS = {
     # there are at least as many 256 x 256 tiles as CUs
     "persist_spl": ("auto", BIG, None),
     "persist_spl128": ("auto", (4096, 4096, 256), None),
+    # per-tensor dual, bf16 output: the persistent tile with four waves
+    "persist4": ("large4", BIG, None),
 }
 # (scale kind, dual) -> the tile paths the dispatcher has for it
 SCALE_PATHS = {
-    ("pt", True): ["deep", "small8", "small2", "large", "persist"],
+    ("pt", True): ["deep", "small8", "small2", "large", "persist", "persist4"],
     ("pt", False): ["deep", "small8", "small2", "large"],
     ("e8m0", True): ["small", "large", "persist"],
     ("e8m0", False): ["small", "persist_spl", "persist_spl128"],
@@ -64,6 +66,8 @@ def _cases():
         for path in paths:
             for od in OUT:
                 if path.startswith("persist_spl") and od != "f32":
+                    continue
+                if path == "persist4" and od != "bf16":
                     continue
                 for af in (0, 1):
                     for bf in (0, 1):
@@ -154,6 +158,8 @@ def test_gemm_instantiation_against_float64(dev, kind, bs, dual, path, od, af, b
     split = "false" if dual else "true"
     if path == "persist_spl":
         want = f"gemm_nt_persist_kernel<{af}, {bf}, float, 0, 1, 6, 64, true>"
+    elif path == "persist4":
+        want = f"gemm_nt_persist_kernel<{af}, {bf}, unsigned short, 0, 0, 4, 128, false>"
     elif path == "persist_spl128":
         want = f"gemm_nt_persist_kernel<{af}, {bf}, float, 0, 1, 8, 128, true>"
     elif frag is None:
