@@ -1508,7 +1508,7 @@ __global__ __launch_bounds__(BNT == 128 && ND == 4 ? 256 : 512, 1) void gemm_nt_
           const bool live = t + 2 < nt + int(more);
           drs = in_tile ? cur : nxt;
           dsoff = in_tile ? uint32_t(t + 2) * kSK : 0u;
-          dbase = live ? lds_base + uint32_t(b) * STAGE : lds0 + uint32_t(NS * STAGE);
+          dbase = live ? lds_base + uint32_t(b) * STAGE : lds0 + uint32_t(NS * STAGE + kBiasB + kDgB);
           dstep = live ? 1024u : 0u;
           vb0 = voff0;
           vb1 = voff1;
