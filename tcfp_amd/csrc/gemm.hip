@@ -1142,7 +1142,7 @@ __global__ __launch_bounds__(BNT == 128 && ND == 4 ? 256 : 512, 1) void gemm_nt_
   constexpr int NST = F32OUT ? NSL * MB * NB * 4 : TMW / RPI;
   static_assert(F32OUT || NW * TMW * RB <= STAGE, "epilogue staging must fit one operand buffer");
   // (a DMA wave holds at most two stages' DMA and one tile's stores in flight)
-  static_assert(NST + 2 * DI <= 63, "vmcnt immediate");
+  static_assert(NST + 2 * (DI + (SCALE == 1 ? 1 : 0)) <= 63, "vmcnt immediate");
   // EPI 2's column partials: a wave's rows are one 64-row group, its two
   // m-blocks the group's halves
   static_assert(EPI != 2 || (TMW == kColGroup && MB == 2), "wave rows vs. column groups");
@@ -1163,7 +1163,13 @@ __global__ __launch_bounds__(BNT == 128 && ND == 4 ? 256 : 512, 1) void gemm_nt_
   // W4: 1 KiB that the refill DMA of a stage with nothing to load writes
   // (zeros from an out-of-range offset), so that its issue needs no branch
   constexpr int kDumB = W4 ? 1024 : 0;
-  __shared__ __align__(16) uint8_t lds[NS * STAGE + kBiasB + kDgB + kDumB];
+  // SCALE 1: the block exponents of a stage, [K block of the stage][stage
+  // row] (activation rows, then the two weight slots' rows), one area per
+  // operand buffer, DMA'd with the stage (two 1 KiB instructions of
+  // per-lane 16-byte chunks: up to four K blocks at bs 32).
+  constexpr int kExpStage = SCALE == 1 ? 2048 : 0;
+  static_assert(SCALE != 1 || 4 * SROWS <= kExpStage, "a stage's exponents fit their area");
+  __shared__ __align__(16) uint8_t lds[NS * STAGE + kBiasB + kDgB + kDumB + 2 * kExpStage];
   float* const bias_s = reinterpret_cast<float*>(lds + NS * STAGE);
   const float* const dgl = reinterpret_cast<const float*>(lds + NS * STAGE + kBiasB);
   // GELU epilogues: EPI 1 the lane's int / uint maxima of the h bits (the
@@ -1290,58 +1296,66 @@ __global__ __launch_bounds__(BNT == 128 && ND == 4 ? 256 : 512, 1) void gemm_nt_
     else return acc[0][j][i][r] * c0 + acc[NACC - 1][j][i][r] * c1;
   };
 
-  // ---- block exponents (SCALE 1).  Weight fragment q reads row
-  // n0 + wn * TNW + 32 * (q % NB) + lr of e_0 (q < NB, W_hi) or e_1 (W_lo),
-  // activation fragment i row m0 + wm * TMW + 32 * i + lr of e_a; sub-step
-  // h of stage t covers K block t * (kSK >> bs) + ((64 h + 32 lg) >> bs) for
-  // this lane's 32-column half lg.
+  // ---- block exponents (SCALE 1).  Weight fragment q takes the exponent of
+  // weight row n0 + wn * TNW + 32 * (q % NB) + lr of e_0 (slot 0) or e_1
+  // (slot 1), activation fragment i that of row m0 + wm * TMW + 32 * i + lr
+  // of e_a; sub-step h of stage t covers K block t * (kSK >> bs) +
+  // ((64 h + 32 lg) >> bs) for this lane's 32-column half lg.
   const int bsh = SCALE == 1 ? g.bs_shift : 0;
   const uint32_t kbs = uint32_t(kSK >> bsh);  // K blocks per stage
-  const uint32_t kbl0 = uint32_t((32 * lg) >> bsh), kbl1 = uint32_t((64 + 32 * lg) >> bsh);
-  const uint32_t nkb = SCALE == 1 ? uint32_t(K >> bsh) : 0u;
-  const __amdgpu_buffer_rsrc_t er0 = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<int8_t*>(g.e_0), 0, int(nkb * uint32_t(N)), 0x00020000);
-  const __amdgpu_buffer_rsrc_t er1 = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<int8_t*>(g.e_1), 0, int(nkb * uint32_t(N)), 0x00020000);
-  const __amdgpu_buffer_rsrc_t era = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<int8_t*>(g.e_a), 0, int(nkb * uint32_t(M)), 0x00020000);
-  // lane offsets of a tile's sub-step 0 / 1 exponents: weight, activation
-  struct EOff { uint32_t w0, w1, a0, a1; };
-  auto eoff_of = [&](int m0, int n0) {
-    const uint32_t rw = uint32_t(n0 + wn * TNW + lr), ra = uint32_t(m0 + wm * TMW + lr);
-    return EOff{kbl0 * uint32_t(N) + rw, kbl1 * uint32_t(N) + rw, kbl0 * uint32_t(M) + ra,
-                kbl1 * uint32_t(M) + ra};
-  };
-  // raw bytes of stage t: [2 q + h] weight fragment q, [2 (NF + i) + h]
-  // activation fragment i
-  uint32_t raw[SCALE == 1 ? 2 * (NF + MB) : 1];
-  uint32_t sc[SCALE == 1 ? 2 * (NF + MB) : 1];
-  auto load_raw = [&](uint32_t* raw, const EOff& eo, int t) {
+  // The exponent DMA: waves 0 and 1 each move 64 chunks of 16 bytes, chunk
+  // c = 64 * wave + lane holding K block c / (SROWS / 16) of stage rows
+  // 16 * (c % (SROWS / 16)) .. + 15; chunks past the stage's K blocks
+  // re-read chunk 0 into the unused rest of the area.  Issued with the
+  // stage's operand DMA, so they land two stages ahead as the operands do
+  // (loaded per lane at the top of the stage before, the exponents' wait at
+  // the barrier was exposed: the whole exponent handling measured 7-8% of
+  // the block GEMM's time).
+  constexpr int kCpk = SROWS / 16;
+  const int ec = (wave & 1) * 64 + lane;  // (the issuing pair rotates with the stage)
+  const bool ein = SCALE == 1 && uint32_t(ec / kCpk) < kbs;
+  const int ekb = ein ? ec / kCpk : 0, er0 = ein ? (ec % kCpk) * 16 : 0;
+  const int ereg = er0 < BM ? 0 : (er0 < BM + BN ? 1 : 2);
+  const int erow = ereg == 0 ? er0 : (ereg == 1 ? er0 - BM : er0 - BM - BN);
+  const int8_t* const ebase = ereg == 0 ? g.e_a : (ereg == 1 ? g.e_0 : g.e_1);
+  const int64_t eld = ereg == 0 ? M : N;
+  const uint32_t exp_lds0 = lds0 + uint32_t(NS * STAGE + kBiasB + kDgB + kDumB);
+  auto issue_e = [&](int mt, int ntl, int t, int b) {
     if constexpr (SCALE == 1) {
-      const int sw = int(uint32_t(t) * kbs * uint32_t(N)), sa = int(uint32_t(t) * kbs * uint32_t(M));
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const uint32_t ow = h ? eo.w1 : eo.w0, oa = h ? eo.a1 : eo.a0;
-#pragma unroll
-        for (int q = 0; q < NF; ++q)
-          raw[2 * q + h] = __builtin_amdgcn_raw_buffer_load_b8(q < NB ? er0 : er1,
-                                                               int(ow + 32u * (q % NB)), sw, 0);
-#pragma unroll
-        for (int i = 0; i < MB; ++i)
-          raw[2 * (NF + i) + h] = __builtin_amdgcn_raw_buffer_load_b8(era, int(oa + 32u * i), sa, 0);
+      // waves 2 (t % (ND / 2)) and 2 (t % (ND / 2)) + 1 (all of them DMA waves)
+      if ((wave >> 1) == t % (ND / 2)) {
+        const int8_t* src =
+            ebase + (int64_t(t) * kbs + ekb) * eld + (ereg == 0 ? mt : ntl) + erow;
+        gdma16(src, exp_lds0 + uint32_t(b) * kExpStage + uint32_t(wave & 1) * 1024u);
       }
     }
   };
-  // the loads have landed (a use here makes the compiler wait at this point)
-  auto hold_raw = [&](uint32_t* raw) {
+  uint32_t sc[SCALE == 1 ? 2 * (NF + MB) : 1];
+  // The exponents of weight fragment q / activation fragment i of sub-step
+  // h are bytes [K block (64 h + 32 lg) >> bs][row] of the stage's area;
+  // their E8M0 codes go to sc[2 q + h] / sc[2 (NF + i) + h].  An int8
+  // exponent byte u becomes (u ^ 128) - 1 saturated at 0: e = -128 .. 127
+  // map to 0 (2^-127, the sentinel too), 0, 1, ..., 254.
+  // raw exponent bytes of the stage whose exponents sit in area b, read
+  // right after the barrier that makes them valid (an LDS round trip at the
+  // end of the stage delayed the next stage's first MFMAs), and their E8M0
+  // codes formed at the end of the stage
+  uint32_t raw[SCALE == 1 ? 2 * (NF + MB) : 1];
+  auto read_exps = [&](int b) {
     if constexpr (SCALE == 1) {
+      const uint8_t* ea = lds + NS * STAGE + kBiasB + kDgB + kDumB + b * kExpStage;
 #pragma unroll
-      for (int f = 0; f < 2 * (NF + MB); ++f) asm volatile("" : "+v"(raw[f]));
+      for (int h = 0; h < 2; ++h) {
+        const int kb = (64 * h + 32 * lg) >> bsh;
+#pragma unroll
+        for (int q = 0; q < NF; ++q)
+          raw[2 * q + h] = ea[kb * SROWS + BM + (q / NB) * BN + wn * TNW + (q % NB) * 32 + lr];
+#pragma unroll
+        for (int i = 0; i < MB; ++i) raw[2 * (NF + i) + h] = ea[kb * SROWS + wm * TMW + i * 32 + lr];
+      }
     }
   };
-  // E8M0 code of an int8 exponent byte u: (u ^ 128) - 1 saturated at 0 maps
-  // e = -128 .. 127 to 0 (2^-127, the sentinel too), 0, 1, ..., 254
-  auto pack = [&](const uint32_t* raw) {
+  auto pack = [&]() {
     if constexpr (SCALE == 1) {
 #pragma unroll
       for (int f = 0; f < 2 * (NF + MB); ++f)
@@ -1430,20 +1444,20 @@ __global__ __launch_bounds__(BNT == 128 && ND == 4 ? 256 : 512, 1) void gemm_nt_
   int m0, n0;
   tile_of(0, m0, n0);
   v4i cur = src_of(m0, n0);
-  EOff eo = eoff_of(m0, n0);
   v8i f0[NF + MB], f1[NF + MB];
   zero_acc();
   // prologue: stages 0 and 1 of the first tile (nt >= 2 for this kernel),
   // after stage 0's exponents (complete at the wait, which leaves only the
   // newest DI operations in flight)
-  load_raw(raw, eo, 0);
+  issue_e(m0, n0, 0, 0);
   issue(cur, 0, 0);
+  issue_e(m0, n0, 1, 1);
   issue(cur, 1, 1);
   __builtin_amdgcn_s_waitcnt((DI & 15) | (7 << 4) | ((DI >> 4) << 14));
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
-  hold_raw(raw);
-  pack(raw);
+  read_exps(0);
+  pack();
   read_frags(f0, 0, 0);
 
   int cb0 = 0;  // buffer of the current tile's stage 0
@@ -1452,31 +1466,14 @@ __global__ __launch_bounds__(BNT == 128 && ND == 4 ? 256 : 512, 1) void gemm_nt_
     v4i dgr{};
     if constexpr (DGL) dgr = make_rsrc(g.aux + int64_t(m0) * g.ldo + n0, dg_nrec);
     v4i nxt = cur;
-    EOff eo_n = eo;
     int m1 = 0, n1 = 0;
     if (more) {
       tile_of(it + 1, m1, n1);
       nxt = src_of(m1, n1);
-      if constexpr (SCALE == 1) eo_n = eoff_of(m1, n1);
     }
     for (int t = 0; t < nt; ++t) {
       const int b = (cb0 + t) & 1;
       __builtin_amdgcn_sched_barrier(0);
-      // exponents of the next stage (after the last: the next tile's stage
-      // 0), waited for after this stage's barrier.  (One load site: loads
-      // in two branches land in different registers, and the copy where
-      // they merge would wait for them right here.  In a tile's first
-      // stage the wait also covers the previous tile's output stores:
-      // issuing these loads in the previous tile's epilogue, before its
-      // stores, measured no faster for dual GEMMs and 3-9% slower for the
-      // 256 x 256 single GEMM.)
-      if constexpr (SCALE == 1) {
-        const bool last = t + 1 == nt;
-        if (!last || more) {
-          const EOff e = last ? eo_n : eo;
-          load_raw(raw, e, last ? 0 : t + 1);
-        }
-      }
       const bool bias_stage =
           kBiasLds && g.bias != nullptr && t == (nt > 2 ? nt - 2 : 0) && tid < NSL * BN;
       float bv = 0.0f;
@@ -1585,19 +1582,23 @@ __global__ __launch_bounds__(BNT == 128 && ND == 4 ? 256 : 512, 1) void gemm_nt_
           sync_keep(std::integral_constant<int, NST>{}, false);
         else
           sync_keep(std::integral_constant<int, 0>{}, false);
-        hold_raw(raw);
         if (bias_stage) bias_s[tid] = bv;
+        read_exps(b ^ 1);
         // the next weight fragment's MFMAs refill the pipes after the
         // barrier, then the refill DMA and sub-step 0 of stage t + 1 (after
         // the last stage: the next tile's stage 0, landed at this barrier;
         // stale and unused after the last tile) into the free registers
         mfma_roll(f0, f1, 1, PRE, -1, 0);
-        if (t + 2 < nt)
+        if (t + 2 < nt) {
+          issue_e(m0, n0, t + 2, b);
           issue(cur, t + 2, b);
-        else if (t + 2 == nt && more)
+        } else if (t + 2 == nt && more) {
+          issue_e(m1, n1, 0, b);
           issue(nxt, 0, b);
-        else if (more)
+        } else if (more) {
+          issue_e(m1, n1, 1, b);
           issue(nxt, 1, b);
+        }
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int i = 0; i < MB; ++i) read_one(f0[NF + i], b ^ 1, 0, NF + i);
@@ -1606,7 +1607,7 @@ __global__ __launch_bounds__(BNT == 128 && ND == 4 ? 256 : 512, 1) void gemm_nt_
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int q = PRE + 1; q < NF; ++q) mfma_roll(f0, f1, 1, q, b ^ 1, 0);
-        pack(raw);
+        pack();
         continue;
       }
       read_frags(f1, b, 1);
@@ -1617,17 +1618,21 @@ __global__ __launch_bounds__(BNT == 128 && ND == 4 ? 256 : 512, 1) void gemm_nt_
         sync_keep(std::integral_constant<int, NST>{}, t + 1 == nt);
       else
         sync_keep(std::integral_constant<int, 0>{}, t + 1 == nt);
-      hold_raw(raw);
       if (bias_stage) bias_s[tid] = bv;
+      read_exps(b ^ 1);
       mfmas_range(f0, 0, NP / 2, NP);
       pin_range(NP / 2, NP);
       __builtin_amdgcn_sched_barrier(0);
-      if (t + 2 < nt)
+      if (t + 2 < nt) {
+        issue_e(m0, n0, t + 2, b);
         issue(cur, t + 2, b);
-      else if (t + 2 == nt && more)
+      } else if (t + 2 == nt && more) {
+        issue_e(m1, n1, 0, b);
         issue(nxt, 0, b);  // the next tile's stage 0
-      else if (F32OUT && more)
+      } else if (F32OUT && more) {
+        issue_e(m1, n1, 1, b);
         issue(nxt, 1, b);  // the next tile's stage 1 (no output staging)
+      }
       issue_dg(dgr, t);
       __builtin_amdgcn_sched_barrier(0);
       // sub-step 0 of stage t + 1 (after the last stage: the next tile's
@@ -1637,7 +1642,7 @@ __global__ __launch_bounds__(BNT == 128 && ND == 4 ? 256 : 512, 1) void gemm_nt_
       if (EPI != 2 || t + 1 < nt) read_frags(f0, b ^ 1, 0);
       mfmas_range(f1, 1, 0, NP);
       interleave_mfma_lds<NP, 2 * (NF + MB), 0>();
-      pack(raw);  // the next stage's E8M0 codes (its sub-step 1 MFMAs are issued)
+      pack();  // the next stage's E8M0 codes (its sub-step 1 MFMAs are issued)
     }
 
     const int sb = (cb0 + nt - 1) & 1;
@@ -1781,8 +1786,7 @@ __global__ __launch_bounds__(BNT == 128 && ND == 4 ? 256 : 512, 1) void gemm_nt_
       zero_acc();
       cb0 = sb ^ 1;
       cur = nxt;
-      eo = eo_n;
-      m0 = m1;
+        m0 = m1;
       n0 = n1;
       continue;
     }
@@ -1844,6 +1848,7 @@ __global__ __launch_bounds__(BNT == 128 && ND == 4 ? 256 : 512, 1) void gemm_nt_
       __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0), vmcnt and expcnt untouched
       __builtin_amdgcn_s_barrier();
       asm volatile("" ::: "memory");
+      issue_e(m1, n1, 1, sb);
       issue(nxt, 1, sb);
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -1862,7 +1867,6 @@ __global__ __launch_bounds__(BNT == 128 && ND == 4 ? 256 : 512, 1) void gemm_nt_
     zero_acc();
     cb0 = sb ^ 1;  // the next tile's stage 0 sits in the other buffer
     cur = nxt;
-    eo = eo_n;
     m0 = m1;
     n0 = n1;
   }
@@ -1942,6 +1946,13 @@ bool persist_eligible(const GemmArgs& ga) {
   return int64_t(ga.M / 256) * (ga.N / 128) > num_cus();
 }
 
+// The persistent kernel DMAs each stage's block exponents into LDS as
+// 16-byte chunks of the exponent arrays: their bases must be 16-byte aligned
+// (rows and columns of its full tiles are multiples of 64).
+bool exps_al16(const GemmArgs& ga) {
+  return al16(ga.e_a) && al16(ga.e_0) && (ga.e_1 == nullptr || al16(ga.e_1));
+}
+
 template <int AF, int BF, bool SPLIT, typename OutT, int SCALE>
 int launch_gemm(GemmArgs ga, hipStream_t st) {
   const int m = ga.M, n = ga.N, k = ga.K;
@@ -1951,7 +1962,7 @@ int launch_gemm(GemmArgs ga, hipStream_t st) {
     // blocks (32-bit exponent offsets) -- 128-row slots (256 x 256 output
     // tiles) when there are at least as many of those as CUs (automatic
     // tile policy), else 64-row slots (256 x 128 output tiles)
-    if (persist_eligible(ga) &&
+    if (persist_eligible(ga) && exps_al16(ga) &&
         int64_t(k >> ga.bs_shift) * (m > n ? m : n) < int64_t(INT32_MAX)) {
       if (ga.bias != nullptr && (reinterpret_cast<uintptr_t>(ga.bias) & 15) != 0)
         return TCFP_ERR_ALIGN;
@@ -2023,8 +2034,9 @@ int launch_gemm(GemmArgs ga, hipStream_t st) {
       if constexpr (!SPLIT && AF != kBF16) {
         // (block exponents: 32-bit exponent offsets)
         persist = persist_eligible(ga) &&
-                  (SCALE == 0 || int64_t(ga.K >> ga.bs_shift) * (ga.M > ga.N ? ga.M : ga.N) <
-                                     int64_t(INT32_MAX));
+                  (SCALE == 0 || (exps_al16(ga) && int64_t(ga.K >> ga.bs_shift) *
+                                                           (ga.M > ga.N ? ga.M : ga.N) <
+                                                       int64_t(INT32_MAX)));
         if (persist) {
           if constexpr (SCALE == 0 && std::is_same<OutT, uint16_t>::value) {
             // the four-wave tile (one wave per SIMD, 128 x 64 x 2 per wave):
