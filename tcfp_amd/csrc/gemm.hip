@@ -1068,13 +1068,10 @@ __global__ __launch_bounds__(NW * 64, (NW == 4 && NS == 2 && BM <= 128 ? 2 : 1))
 // stage 1 right at the last stage's barrier.
 //
 // SCALE 1: block exponents (E8M0 MFMA scale operands, one accumulator set
-// for W_hi and W_lo).  A lane's 12 exponent bytes of a stage are buffer
-// loads at a 32-bit lane offset fixed per tile and a uniform per-stage
-// offset (full tiles: no bounds predicates), issued at the top of the
-// stage before and waited for at its barrier, which waits for every
-// earlier load anyway; the E8M0 codes are formed at the end of the stage,
-// after the refill DMA, without a further wait (a wait there would also
-// wait for that DMA).
+// for W_hi and W_lo).  A stage's exponents are DMA'd into an LDS area of
+// their own with the stage's operands (two instructions of 16-byte chunks
+// of the exponent rows), read by each lane right after the barrier that
+// makes them valid, and turned into E8M0 codes at the end of the stage.
 //
 // SPL (single GEMM, 256 x 64 slots): the two weight slots are two adjacent
 // 64-row blocks of one B (the launcher points B1 / e_1 64 rows past B0 /
