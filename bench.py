@@ -459,7 +459,7 @@ def bench_dual_quant(iters=20, cold_rounds=4):
     return out
 
 
-def bench_mlp(steps=100, time_iters=20, arms=("tcfp", "tcfp_fused", "bf16", "fp32")):
+def bench_mlp(steps=100, time_iters=20, arms=("tcfp", "tcfp_fused", "bf16", "fp32"), rounds=5):
     """1024 -> 4096 -> 1024 GELU MLP, 8192 tokens, MSE, AdamW 1e-3.
 
     Arms: TCFP-12 (both linears converted, per-tensor scales with EF: the
@@ -467,7 +467,11 @@ def bench_mlp(steps=100, time_iters=20, arms=("tcfp", "tcfp_fused", "bf16", "fp3
     quantisation around it (``fuse_tcfp_mlp``; bit-identical results),
     BF16 autocast (the target's baseline), and the same model in fp32 (the
     reference harness's "BF16" baseline is an fp32 model,
-    benchmarks/benchmark_tcfp.py:482-516; context only)."""
+    benchmarks/benchmark_tcfp.py:482-516; context only).  Each arm trains
+    ``steps`` steps (the losses); then the arms are timed in ``rounds``
+    interleaved rounds of ``time_iters`` steps each (HIP events), and each
+    arm's median round is reported, so that clock drift over the run falls
+    on every arm alike."""
     import torch
     import torch.nn as nn
 
@@ -489,7 +493,7 @@ def bench_mlp(steps=100, time_iters=20, arms=("tcfp", "tcfp_fused", "bf16", "fp3
 
     xf = x.float()
 
-    def run(arm):
+    def train(arm):
         m = make(arm)
         opt = torch.optim.AdamW(m.parameters(), lr=1e-3)
 
@@ -511,8 +515,18 @@ def bench_mlp(steps=100, time_iters=20, arms=("tcfp", "tcfp_fused", "bf16", "fp3
         for i in range(steps):
             losses.append(step())
         torch.cuda.synchronize()
-        ms = event_time_ms(step, time_iters, torch.cuda.current_stream(dev))
-        return [float(v) for v in torch.stack(losses).detach().cpu()], ms
+        return [float(v) for v in torch.stack(losses).detach().cpu()], step
+
+    trained = {arm: train(arm) for arm in arms}
+    stream = torch.cuda.current_stream(dev)
+    times = {arm: [] for arm in arms}
+    for _ in range(rounds):
+        for arm in arms:
+            times[arm].append(event_time_ms(trained[arm][1], time_iters, stream))
+    ms_of = {arm: sorted(v)[len(v) // 2] for arm, v in times.items()}
+
+    def run(arm):
+        return trained[arm][0], ms_of[arm]
 
     res = {"steps": steps}
     if "tcfp" in arms:
@@ -865,7 +879,7 @@ def main():
               "mlp": lambda: bench_mlp(
                   steps=args.steps,
                   arms=("tcfp", "tcfp_fused", "bf16", "fp32") if args.arm == "both"
-                  else (args.arm,)),
+                  else (args.arm,), rounds=5 if args.arm == "both" else 1),
               "copy": lambda: bench_copy(args.steps),
               "scaled_mm": lambda: bench_scaled_mm(args.steps, args.warmup)}
         log(f"[bench] part {args.part}")
