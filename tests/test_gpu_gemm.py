@@ -157,6 +157,35 @@ def test_tile_policies_agree_bitwise(dev, M, K_, N):
         assert torch.equal(outs[0], outs[i]) and torch.equal(outs[1], outs[i + 1]), i
 
 
+@pytest.mark.parametrize("M,N,K_", [(4096, 1024, 8192), (1024, 4096, 8192), (1000, 1000, 4112),
+                                    (520, 264, 400)])
+def test_four_stage_small_tile_matches_eight_wave(dev, M, N, K_):
+    """The single-round small-tile launch (one four-wave workgroup per CU,
+    four stages in flight, each stage's fragments read during the stage
+    before) against the eight-wave variant of the same tile, bit for bit:
+    the C4 wgrad shapes (E5M2 x E4M3, fp32 out), an odd stage count with a
+    16-column last stage (K = 4112: 33 stages) and ragged rows; the last
+    case also to the float64 oracle."""
+    print(f"four-stage small tile M={M} N={N} K={K_}", flush=True)
+    a, sa = make_act((M, K_), 41, dev, torch.float8_e5m2)
+    b, sb = make_act((N, K_), 42, dev)
+    fn = lambda: K.fp8_gemm_nt(a, b, sa, sb)
+    names = _kernel_names(fn)
+    assert any("gemm_nt_dma_kernel<1, 0, true, float, 4, 128, 64, 0, 4, 0, 0>" in n
+               for n in names), names
+    out = fn()
+    try:
+        K.set_gemm_tile_policy("small8")
+        assert any("<1, 0, true, float, 8, 128, 64, 0, 4, 0, 0>" in n for n in _kernel_names(fn))
+        ref8 = fn()
+    finally:
+        K.set_gemm_tile_policy("auto")
+    assert torch.equal(out.view(torch.int32), ref8.view(torch.int32))
+    if M * N * K_ <= 1 << 27:
+        ref = og.gemm_nt(u8(a), ofp8.E5M2, u8(b), ofp8.E4M3, sa.item(), sb.item())
+        assert og.rel_fro(out.cpu().numpy(), ref) < EXACT
+
+
 @pytest.mark.parametrize("afmt", [torch.float8_e4m3fn, torch.float8_e5m2])
 @pytest.mark.parametrize("od", [torch.float32, torch.bfloat16])
 def test_small_tile_two_stage_launch(dev, afmt, od):
