@@ -194,12 +194,16 @@ def bench_comparators(t, iters=200, heat=300, rounds=3):
     return res
 
 
-def bench_block_gemms(iters=20):
+def bench_block_gemms(iters=100, heat=300, rounds=3):
     """block-scaled dual GEMM at 4096^3, bs 32/64/128 (int8
     power-of-two exponents, the reference's block format, and fp32
     448/amax block scales, the configuration's literal form), plus the
     single block-scaled GEMM at bs 64.  fp32 out, as the reference's
-    kernels."""
+    kernels.  Timed as the comparators are: per arm and round, ``heat``
+    untimed back-to-back calls (out of the idle clock state), then
+    ``iters`` calls timed by HIP events; the median of ``rounds``
+    interleaved rounds.  (``--part block`` keeps the short form, 3 untimed
+    and 20 timed calls per arm, for the profiler runs.)"""
     import torch
 
     from tcfp_amd import kernels as K
@@ -209,24 +213,32 @@ def bench_block_gemms(iters=20):
     n = 4096
     x = torch.randn(n, n, generator=torch.Generator().manual_seed(0)).bfloat16().to(dev)
     w = torch.randn(n, n, generator=torch.Generator().manual_seed(1)).to(dev)
-    res = {}
+    arms = {}  # name -> (GEMMs per call, fn)
     for bs in (32, 64, 128):
         a, ea = K.block_quantize_fp8(x, bs)
         h, l, eh, el = K.fused_dual_quantize_fp8(w, bs)
-        ms = event_time_ms(
-            lambda: K.fused_block_scaled_dual_gemm_forward(a, h, l, ea, eh, el, bs), iters, stream)
-        res[f"block{bs}_dual_ms"] = ms
-        res[f"block{bs}_dual_tflops"] = 4 * n**3 / (ms * 1e-3) / 1e12
+        arms[f"block{bs}_dual"] = (
+            2, lambda a=a, h=h, l=l, ea=ea, eh=eh, el=el, bs=bs:
+            K.fused_block_scaled_dual_gemm_forward(a, h, l, ea, eh, el, bs))
         if bs == 64:
-            ms = event_time_ms(lambda: K.block_scaled_gemm(a, h, ea, eh, bs), iters, stream)
-            res["block64_single_ms"] = ms
-            res["block64_single_tflops"] = 2 * n**3 / (ms * 1e-3) / 1e12
+            arms["block64_single"] = (
+                1, lambda a=a, h=h, ea=ea, eh=eh: K.block_scaled_gemm(a, h, ea, eh, 64))
         a, sa = K.block_quantize_fp8(x, bs, scale_format="fp32")
         h, l, sh, sl = K.fused_dual_quantize_fp8(w, bs, scale_format="fp32")
-        ms = event_time_ms(
-            lambda: K.fused_block_scaled_dual_gemm_forward(a, h, l, sa, sh, sl, bs), iters, stream)
-        res[f"block{bs}_f32s_dual_ms"] = ms
-        res[f"block{bs}_f32s_dual_tflops"] = 4 * n**3 / (ms * 1e-3) / 1e12
+        arms[f"block{bs}_f32s_dual"] = (
+            2, lambda a=a, h=h, l=l, sa=sa, sh=sh, sl=sl, bs=bs:
+            K.fused_block_scaled_dual_gemm_forward(a, h, l, sa, sh, sl, bs))
+    times = {k: [] for k in arms}
+    for _ in range(rounds):
+        for k, (_, fn) in arms.items():
+            times[k].append(event_time_ms(fn, iters, stream, warmup=heat))
+    res = {}
+    for k, (mult, _) in arms.items():
+        ms = statistics.median(times[k])
+        res[f"{k}_ms"] = ms
+        res[f"{k}_tflops"] = 2 * mult * n**3 / (ms * 1e-3) / 1e12
+    res["method"] = (f"per arm and round: {heat} untimed calls then {iters} timed (HIP events); "
+                     f"median of {rounds} interleaved rounds")
     return res
 
 
@@ -871,7 +883,7 @@ def main():
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     if args.part != "all" and args.part != "gemm":
-        fn = {"quant": lambda: bench_dual_quant(), "block": lambda: bench_block_gemms(),
+        fn = {"quant": lambda: bench_dual_quant(), "block": lambda: bench_block_gemms(iters=20, heat=3, rounds=1),
               "c5": lambda: bench_c5(), "c5mem": lambda: bench_c5_memory(),
               "quantcold": lambda: bench_dual_quant_cold(max(1, args.steps // 20)),
               "quantfuse": lambda: bench_quant_in_consumer(),
