@@ -1070,6 +1070,66 @@ def _lo_threshold(w_lo: torch.Tensor, lo_scales: torch.Tensor, threshold: float,
     return codes.reshape(n, num_kb * block_size).view(w_lo.dtype), lo_scales
 
 
+def block_linear_forward(x2d, weight, bias, block_size, error_buf=None, srr=False,
+                         update_ef=True):
+    """The launches of a block-scaled TCFP layer's forward, as the public ops
+    run them and with the same results bit for bit: ``fused_dual_quantize_fp8``
+    of W (EF or SRR, the same seed draw), then ``fused_act_quant_dual_gemm_forward``
+    for layers of at most four 128-column tiles, else ``block_quantize_fp8``
+    of X and ``fused_block_scaled_dual_gemm_forward`` (the reference's
+    dispatch, ``tcfp/nn/__init__.py:617-650``).
+
+    For ``tcfp_amd.nn``'s block-scaled layer, whose W, EF buffer and bias are
+    its own: it skips the per-op argument checks and Python calls (one host
+    call instead of three; the layer's forward enqueues ~11 us faster, which
+    small host-bound models see).  ``x2d`` [M, K] fp32/bf16, ``weight``
+    [N, K] contiguous.  Returns ``(out fp32 [M, N], w_hi, w_lo, e_hi, e_lo,
+    act_fp8, act_e)``."""
+    bs = block_size
+    if bs not in (32, 64, 128):
+        raise ValueError(f"block_size must be 32, 64, or 128, got {bs}")
+    M, Kd = x2d.shape
+    N = weight.shape[0]
+    assert weight.is_contiguous() and weight.shape[1] == Kd and Kd % bs == 0, (
+        f"weight {tuple(weight.shape)} vs input ({M}, {Kd}), block {bs}")
+    if srr and error_buf is not None:
+        raise ValueError("stochastic_lo and error_buf are mutually exclusive")
+    dev = _hip.require_gpu(x2d, weight, error_buf, bias)
+    lib = _hip.lib()
+    st = _hip.stream_of(dev)
+    nkb = Kd // bs
+    e4 = torch.float8_e4m3fn
+    w_hi = torch.empty((N, Kd), dtype=e4, device=dev)
+    w_lo = torch.empty((N, Kd), dtype=e4, device=dev)
+    e_hi = torch.empty((nkb, N), dtype=torch.int8, device=dev)
+    e_lo = torch.empty((nkb, N), dtype=torch.int8, device=dev)
+    seed = int(torch.randint(0, 2**62, (1,)).item()) if srr else 0
+    check(lib.tcfp_block_dual_quantize(
+        ptr(weight), _in_dtype(weight), N, Kd, bs, ptr(error_buf), int(bool(update_ef)),
+        int(bool(srr)), seed, 0, ptr(w_hi), ptr(w_lo), ptr(e_hi), ptr(e_lo), st),
+        "fused_dual_quantize_fp8")
+    act = x2d
+    if not act.is_contiguous() or act.data_ptr() % 16 != 0:
+        act = act.contiguous()
+    b = _bias_f32(bias, N) if bias is not None else None
+    out = torch.empty((M, N), dtype=torch.float32, device=dev)
+    act_fp8 = torch.empty((M, Kd), dtype=e4, device=dev)
+    act_e = torch.empty((nkb, M), dtype=torch.int8, device=dev)
+    if (N + 127) // 128 <= 4:
+        check(lib.tcfp_act_quant_block_dual_gemm(
+            ptr(act), _in_dtype(act), Kd, ptr(w_hi), ptr(w_lo), Kd, ptr(e_hi), ptr(e_lo), M, N,
+            Kd, bs, ptr(b), ptr(out), N, ptr(act_fp8), ptr(act_e), st),
+            "fused_act_quant_dual_gemm_forward")
+    else:
+        check(lib.tcfp_block_quantize(ptr(act), _in_dtype(act), M, Kd, bs, FP8_E4M3,
+                                      ptr(act_fp8), ptr(act_e), st), "block_quantize_fp8")
+        check(lib.tcfp_block_dual_gemm(
+            ptr(act_fp8), FP8_E4M3, Kd, ptr(act_e), ptr(w_hi), ptr(w_lo), FP8_E4M3, Kd,
+            ptr(e_hi), ptr(e_lo), M, N, Kd, bs, ptr(b), ptr(out), DTYPE_F32, N, st),
+            "block_dual_gemm")
+    return out, w_hi, w_lo, e_hi, e_lo, act_fp8, act_e
+
+
 def fused_block_scaled_dual_gemm_forward(
     act_fp8: torch.Tensor,
     w_hi_fp8: torch.Tensor,
@@ -1418,6 +1478,67 @@ def block_backward_prep(
     if fp8:
         return g_deq, g_split, bias_grad, g_fp8, g_exps
     return g_deq, g_split, bias_grad
+
+
+_BWD_WS: dict[tuple, tuple[int, int, int]] = {}
+
+
+def block_linear_backward(grad_2d, act_fp8, act_e, w_hi, w_lo, e_hi, e_lo, block_size,
+                          need_dx, need_dw, want_db, split_lo=True):
+    """The launches of a block-scaled TCFP layer's default backward, as
+    :func:`block_backward_prep`, :func:`block_wgrad_from_prep` and
+    :func:`block_dgrad_from_prep` run them, with the same results bit for
+    bit: one pass over the gradient, then the wgrad from the split gradient
+    (released before dX is allocated), then the exact dgrad.
+
+    For ``tcfp_amd.nn``'s block-scaled layer (its saved operands): one host
+    call without the per-op checks, the workspace sizes cached per shape.
+    ``grad_2d`` [M, D_out]; ``act_fp8`` / ``act_e`` the forward's activation
+    codes and exponents (``need_dw``; M % 4 == 0, and M % 64 == 0 without
+    ``split_lo``); ``w_hi`` .. ``e_lo`` the forward's weight operands
+    (``need_dx``).  Returns ``(dx fp32 [M, D_in], dw fp32 [D_out, D_in],
+    db fp32 [D_out])``, None where not requested."""
+    bs = block_size
+    M, Nout = grad_2d.shape
+    Kin = w_hi.shape[1] if need_dx else (act_fp8.shape[1] if need_dw else 0)
+    dev = _hip.require_gpu(grad_2d, act_fp8, w_hi)
+    lib = _hip.lib()
+    st = _hip.stream_of(dev)
+    key = (M, Nout, Kin, bool(split_lo), bool(want_db), bool(need_dw), bool(need_dx))
+    sizes = _BWD_WS.get(key)
+    if sizes is None:
+        sizes = (int(lib.tcfp_block_grad_prep_workspace_bytes(M, Nout)) if want_db else 0,
+                 int(lib.tcfp_block_wgrad_presplit_workspace_bytes(M, Nout, Kin, int(split_lo)))
+                 if need_dw else 0,
+                 int(lib.tcfp_block_dual_gemm_dx_bf16_workspace_bytes(Nout, Kin)) if need_dx else 0)
+        _BWD_WS[key] = sizes
+    n_prep, n_w, n_d = sizes
+    g = grad_2d if (grad_2d.dtype == torch.float32 and grad_2d.is_contiguous()) else (
+        grad_2d.float().contiguous())
+    bf = torch.bfloat16
+    g_deq = torch.empty((M, Nout), dtype=bf, device=dev) if need_dx else None
+    g_split = (torch.empty((Nout, 2 * M if split_lo else M), dtype=bf, device=dev)
+               if need_dw else None)
+    db = torch.empty((Nout,), dtype=torch.float32, device=dev) if want_db else None
+    ws = torch.empty(max(n_prep, 1), dtype=torch.uint8, device=dev) if want_db else None
+    check(lib.tcfp_block_grad_prep(ptr(g), M, Nout, bs, ptr(g_deq), ptr(g_split), int(split_lo),
+                                   ptr(db), None, None, ptr(ws), n_prep, st),
+          "block_backward_prep")
+    dw = dx = None
+    if need_dw:
+        dw = torch.empty((Nout, Kin), dtype=torch.float32, device=dev)
+        ws = torch.empty(max(n_w, 1), dtype=torch.uint8, device=dev)
+        check(lib.tcfp_block_wgrad_presplit(
+            ptr(g_split), int(split_lo), M, Nout, ptr(act_fp8), _fmt(act_fp8.dtype), ptr(act_e),
+            Kin, bs, ptr(dw), ptr(ws), n_w, st), "block_wgrad_from_prep")
+    g_split = None  # (released before dX is allocated)
+    if need_dx:
+        dx = torch.empty((M, Kin), dtype=torch.float32, device=dev)
+        ws = torch.empty(max(n_d, 1), dtype=torch.uint8, device=dev)
+        check(lib.tcfp_block_dual_gemm_dx_bf16(
+            ptr(g_deq), ptr(w_hi), ptr(w_lo), ptr(e_hi), ptr(e_lo), M, Nout, Kin, bs, ptr(dx),
+            ptr(ws), n_d, st), "block_dgrad_from_prep")
+    return dx, dw, db
 
 
 def block_dgrad_from_prep(g_deq, w_hi_fp8, w_lo_fp8, w_hi_scales, w_lo_scales, block_size):

@@ -261,24 +261,18 @@ class _TCFP12BlockScaledFunction(torch.autograd.Function):
         bs = scale_block_size
         error_buf = _ef_buffer(error_state, param_name, weight)
         w = weight if weight.is_contiguous() else weight.contiguous()
-        # EF is read, and rewritten in place only when update_ef (the
-        # reference clones the buffer instead, :597-608).
-        w_hi, w_lo, sh, sl = K.fused_dual_quantize_fp8(
-            w, block_size=bs, error_buf=error_buf, stochastic_lo=srr, update_ef=update_ef
-        )
         input_shape = input.shape
         input_2d = _flatten(input)
-        # the reference's dispatch (tcfp/nn/__init__.py:617-650): the fused
-        # act-quant entry point for narrow layers, separate quant otherwise
-        if (w.shape[0] + 127) // 128 <= 4:
-            out_2d, act_fp8, act_scales = K.fused_act_quant_dual_gemm_forward(
-                input_2d, w_hi, w_lo, sh, sl, block_size=bs, bias=bias
-            )
-        else:
-            act_fp8, act_scales = K.block_quantize_fp8(input_2d, block_size=bs)
-            out_2d = K.fused_block_scaled_dual_gemm_forward(
-                act_fp8, w_hi, w_lo, act_scales, sh, sl, block_size=bs, bias=bias
-            )
+        # W's dual quantisation (EF is read, and rewritten in place only when
+        # update_ef; the reference clones the buffer instead, :597-608), then
+        # the reference's dispatch (:617-650): the fused act-quant GEMM for
+        # narrow layers, separate activation quantisation otherwise -- the
+        # launches of K.fused_dual_quantize_fp8, K.fused_act_quant_dual_gemm_forward
+        # / K.block_quantize_fp8 + K.fused_block_scaled_dual_gemm_forward in
+        # one host call
+        out_2d, w_hi, w_lo, sh, sl, act_fp8, act_scales = K.block_linear_forward(
+            input_2d, w, bias, bs, error_buf=error_buf, srr=srr, update_ef=update_ef
+        )
         output = out_2d.reshape(*input_shape[:-1], out_2d.shape[-1])
 
         ctx.hp_grad_weight = hp_grad_weight
@@ -318,13 +312,28 @@ class _TCFP12BlockScaledFunction(torch.autograd.Function):
         # wgrad, and the bias gradient
         fp8_wgrad = need_dw and not ctx.hp_grad_weight and grad_2d.shape[0] % 4 == 0
         want_db = need_db and ctx.has_bias
+        split_lo = not (ctx.bf16_wgrad and grad_2d.shape[0] % 64 == 0)
+        if (not ctx.fp8_dgrad and not ctx.hp_grad_weight and (fp8_wgrad or not need_dw)
+                and (need_dx or need_dw or want_db)):
+            # the default modes: the prep pass, the wgrad, the exact dgrad
+            # in one host call (the same launches as below)
+            dx, dw, db = K.block_linear_backward(
+                grad_2d, saved_act, act_scales, w_hi, w_lo, sh, sl, bs, need_dx, need_dw,
+                want_db, split_lo=split_lo)
+            if dx is not None:
+                grad_input = dx.reshape(ctx.input_shape)
+            if dw is not None:
+                grad_weight = dw.to(grad_2d.dtype)
+            if want_db:
+                grad_bias = db.to(grad_2d.dtype)
+            return (grad_input, grad_weight, grad_bias) + (None,) * 7
         g_deq = g_split = db = g_codes = None
         exact_dx = need_dx and not ctx.fp8_dgrad
         fp8_dx = need_dx and ctx.fp8_dgrad
         if exact_dx or fp8_wgrad or want_db or fp8_dx:
             res = K.block_backward_prep(
                 grad_2d, bs, dequant=exact_dx, split=fp8_wgrad, bias=want_db, fp8=fp8_dx,
-                split_lo=not (ctx.bf16_wgrad and grad_2d.shape[0] % 64 == 0),
+                split_lo=split_lo,
             )
             g_deq, g_split, db = res[:3]
             if fp8_dx:

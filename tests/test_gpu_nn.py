@@ -396,3 +396,62 @@ def test_c5_scaleup_layer_full_size(dev, d_in, d_out):
     assert err < 1e-4, err
     assert dw_err < 2e-5, dw_err
     assert dx_err < 5e-3, dx_err  # x is bf16: dX is rounded to bf16 (2^-9)
+
+
+@pytest.mark.parametrize("M,Kd,N", [(256, 256, 384), (300, 512, 1024), (128, 1024, 256)])
+@pytest.mark.parametrize("mode", ["ef", "srr", "srr_bias_bf16", "split_off"])
+def test_block_layer_one_call_paths_match_the_ops(dev, M, Kd, N, mode):
+    """The block-scaled layer's one-call forward and backward
+    (``block_linear_forward`` / ``block_linear_backward``) against the public
+    ops they replace, bit for bit: W's dual quantisation with EF (updated in
+    place) or SRR (the same seed draw from torch's generator), the narrow
+    layers' fused act-quant GEMM (N <= 512) or activation quantisation + block
+    GEMM, the gradient prep pass, the split (or single-pass) wgrad, the exact
+    dgrad and the bias gradient; and the layer's backward with input and
+    bias gradients off."""
+    from tcfp_amd import kernels as K
+
+    print(f"one-call block layer M={M} K={Kd} N={N} {mode}", flush=True)
+    bs = 64
+    g = torch.Generator().manual_seed(M + N)
+    xdt = torch.bfloat16 if "bf16" in mode else torch.float32
+    x = torch.randn(M, Kd, generator=g).to(xdt).to(dev)
+    w = (torch.randn(N, Kd, generator=g) * 0.05).to(dev)
+    bias = torch.randn(N, generator=g).to(dev) if "bias" in mode else None
+    gout = torch.randn(M, N, generator=g).to(dev)
+    srr = "srr" in mode
+    efa = None if srr else (torch.randn(N, Kd, generator=g) * 1e-3).to(dev)
+    efb = None if srr else efa.clone()
+    split_lo = not (mode == "split_off" and M % 64 == 0)  # (the single pass needs M % 64 == 0)
+
+    torch.manual_seed(7)
+    h, l, sh, sl = K.fused_dual_quantize_fp8(w, block_size=bs, error_buf=efa, stochastic_lo=srr)
+    if (N + 127) // 128 <= 4:
+        out, a, ea = K.fused_act_quant_dual_gemm_forward(x, h, l, sh, sl, block_size=bs, bias=bias)
+    else:
+        a, ea = K.block_quantize_fp8(x, block_size=bs)
+        out = K.fused_block_scaled_dual_gemm_forward(a, h, l, ea, sh, sl, block_size=bs, bias=bias)
+    gd, gs, db = K.block_backward_prep(gout, bs, dequant=True, split=True, bias=True,
+                                       split_lo=split_lo)
+    dw = K.block_wgrad_from_prep(gs, a, ea, bs)
+    dx = K.block_dgrad_from_prep(gd, h, l, sh, sl, bs)
+
+    torch.manual_seed(7)
+    outb, hb, lb, shb, slb, ab, eab = K.block_linear_forward(x, w, bias, bs, error_buf=efb,
+                                                             srr=srr)
+    dxb, dwb, dbb = K.block_linear_backward(gout, ab, eab, hb, lb, shb, slb, bs, True, True,
+                                            True, split_lo=split_lo)
+    u8 = lambda t: t.view(torch.uint8)
+    for p, q in ((h, hb), (l, lb), (a, ab)):
+        assert torch.equal(u8(p), u8(q))
+    for p, q in ((sh, shb), (sl, slb), (ea, eab)):
+        assert torch.equal(p, q)
+    for p, q in ((out, outb), (dw, dwb), (dx, dxb), (db, dbb)):
+        assert torch.equal(p.view(torch.int32), q.view(torch.int32))
+    if not srr:
+        assert torch.equal(efa.view(torch.int32), efb.view(torch.int32))
+    # the layer's backward with only the weight gradient (no dX, no bias)
+    none = K.block_linear_backward(gout, ab, eab, None, None, None, None, bs, False, True, False,
+                                   split_lo=split_lo)
+    assert none[0] is None and none[2] is None
+    assert torch.equal(none[1].view(torch.int32), dw.view(torch.int32))
