@@ -1524,14 +1524,16 @@ def block_linear_backward(grad_2d, act_fp8, act_e, w_hi, w_lo, e_hi, e_lo, block
     check(lib.tcfp_block_grad_prep(ptr(g), M, Nout, bs, ptr(g_deq), ptr(g_split), int(split_lo),
                                    ptr(db), None, None, ptr(ws), n_prep, st),
           "block_backward_prep")
-    dw = dx = None
+    # (the gradient copy and each scratch are released before the next
+    # allocation, as the per-op calls release theirs on return)
+    g = dw = dx = ws = None
     if need_dw:
         dw = torch.empty((Nout, Kin), dtype=torch.float32, device=dev)
         ws = torch.empty(max(n_w, 1), dtype=torch.uint8, device=dev)
         check(lib.tcfp_block_wgrad_presplit(
             ptr(g_split), int(split_lo), M, Nout, ptr(act_fp8), _fmt(act_fp8.dtype), ptr(act_e),
             Kin, bs, ptr(dw), ptr(ws), n_w, st), "block_wgrad_from_prep")
-    g_split = None  # (released before dX is allocated)
+    g_split = ws = None  # (released before dX is allocated)
     if need_dx:
         dx = torch.empty((M, Kin), dtype=torch.float32, device=dev)
         ws = torch.empty(max(n_d, 1), dtype=torch.uint8, device=dev)
