@@ -631,12 +631,14 @@ def _tiny_gpt(vocab=256, d=256, layers=4, heads=4, ffn=1024, seq=128):
     return TinyGPT()
 
 
-def bench_c5(steps=50, time_iters=10):
+def bench_c5(steps=50, time_iters=10, rounds=5):
     """TinyGPT (d 256, 4 layers, 4 heads, FFN 1024, vocab 256,
     seq 128, batch 32) with every QKV/O/FFN linear TCFP-12 block-64 + SRR,
     against BF16 autocast; and the 4096 -> 16384 -> 4096 scale-up layer at
     8192 tokens (peak memory and fwd+bwd time: block-64 SRR, block-64 EF,
-    BF16)."""
+    BF16).  The TinyGPT arms train ``steps`` steps each (the losses), then
+    are timed in ``rounds`` interleaved rounds of ``time_iters`` steps
+    (median): the step is host-bound, so it follows the host's state."""
     import torch
     import torch.nn as nn
     import torch.nn.functional as F
@@ -646,8 +648,10 @@ def bench_c5(steps=50, time_iters=10):
     dev = torch.device("cuda:0")
     stream = torch.cuda.current_stream(dev)
     g = torch.Generator().manual_seed(0)
-    data = torch.randint(0, 256, (steps + time_iters + 3, 32, 129), generator=g).to(dev)
+    data = torch.randint(0, 256, (steps + rounds * (time_iters + 3) + 3, 32, 129),
+                         generator=g).to(dev)
     res = {}
+    step_of = {}
     for arm in ("tcfp_block64_srr", "bf16"):
         torch.manual_seed(1)
         model = _tiny_gpt().to(dev)
@@ -657,7 +661,7 @@ def bench_c5(steps=50, time_iters=10):
         opt = torch.optim.AdamW(model.parameters(), lr=3e-4, weight_decay=0.01)
         it = iter(range(data.shape[0]))
 
-        def step():
+        def step(arm=arm, model=model, opt=opt, it=it):
             b = data[next(it)]
             with torch.autocast("cuda", dtype=torch.bfloat16, enabled=(arm == "bf16")):
                 logits = model(b[:, :-1])
@@ -668,9 +672,18 @@ def bench_c5(steps=50, time_iters=10):
             return loss
 
         losses = [step() for _ in range(steps)]
-        ms = event_time_ms(step, time_iters, stream, warmup=0)
         lv = [float(v) for v in torch.stack(losses).detach().cpu()]
-        res[arm] = {"step_ms": ms, "loss_first": lv[0], "loss_last": lv[-1], "steps": steps}
+        res[arm] = {"loss_first": lv[0], "loss_last": lv[-1], "steps": steps}
+        step_of[arm] = step
+    times = {arm: [] for arm in step_of}
+    for _ in range(rounds):
+        for arm, step in step_of.items():
+            times[arm].append(event_time_ms(step, time_iters, stream, warmup=3))
+    for arm in step_of:
+        res[arm]["step_ms"] = statistics.median(times[arm])
+    # (the TinyGPT arms are released before the scale-up layer's memory figures)
+    step_of.clear()
+    del step, model, opt, it
     res["loss_rel_diff_last"] = (abs(res["tcfp_block64_srr"]["loss_last"] - res["bf16"]["loss_last"])
                                  / res["bf16"]["loss_last"])
     # scale-up layer
