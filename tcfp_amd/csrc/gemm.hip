@@ -135,6 +135,15 @@ TCFP_DEV void dma16(v4i rsrc, uint32_t voff, uint32_t soff, uint32_t lds) {
                : "memory");
 }
 
+// dma16 with the non-temporal hint (data read once: kept out of the way of
+// the operands in L2 and the Infinity Cache).
+TCFP_DEV void dma16_nt(v4i rsrc, uint32_t voff, uint32_t soff, uint32_t lds) {
+  asm volatile("buffer_load_dwordx4 %0, %1, %2 offen nt lds"
+               :
+               : "v"(voff), "s"(rsrc), "s"(soff), "{m0}"(lds)
+               : "memory");
+}
+
 // 16 bytes from a per-lane global address into LDS at lds + 16 * lane
 // (lds wave-uniform); counted by vmcnt like dma16.
 TCFP_DEV void gdma16(const void* src, uint32_t lds) {
@@ -1343,7 +1352,7 @@ __global__ __launch_bounds__(BNT == 128 && ND == 4 ? 256 : 512, 1) void gemm_nt_
         const int p = (wave - ND) + NDG * k;
         const int row = 4 * p + (lane >> 4);
         const uint32_t vo = uint32_t(row) * ldo_b + uint32_t(((lane & 15) ^ (row & 15)) * 16);
-        dma16(rs, vo, 0u, dg_lds0 + uint32_t(p) * 1024u);
+        dma16_nt(rs, vo, 0u, dg_lds0 + uint32_t(p) * 1024u);  // (read once)
       }
     }
   };

@@ -884,6 +884,29 @@ struct TileLoad {
   static constexpr int RPI = kThreads / TPR;          // tile rows per pass
 };
 
+// loadvec with the non-temporal hint, for a pass that is its input's last
+// reader: the streamed input then does not displace, in L2 and the Infinity
+// Cache, the codes the next GEMM reads (C4 training step, one process:
+// 0.851 -> 0.826 ms with the transposing pass's loads and the GELU
+// derivative factors' stores streamed).
+typedef float f32x4_nt __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_nt __attribute__((ext_vector_type(4)));
+template <typename InT>
+TCFP_DEV void loadvec_nt(const InT* p, float* v);
+template <>
+TCFP_DEV void loadvec_nt<float>(const float* p, float* v) {
+  const f32x4_nt a = __builtin_nontemporal_load(reinterpret_cast<const f32x4_nt*>(p));
+  v[0] = a[0]; v[1] = a[1]; v[2] = a[2]; v[3] = a[3];
+}
+template <>
+TCFP_DEV void loadvec_nt<uint16_t>(const uint16_t* p, float* v) {
+  const u32x4_nt a = __builtin_nontemporal_load(reinterpret_cast<const u32x4_nt*>(p));
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    v[2 * i] = __uint_as_float(a[i] << 16);
+    v[2 * i + 1] = __uint_as_float(a[i] & 0xFFFF0000u);
+  }
+}
 template <typename InT>
 TCFP_DEV void loadvec(const InT* p, float* v);
 template <>
@@ -932,13 +955,15 @@ TCFP_DEV void quant_t_body(
     const bool valid = r < rows && c < cols;
     float v[VEC];
     if (valid) {
-      loadvec<InT>(x + r * cols + c, v);
+      loadvec_nt<InT>(x + r * cols + c, v);  // (every caller's last read of x)
       if constexpr (GELU_IN) {
         if (dg_out) {
           float d[VEC];
 #pragma unroll
           for (int j = 0; j < VEC; ++j) gelu_and_deriv(v[j], v[j], d[j]);
-          *reinterpret_cast<float4*>(dg_out + r * cols + c) = make_float4(d[0], d[1], d[2], d[3]);
+          // (read back only by the backward's dgrad, long after)
+          const f32x4_nt dv = {d[0], d[1], d[2], d[3]};
+          __builtin_nontemporal_store(dv, reinterpret_cast<f32x4_nt*>(dg_out + r * cols + c));
         } else {
 #pragma unroll
           for (int j = 0; j < VEC; ++j) v[j] = gelu_f32(v[j]);
