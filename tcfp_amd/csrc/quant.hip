@@ -955,7 +955,7 @@ TCFP_DEV void quant_t_body(
     const bool valid = r < rows && c < cols;
     float v[VEC];
     if (valid) {
-      loadvec_nt<InT>(x + r * cols + c, v);  // (every caller's last read of x)
+      loadvec_nt<InT>(x + r * cols + c, v);  // (the op's last read of x)
       if constexpr (GELU_IN) {
         if (dg_out) {
           float d[VEC];
